@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""RMSNorm layer forward + VJP on one MI355X, through the C ABI.
+
+One step = agk_rmsnorm_fwd (y, inv_rms) + agk_rmsnorm_bwd (dx, dgamma: the
+backward kernel and the dgamma column reduction) over one batch of the
+configuration, inputs resident in HBM before the timed region starts.
+
+  value        algorithmic bytes per step / wall time per step (GB/s), with
+               bytes = 5*R*D*s + 2*D*s_gamma + 2*R*4 + D*4
+  roofline     the backward launch (dominant: 3 of the 5 passes), its
+               algorithmic bytes / its average duration from HIP events on
+               the stream it runs on, against MI355X's 8 TB/s HBM peak
+  cpu_baseline the CPU oracle (op-by-op restatement of the reference path,
+               OpenMP over the host cores) on a bounded row sample
+
+Default workload: configuration c2, x [32,2048,4096] fp32 (65,536 rows of
+4096).  --config selects another configuration (c1..c4c) for exploration;
+--gpus above 1 is refused (this build runs on one GPU).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("RMSNorm fwd+bwd achieved HBM GB/s (% of peak) at [32,2048,4096]; vs host CPU")
+HBM_PEAK_GBS = 8000.0
+DEFAULT_CONFIG = "c2"
+
+
+def _device_inputs(cfg, dev, seed):
+    import torch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    R, D = cfg.rows, cfg.cols
+    x = torch.randn((R, D), generator=gen, device=dev) * cfg.x_std
+    g = torch.rand(D, generator=gen, device=dev) + 0.5
+    dy = torch.randn((R, D), generator=gen, device=dev)
+    if cfg.outlier_p > 0:
+        mask = torch.rand((R, D), generator=gen, device=dev) < cfg.outlier_p
+        x = torch.where(mask, x * cfg.outlier_scale, x)
+        del mask
+    if cfg.dtype == "bf16":
+        x, g, dy = x.bfloat16(), g.bfloat16(), dy.bfloat16()
+    return x.contiguous(), g.contiguous(), dy.contiguous()
+
+
+def _traffic(config_name):
+    """HBM bytes per backward launch measured with rocprofv3 --pmc, if recorded."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config_name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        rec = json.load(fh)
+    return rec.get("bwd_hbm_bytes_per_launch")
+
+
+def cpu_baseline(cfg, seconds):
+    import numpy as np
+
+    import oracle
+    from cgadimpl_amd import configs
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    oracle.set_threads(threads)
+    sample_rows = max(1, min(cfg.rows, (4 << 20) // cfg.cols))  # ~4M elements
+    shape = (sample_rows, cfg.cols)
+    x, g, dy = configs.config_inputs(cfg, shape)
+    def one():
+        _, inv = oracle.fwd(x, g, cfg.eps)
+        oracle.bwd(x, g, inv, dy)
+    one()  # warm-up (page-in, thread pool)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    s = cfg.storage_bytes
+    R, D = sample_rows, cfg.cols
+    sample_bytes = 5 * R * D * s + 2 * D * s + 2 * R * 4 + D * 4
+    gbs = sample_bytes * reps / el / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{R} of {cfg.rows} rows x {D} {cfg.dtype}, fwd+bwd of the oracle's "
+                   f"op-by-op restatement of the reference path (every intermediate "
+                   f"materialised), {reps} reps in {el:.1f} s; rows/s "
+                   f"{R * reps / el:.4g}"),
+    }
+
+
+def run(cfg_name, steps, warmup, cpu_seconds):
+    import torch
+
+    import cgadimpl_amd as agk
+    from cgadimpl_amd import configs
+
+    cfg = configs.CONFIGS[cfg_name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    R, D = cfg.rows, cfg.cols
+    per_set = (4 if cfg.dtype == "f32" else 2) * R * D * 4  # x, dy, y, dx
+    # rotate input/output sets so that small configurations are not served
+    # from the 256 MB Infinity Cache between steps
+    nsets = max(1, min(8, math.ceil((2 << 30) / per_set)))
+    sets = []
+    for i in range(nsets):
+        x, g, dy = _device_inputs(cfg, dev, cfg.seed + i)
+        y = torch.empty_like(x)
+        inv = torch.empty(R, dtype=torch.float32, device=dev)
+        dx = torch.empty_like(x)
+        dg = torch.empty(D, dtype=torch.float32, device=dev)
+        sets.append((x, g, dy, y, inv, dx, dg))
+    ws = torch.empty(max(1, agk.rmsnorm_bwd_workspace_bytes(R, D)), dtype=torch.uint8,
+                     device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        x, g, dy, y, inv, dx, dg = sets[i % nsets]
+        if ev is not None:
+            ev[0].record(stream)
+        agk.rmsnorm_fwd(x, g, cfg.eps, y=y, inv_rms=inv, stream=stream)
+        if ev is not None:
+            ev[1].record(stream)
+        agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=stream)
+        if ev is not None:
+            ev[2].record(stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
+    ms_per_step = wall * 1e3 / steps
+    alg = cfg.algorithmic_bytes()
+    value = alg / (ms_per_step * 1e-3) / 1e9
+    bwd_gbs = cfg.bwd_bytes() / (bwd_ms * 1e-3) / 1e9
+    fwd_gbs = cfg.fwd_bytes() / (fwd_ms * 1e-3) / 1e9
+    traffic = _traffic(cfg_name)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.dtype,
+        "data": ("synthetic: x~N(0,%g), gamma~U(0.5,1.5), dy~N(0,1) drawn on the device "
+                 "(torch Philox), %d rotating input sets" % (cfg.x_std, nsets)),
+        "config": {
+            "workload": f"{cfg.name}: RMSNorm layer fwd+VJP x{list(cfg.shape)} {cfg.dtype}, "
+                        f"eps {cfg.eps:g}",
+            "rows": R,
+            "cols": D,
+            "algorithmic_bytes_per_step": alg,
+            "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+            "rows_per_s": round(R / (ms_per_step * 1e-3), 1),
+        },
+        "roofline": {
+            "kernel": "agk_rmsnorm_bwd (rms_bwd_resident + dgamma_finalize)",
+            "bound": "hbm",
+            "achieved": round(bwd_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": cfg.bwd_bytes(),
+            "avg_launch_ms": round(bwd_ms, 5),
+        },
+        "kernels": {
+            "fwd": {"avg_ms": round(fwd_ms, 5), "alg_bytes": cfg.fwd_bytes(),
+                    "gbs": round(fwd_gbs, 2), "frac": round(fwd_gbs / HBM_PEAK_GBS, 4)},
+            "bwd": {"avg_ms": round(bwd_ms, 5), "alg_bytes": cfg.bwd_bytes(),
+                    "gbs": round(bwd_gbs, 2), "frac": round(bwd_gbs / HBM_PEAK_GBS, 4)},
+        },
+        "cpu_baseline": None,
+    }
+    del sets, ws
+    torch.cuda.empty_cache()
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline(cfg, cpu_seconds)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default=DEFAULT_CONFIG,
+                    help="c1, c2 (default, the headline), c3, c4a, c4b, c4c, or 'all'")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU baseline budget in seconds (0 disables it)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        rank = int(os.environ.get("RANK", "0"))
+        if rank == 0:
+            print(f"bench.py: this build runs the RMSNorm path on one GPU; --gpus {args.gpus} "
+                  f"(WORLD_SIZE {world}) is not supported. Rows shard across GPUs with no "
+                  "communication except one dgamma reduction; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    from cgadimpl_amd import configs
+    names = list(configs.CONFIGS) if args.config == "all" else [args.config]
+    for name in names:
+        rec = run(name, args.steps, args.warmup,
+                  args.cpu_seconds if name == DEFAULT_CONFIG or args.config != "all" else 0)
+        print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,189 @@
+"""cgadimpl_amd -- MI355X (gfx950) RMSNorm layer path for cgadimpl's autodiff API.
+
+The product is native: HIP kernels behind the C ABI in ``include/agk_rmsnorm.h``
+(``lib/libagk_rmsnorm.so``) and the C++ ``ag::`` layer above it.  This Python
+module is plumbing for tests and benchmarks: it binds that C ABI with ctypes
+and hands it torch device tensors (memory) and the current HIP stream.  There
+is no Python or CPU fallback: if the library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+__all__ = [
+    "AgkError", "lib", "lib_path", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_bwd_workspace_bytes",
+    "mul_rowbcast_fwd", "mul_rowbcast_bwd", "AGK_F32", "AGK_BF16", "STATUS",
+]
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(_PKG, "lib")
+
+AGK_F32 = 0
+AGK_BF16 = 1
+STATUS = {0: "AGK_OK", 1: "AGK_EINVAL", 2: "AGK_EDTYPE", 3: "AGK_EWORKSPACE", 4: "AGK_EHIP"}
+
+# Every symbol include/agk_rmsnorm.h declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+SIGNATURES = {
+    "agk_rmsnorm_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_float, ctypes.c_int, _P]),
+    "agk_rmsnorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "agk_rmsnorm_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
+                                       ctypes.c_int, ctypes.c_int, _P]),
+    "agk_mul_rowbcast_fwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_mul_rowbcast_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "agk_mul_rowbcast_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
+                                            ctypes.c_int, ctypes.c_int, _P]),
+    "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
+    "agk_version": (ctypes.c_char_p, []),
+}
+
+
+class AgkError(RuntimeError):
+    """A non-zero agk_status returned through the C ABI."""
+
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: {STATUS.get(status, status)} ({_status_str(status)})")
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib_path() -> str:
+    return os.path.join(LIB_DIR, "libagk_rmsnorm.so")
+
+
+def lib() -> ctypes.CDLL:
+    """Load libagk_rmsnorm.so (built by __graft_entry__.build()); raise if absent."""
+    global _lib
+    if _lib is None:
+        path = lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first "
+                               "(the RMSNorm path has no fallback)")
+        handle = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _status_str(status: int) -> str:
+    try:
+        return lib().agk_status_str(status).decode()
+    except Exception:  # noqa: BLE001 - only used while formatting an error
+        return "?"
+
+
+def _check(status: int, where: str) -> None:
+    if status != 0:
+        raise AgkError(status, where)
+
+
+# ---- torch plumbing ------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dtype_code(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return AGK_F32
+    if t.dtype == torch.bfloat16:
+        return AGK_BF16
+    raise TypeError(f"unsupported storage dtype {t.dtype} (float32 or bfloat16)")
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("tensor must live on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous (row-major, normalised axis last)")
+    return t.data_ptr()
+
+
+def _stream(stream) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def rmsnorm_bwd_workspace_bytes(rows: int, cols: int) -> int:
+    return int(lib().agk_rmsnorm_bwd_workspace_bytes(rows, cols))
+
+
+def rmsnorm_fwd(x, gamma, eps: float, y=None, inv_rms=None, stream=None):
+    """y = x * rsqrt(mean(x^2, -1) + eps) * gamma; returns (y, inv_rms[rows])."""
+    torch = _torch()
+    cols = x.shape[-1] if x.dim() else 1
+    rows = x.numel() // cols if cols else 0
+    if y is None:
+        y = torch.empty_like(x)
+    if inv_rms is None:
+        inv_rms = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    rc = lib().agk_rmsnorm_fwd(_ptr(x), _ptr(gamma), _ptr(y), _ptr(inv_rms), rows, cols,
+                               float(eps), _dtype_code(x), _stream(stream))
+    _check(rc, "agk_rmsnorm_fwd")
+    return y, inv_rms
+
+
+def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate: bool = False,
+                want_dgamma: bool = True, workspace=None, stream=None):
+    """VJP of the layer; returns (dx, dgamma or None)."""
+    torch = _torch()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    if dx is None:
+        dx = torch.empty_like(x) if not accumulate else torch.zeros_like(x)
+    if want_dgamma and dgamma is None:
+        dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
+    ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols) if dgamma is not None else 0
+    if dgamma is not None and workspace is None and ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    ws_have = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    rc = lib().agk_rmsnorm_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(dy), _ptr(dx),
+                               _ptr(dgamma), _ptr(workspace), ws_have, rows, cols,
+                               _dtype_code(x), int(bool(accumulate)), _stream(stream))
+    _check(rc, "agk_rmsnorm_bwd")
+    return dx, dgamma
+
+
+def mul_rowbcast_fwd(a, b, y=None, stream=None):
+    torch = _torch()
+    cols = a.shape[-1]
+    rows = a.numel() // cols if cols else 0
+    if y is None:
+        y = torch.empty_like(a)
+    rc = lib().agk_mul_rowbcast_fwd(_ptr(a), _ptr(b), _ptr(y), rows, cols, _dtype_code(a),
+                                    _stream(stream))
+    _check(rc, "agk_mul_rowbcast_fwd")
+    return y
+
+
+def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate: bool = False, want_da: bool = True,
+                     want_db: bool = True, stream=None) -> Tuple[object, object]:
+    torch = _torch()
+    cols = a.shape[-1]
+    rows = a.numel() // cols if cols else 0
+    if want_da and da is None:
+        da = torch.empty_like(a) if not accumulate else torch.zeros_like(a)
+    if want_db and db is None:
+        db = torch.empty(cols, dtype=torch.float32, device=a.device)
+    ws = None
+    ws_bytes = int(lib().agk_mul_rowbcast_bwd_workspace_bytes(rows, cols)) if db is not None else 0
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device)
+    rc = lib().agk_mul_rowbcast_bwd(_ptr(gy), _ptr(a), _ptr(b), _ptr(da), _ptr(db), _ptr(ws),
+                                    ws_bytes, rows, cols, _dtype_code(a), int(bool(accumulate)),
+                                    _stream(stream))
+    _check(rc, "agk_mul_rowbcast_bwd")
+    return da, db

@@ -1,0 +1,132 @@
+"""C ABI of libagk_rmsnorm.so, checked without a GPU.
+
+Loads the library, checks it exports every function include/agk_rmsnorm.h
+declares (and that the ctypes binding covers exactly those), and exercises
+the argument validation that runs before any HIP call: null pointers,
+negative or overflowing sizes, unknown dtypes, missing or short workspaces.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import cgadimpl_amd as agk
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "agk_rmsnorm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(agk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    fns = declared_functions()
+    for want in ("agk_rmsnorm_fwd", "agk_rmsnorm_bwd", "agk_rmsnorm_bwd_workspace_bytes",
+                 "agk_status_str"):
+        assert want in fns
+
+
+def test_library_exports_every_declared_symbol():
+    path = agk.lib_path()
+    assert os.path.exists(path), "build first: python -c 'import __graft_entry__ as g; g.build()'"
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(ln.split()[-1] for ln in out.splitlines() if " T " in ln)
+    missing = [f for f in declared_functions() if f not in exported]
+    assert not missing, missing
+    # the ctypes binding covers exactly the header
+    assert sorted(agk.SIGNATURES) == declared_functions()
+    lib = agk.lib()
+    for f in declared_functions():
+        assert getattr(lib, f) is not None
+
+
+def test_status_strings_and_version():
+    lib = agk.lib()
+    for code, name in agk.STATUS.items():
+        assert lib.agk_status_str(code).decode().startswith(name)
+    assert b"unknown" in lib.agk_status_str(99)
+    assert b"gfx950" in lib.agk_version()
+
+
+def test_workspace_bytes_rule():
+    lib = agk.lib()
+    ws = lib.agk_rmsnorm_bwd_workspace_bytes
+    assert ws(0, 4096) == 0 and ws(16, 0) == 0 and ws(-1, 4) == 0 and ws(4, -1) == 0
+    # rows per block = max(16, ceil(rows / 1024)); one fp32 partial row per block
+    assert ws(65536, 4096) == 1024 * 4096 * 4
+    assert ws(512, 512) == 32 * 512 * 4
+    assert ws(51, 13824) == 4 * 13824 * 4
+    assert ws(1048576, 128) == 1024 * 128 * 4
+    assert ws(7161, 5120) == ((7161 + 15) // 16) * 5120 * 4
+    assert lib.agk_mul_rowbcast_bwd_workspace_bytes(65536, 4096) == ws(65536, 4096)
+
+
+FAKE = 0x1000  # never dereferenced: validation rejects before any HIP call
+
+
+def test_fwd_argument_validation():
+    lib = agk.lib()
+    f = lib.agk_rmsnorm_fwd
+    assert f(FAKE, None, FAKE, FAKE, -1, 8, 1e-6, 0, None) == 1
+    assert f(FAKE, None, FAKE, FAKE, 8, -1, 1e-6, 0, None) == 1
+    assert f(FAKE, None, FAKE, FAKE, 8, 2 ** 31, 1e-6, 0, None) == 1     # cols > INT_MAX
+    assert f(FAKE, None, FAKE, FAKE, 2 ** 62, 2 ** 20, 1e-6, 0, None) == 1  # rows*cols overflow
+    assert f(FAKE, None, FAKE, FAKE, 8, 8, 1e-6, 7, None) == 2            # dtype
+    assert f(None, None, FAKE, FAKE, 8, 8, 1e-6, 0, None) == 1
+    assert f(FAKE, None, None, FAKE, 8, 8, 1e-6, 0, None) == 1
+    assert f(FAKE, None, FAKE, None, 8, 8, 1e-6, 1, None) == 1
+    # empty inputs are a valid no-op, null pointers allowed
+    assert f(None, None, None, None, 0, 8, 1e-6, 0, None) == 0
+    assert f(None, None, None, None, 8, 0, 1e-6, 0, None) == 0
+
+
+def test_bwd_argument_validation():
+    lib = agk.lib()
+    b = lib.agk_rmsnorm_bwd
+    args = dict(x=FAKE, g=None, inv=FAKE, dy=FAKE, dx=FAKE, dg=FAKE, ws=FAKE, wsb=1 << 30,
+                rows=64, cols=64, dt=0, acc=0)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return b(a["x"], a["g"], a["inv"], a["dy"], a["dx"], a["dg"], a["ws"], a["wsb"],
+                 a["rows"], a["cols"], a["dt"], a["acc"], None)
+
+    assert call(rows=-2) == 1
+    assert call(dt=3) == 2
+    assert call(x=None) == 1
+    assert call(inv=None) == 1
+    assert call(dy=None) == 1
+    assert call(dx=None) == 1
+    need = lib.agk_rmsnorm_bwd_workspace_bytes(64, 64)
+    assert call(ws=None) == 3
+    assert call(wsb=need - 1) == 3
+    # no dgamma requested: workspace is not needed, but data pointers still are
+    assert call(dg=None, ws=None, wsb=0, x=None) == 1
+    # empty rows with accumulate: nothing to do
+    assert call(rows=0, acc=1, x=None, inv=None, dy=None, dx=None, ws=None, wsb=0) == 0
+
+
+def test_mul_argument_validation():
+    lib = agk.lib()
+    assert lib.agk_mul_rowbcast_fwd(None, FAKE, FAKE, 4, 4, 0, None) == 1
+    assert lib.agk_mul_rowbcast_fwd(FAKE, FAKE, FAKE, 4, 4, 5, None) == 2
+    assert lib.agk_mul_rowbcast_fwd(None, None, None, 0, 4, 0, None) == 0
+    m = lib.agk_mul_rowbcast_bwd
+    assert m(None, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, 4, 4, 0, 0, None) == 1  # gy
+    assert m(FAKE, FAKE, None, FAKE, None, None, 0, 4, 4, 0, 0, None) == 1        # da needs b
+    assert m(FAKE, None, FAKE, None, FAKE, FAKE, 1 << 20, 4, 4, 0, 0, None) == 1  # db needs a
+    assert m(FAKE, FAKE, FAKE, None, FAKE, None, 0, 4, 4, 0, 0, None) == 3        # db needs ws
+    assert m(FAKE, FAKE, FAKE, None, None, None, 0, 4, 4, 0, 0, None) == 0        # nothing asked
+
+
+def test_python_binding_raises_without_gpu_tensors():
+    torch = pytest.importorskip("torch")
+    x = torch.zeros(4, 8)
+    with pytest.raises(ValueError):
+        agk.rmsnorm_fwd(x, None, 1e-6, y=x, inv_rms=torch.zeros(4))
