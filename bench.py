@@ -206,6 +206,23 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     return out
 
 
+def copy_probe(mib, steps):
+    """Device-to-device copies of a known size (torch's copy kernel).
+
+    Under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE this gives the counter's
+    reading for exactly mib MiB read and mib MiB written per dispatch, the
+    factor that turns the counters into HBM bytes for the RMSNorm kernels.
+    """
+    import torch
+    n = (mib << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": n * 4, "dispatches": steps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,7 +232,12 @@ def main():
                     help="c1, c2 (default, the headline), c3, c4a, c4b, c4c, or 'all'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline budget in seconds (0 disables it)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run MIB-MiB device copies (counter calibration), then exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe, args.steps)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -14,7 +14,7 @@ from typing import Optional, Tuple
 
 __all__ = [
     "AgkError", "lib", "lib_path", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_bwd_workspace_bytes",
-    "mul_rowbcast_fwd", "mul_rowbcast_bwd", "AGK_F32", "AGK_BF16", "STATUS",
+    "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -36,7 +36,9 @@ SIGNATURES = {
     "agk_mul_rowbcast_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_mul_rowbcast_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
                                             ctypes.c_int, ctypes.c_int, _P]),
+    "agk_rmsnorm_launch_plan": (ctypes.c_int, [_I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
+    "agk_last_error": (ctypes.c_char_p, []),
     "agk_version": (ctypes.c_char_p, []),
 }
 
@@ -46,7 +48,13 @@ class AgkError(RuntimeError):
 
     def __init__(self, status: int, where: str):
         self.status = status
-        super().__init__(f"{where}: {STATUS.get(status, status)} ({_status_str(status)})")
+        detail = _status_str(status)
+        if status == 4:
+            try:
+                detail += "; HIP: " + lib().agk_last_error().decode()
+            except Exception:  # noqa: BLE001 - only used while formatting an error
+                pass
+        super().__init__(f"{where}: {STATUS.get(status, status)} ({detail})")
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -64,6 +72,12 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first "
                                "(the RMSNorm path has no fallback)")
+        # torch ships its own HIP runtime (SONAME libamdhip64.so.7) and links it
+        # by the name libamdhip64.so.  Loading torch first makes this library's
+        # libamdhip64.so.7 dependency resolve to that same runtime; loading this
+        # library first would bring in /opt/rocm's copy, torch would then load
+        # a second runtime beside it, and one of the two sees no device.
+        import torch  # noqa: F401
         handle = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)
@@ -155,6 +169,14 @@ def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate: bool = 
                                _dtype_code(x), int(bool(accumulate)), _stream(stream))
     _check(rc, "agk_rmsnorm_bwd")
     return dx, dgamma
+
+
+def launch_plan(rows: int, cols: int, dtype: int, backward: bool) -> dict:
+    """The launch shape agk_rmsnorm_{fwd,bwd} picks for these sizes (diagnostic)."""
+    out = (ctypes.c_int32 * 5)()
+    _check(lib().agk_rmsnorm_launch_plan(rows, cols, dtype, int(bool(backward)), out),
+           "agk_rmsnorm_launch_plan")
+    return {"tpr": out[0], "nv": out[1], "g": out[2], "rpb": out[3], "nblk": out[4]}
 
 
 def mul_rowbcast_fwd(a, b, y=None, stream=None):

@@ -44,7 +44,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBlock = 256;          // threads per workgroup (TPR <= 256)
 constexpr int kTargetBlocks = 1024;  // backward row blocks (sets partial rows)
-constexpr int kMinRowsPerBlock = 16;
+constexpr int kMinRowsPerBlockLarge = 4;     // once rows >= kLargeRows / 8
+constexpr int64_t kLargeRows = 16384;        // plan switch: more rows than this
+                                             // keep enough workgroups with fewer
+                                             // lanes in flight per row
 
 // ---- storage types --------------------------------------------------------
 
@@ -104,13 +107,22 @@ __device__ __forceinline__ void opaque(u32x4& a, u32x4& b) {
     asm volatile("" : "+v"(a), "+v"(b));
 }
 
+// 16-byte accesses.  load16 is for data that is reused (gamma); the
+// stream variants set the non-temporal bit, for row data that each kernel
+// touches exactly once, so it does not displace reused lines in L2 and the
+// Infinity Cache (measured on MI355X: a plain 16-byte copy kernel moves
+// 6.2 TB/s, the same kernel with non-temporal loads and stores 6.5 TB/s).
 template <class S>
 __device__ __forceinline__ u32x4 load16(const typename S::T* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
 template <class S>
-__device__ __forceinline__ void store16(typename S::T* p, u32x4 v) {
-    *reinterpret_cast<u32x4*>(p) = v;
+__device__ __forceinline__ u32x4 load16_stream(const typename S::T* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+template <class S>
+__device__ __forceinline__ void store16_stream(typename S::T* p, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
 // ---- reductions -------------------------------------------------------------
@@ -124,17 +136,20 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// Row sum for a row spread over TPR lanes.  For TPR > 64 the per-wave sums go
-// through `red` (double-buffered by `parity`, so one barrier per row is
-// enough) and are added in wave order.
-template <int TPR>
-__device__ __forceinline__ float row_sum(float v, float (*red)[16], int parity) {
+// Row sum for a row spread over TPR lanes; the workgroup holds G such rows.
+// For TPR > 64 the per-wave sums go through `red` (double-buffered by
+// `parity`, so one barrier per row is enough: a wave can only overwrite a
+// slot after every wave has passed the barrier that follows its last read)
+// and are added in wave order.
+template <int TPR, int G>
+__device__ __forceinline__ float row_sum(float v, float (*red)[TPR > 64 ? G * (TPR / 64) : 1],
+                                         int parity) {
     v = group_sum<TPR>(v);
     if constexpr (TPR > 64) {
         constexpr int kWaves = TPR / 64;
         const int lane = threadIdx.x & 63;
         const int wave_in_row = (threadIdx.x % TPR) >> 6;
-        const int row_slot = threadIdx.x / TPR;  // 0 when TPR >= kBlock
+        const int row_slot = threadIdx.x / TPR;
         if (lane == 0) red[parity][row_slot * kWaves + wave_in_row] = v;
         __syncthreads();
         float s = 0.0f;
@@ -147,18 +162,18 @@ __device__ __forceinline__ float row_sum(float v, float (*red)[16], int parity) 
 
 // ---- register-resident forward ---------------------------------------------
 // y[row] = (x[row] * r) * gamma, r = 1 / sqrt(sum(x^2)/cols + eps); inv_rms[row] = r.
-// gamma == nullptr: no scale.  Requires 16-byte aligned x/y/gamma and
-// cols % S::kVec == 0, and cols <= TPR * NV * kVec.
-template <class S, int TPR, int NV>
-__global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_fwd_resident(
+// A workgroup of TPR*G lanes normalises G rows, one per TPR-lane group; each
+// lane holds NV 16-byte slots of its row (columns (t + k*TPR)*W .. +W).
+// gamma == nullptr: no scale.  Requires 16-byte aligned x/y/gamma,
+// cols % S::kVec == 0 and cols <= TPR * NV * kVec.
+template <class S, int TPR, int NV, int G>
+__global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     typename S::T* __restrict__ y, float* __restrict__ inv_rms, int64_t rows, int cols,
     float eps) {
     using T = typename S::T;
     constexpr int W = S::kVec;
-    constexpr int BLOCK = TPR > kBlock ? TPR : kBlock;
-    constexpr int G = BLOCK / TPR;
-    __shared__ float red[2][16];
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
 
     const int t = threadIdx.x % TPR;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * G + threadIdx.x / TPR;
@@ -172,7 +187,7 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_fwd_resident(
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int col = (t + k * TPR) * W;
-        xv[k] = (active && col < cols) ? load16<S>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+        xv[k] = (active && col < cols) ? load16_stream<S>(xr + col) : u32x4{0u, 0u, 0u, 0u};
         float f[W];
         S::unpack(xv[k], f);
 #pragma unroll
@@ -181,7 +196,7 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_fwd_resident(
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < W; ++e) ss += part[e];
-    ss = row_sum<TPR>(ss, red, 0);
+    ss = row_sum<TPR, G>(ss, red, 0);
 
     const float ms = ss / static_cast<float>(cols);
     const float r = 1.0f / sqrtf(ms + eps);
@@ -204,29 +219,48 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_fwd_resident(
 #pragma unroll
                 for (int e = 0; e < W; ++e) f[e] = f[e] * r;
             }
-            store16<S>(yr + col, S::pack(f));
+            store16_stream<S>(yr + col, S::pack(f));
         }
     }
 }
 
 // ---- register-resident backward --------------------------------------------
-// Workgroup b owns rows [b*rpb, min(rows, (b+1)*rpb)); its TPR-lane groups
-// take rows round-robin.  Per row:
+// Workgroup b owns rows [b*rpb, min(rows, (b+1)*rpb)); its G groups of TPR
+// lanes take rows round-robin (group q: rows b*rpb + q, + G, + 2G, ...).
+// Per row:
 //   g = dy*gamma, dot = sum(g*x), dx (+)= r*(g - x*(r*r*dot/cols))
 // and, when partials != nullptr, each lane accumulates dy*(x*r) for the
-// columns it owns; the groups' sums are added in group order into
-// partials[b][*].
-template <class S, int TPR, int NV>
-__global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
+// columns it owns.  At the end the G groups' sums are added in group order
+// (through LDS) into partials[b][*], one fp32 row per workgroup.
+// With PF the loop is software-pipelined: the loads of a group's next row are
+// issued before the current row's reduction, so HBM traffic overlaps the
+// barrier and the arithmetic.  Without PF (wide rows, where the second set of
+// row registers would not fit) each row is loaded when it is processed.
+// gamma is read once per lane and kept in registers.
+template <class S, int TPR, int NV, int G>
+__device__ __forceinline__ void load_row_slots(const typename S::T* __restrict__ x,
+                                               const typename S::T* __restrict__ dy,
+                                               int64_t off, bool active, int cols, int t,
+                                               u32x4 (&xv)[NV], u32x4 (&dv)[NV]) {
+    constexpr int W = S::kVec;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = (t + k * TPR) * W;
+        const bool ok = active && col < cols;
+        xv[k] = ok ? load16_stream<S>(x + off + col) : u32x4{0u, 0u, 0u, 0u};
+        dv[k] = ok ? load16_stream<S>(dy + off + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+template <class S, int TPR, int NV, int G, bool PF>
+__global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
     typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
     int64_t rpb, int accumulate) {
     constexpr int W = S::kVec;
-    constexpr int BLOCK = TPR > kBlock ? TPR : kBlock;
-    constexpr int G = BLOCK / TPR;
-    __shared__ float red[2][16];
-    extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
+    extern __shared__ float lds_part[];  // [cols] when G > 1 and partials
 
     const int t = threadIdx.x % TPR;
     const int grp = threadIdx.x / TPR;
@@ -236,38 +270,50 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
     const bool want_dg = partials != nullptr;
     const float inv_cols = 1.0f / static_cast<float>(cols);
 
+    u32x4 gv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = (t + k * TPR) * W;
+        gv[k] = (gamma && col < cols) ? load16<S>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+
     float dg[NV][W];
 #pragma unroll
     for (int k = 0; k < NV; ++k)
 #pragma unroll
         for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
 
+    int64_t row = row_begin + grp;
+    bool active = row < row_end;
+    u32x4 xv[NV], dv[NV];
+    load_row_slots<S, TPR, NV, G>(x, dy, (active ? row : 0) * static_cast<int64_t>(cols), active,
+                                  cols, t, xv, dv);
+    float r = active ? inv_rms[row] : 0.0f;
+
     for (int64_t it = 0; it < niter; ++it) {
-        const int64_t row = row_begin + it * G + grp;
-        const bool active = row < row_end;
-        const int64_t off = (active ? row : 0) * static_cast<int64_t>(cols);
-        u32x4 xv[NV], dv[NV];
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int col = (t + k * TPR) * W;
-            const bool ok = active && col < cols;
-            xv[k] = ok ? load16<S>(x + off + col) : u32x4{0u, 0u, 0u, 0u};
-            dv[k] = ok ? load16<S>(dy + off + col) : u32x4{0u, 0u, 0u, 0u};
+        // issue the next row's loads first
+        const int64_t nrow = row + G;
+        const bool nactive = nrow < row_end;
+        u32x4 xn[NV], dn[NV];
+        float rn = 0.0f;
+        if constexpr (PF) {
+            load_row_slots<S, TPR, NV, G>(x, dy,
+                                          (nactive ? nrow : 0) * static_cast<int64_t>(cols),
+                                          nactive, cols, t, xn, dn);
+            rn = nactive ? inv_rms[nrow] : 0.0f;
         }
-        const float r = active ? inv_rms[row] : 0.0f;
 
         float part[W];
 #pragma unroll
         for (int e = 0; e < W; ++e) part[e] = 0.0f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const int col = (t + k * TPR) * W;
             float fx[W], fd[W];
             S::unpack(xv[k], fx);
             S::unpack(dv[k], fd);
-            if (gamma && col < cols) {
+            if (gamma) {
                 float gm[W];
-                S::unpack(load16<S>(gamma + col), gm);
+                S::unpack(gv[k], gm);
 #pragma unroll
                 for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
             }
@@ -277,7 +323,7 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
         float dot = 0.0f;
 #pragma unroll
         for (int e = 0; e < W; ++e) dot += part[e];
-        dot = row_sum<TPR>(dot, red, static_cast<int>(it & 1));
+        dot = row_sum<TPR, G>(dot, red, static_cast<int>(it & 1));
         const float s = (r * r * dot) * inv_cols;
         // Re-derive the unpacked values from the raw slots after the
         // reduction instead of keeping both copies live across it.
@@ -285,6 +331,7 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
         for (int k = 0; k < NV; ++k) opaque(xv[k], dv[k]);
 
         if (active) {
+            const int64_t off = row * static_cast<int64_t>(cols);
 #pragma unroll
             for (int k = 0; k < NV; ++k) {
                 const int col = (t + k * TPR) * W;
@@ -294,7 +341,7 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
                     S::unpack(dv[k], fd);
                     if (gamma) {
                         float gm[W];
-                        S::unpack(load16<S>(gamma + col), gm);
+                        S::unpack(gv[k], gm);
 #pragma unroll
                         for (int e = 0; e < W; ++e) gk[e] = fd[e] * gm[e];
                     } else {
@@ -306,11 +353,11 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
                     for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
                     if (accumulate) {
                         float old[W];
-                        S::unpack(load16<S>(dx + off + col), old);
+                        S::unpack(load16_stream<S>(dx + off + col), old);
 #pragma unroll
                         for (int e = 0; e < W; ++e) o[e] = old[e] + o[e];
                     }
-                    store16<S>(dx + off + col, S::pack(o));
+                    store16_stream<S>(dx + off + col, S::pack(o));
                     if (want_dg) {
 #pragma unroll
                         for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
@@ -318,6 +365,21 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
                 }
             }
         }
+        if constexpr (PF) {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                xv[k] = xn[k];
+                dv[k] = dn[k];
+            }
+            r = rn;
+        } else if (it + 1 < niter) {
+            load_row_slots<S, TPR, NV, G>(x, dy,
+                                          (nactive ? nrow : 0) * static_cast<int64_t>(cols),
+                                          nactive, cols, t, xv, dv);
+            r = nactive ? inv_rms[nrow] : 0.0f;
+        }
+        row = nrow;
+        active = nactive;
     }
 
     if (!want_dg) return;
@@ -332,21 +394,23 @@ __global__ __launch_bounds__(TPR > kBlock ? TPR : kBlock) void rms_bwd_resident(
             }
         }
     } else {
+        // groups add their sums into one LDS row in group order
+#pragma unroll 1
+        for (int q = 0; q < G; ++q) {
+            if (grp == q) {
 #pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int col = (t + k * TPR) * W;
-            if (col < cols) {
+                for (int k = 0; k < NV; ++k) {
+                    const int col = (t + k * TPR) * W;
+                    if (col < cols) {
 #pragma unroll
-                for (int e = 0; e < W; ++e) lds_part[grp * cols + col + e] = dg[k][e];
+                        for (int e = 0; e < W; ++e)
+                            lds_part[col + e] = q == 0 ? dg[k][e] : lds_part[col + e] + dg[k][e];
+                    }
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
-        for (int c = threadIdx.x; c < cols; c += BLOCK) {
-            float acc = lds_part[c];
-#pragma unroll
-            for (int q = 1; q < G; ++q) acc += lds_part[q * cols + c];
-            prow[c] = acc;
-        }
+        for (int c = threadIdx.x; c < cols; c += TPR * G) prow[c] = lds_part[c];
     }
 }
 
@@ -360,7 +424,7 @@ __global__ __launch_bounds__(kBlock) void rms_fwd_looped(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     typename S::T* __restrict__ y, float* __restrict__ inv_rms, int64_t rows, int cols,
     float eps) {
-    __shared__ float red[2][16];
+    __shared__ float red[2][kBlock / 64];
     const int64_t row = blockIdx.x;
     if (row >= rows) return;  // block-uniform
     const int64_t off = row * static_cast<int64_t>(cols);
@@ -369,7 +433,7 @@ __global__ __launch_bounds__(kBlock) void rms_fwd_looped(
         const float v = S::get(x + off + c);
         ss += v * v;
     }
-    ss = row_sum<kBlock>(ss, red, 0);
+    ss = row_sum<kBlock, 1>(ss, red, 0);
     const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     if (threadIdx.x == 0) inv_rms[row] = r;
     for (int c = threadIdx.x; c < cols; c += kBlock) {
@@ -385,7 +449,7 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
     typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
     int64_t rpb, int accumulate) {
-    __shared__ float red[2][16];
+    __shared__ float red[2][kBlock / 64];
     const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
     const float inv_cols = 1.0f / static_cast<float>(cols);
@@ -399,7 +463,7 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
             if (gamma) g = g * S::get(gamma + c);
             dot += g * S::get(x + off + c);
         }
-        dot = row_sum<kBlock>(dot, red, parity);
+        dot = row_sum<kBlock, 1>(dot, red, parity);
         const float r = inv_rms[row];
         const float s = (r * r * dot) * inv_cols;
         const bool first = row == row_begin;
@@ -431,11 +495,11 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_fwd_kernel(
     if (vec) {
         for (int c = threadIdx.x * W; c < cols; c += kBlock * W) {
             float fa[W], fb[W];
-            S::unpack(load16<S>(a + off + c), fa);
+            S::unpack(load16_stream<S>(a + off + c), fa);
             S::unpack(load16<S>(b + c), fb);
 #pragma unroll
             for (int e = 0; e < W; ++e) fa[e] = fa[e] * fb[e];
-            store16<S>(y + off + c, S::pack(fa));
+            store16_stream<S>(y + off + c, S::pack(fa));
         }
     } else {
         for (int c = threadIdx.x; c < cols; c += kBlock)
@@ -471,23 +535,40 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
 }
 
 // ---- dgamma: fixed-order column sum of the partial rows ------------------------
-// Workgroup: 64 columns x 4 row splits.  Split s sums partial rows s, s+4, ...
-// in increasing order in fp64; the 4 split sums are then added in split order.
-__global__ __launch_bounds__(kBlock) void dgamma_finalize(const float* __restrict__ partials,
-                                                          float* __restrict__ dgamma,
-                                                          int64_t nblk, int cols,
-                                                          int accumulate) {
-    __shared__ double red[4][64];
+// Workgroup: 64 columns x kFinSplits row splits.  Split s sums partial rows
+// s, s + kFinSplits, ... in increasing order in fp64; the split sums are then
+// added in split order.  The order depends only on nblk, never on timing.
+constexpr int kFinSplits = 16;
+
+__global__ __launch_bounds__(64 * kFinSplits) void dgamma_finalize(
+    const float* __restrict__ partials, float* __restrict__ dgamma, int64_t nblk, int cols,
+    int accumulate) {
+    __shared__ double red[kFinSplits][64];
     const int lane = threadIdx.x & 63;
     const int split = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + lane;
     double acc = 0.0;
-    if (c < cols)
-        for (int64_t b = split; b < nblk; b += 4) acc += partials[b * cols + c];
+    if (c < cols) {
+        int64_t b = split;
+        // four independent loads in flight per step, added in row order
+        for (; b + 3 * kFinSplits < nblk; b += 4 * kFinSplits) {
+            const float p0 = partials[b * cols + c];
+            const float p1 = partials[(b + kFinSplits) * cols + c];
+            const float p2 = partials[(b + 2 * kFinSplits) * cols + c];
+            const float p3 = partials[(b + 3 * kFinSplits) * cols + c];
+            acc += p0;
+            acc += p1;
+            acc += p2;
+            acc += p3;
+        }
+        for (; b < nblk; b += kFinSplits) acc += partials[b * cols + c];
+    }
     red[split][lane] = acc;
     __syncthreads();
     if (split == 0 && c < cols) {
-        const double tot = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+        double tot = red[0][lane];
+#pragma unroll
+        for (int q = 1; q < kFinSplits; ++q) tot += red[q][lane];
         const float v = static_cast<float>(tot);
         dgamma[c] = accumulate ? dgamma[c] + v : v;
     }
@@ -500,72 +581,125 @@ __global__ __launch_bounds__(kBlock) void fill_zero_f32(float* __restrict__ p, i
 
 // ---- launch plans -------------------------------------------------------------
 
-struct RowPlan {
-    int tpr = 0;  // lanes per row; 0 = looped kernel
-    int nv = 0;   // 16-byte slots per lane
+// A resident launch shape: TPR lanes per row, NV 16-byte slots per lane, G
+// rows in flight per workgroup (workgroup = TPR * G lanes).
+struct Plan {
+    int tpr = 0;  // 0 = looped kernel
+    int nv = 0;
+    int g = 0;
 };
 
-// (TPR, NV) pairs with resident instantiations.  Every entry compiles
-// without register spills for both storage types (checked with
-// -Rpass-analysis=kernel-resource-usage); wider rows take the looped kernels.
-#define AGK_FWD_SHAPES(X) \
-    X(1, 1) X(2, 1) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) \
-    X(64, 2) X(64, 4) X(64, 8) X(64, 16) \
-    X(128, 8) X(128, 16) \
-    X(256, 8) X(256, 16) \
-    X(512, 8) X(512, 16) \
-    X(1024, 8)
+// Instantiated shapes.  Each compiles without register spills for both
+// storage types (hipcc -Rpass-analysis=kernel-resource-usage); wider rows
+// take the looped kernels.
+#define AGK_FWD_SHAPES(X)                                                                  \
+    X(1, 1, 256) X(2, 1, 128) X(4, 1, 64) X(8, 1, 32) X(16, 1, 16) X(32, 1, 16) X(64, 1, 8) \
+    X(64, 2, 4) X(64, 4, 4) X(128, 2, 2) X(128, 4, 2) X(256, 2, 1) X(256, 4, 1)            \
+    X(512, 2, 1) X(512, 4, 1) X(1024, 2, 1) X(1024, 4, 1) X(1024, 8, 1)
 
-#define AGK_BWD_SHAPES(X) \
-    X(1, 1) X(2, 1) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) \
-    X(64, 2) X(64, 4) X(64, 8) \
-    X(128, 4) X(128, 8) \
-    X(256, 4) X(256, 8) \
-    X(512, 4) X(512, 8) \
-    X(1024, 4)
+// (TPR, NV, G, prefetch).  Prefetching shapes hold two rows' slots per lane;
+// the widest shapes hold one.
+#define AGK_BWD_SHAPES(X)                                                                  \
+    X(1, 1, 256, 1) X(2, 1, 128, 1) X(4, 1, 64, 1) X(8, 1, 32, 1) X(16, 1, 16, 1)          \
+    X(32, 1, 32, 1) X(64, 1, 4, 1) X(64, 2, 4, 1) X(128, 2, 2, 1) X(256, 2, 2, 1)         \
+    X(512, 2, 2, 1) X(1024, 2, 1, 1) X(1024, 4, 1, 0)
 
-struct Shape2 { int tpr, nv; };
-constexpr Shape2 kFwdShapes[] = {
-#define AGK_X(a, b) {a, b},
+struct Shape3 { int tpr, nv, g; };
+constexpr Shape3 kFwdShapes[] = {
+#define AGK_X(a, b, c) {a, b, c},
     AGK_FWD_SHAPES(AGK_X)
 #undef AGK_X
 };
-constexpr Shape2 kBwdShapes[] = {
-#define AGK_X(a, b) {a, b},
+constexpr Shape3 kBwdShapes[] = {
+#define AGK_X(a, b, c, d) {a, b, c},
     AGK_BWD_SHAPES(AGK_X)
 #undef AGK_X
 };
 
-// Pick the resident shape for a row of `nslot` 16-byte slots.  Among shapes
-// that fit, prefer the highest slot utilisation, then the smaller TPR (no
-// cross-wave exchange).  For the backward, `lds_cap` bounds the
-// [groups][cols] fp32 combine buffer.
 template <size_t N>
-inline RowPlan choose_plan(const Shape2 (&shapes)[N], int64_t nslot, int64_t cols,
-                           int64_t lds_cap) {
-    RowPlan best;
-    double best_util = -1.0;
-    for (const Shape2& s : shapes) {
-        const int64_t need_nv = (nslot + s.tpr - 1) / s.tpr;
-        if (need_nv > s.nv) continue;
-        if (s.nv > 1 && need_nv <= s.nv / 2) continue;  // a smaller NV fits
-        const int groups = s.tpr >= kBlock ? 1 : kBlock / s.tpr;
-        if (lds_cap > 0 && groups > 1 && groups * cols * 4 > lds_cap) continue;
-        const double util = static_cast<double>(nslot) / (static_cast<double>(s.tpr) * s.nv);
-        if (util > best_util + 1e-9) {
-            best_util = util;
-            best.tpr = s.tpr;
-            best.nv = s.nv;
+inline bool has_shape(const Shape3 (&shapes)[N], const Plan& p) {
+    for (const Shape3& s : shapes)
+        if (s.tpr == p.tpr && s.nv == p.nv && s.g == p.g) return true;
+    return false;
+}
+
+inline int pow2_at_least(int64_t v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+// Resident shapes, chosen from the row width in 16-byte slots (nslot) and the
+// row count (measured on MI355X with a sweep of every instantiated shape):
+//  - rows of at most 64 slots: one slot per lane, TPR = nslot rounded up to a
+//    power of two, several rows per workgroup;
+//  - wider rows: NV slots per lane, TPR = nslot / NV rounded up.  With many
+//    rows NV = 2 (more lanes in flight per row); with fewer rows NV = 4, so
+//    the grid still has enough workgroups.  NV doubles when a row would need
+//    more than 1024 lanes.
+// Returns tpr = 0 (looped kernel) when no instantiated shape holds the row.
+template <size_t N>
+inline Plan pick_plan(const Shape3 (&shapes)[N], int64_t nslot, int nv0, int small_threads,
+                      int max_nv) {
+    Plan p;
+    if (nslot <= 64) {
+        p.tpr = pow2_at_least(nslot);
+        p.nv = 1;
+        p.g = p.tpr >= 32 ? small_threads / p.tpr : 256 / p.tpr;
+    } else {
+        int nv = nv0;
+        int64_t tpr = pow2_at_least((nslot + nv - 1) / nv);
+        while (tpr > 1024 && nv < max_nv) {
+            nv <<= 1;
+            tpr = pow2_at_least((nslot + nv - 1) / nv);
         }
+        if (tpr > 1024) return Plan{};
+        if (tpr < 64) {
+            tpr = 64;
+            nv = pow2_at_least((nslot + 63) / 64);
+        }
+        p.tpr = static_cast<int>(tpr);
+        p.nv = nv;
+        p.g = tpr >= 256 ? 1 : static_cast<int>(256 / tpr);
     }
-    return best;
+    if (has_shape(shapes, p)) return p;
+    for (const Shape3& s : shapes)  // same (TPR, NV), another G
+        if (s.tpr == p.tpr && s.nv == p.nv) return Plan{s.tpr, s.nv, s.g};
+    return Plan{};
+}
+
+inline Plan fwd_plan(int64_t nslot, int64_t rows) {
+    return pick_plan(kFwdShapes, nslot, rows > kLargeRows ? 2 : 4, 512, 8);
+}
+
+// Backward shapes that are not built for a storage type: bf16 unpacks to
+// twice the floats per slot, and the widest shape would spill registers.
+template <class S>
+constexpr bool bwd_shape_enabled(int tpr, int nv) {
+    return !(std::is_same<S, BF16>::value && tpr == 1024 && nv == 4);
+}
+
+template <class S>
+inline Plan bwd_plan(int64_t nslot, int64_t rows) {
+    Plan p = pick_plan(kBwdShapes, nslot, 2, 1024, 4);
+    // many rows: two rows per workgroup where that shape exists
+    if (p.tpr >= 256 && rows > kLargeRows && has_shape(kBwdShapes, Plan{p.tpr, p.nv, 2}))
+        p.g = 2;
+    if (p.tpr != 0 && !bwd_shape_enabled<S>(p.tpr, p.nv)) return Plan{};
+    return p;
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Backward row blocking: about kTargetBlocks workgroups, each owning a run of
+// consecutive rows and writing one partial row of dgamma (at least
+// kMinRowsPerBlockLarge rows once there are enough rows, so the partial rows
+// stay a small fraction of the traffic).  Depends only on rows, so the dgamma
+// summation order is fixed by the shape.
 inline int64_t bwd_rows_per_block(int64_t rows) {
     int64_t rpb = (rows + kTargetBlocks - 1) / kTargetBlocks;
-    return rpb < kMinRowsPerBlock ? kMinRowsPerBlock : rpb;
+    if (rows >= kLargeRows / 8 && rpb < kMinRowsPerBlockLarge) rpb = kMinRowsPerBlockLarge;
+    return rpb < 1 ? 1 : rpb;
 }
 inline int64_t bwd_num_blocks(int64_t rows) {
     if (rows <= 0) return 0;
@@ -573,38 +707,86 @@ inline int64_t bwd_num_blocks(int64_t rows) {
     return (rows + rpb - 1) / rpb;
 }
 
-inline int status_from_hip(hipError_t e) { return e == hipSuccess ? AGK_OK : AGK_EHIP; }
+// The HIP error behind the calling thread's last AGK_EHIP (hipSuccess if none).
+thread_local hipError_t t_last_hip_error = hipSuccess;
+
+inline int status_from_hip(hipError_t e) {
+    if (e == hipSuccess) return AGK_OK;
+    t_last_hip_error = e;
+    return AGK_EHIP;
+}
 
 inline int check_launch() { return status_from_hip(hipGetLastError()); }
 
+// Discards an error another component left pending on this thread (HIP keeps
+// the last error until someone reads it), so that check_launch() reports only
+// failures of this library's own launches.
+inline void clear_pending_error() { (void)hipGetLastError(); }
+
 template <class S>
-int launch_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_t rows,
-               int cols, float eps, hipStream_t st) {
+int launch_fwd_plan(const Plan& p, const void* x, const void* gamma, void* y, float* inv_rms,
+                    int64_t rows, int cols, float eps, hipStream_t st) {
     using T = typename S::T;
     const T* xp = static_cast<const T*>(x);
     const T* gp = static_cast<const T*>(gamma);
     T* yp = static_cast<T*>(y);
-    const bool vec = (cols % S::kVec) == 0 && aligned16(x) && aligned16(y) &&
-                     (gamma == nullptr || aligned16(gamma));
-    RowPlan p;
-    if (vec) p = choose_plan(kFwdShapes, cols / S::kVec, cols, 0);
     if (p.tpr == 0) {
         if (rows > 0x7fffffffLL) return AGK_EINVAL;
         hipLaunchKernelGGL(rms_fwd_looped<S>, dim3(static_cast<unsigned>(rows)), dim3(kBlock), 0,
                            st, xp, gp, yp, inv_rms, rows, cols, eps);
         return check_launch();
     }
-    const int block = p.tpr > kBlock ? p.tpr : kBlock;
-    const int groups = block / p.tpr;
-    const int64_t grid = (rows + groups - 1) / groups;
+    const int64_t grid = (rows + p.g - 1) / p.g;
     if (grid > 0x7fffffffLL) return AGK_EINVAL;
-#define AGK_X(a, b)                                                                         \
-    if (p.tpr == a && p.nv == b) {                                                          \
-        hipLaunchKernelGGL((rms_fwd_resident<S, a, b>), dim3(static_cast<unsigned>(grid)),  \
-                           dim3(block), 0, st, xp, gp, yp, inv_rms, rows, cols, eps);       \
-        return check_launch();                                                              \
+#define AGK_X(a, b, c)                                                                       \
+    if (p.tpr == a && p.nv == b && p.g == c) {                                               \
+        hipLaunchKernelGGL((rms_fwd_resident<S, a, b, c>), dim3(static_cast<unsigned>(grid)), \
+                           dim3(a * c), 0, st, xp, gp, yp, inv_rms, rows, cols, eps);        \
+        return check_launch();                                                               \
     }
     AGK_FWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
+template <class S>
+int launch_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_t rows,
+               int cols, float eps, hipStream_t st) {
+    const bool vec = (cols % S::kVec) == 0 && aligned16(x) && aligned16(y) &&
+                     (gamma == nullptr || aligned16(gamma));
+    Plan p;
+    if (vec) p = fwd_plan(cols / S::kVec, rows);
+    return launch_fwd_plan<S>(p, x, gamma, y, inv_rms, rows, cols, eps, st);
+}
+
+template <class S>
+int launch_bwd_plan(const Plan& p, int64_t rpb, const void* x, const void* gamma,
+                    const float* inv_rms, const void* dy, void* dx, float* partials,
+                    int64_t rows, int cols, int accumulate, hipStream_t st) {
+    using T = typename S::T;
+    const T* xp = static_cast<const T*>(x);
+    const T* gp = static_cast<const T*>(gamma);
+    const T* dyp = static_cast<const T*>(dy);
+    T* dxp = static_cast<T*>(dx);
+    const int64_t nblk = (rows + rpb - 1) / rpb;
+    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    if (p.tpr == 0) {
+        hipLaunchKernelGGL(rms_bwd_looped<S>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0,
+                           st, xp, gp, inv_rms, dyp, dxp, partials, rows, cols, rpb, accumulate);
+        return check_launch();
+    }
+    const size_t lds = (partials && p.g > 1) ? static_cast<size_t>(cols) * 4 : 0;
+#define AGK_X(a, b, c, d)                                                                  \
+    if constexpr (bwd_shape_enabled<S>(a, b)) {                                            \
+        if (p.tpr == a && p.nv == b && p.g == c) {                                         \
+            hipLaunchKernelGGL((rms_bwd_resident<S, a, b, c, d>),                          \
+                               dim3(static_cast<unsigned>(nblk)), dim3(a * c), lds, st, xp, \
+                               gp, inv_rms, dyp, dxp, partials, rows, cols, rpb,            \
+                               accumulate);                                                \
+            return check_launch();                                                         \
+        }                                                                                  \
+    }
+    AGK_BWD_SHAPES(AGK_X)
 #undef AGK_X
     return AGK_EINVAL;
 }
@@ -613,43 +795,21 @@ template <class S>
 int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
                void* dx, float* partials, int64_t rows, int cols, int accumulate,
                hipStream_t st) {
-    using T = typename S::T;
-    const T* xp = static_cast<const T*>(x);
-    const T* gp = static_cast<const T*>(gamma);
-    const T* dyp = static_cast<const T*>(dy);
-    T* dxp = static_cast<T*>(dx);
-    const int64_t rpb = bwd_rows_per_block(rows);
-    const int64_t nblk = bwd_num_blocks(rows);
-    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
     const bool vec = (cols % S::kVec) == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) &&
                      (gamma == nullptr || aligned16(gamma));
-    RowPlan p;
-    if (vec) p = choose_plan(kBwdShapes, cols / S::kVec, cols, 60 * 1024);
-    if (p.tpr == 0) {
-        hipLaunchKernelGGL(rms_bwd_looped<S>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0,
-                           st, xp, gp, inv_rms, dyp, dxp, partials, rows, cols, rpb, accumulate);
-        return check_launch();
-    }
-    const int block = p.tpr > kBlock ? p.tpr : kBlock;
-    const int groups = block / p.tpr;
-    const size_t lds = (partials && groups > 1) ? static_cast<size_t>(groups) * cols * 4 : 0;
-#define AGK_X(a, b)                                                                          \
-    if (p.tpr == a && p.nv == b) {                                                           \
-        hipLaunchKernelGGL((rms_bwd_resident<S, a, b>), dim3(static_cast<unsigned>(nblk)),   \
-                           dim3(block), lds, st, xp, gp, inv_rms, dyp, dxp, partials, rows,  \
-                           cols, rpb, accumulate);                                           \
-        return check_launch();                                                               \
-    }
-    AGK_BWD_SHAPES(AGK_X)
-#undef AGK_X
-    return AGK_EINVAL;
+    Plan p;
+    if (vec) p = bwd_plan<S>(cols / S::kVec, rows);
+    // the G-row combine buffer must fit in LDS
+    if (p.tpr != 0 && p.g > 1 && static_cast<int64_t>(cols) * 4 > 64 * 1024) p = Plan{};
+    return launch_bwd_plan<S>(p, bwd_rows_per_block(rows), x, gamma, inv_rms, dy, dx, partials,
+                              rows, cols, accumulate, st);
 }
 
 inline int launch_finalize(const float* partials, float* dgamma, int64_t nblk, int cols,
                            int accumulate, hipStream_t st) {
     const unsigned grid = static_cast<unsigned>((cols + 63) / 64);
-    hipLaunchKernelGGL(dgamma_finalize, dim3(grid), dim3(kBlock), 0, st, partials, dgamma, nblk,
-                       cols, accumulate);
+    hipLaunchKernelGGL(dgamma_finalize, dim3(grid), dim3(64 * kFinSplits), 0, st, partials,
+                       dgamma, nblk, cols, accumulate);
     return check_launch();
 }
 
@@ -684,6 +844,7 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms, i
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
     if (rows == 0 || cols == 0) return AGK_OK;
     if (!x || !y || !inv_rms) return AGK_EINVAL;
+    clear_pending_error();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (dtype == AGK_F32)
         return launch_fwd<F32>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps, st);
@@ -703,6 +864,7 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     if (int rc = check_sizes(rows, cols)) return rc;
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    clear_pending_error();
     if (rows == 0 || cols == 0) {
         if (dgamma && !accumulate && cols > 0) return zero_fill(dgamma, cols, st);
         return AGK_OK;
@@ -730,6 +892,7 @@ int agk_mul_rowbcast_fwd(const void* a, const void* b, void* y, int64_t rows, in
     if (rows == 0 || cols == 0) return AGK_OK;
     if (!a || !b || !y) return AGK_EINVAL;
     if (rows > 0x7fffffffLL) return AGK_EINVAL;
+    clear_pending_error();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int c = static_cast<int>(cols);
     if (dtype == AGK_F32) {
@@ -758,6 +921,7 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
     if (int rc = check_sizes(rows, cols)) return rc;
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    clear_pending_error();
     if (rows == 0 || cols == 0) {
         if (db && !accumulate && cols > 0) return zero_fill(db, cols, st);
         return AGK_OK;
@@ -791,6 +955,30 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
     return launch_finalize(partials, db, nblk, c, acc, st);
 }
 
+int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
+                            int32_t* plan) {
+    using namespace agk;
+    if (int rc = check_sizes(rows, cols)) return rc;
+    if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    if (!plan) return AGK_EINVAL;
+    const int w = dtype == AGK_F32 ? F32::kVec : BF16::kVec;
+    Plan p;
+    if (cols > 0 && cols % w == 0) {
+        const int64_t nslot = cols / w;
+        if (!backward)
+            p = fwd_plan(nslot, rows);
+        else
+            p = dtype == AGK_F32 ? bwd_plan<F32>(nslot, rows) : bwd_plan<BF16>(nslot, rows);
+        if (backward && p.tpr != 0 && p.g > 1 && cols * 4 > 64 * 1024) p = Plan{};
+    }
+    plan[0] = p.tpr;
+    plan[1] = p.nv;
+    plan[2] = p.g;
+    plan[3] = backward ? static_cast<int32_t>(bwd_rows_per_block(rows)) : 0;
+    plan[4] = backward ? static_cast<int32_t>(bwd_num_blocks(rows)) : 0;
+    return AGK_OK;
+}
+
 const char* agk_status_str(int status) {
     switch (status) {
         case AGK_OK: return "AGK_OK: success";
@@ -802,6 +990,11 @@ const char* agk_status_str(int status) {
     }
 }
 
-const char* agk_version(void) { return "agk_rmsnorm 0.1 gfx950"; }
+const char* agk_last_error(void) {
+    return agk::t_last_hip_error == hipSuccess ? "no HIP error"
+                                               : hipGetErrorString(agk::t_last_hip_error);
+}
+
+const char* agk_version(void) { return "agk_rmsnorm 0.2 gfx950"; }
 
 }  // extern "C"

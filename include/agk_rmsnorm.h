@@ -67,9 +67,12 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
                     int64_t rows, int64_t cols, float eps, int dtype,
                     agk_stream_t stream);
 
-/* Bytes of workspace agk_rmsnorm_bwd needs for these sizes (fp32 dgamma
- * partials, one row of cols floats per row block).  Depends only on rows and
- * cols, never on the device, so the reduction order is the same everywhere. */
+/* Bytes of workspace agk_rmsnorm_bwd needs for these sizes: fp32 dgamma
+ * partials, one row of cols floats per row block, where a row block is
+ *   rpb = ceil(rows / 1024) rows, at least 4 once rows >= 2048,
+ * so nblk = ceil(rows / rpb) and the size is nblk * cols * 4 bytes.  Depends
+ * only on rows and cols, never on the device, so the dgamma summation order
+ * is the same everywhere.                                                    */
 size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
 /* Backward (VJP) of the RMSNorm layer.
@@ -107,8 +110,25 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
                          size_t workspace_bytes, int64_t rows, int64_t cols,
                          int dtype, int accumulate, agk_stream_t stream);
 
+/* Diagnostic, with no counterpart in the reference: the launch shape the
+ * library picks for a forward (backward = 0) or backward (backward != 0)
+ * call of these sizes with 16-byte aligned pointers.  plan[5] receives
+ *   {lanes per row, 16-byte slots per lane, rows per workgroup,
+ *    rows per dgamma block (backward), dgamma blocks (backward)};
+ * lanes per row == 0 means the looped kernel (rows that are not a whole
+ * number of 16-byte slots, or too wide to keep in registers).  Used by the
+ * tests to run every reachable shape.                                        */
+int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
+                            int32_t* plan);
+
 /* Human-readable name of a status code (static storage). */
 const char* agk_status_str(int status);
+
+/* The HIP runtime's description of the error behind the calling thread's
+ * most recent AGK_EHIP (static storage; "no HIP error" if there was none).
+ * The reference prints the CUDA error string before exiting
+ * (cgadimpl/src/runtime/cuda_graphs.cpp:12-19); here the caller decides.   */
+const char* agk_last_error(void);
 
 /* Library version string, "agk_rmsnorm <major>.<minor> gfx950". */
 const char* agk_version(void);

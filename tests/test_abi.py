@@ -54,17 +54,50 @@ def test_status_strings_and_version():
     assert b"gfx950" in lib.agk_version()
 
 
+def _blocks(rows):
+    rpb = -(-rows // 1024)
+    if rows >= 2048:
+        rpb = max(rpb, 4)
+    return -(-rows // rpb)
+
+
 def test_workspace_bytes_rule():
     lib = agk.lib()
     ws = lib.agk_rmsnorm_bwd_workspace_bytes
     assert ws(0, 4096) == 0 and ws(16, 0) == 0 and ws(-1, 4) == 0 and ws(4, -1) == 0
-    # rows per block = max(16, ceil(rows / 1024)); one fp32 partial row per block
+    # rows per block = ceil(rows / 1024), at least 4 once rows >= 2048;
+    # one fp32 partial row per block
     assert ws(65536, 4096) == 1024 * 4096 * 4
-    assert ws(512, 512) == 32 * 512 * 4
-    assert ws(51, 13824) == 4 * 13824 * 4
+    assert ws(512, 512) == 512 * 512 * 4
+    assert ws(51, 13824) == 51 * 13824 * 4
     assert ws(1048576, 128) == 1024 * 128 * 4
-    assert ws(7161, 5120) == ((7161 + 15) // 16) * 5120 * 4
+    assert ws(7161, 5120) == 1023 * 5120 * 4
+    assert ws(2048, 64) == 512 * 64 * 4
+    for rows in (1, 2, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 65535, 10 ** 7):
+        assert ws(rows, 8) == _blocks(rows) * 8 * 4, rows
+        plan = agk.launch_plan(rows, 8, agk.AGK_F32, True)
+        assert plan["nblk"] == _blocks(rows)
+        assert (plan["nblk"] - 1) * plan["rpb"] < rows <= plan["nblk"] * plan["rpb"]
     assert lib.agk_mul_rowbcast_bwd_workspace_bytes(65536, 4096) == ws(65536, 4096)
+
+
+def test_launch_plans_are_well_formed():
+    """Every reachable resident shape holds its row: lanes * slots * width >= cols."""
+    from plans import reachable_plans
+    cases = reachable_plans()
+    assert len(cases) > 20
+    for (dt, direction, tpr, nv, g), reps in cases.items():
+        w = 4 if dt == agk.AGK_F32 else 8
+        for rows, cols in reps:
+            assert tpr * nv * w >= cols
+            assert nv == 1 or tpr * nv * w // 2 < cols or tpr == 64, (tpr, nv, cols)
+            assert 64 <= tpr * g <= 1024 and (tpr & (tpr - 1)) == 0
+    # the headline shapes
+    assert agk.launch_plan(65536, 4096, agk.AGK_F32, False)["tpr"] == 512
+    assert agk.launch_plan(65536, 4096, agk.AGK_F32, True)["g"] == 2
+    # rows that are not whole 16-byte slots take the looped kernels
+    assert agk.launch_plan(64, 4098, agk.AGK_F32, False)["tpr"] == 0
+    assert agk.launch_plan(64, 4100, agk.AGK_BF16, True)["tpr"] == 0
 
 
 FAKE = 0x1000  # never dereferenced: validation rejects before any HIP call

@@ -16,7 +16,7 @@ import cgadimpl_amd as agk
 import oracle
 import pins
 from cgadimpl_amd import configs
-from gpu_util import as_f32, gpu_layer, to_dev, to_host
+from gpu_util import as_f32, check_on_device, device_inputs, gpu_layer, to_dev, to_host
 from tolerances import TOL_BF16, TOL_F32, dx_rel_err, row_rel_err, vec_rel_err
 
 pytestmark = pytest.mark.gpu
@@ -107,9 +107,11 @@ def test_width_sweep(cuda, cols, dtype):
     _compare(x, g, dy, 1e-6, got, f"sweep {dtype} {rows}x{cols}")
 
 
-@pytest.mark.parametrize("rows", [1, 15, 16, 17, 255, 1025, 16385])
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 255, 1023, 1024, 1025, 2047, 2048, 2049,
+                                  4097, 16385])
 def test_row_count_sweep(cuda, rows):
-    # ragged row blocks in the backward (16 rows per block minimum)
+    # ragged dgamma row blocks: 1 row per block up to 1024 rows, then
+    # ceil(rows / 1024) with at least 4 from 2048 rows on
     x, g, dy = configs.make_inputs((rows, 256), seed=rows)
     got = gpu_layer(x, g, dy, 1e-6, cuda)
     _compare(x, g, dy, 1e-6, got, f"rows {rows}x256")
@@ -194,71 +196,46 @@ def test_workspace_too_small_is_an_error(cuda):
     assert ei.value.status == 3
 
 
+# ---- every reachable launch shape ------------------------------------------------
+
+def _plan_cases():
+    from plans import reachable_plans
+    seen = set()
+    cases = []
+    for (dt, _direction, _tpr, _nv, _g), reps in sorted(reachable_plans().items()):
+        for rows, cols in reps:
+            key = ("f32" if dt == agk.AGK_F32 else "bf16", rows, cols)
+            if key not in seen:
+                seen.add(key)
+                cases.append(key)
+    return cases
+
+
+@pytest.mark.parametrize("dtype,rows,cols", _plan_cases(),
+                         ids=lambda v: str(v))
+def test_every_launch_shape(cuda, dtype, rows, cols):
+    """Each resident (lanes, slots, rows-per-workgroup) shape the library can pick,
+    at the narrowest and widest width that maps to it, below and above the
+    large-batch threshold."""
+    dt = agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16
+    fp, bp = agk.launch_plan(rows, cols, dt, False), agk.launch_plan(rows, cols, dt, True)
+    label = f"{dtype} {rows}x{cols} fwd{(fp['tpr'], fp['nv'], fp['g'])} bwd{(bp['tpr'], bp['nv'], bp['g'])} rpb {bp['rpb']}"
+    print(label, flush=True)
+    x, g, dy = device_inputs((rows, cols), dtype, rows * 131 + cols, cuda)
+    check_on_device(x, g, dy, 1e-6, label, _compare)
+
+
 # ---- full-size configurations: size-independent properties ----------------------
 
-def _full_inputs(cfg, dev):
-    """Full-size inputs generated on the GPU (torch's Philox) with cfg's distributions."""
-    import torch
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(cfg.seed)
-    x = torch.randn(cfg.shape, generator=gen, device=dev) * cfg.x_std
-    g = torch.rand(cfg.cols, generator=gen, device=dev) + 0.5
-    dy = torch.randn(cfg.shape, generator=gen, device=dev)
-    if cfg.outlier_p > 0:
-        mask = torch.rand(cfg.shape, generator=gen, device=dev) < cfg.outlier_p
-        x = torch.where(mask, x * cfg.outlier_scale, x)
-    if cfg.dtype == "bf16":
-        x, g, dy = x.bfloat16(), g.bfloat16(), dy.bfloat16()
-    return x.contiguous(), g.contiguous(), dy.contiguous()
-
-
 @pytest.mark.slow
-@pytest.mark.parametrize("name", ["c2", "c3", "c4a", "c4b"])
+@pytest.mark.parametrize("name", ["c2", "c3", "c4a", "c4b", "c4c"])
 def test_full_size_properties(cuda, name):
-    import torch
     cfg = configs.CONFIGS[name]
     print(f"full-size {name} {cfg.shape} {cfg.dtype}", flush=True)
-    x, g, dy = _full_inputs(cfg, cuda)
+    x, g, dy = device_inputs(cfg.shape, cfg.dtype, cfg.seed, cuda, cfg.x_std, cfg.outlier_p,
+                             cfg.outlier_scale)
     R, D = cfg.rows, cfg.cols
-    x2, dy2 = x.view(R, D), dy.view(R, D)
-    y, inv = agk.rmsnorm_fwd(x2, g, cfg.eps)
-    dx, dg = agk.rmsnorm_bwd(x2, g, inv, dy2)
-    torch.cuda.synchronize()
-
-    # 1. sampled rows against the oracle (rows are independent for y, r, dx)
-    rng = np.random.default_rng(0)
-    rows = np.unique(np.concatenate([[0, R - 1], rng.integers(0, R, 254)]))
-    idx = torch.from_numpy(rows).to(cuda)
-    xs, dys, gs = to_host(x2[idx].contiguous()), to_host(dy2[idx].contiguous()), to_host(g)
-    _compare(xs, gs, dys, cfg.eps, (to_host(y[idx].contiguous()), to_host(inv[idx]),
-                                    to_host(dx[idx].contiguous()), None),
-             f"{name} sampled rows", check_dg=False)
-
-    # 2. dgamma against an fp64 evaluation of sum_rows dy * x * r on the device
-    x64 = x2.double()
-    r64 = torch.rsqrt((x64 * x64).mean(dim=1, keepdim=True) + cfg.eps)
-    ref = (dy2.double() * x64 * r64).sum(dim=0)
-    e = vec_rel_err(to_host(dg), ref.cpu().numpy())
-    print(f"[{name}] dgamma vs fp64: {e:.2e}", flush=True)
-    assert e <= (TOL_BF16 if cfg.dtype == "bf16" else TOL_F32)
-
-    # 3. the identity sum_j x_j dx_j = dot * eps * r^3, all rows, fp64
-    gy = dy2.double() * g.double()
-    dot = (gy * x64).sum(dim=1)
-    lhs = (x64 * dx.double()).sum(dim=1)
-    rhs = dot * cfg.eps * r64.squeeze(1) ** 3
-    scale = r64.squeeze(1) * (gy * x64).abs().sum(dim=1)
-    ident = float(((lhs - rhs).abs() / scale).max())
-    print(f"[{name}] identity residual: {ident:.2e}", flush=True)
-    assert ident <= (5e-3 if cfg.dtype == "bf16" else 1e-5)
-    del x64, r64, gy
-
-    # 4. dgamma is bit-identical across runs, and dx too
-    for _ in range(2):
-        dx2, dg2 = agk.rmsnorm_bwd(x2, g, inv, dy2)
-        torch.cuda.synchronize()
-        assert torch.equal(dg2, dg)
-        assert torch.equal(dx2, dx)
+    check_on_device(x.view(R, D), g, dy.view(R, D), cfg.eps, name, _compare)
 
 
 # ---- broadcast multiply (the unfused ag::rms(x) * gamma form) ---------------------
