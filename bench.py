@@ -53,8 +53,9 @@ def _device_inputs(cfg, dev, seed):
 
 
 def _traffic(config_name):
-    """HBM bytes per backward launch measured with rocprofv3 --pmc, if recorded."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{config_name}.json")
+    """HBM bytes per backward call (FETCH_SIZE + WRITE_SIZE, scaled by a copy of
+    known size) from the committed rocprofv3 summary, if there is one."""
+    path = os.path.join(ROOT, "profiles", f"rmsnorm_{config_name}_hbm_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as fh:

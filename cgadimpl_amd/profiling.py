@@ -1,0 +1,140 @@
+"""Summaries of rocprofv3 output for the RMSNorm kernels (maintainer tool).
+
+Turns the CSV files of two kinds of rocprofv3 runs into short text summaries
+under profiles/:
+
+  kernel trace   rocprofv3 --kernel-trace --stats -T -d <dir> -o run -f csv -- <cmd>
+                 -> per-kernel calls and average / min / max duration
+  HBM traffic    rocprofv3 --pmc FETCH_SIZE ... and --pmc WRITE_SIZE ..., for the
+                 workload and for `bench.py --copy-probe MIB` (a device copy of
+                 known size), -> HBM bytes per dispatch of each kernel
+
+FETCH_SIZE and WRITE_SIZE are reported in KiB per dispatch.  Each counter is
+scaled by what it reads for the copy kernel, whose true traffic is MIB MiB
+read and MIB MiB written, so the scaled figures are bytes that actually
+crossed the HBM interface.
+
+Usage:
+  python -m cgadimpl_amd.profiling trace  <run_kernel_stats.csv> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling traffic <fetch_dir> <write_dir> <copy_fetch_dir>
+        <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
+"""
+from __future__ import annotations
+
+import csv
+import json
+import os
+import sys
+from collections import defaultdict
+
+# Kernels that make up one call of each C-ABI entry point.
+ENTRY_KERNELS = {
+    "agk_rmsnorm_fwd": ("rms_fwd_resident", "rms_fwd_looped"),
+    "agk_rmsnorm_bwd": ("rms_bwd_resident", "rms_bwd_looped", "dgamma_finalize"),
+}
+
+
+def _rows(path):
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def kernel_stats(stats_csv):
+    """{kernel: (calls, avg_ns, min_ns, max_ns)} from run_kernel_stats.csv."""
+    out = {}
+    for r in _rows(stats_csv):
+        out[r["Name"]] = (int(r["Calls"]), float(r["AverageNs"]), float(r["MinNs"]),
+                          float(r["MaxNs"]))
+    return out
+
+
+def write_trace_summary(stats_csv, out_md, command):
+    st = kernel_stats(stats_csv)
+    lines = ["# Kernel durations (rocprofv3 --kernel-trace --stats)", "",
+             "Command:", "", "```", command, "```", "",
+             "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for name, (calls, avg, mn, mx) in sorted(st.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+        lines.append(f"| {name} | {calls} | {avg / 1e3:.1f} | {mn / 1e3:.1f} | {mx / 1e3:.1f} |")
+    lines.append("")
+    for entry, kernels in ENTRY_KERNELS.items():
+        tot = sum(st[k][1] for k in kernels if k in st)
+        if tot:
+            lines.append(f"- one `{entry}` call: {tot / 1e3:.1f} us "
+                         f"({' + '.join(k for k in kernels if k in st)})")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
+def _counter_by_kernel(run_dir, counter):
+    """{kernel: [per-dispatch values]} of one counter (KiB per dispatch)."""
+    vals = defaultdict(list)
+    for r in _rows(os.path.join(run_dir, "run_counter_collection.csv")):
+        if r["Counter_Name"] == counter:
+            vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return vals
+
+
+def _median(v):
+    s = sorted(v)
+    return s[len(s) // 2]
+
+
+def traffic(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib):
+    """Scaled HBM bytes per dispatch: {kernel: (read_bytes, write_bytes)}, factors."""
+    cf = _counter_by_kernel(copy_fetch_dir, "FETCH_SIZE")
+    cw = _counter_by_kernel(copy_write_dir, "WRITE_SIZE")
+    copy_kib = copy_mib * 1024.0
+    fetch_scale = copy_kib / _median(next(v for k, v in cf.items() if "copy" in k.lower()))
+    write_scale = copy_kib / _median(next(v for k, v in cw.items() if "copy" in k.lower()))
+    f = _counter_by_kernel(fetch_dir, "FETCH_SIZE")
+    w = _counter_by_kernel(write_dir, "WRITE_SIZE")
+    out = {}
+    for k in set(f) | set(w):
+        rd = _median(f[k]) * fetch_scale * 1024.0 if k in f else 0.0
+        wr = _median(w[k]) * write_scale * 1024.0 if k in w else 0.0
+        out[k] = (rd, wr)
+    return out, fetch_scale, write_scale
+
+
+def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib,
+                          config, out_stem, command):
+    from . import configs
+    cfg = configs.CONFIGS[config]
+    per_kernel, fs, ws = traffic(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir,
+                                 copy_mib)
+    alg = {"agk_rmsnorm_fwd": cfg.fwd_bytes(), "agk_rmsnorm_bwd": cfg.bwd_bytes()}
+    lines = [f"# HBM traffic per call, configuration {config} {list(cfg.shape)} {cfg.dtype}",
+             "", "Commands (each counter in its own run):", "", "```", command, "```", "",
+             f"Counter scale from a {copy_mib} MiB device copy (`bench.py --copy-probe "
+             f"{copy_mib}`): FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {ws:.4f}.", "",
+             "| kernel | read MB | write MB |", "|---|---|---|"]
+    for k, (rd, wr) in sorted(per_kernel.items()):
+        if any(k in ks for ks in ENTRY_KERNELS.values()):
+            lines.append(f"| {k} | {rd / 1e6:.1f} | {wr / 1e6:.1f} |")
+    lines += ["", "| entry point | HBM bytes | algorithmic bytes | ratio |", "|---|---|---|---|"]
+    rec = {"config": config, "fetch_scale": fs, "write_scale": ws}
+    for entry, kernels in ENTRY_KERNELS.items():
+        tot = sum(sum(per_kernel[k]) for k in kernels if k in per_kernel)
+        lines.append(f"| {entry} | {tot:.4g} | {alg[entry]:.4g} | {tot / alg[entry]:.4f} |")
+        rec[entry.replace("agk_rmsnorm_", "") + "_hbm_bytes_per_launch"] = round(tot)
+    with open(out_stem + ".md", "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    with open(out_stem + ".json", "w") as fh:
+        json.dump(rec, fh, indent=1)
+        fh.write("\n")
+
+
+def main(argv):
+    if len(argv) >= 4 and argv[0] == "trace":
+        write_trace_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 9 and argv[0] == "traffic":
+        write_traffic_summary(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6],
+                              argv[7], argv[8])
+    else:
+        sys.stderr.write(__doc__)
+        return 2
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))
