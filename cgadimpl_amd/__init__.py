@@ -22,6 +22,9 @@ LIB_DIR = os.path.join(_PKG, "lib")
 
 AGK_F32 = 0
 AGK_BF16 = 1
+AGK_ACCUM_DX = 1
+AGK_ACCUM_DGAMMA = 2
+AGK_ACCUM_ALL = 3
 STATUS = {0: "AGK_OK", 1: "AGK_EINVAL", 2: "AGK_EDTYPE", 3: "AGK_EWORKSPACE", 4: "AGK_EHIP"}
 
 # Every symbol include/agk_rmsnorm.h declares, with its ctypes signature.
@@ -150,14 +153,24 @@ def rmsnorm_fwd(x, gamma, eps: float, y=None, inv_rms=None, stream=None):
     return y, inv_rms
 
 
-def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate: bool = False,
-                want_dgamma: bool = True, workspace=None, stream=None):
-    """VJP of the layer; returns (dx, dgamma or None)."""
+def _accum_flags(accumulate) -> int:
+    """True -> both outputs accumulate; False -> neither; an int is the bit set."""
+    if isinstance(accumulate, bool):
+        return AGK_ACCUM_ALL if accumulate else 0
+    return int(accumulate)
+
+
+def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate=False,
+                want_dgamma: bool = True, want_dx: bool = True, workspace=None, stream=None):
+    """VJP of the layer; returns (dx or None, dgamma or None).
+
+    accumulate: bool (both outputs) or agk_accumulate bits."""
     torch = _torch()
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
-    if dx is None:
-        dx = torch.empty_like(x) if not accumulate else torch.zeros_like(x)
+    acc = _accum_flags(accumulate)
+    if want_dx and dx is None:
+        dx = torch.empty_like(x) if not acc & AGK_ACCUM_DX else torch.zeros_like(x)
     if want_dgamma and dgamma is None:
         dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
     ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols) if dgamma is not None else 0
@@ -166,7 +179,7 @@ def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate: bool = 
     ws_have = workspace.numel() * workspace.element_size() if workspace is not None else 0
     rc = lib().agk_rmsnorm_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(dy), _ptr(dx),
                                _ptr(dgamma), _ptr(workspace), ws_have, rows, cols,
-                               _dtype_code(x), int(bool(accumulate)), _stream(stream))
+                               _dtype_code(x), acc, _stream(stream))
     _check(rc, "agk_rmsnorm_bwd")
     return dx, dgamma
 
@@ -191,13 +204,14 @@ def mul_rowbcast_fwd(a, b, y=None, stream=None):
     return y
 
 
-def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate: bool = False, want_da: bool = True,
+def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate=False, want_da: bool = True,
                      want_db: bool = True, stream=None) -> Tuple[object, object]:
     torch = _torch()
     cols = a.shape[-1]
     rows = a.numel() // cols if cols else 0
+    acc = _accum_flags(accumulate)
     if want_da and da is None:
-        da = torch.empty_like(a) if not accumulate else torch.zeros_like(a)
+        da = torch.empty_like(a) if not acc & AGK_ACCUM_DX else torch.zeros_like(a)
     if want_db and db is None:
         db = torch.empty(cols, dtype=torch.float32, device=a.device)
     ws = None
@@ -205,7 +219,6 @@ def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate: bool = False, want_
     if ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device)
     rc = lib().agk_mul_rowbcast_bwd(_ptr(gy), _ptr(a), _ptr(b), _ptr(da), _ptr(db), _ptr(ws),
-                                    ws_bytes, rows, cols, _dtype_code(a), int(bool(accumulate)),
-                                    _stream(stream))
+                                    ws_bytes, rows, cols, _dtype_code(a), acc, _stream(stream))
     _check(rc, "agk_mul_rowbcast_bwd")
     return da, db

@@ -257,7 +257,7 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
     typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
-    int64_t rpb, int accumulate) {
+    int64_t rpb, int acc_dx) {
     constexpr int W = S::kVec;
     __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
     extern __shared__ float lds_part[];  // [cols] when G > 1 and partials
@@ -268,6 +268,7 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
     const int64_t niter = (row_end - row_begin + G - 1) / G;  // uniform in the block
     const bool want_dg = partials != nullptr;
+    const bool want_dx = dx != nullptr;
     const float inv_cols = 1.0f / static_cast<float>(cols);
 
     u32x4 gv[NV];
@@ -303,32 +304,35 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
             rn = nactive ? inv_rms[nrow] : 0.0f;
         }
 
-        float part[W];
+        float s = 0.0f;
+        if (want_dx) {  // dot = sum(g*x) is only needed for dx (uniform branch)
+            float part[W];
 #pragma unroll
-        for (int e = 0; e < W; ++e) part[e] = 0.0f;
+            for (int e = 0; e < W; ++e) part[e] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            float fx[W], fd[W];
-            S::unpack(xv[k], fx);
-            S::unpack(dv[k], fd);
-            if (gamma) {
-                float gm[W];
-                S::unpack(gv[k], gm);
+            for (int k = 0; k < NV; ++k) {
+                float fx[W], fd[W];
+                S::unpack(xv[k], fx);
+                S::unpack(dv[k], fd);
+                if (gamma) {
+                    float gm[W];
+                    S::unpack(gv[k], gm);
 #pragma unroll
-                for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+                    for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+                }
+#pragma unroll
+                for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
             }
+            float dot = 0.0f;
 #pragma unroll
-            for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
+            for (int e = 0; e < W; ++e) dot += part[e];
+            dot = row_sum<TPR, G>(dot, red, static_cast<int>(it & 1));
+            s = (r * r * dot) * inv_cols;
+            // Re-derive the unpacked values from the raw slots after the
+            // reduction instead of keeping both copies live across it.
+#pragma unroll
+            for (int k = 0; k < NV; ++k) opaque(xv[k], dv[k]);
         }
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < W; ++e) dot += part[e];
-        dot = row_sum<TPR, G>(dot, red, static_cast<int>(it & 1));
-        const float s = (r * r * dot) * inv_cols;
-        // Re-derive the unpacked values from the raw slots after the
-        // reduction instead of keeping both copies live across it.
-#pragma unroll
-        for (int k = 0; k < NV; ++k) opaque(xv[k], dv[k]);
 
         if (active) {
             const int64_t off = row * static_cast<int64_t>(cols);
@@ -348,16 +352,18 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
 #pragma unroll
                         for (int e = 0; e < W; ++e) gk[e] = fd[e];
                     }
-                    float o[W];
+                    if (want_dx) {
+                        float o[W];
 #pragma unroll
-                    for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
-                    if (accumulate) {
-                        float old[W];
-                        S::unpack(load16_stream<S>(dx + off + col), old);
+                        for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
+                        if (acc_dx) {
+                            float old[W];
+                            S::unpack(load16_stream<S>(dx + off + col), old);
 #pragma unroll
-                        for (int e = 0; e < W; ++e) o[e] = old[e] + o[e];
+                            for (int e = 0; e < W; ++e) o[e] = old[e] + o[e];
+                        }
+                        store16_stream<S>(dx + off + col, S::pack(o));
                     }
-                    store16_stream<S>(dx + off + col, S::pack(o));
                     if (want_dg) {
 #pragma unroll
                         for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
@@ -448,7 +454,7 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
     typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
-    int64_t rpb, int accumulate) {
+    int64_t rpb, int acc_dx) {
     __shared__ float red[2][kBlock / 64];
     const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
@@ -457,23 +463,28 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
     int parity = 0;
     for (int64_t row = row_begin; row < row_end; ++row, parity ^= 1) {
         const int64_t off = row * static_cast<int64_t>(cols);
-        float dot = 0.0f;
-        for (int c = threadIdx.x; c < cols; c += kBlock) {
-            float g = S::get(dy + off + c);
-            if (gamma) g = g * S::get(gamma + c);
-            dot += g * S::get(x + off + c);
-        }
-        dot = row_sum<kBlock, 1>(dot, red, parity);
         const float r = inv_rms[row];
-        const float s = (r * r * dot) * inv_cols;
+        float s = 0.0f;
+        if (dx) {  // block-uniform
+            float dot = 0.0f;
+            for (int c = threadIdx.x; c < cols; c += kBlock) {
+                float g = S::get(dy + off + c);
+                if (gamma) g = g * S::get(gamma + c);
+                dot += g * S::get(x + off + c);
+            }
+            dot = row_sum<kBlock, 1>(dot, red, parity);
+            s = (r * r * dot) * inv_cols;
+        }
         const bool first = row == row_begin;
         for (int c = threadIdx.x; c < cols; c += kBlock) {
             const float xv = S::get(x + off + c);
             const float d = S::get(dy + off + c);
-            const float g = gamma ? d * S::get(gamma + c) : d;
-            float o = r * (g - xv * s);
-            if (accumulate) o = S::get(dx + off + c) + o;
-            S::put(dx + off + c, o);
+            if (dx) {
+                const float g = gamma ? d * S::get(gamma + c) : d;
+                float o = r * (g - xv * s);
+                if (acc_dx) o = S::get(dx + off + c) + o;
+                S::put(dx + off + c, o);
+            }
             if (prow) {
                 const float t = d * (xv * r);
                 prow[c] = first ? t : prow[c] + t;
@@ -512,7 +523,7 @@ template <class S>
 __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
     const typename S::T* __restrict__ gy, const typename S::T* __restrict__ a,
     const typename S::T* __restrict__ b, typename S::T* __restrict__ da,
-    float* __restrict__ partials, int64_t rows, int cols, int64_t rpb, int accumulate) {
+    float* __restrict__ partials, int64_t rows, int cols, int64_t rpb, int acc_da) {
     const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
     float* prow = partials ? partials + static_cast<int64_t>(blockIdx.x) * cols : nullptr;
@@ -523,7 +534,7 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
             const float g = S::get(gy + off + c);
             if (da) {
                 float o = g * S::get(b + c);
-                if (accumulate) o = S::get(da + off + c) + o;
+                if (acc_da) o = S::get(da + off + c) + o;
                 S::put(da + off + c, o);
             }
             if (prow) {
@@ -865,11 +876,15 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     clear_pending_error();
+    if (accumulate & ~AGK_ACCUM_ALL) return AGK_EINVAL;
+    const int acc_dx = (accumulate & AGK_ACCUM_DX) != 0;
+    const int acc_dg = (accumulate & AGK_ACCUM_DGAMMA) != 0;
     if (rows == 0 || cols == 0) {
-        if (dgamma && !accumulate && cols > 0) return zero_fill(dgamma, cols, st);
+        if (dgamma && !acc_dg && cols > 0) return zero_fill(dgamma, cols, st);
         return AGK_OK;
     }
-    if (!x || !inv_rms || !dy || !dx) return AGK_EINVAL;
+    if (!x || !inv_rms || !dy) return AGK_EINVAL;
+    if (!dx && !dgamma) return AGK_OK;  // nothing requested
     float* partials = nullptr;
     if (dgamma) {
         const size_t need = agk_rmsnorm_bwd_workspace_bytes(rows, cols);
@@ -878,10 +893,10 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     }
     const int c = static_cast<int>(cols);
     int rc = dtype == AGK_F32
-                 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, partials, rows, c, accumulate != 0, st)
-                 : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, partials, rows, c, accumulate != 0, st);
+                 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st)
+                 : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st);
     if (rc != AGK_OK || !dgamma) return rc;
-    return launch_finalize(partials, dgamma, bwd_num_blocks(rows), c, accumulate != 0, st);
+    return launch_finalize(partials, dgamma, bwd_num_blocks(rows), c, acc_dg, st);
 }
 
 int agk_mul_rowbcast_fwd(const void* a, const void* b, void* y, int64_t rows, int64_t cols,
@@ -922,8 +937,11 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     clear_pending_error();
+    if (accumulate & ~AGK_ACCUM_ALL) return AGK_EINVAL;
+    const int acc_da = (accumulate & AGK_ACCUM_DX) != 0;
+    const int acc_db = (accumulate & AGK_ACCUM_DGAMMA) != 0;
     if (rows == 0 || cols == 0) {
-        if (db && !accumulate && cols > 0) return zero_fill(db, cols, st);
+        if (db && !acc_db && cols > 0) return zero_fill(db, cols, st);
         return AGK_OK;
     }
     if (!gy || (da && !b) || (db && !a)) return AGK_EINVAL;
@@ -938,21 +956,20 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
     const int64_t nblk = bwd_num_blocks(rows);
     if (nblk > 0x7fffffffLL) return AGK_EINVAL;
     const int c = static_cast<int>(cols);
-    const int acc = accumulate != 0;
     if (dtype == AGK_F32) {
         hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, dim3(static_cast<unsigned>(nblk)),
                            dim3(kBlock), 0, st, static_cast<const float*>(gy),
                            static_cast<const float*>(a), static_cast<const float*>(b),
-                           static_cast<float*>(da), partials, rows, c, rpb, acc);
+                           static_cast<float*>(da), partials, rows, c, rpb, acc_da);
     } else {
         hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<BF16>, dim3(static_cast<unsigned>(nblk)),
                            dim3(kBlock), 0, st, static_cast<const uint16_t*>(gy),
                            static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
-                           static_cast<uint16_t*>(da), partials, rows, c, rpb, acc);
+                           static_cast<uint16_t*>(da), partials, rows, c, rpb, acc_da);
     }
     int rc = check_launch();
     if (rc != AGK_OK || !db) return rc;
-    return launch_finalize(partials, db, nblk, c, acc, st);
+    return launch_finalize(partials, db, nblk, c, acc_db, st);
 }
 
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,

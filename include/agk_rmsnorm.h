@@ -55,6 +55,18 @@ typedef enum {
     AGK_BF16 = 1
 } agk_dtype;
 
+/* `accumulate` argument of the backward entry points: a bit per output.
+ * A set bit adds into that output (the reference's Node::accumulate_grad,
+ * grad += g, cgadimpl/src/core/graph.cpp:44-47); a clear bit overwrites it,
+ * which is what a fresh, zero-filled reference gradient would end up holding
+ * without the caller having to zero-fill it first.  Other bits are invalid.  */
+typedef enum {
+    AGK_ACCUM_NONE = 0,
+    AGK_ACCUM_DX = 1,      /* dx (or da) += ...          */
+    AGK_ACCUM_DGAMMA = 2,  /* dgamma (or db) += ...      */
+    AGK_ACCUM_ALL = 3
+} agk_accumulate;
+
 /* Forward of the RMSNorm layer.
  * Replaces the eager forward of `ag::rms(x) * gamma`:
  *   rms_nodeops   cgadimpl/src/ops/normalization.cpp:23-35
@@ -84,10 +96,11 @@ size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
  * computing
  *   g = dy*gamma, dot = sum_j g*x, dx = r*(g - x*r*r*dot/cols),
  *   dgamma = sum_rows dy*x*r.
- * gamma == NULL means no scale.  dgamma == NULL skips the dgamma reduction.
- * accumulate == 0 writes dx and dgamma; accumulate != 0 adds into them, the
- * reference's accumulate_grad semantics.  workspace must hold at least
- * agk_rmsnorm_bwd_workspace_bytes(rows, cols) bytes when dgamma != NULL.    */
+ * gamma == NULL means no scale.  dx == NULL skips dx (only dgamma wanted);
+ * dgamma == NULL skips the dgamma reduction; both NULL is a no-op.
+ * accumulate is a set of agk_accumulate bits (AGK_ACCUM_DX, AGK_ACCUM_DGAMMA).
+ * workspace must hold at least agk_rmsnorm_bwd_workspace_bytes(rows, cols)
+ * bytes when dgamma != NULL.                                                 */
 int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms,
                     const void* dy, void* dx, float* dgamma, void* workspace,
                     size_t workspace_bytes, int64_t rows, int64_t cols,
@@ -104,7 +117,8 @@ size_t agk_mul_rowbcast_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
 /* vjp_Mul for that broadcast (autodiff_vjp_ops.cpp:54-59 with
  * reduce_for_broadcast, :15-35):  da (+)= gy*b,  db (+)= sum_rows gy*a.
- * da or db may be NULL to skip that gradient.  db is fp32.                   */
+ * da or db may be NULL to skip that gradient.  db is fp32.  accumulate:
+ * AGK_ACCUM_DX adds into da, AGK_ACCUM_DGAMMA adds into db.                 */
 int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
                          void* da, float* db, void* workspace,
                          size_t workspace_bytes, int64_t rows, int64_t cols,

@@ -135,14 +135,17 @@ def test_bwd_argument_validation():
     assert call(x=None) == 1
     assert call(inv=None) == 1
     assert call(dy=None) == 1
-    assert call(dx=None) == 1
+    assert call(acc=4) == 1          # only AGK_ACCUM_DX | AGK_ACCUM_DGAMMA bits exist
+    assert call(acc=-1) == 1
+    # neither dx nor dgamma requested: a valid no-op (dx alone may be NULL)
+    assert call(dx=None, dg=None, ws=None, wsb=0) == 0
     need = lib.agk_rmsnorm_bwd_workspace_bytes(64, 64)
     assert call(ws=None) == 3
     assert call(wsb=need - 1) == 3
     # no dgamma requested: workspace is not needed, but data pointers still are
     assert call(dg=None, ws=None, wsb=0, x=None) == 1
     # empty rows with accumulate: nothing to do
-    assert call(rows=0, acc=1, x=None, inv=None, dy=None, dx=None, ws=None, wsb=0) == 0
+    assert call(rows=0, acc=3, x=None, inv=None, dy=None, dx=None, ws=None, wsb=0) == 0
 
 
 def test_mul_argument_validation():
@@ -156,6 +159,7 @@ def test_mul_argument_validation():
     assert m(FAKE, None, FAKE, None, FAKE, FAKE, 1 << 20, 4, 4, 0, 0, None) == 1  # db needs a
     assert m(FAKE, FAKE, FAKE, None, FAKE, None, 0, 4, 4, 0, 0, None) == 3        # db needs ws
     assert m(FAKE, FAKE, FAKE, None, None, None, 0, 4, 4, 0, 0, None) == 0        # nothing asked
+    assert m(FAKE, FAKE, FAKE, FAKE, None, None, 0, 4, 4, 0, 8, None) == 1        # bad accumulate
 
 
 def test_python_binding_raises_without_gpu_tensors():

@@ -149,6 +149,41 @@ def test_accumulate(cuda, dtype):
     assert vec_rel_err(dg, rdg) <= _tol(x)
 
 
+@pytest.mark.parametrize("cols", [2048, 1030])   # resident kernel, looped kernel
+@pytest.mark.parametrize("flags", [agk.AGK_ACCUM_DX, agk.AGK_ACCUM_DGAMMA])
+def test_accumulate_one_output(cuda, cols, flags):
+    """dx and dgamma accumulate independently (a tied gamma already holds a
+    gradient while x's gradient is fresh, and the other way round)."""
+    import torch
+    x, g, dy = configs.make_inputs((40, cols), seed=cols + flags)
+    xd, gd, dyd = to_dev(x, cuda), to_dev(g, cuda), to_dev(dy, cuda)
+    _, inv = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    fresh_dx, fresh_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    pre_dx = torch.full_like(xd, 0.25)
+    pre_dg = torch.full((cols,), -0.5, device=cuda)
+    dx, dg = agk.rmsnorm_bwd(xd, gd, inv, dyd, dx=pre_dx.clone(), dgamma=pre_dg.clone(),
+                             accumulate=flags)
+    torch.cuda.synchronize()
+    if flags == agk.AGK_ACCUM_DX:
+        assert torch.equal(dx, pre_dx + fresh_dx) and torch.equal(dg, fresh_dg)
+    else:
+        assert torch.equal(dx, fresh_dx) and torch.equal(dg, pre_dg + fresh_dg)
+
+
+@pytest.mark.parametrize("dtype,cols", [("f32", 4096), ("bf16", 8192), ("f32", 1030)])
+def test_dgamma_only(cuda, dtype, cols):
+    """dx == NULL: only dgamma, bit-identical to the dgamma of a full call."""
+    import torch
+    x, g, dy = configs.make_inputs((300, cols), dtype=dtype, seed=11)
+    xd, gd, dyd = to_dev(x, cuda), to_dev(g, cuda), to_dev(dy, cuda)
+    _, inv = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    _, full_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    dx, dg = agk.rmsnorm_bwd(xd, gd, inv, dyd, want_dx=False)
+    torch.cuda.synchronize()
+    assert dx is None
+    assert torch.equal(dg, full_dg)
+
+
 def test_misaligned_pointers_take_scalar_path(cuda):
     import torch
     rows, cols = 33, 1024
