@@ -3,6 +3,10 @@
 Outputs (in-tree, git-ignored, shipped with the source tree):
   cgadimpl_amd/lib/libagk_rmsnorm.so   HIP kernels + C ABI (include/agk_rmsnorm.h)
   cgadimpl_amd/lib/libagk_synth.so     seeded synthetic input generator (host)
+  cgadimpl_amd/lib/libag.so            the C++ graph layer (ag::Value, rms, rms_norm,
+                                       mul, backward) over the C ABI (host C++)
+  cgadimpl_amd/lib/test_ag_layer       its GPU test program (tests/cpp/)
+  cgadimpl_amd/lib/rmsnorm_layer_bench the layer benchmark through the graph layer
 
 Every HIP translation unit is compiled for gfx950 only, with packed-fp32
 instruction generation disabled.
@@ -68,6 +72,31 @@ def host_library(name: str, sources: list[str], compiler: str = "g++") -> str:
     return out
 
 
+AG_DIR = os.path.join(PKG, "ag")
+AG_SOURCES = ["tensor.cpp", "graph.cpp", "ops.cpp", "autodiff.cpp", "nn.cpp"]
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+# Host C++ against the HIP runtime API (no device code in these files).
+HOST_HIP_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+                  f"-I{ROCM}/include", f"-I{os.path.join(AG_DIR, 'include')}", f"-I{INCLUDE}"]
+HOST_HIP_LIBS = [f"-L{LIB}", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN",
+                 f"-Wl,-rpath,{ROCM}/lib"]
+
+
+def ag_library() -> str:
+    out = os.path.join(LIB, "libag.so")
+    srcs = [os.path.join(AG_DIR, "src", s) for s in AG_SOURCES]
+    _atomic_build(out, lambda o: ["g++", *HOST_HIP_FLAGS, "-shared", *srcs, "-o", o,
+                                  "-lagk_rmsnorm", *HOST_HIP_LIBS])
+    return out
+
+
+def ag_program(name: str, source: str) -> str:
+    out = os.path.join(LIB, name)
+    _atomic_build(out, lambda o: ["g++", *HOST_HIP_FLAGS, source, "-o", o, "-lag",
+                                  "-lagk_rmsnorm", *HOST_HIP_LIBS, "-pthread"])
+    return out
+
+
 def build_all(verbose: bool = True) -> list[str]:
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
@@ -78,6 +107,10 @@ def build_all(verbose: bool = True) -> list[str]:
     ]
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
         outs = [f.result() for f in [ex.submit(j) for j in jobs]]
+    # the graph layer links the kernel library, its programs link both
+    outs.append(ag_library())
+    outs.append(ag_program("test_ag_layer", os.path.join(ROOT, "tests", "cpp",
+                                                         "test_ag_layer.cpp")))
     if verbose:
         for o in outs:
             print(f"built {os.path.relpath(o, ROOT)}")

@@ -1,0 +1,41 @@
+// ops.hpp -- forward operations of the RMSNorm layer path.
+//
+// The reference writes the layer as two graph ops, `ag::rms(x) * gamma`
+// (cgadimpl/include/ad/ops/ops.hpp:81,124; forward in
+// cgadimpl/src/ops/normalization.cpp:23-35 and arithmetic.cpp:31-39).  Both
+// are here with the same names and meaning, running on the HIP kernels behind
+// include/agk_rmsnorm.h, plus the fused layer rms_norm(x, gamma, eps), one node
+// whose forward and backward are one kernel call each.
+#pragma once
+
+#include <memory>
+
+#include "ag/graph.hpp"
+
+namespace ag {
+
+// x * (mean(x^2, last axis) + 1e-5)^(-1/2).  eps is 1e-5 as in the reference
+// (normalization.cpp:26).  Tape: {inv_rms [rows] fp32, y}.
+Value rms(const Value& x);
+
+// The fused RMSNorm layer: x * rsqrt(mean(x^2) + eps) * gamma, gamma of shape
+// [D] or [1, D] for x of shape [..., D].  Tape: {inv_rms [rows] fp32}.  The
+// gradient of gamma is fp32 whatever gamma's storage type.
+Value rms_norm(const Value& x, const Value& gamma, float eps = 1e-5f);
+
+// Element-wise product where one operand is a row vector ([D] or [1, D])
+// broadcast over the other's leading axes, or both have the same shape
+// (cgadimpl/src/ops/arithmetic.cpp:31-39).  The gradient of a broadcast
+// operand is fp32.  Other broadcasts throw std::runtime_error.
+Value mul(const Value& a, const Value& b);
+inline Value operator*(const Value& a, const Value& b) { return mul(a, b); }
+
+namespace detail {
+std::shared_ptr<Node> rms_nodeops(const std::shared_ptr<Node>& x);
+std::shared_ptr<Node> rms_norm_nodeops(const std::shared_ptr<Node>& x,
+                                       const std::shared_ptr<Node>& gamma, float eps);
+std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a,
+                                  const std::shared_ptr<Node>& b);
+}  // namespace detail
+
+}  // namespace ag

@@ -1,0 +1,117 @@
+// tensor.hpp -- the device tensor the graph layer holds in its nodes.
+//
+// The reference keeps every value and gradient in an OwnTensor::Tensor
+// (cgadimpl/include/tensor.hpp:6-15), whose library is not part of this
+// build.  This is the part of that interface the RMSNorm layer path uses:
+// a row-major, contiguous block of fp32 or bf16 elements on the current HIP
+// device with a shape, plus host transfers for tests and callers.
+//
+// Memory comes from HIP's stream-ordered pool (hipMallocAsync on the calling
+// thread's current stream, returned with hipFreeAsync on the same stream when
+// the last reference goes), with the pool told to keep freed memory, so the
+// per-call gradient and workspace buffers of a training loop are recycled
+// without device-wide synchronisation.  A tensor is stream-ordered to the
+// stream it was allocated on: work on another stream must be ordered against
+// that stream by the caller.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+namespace ag {
+
+enum class Dtype : uint8_t { Float32 = 0, BFloat16 = 1 };
+
+size_t dtype_size(Dtype dt);
+const char* dtype_name(Dtype dt);
+
+// The stream GPU work of the calling thread is enqueued on (nullptr = the
+// null stream).  Thread-local, like the reference's current_stream()
+// (cgadimpl/include/ad/runtime/cuda_graphs.hpp:12-23).
+hipStream_t current_stream();
+void set_current_stream(hipStream_t stream);
+
+// RAII: makes `stream` current for the lifetime of the guard.
+class StreamGuard {
+  public:
+    explicit StreamGuard(hipStream_t stream) : prev_(current_stream()) {
+        set_current_stream(stream);
+    }
+    ~StreamGuard() { set_current_stream(prev_); }
+    StreamGuard(const StreamGuard&) = delete;
+    StreamGuard& operator=(const StreamGuard&) = delete;
+
+  private:
+    hipStream_t prev_;
+};
+
+// One device allocation from the stream-ordered pool.
+class Storage {
+  public:
+    Storage(size_t bytes, hipStream_t stream);
+    ~Storage();
+    Storage(const Storage&) = delete;
+    Storage& operator=(const Storage&) = delete;
+    void* data() const { return ptr_; }
+    size_t bytes() const { return bytes_; }
+    hipStream_t stream() const { return stream_; }
+
+  private:
+    void* ptr_ = nullptr;
+    size_t bytes_ = 0;
+    hipStream_t stream_ = nullptr;
+};
+
+class Tensor {
+  public:
+    Tensor() = default;  // undefined: no shape, no storage
+
+    // Uninitialised / zero-filled / filled device tensors on the current stream.
+    static Tensor empty(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
+    static Tensor zeros(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
+    static Tensor ones(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
+    // Copies `shape`-many elements of `dt` from host memory (bf16 as raw bits).
+    static Tensor from_host(const void* src, const std::vector<int64_t>& shape,
+                            Dtype dt = Dtype::Float32);
+    static Tensor from_host_f32(const std::vector<float>& src, const std::vector<int64_t>& shape);
+
+    // Synchronous copies to host memory (wait for the tensor's stream).
+    void copy_to_host(void* dst) const;
+    std::vector<float> to_host_f32() const;  // bf16 decoded to fp32
+    // Device-to-device copy on the current stream (shapes must hold the same count).
+    void copy_from(const Tensor& src);
+
+    bool defined() const { return static_cast<bool>(storage_); }
+    const std::vector<int64_t>& shape() const { return shape_; }
+    Dtype dtype() const { return dtype_; }
+    int64_t numel() const;
+    int64_t dim() const { return static_cast<int64_t>(shape_.size()); }
+    // Normalised axis = the last one: cols() = shape.back(), rows() = numel()/cols().
+    int64_t cols() const;
+    int64_t rows() const;
+    size_t nbytes() const { return static_cast<size_t>(numel()) * dtype_size(dtype_); }
+    void* data() const { return storage_ ? storage_->data() : nullptr; }
+
+    // Same storage, another shape with the same element count.
+    Tensor reshape(const std::vector<int64_t>& shape) const;
+
+    // The reference's tensors carry requires_grad, which make_tensor() reads
+    // (cgadimpl/include/ad/core/graph.hpp:82-84).
+    bool requires_grad() const { return requires_grad_; }
+    Tensor& set_requires_grad(bool on) {
+        requires_grad_ = on;
+        return *this;
+    }
+
+  private:
+    std::vector<int64_t> shape_;
+    Dtype dtype_ = Dtype::Float32;
+    bool requires_grad_ = false;
+    std::shared_ptr<Storage> storage_;
+};
+
+}  // namespace ag

@@ -1,0 +1,141 @@
+// autodiff.cpp -- backward(), zero_grad() and the VJP table.
+//
+// Follows cgadimpl/src/core/autodiff.cpp:27-170: topological order from the
+// root, dependency counters, the root's gradient assigned from the seed
+// (ones without one), then every node's VJP in reverse order, sequentially or
+// on worker threads (a node becomes ready when all its consumers have run).
+// Differences, both deliberate:
+//   - every VJP launches on the stream that is current where backward() was
+//     called (worker threads take it over), where the reference's workers
+//     fall back to the null stream; one stream keeps the device order equal
+//     to the dependency order the host enforces;
+//   - a node whose gradient never arrived (no consumer contributed) has a
+//     zero upstream gradient, so its VJP is skipped instead of run on zeros.
+#include <algorithm>
+#include <condition_variable>
+#include <deque>
+#include <exception>
+#include <thread>
+
+#include "ag/autodiff.hpp"
+#include "check.hpp"
+
+namespace ag {
+
+using internal::fail;
+
+VjpFn vjp_lookup(Op op) {
+    switch (op) {
+#define AG_OP(name, arity, str) \
+    case Op::name:              \
+        return &detail::vjp_##name;
+#include "ag/ops.def"
+#undef AG_OP
+        default:
+            return nullptr;
+    }
+}
+
+void zero_grad(const Value& root) {
+    for (Node* n : topo_from(root.node.get()))
+        if (n->requires_grad()) {
+            n->grad = Tensor();  // reads as zeros; the next contribution overwrites
+            n->grad_is_materialized_zero = false;
+            n->grad_is_borrowed = false;
+        }
+}
+
+namespace {
+
+void run_node(Node* n) {
+    if (n->grad.defined()) {
+        VjpFn fn = vjp_lookup(n->op);
+        if (fn) fn(n, n->grad);
+    }
+    for (auto& hook : n->post_acc_grad_hooks) hook(n);
+}
+
+void backward_parallel(const std::vector<Node*>& order, Node* root, hipStream_t stream) {
+    // consumers of each node that still have to run (reference: autodiff.cpp:37-49)
+    for (Node* n : order) n->child_grad_count = 0;
+    size_t pending = 0;
+    for (Node* n : order) {
+        if (!n->requires_grad()) continue;
+        ++pending;
+        for (auto& p : n->inputs)
+            if (p && p->requires_grad()) p->child_grad_count++;
+    }
+
+    std::mutex mu;
+    std::condition_variable cv;
+    std::deque<Node*> ready{root};
+    size_t done = 0;
+    std::exception_ptr error;
+
+    auto worker = [&]() {
+        StreamGuard guard(stream);
+        for (;;) {
+            Node* n = nullptr;
+            {
+                std::unique_lock<std::mutex> lk(mu);
+                cv.wait(lk, [&] { return !ready.empty() || done == pending || error; });
+                if (done == pending || error) return;
+                n = ready.front();
+                ready.pop_front();
+            }
+            try {
+                run_node(n);
+            } catch (...) {
+                std::lock_guard<std::mutex> lk(mu);
+                if (!error) error = std::current_exception();
+                cv.notify_all();
+                return;
+            }
+            std::lock_guard<std::mutex> lk(mu);
+            for (auto& p : n->inputs)
+                if (p && p->requires_grad() && p->child_grad_count.fetch_sub(1) == 1)
+                    ready.push_back(p.get());
+            ++done;
+            cv.notify_all();
+        }
+    };
+
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const size_t nthreads = std::min<size_t>({static_cast<size_t>(hw), pending, 64});
+    std::vector<std::thread> threads;
+    threads.reserve(nthreads);
+    for (size_t i = 0; i < nthreads; ++i) threads.emplace_back(worker);
+    for (auto& t : threads) t.join();
+    if (error) std::rethrow_exception(error);
+    if (done != pending) fail("backward: dependency counting left nodes unprocessed");
+}
+
+}  // namespace
+
+void backward(const Value& root, const Tensor* grad_seed, bool enable_parallel) {
+    if (!root.node) fail("backward: empty root");
+    Node* r = root.node.get();
+    if (!r->requires_grad()) return;  // no input of the graph requires grad
+    const std::vector<Node*> order = topo_from(r);
+
+    // seed: assignment, not accumulation (reference autodiff.cpp:53-55)
+    if (grad_seed) {
+        if (grad_seed->shape() != r->value.shape() || grad_seed->dtype() != r->value.dtype())
+            fail("backward: the seed must have the root's shape and dtype");
+        r->grad = *grad_seed;
+        r->grad_is_borrowed = true;
+    } else {
+        r->grad = Tensor::ones(r->value.shape(), r->value.dtype());
+        r->grad_is_borrowed = false;
+    }
+    r->grad_is_materialized_zero = false;
+
+    if (!enable_parallel) {
+        for (auto it = order.rbegin(); it != order.rend(); ++it)
+            if ((*it)->requires_grad()) run_node(*it);
+        return;
+    }
+    backward_parallel(order, r, current_stream());
+}
+
+}  // namespace ag
