@@ -127,12 +127,30 @@ __device__ __forceinline__ void store16_stream(typename S::T* p, u32x4 v) {
 
 // ---- reductions -------------------------------------------------------------
 
-// Sum over the TPR (<= 64) lanes of a row group, butterfly order; every lane
-// of the group ends with the same value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over the TPR (<= 64) lanes of a row group; every lane of the group ends
+// with the same value.  Each step adds the partner lane of a fixed pairing:
+// DPP quad permutes for lanes 1 and 2 apart, DPP row mirrors for the halves of
+// 8- and 16-lane rows (fused into v_add_f32_dpp), a ds_swizzle swap for the
+// 16-lane halves of 32 and two lane reads for the wave halves -- no LDS round
+// trips except the one swizzle.  Pairings are symmetric, so partners compute
+// a + b and b + a, which are the same bits.  Every lane of the wave must be
+// active (all callers reduce with the whole workgroup).
 template <int TPR>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = (TPR < 64 ? TPR : 64) / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    if constexpr (TPR >= 2) v += dpp_mov<0xb1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (TPR >= 4) v += dpp_mov<0x4e>(v);   // quad_perm [2,3,0,1]
+    if constexpr (TPR >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+    if constexpr (TPR >= 16) v += dpp_mov<0x140>(v); // row_mirror
+    if constexpr (TPR >= 32)                         // swap 16-lane halves of 32
+        v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+    if constexpr (TPR >= 64)
+        v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     return v;
 }
 
