@@ -14,7 +14,8 @@ from typing import Optional, Tuple
 
 __all__ = [
     "AgkError", "lib", "lib_path", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_bwd_workspace_bytes",
-    "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "AGK_F32", "AGK_BF16", "STATUS",
+    "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
+    "transpose_bf16", "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -39,6 +40,12 @@ SIGNATURES = {
     "agk_mul_rowbcast_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_mul_rowbcast_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
                                             ctypes.c_int, ctypes.c_int, _P]),
+    "agk_gemm_bf16": (ctypes.c_int, [_P, _I64, ctypes.c_int, _P, _I64, ctypes.c_int, _P, _I64,
+                                     ctypes.c_int, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P,
+                                     ctypes.c_size_t, _P]),
+    "agk_gemm_bf16_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, ctypes.c_int,
+                                                        ctypes.c_int]),
+    "agk_transpose_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),
     "agk_rmsnorm_launch_plan": (ctypes.c_int, [_I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
@@ -182,6 +189,52 @@ def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate=False,
                                _dtype_code(x), acc, _stream(stream))
     _check(rc, "agk_rmsnorm_bwd")
     return dx, dgamma
+
+
+def gemm_bf16_workspace_bytes(M: int, N: int, K: int, trans_a: bool, trans_b: bool) -> int:
+    return int(lib().agk_gemm_bf16_workspace_bytes(M, N, K, int(trans_a), int(trans_b)))
+
+
+def transpose_bf16(src, dst=None, stream=None):
+    """dst = src.T for a 2-D bfloat16 device tensor (through agk_transpose_bf16)."""
+    torch = _torch()
+    rows, cols = src.shape
+    if dst is None:
+        dst = torch.empty(cols, rows, dtype=src.dtype, device=src.device)
+    _check(lib().agk_transpose_bf16(_ptr(src), cols, _ptr(dst), rows, rows, cols, _stream(stream)),
+           "agk_transpose_bf16")
+    return dst
+
+
+def gemm_bf16(a, b, c=None, trans_a: bool = False, trans_b: bool = False, out_dtype=None,
+              kscale=None, rowscale=None, accumulate: bool = False, workspace="auto",
+              stream=None):
+    """C (+)= rowscale[:, None] * ((A * kscale[None, :]) @ B) on MFMA, bf16 in, fp32 accumulate.
+
+    a is A [M, K] (or A^T [K, M] with trans_a); b is B [K, N] (or B^T [N, K]
+    with trans_b); both bfloat16 and contiguous.  kscale: float32 [K] applied
+    to A as it is staged (rounded to bf16); rowscale: float32 [M] applied to
+    the result.  out_dtype: torch.float32 or torch.bfloat16 (default bf16).
+    """
+    torch = _torch()
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError("gemm_bf16 takes bfloat16 operands")
+    M, K = (a.shape[1], a.shape[0]) if trans_a else (a.shape[0], a.shape[1])
+    N = b.shape[0] if trans_b else b.shape[1]
+    if (b.shape[1] if trans_b else b.shape[0]) != K:
+        raise ValueError("inner dimensions differ")
+    if c is None:
+        c = torch.empty(M, N, dtype=out_dtype or torch.bfloat16, device=a.device)
+    if isinstance(workspace, str):  # "auto": allocate what the fast path needs
+        need = gemm_bf16_workspace_bytes(M, N, K, trans_a, trans_b) if kscale is None else 0
+        workspace = torch.empty(need, dtype=torch.uint8, device=a.device) if need else None
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    rc = lib().agk_gemm_bf16(_ptr(a), a.shape[1], int(trans_a), _ptr(b), b.shape[1], int(trans_b),
+                             _ptr(c), c.shape[1], _dtype_code(c), M, N, K, _ptr(kscale),
+                             _ptr(rowscale), int(bool(accumulate)), _ptr(workspace), ws_bytes,
+                             _stream(stream))
+    _check(rc, "agk_gemm_bf16")
+    return c
 
 
 def launch_plan(rows: int, cols: int, dtype: int, backward: bool) -> dict:

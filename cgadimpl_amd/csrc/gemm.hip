@@ -1,0 +1,681 @@
+// gemm.hip -- bf16 GEMM on CDNA4 (gfx950) MFMA with fp32 accumulation, for the
+// RMSNorm + linear layer (configuration c5): the forward y = h * W and the VJP
+// dh = dy * W^T, dW = h^T * dy of the reference's matmul
+// (cgadimpl/src/ops/linalg.cpp:12-20, cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:258-263).
+//
+//   C[m, n] (+)= rowscale[m] * sum_k (A[m, k] * kscale[k]) * B[k, n]
+//
+// The two optional scales carry the RMSNorm into the GEMM without
+// materialising h = diag(r) * x * diag(gamma):
+//   y  = h * W        = diag(r) * (x * diag(gamma)) * W    kscale = gamma, rowscale = r
+//   dW = h^T * dy     = diag(gamma) * (x^T * diag(r)) * dy  kscale = r,     rowscale = gamma
+// (kscale multiplies the A operand as it is staged, rounding to bf16 as a
+// stored h would be; rowscale multiplies the fp32 accumulator.)
+//
+// Kernel shape.  A workgroup of 512 lanes (8 waves, 2 along M x 4 along N)
+// computes a 256 x 256 tile of C; each wave owns 128 x 64 of it as 4 x 2
+// v_mfma_f32_32x32x16_bf16 accumulators (128 fp32 registers per lane).  K is
+// walked in steps of 64: the next step's A and B tiles are loaded from HBM /
+// L2 into registers while the current step's tiles are multiplied out of LDS,
+// then written to the other half of a double-buffered LDS (one barrier per
+// step).  LDS rows are k-contiguous (each MFMA operand is 8 consecutive k of
+// one row or column, one 16-byte LDS read) and padded by 16 bytes against
+// bank conflicts.  An operand stored with k contiguous in memory ([rows][K])
+// is copied in 16-byte chunks; an operand stored with k strided ([K][rows])
+// is read 4 k-rows x 8 values per lane and transposed in registers
+// (v_perm_b32) into 8-byte LDS writes.
+//
+// LDS rows are 128 bytes with XOR-swizzled 16-byte chunks (lds_off), and the
+// global loads are issued unconditionally at clamped in-range addresses (out
+// of range values are zeroed afterwards), so the compiler can keep the next
+// step's loads in flight across the MFMA block.
+//
+// MFMA lane layout (checked on MI355X): A operand lane l holds row l % 32,
+// k = (l / 32) * 8 .. +7; B operand lane l holds column l % 32, the same k;
+// accumulator element e of lane l is C[8 * (e / 4) + 4 * (l / 32) + e % 4][l % 32].
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "agk_rmsnorm.h"
+
+namespace agk_gemm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int kThreads = 512;
+constexpr int kWavesN = 4;
+constexpr int WM = 128, WN = 64;            // per-wave tile
+constexpr int TM = WM / 32, TN = WN / 32;   // MFMA tiles per wave
+constexpr int kStride = BK;                 // bf16 per LDS row (128 bytes)
+constexpr int kStageElems = (BM + BN) * kStride;
+
+// LDS position of k-chunk c (8 bf16 = 16 bytes) of row `row`: chunks are
+// XOR-swizzled by the row's low bits, so the 8 lanes of a 16-byte fragment
+// read (8 consecutive rows, one chunk) and the 8-byte writes of the
+// transposing stager (rows 8 apart) land on different banks.
+__device__ __forceinline__ int lds_off(int row, int c) {
+    return row * kStride + ((c ^ (row & 7) ^ ((row >> 3) & 7)) << 3);
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32: NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+// lo16(a) | lo16(b) << 16 and hi16(a) | hi16(b) << 16 (v_perm_b32)
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// ---- operand staging --------------------------------------------------------
+// An operand tile is R = 256 rows (of A: m, of B: n) by BK = 64 k.
+//
+// k-contiguous source ([rows][ld], k along the row): chunk c = tid + j*512,
+// row = c / 8, 8-element k-chunk c % 8 (every chunk of a thread has the same
+// k-chunk, tid % 8).
+// k-strided source ([K][ld], rows along the row): lane owns 8 rows
+// (8 * (tid % 32) ..) at 4 consecutive k (4 * (tid / 32) ..).
+template <bool KCONTIG>
+struct Stage {
+    u32x4 v[4];
+};
+
+template <bool KCONTIG, bool SCALE>
+__device__ __forceinline__ void load_tile(Stage<KCONTIG>& s, const uint16_t* __restrict__ src,
+                                          int64_t ld, int row0, int rows, int k0, int K,
+                                          const float* __restrict__ kscale) {
+    const int tid = threadIdx.x;
+    if constexpr (KCONTIG) {
+        const int kc = (tid & 7) * 8;
+        const int k = k0 + kc;
+        float ks[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // past K: chunks are zero
+        if constexpr (SCALE) {
+            if (k < K) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(kscale + k);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(kscale + k + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ks[e] = a[e];
+                    ks[e + 4] = b[e];
+                }
+            }
+        }
+        const int kcl = k < K ? k : K - 8;  // in-range address; zeroed below
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = (tid >> 3) + j * (kThreads / 8);
+            const int grow = row0 + row;
+            const int gcl = grow < rows ? grow : rows - 1;
+            u32x4 v = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(gcl) * ld + kcl);
+            if (!(grow < rows && k < K)) v = u32x4{0u, 0u, 0u, 0u};
+            if constexpr (SCALE) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    v[w] = pack_bf16(bf16_lo(v[w]) * ks[2 * w], bf16_hi(v[w]) * ks[2 * w + 1]);
+            }
+            s.v[j] = v;
+        }
+    } else {
+        const int r = (tid & 31) * 8;
+        const int kq = (tid >> 5) * 4;
+        const int grow = row0 + r;
+        const int gcl = grow < rows ? grow : rows - 8;  // in-range address; zeroed below
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = k0 + kq + j;
+            const int kcl = k < K ? k : K - 1;
+            u32x4 v = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(kcl) * ld + gcl);
+            if (!(grow < rows && k < K)) v = u32x4{0u, 0u, 0u, 0u};
+            if constexpr (SCALE) {
+                const float ks = k < K ? kscale[k] : 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    v[w] = pack_bf16(bf16_lo(v[w]) * ks, bf16_hi(v[w]) * ks);
+            }
+            s.v[j] = v;
+        }
+    }
+}
+
+template <bool KCONTIG>
+__device__ __forceinline__ void store_tile(const Stage<KCONTIG>& s, uint16_t* lds) {
+    const int tid = threadIdx.x;
+    if constexpr (KCONTIG) {
+        const int c = tid & 7;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = (tid >> 3) + j * (kThreads / 8);
+            *reinterpret_cast<u32x4*>(lds + lds_off(row, c)) = s.v[j];
+        }
+    } else {
+        // s.v[j] holds k = kq + j for rows r .. r+7 (two rows per word);
+        // row r + e receives its 4 k values as one 8-byte write.
+        const int r = (tid & 31) * 8;
+        const int kq = (tid >> 5) * 4;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const u32x2 even = {lo_pair(s.v[0][w], s.v[1][w]), lo_pair(s.v[2][w], s.v[3][w])};
+            const u32x2 odd = {hi_pair(s.v[0][w], s.v[1][w]), hi_pair(s.v[2][w], s.v[3][w])};
+            *reinterpret_cast<u32x2*>(lds + lds_off(r + 2 * w, kq >> 3) + (kq & 7)) = even;
+            *reinterpret_cast<u32x2*>(lds + lds_off(r + 2 * w + 1, kq >> 3) + (kq & 7)) = odd;
+        }
+    }
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const uint16_t* lds, int row, int k) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + lds_off(row, k >> 3)));
+}
+
+// ---- tile order ----------------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup L runs on
+// XCD L % 8), each XCD with its own L2.  The tile order below gives each XCD
+// a contiguous chunk of a grouped ordering (kGroupM m-tiles x all n-tiles,
+// column by column), so the ~32 workgroups resident on one XCD at a time
+// cover about kGroupM x 8 tiles and share their A row-panels and B column-
+// panels in that XCD's L2, instead of every neighbouring tile landing on a
+// different XCD.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
+
+__device__ __forceinline__ void tile_of(int L, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int T = tiles_m * tiles_n;
+    const int x = L % kXcds, s = L / kXcds;
+    const int q = T / kXcds, r = T % kXcds;  // XCDs below r get q + 1 tiles
+    const int g = x < r ? x * (q + 1) + s : r * (q + 1) + (x - r) * q + s;
+    const int per_group = kGroupM * tiles_n;
+    const int group = g / per_group;
+    const int gm0 = group * kGroupM;
+    const int gsize = tiles_m - gm0 < kGroupM ? tiles_m - gm0 : kGroupM;
+    const int in = g - group * per_group;
+    tm = gm0 + in % gsize;
+    tn = in / gsize;
+}
+
+// ---- the kernel ---------------------------------------------------------------
+
+template <bool A_KCONTIG, bool B_KCONTIG, bool KSCALE, bool OUT_F32>
+__global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
+    void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ kscale,
+    const float* __restrict__ rowscale, int accumulate, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStageElems];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / kWavesN;
+    const int wn = wave % kWavesN;
+    int tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    Stage<A_KCONTIG> sa;
+    Stage<B_KCONTIG> sb;
+    const int nk = (K + BK - 1) / BK;
+    load_tile<A_KCONTIG, KSCALE>(sa, A, lda, m0, M, 0, K, kscale);
+    load_tile<B_KCONTIG, false>(sb, B, ldb, n0, N, 0, K, nullptr);
+    store_tile<A_KCONTIG>(sa, lds);
+    store_tile<B_KCONTIG>(sb, lds + BM * kStride);
+    __syncthreads();
+
+    const int frow = lane & 31;
+    const int fk = (lane >> 5) * 8;
+    for (int kt = 0; kt < nk; ++kt) {
+        const uint16_t* cur = lds + (kt & 1) * kStageElems;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            load_tile<A_KCONTIG, KSCALE>(sa, A, lda, m0, M, (kt + 1) * BK, K, kscale);
+            load_tile<B_KCONTIG, false>(sb, B, ldb, n0, N, (kt + 1) * BK, K, nullptr);
+        }
+        // fragments of k-substep ks + 16 are read while ks is multiplied
+        bf16x8 af[2][TM], bf[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[0][i] = lds_frag(cur, wm * WM + i * 32 + frow, fk);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[0][j] = lds_frag(cur + BM * kStride, wn * WN + j * 32 + frow, fk);
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {
+            const int c = s & 1;
+            if (s + 1 < BK / 16) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    af[c ^ 1][i] = lds_frag(cur, wm * WM + i * 32 + frow, (s + 1) * 16 + fk);
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    bf[c ^ 1][j] = lds_frag(cur + BM * kStride, wn * WN + j * 32 + frow,
+                                            (s + 1) * 16 + fk);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bf[c][j],
+                                                                        acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            uint16_t* nxt = lds + ((kt + 1) & 1) * kStageElems;
+            store_tile<A_KCONTIG>(sa, nxt);
+            store_tile<B_KCONTIG>(sb, nxt + BM * kStride);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: element e of acc[i][j] is C[row][col] below
+    const int col_l = lane & 31;
+    const int row_l = 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm * WM + i * 32 + 8 * (e >> 2) + row_l + (e & 3);
+            if (row >= M) continue;
+            const float rs = rowscale ? rowscale[row] : 1.0f;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + col_l;
+                if (col >= N) continue;
+                float v = acc[i][j][e] * rs;
+                if constexpr (OUT_F32) {
+                    float* p = static_cast<float*>(C) + static_cast<int64_t>(row) * ldc + col;
+                    *p = accumulate ? *p + v : v;
+                } else {
+                    uint16_t* p = static_cast<uint16_t*>(C) + static_cast<int64_t>(row) * ldc + col;
+                    if (accumulate) v = __uint_as_float(static_cast<uint32_t>(*p) << 16) + v;
+                    *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
+                }
+            }
+        }
+    }
+}
+
+// ---- direct-to-LDS kernel: both operands k-contiguous, K a multiple of BK ----
+// Staging without registers: global_load_lds_dwordx4 writes lane l's 16 bytes
+// to LDS at (wave-uniform base) + 16 * l (checked on MI355X), so one wave
+// instruction fills 8 LDS rows of 128 bytes; each lane fetches the global
+// chunk that belongs at its position of the swizzled layout (lds_off).  The
+// two stages are separate LDS objects and the k loop is unrolled by two, so
+// the compiler can tell the stage being multiplied from the one being filled
+// and does not wait for the DMA before the fragment reads.  Rows past M or N
+// are fetched from the last valid row (never stored); K must be a multiple
+// of BK, since a partial k-tile would multiply stale data.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Per-lane element offsets (from the tile's first row) of the 4 A and 4 B
+// chunks a lane fetches per k-tile; the tile bases are wave-uniform.
+struct DirectStage {
+    const uint16_t* a_base;
+    const uint16_t* b_base;
+    uint32_t oa[4];
+    uint32_t ob[4];
+};
+
+__device__ __forceinline__ void direct_issue(const DirectStage& d, uint16_t* stage, int k0,
+                                             int wave) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(d.a_base + d.oa[j] + k0,
+                                         (lds_ptr_t)(stage + (wave * 32 + j * 8) * kStride), 16,
+                                         0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(d.b_base + d.ob[j] + k0,
+                                         (lds_ptr_t)(stage + (BM + wave * 32 + j * 8) * kStride),
+                                         16, 0, 0);
+}
+
+// Instruction classes for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+// One BK-deep step of the wave's 128 x 64 tile out of one LDS stage.  The six
+// fragment reads of k-substep s + 1 are issued together ahead of the eight
+// MFMAs of substep s (scheduling groups), so they are in flight while the
+// matrix cores work and the two substeps' fragments stay in separate
+// registers.
+__device__ __forceinline__ void mfma_tile(const uint16_t* cur, f32x16 (&acc)[TM][TN], int wm,
+                                          int wn, int frow, int fk) {
+    bf16x8 af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[0][i] = lds_frag(cur, wm * WM + i * 32 + frow, fk);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bf[0][j] = lds_frag(cur + BM * kStride, wn * WN + j * 32 + frow, fk);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+        const int c = s & 1;
+        const bool next = s + 1 < BK / 16;
+        if (next) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                af[c ^ 1][i] = lds_frag(cur, wm * WM + i * 32 + frow, (s + 1) * 16 + fk);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bf[c ^ 1][j] = lds_frag(cur + BM * kStride, wn * WN + j * 32 + frow,
+                                        (s + 1) * 16 + fk);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bf[c][j], acc[i][j],
+                                                                    0, 0, 0);
+        if (next) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, TM + TN, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, TM * TN, 0);
+    }
+}
+
+template <bool OUT_F32>
+__device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
+                                        int64_t ldc, int M, int N, int m0, int n0, int wm, int wn,
+                                        int lane, const float* __restrict__ rowscale,
+                                        int accumulate) {
+    const int col_l = lane & 31;
+    const int row_l = 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm * WM + i * 32 + 8 * (e >> 2) + row_l + (e & 3);
+            if (row >= M) continue;
+            const float rs = rowscale ? rowscale[row] : 1.0f;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + col_l;
+                if (col >= N) continue;
+                float v = acc[i][j][e] * rs;
+                if constexpr (OUT_F32) {
+                    float* p = static_cast<float*>(C) + static_cast<int64_t>(row) * ldc + col;
+                    *p = accumulate ? *p + v : v;
+                } else {
+                    uint16_t* p = static_cast<uint16_t*>(C) + static_cast<int64_t>(row) * ldc + col;
+                    if (accumulate) v = __uint_as_float(static_cast<uint32_t>(*p) << 16) + v;
+                    *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
+                }
+            }
+        }
+    }
+}
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
+    void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
+    int accumulate, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint16_t stage0[kStageElems];
+    __shared__ __attribute__((aligned(16))) uint16_t stage1[kStageElems];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / kWavesN;
+    const int wn = wave % kWavesN;
+    int tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+
+    DirectStage d;
+    d.a_base = A + static_cast<int64_t>(m0) * lda;
+    d.b_base = B + static_cast<int64_t>(n0) * ldb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = wave * 32 + j * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 7);
+        const int ra = m0 + row < M ? row : M - 1 - m0;
+        const int rb = n0 + row < N ? row : N - 1 - n0;
+        d.oa[j] = static_cast<uint32_t>(ra) * static_cast<uint32_t>(lda) + c * 8;
+        d.ob[j] = static_cast<uint32_t>(rb) * static_cast<uint32_t>(ldb) + c * 8;
+    }
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int nk = K / BK;
+    const int frow = lane & 31;
+    const int fk = (lane >> 5) * 8;
+    direct_issue(d, stage0, 0, wave);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        uint16_t* cur = (kt & 1) ? stage1 : stage0;
+        uint16_t* nxt = (kt & 1) ? stage0 : stage1;
+        if (kt + 1 < nk) direct_issue(d, nxt, (kt + 1) * BK, wave);
+        mfma_tile(cur, acc, wm, wn, frow, fk);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    store_c<OUT_F32>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale, accumulate);
+}
+
+// ---- transpose ----------------------------------------------------------------
+// dst[c][r] = src[r][c] for a rows x cols bf16 matrix (rows, cols multiples of
+// 8).  A 256-lane workgroup moves a 128 x 128 tile: each lane reads an 8 x 8
+// block as 8 coalesced 16-byte row pieces, transposes it in registers
+// (v_perm_b32) and writes its 8 columns as 16-byte pieces into an LDS tile
+// laid out [dst row][src row] (rows padded by 16 bytes); after a barrier the
+// tile leaves as coalesced 16-byte pieces of dst rows.  HBM-bound: one read and
+// one write of the matrix.
+constexpr int kTrTile = 128;
+constexpr int kTrStride = kTrTile + 8;
+
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
+                                                             int64_t ld_src,
+                                                             uint16_t* __restrict__ dst,
+                                                             int64_t ld_dst, int rows, int cols,
+                                                             int tiles_c) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kTrTile * kTrStride];
+    const int t = threadIdx.x;
+    const int r0 = (blockIdx.x / tiles_c) * kTrTile;
+    const int c0 = (blockIdx.x % tiles_c) * kTrTile;
+    const int bc = t & 15, br = t >> 4;  // this lane's 8 x 8 block
+    const int gr = r0 + br * 8, gc = c0 + bc * 8;
+    if (gr < rows && gc < cols) {
+        u32x4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(gr + i) * ld_src + gc));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const u32x4 even = {lo_pair(v[0][w], v[1][w]), lo_pair(v[2][w], v[3][w]),
+                                lo_pair(v[4][w], v[5][w]), lo_pair(v[6][w], v[7][w])};
+            const u32x4 odd = {hi_pair(v[0][w], v[1][w]), hi_pair(v[2][w], v[3][w]),
+                               hi_pair(v[4][w], v[5][w]), hi_pair(v[6][w], v[7][w])};
+            *reinterpret_cast<u32x4*>(tile + (bc * 8 + 2 * w) * kTrStride + br * 8) = even;
+            *reinterpret_cast<u32x4*>(tile + (bc * 8 + 2 * w + 1) * kTrStride + br * 8) = odd;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int lr = (t >> 4) + 16 * j;  // dst row within the tile
+        const int ch = t & 15;             // 16-byte piece of it
+        const int dr = c0 + lr, dc = r0 + ch * 8;
+        if (dr < cols && dc < rows)
+            __builtin_nontemporal_store(
+                *reinterpret_cast<const u32x4*>(tile + lr * kTrStride + ch * 8),
+                reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(dr) * ld_dst + dc));
+    }
+}
+
+inline int launch_transpose(const void* src, int64_t ld_src, void* dst, int64_t ld_dst, int rows,
+                            int cols, hipStream_t st) {
+    const int tr = (rows + kTrTile - 1) / kTrTile, tc = (cols + kTrTile - 1) / kTrTile;
+    hipLaunchKernelGGL(transpose_bf16_kernel, dim3(tr * tc), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(src), ld_src, static_cast<uint16_t*>(dst),
+                       ld_dst, rows, cols, tc);
+    return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <bool AK, bool BK_, bool KS, bool F32>
+int launch(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int M,
+           int N, int K, const float* kscale, const float* rowscale, int accumulate,
+           hipStream_t st) {
+    const int tiles_m = (M + BM - 1) / BM;
+    const int tiles_n = (N + BN - 1) / BN;
+    hipLaunchKernelGGL((gemm_bf16_kernel<AK, BK_, KS, F32>), dim3(tiles_m * tiles_n),
+                       dim3(kThreads), 0, st, static_cast<const uint16_t*>(A), lda,
+                       static_cast<const uint16_t*>(B), ldb, C, ldc, M, N, K, kscale, rowscale,
+                       accumulate, tiles_m, tiles_n);
+    return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
+}
+
+// Dispatch over (A k-contiguous, B k-contiguous, k-scale, fp32 output).
+template <bool AK, bool BK_, bool KS>
+int dispatch_out(int c_dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
+                 int64_t ldc, int M, int N, int K, const float* ks, const float* rs, int acc,
+                 hipStream_t st) {
+    return c_dtype == AGK_F32 ? launch<AK, BK_, KS, true>(A, lda, B, ldb, C, ldc, M, N, K, ks, rs,
+                                                          acc, st)
+                              : launch<AK, BK_, KS, false>(A, lda, B, ldb, C, ldc, M, N, K, ks,
+                                                           rs, acc, st);
+}
+template <bool AK, bool BK_>
+int dispatch_ks(bool has_ks, int c_dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+                void* C, int64_t ldc, int M, int N, int K, const float* ks, const float* rs,
+                int acc, hipStream_t st) {
+    return has_ks ? dispatch_out<AK, BK_, true>(c_dtype, A, lda, B, ldb, C, ldc, M, N, K, ks, rs,
+                                                acc, st)
+                  : dispatch_out<AK, BK_, false>(c_dtype, A, lda, B, ldb, C, ldc, M, N, K, ks, rs,
+                                                 acc, st);
+}
+
+}  // namespace agk_gemm
+
+namespace agk_gemm {
+
+// Whether a call takes the direct-to-LDS kernel once its operands are k-contiguous.
+inline bool direct_eligible(int64_t K, const float* kscale) {
+    return kscale == nullptr && K % BK == 0;
+}
+
+inline size_t workspace_for(int64_t M, int64_t N, int64_t K, int a_trans, int b_trans,
+                            const float* kscale) {
+    if (!direct_eligible(K, kscale)) return 0;
+    size_t bytes = 0;
+    if (a_trans) bytes += static_cast<size_t>(M) * K * 2;
+    if (!b_trans) bytes += static_cast<size_t>(N) * K * 2;
+    return bytes;
+}
+
+}  // namespace agk_gemm
+
+extern "C" size_t agk_gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_trans,
+                                                int b_trans) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return agk_gemm::workspace_for(M, N, K, a_trans, b_trans, nullptr);
+}
+
+extern "C" int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_dst,
+                                  int64_t rows, int64_t cols, agk_stream_t stream) {
+    using namespace agk_gemm;
+    if (rows < 0 || cols < 0 || rows > 0x7fffffffLL || cols > 0x7fffffffLL) return AGK_EINVAL;
+    if (rows == 0 || cols == 0) return AGK_OK;
+    if (!src || !dst || rows % 8 || cols % 8 || ld_src % 8 || ld_dst % 8) return AGK_EINVAL;
+    if (ld_src < cols || ld_dst < rows || !aligned16(src) || !aligned16(dst)) return AGK_EINVAL;
+    (void)hipGetLastError();
+    return launch_transpose(src, ld_src, dst, ld_dst, static_cast<int>(rows),
+                            static_cast<int>(cols), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
+                             int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
+                             int64_t K, const float* kscale, const float* rowscale,
+                             int accumulate, void* workspace, size_t workspace_bytes,
+                             agk_stream_t stream) {
+    using namespace agk_gemm;
+    if (M < 0 || N < 0 || K < 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+        return AGK_EINVAL;
+    if (c_dtype != AGK_F32 && c_dtype != AGK_BF16) return AGK_EDTYPE;
+    if (M == 0 || N == 0) return AGK_OK;
+    if (!A || !B || !C) return AGK_EINVAL;
+    // 16-byte vector accesses along the contiguous dimension of each operand
+    if ((M | N | K) % 8 != 0) return AGK_EINVAL;
+    if (lda % 8 || ldb % 8 || ldc < N) return AGK_EINVAL;
+    if (lda < (a_trans ? M : K) || ldb < (b_trans ? K : N)) return AGK_EINVAL;
+    if (!aligned16(A) || !aligned16(B)) return AGK_EINVAL;
+    if (kscale && !aligned16(kscale)) return AGK_EINVAL;
+    (void)hipGetLastError();  // report only this call's launch failures
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    const int acc = accumulate != 0;
+
+    // With a workspace, operands stored with k strided are transposed into it
+    // (one HBM-bound pass each) so the GEMM runs on the direct-to-LDS kernel.
+    const size_t need = workspace_for(M, N, K, a_trans, b_trans, kscale);
+    if (direct_eligible(K, kscale) && (need == 0 || (workspace && workspace_bytes >= need &&
+                                                     aligned16(workspace)))) {
+        const void* a_nt = A;
+        const void* b_nt = B;
+        int64_t lda_nt = lda, ldb_nt = ldb;
+        char* ws = static_cast<char*>(workspace);
+        if (a_trans) {  // A stored [K][lda] -> [M][K]
+            if (int rc = launch_transpose(A, lda, ws, K, k, m, st)) return rc;
+            a_nt = ws;
+            lda_nt = K;
+            ws += static_cast<size_t>(M) * K * 2;
+        }
+        if (!b_trans) {  // B stored [K][ldb] -> [N][K]
+            if (int rc = launch_transpose(B, ldb, ws, K, k, n, st)) return rc;
+            b_nt = ws;
+            ldb_nt = K;
+        }
+        if (lda_nt < (1 << 23) && ldb_nt < (1 << 23)) {
+            const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+            if (c_dtype == AGK_F32)
+                hipLaunchKernelGGL(gemm_nt_direct_kernel<true>, dim3(tiles_m * tiles_n),
+                                   dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
+                                   lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
+                                   n, k, rowscale, acc, tiles_m, tiles_n);
+            else
+                hipLaunchKernelGGL(gemm_nt_direct_kernel<false>, dim3(tiles_m * tiles_n),
+                                   dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
+                                   lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
+                                   n, k, rowscale, acc, tiles_m, tiles_n);
+            return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
+        }
+        A = a_nt;  // leading dimensions too large for the direct kernel's offsets
+        B = b_nt;
+        lda = lda_nt;
+        ldb = ldb_nt;
+        a_trans = 0;
+        b_trans = 1;
+    }
+    const bool ak = !a_trans, bk = b_trans != 0, ks = kscale != nullptr;
+    if (ak && bk) return dispatch_ks<true, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
+    if (ak && !bk) return dispatch_ks<true, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
+    if (!ak && bk) return dispatch_ks<false, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
+    return dispatch_ks<false, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
+}

@@ -124,6 +124,45 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
                          size_t workspace_bytes, int64_t rows, int64_t cols,
                          int dtype, int accumulate, agk_stream_t stream);
 
+/* bf16 GEMM on MFMA with fp32 accumulation, for the RMSNorm + linear layer:
+ *   C[m, n] (+)= rowscale[m] * sum_k (A[m, k] * kscale[k]) * B[k, n]
+ * Replaces the tensor-library matmul behind the reference's matmul node and
+ * its VJP (cgadimpl/src/ops/linalg.cpp:12-20: Y = A B;
+ * cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:258-263: dA += gy B^T,
+ * dB += A^T gy).
+ *   A: a_trans == 0 -> stored [M][lda] (row m, k contiguous);
+ *      a_trans != 0 -> stored [K][lda] (A^T, m contiguous).
+ *   B: b_trans == 0 -> stored [K][ldb] (n contiguous);
+ *      b_trans != 0 -> stored [N][ldb] (B^T, k contiguous).
+ *   C: [M][ldc], c_dtype AGK_F32 or AGK_BF16 (round to nearest even);
+ *      accumulate != 0 adds into C.
+ *   kscale (nullable, fp32 [K]): multiplies A's column k as A is staged, the
+ *      product rounded to bf16 (h = x * gamma without materialising h);
+ *   rowscale (nullable, fp32 [M]): multiplies row m of the fp32 result.
+ *   workspace (nullable): with at least agk_gemm_bf16_workspace_bytes(...)
+ *      bytes, operands stored with k strided are first transposed into it
+ *      and the product runs on the faster kernel for k-contiguous operands
+ *      (used when kscale == NULL and K % 64 == 0); without it the operands
+ *      are transposed while they are staged.
+ * A, B, kscale, workspace 16-byte aligned; M, N, K, lda, ldb multiples of 8;
+ * the result is deterministic (fixed accumulation order).                    */
+int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
+                  int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
+                  int64_t K, const float* kscale, const float* rowscale, int accumulate,
+                  void* workspace, size_t workspace_bytes, agk_stream_t stream);
+
+/* Bytes of workspace that let agk_gemm_bf16 use the k-contiguous kernel:
+ * M*K*2 if a_trans, plus N*K*2 if !b_trans; 0 when K % 64 != 0. */
+size_t agk_gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_trans, int b_trans);
+
+/* dst[c][r] = src[r][c] for a bf16 matrix of rows x cols (multiples of 8),
+ * 16-byte aligned, leading dimensions multiples of 8.  No reference
+ * counterpart: the reference's OwnTensor `.t()` feeding matmul
+ * (autodiff_vjp_ops.cpp:261-262) is a view; here operands are laid out for
+ * the matrix cores explicitly.                                               */
+int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_dst,
+                       int64_t rows, int64_t cols, agk_stream_t stream);
+
 /* Diagnostic, with no counterpart in the reference: the launch shape the
  * library picks for a forward (backward = 0) or backward (backward != 0)
  * call of these sizes with 16-byte aligned pointers.  plan[5] receives

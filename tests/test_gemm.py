@@ -1,0 +1,120 @@
+"""bf16 GEMM on MFMA (agk_gemm_bf16) and the bf16 transpose, through the C ABI.
+
+GPU: every operand layout, with and without workspace (the direct-to-LDS
+kernel and the staging kernel), the k- and row-scales, fp32 and bf16 output,
+accumulation and ragged sizes, each against a plain PyTorch fp32 product of
+the same bf16 operands; transposes bit-exact; repeated calls bit-identical.
+CPU: argument validation and the workspace rule.
+"""
+import pytest
+
+import cgadimpl_amd as agk
+
+FAKE = 0x1000  # never dereferenced: validation rejects before any HIP call
+
+
+def test_gemm_argument_validation():
+    lib = agk.lib()
+    g = lib.agk_gemm_bf16
+
+    def call(M=64, N=64, K=64, lda=64, ldb=64, ldc=64, ta=0, tb=1, dt=0, a=FAKE, b=FAKE, c=FAKE):
+        return g(a, lda, ta, b, ldb, tb, c, ldc, dt, M, N, K, None, None, 0, None, 0, None)
+
+    assert call(M=-1) == 1
+    assert call(dt=7) == 2
+    assert call(M=0) == 0 and call(N=0) == 0          # empty result: nothing to do
+    assert call(a=None) == 1 and call(c=None) == 1
+    assert call(M=60, lda=64) == 1                     # M not a multiple of 8
+    assert call(K=36) == 1                             # K not a multiple of 8
+    assert call(lda=60) == 1                           # lda < K
+    assert call(ldc=32) == 1                           # ldc < N
+    assert call(a=FAKE + 4) == 1                       # A not 16-byte aligned
+    ws = lib.agk_gemm_bf16_workspace_bytes
+    assert ws(8192, 11008, 4096, 0, 1) == 0            # already k-contiguous
+    assert ws(8192, 11008, 4096, 0, 0) == 11008 * 4096 * 2
+    assert ws(4096, 11008, 8192, 1, 0) == (4096 + 11008) * 8192 * 2
+    assert ws(64, 64, 72, 1, 0) == 0                   # K % 64: staged kernel, no workspace
+    t = lib.agk_transpose_bf16
+    assert t(FAKE, 64, FAKE, 64, 64, 60, None) == 1    # cols not a multiple of 8
+    assert t(FAKE, 64, FAKE, 32, 64, 64, None) == 1    # ld_dst < rows
+    assert t(None, 64, None, 64, 0, 64, None) == 0
+
+
+def _ref(a, b, ta, tb, ks, rs):
+    A = (a.t() if ta else a).float()
+    B = (b.t() if tb else b).float()
+    if ks is not None:
+        A = (A * ks[None, :]).bfloat16().float()   # the stored product is bf16
+    C = A @ B
+    if rs is not None:
+        C = C * rs[:, None]
+    return C
+
+
+CASES = [(256, 256, 64), (264, 520, 72), (8, 8, 8), (1000, 1032, 520), (512, 768, 1024),
+         (136, 264, 192)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", CASES)
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 1), (1, 0)])
+@pytest.mark.parametrize("ws", ["auto", None])
+def test_gemm_against_torch(cuda, M, N, K, ta, tb, ws):
+    import torch
+    torch.manual_seed(M * 7 + N * 3 + K + ta * 2 + tb)
+    a = torch.randn((K, M) if ta else (M, K), device=cuda).bfloat16()
+    b = torch.randn((N, K) if tb else (K, N), device=cuda).bfloat16()
+    for scaled in (False, True):
+        ks = torch.rand(K, device=cuda) + 0.5 if scaled else None
+        rs = torch.rand(M, device=cuda) + 0.5 if scaled else None
+        r = _ref(a, b, ta, tb, ks, rs)
+        for od, tol in ((torch.float32, 1e-5), (torch.bfloat16, 8e-3)):
+            c = agk.gemm_bf16(a, b, trans_a=bool(ta), trans_b=bool(tb), out_dtype=od, kscale=ks,
+                              rowscale=rs, workspace=ws)
+            torch.cuda.synchronize()
+            err = ((c.float() - r).abs().max() / r.abs().max()).item()
+            assert err <= tol, (M, N, K, ta, tb, ws, scaled, od, err)
+    # accumulate into an existing fp32 C, and bit-identical repeats
+    base = torch.randn(M, N, device=cuda)
+    c = agk.gemm_bf16(a, b, c=base.clone(), trans_a=bool(ta), trans_b=bool(tb), accumulate=True,
+                      workspace=ws)
+    c2 = agk.gemm_bf16(a, b, c=base.clone(), trans_a=bool(ta), trans_b=bool(tb), accumulate=True,
+                       workspace=ws)
+    torch.cuda.synchronize()
+    r = _ref(a, b, ta, tb, None, None) + base
+    assert ((c - r).abs().max() / r.abs().max()).item() <= 1e-5
+    assert torch.equal(c, c2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols", [(8, 8), (128, 128), (136, 264), (4096, 11008), (1000, 8)])
+def test_transpose_bit_exact(cuda, rows, cols):
+    import torch
+    x = torch.randn(rows, cols, device=cuda).bfloat16()
+    y = agk.transpose_bf16(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, x.t().contiguous())
+
+
+@pytest.mark.gpu
+def test_gemm_c5_shapes(cuda):
+    """The three products of the RMSNorm + linear layer at full size (8192 x 4096 x 11008),
+    against torch fp32 on sampled rows."""
+    import torch
+    torch.manual_seed(5)
+    M, K, N = 8192, 4096, 11008
+    h = torch.randn(M, K, device=cuda).bfloat16()
+    W = (torch.randn(K, N, device=cuda) * 0.02).bfloat16()
+    dy = torch.randn(M, N, device=cuda).bfloat16()
+    rows = torch.randint(0, M, (64,), device=cuda)
+    y = agk.gemm_bf16(h, W)                                     # y = h W
+    dh = agk.gemm_bf16(dy, W, trans_b=True)                     # dh = dy W^T
+    dW = agk.gemm_bf16(h, dy, trans_a=True, out_dtype=torch.float32)   # dW = h^T dy
+    torch.cuda.synchronize()
+    ry = h[rows].float() @ W.float()
+    rdh = dy[rows].float() @ W.float().t()
+    assert ((y[rows].float() - ry).abs().max() / ry.abs().max()).item() <= 8e-3
+    assert ((dh[rows].float() - rdh).abs().max() / rdh.abs().max()).item() <= 8e-3
+    cols = torch.randint(0, K, (16,), device=cuda)
+    rdW = h[:, cols].float().t() @ dy.float()
+    assert ((dW[cols] - rdW).abs().max() / rdW.abs().max()).item() <= 1e-5
