@@ -207,6 +207,124 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     return out
 
 
+C5_SHAPE = (8192, 4096, 11008)   # x [M, K], W [K, N], dy [M, N]
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+
+
+def run_c5(steps, warmup):
+    """RMSNorm + linear layer (configuration c5): forward + full VJP on one GPU.
+
+    fwd: agk_rmsnorm_fwd (h, inv_rms) -> agk_transpose_bf16 (W^T) -> GEMM y = h W
+    bwd: GEMM dh = dy W^T -> GEMM dW = h^T dy (h, dy transposed into a workspace,
+         fp32 result) -> agk_rmsnorm_bwd (dx, dgamma from dh)
+    The three products are 3 * 2*M*N*K flops; torch.matmul (hipBLASLt) is timed
+    on the same operands in the same run for comparison.
+    """
+    import torch
+
+    import cgadimpl_amd as agk
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, K, N = C5_SHAPE
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    x = torch.randn(M, K, generator=gen, device=dev).bfloat16()
+    g = (torch.rand(K, generator=gen, device=dev) + 0.5).bfloat16()
+    W = (torch.randn(K, N, generator=gen, device=dev) * 0.02).bfloat16()
+    dy = torch.randn(M, N, generator=gen, device=dev).bfloat16()
+    eps = 1e-5
+    h = torch.empty_like(x)
+    inv = torch.empty(M, dtype=torch.float32, device=dev)
+    wt = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    dh = torch.empty_like(x)
+    dW = torch.empty(K, N, dtype=torch.float32, device=dev)
+    dx = torch.empty_like(x)
+    dg = torch.empty(K, dtype=torch.float32, device=dev)
+    ws_n = torch.empty(max(1, agk.rmsnorm_bwd_workspace_bytes(M, K)), dtype=torch.uint8, device=dev)
+    ws_w = torch.empty(agk.gemm_bf16_workspace_bytes(K, N, M, True, False), dtype=torch.uint8,
+                       device=dev)
+    stream = torch.cuda.current_stream()
+    stages = ["rmsnorm_fwd", "transpose_W", "gemm_y", "gemm_dh", "gemm_dW", "rmsnorm_bwd"]
+
+    def step(ev=None):
+        def mark(i):
+            if ev is not None:
+                ev[i].record(stream)
+        mark(0)
+        agk.rmsnorm_fwd(x, g, eps, y=h, inv_rms=inv, stream=stream)
+        mark(1)
+        agk.transpose_bf16(W, wt, stream=stream)
+        mark(2)
+        agk.gemm_bf16(h, wt, y, trans_b=True, workspace=None, stream=stream)
+        mark(3)
+        agk.gemm_bf16(dy, W, dh, trans_b=True, workspace=None, stream=stream)
+        mark(4)
+        agk.gemm_bf16(h, dy, dW, trans_a=True, workspace=ws_w, stream=stream)
+        mark(5)
+        agk.rmsnorm_bwd(x, g, inv, dh, dx=dx, dgamma=dg, workspace=ws_n, stream=stream)
+        mark(6)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {name: sum(e[i].elapsed_time(e[i + 1]) for e in events) / steps
+           for i, name in enumerate(stages)}
+
+    def lib_ms(f, reps=max(3, steps)):
+        for _ in range(2):
+            f()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            f()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    torch_ms = {"gemm_y": lib_ms(lambda: h @ W), "gemm_dh": lib_ms(lambda: dy @ W.t()),
+                "gemm_dW": lib_ms(lambda: h.t() @ dy)}
+    flops = 2.0 * M * N * K
+    gemm_ms = per["gemm_y"] + per["gemm_dh"] + per["gemm_dW"]
+    tflops = 3 * flops / (gemm_ms * 1e-3) / 1e12
+    ms_per_step = wall * 1e3 / steps
+    norm_bytes = 5 * M * K * 2 + 2 * K * 2 + 2 * M * 4 + K * 4
+    norm_ms = per["rmsnorm_fwd"] + per["rmsnorm_bwd"]
+    return {
+        "metric": "RMSNorm+linear fwd+VJP (c5): GEMM TFLOP/s on bf16 MFMA (% of 2.5 PF dense)",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x~N(0,1), gamma~U(0.5,1.5), W~N(0,0.02^2), dy~N(0,1) (torch Philox)",
+        "config": {"workload": "c5: rms_norm(x) * gamma -> matmul W, fwd + VJP (dx, dgamma, dW)",
+                   "M": M, "K": K, "N": N, "gemm_flops_per_step": 3 * flops},
+        "roofline": {"kernel": "gemm_nt_direct (3 products)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "stages_ms": {k: round(v, 4) for k, v in per.items()},
+        "rmsnorm_gbs": round(norm_bytes / (norm_ms * 1e-3) / 1e9, 1),
+        "torch_hipblaslt_ms": {k: round(v, 4) for k, v in torch_ms.items()},
+        "torch_hipblaslt_tflops": round(3 * flops / (sum(torch_ms.values()) * 1e-3) / 1e12, 1),
+        "cpu_baseline": None,
+    }
+
+
 def copy_probe(mib, steps):
     """Device-to-device copies of a known size (torch's copy kernel).
 
@@ -230,7 +348,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default=DEFAULT_CONFIG,
-                    help="c1, c2 (default, the headline), c3, c4a, c4b, c4c, or 'all'")
+                    help="c1, c2 (default, the headline), c3, c4a, c4b, c4c, c5 (RMSNorm + "
+                         "linear), or 'all'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline budget in seconds (0 disables it)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -250,10 +369,13 @@ def main():
         sys.exit(2)
 
     from cgadimpl_amd import configs
-    names = list(configs.CONFIGS) if args.config == "all" else [args.config]
+    names = list(configs.CONFIGS) + ["c5"] if args.config == "all" else [args.config]
     for name in names:
-        rec = run(name, args.steps, args.warmup,
-                  args.cpu_seconds if name == DEFAULT_CONFIG or args.config != "all" else 0)
+        if name == "c5":
+            rec = run_c5(args.steps, args.warmup)
+        else:
+            rec = run(name, args.steps, args.warmup,
+                      args.cpu_seconds if name == DEFAULT_CONFIG or args.config != "all" else 0)
         print(json.dumps(rec), flush=True)
 
 

@@ -15,7 +15,7 @@ from typing import Optional, Tuple
 __all__ = [
     "AgkError", "lib", "lib_path", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_bwd_workspace_bytes",
     "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
-    "transpose_bf16", "AGK_F32", "AGK_BF16", "STATUS",
+    "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -275,3 +275,29 @@ def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate=False, want_da: bool
                                     ws_bytes, rows, cols, _dtype_code(a), acc, _stream(stream))
     _check(rc, "agk_mul_rowbcast_bwd")
     return da, db
+
+
+# ---- the RMSNorm + linear layer (configuration c5) --------------------------------
+
+def rmsnorm_linear_fwd(x, gamma, W, eps: float, wt=None, stream=None):
+    """h = rms_norm(x) * gamma, y = h @ W.  bf16 x [M, K], gamma [K], W [K, N].
+
+    W is transposed once (wt, [N, K]) so the product runs with both operands
+    k-contiguous.  Returns (y, h, inv_rms, wt).
+    """
+    h, inv = rmsnorm_fwd(x, gamma, eps, stream=stream)
+    wt = transpose_bf16(W, wt, stream=stream)
+    y = gemm_bf16(h, wt, trans_b=True, workspace=None, stream=stream)
+    return y, h, inv, wt
+
+
+def rmsnorm_linear_bwd(x, gamma, inv_rms, h, W, dy, dw_dtype=None, stream=None):
+    """VJP of the layer: dh = dy @ W^T, dW = h^T @ dy, then the RMSNorm VJP of dh.
+
+    Returns (dx, dgamma, dW); dW is float32 unless dw_dtype says otherwise.
+    """
+    torch = _torch()
+    dh = gemm_bf16(dy, W, trans_b=True, workspace=None, stream=stream)
+    dW = gemm_bf16(h, dy, trans_a=True, out_dtype=dw_dtype or torch.float32, stream=stream)
+    dx, dgamma = rmsnorm_bwd(x, gamma, inv_rms, dh, stream=stream)
+    return dx, dgamma, dW

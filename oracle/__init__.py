@@ -141,3 +141,43 @@ def bf16_decode(bits: np.ndarray) -> np.ndarray:
     out = np.empty(bits.shape, dtype=np.float32)
     load().oracle_bf16_decode(_p(bits), _p(out), bits.size)
     return out
+
+
+# ---- RMSNorm + linear layer (configuration c5) --------------------------------
+# The reference composes the layer from graph ops: h = rms(x) * gamma
+# (normalization.cpp:23-35, arithmetic.cpp:31-39), y = matmul(h, W)
+# (cgadimpl/src/ops/linalg.cpp:12-20), and its VJP runs vjp_MatMul
+# (cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:258-263: dA += gy B^T,
+# dB += A^T gy) before the RMSNorm rules.  Restated here with bf16 storage of
+# x, gamma, W, h, y, dy and dh (values rounded to nearest even where the graph
+# stores them), products in float64, dW returned in float32.
+
+def matmul_f64(a, b):
+    """A @ B in float64 (the textbook product; numpy's routine)."""
+    return np.asarray(a, np.float64) @ np.asarray(b, np.float64)
+
+
+def linear_fwd(h_bits, w_bits):
+    """y = h W for bf16 bit patterns; returns y as bf16 bits."""
+    return bf16_encode(matmul_f64(bf16_decode(h_bits), bf16_decode(w_bits)).astype(np.float32))
+
+
+def linear_bwd(h_bits, w_bits, dy_bits):
+    """vjp_MatMul: dh = dy W^T (bf16 bits), dW = h^T dy (float32)."""
+    h, w, dy = bf16_decode(h_bits), bf16_decode(w_bits), bf16_decode(dy_bits)
+    dh = bf16_encode(matmul_f64(dy, w.T).astype(np.float32))
+    dw = matmul_f64(h.T, dy).astype(np.float32)
+    return dh, dw
+
+
+def rmsnorm_linear_layer(x_bits, gamma_bits, w_bits, dy_bits, eps):
+    """Forward + VJP of matmul(rms_norm(x) * gamma, W) seeded with dy.
+
+    Returns dict(h, inv_rms, y, dh, dx, dgamma, dW): bf16 bits for h, y, dh,
+    dx; float32 for inv_rms, dgamma, dW.
+    """
+    h, inv = fwd(x_bits, gamma_bits, eps)
+    y = linear_fwd(h, w_bits)
+    dh, dw = linear_bwd(h, w_bits, dy_bits)
+    dx, dg = bwd(x_bits, gamma_bits, inv, dh)
+    return {"h": h, "inv_rms": inv, "y": y, "dh": dh, "dx": dx, "dgamma": dg, "dW": dw}

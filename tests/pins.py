@@ -19,6 +19,9 @@ planted mistake (each must fail at least one check).  What pins what:
   dgamma_ones  dy = 1, no gamma: dgamma = column sums of the forward output
   permutation  permuting rows permutes y and dx and leaves dgamma unchanged
   accumulate   accumulate=1 adds onto existing gradients
+  linear       the RMSNorm + linear layer: y = h I = h for an identity W; central
+               differences of sum(y * dy) with respect to h and W give dh and dW;
+               the layer's dx equals the RMSNorm VJP of dh = dy W^T
 """
 from __future__ import annotations
 
@@ -268,8 +271,60 @@ def check_accumulate(mutation: int = 0):
     return fails
 
 
+def check_linear(mutation: int = 0):
+    """matmul + VJP of the c5 layer on small bf16 inputs."""
+    fails = []
+    rng = np.random.default_rng(23)
+    bits = lambda a: oracle.bf16_encode(np.asarray(a, np.float32))  # noqa: E731
+    dec = oracle.bf16_decode
+    # identity: y == h exactly (products of bf16 values by 1 and 0 are exact)
+    h = bits(rng.standard_normal((6, 8)))
+    y = oracle.linear_fwd(h, bits(np.eye(8)))
+    if not np.array_equal(y, h):
+        fails.append("linear identity: y != h")
+    # central differences of L = sum(y * dy) in float64 (the bf16 rounding of y
+    # is outside the derivative; compare against the exact products)
+    hf = dec(bits(rng.standard_normal((5, 7)))).astype(np.float64)
+    wf = dec(bits(0.3 * rng.standard_normal((7, 4)))).astype(np.float64)
+    dyf = dec(bits(rng.standard_normal((5, 4)))).astype(np.float64)
+    dh, dw = oracle.linear_bwd(bits(hf), bits(wf), bits(dyf))
+
+    def loss(hh, ww):
+        return float(np.sum(oracle.matmul_f64(hh, ww) * dyf))
+
+    eps = 1e-4
+    num_dh = np.zeros_like(hf)
+    for i in np.ndindex(hf.shape):
+        p, m = hf.copy(), hf.copy()
+        p[i] += eps
+        m[i] -= eps
+        num_dh[i] = (loss(p, wf) - loss(m, wf)) / (2 * eps)
+    num_dw = np.zeros_like(wf)
+    for i in np.ndindex(wf.shape):
+        p, m = wf.copy(), wf.copy()
+        p[i] += eps
+        m[i] -= eps
+        num_dw[i] = (loss(hf, p) - loss(hf, m)) / (2 * eps)
+    if not np.max(np.abs(dec(dh) - num_dh)) <= 1e-2 * max(1.0, np.max(np.abs(num_dh))):
+        fails.append("linear dh central differences")
+    if not np.max(np.abs(dw - num_dw)) <= 1e-6 * max(1.0, np.max(np.abs(num_dw))):
+        fails.append("linear dW central differences")
+    # the layer composes the RMSNorm VJP with dh
+    x = bits(rng.standard_normal((4, 16)))
+    g = bits(rng.uniform(0.5, 1.5, 16))
+    w = bits(0.2 * rng.standard_normal((16, 8)))
+    dy = bits(rng.standard_normal((4, 8)))
+    out = oracle.rmsnorm_linear_layer(x, g, w, dy, 1e-5)
+    h2, inv2 = oracle.fwd(x, g, 1e-5, mutation=mutation)
+    dh2, _ = oracle.linear_bwd(h2, w, dy)
+    dx2, dg2 = oracle.bwd(x, g, inv2, dh2, mutation=mutation)
+    if not (np.array_equal(out["dx"], dx2) and np.array_equal(out["dgamma"], dg2)):
+        fails.append("layer: dx, dgamma != RMSNorm VJP of dh")
+    return fails
+
+
 ALL_CHECKS = (check_golden, check_fd, check_fd_truth, check_invariant, check_special,
-              check_dgamma_ones, check_permutation, check_accumulate)
+              check_dgamma_ones, check_permutation, check_accumulate, check_linear)
 
 
 def run_all(mutation: int = 0):
