@@ -1,7 +1,7 @@
 """cgadimpl_amd -- MI355X (gfx950) RMSNorm layer path for cgadimpl's autodiff API.
 
 The product is native: HIP kernels behind the C ABI in ``include/agk_rmsnorm.h``
-(``lib/libagk_rmsnorm.so``) and the C++ ``ag::`` layer above it.  This Python
+and ``include/agk_rowops.h`` (``lib/libagk_rmsnorm.so``) and the C++ ``ag::`` layer above it.  This Python
 module is plumbing for tests and benchmarks: it binds that C ABI with ctypes
 and hands it torch device tensors (memory) and the current HIP stream.  There
 is no Python or CPU fallback: if the library is missing, every call raises.
@@ -15,7 +15,9 @@ from typing import Optional, Tuple
 __all__ = [
     "AgkError", "lib", "lib_path", "rmsnorm_fwd", "rmsnorm_bwd", "rmsnorm_bwd_workspace_bytes",
     "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
-    "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "AGK_F32", "AGK_BF16", "STATUS",
+    "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "rmsnorm_jvp", "layernorm_fwd",
+    "layernorm_bwd", "softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
+    "logsumexp_jvp", "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -28,7 +30,8 @@ AGK_ACCUM_DGAMMA = 2
 AGK_ACCUM_ALL = 3
 STATUS = {0: "AGK_OK", 1: "AGK_EINVAL", 2: "AGK_EDTYPE", 3: "AGK_EWORKSPACE", 4: "AGK_EHIP"}
 
-# Every symbol include/agk_rmsnorm.h declares, with its ctypes signature.
+# Every symbol include/agk_rmsnorm.h and include/agk_rowops.h declare, with its
+# ctypes signature.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 SIGNATURES = {
@@ -47,6 +50,16 @@ SIGNATURES = {
                                                         ctypes.c_int]),
     "agk_transpose_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),
     "agk_rmsnorm_launch_plan": (ctypes.c_int, [_I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
+    "agk_rmsnorm_jvp": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_layernorm_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_float, ctypes.c_int,
+                                         _P]),
+    "agk_layernorm_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int,
+                                         _P]),
+    "agk_softmax_fwd": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_softmax_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
+    "agk_logsumexp_fwd": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_logsumexp_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
+    "agk_logsumexp_jvp": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
     "agk_version": (ctypes.c_char_p, []),
@@ -301,3 +314,105 @@ def rmsnorm_linear_bwd(x, gamma, inv_rms, h, W, dy, dw_dtype=None, stream=None):
     dW = gemm_bf16(h, dy, trans_a=True, out_dtype=dw_dtype or torch.float32, stream=stream)
     dx, dgamma = rmsnorm_bwd(x, gamma, inv_rms, dh, stream=stream)
     return dx, dgamma, dW
+
+
+# ---- row ops sharing the row-reduce skeleton (include/agk_rowops.h) -------------
+
+def _rows_cols(t):
+    cols = t.shape[-1] if t.dim() else 1
+    return (t.numel() // cols if cols else 0), cols
+
+
+def _row_stat_like(x, dtype):
+    torch = _torch()
+    return torch.empty(x.shape[:-1] + (1,), dtype=dtype, device=x.device)
+
+
+def _acc_dx(accumulate) -> int:
+    return AGK_ACCUM_DX if accumulate else 0
+
+
+def rmsnorm_jvp(x, gamma, inv_rms, tx, tgamma=None, ty=None, stream=None):
+    """Tangent of y = rms_norm(x) * gamma along (tx, tgamma); inv_rms from rmsnorm_fwd."""
+    torch = _torch()
+    rows, cols = _rows_cols(x)
+    if ty is None:
+        ty = torch.empty_like(x)
+    rc = lib().agk_rmsnorm_jvp(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(tx), _ptr(tgamma),
+                               _ptr(ty), rows, cols, _dtype_code(x), _stream(stream))
+    _check(rc, "agk_rmsnorm_jvp")
+    return ty
+
+
+def layernorm_fwd(x, eps: float = 1e-5, y=None, mean=None, rstd=None, stream=None):
+    """y = (x - mean) / sqrt(var + eps) over the last axis; returns (y, mean, rstd)."""
+    torch = _torch()
+    rows, cols = _rows_cols(x)
+    y = torch.empty_like(x) if y is None else y
+    mean = _row_stat_like(x, torch.float32) if mean is None else mean
+    rstd = _row_stat_like(x, torch.float32) if rstd is None else rstd
+    rc = lib().agk_layernorm_fwd(_ptr(x), _ptr(y), _ptr(mean), _ptr(rstd), rows, cols,
+                                 float(eps), _dtype_code(x), _stream(stream))
+    _check(rc, "agk_layernorm_fwd")
+    return y, mean, rstd
+
+
+def layernorm_bwd(x, mean, rstd, dy, dx=None, accumulate: bool = False, stream=None):
+    """dx (+)= VJP of LayerNorm for upstream dy (also the JVP for dy = a tangent)."""
+    torch = _torch()
+    rows, cols = _rows_cols(x)
+    dx = (torch.zeros_like(x) if accumulate else torch.empty_like(x)) if dx is None else dx
+    rc = lib().agk_layernorm_bwd(_ptr(x), _ptr(mean), _ptr(rstd), _ptr(dy), _ptr(dx), rows, cols,
+                                 _dtype_code(x), _acc_dx(accumulate), _stream(stream))
+    _check(rc, "agk_layernorm_bwd")
+    return dx
+
+
+def softmax_fwd(z, y=None, stream=None):
+    torch = _torch()
+    rows, cols = _rows_cols(z)
+    y = torch.empty_like(z) if y is None else y
+    rc = lib().agk_softmax_fwd(_ptr(z), _ptr(y), rows, cols, _dtype_code(z), _stream(stream))
+    _check(rc, "agk_softmax_fwd")
+    return y
+
+
+def softmax_bwd(y, dy, dz=None, accumulate: bool = False, stream=None):
+    """dz (+)= y * (dy - sum(y * dy)) (also the JVP for dy = a tangent)."""
+    torch = _torch()
+    rows, cols = _rows_cols(y)
+    dz = (torch.zeros_like(y) if accumulate else torch.empty_like(y)) if dz is None else dz
+    rc = lib().agk_softmax_bwd(_ptr(y), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(y),
+                               _acc_dx(accumulate), _stream(stream))
+    _check(rc, "agk_softmax_bwd")
+    return dz
+
+
+def logsumexp_fwd(z, y=None, stream=None):
+    """y[..., 0] = log(sum(exp(z), -1)); y has z's dtype and shape z.shape[:-1] + (1,)."""
+    rows, cols = _rows_cols(z)
+    y = _row_stat_like(z, z.dtype) if y is None else y
+    rc = lib().agk_logsumexp_fwd(_ptr(z), _ptr(y), rows, cols, _dtype_code(z), _stream(stream))
+    _check(rc, "agk_logsumexp_fwd")
+    return y
+
+
+def logsumexp_bwd(z, dy, dz=None, accumulate: bool = False, stream=None):
+    """dz (+)= dy * softmax(z); dy has shape z.shape[:-1] + (1,) and z's dtype."""
+    torch = _torch()
+    rows, cols = _rows_cols(z)
+    dz = (torch.zeros_like(z) if accumulate else torch.empty_like(z)) if dz is None else dz
+    rc = lib().agk_logsumexp_bwd(_ptr(z), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(z),
+                                 _acc_dx(accumulate), _stream(stream))
+    _check(rc, "agk_logsumexp_bwd")
+    return dz
+
+
+def logsumexp_jvp(z, tz, ty=None, stream=None):
+    """ty[..., 0] = sum(softmax(z) * tz, -1)."""
+    rows, cols = _rows_cols(z)
+    ty = _row_stat_like(z, z.dtype) if ty is None else ty
+    rc = lib().agk_logsumexp_jvp(_ptr(z), _ptr(tz), _ptr(ty), rows, cols, _dtype_code(z),
+                                 _stream(stream))
+    _check(rc, "agk_logsumexp_jvp")
+    return ty

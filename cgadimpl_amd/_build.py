@@ -1,7 +1,8 @@
 """Build recipe for the native libraries of cgadimpl_amd.
 
 Outputs (in-tree, git-ignored, shipped with the source tree):
-  cgadimpl_amd/lib/libagk_rmsnorm.so   HIP kernels + C ABI (include/agk_rmsnorm.h)
+  cgadimpl_amd/lib/libagk_rmsnorm.so   HIP kernels + C ABI (include/agk_rmsnorm.h,
+                                       include/agk_rowops.h)
   cgadimpl_amd/lib/libagk_synth.so     seeded synthetic input generator (host)
   cgadimpl_amd/lib/libag.so            the C++ graph layer (ag::Value, rms, rms_norm,
                                        mul, backward) over the C ABI (host C++)
@@ -57,10 +58,20 @@ def _atomic_build(out: str, cmd_for: callable) -> None:
 
 
 def hip_library(name: str, sources: list[str], extra: list[str] | None = None) -> str:
+    """Compiles each source to an object (in parallel), then links the library."""
     out = os.path.join(LIB, name)
-    srcs = [os.path.join(CSRC, s) for s in sources]
-    _atomic_build(out, lambda o: [HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs,
-                                  *(extra or []), "-o", o])
+    objdir = os.path.join(LIB, "obj")
+    os.makedirs(objdir, exist_ok=True)
+
+    def compile_one(src: str) -> str:
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        _atomic_build(obj, lambda o: [HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", "-c",
+                                      os.path.join(CSRC, src), *(extra or []), "-o", o])
+        return obj
+
+    with ThreadPoolExecutor(max_workers=len(sources)) as ex:
+        objs = list(ex.map(compile_one, sources))
+    _atomic_build(out, lambda o: [HIPCC, *HIP_FLAGS, "-shared", *objs, "-o", o])
     return out
 
 
@@ -102,7 +113,7 @@ def build_all(verbose: bool = True) -> list[str]:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(LIB, exist_ok=True)
     jobs = [
-        lambda: hip_library("libagk_rmsnorm.so", ["rmsnorm.hip", "gemm.hip"]),
+        lambda: hip_library("libagk_rmsnorm.so", ["rmsnorm.hip", "gemm.hip", "rowops.hip"]),
         lambda: host_library("libagk_synth.so", ["synth.cpp"]),
     ]
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:

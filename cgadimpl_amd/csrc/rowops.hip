@@ -1,0 +1,688 @@
+// rowops.hip -- CDNA4 (gfx950) kernels and C ABI (include/agk_rowops.h) for
+// the row ops that share the RMSNorm layer's row-reduce skeleton: the
+// corrected forward-mode product of RMSNorm, LayerNorm, row softmax and row
+// log-sum-exp, with their backward (and forward-mode) products.
+//
+// Reference behaviour replaced here (paths relative to the reference tree):
+//   jvp_RMSNorm            cgadimpl/src/autodiff/autodiff_jvp_ops.cpp:366-379
+//                          (with its 1/rms-vs-rms error corrected)
+//   laynor_nodeops         cgadimpl/src/ops/normalization.cpp:10-22
+//   vjp_LayerNorm          cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:351-365
+//   softmax_row_nodeops    cgadimpl/src/ops/reduction.cpp:42-53
+//   vjp_SoftmaxRow         autodiff_vjp_ops.cpp:421-428
+//   logsumexp_row_nodeops  reduction.cpp:54-66
+//   vjp_LogSumExpRow       autodiff_vjp_ops.cpp:430-440
+//   jvp_LogSumExpRow       autodiff_jvp_ops.cpp:421-434
+// The reference evaluates each of these as a chain of tensor-library kernels
+// that materialise every intermediate (max, shifted row, exponentials, sums,
+// quotients).  Here every op is one kernel: each input row is read from HBM
+// once into registers, the row reductions run on the held values (DPP within
+// a wave, LDS across waves), and each output row is written once.
+//
+// Structure.  An op is a small policy (the structs under "ops") written
+// against a row context that offers sum / sum2 / max reductions over the row
+// and a store of an element-wise function of it.  Two contexts implement that
+// interface: Resident (the row held in registers by TPR lanes, NV 16-byte
+// slots per lane, G rows per workgroup -- the launch shapes and plan of the
+// RMSNorm forward) and Looped (one 256-lane workgroup per row, element-wise
+// accesses that re-read the row from cache; any alignment, any width).
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "agk_rowops.h"
+#include "rowcommon.hpp"
+
+namespace agk {
+namespace rowops {
+
+// Pointers and scalars of one call.  Each op names the fields it reads.
+struct RowArgs {
+    const void* in0 = nullptr;   // row input 0, [rows, cols]
+    const void* in1 = nullptr;   // row input 1, [rows, cols]
+    const void* col0 = nullptr;  // column vector 0, [cols]
+    const void* col1 = nullptr;  // column vector 1, [cols]
+    const float* rs0 = nullptr;  // per-row fp32 input 0, [rows]
+    const float* rs1 = nullptr;  // per-row fp32 input 1, [rows]
+    const void* rsv = nullptr;   // per-row input of the storage type, [rows]
+    void* out = nullptr;         // row output, [rows, cols]
+    void* out_row = nullptr;     // per-row output of the storage type, [rows]
+    float* ws0 = nullptr;        // per-row fp32 output 0, [rows]
+    float* ws1 = nullptr;        // per-row fp32 output 1, [rows]
+    float eps = 0.0f;
+    int acc = 0;                 // out += f instead of out = f
+};
+
+// ---- reductions ----------------------------------------------------------------
+
+struct SumR {
+    static constexpr float kId = 0.0f;
+    __device__ static float op(float a, float b) { return a + b; }
+};
+struct MaxR {
+    static constexpr float kId = -__builtin_inff();
+    __device__ static float op(float a, float b) { return fmaxf(a, b); }
+};
+
+// Reduction over the TPR (<= 64) lanes of a row group with the pairing of
+// group_sum: every pairing is symmetric, so all lanes of the group end with
+// the same bits.
+template <int TPR, class R>
+__device__ __forceinline__ float group_reduce(float v) {
+    if constexpr (TPR >= 2) v = R::op(v, dpp_mov<0xb1>(v));
+    if constexpr (TPR >= 4) v = R::op(v, dpp_mov<0x4e>(v));
+    if constexpr (TPR >= 8) v = R::op(v, dpp_mov<0x141>(v));
+    if constexpr (TPR >= 16) v = R::op(v, dpp_mov<0x140>(v));
+    if constexpr (TPR >= 32)
+        v = R::op(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f)));
+    if constexpr (TPR >= 64)
+        v = R::op(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+    return v;
+}
+
+// LDS slots per parity for N <= 2 values per row.
+template <int TPR, int G>
+constexpr int red_slots() {
+    return TPR > 64 ? 2 * G * (TPR / 64) : 1;
+}
+
+// Row reduction of N values for rows spread over TPR lanes, G rows per
+// workgroup.  For TPR > 64 the per-wave results meet in `red` (double-buffered
+// by `parity`, one barrier per reduction) and are combined in wave order.
+template <int TPR, int G, int N, class R>
+__device__ __forceinline__ void row_reduce(float (&v)[N],
+                                           float (*red)[TPR > 64 ? 2 * G * (TPR / 64) : 1],
+                                           int parity) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = group_reduce<TPR, R>(v[i]);
+    if constexpr (TPR > 64) {
+        constexpr int kWaves = TPR / 64;
+        const int lane = threadIdx.x & 63;
+        const int base = (threadIdx.x / TPR) * kWaves;
+        const int wave_in_row = (threadIdx.x % TPR) >> 6;
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) red[parity][(base + wave_in_row) * N + i] = v[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            float s = red[parity][base * N + i];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) s = R::op(s, red[parity][(base + w) * N + i]);
+            v[i] = s;
+        }
+    }
+}
+
+// ---- row contexts --------------------------------------------------------------
+// Interface used by the ops (every lane of the workgroup calls the reductions;
+// store and the put_* calls act only for rows that exist):
+//   ncols, inv_cols                  cols and 1 / cols as floats
+//   sum(f), max(f)                   reduce f(a, b) over the row
+//   sum2(f, s0, s1)                  f(a, b, o) fills o[2]; both summed
+//   store(out, acc, c0, d0, c1, d1, f)
+//                                    out[col] (+)= f(a, b, u, v), u = c0[col]
+//                                    (d0 when c0 is null), v likewise
+//   row_f32(p), row_val(p)           p[row] (fp32 / storage type)
+//   put_f32(p, v), put_val(p, v)     p[row] = v (fp32 / storage type)
+// a and b are the elements of in0 and in1 (b = 0 for one-input ops).
+
+template <class S, int TPR, int NV, int G, int NIN>
+struct Resident {
+    using T = typename S::T;
+    static constexpr int W = S::kVec;
+    static constexpr int kSlots = red_slots<TPR, G>();
+
+    float (*red)[kSlots];
+    int parity = 0;
+    int t;
+    int64_t row;
+    bool active;
+    int cols;
+    float ncols, inv_cols;
+    u32x4 a[NV], b[NV];
+
+    __device__ Resident(const RowArgs& p, int64_t rows, int cols_, float (*red_)[kSlots])
+        : red(red_), cols(cols_) {
+        t = threadIdx.x % TPR;
+        row = static_cast<int64_t>(blockIdx.x) * G + threadIdx.x / TPR;
+        active = row < rows;
+        ncols = static_cast<float>(cols);
+        inv_cols = 1.0f / ncols;
+        const int64_t off = (active ? row : 0) * static_cast<int64_t>(cols);
+        const T* x = static_cast<const T*>(p.in0) + off;
+        const T* y = NIN == 2 ? static_cast<const T*>(p.in1) + off : nullptr;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            const bool ok = active && col < cols;
+            a[k] = ok ? load16_stream<S>(x + col) : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (NIN == 2)
+                b[k] = ok ? load16_stream<S>(y + col) : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+
+    template <class R, int N, class F>
+    __device__ __forceinline__ void reduce(float (&res)[N], F f) {
+        float part[N][W];
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[i][e] = R::kId;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            if ((t + k * TPR) * W < cols) {
+                float fa[W], fb[W];
+                S::unpack(a[k], fa);
+                if constexpr (NIN == 2) S::unpack(b[k], fb);
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    float o[N];
+                    f(fa[e], NIN == 2 ? fb[e] : 0.0f, o);
+#pragma unroll
+                    for (int i = 0; i < N; ++i) part[i][e] = R::op(part[i][e], o[i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            float s = part[i][0];
+#pragma unroll
+            for (int e = 1; e < W; ++e) s = R::op(s, part[i][e]);
+            res[i] = s;
+        }
+        row_reduce<TPR, G, N, R>(res, red, parity);
+        parity ^= 1;
+    }
+
+    template <class F>
+    __device__ __forceinline__ float sum(F f) {
+        float r[1];
+        reduce<SumR>(r, [&](float x, float y, float (&o)[1]) { o[0] = f(x, y); });
+        return r[0];
+    }
+    template <class F>
+    __device__ __forceinline__ float max(F f) {
+        float r[1];
+        reduce<MaxR>(r, [&](float x, float y, float (&o)[1]) { o[0] = f(x, y); });
+        return r[0];
+    }
+    template <class F>
+    __device__ __forceinline__ void sum2(F f, float& s0, float& s1) {
+        float r[2];
+        reduce<SumR>(r, f);
+        s0 = r[0];
+        s1 = r[1];
+    }
+
+    template <class F>
+    __device__ __forceinline__ void store(void* out, int acc, const void* c0, float d0,
+                                          const void* c1, float d1, F f) const {
+        if (!active) return;
+        T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            if (col < cols) {
+                float fa[W], fb[W], fu[W], fv[W], r[W];
+                S::unpack(a[k], fa);
+                if constexpr (NIN == 2) S::unpack(b[k], fb);
+                if (c0) {
+                    S::unpack(load16<S>(static_cast<const T*>(c0) + col), fu);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) fu[e] = d0;
+                }
+                if (c1) {
+                    S::unpack(load16<S>(static_cast<const T*>(c1) + col), fv);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) fv[e] = d1;
+                }
+#pragma unroll
+                for (int e = 0; e < W; ++e) r[e] = f(fa[e], NIN == 2 ? fb[e] : 0.0f, fu[e], fv[e]);
+                if (acc) {
+                    float old[W];
+                    S::unpack(load16_stream<S>(o + col), old);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) r[e] = old[e] + r[e];
+                }
+                store16_stream<S>(o + col, S::pack(r));
+            }
+        }
+    }
+
+    __device__ float row_f32(const float* p) const { return active ? p[row] : 0.0f; }
+    __device__ float row_val(const void* p) const {
+        return active ? S::get(static_cast<const T*>(p) + row) : 0.0f;
+    }
+    __device__ void put_f32(float* p, float v) const {
+        if (active && t == 0) p[row] = v;
+    }
+    __device__ void put_val(void* p, float v) const {
+        if (active && t == 0) S::put(static_cast<T*>(p) + row, v);
+    }
+};
+
+template <class S, int NIN>
+struct Looped {
+    using T = typename S::T;
+    static constexpr int kSlots = red_slots<kBlock, 1>();
+
+    float (*red)[kSlots];
+    int parity = 0;
+    int64_t row;
+    int cols;
+    float ncols, inv_cols;
+    const T* x;
+    const T* y;
+
+    __device__ Looped(const RowArgs& p, int64_t row_, int cols_, float (*red_)[kSlots])
+        : red(red_), row(row_), cols(cols_) {
+        ncols = static_cast<float>(cols);
+        inv_cols = 1.0f / ncols;
+        const int64_t off = row * static_cast<int64_t>(cols);
+        x = static_cast<const T*>(p.in0) + off;
+        y = NIN == 2 ? static_cast<const T*>(p.in1) + off : nullptr;
+    }
+
+    template <class R, int N, class F>
+    __device__ __forceinline__ void reduce(float (&res)[N], F f) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) res[i] = R::kId;
+        for (int c = threadIdx.x; c < cols; c += kBlock) {
+            float o[N];
+            f(S::get(x + c), NIN == 2 ? S::get(y + c) : 0.0f, o);
+#pragma unroll
+            for (int i = 0; i < N; ++i) res[i] = R::op(res[i], o[i]);
+        }
+        row_reduce<kBlock, 1, N, R>(res, red, parity);
+        parity ^= 1;
+    }
+
+    template <class F>
+    __device__ __forceinline__ float sum(F f) {
+        float r[1];
+        reduce<SumR>(r, [&](float a, float b, float (&o)[1]) { o[0] = f(a, b); });
+        return r[0];
+    }
+    template <class F>
+    __device__ __forceinline__ float max(F f) {
+        float r[1];
+        reduce<MaxR>(r, [&](float a, float b, float (&o)[1]) { o[0] = f(a, b); });
+        return r[0];
+    }
+    template <class F>
+    __device__ __forceinline__ void sum2(F f, float& s0, float& s1) {
+        float r[2];
+        reduce<SumR>(r, f);
+        s0 = r[0];
+        s1 = r[1];
+    }
+
+    template <class F>
+    __device__ __forceinline__ void store(void* out, int acc, const void* c0, float d0,
+                                          const void* c1, float d1, F f) const {
+        T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
+        const T* u = static_cast<const T*>(c0);
+        const T* v = static_cast<const T*>(c1);
+        for (int c = threadIdx.x; c < cols; c += kBlock) {
+            float r = f(S::get(x + c), NIN == 2 ? S::get(y + c) : 0.0f, u ? S::get(u + c) : d0,
+                        v ? S::get(v + c) : d1);
+            if (acc) r = S::get(o + c) + r;
+            S::put(o + c, r);
+        }
+    }
+
+    __device__ float row_f32(const float* p) const { return p[row]; }
+    __device__ float row_val(const void* p) const {
+        return S::get(static_cast<const T*>(p) + row);
+    }
+    __device__ void put_f32(float* p, float v) const {
+        if (threadIdx.x == 0) p[row] = v;
+    }
+    __device__ void put_val(void* p, float v) const {
+        if (threadIdx.x == 0) S::put(static_cast<T*>(p) + row, v);
+    }
+};
+
+// ---- ops -------------------------------------------------------------------------
+
+// Forward-mode product of the RMSNorm layer (in0 = x, in1 = tx, col0 = gamma,
+// col1 = tgamma, rs0 = inv_rms, out = ty):
+//   ty = gamma * (r * (tx - x * s)) + tgamma * (x * r),  s = r^2 * sum(tx*x) / cols
+struct RmsJvp {
+    static constexpr int kIn = 2;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float r = c.row_f32(p.rs0);
+        const float dot = c.sum([](float x, float t) { return t * x; });
+        const float s = (r * r * dot) * c.inv_cols;
+        const bool has_tg = p.col1 != nullptr;
+        c.store(p.out, 0, p.col0, 1.0f, p.col1, 0.0f,
+                [=](float x, float t, float g, float tg) {
+                    const float o = g * (r * (t - x * s));
+                    return has_tg ? o + tg * (x * r) : o;
+                });
+    }
+};
+
+// LayerNorm forward (in0 = x, out = y, ws0 = mean, ws1 = rstd):
+//   mean = sum(x)/cols, var = sum((x - mean)^2)/cols, rstd = 1/sqrt(var + eps),
+//   y = (x - mean) * rstd
+struct LnFwd {
+    static constexpr int kIn = 1;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float mean = c.sum([](float x, float) { return x; }) / c.ncols;
+        const float var = c.sum([=](float x, float) {
+            const float d = x - mean;
+            return d * d;
+        }) / c.ncols;
+        const float rstd = 1.0f / sqrtf(var + p.eps);
+        c.put_f32(p.ws0, mean);
+        c.put_f32(p.ws1, rstd);
+        c.store(p.out, 0, nullptr, 0.0f, nullptr, 0.0f,
+                [=](float x, float, float, float) { return (x - mean) * rstd; });
+    }
+};
+
+// LayerNorm backward (in0 = x, in1 = dy, rs0 = mean, rs1 = rstd, out = dx):
+//   xhat = (x - mean) * rstd,  dx (+)= rstd * (dy - sum(dy)/cols - xhat * sum(dy*xhat)/cols)
+struct LnBwd {
+    static constexpr int kIn = 2;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float mean = c.row_f32(p.rs0);
+        const float rstd = c.row_f32(p.rs1);
+        float sg = 0.0f, sgx = 0.0f;
+        c.sum2(
+            [=](float x, float g, float (&o)[2]) {
+                o[0] = g;
+                o[1] = g * ((x - mean) * rstd);
+            },
+            sg, sgx);
+        const float mg = sg * c.inv_cols;
+        const float mgx = sgx * c.inv_cols;
+        c.store(p.out, p.acc, nullptr, 0.0f, nullptr, 0.0f,
+                [=](float x, float g, float, float) {
+                    return rstd * (g - mg - ((x - mean) * rstd) * mgx);
+                });
+    }
+};
+
+// Row softmax (in0 = z, out = y): y = exp(z - m) / sum(exp(z - m)), m = max(z).
+struct SmFwd {
+    static constexpr int kIn = 1;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float m = c.max([](float z, float) { return z; });
+        const float s = c.sum([=](float z, float) { return expf(z - m); });
+        c.store(p.out, 0, nullptr, 0.0f, nullptr, 0.0f,
+                [=](float z, float, float, float) { return expf(z - m) / s; });
+    }
+};
+
+// Row softmax backward from the output (in0 = y, in1 = dy, out = dz):
+//   dz (+)= y * (dy - sum(y * dy))
+struct SmBwd {
+    static constexpr int kIn = 2;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float dot = c.sum([](float y, float g) { return y * g; });
+        c.store(p.out, p.acc, nullptr, 0.0f, nullptr, 0.0f,
+                [=](float y, float g, float, float) { return y * (g - dot); });
+    }
+};
+
+// Row log-sum-exp (in0 = z, out_row = y): y = log(sum(exp(z - m))) + m.
+struct LseFwd {
+    static constexpr int kIn = 1;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float m = c.max([](float z, float) { return z; });
+        const float s = c.sum([=](float z, float) { return expf(z - m); });
+        c.put_val(p.out_row, logf(s) + m);
+    }
+};
+
+// Row log-sum-exp backward (in0 = z, rsv = dy, out = dz):
+//   dz (+)= dy * (exp(z - m) / sum(exp(z - m)))
+struct LseBwd {
+    static constexpr int kIn = 1;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float m = c.max([](float z, float) { return z; });
+        const float s = c.sum([=](float z, float) { return expf(z - m); });
+        const float g = c.row_val(p.rsv);
+        c.store(p.out, p.acc, nullptr, 0.0f, nullptr, 0.0f,
+                [=](float z, float, float, float) { return g * (expf(z - m) / s); });
+    }
+};
+
+// Row log-sum-exp forward-mode product (in0 = z, in1 = tz, out_row = ty):
+//   ty = sum(exp(z - m) * tz) / sum(exp(z - m))
+struct LseJvp {
+    static constexpr int kIn = 2;
+    template <class C>
+    __device__ static void run(C& c, const RowArgs& p) {
+        const float m = c.max([](float z, float) { return z; });
+        float s = 0.0f, d = 0.0f;
+        c.sum2(
+            [=](float z, float t, float (&o)[2]) {
+                const float e = expf(z - m);
+                o[0] = e;
+                o[1] = e * t;
+            },
+            s, d);
+        c.put_val(p.out_row, d / s);
+    }
+};
+
+// ---- kernels and launch ------------------------------------------------------------
+
+template <class S, int TPR, int NV, int G, class Op>
+__global__ __launch_bounds__(TPR * G) void row_resident(const RowArgs p, int64_t rows, int cols) {
+    using Ctx = Resident<S, TPR, NV, G, Op::kIn>;
+    __shared__ float red[2][Ctx::kSlots];
+    Ctx c(p, rows, cols, red);
+    Op::run(c, p);
+}
+
+template <class S, class Op>
+__global__ __launch_bounds__(kBlock) void row_looped(const RowArgs p, int64_t rows, int cols) {
+    using Ctx = Looped<S, Op::kIn>;
+    __shared__ float red[2][Ctx::kSlots];
+    const int64_t row = blockIdx.x;
+    if (row >= rows) return;  // workgroup-uniform
+    Ctx c(p, row, cols, red);
+    Op::run(c, p);
+}
+
+inline bool aligned_or_null(const void* p) { return p == nullptr || aligned16(p); }
+
+template <class Op, class S>
+int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
+    const bool vec = (cols % S::kVec) == 0 && aligned16(p.in0) && aligned_or_null(p.in1) &&
+                     aligned_or_null(p.out) && aligned_or_null(p.col0) &&
+                     aligned_or_null(p.col1);
+    Plan pl;
+    if (vec) pl = fwd_plan(cols / S::kVec, rows);
+    if (pl.tpr == 0) {
+        if (rows > 0x7fffffffLL) return AGK_EINVAL;
+        hipLaunchKernelGGL((row_looped<S, Op>), dim3(static_cast<unsigned>(rows)), dim3(kBlock),
+                           0, st, p, rows, cols);
+        return check_launch();
+    }
+    const int64_t grid = (rows + pl.g - 1) / pl.g;
+    if (grid > 0x7fffffffLL) return AGK_EINVAL;
+#define AGK_X(a, b, c)                                                                          \
+    if (pl.tpr == a && pl.nv == b && pl.g == c) {                                               \
+        hipLaunchKernelGGL((row_resident<S, a, b, c, Op>), dim3(static_cast<unsigned>(grid)),    \
+                           dim3(a * c), 0, st, p, rows, cols);                                  \
+        return check_launch();                                                                  \
+    }
+    AGK_FWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
+template <class Op>
+int run(const RowArgs& p, int64_t rows, int64_t cols, int dtype, agk_stream_t stream) {
+    clear_pending_error();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int c = static_cast<int>(cols);
+    return dtype == AGK_F32 ? launch<Op, F32>(p, rows, c, st) : launch<Op, BF16>(p, rows, c, st);
+}
+
+// Checks shared by every entry point; sets *done when there is nothing to do.
+inline int precheck(int64_t rows, int64_t cols, int dtype, bool* done) {
+    *done = false;
+    if (int rc = check_sizes(rows, cols)) return rc;
+    if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    if (rows == 0 || cols == 0) *done = true;
+    return AGK_OK;
+}
+
+inline bool valid_accumulate(int accumulate) { return (accumulate & ~AGK_ACCUM_DX) == 0; }
+
+}  // namespace rowops
+}  // namespace agk
+
+// ---- C ABI ------------------------------------------------------------------------
+
+extern "C" {
+
+int agk_rmsnorm_jvp(const void* x, const void* gamma, const float* inv_rms, const void* tx,
+                    const void* tgamma, void* ty, int64_t rows, int64_t cols, int dtype,
+                    agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (tgamma && !gamma) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!x || !inv_rms || !tx || !ty) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = x;
+    p.in1 = tx;
+    p.col0 = gamma;
+    p.col1 = tgamma;
+    p.rs0 = inv_rms;
+    p.out = ty;
+    return run<RmsJvp>(p, rows, cols, dtype, stream);
+}
+
+int agk_layernorm_fwd(const void* x, void* y, float* mean, float* rstd, int64_t rows,
+                      int64_t cols, float eps, int dtype, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (done) return AGK_OK;
+    if (!x || !y || !mean || !rstd) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = x;
+    p.out = y;
+    p.ws0 = mean;
+    p.ws1 = rstd;
+    p.eps = eps;
+    return run<LnFwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_layernorm_bwd(const void* x, const float* mean, const float* rstd, const void* dy,
+                      void* dx, int64_t rows, int64_t cols, int dtype, int accumulate,
+                      agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (!valid_accumulate(accumulate)) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!x || !mean || !rstd || !dy || !dx) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = x;
+    p.in1 = dy;
+    p.rs0 = mean;
+    p.rs1 = rstd;
+    p.out = dx;
+    p.acc = accumulate & AGK_ACCUM_DX;
+    return run<LnBwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_softmax_fwd(const void* z, void* y, int64_t rows, int64_t cols, int dtype,
+                    agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (done) return AGK_OK;
+    if (!z || !y) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.out = y;
+    return run<SmFwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_softmax_bwd(const void* y, const void* dy, void* dz, int64_t rows, int64_t cols,
+                    int dtype, int accumulate, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (!valid_accumulate(accumulate)) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!y || !dy || !dz) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = y;
+    p.in1 = dy;
+    p.out = dz;
+    p.acc = accumulate & AGK_ACCUM_DX;
+    return run<SmBwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_logsumexp_fwd(const void* z, void* y, int64_t rows, int64_t cols, int dtype,
+                      agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (rows > 0 && cols == 0) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!z || !y) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.out_row = y;
+    return run<LseFwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_logsumexp_bwd(const void* z, const void* dy, void* dz, int64_t rows, int64_t cols,
+                      int dtype, int accumulate, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (!valid_accumulate(accumulate)) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!z || !dy || !dz) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.rsv = dy;
+    p.out = dz;
+    p.acc = accumulate & AGK_ACCUM_DX;
+    return run<LseBwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows, int64_t cols,
+                      int dtype, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (rows > 0 && cols == 0) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!z || !tz || !ty) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.in1 = tz;
+    p.out_row = ty;
+    return run<LseJvp>(p, rows, cols, dtype, stream);
+}
+
+}  // extern "C"

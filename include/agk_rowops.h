@@ -1,0 +1,107 @@
+/*
+ * agk_rowops.h -- C ABI of the row kernels that share the RMSNorm layer's
+ * row-reduce skeleton: the forward-mode product (JVP) of RMSNorm, LayerNorm,
+ * row softmax and row log-sum-exp, with their vector-Jacobian products.
+ *
+ * Implemented by the same library as agk_rmsnorm.h (libagk_rmsnorm.so), with
+ * the same conventions: device pointers; row-major contiguous [rows, cols]
+ * with the reduced axis last; `dtype` is the storage type (AGK_F32 or
+ * AGK_BF16) of every [rows, cols] tensor and of the per-row values that have
+ * the storage type (noted below), arithmetic is fp32; per-row statistics are
+ * fp32; work is enqueued on `stream` without synchronising; no global state;
+ * deterministic results; an agk_status is returned.
+ *
+ * `accumulate` (backward entry points): AGK_ACCUM_NONE overwrites the output,
+ * AGK_ACCUM_DX adds into it (Node::accumulate_grad, grad += g,
+ * cgadimpl/src/core/graph.cpp:44-47); other bits are AGK_EINVAL.
+ *
+ * rows == 0 or cols == 0 is a no-op returning AGK_OK, except for
+ * agk_logsumexp_fwd / agk_logsumexp_jvp with rows > 0 and cols == 0, which
+ * return AGK_EINVAL (the log-sum-exp of an empty row is not defined there).
+ *
+ * Any alignment and any cols are accepted: 16-byte aligned tensors with cols
+ * a multiple of the vector width (4 fp32 / 8 bf16) take the register-resident
+ * kernels (one HBM read per input element, one write per output element);
+ * anything else takes a looped kernel that re-reads the row from cache.
+ */
+#ifndef AGK_ROWOPS_H
+#define AGK_ROWOPS_H
+
+#include "agk_rmsnorm.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Forward-mode derivative of the RMSNorm layer y = x * r * gamma with
+ * r = 1/sqrt(mean(x^2) + eps) (r is the inv_rms saved by agk_rmsnorm_fwd):
+ *     ty = gamma * r * (tx - x * r^2 * sum(tx * x) / cols) + tgamma * x * r
+ * i.e. t*r - y*r*sum(t*y)/cols for the unscaled node, plus the gamma terms.
+ * Replaces jvp_RMSNorm, cgadimpl/src/autodiff/autodiff_jvp_ops.cpp:366-379,
+ * with that rule corrected: the reference divides by tape[0], which holds
+ * 1/rms (normalization.cpp:26-29), so it returns t/r - ... instead of t*r - ...
+ * gamma == NULL: no scale (ag::rms); tgamma == NULL: gamma has no tangent.
+ * tgamma without gamma is AGK_EINVAL.  ty may not alias x or tx.             */
+int agk_rmsnorm_jvp(const void* x, const void* gamma, const float* inv_rms,
+                    const void* tx, const void* tgamma, void* ty,
+                    int64_t rows, int64_t cols, int dtype, agk_stream_t stream);
+
+/* LayerNorm without affine parameters, y = (x - mean) / sqrt(var + eps),
+ * mean and (biased) var over the last axis.  Replaces laynor_nodeops,
+ * cgadimpl/src/ops/normalization.cpp:10-22 (which fixes eps = 1e-5).
+ * Saves mean[rows] and rstd[rows] = 1/sqrt(var + eps) in fp32 for the
+ * backward (the reference's tape holds var and mean, :15-16).  The variance
+ * is computed from the register-held row as mean((x - mean)^2), like the
+ * reference's x_minus_mean pass, not as E[x^2] - mean^2.                     */
+int agk_layernorm_fwd(const void* x, void* y, float* mean, float* rstd,
+                      int64_t rows, int64_t cols, float eps, int dtype,
+                      agk_stream_t stream);
+
+/* VJP of LayerNorm, replacing vjp_LayerNorm,
+ * cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:351-365:
+ *     xhat = (x - mean) * rstd
+ *     dx (+)= rstd * (dy - sum(dy)/cols - xhat * sum(dy * xhat)/cols)
+ * which is the reference's d_xhat + d_var*(x-mean)*2/D + d_mean/D with its
+ * sum(x - mean) term (zero up to rounding) dropped.  The Jacobian is
+ * symmetric, so the same call with dy = a tangent gives the JVP.             */
+int agk_layernorm_bwd(const void* x, const float* mean, const float* rstd,
+                      const void* dy, void* dx, int64_t rows, int64_t cols,
+                      int dtype, int accumulate, agk_stream_t stream);
+
+/* Row softmax, y = exp(z - max(z)) / sum(exp(z - max(z))) over the last
+ * axis.  Replaces softmax_row_nodeops, cgadimpl/src/ops/reduction.cpp:42-53. */
+int agk_softmax_fwd(const void* z, void* y, int64_t rows, int64_t cols,
+                    int dtype, agk_stream_t stream);
+
+/* VJP of the row softmax from its output, dz (+)= y * (dy - sum(y * dy)),
+ * replacing vjp_SoftmaxRow, autodiff_vjp_ops.cpp:421-428.  The Jacobian is
+ * symmetric: with dy = a tangent of z this is jvp_SoftmaxRow
+ * (autodiff_jvp_ops.cpp:411-420).                                            */
+int agk_softmax_bwd(const void* y, const void* dy, void* dz, int64_t rows,
+                    int64_t cols, int dtype, int accumulate, agk_stream_t stream);
+
+/* Row log-sum-exp, y[row] = log(sum(exp(z - m))) + m with m = max(z) over
+ * the last axis.  y has `rows` elements of the storage type (the reference's
+ * [.., 1] output).  Replaces logsumexp_row_nodeops, reduction.cpp:54-66.     */
+int agk_logsumexp_fwd(const void* z, void* y, int64_t rows, int64_t cols,
+                      int dtype, agk_stream_t stream);
+
+/* VJP of the row log-sum-exp: dz (+)= dy[row] * softmax(z), softmax
+ * recomputed from z (max, then sum of exponentials) as the reference does,
+ * vjp_LogSumExpRow, autodiff_vjp_ops.cpp:430-440.  dy has `rows` elements of
+ * the storage type.                                                          */
+int agk_logsumexp_bwd(const void* z, const void* dy, void* dz, int64_t rows,
+                      int64_t cols, int dtype, int accumulate,
+                      agk_stream_t stream);
+
+/* JVP of the row log-sum-exp: ty[row] = sum(softmax(z) * tz) over the row,
+ * jvp_LogSumExpRow, autodiff_jvp_ops.cpp:421-434.  ty has `rows` elements of
+ * the storage type.                                                          */
+int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows,
+                      int64_t cols, int dtype, agk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AGK_ROWOPS_H */

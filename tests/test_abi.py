@@ -1,7 +1,7 @@
 """C ABI of libagk_rmsnorm.so, checked without a GPU.
 
-Loads the library, checks it exports every function include/agk_rmsnorm.h
-declares (and that the ctypes binding covers exactly those), and exercises
+Loads the library, checks it exports every function include/*.h declares
+(and that the ctypes binding covers exactly those), and exercises
 the argument validation that runs before any HIP call: null pointers,
 negative or overflowing sizes, unknown dtypes, missing or short workspaces.
 """
@@ -15,19 +15,26 @@ import pytest
 import cgadimpl_amd as agk
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "agk_rmsnorm.h")
+INCLUDE = os.path.join(ROOT, "include")
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(agk_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in sorted(os.listdir(INCLUDE)):
+        if not h.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(agk_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_expected_entry_points():
     fns = declared_functions()
     for want in ("agk_rmsnorm_fwd", "agk_rmsnorm_bwd", "agk_rmsnorm_bwd_workspace_bytes",
-                 "agk_status_str"):
+                 "agk_status_str", "agk_rmsnorm_jvp", "agk_layernorm_fwd", "agk_layernorm_bwd",
+                 "agk_softmax_fwd", "agk_softmax_bwd", "agk_logsumexp_fwd", "agk_logsumexp_bwd",
+                 "agk_logsumexp_jvp", "agk_gemm_bf16"):
         assert want in fns
 
 
@@ -160,6 +167,48 @@ def test_mul_argument_validation():
     assert m(FAKE, FAKE, FAKE, None, FAKE, None, 0, 4, 4, 0, 0, None) == 3        # db needs ws
     assert m(FAKE, FAKE, FAKE, None, None, None, 0, 4, 4, 0, 0, None) == 0        # nothing asked
     assert m(FAKE, FAKE, FAKE, FAKE, None, None, 0, 4, 4, 0, 8, None) == 1        # bad accumulate
+
+
+def test_rowops_argument_validation():
+    lib = agk.lib()
+    j = lib.agk_rmsnorm_jvp
+    assert j(None, None, FAKE, FAKE, None, FAKE, 4, 8, 0, None) == 1           # x
+    assert j(FAKE, None, None, FAKE, None, FAKE, 4, 8, 0, None) == 1           # inv_rms
+    assert j(FAKE, None, FAKE, None, None, FAKE, 4, 8, 0, None) == 1           # tx
+    assert j(FAKE, None, FAKE, FAKE, None, None, 4, 8, 0, None) == 1           # ty
+    assert j(FAKE, None, FAKE, FAKE, FAKE, FAKE, 4, 8, 0, None) == 1           # tgamma w/o gamma
+    assert j(FAKE, FAKE, FAKE, FAKE, None, FAKE, 4, 8, 9, None) == 2           # dtype
+    assert j(None, None, None, None, None, None, 0, 8, 0, None) == 0           # empty
+    assert j(FAKE, FAKE, FAKE, FAKE, None, FAKE, -4, 8, 0, None) == 1          # size
+
+    lf = lib.agk_layernorm_fwd
+    assert lf(None, FAKE, FAKE, FAKE, 4, 8, 1e-5, 0, None) == 1
+    assert lf(FAKE, FAKE, None, FAKE, 4, 8, 1e-5, 0, None) == 1
+    assert lf(FAKE, FAKE, FAKE, None, 4, 8, 1e-5, 0, None) == 1
+    assert lf(FAKE, FAKE, FAKE, FAKE, 4, 8, 1e-5, 2, None) == 2
+    assert lf(None, None, None, None, 4, 0, 1e-5, 0, None) == 0
+    lb = lib.agk_layernorm_bwd
+    assert lb(FAKE, FAKE, FAKE, FAKE, None, 4, 8, 0, 0, None) == 1             # dx
+    assert lb(FAKE, None, FAKE, FAKE, FAKE, 4, 8, 0, 0, None) == 1             # mean
+    assert lb(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 0, 2, None) == 1             # no dgamma here
+    assert lb(None, None, None, None, None, 0, 8, 0, 1, None) == 0
+
+    assert lib.agk_softmax_fwd(None, FAKE, 4, 8, 0, None) == 1
+    assert lib.agk_softmax_fwd(FAKE, FAKE, 4, 8, 3, None) == 2
+    assert lib.agk_softmax_fwd(None, None, 0, 8, 0, None) == 0
+    sb = lib.agk_softmax_bwd
+    assert sb(FAKE, None, FAKE, 4, 8, 0, 0, None) == 1
+    assert sb(FAKE, FAKE, FAKE, 4, 8, 0, 3, None) == 1
+    assert sb(None, None, None, 4, 0, 0, 1, None) == 0
+
+    assert lib.agk_logsumexp_fwd(FAKE, FAKE, 4, 0, 0, None) == 1   # log-sum-exp of empty rows
+    assert lib.agk_logsumexp_fwd(None, None, 0, 0, 0, None) == 0
+    assert lib.agk_logsumexp_fwd(FAKE, None, 4, 8, 0, None) == 1
+    assert lib.agk_logsumexp_bwd(FAKE, None, FAKE, 4, 8, 0, 0, None) == 1
+    assert lib.agk_logsumexp_bwd(FAKE, FAKE, FAKE, 4, 8, 0, -1, None) == 1
+    assert lib.agk_logsumexp_jvp(FAKE, FAKE, FAKE, 4, 0, 0, None) == 1
+    assert lib.agk_logsumexp_jvp(FAKE, None, FAKE, 4, 8, 0, None) == 1
+    assert lib.agk_logsumexp_jvp(FAKE, FAKE, FAKE, 4, 8, 1 << 20, None) == 2
 
 
 def test_python_binding_raises_without_gpu_tensors():

@@ -1,0 +1,367 @@
+"""Parity of the row ops of include/agk_rowops.h with the pinned oracle (oracle/rowops.py).
+
+Every op runs on the GPU through the C ABI on a full tensor; rows are
+independent, so the oracle checks all rows of small cases and a fixed sample
+of rows (first, last, random) of large ones.  Bars (tests/tolerances.py):
+fp32 storage 1e-5, bf16 storage 1e-2, per row, relative to the row's scale:
+  - outputs that are plain values (y of LayerNorm / softmax, log-sum-exp,
+    the log-sum-exp VJP): max|d| / max|ref| per row;
+  - outputs that are a difference of terms (LayerNorm dx, softmax dz, the
+    RMSNorm and log-sum-exp JVPs): max|d| over the sum of the terms' per-row
+    magnitudes, the only bound fp32 can meet where the terms cancel;
+  - per-row statistics (mean, rstd): 1e-5 (fp32 arithmetic either way).
+Also covered: every resident launch shape (at its narrowest and widest
+width, below and above the large-batch threshold), widths that take the
+looped kernel, misaligned pointers, masked (-inf) entries, accumulation,
+run-to-run determinism and full-size configurations through properties.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import cgadimpl_amd as agk
+from gpu_util import as_f32, device_inputs, to_host
+from oracle import rowops as ro
+from tolerances import TOL_BF16, TOL_F32
+
+pytestmark = pytest.mark.gpu
+
+OPS = ("rmsnorm_jvp", "layernorm", "softmax", "logsumexp")
+SHAPES = [(5, 1), (3, 3), (17, 13), (9, 100), (33, 127), (65, 129), (8, 1000), (37, 4096),
+          (4, 4099), (2, 40000), (300, 64), (1000, 128), (512, 512), (64, 5120), (3, 65536)]
+EPS = 1e-5
+
+
+def _tol(bf16):
+    return TOL_BF16 if bf16 else TOL_F32
+
+
+def _sample_rows(R, seed, n=254):
+    if R <= n + 2:
+        return np.arange(R)
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, R - 1], rng.integers(0, R, n)]))
+
+
+def _host_rows(t, rows):
+    import torch
+    if t is None:
+        return None
+    if t.dim() == 1:  # column vector: not per row
+        return to_host(t)
+    idx = torch.from_numpy(rows).to(t.device)
+    return to_host(t[idx].contiguous())
+
+
+def _f64(a):
+    return as_f32(a).astype(np.float64)
+
+
+def _rowmax(a):
+    return np.max(np.abs(a), axis=-1)
+
+
+def _scaled_err(got, ref, scale):
+    d = _rowmax(_f64(got) - _f64(ref))
+    if not np.all(np.isfinite(as_f32(got))):
+        return float("inf")
+    return float(np.max(np.where(scale > 0, d / np.where(scale > 0, scale, 1.0), d)))
+
+
+def _row_rel(got, ref):
+    return _scaled_err(got, ref, _rowmax(_f64(ref)))
+
+
+# ---- per-op runners: GPU on full tensors, oracle on sampled rows ----------------------
+
+def check_rmsnorm_jvp(x, g, t, label):
+    """ty for the scaled layer (with and without a gamma tangent) and the bare node."""
+    import torch
+    bf16 = x.dtype == torch.bfloat16
+    tg = torch.flip(g, [0]).contiguous() - 1.0
+    _, inv = agk.rmsnorm_fwd(x, g, EPS)
+    ty = agk.rmsnorm_jvp(x, g, inv, t, tg)
+    ty_nog = agk.rmsnorm_jvp(x, g, inv, t, None)
+    _, inv0 = agk.rmsnorm_fwd(x, None, EPS)
+    ty0 = agk.rmsnorm_jvp(x, None, inv0, t, None)
+    torch.cuda.synchronize()
+    rows = _sample_rows(x.shape[0], x.shape[1])
+    xs, ts = _host_rows(x, rows), _host_rows(t, rows)
+    gs, tgs = to_host(g), to_host(tg)
+    xf, tf, gf, tgf = _f64(xs), _f64(ts), _f64(gs), _f64(tgs)
+    D = xf.shape[-1]
+    r = 1.0 / np.sqrt(np.mean(xf * xf, -1) + EPS)
+    dot = np.sum(tf * xf, -1)
+    t1 = r * _rowmax(gf * tf)
+    t2 = r ** 3 * _rowmax(gf * xf) * np.abs(dot) / D
+    t3 = r * _rowmax(tgf * xf)
+    if bf16:
+        ref = ro.rmsnorm_jvp_bf16(xs, gs, ts, tgs, EPS)
+        ref_nog = ro.rmsnorm_jvp_bf16(xs, gs, ts, None, EPS)
+        ref0 = ro.rmsnorm_jvp_bf16(xs, None, ts, None, EPS)
+    else:
+        ref = ro.rmsnorm_jvp(xs, gs, ts, tgs, EPS)
+        ref_nog = ro.rmsnorm_jvp(xs, gs, ts, None, EPS)
+        ref0 = ro.rmsnorm_jvp(xs, None, ts, None, EPS)
+    e = {
+        "ty": _scaled_err(_host_rows(ty, rows), ref, t1 + t2 + t3),
+        "ty_no_tgamma": _scaled_err(_host_rows(ty_nog, rows), ref_nog, t1 + t2),
+        "ty_node": _scaled_err(_host_rows(ty0, rows), ref0,
+                               r * _rowmax(tf) + r ** 3 * _rowmax(xf) * np.abs(dot) / D),
+    }
+    return e
+
+
+def check_layernorm(x, dy, label, eps=EPS):
+    import torch
+    bf16 = x.dtype == torch.bfloat16
+    y, mean, rstd = agk.layernorm_fwd(x, eps)
+    dx = agk.layernorm_bwd(x, mean, rstd, dy)
+    torch.cuda.synchronize()
+    rows = _sample_rows(x.shape[0], x.shape[1] + 1)
+    xs, dys = _host_rows(x, rows), _host_rows(dy, rows)
+    if bf16:
+        ry, rmean, rvar = ro.layernorm_fwd_bf16(xs, eps)
+        rdx = ro.layernorm_bwd_bf16(xs, rmean, rvar, dys, eps)
+    else:
+        ry, rmean, rvar = ro.layernorm_fwd(xs, eps)
+        rdx = ro.layernorm_bwd(xs, rmean, rvar, dys, eps)
+    xf, gf = _f64(xs), _f64(dys)
+    rm, rv = rmean.astype(np.float64)[:, 0], rvar.astype(np.float64)[:, 0]
+    rs = 1.0 / np.sqrt(rv + eps)
+    xhat = (xf - rm[:, None]) * rs[:, None]
+    scale = rs * (_rowmax(gf) + np.abs(gf.mean(-1)) + _rowmax(xhat) * np.abs((gf * xhat).mean(-1)))
+    gm = _host_rows(mean, rows).reshape(-1).astype(np.float64)
+    gr = _host_rows(rstd, rows).reshape(-1).astype(np.float64)
+    e = {
+        "y": _row_rel(_host_rows(y, rows), ry),
+        "mean": float(np.max(np.abs(gm - rm) / np.maximum(_rowmax(xf), 1e-30))),
+        "rstd": float(np.max(np.abs(gr - rs) / rs)),
+        "dx": _scaled_err(_host_rows(dx, rows), rdx, scale),
+    }
+    return e
+
+
+def check_softmax(z, dy, label):
+    import torch
+    bf16 = z.dtype == torch.bfloat16
+    y = agk.softmax_fwd(z)
+    dz = agk.softmax_bwd(y, dy)
+    torch.cuda.synchronize()
+    rows = _sample_rows(z.shape[0], z.shape[1] + 2)
+    zs, dys, ys = _host_rows(z, rows), _host_rows(dy, rows), _host_rows(y, rows)
+    if bf16:
+        ry = ro.softmax_fwd_bf16(zs)
+        rdz = ro.softmax_bwd_bf16(ys, dys)   # the backward from the GPU's own y
+    else:
+        ry = ro.softmax_fwd(zs)
+        rdz = ro.softmax_bwd(ys, dys)
+    yf, gf = _f64(ys), _f64(dys)
+    scale = _rowmax(yf) * (_rowmax(gf) + np.abs(np.sum(yf * gf, -1)))
+    return {"y": _row_rel(ys, ry), "dz": _scaled_err(_host_rows(dz, rows), rdz, scale)}
+
+
+def check_logsumexp(z, t, label):
+    import torch
+    bf16 = z.dtype == torch.bfloat16
+    R = z.shape[0]
+    dy = t[:, :1].contiguous() if t.shape[1] else torch.ones(R, 1, dtype=z.dtype,
+                                                             device=z.device)
+    y = agk.logsumexp_fwd(z)
+    dz = agk.logsumexp_bwd(z, dy)
+    ty = agk.logsumexp_jvp(z, t)
+    torch.cuda.synchronize()
+    rows = _sample_rows(R, z.shape[1] + 3)
+    zs, ts, dys = _host_rows(z, rows), _host_rows(t, rows), _host_rows(dy, rows)
+    if bf16:
+        ry, rdz, rty = (ro.logsumexp_fwd_bf16(zs), ro.logsumexp_bwd_bf16(zs, dys),
+                        ro.logsumexp_jvp_bf16(zs, ts))
+    else:
+        ry, rdz, rty = ro.logsumexp_fwd(zs), ro.logsumexp_bwd(zs, dys), ro.logsumexp_jvp(zs, ts)
+    zf = _f64(zs)
+    sm = np.exp(zf - zf.max(-1, keepdims=True))
+    sm /= sm.sum(-1, keepdims=True)
+    jscale = np.sum(np.abs(sm * _f64(ts)), -1)
+    return {
+        "y": _scaled_err(_host_rows(y, rows), ry, np.maximum(np.abs(_f64(ry))[:, 0], 1.0)),
+        "dz": _row_rel(_host_rows(dz, rows), rdz),
+        "ty": _scaled_err(_host_rows(ty, rows), rty, jscale),
+    }
+
+
+def run_op(op, x, g, dy, label):
+    if op == "rmsnorm_jvp":
+        return check_rmsnorm_jvp(x, g, dy, label)
+    if op == "layernorm":
+        return check_layernorm(x, dy, label)
+    if op == "softmax":
+        return check_softmax(x * 4.0, dy, label)
+    return check_logsumexp(x * 4.0, dy, label)
+
+
+def assert_ok(e, tol, label):
+    print(f"[{label}] " + " ".join(f"{k}={v:.2e}" for k, v in e.items()), flush=True)
+    for k, v in e.items():
+        lim = TOL_F32 if k in ("mean", "rstd") else tol
+        assert v <= lim, (label, k, v, lim)
+
+
+# ---- cases ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,cols", SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("op", OPS)
+def test_op_matches_oracle(cuda, op, rows, cols, dtype):
+    dt = agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16
+    p = agk.launch_plan(rows, cols, dt, False)
+    label = f"{op} {dtype} {rows}x{cols} plan{(p['tpr'], p['nv'], p['g'])}"
+    print(label, flush=True)
+    x, g, dy = device_inputs((rows, cols), dtype, rows * 1009 + cols, cuda)
+    assert_ok(run_op(op, x, g, dy, label), _tol(dtype == "bf16"), label)
+
+
+def _plan_cases():
+    from plans import reachable_plans
+    seen, cases = set(), []
+    for (dt, direction, _tpr, _nv, _g), reps in sorted(reachable_plans().items()):
+        if direction != "fwd":
+            continue
+        for rows, cols in reps:
+            key = ("f32" if dt == agk.AGK_F32 else "bf16", rows, cols)
+            if key not in seen:
+                seen.add(key)
+                cases.append(key)
+    return cases
+
+
+@pytest.mark.parametrize("dtype,rows,cols", _plan_cases(), ids=lambda v: str(v))
+def test_every_launch_shape(cuda, dtype, rows, cols):
+    """All four ops at every resident shape the row plan can pick."""
+    dt = agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16
+    p = agk.launch_plan(rows, cols, dt, False)
+    x, g, dy = device_inputs((rows, cols), dtype, rows * 31 + cols, cuda)
+    for op in OPS:
+        label = f"{op} {dtype} {rows}x{cols} plan{(p['tpr'], p['nv'], p['g'])}"
+        print(label, flush=True)
+        assert_ok(run_op(op, x, g, dy, label), _tol(dtype == "bf16"), label)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("op", OPS)
+def test_misaligned_pointers_take_the_looped_kernel(cuda, op, dtype):
+    import torch
+    rows, cols = 24, 256
+    x, g, dy = device_inputs((rows, cols), dtype, 77, cuda)
+
+    def shifted(t):  # same values, 1 element past a 16-byte boundary
+        buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+        v = buf[1:1 + t.numel()].view(t.shape)
+        v.copy_(t)
+        return v
+
+    label = f"{op} {dtype} misaligned"
+    print(label, flush=True)
+    e_al = run_op(op, x, g, dy, label + " (aligned)")
+    e_mis = run_op(op, shifted(x), shifted(g), shifted(dy), label)
+    assert_ok(e_mis, _tol(dtype == "bf16"), label)
+    assert_ok(e_al, _tol(dtype == "bf16"), label + " (aligned)")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_backward_accumulates(cuda, dtype):
+    import torch
+    x, g, dy = device_inputs((40, 384), dtype, 5, cuda)
+    pre = torch.randn(x.shape, device=cuda).to(x.dtype)
+    y, mean, rstd = agk.layernorm_fwd(x)
+    outs = {
+        "layernorm": (agk.layernorm_bwd(x, mean, rstd, dy),
+                      agk.layernorm_bwd(x, mean, rstd, dy, dx=pre.clone(), accumulate=True)),
+    }
+    s = agk.softmax_fwd(x)
+    outs["softmax"] = (agk.softmax_bwd(s, dy),
+                       agk.softmax_bwd(s, dy, dz=pre.clone(), accumulate=True))
+    dr = dy[:, :1].contiguous()
+    outs["logsumexp"] = (agk.logsumexp_bwd(x, dr),
+                         agk.logsumexp_bwd(x, dr, dz=pre.clone(), accumulate=True))
+    torch.cuda.synchronize()
+    tol = 2 * _tol(dtype == "bf16")
+    for name, (fresh, acc) in outs.items():
+        want = pre.double() + fresh.double()
+        err = float(((acc.double() - want).abs().max() / want.abs().max()).item())
+        print(f"[accumulate {name} {dtype}] {err:.2e}", flush=True)
+        assert err <= tol, (name, err)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_masked_entries(cuda, dtype):
+    """-inf entries (masked logits) get probability 0 and drop out of the log-sum-exp."""
+    import torch
+    z = torch.randn(16, 96, device=cuda) * 3
+    z[:, ::3] = float("-inf")
+    z = z.to(torch.bfloat16 if dtype == "bf16" else torch.float32).contiguous()
+    y = agk.softmax_fwd(z)
+    lse = agk.logsumexp_fwd(z)
+    torch.cuda.synchronize()
+    assert torch.all(y[:, ::3] == 0)
+    keep = z.float()[:, [j for j in range(96) if j % 3]]
+    want = torch.logsumexp(keep.double(), -1, keepdim=True)
+    assert float((lse.double() - want).abs().max()) <= _tol(dtype == "bf16") * float(
+        want.abs().max())
+    assert float((y.double().sum(-1) - 1).abs().max()) <= 2 * _tol(dtype == "bf16")
+
+
+def test_results_are_deterministic(cuda):
+    import torch
+    x, g, dy = device_inputs((4099, 1000), "f32", 3, cuda)
+    first = None
+    for _ in range(3):
+        y, mean, rstd = agk.layernorm_fwd(x)
+        outs = [y, mean, rstd, agk.layernorm_bwd(x, mean, rstd, dy), agk.softmax_fwd(x),
+                agk.logsumexp_fwd(x), agk.logsumexp_jvp(x, dy)]
+        torch.cuda.synchronize()
+        if first is None:
+            first = [o.clone() for o in outs]
+        else:
+            for a, b in zip(first, outs):
+                assert torch.equal(a, b)
+
+
+# ---- full-size configurations -------------------------------------------------------
+
+@pytest.mark.slow
+@pytest.mark.parametrize("name", ["c2", "c3"])
+def test_full_size(cuda, name):
+    """[32,2048,4096] fp32 and [16,4096,8192] bf16: sampled rows against the
+    oracle, plus properties over every row in fp64 on the device."""
+    import torch
+    from cgadimpl_amd import configs
+    cfg = configs.CONFIGS[name]
+    R, D = cfg.rows, cfg.cols
+    bf16 = cfg.dtype == "bf16"
+    x, g, dy = device_inputs((R, D), cfg.dtype, cfg.seed, cuda)
+    tol = _tol(bf16)
+    for op in OPS:
+        label = f"{op} full-size {name}"
+        print(label, flush=True)
+        assert_ok(run_op(op, x, g, dy, label), tol, label)
+    # softmax rows sum to 1, LayerNorm rows have mean 0 and variance var/(var+eps)
+    y = agk.softmax_fwd(x)
+    s = y.double().sum(-1)
+    assert float((s - 1).abs().max()) <= (2.0 ** -7 if bf16 else 1e-5)
+    ln, mean, rstd = agk.layernorm_fwd(x)
+    lnd = ln.double()
+    assert float(lnd.mean(-1).abs().max()) <= (1e-2 if bf16 else 1e-5)
+    del y, s, ln, lnd
+    # adjoint identity between the RMSNorm JVP and the (separately pinned) VJP
+    tg = torch.flip(g, [0]).contiguous() - 1.0
+    _, inv = agk.rmsnorm_fwd(x, g, EPS)
+    ty = agk.rmsnorm_jvp(x, g, inv, dy, tg)
+    w = torch.randn(x.shape, device=cuda).to(x.dtype)
+    dx, dgam = agk.rmsnorm_bwd(x, g, inv, w)
+    torch.cuda.synchronize()
+    lhs = float((w.double() * ty.double()).sum())
+    rhs = float((dx.double() * dy.double()).sum() + (dgam.double() * tg.double()).sum())
+    rel = abs(lhs - rhs) / max(abs(rhs), float((w.double() * ty.double()).abs().sum()) * 1e-3)
+    print(f"[{name}] adjoint identity <w, J t> vs <J^T w, t>: {rel:.2e}", flush=True)
+    assert rel <= (5e-2 if bf16 else 1e-4)
