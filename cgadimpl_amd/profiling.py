@@ -48,14 +48,43 @@ def kernel_stats(stats_csv):
     return out
 
 
+def short_name(name):
+    """Library kernels (hipBLASLt's long tuned names) shortened for the tables."""
+    if name.startswith(("Cijk_", "Custom_Cijk_")):
+        return "hipBLASLt " + name.split("_MT")[0] + ("_MT" + name.split("_MT")[1][:12]
+                                                      if "_MT" in name else "")
+    return name
+
+
+def dispatch_stats(trace_csv):
+    """{(kernel, grid, workgroup): [durations ns]} from run_kernel_trace.csv."""
+    out = defaultdict(list)
+    for r in _rows(trace_csv):
+        key = (r["Kernel_Name"], f'{r["Grid_Size_X"]}x{r["Grid_Size_Y"]}',
+               r["Workgroup_Size_X"])
+        out[key].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
+    return out
+
+
 def write_trace_summary(stats_csv, out_md, command):
     st = kernel_stats(stats_csv)
     lines = ["# Kernel durations (rocprofv3 --kernel-trace --stats)", "",
              "Command:", "", "```", command, "```", "",
              "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
     for name, (calls, avg, mn, mx) in sorted(st.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
-        lines.append(f"| {name} | {calls} | {avg / 1e3:.1f} | {mn / 1e3:.1f} | {mx / 1e3:.1f} |")
+        lines.append(f"| {short_name(name)} | {calls} | {avg / 1e3:.1f} | {mn / 1e3:.1f} | "
+                     f"{mx / 1e3:.1f} |")
     lines.append("")
+    trace_csv = os.path.join(os.path.dirname(stats_csv),
+                             os.path.basename(stats_csv).replace("kernel_stats", "kernel_trace"))
+    if os.path.exists(trace_csv):
+        lines += ["Per launch shape (grid threads x, y; workgroup size), from the trace:", "",
+                  "| kernel | grid | workgroup | calls | avg us |", "|---|---|---|---|---|"]
+        ds = dispatch_stats(trace_csv)
+        for (name, grid, wg), v in sorted(ds.items(), key=lambda kv: -sum(kv[1])):
+            lines.append(f"| {short_name(name)} | {grid} | {wg} | {len(v)} | "
+                         f"{sum(v) / len(v) / 1e3:.1f} |")
+        lines.append("")
     for entry, kernels in ENTRY_KERNELS.items():
         tot = sum(st[k][1] for k in kernels if k in st)
         if tot:
