@@ -84,7 +84,7 @@ def host_library(name: str, sources: list[str], compiler: str = "g++") -> str:
 
 
 AG_DIR = os.path.join(PKG, "ag")
-AG_SOURCES = ["tensor.cpp", "graph.cpp", "ops.cpp", "autodiff.cpp", "nn.cpp"]
+AG_SOURCES = ["tensor.cpp", "graph.cpp", "ops.cpp", "autodiff.cpp", "nn.cpp", "runtime.cpp"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 # Host C++ against the HIP runtime API (no device code in these files).
 HOST_HIP_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",

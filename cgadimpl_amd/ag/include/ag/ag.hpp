@@ -6,4 +6,5 @@
 #include "ag/graph.hpp"
 #include "ag/nn.hpp"
 #include "ag/ops.hpp"
+#include "ag/runtime.hpp"
 #include "ag/tensor.hpp"

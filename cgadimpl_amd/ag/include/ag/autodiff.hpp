@@ -12,6 +12,9 @@
 // order on the device.
 #pragma once
 
+#include <functional>
+#include <unordered_map>
+
 #include "ag/graph.hpp"
 
 namespace ag {
@@ -24,8 +27,27 @@ void backward(const Value& root, const Tensor* grad_seed = nullptr, bool enable_
 using VjpFn = void (*)(Node* n, const Tensor& gy);
 VjpFn vjp_lookup(Op op);
 
+// Forward mode (cgadimpl/include/ad/autodiff/autodiff.hpp:15,
+// cgadimpl/src/core/autodiff.cpp:221-250): the tangent of root for the given
+// tangents of some nodes (normally leaves), each of its node's shape and
+// dtype.  Nodes without a seed, whose inputs carry no tangent, have a zero
+// tangent; the result is zeros if nothing reaches the root.  Kernels run on
+// the current stream.  Differs from the reference where it is wrong: a seeded
+// leaf keeps its seed (the reference's jvp_Leaf replaces it with an empty
+// tensor, autodiff_jvp_ops.cpp:189-192), and the RMSNorm rule is the
+// corrected one (autodiff_jvp_ops.cpp:366-379 divides by 1/rms).
+Tensor jvp(const Value& root, const std::unordered_map<Node*, Tensor>& seed);
+
+// JVP of one node: the tangent of n from the tangents of its inputs
+// (tangent_of returns an undefined Tensor for a zero tangent); an undefined
+// result is a zero tangent.
+using JvpFn = Tensor (*)(Node* n, const std::function<const Tensor&(Node*)>& tangent_of);
+JvpFn jvp_lookup(Op op);
+
 namespace detail {
-#define AG_OP(name, arity, str) void vjp_##name(Node* n, const Tensor& gy);
+#define AG_OP(name, arity, str)                          \
+    void vjp_##name(Node* n, const Tensor& gy);           \
+    Tensor jvp_##name(Node* n, const std::function<const Tensor&(Node*)>& tangent_of);
 #include "ag/ops.def"
 #undef AG_OP
 }  // namespace detail

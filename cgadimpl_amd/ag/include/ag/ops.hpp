@@ -1,11 +1,13 @@
-// ops.hpp -- forward operations of the RMSNorm layer path.
+// ops.hpp -- forward operations of the RMSNorm layer path and its neighbours.
 //
 // The reference writes the layer as two graph ops, `ag::rms(x) * gamma`
 // (cgadimpl/include/ad/ops/ops.hpp:81,124; forward in
 // cgadimpl/src/ops/normalization.cpp:23-35 and arithmetic.cpp:31-39).  Both
 // are here with the same names and meaning, running on the HIP kernels behind
 // include/agk_rmsnorm.h, plus the fused layer rms_norm(x, gamma, eps), one node
-// whose forward and backward are one kernel call each.
+// whose forward and backward are one kernel call each.  matmul, laynor,
+// softmax_row and logsumexp_row (ops.hpp:62,78,96-97) run on the GEMM and the
+// row kernels of include/agk_rowops.h.
 #pragma once
 
 #include <memory>
@@ -30,12 +32,32 @@ Value rms_norm(const Value& x, const Value& gamma, float eps = 1e-5f);
 Value mul(const Value& a, const Value& b);
 inline Value operator*(const Value& a, const Value& b) { return mul(a, b); }
 
+// a [..., K] (bf16) times b [K, N] (bf16) -> [..., N] (bf16), on the MFMA GEMM
+// (cgadimpl/src/ops/linalg.cpp:12-20).  a's gradient is bf16, b's is fp32
+// (a weight accumulates in fp32).  fp32 operands throw std::runtime_error.
+Value matmul(const Value& a, const Value& b);
+
+// (x - mean) / sqrt(var + 1e-5) over the last axis (normalization.cpp:10-22;
+// eps fixed as there).  Tape: {mean, rstd}, fp32 [..., 1].
+Value laynor(const Value& x);
+
+// Row softmax over the last axis (cgadimpl/src/ops/reduction.cpp:42-53).
+Value softmax_row(const Value& z);
+
+// Row log-sum-exp over the last axis, [..., D] -> [..., 1] (reduction.cpp:54-66).
+Value logsumexp_row(const Value& z);
+
 namespace detail {
 std::shared_ptr<Node> rms_nodeops(const std::shared_ptr<Node>& x);
 std::shared_ptr<Node> rms_norm_nodeops(const std::shared_ptr<Node>& x,
                                        const std::shared_ptr<Node>& gamma, float eps);
 std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a,
                                   const std::shared_ptr<Node>& b);
+std::shared_ptr<Node> matmul_nodeops(const std::shared_ptr<Node>& a,
+                                     const std::shared_ptr<Node>& b);
+std::shared_ptr<Node> laynor_nodeops(const std::shared_ptr<Node>& x);
+std::shared_ptr<Node> softmax_row_nodeops(const std::shared_ptr<Node>& z);
+std::shared_ptr<Node> logsumexp_row_nodeops(const std::shared_ptr<Node>& z);
 }  // namespace detail
 
 }  // namespace ag

@@ -20,6 +20,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <memory>
+#include <mutex>
 #include <vector>
 
 namespace ag {
@@ -49,7 +50,41 @@ class StreamGuard {
     hipStream_t prev_;
 };
 
-// One device allocation from the stream-ordered pool.
+// Device memory for the allocations made on a stream while it is being
+// captured into a HIP graph (see ag/runtime.hpp).  One hipMalloc'd block,
+// handed out in 256-byte aligned pieces that are never reused: a captured
+// graph replays the same addresses, so every buffer it touches must stay put
+// for as long as the graph or a tensor in the block lives.  Pool memory that
+// is released on the capturing stream during capture is kept here too and
+// freed with the arena, since a stream-ordered free would otherwise become a
+// node of the graph and run again at every replay.
+class CaptureArena {
+  public:
+    explicit CaptureArena(size_t bytes);
+    ~CaptureArena();
+    CaptureArena(const CaptureArena&) = delete;
+    CaptureArena& operator=(const CaptureArena&) = delete;
+    void* take(size_t bytes);          // throws when the block is exhausted
+    void defer_free(void* pool_ptr);   // freed when the arena is destroyed
+    size_t used() const;
+    size_t capacity() const { return capacity_; }
+
+  private:
+    void* base_ = nullptr;
+    size_t capacity_ = 0;
+    size_t used_ = 0;
+    std::vector<void*> deferred_;
+    mutable std::mutex mu_;
+};
+
+// Routes Storage allocations on `stream` to `arena` while it is set (nullptr
+// clears it).  Used by GraphRunner around a capture.
+void set_capture_arena(hipStream_t stream, std::shared_ptr<CaptureArena> arena);
+// The arena set for `stream`, or nullptr.
+std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream);
+
+// One device allocation: from the stream-ordered pool, or from the capture
+// arena of the stream when it is being captured.
 class Storage {
   public:
     Storage(size_t bytes, hipStream_t stream);
@@ -64,6 +99,7 @@ class Storage {
     void* ptr_ = nullptr;
     size_t bytes_ = 0;
     hipStream_t stream_ = nullptr;
+    std::shared_ptr<CaptureArena> arena_;  // set: the memory belongs to the arena
 };
 
 class Tensor {
@@ -71,6 +107,9 @@ class Tensor {
     Tensor() = default;  // undefined: no shape, no storage
 
     // Uninitialised / zero-filled / filled device tensors on the current stream.
+    // zeros() and ones() fill with hipMemset*, so they throw while the current
+    // stream is being captured into a graph (memset nodes are kept out of
+    // captured graphs); empty() works there.
     static Tensor empty(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
     static Tensor zeros(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
     static Tensor ones(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);

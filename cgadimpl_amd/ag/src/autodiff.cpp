@@ -1,4 +1,4 @@
-// autodiff.cpp -- backward(), zero_grad() and the VJP table.
+// autodiff.cpp -- backward(), zero_grad(), jvp() and the VJP / JVP tables.
 //
 // Follows cgadimpl/src/core/autodiff.cpp:27-170: topological order from the
 // root, dependency counters, the root's gradient assigned from the seed
@@ -34,6 +34,48 @@ VjpFn vjp_lookup(Op op) {
         default:
             return nullptr;
     }
+}
+
+JvpFn jvp_lookup(Op op) {
+    switch (op) {
+#define AG_OP(name, arity, str) \
+    case Op::name:              \
+        return &detail::jvp_##name;
+#include "ag/ops.def"
+#undef AG_OP
+        default:
+            return nullptr;
+    }
+}
+
+Tensor jvp(const Value& root, const std::unordered_map<Node*, Tensor>& seed) {
+    if (!root.node) fail("jvp: empty root");
+    const std::vector<Node*> order = topo_from(root.node.get());
+    std::unordered_map<Node*, Tensor> tangent;
+    tangent.reserve(order.size());
+    const Tensor none;
+    auto tangent_of = [&](Node* p) -> const Tensor& {
+        auto it = tangent.find(p);
+        return it == tangent.end() ? none : it->second;
+    };
+    for (Node* n : order) {
+        Tensor t;
+        if (n->op == Op::Leaf) {
+            auto it = seed.find(n);
+            if (it != seed.end()) {
+                const Tensor& s = it->second;
+                if (s.defined() && (s.shape() != n->value.shape() || s.dtype() != n->value.dtype()))
+                    fail("jvp: a seed must have its node's shape and dtype");
+                t = s;
+            }
+        } else if (JvpFn fn = jvp_lookup(n->op)) {
+            t = fn(n, tangent_of);
+        }
+        if (t.defined()) tangent[n] = t;
+    }
+    const Tensor& out = tangent_of(root.node.get());
+    if (out.defined()) return out;
+    return Tensor::zeros(root.node->value.shape(), root.node->value.dtype());
 }
 
 void zero_grad(const Value& root) {

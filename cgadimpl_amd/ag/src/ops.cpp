@@ -1,11 +1,23 @@
-// ops.cpp -- forward ops and VJP rules of the RMSNorm layer path, on the HIP
-// kernels behind include/agk_rmsnorm.h.
+// ops.cpp -- forward ops, VJP and JVP rules of the RMSNorm layer path and its
+// neighbours, on the HIP kernels behind include/agk_rmsnorm.h and
+// include/agk_rowops.h.
 //
 // Reference behaviour (paths relative to the reference tree):
 //   rms_nodeops      cgadimpl/src/ops/normalization.cpp:23-35
 //   mul_nodeops      cgadimpl/src/ops/arithmetic.cpp:31-39
+//   matmul_nodeops   cgadimpl/src/ops/linalg.cpp:12-20
+//   laynor_nodeops   normalization.cpp:10-22
+//   softmax_row_nodeops, logsumexp_row_nodeops  cgadimpl/src/ops/reduction.cpp:42-66
 //   vjp_RMSNorm      cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:368-377
 //   vjp_Mul          autodiff_vjp_ops.cpp:54-59, with reduce_for_broadcast :15-35
+//   vjp_MatMul       autodiff_vjp_ops.cpp:258-263
+//   vjp_LayerNorm    autodiff_vjp_ops.cpp:351-365
+//   vjp_SoftmaxRow, vjp_LogSumExpRow  autodiff_vjp_ops.cpp:421-440
+//   jvp_* rules      cgadimpl/src/autodiff/autodiff_jvp_ops.cpp (Mul :24-31,
+//                    MatMul :245-249, RMSNorm :366-379 corrected, SoftmaxRow
+//                    :411-420, LogSumExpRow :421-434; LayerNorm, which the
+//                    reference leaves unimplemented (:360-362), uses its
+//                    symmetric Jacobian: the VJP kernel applied to the tangent)
 //   accumulate_grad  cgadimpl/src/core/graph.cpp:44-47
 // Each forward records the same node structure as the reference (inputs,
 // tape, child_grad_count, the node-created hook); each VJP adds its
@@ -15,6 +27,7 @@
 
 #include "ag/autodiff.hpp"
 #include "ag/ops.hpp"
+#include "agk_rowops.h"
 #include "check.hpp"
 
 namespace ag {
@@ -72,6 +85,21 @@ struct GradLocks {
         }
     }
 };
+
+// C = op(A) op(B) on the MFMA GEMM, with the workspace that lets it run its
+// k-contiguous kernel (from the pool, or the capture arena).
+void gemm(const void* A, int64_t lda, bool at, const void* B, int64_t ldb, bool bt, void* C,
+          int64_t ldc, Dtype cdt, int64_t M, int64_t N, int64_t K, bool acc, const char* what) {
+    const size_t wsb = agk_gemm_bf16_workspace_bytes(M, N, K, at, bt);
+    std::unique_ptr<Storage> ws;
+    if (wsb) ws = std::make_unique<Storage>(wsb, current_stream());
+    agk_check(agk_gemm_bf16(A, lda, at, B, ldb, bt, C, ldc, agk_dtype_of(cdt), M, N, K, nullptr,
+                            nullptr, acc ? 1 : 0, ws ? ws->data() : nullptr, wsb, stream_arg()),
+              what);
+}
+
+// A tangent of `like`'s shape and dtype that is all zeros.
+Tensor zero_tangent(const Tensor& like) { return Tensor::zeros(like.shape(), like.dtype()); }
 
 }  // namespace
 
@@ -149,6 +177,78 @@ std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a,
     }
     auto n = std::make_shared<Node>(y, Op::Mul, a->requires_grad() || b->requires_grad(), "*");
     link_inputs(n, {a, b});
+    return n;
+}
+
+std::shared_ptr<Node> matmul_nodeops(const std::shared_ptr<Node>& a,
+                                     const std::shared_ptr<Node>& b) {
+    require_value(a, "matmul");
+    require_value(b, "matmul");
+    const Tensor& av = a->value;
+    const Tensor& bv = b->value;
+    if (av.dtype() != Dtype::BFloat16 || bv.dtype() != Dtype::BFloat16)
+        fail("matmul: operands must be bfloat16 (the product runs on the bf16 matrix cores)");
+    if (bv.dim() != 2 || av.dim() < 1 || av.cols() != bv.shape()[0])
+        fail("matmul: expects a [..., K] and b [K, N]");
+    const int64_t M = av.rows(), K = av.cols(), N = bv.shape()[1];
+    if (M % 8 || N % 8 || K % 8) fail("matmul: M, N and K must be multiples of 8");
+    std::vector<int64_t> ys = av.shape();
+    ys.back() = N;
+    Tensor y = Tensor::empty(ys, Dtype::BFloat16);
+    if (M && N) {
+        if (K == 0) fail("matmul: K must be positive");
+        gemm(av.data(), K, false, bv.data(), N, false, y.data(), N, Dtype::BFloat16, M, N, K,
+             false, "matmul");
+    }
+    auto n = std::make_shared<Node>(y, Op::MatMul, a->requires_grad() || b->requires_grad(),
+                                    "matmul");
+    link_inputs(n, {a, b});
+    return n;
+}
+
+std::shared_ptr<Node> laynor_nodeops(const std::shared_ptr<Node>& x) {
+    require_value(x, "laynor");
+    const Tensor& xv = x->value;
+    if (xv.dim() < 1) fail("laynor: input needs at least one axis");
+    constexpr float kEps = 1e-5f;  // fixed, as cgadimpl/src/ops/normalization.cpp:14
+    Tensor y = Tensor::empty(xv.shape(), xv.dtype());
+    auto mean = std::make_shared<Tensor>(Tensor::empty(row_stat_shape(xv), Dtype::Float32));
+    auto rstd = std::make_shared<Tensor>(Tensor::empty(row_stat_shape(xv), Dtype::Float32));
+    agk_check(agk_layernorm_fwd(xv.data(), y.data(), static_cast<float*>(mean->data()),
+                                static_cast<float*>(rstd->data()), xv.rows(), xv.cols(), kEps,
+                                agk_dtype_of(xv.dtype()), stream_arg()),
+              "laynor");
+    auto n = std::make_shared<Node>(y, Op::LayerNorm, x->requires_grad(), "layernor");
+    n->eps = kEps;
+    n->tape.push_back(mean);
+    n->tape.push_back(rstd);
+    link_inputs(n, {x});
+    return n;
+}
+
+std::shared_ptr<Node> softmax_row_nodeops(const std::shared_ptr<Node>& z) {
+    require_value(z, "softmax_row");
+    const Tensor& zv = z->value;
+    if (zv.dim() < 1) fail("softmax_row: input needs at least one axis");
+    Tensor y = Tensor::empty(zv.shape(), zv.dtype());
+    agk_check(agk_softmax_fwd(zv.data(), y.data(), zv.rows(), zv.cols(), agk_dtype_of(zv.dtype()),
+                              stream_arg()),
+              "softmax_row");
+    auto n = std::make_shared<Node>(y, Op::SoftmaxRow, z->requires_grad(), "softmax_row");
+    link_inputs(n, {z});
+    return n;
+}
+
+std::shared_ptr<Node> logsumexp_row_nodeops(const std::shared_ptr<Node>& z) {
+    require_value(z, "logsumexp_row");
+    const Tensor& zv = z->value;
+    if (zv.dim() < 1 || zv.cols() == 0) fail("logsumexp_row: needs a non-empty last axis");
+    Tensor y = Tensor::empty(row_stat_shape(zv), zv.dtype());
+    agk_check(agk_logsumexp_fwd(zv.data(), y.data(), zv.rows(), zv.cols(),
+                                agk_dtype_of(zv.dtype()), stream_arg()),
+              "logsumexp_row");
+    auto n = std::make_shared<Node>(y, Op::LogSumExpRow, z->requires_grad(), "logsumexp_row");
+    link_inputs(n, {z});
     return n;
 }
 
@@ -274,6 +374,246 @@ void vjp_Mul(Node* n, const Tensor& gy) {
               "vjp_Mul");
 }
 
+// A.grad += gy B^T (bf16), B.grad += A^T gy (fp32)   (autodiff_vjp_ops.cpp:258-263)
+void vjp_MatMul(Node* n, const Tensor& gy) {
+    Node* A = n->inputs[0].get();
+    Node* B = n->inputs[1].get();
+    const bool want_a = A->requires_grad();
+    const bool want_b = B->requires_grad();
+    if (!want_a && !want_b) return;
+    check_upstream(n, gy, "vjp_MatMul");
+    const Tensor& av = A->value;
+    const Tensor& bv = B->value;
+    const int64_t M = av.rows(), K = av.cols(), N = bv.shape()[1];
+    GradLocks lock(A, B);
+    if (want_a) {
+        bool acc = false;
+        Tensor& da = A->grad_for_write(Dtype::BFloat16, &acc);
+        if (M && K) {
+            if (N == 0) fail("vjp_MatMul: N must be positive");
+            gemm(gy.data(), N, false, bv.data(), N, true, da.data(), K, Dtype::BFloat16, M, K, N,
+                 acc, "vjp_MatMul dA");
+        }
+    }
+    if (want_b) {
+        bool acc = false;
+        Tensor& db = B->grad_for_write(Dtype::Float32, &acc);
+        if (K && N) {
+            if (M == 0) fail("vjp_MatMul: the batch must not be empty");
+            gemm(av.data(), K, true, gy.data(), N, false, db.data(), N, Dtype::Float32, K, N, M,
+                 acc, "vjp_MatMul dB");
+        }
+    }
+}
+
+// X.grad += rstd * (gy - mean(gy) - xhat * mean(gy * xhat))   (autodiff_vjp_ops.cpp:351-365)
+void vjp_LayerNorm(Node* n, const Tensor& gy) {
+    Node* X = n->inputs[0].get();
+    if (!X->requires_grad()) return;
+    check_upstream(n, gy, "vjp_LayerNorm");
+    const Tensor& x = X->value;
+    GradLocks lock(X, nullptr);
+    bool acc = false;
+    Tensor& dx = X->grad_for_write(x.dtype(), &acc);
+    agk_check(agk_layernorm_bwd(x.data(), static_cast<const float*>(n->tape[0]->data()),
+                                static_cast<const float*>(n->tape[1]->data()), gy.data(),
+                                dx.data(), x.rows(), x.cols(), agk_dtype_of(x.dtype()),
+                                acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE, stream_arg()),
+              "vjp_LayerNorm");
+}
+
+// Z.grad += y * (gy - sum(y * gy))   (autodiff_vjp_ops.cpp:421-428)
+void vjp_SoftmaxRow(Node* n, const Tensor& gy) {
+    Node* Z = n->inputs[0].get();
+    if (!Z->requires_grad()) return;
+    check_upstream(n, gy, "vjp_SoftmaxRow");
+    const Tensor& y = n->value;
+    GradLocks lock(Z, nullptr);
+    bool acc = false;
+    Tensor& dz = Z->grad_for_write(y.dtype(), &acc);
+    agk_check(agk_softmax_bwd(y.data(), gy.data(), dz.data(), y.rows(), y.cols(),
+                              agk_dtype_of(y.dtype()), acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE,
+                              stream_arg()),
+              "vjp_SoftmaxRow");
+}
+
+// Z.grad += gy * softmax(z)   (autodiff_vjp_ops.cpp:430-440)
+void vjp_LogSumExpRow(Node* n, const Tensor& gy) {
+    Node* Z = n->inputs[0].get();
+    if (!Z->requires_grad()) return;
+    check_upstream(n, gy, "vjp_LogSumExpRow");
+    const Tensor& z = Z->value;
+    GradLocks lock(Z, nullptr);
+    bool acc = false;
+    Tensor& dz = Z->grad_for_write(z.dtype(), &acc);
+    agk_check(agk_logsumexp_bwd(z.data(), gy.data(), dz.data(), z.rows(), z.cols(),
+                                agk_dtype_of(z.dtype()), acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE,
+                                stream_arg()),
+              "vjp_LogSumExpRow");
+}
+
+// ---- JVP rules ------------------------------------------------------------------
+// Each returns the tangent of n, or an undefined Tensor when every input
+// tangent is zero.  `tan(p)` is the tangent of input p (undefined: zero).
+
+using TangentOf = std::function<const Tensor&(Node*)>;
+
+namespace {
+void check_tangent(const Tensor& t, const Tensor& like, const char* op) {
+    if (t.defined() && (t.shape() != like.shape() || t.dtype() != like.dtype()))
+        fail(std::string(op) + ": a tangent must have its node's shape and dtype");
+}
+}  // namespace
+
+Tensor jvp_Leaf(Node*, const TangentOf&) { return Tensor(); }  // seeds are set by jvp()
+
+// tA * B + A * tB   (autodiff_jvp_ops.cpp:24-31)
+Tensor jvp_Mul(Node* n, const TangentOf& tan) {
+    Node* A = n->inputs[0].get();
+    Node* B = n->inputs[1].get();
+    const Tensor& ta = tan(A);
+    const Tensor& tb = tan(B);
+    if (!ta.defined() && !tb.defined()) return Tensor();
+    check_tangent(ta, A->value, "jvp_Mul");
+    check_tangent(tb, B->value, "jvp_Mul");
+    const Tensor& av = A->value;
+    const Tensor& bv = B->value;
+    Tensor out = Tensor::empty(n->value.shape(), n->value.dtype());
+    const int dt = agk_dtype_of(av.dtype());
+    // full [..., D] times row [D]: out (+)= t_full * row and full * t_row, each
+    // through the broadcast multiply's da path (equal shapes: one row of numel)
+    const bool equal = av.shape() == bv.shape();
+    const bool b_is_row = !equal && av.dim() >= 1 && is_row_vector(bv, av.cols());
+    const Tensor& full = equal || b_is_row ? av : bv;
+    const int64_t rows = equal ? 1 : full.rows();
+    const int64_t cols = equal ? full.numel() : full.cols();
+    bool first = true;
+    auto add_product = [&](const Tensor& f, const Tensor& r) {  // out (+)= f * r
+        agk_check(agk_mul_rowbcast_bwd(f.data(), nullptr, r.data(), out.data(), nullptr, nullptr,
+                                       0, rows, cols, dt, first ? AGK_ACCUM_NONE : AGK_ACCUM_DX,
+                                       stream_arg()),
+                  "jvp_Mul");
+        first = false;
+    };
+    if (equal) {
+        if (ta.defined()) add_product(ta, bv);
+        if (tb.defined()) add_product(tb, av);
+    } else {
+        Node* F = b_is_row ? A : B;
+        Node* Rw = b_is_row ? B : A;
+        const Tensor& tf = tan(F);
+        const Tensor& tr = tan(Rw);
+        if (tf.defined()) add_product(tf, Rw->value);
+        if (tr.defined()) add_product(F->value, tr);
+    }
+    return out;
+}
+
+// tA B + A tB   (autodiff_jvp_ops.cpp:245-249)
+Tensor jvp_MatMul(Node* n, const TangentOf& tan) {
+    Node* A = n->inputs[0].get();
+    Node* B = n->inputs[1].get();
+    const Tensor& ta = tan(A);
+    const Tensor& tb = tan(B);
+    if (!ta.defined() && !tb.defined()) return Tensor();
+    check_tangent(ta, A->value, "jvp_MatMul");
+    check_tangent(tb, B->value, "jvp_MatMul");
+    const Tensor& av = A->value;
+    const Tensor& bv = B->value;
+    const int64_t M = av.rows(), K = av.cols(), N = bv.shape()[1];
+    Tensor out = Tensor::empty(n->value.shape(), Dtype::BFloat16);
+    if (M == 0 || N == 0) return out;
+    bool acc = false;
+    if (ta.defined()) {
+        gemm(ta.data(), K, false, bv.data(), N, false, out.data(), N, Dtype::BFloat16, M, N, K,
+             false, "jvp_MatMul");
+        acc = true;
+    }
+    if (tb.defined())
+        gemm(av.data(), K, false, tb.data(), N, false, out.data(), N, Dtype::BFloat16, M, N, K,
+             acc, "jvp_MatMul");
+    return out;
+}
+
+// t*r - y*r*sum(t*y)/D   (autodiff_jvp_ops.cpp:366-379, corrected)
+Tensor jvp_RMSNorm(Node* n, const TangentOf& tan) {
+    Node* X = n->inputs[0].get();
+    const Tensor& tx = tan(X);
+    if (!tx.defined()) return Tensor();
+    check_tangent(tx, X->value, "jvp_RMSNorm");
+    const Tensor& x = X->value;
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    agk_check(agk_rmsnorm_jvp(x.data(), nullptr, static_cast<const float*>(n->tape[0]->data()),
+                              tx.data(), nullptr, out.data(), x.rows(), x.cols(),
+                              agk_dtype_of(x.dtype()), stream_arg()),
+              "jvp_RMSNorm");
+    return out;
+}
+
+// gamma * (t*r - y*r*sum(t*y)/D) + tgamma * x * r  (the rule above, then jvp_Mul)
+Tensor jvp_RMSNormAffine(Node* n, const TangentOf& tan) {
+    Node* X = n->inputs[0].get();
+    Node* G = n->inputs[1].get();
+    const Tensor& tx = tan(X);
+    const Tensor& tg = tan(G);
+    if (!tx.defined() && !tg.defined()) return Tensor();
+    check_tangent(tx, X->value, "jvp_RMSNormAffine");
+    check_tangent(tg, G->value, "jvp_RMSNormAffine");
+    const Tensor& x = X->value;
+    const Tensor txz = tx.defined() ? tx : zero_tangent(x);
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    agk_check(agk_rmsnorm_jvp(x.data(), G->value.data(),
+                              static_cast<const float*>(n->tape[0]->data()), txz.data(),
+                              tg.defined() ? tg.data() : nullptr, out.data(), x.rows(), x.cols(),
+                              agk_dtype_of(x.dtype()), stream_arg()),
+              "jvp_RMSNormAffine");
+    return out;
+}
+
+// The LayerNorm Jacobian is symmetric: its VJP kernel applied to the tangent.
+Tensor jvp_LayerNorm(Node* n, const TangentOf& tan) {
+    Node* X = n->inputs[0].get();
+    const Tensor& tx = tan(X);
+    if (!tx.defined()) return Tensor();
+    check_tangent(tx, X->value, "jvp_LayerNorm");
+    const Tensor& x = X->value;
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    agk_check(agk_layernorm_bwd(x.data(), static_cast<const float*>(n->tape[0]->data()),
+                                static_cast<const float*>(n->tape[1]->data()), tx.data(),
+                                out.data(), x.rows(), x.cols(), agk_dtype_of(x.dtype()),
+                                AGK_ACCUM_NONE, stream_arg()),
+              "jvp_LayerNorm");
+    return out;
+}
+
+// y * (t - sum(y * t))   (autodiff_jvp_ops.cpp:411-420)
+Tensor jvp_SoftmaxRow(Node* n, const TangentOf& tan) {
+    Node* Z = n->inputs[0].get();
+    const Tensor& tz = tan(Z);
+    if (!tz.defined()) return Tensor();
+    check_tangent(tz, Z->value, "jvp_SoftmaxRow");
+    const Tensor& y = n->value;
+    Tensor out = Tensor::empty(y.shape(), y.dtype());
+    agk_check(agk_softmax_bwd(y.data(), tz.data(), out.data(), y.rows(), y.cols(),
+                              agk_dtype_of(y.dtype()), AGK_ACCUM_NONE, stream_arg()),
+              "jvp_SoftmaxRow");
+    return out;
+}
+
+// sum(softmax(z) * t)   (autodiff_jvp_ops.cpp:421-434)
+Tensor jvp_LogSumExpRow(Node* n, const TangentOf& tan) {
+    Node* Z = n->inputs[0].get();
+    const Tensor& tz = tan(Z);
+    if (!tz.defined()) return Tensor();
+    check_tangent(tz, Z->value, "jvp_LogSumExpRow");
+    const Tensor& z = Z->value;
+    Tensor out = Tensor::empty(n->value.shape(), z.dtype());
+    agk_check(agk_logsumexp_jvp(z.data(), tz.data(), out.data(), z.rows(), z.cols(),
+                                agk_dtype_of(z.dtype()), stream_arg()),
+              "jvp_LogSumExpRow");
+    return out;
+}
+
 }  // namespace detail
 
 Value rms(const Value& x) { return Value(detail::rms_nodeops(x.node)); }
@@ -283,5 +623,15 @@ Value rms_norm(const Value& x, const Value& gamma, float eps) {
 }
 
 Value mul(const Value& a, const Value& b) { return Value(detail::mul_nodeops(a.node, b.node)); }
+
+Value matmul(const Value& a, const Value& b) {
+    return Value(detail::matmul_nodeops(a.node, b.node));
+}
+
+Value laynor(const Value& x) { return Value(detail::laynor_nodeops(x.node)); }
+
+Value softmax_row(const Value& z) { return Value(detail::softmax_row_nodeops(z.node)); }
+
+Value logsumexp_row(const Value& z) { return Value(detail::logsumexp_row_nodeops(z.node)); }
 
 }  // namespace ag

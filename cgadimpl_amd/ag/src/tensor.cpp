@@ -1,9 +1,11 @@
 // tensor.cpp -- device tensors on HIP's stream-ordered memory pool.
 #include "ag/tensor.hpp"
 
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <numeric>
+#include <string>
 
 #include "check.hpp"
 
@@ -58,14 +60,82 @@ const char* dtype_name(Dtype dt) { return dt == Dtype::Float32 ? "float32" : "bf
 hipStream_t current_stream() { return t_current_stream; }
 void set_current_stream(hipStream_t stream) { t_current_stream = stream; }
 
+// ---- capture arenas ------------------------------------------------------------
+
+CaptureArena::CaptureArena(size_t bytes) : capacity_(bytes) {
+    if (bytes) hip_check(hipMalloc(&base_, bytes), "hipMalloc (capture arena)");
+}
+
+CaptureArena::~CaptureArena() {
+    for (void* p : deferred_) (void)hipFree(p);
+    if (base_) (void)hipFree(base_);
+}
+
+void* CaptureArena::take(size_t bytes) {
+    std::lock_guard<std::mutex> lock(mu_);
+    const size_t off = (used_ + 255) & ~size_t(255);
+    if (off > capacity_ || bytes > capacity_ - off)
+        fail("graph capture: the capture arena (" + std::to_string(capacity_) +
+             " bytes) cannot hold another " + std::to_string(bytes) +
+             " bytes; construct the GraphRunner with a larger arena");
+    used_ = off + bytes;
+    return static_cast<char*>(base_) + off;
+}
+
+void CaptureArena::defer_free(void* pool_ptr) {
+    std::lock_guard<std::mutex> lock(mu_);
+    deferred_.push_back(pool_ptr);
+}
+
+size_t CaptureArena::used() const {
+    std::lock_guard<std::mutex> lock(mu_);
+    return used_;
+}
+
+namespace {
+std::mutex g_arena_mu;
+std::vector<std::pair<hipStream_t, std::shared_ptr<CaptureArena>>> g_arenas;
+std::atomic<int> g_narenas{0};
+}  // namespace
+
+void set_capture_arena(hipStream_t stream, std::shared_ptr<CaptureArena> arena) {
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    for (auto it = g_arenas.begin(); it != g_arenas.end(); ++it)
+        if (it->first == stream) {
+            g_arenas.erase(it);
+            break;
+        }
+    if (arena) g_arenas.emplace_back(stream, std::move(arena));
+    g_narenas.store(static_cast<int>(g_arenas.size()));
+}
+
+std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream) {
+    if (g_narenas.load() == 0) return nullptr;  // no capture anywhere: the usual case
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    for (auto& [s, a] : g_arenas)
+        if (s == stream) return a;
+    return nullptr;
+}
+
+// ---- storage --------------------------------------------------------------------
+
 Storage::Storage(size_t bytes, hipStream_t stream) : bytes_(bytes), stream_(stream) {
     if (bytes == 0) return;
+    if ((arena_ = capture_arena(stream))) {
+        ptr_ = arena_->take(bytes);
+        return;
+    }
     retain_pool_memory();
     hip_check(hipMallocAsync(&ptr_, bytes, stream), "hipMallocAsync");
 }
 
 Storage::~Storage() {
-    if (ptr_) (void)hipFreeAsync(ptr_, stream_);
+    if (!ptr_ || arena_) return;  // arena memory goes with the arena
+    if (auto a = capture_arena(stream_)) {
+        a->defer_free(ptr_);  // a free on a capturing stream would be recorded
+        return;
+    }
+    (void)hipFreeAsync(ptr_, stream_);
 }
 
 Tensor Tensor::empty(const std::vector<int64_t>& shape, Dtype dt) {
@@ -77,7 +147,16 @@ Tensor Tensor::empty(const std::vector<int64_t>& shape, Dtype dt) {
     return t;
 }
 
+namespace {
+void no_fill_under_capture(const char* what) {
+    if (capture_arena(current_stream()))
+        fail(std::string(what) + ": not available while the current stream is captured into a "
+             "graph (no memset nodes in captured graphs); create the tensor before the capture");
+}
+}  // namespace
+
 Tensor Tensor::zeros(const std::vector<int64_t>& shape, Dtype dt) {
+    no_fill_under_capture("ag::Tensor::zeros");
     Tensor t = empty(shape, dt);
     if (t.nbytes())
         hip_check(hipMemsetAsync(t.data(), 0, t.nbytes(), current_stream()), "hipMemsetAsync");
@@ -85,6 +164,7 @@ Tensor Tensor::zeros(const std::vector<int64_t>& shape, Dtype dt) {
 }
 
 Tensor Tensor::ones(const std::vector<int64_t>& shape, Dtype dt) {
+    no_fill_under_capture("ag::Tensor::ones");
     Tensor t = empty(shape, dt);
     const size_t n = static_cast<size_t>(t.numel());
     if (n == 0) return t;

@@ -1,5 +1,6 @@
 // test_ag_layer.cpp -- the ag:: graph layer (Value, rms, rms_norm, mul,
-// backward) on the GPU.
+// matmul, laynor, softmax_row, logsumexp_row, backward, jvp, GraphRunner) on
+// the GPU.
 //
 //   test_ag_layer selftest     checks below; prints PASS/FAIL per check and
 //                              exits with the number of failures
@@ -15,7 +16,11 @@
 // 262-267), gradient accumulation across backward calls and zero_grad
 // (Tests/test_phase1_advanced.cpp:32-64), sequential against parallel
 // backward (Tests/dependency_counter_correctness/test_dependency_correctness.cpp),
-// and broadcast-multiply gradients (test_core_ops_gpu.cpp:198-205).
+// and broadcast-multiply gradients (test_core_ops_gpu.cpp:198-205).  Forward
+// mode is checked against central differences of host fp64 restatements of
+// each op, matmul against a host fp64 product, and hipGraph capture by
+// replaying a captured forward + backward on changed inputs, with eager work
+// in between, against eager runs (bitwise: the kernels are deterministic).
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -355,6 +360,356 @@ void test_user_stream() {
     (void)hipStreamDestroy(s);
 }
 
+
+// ---- matmul, the row ops beside RMSNorm, forward mode, graph capture ----------
+
+std::vector<uint16_t> to_bf16_bits(const std::vector<float>& v) {
+    std::vector<uint16_t> b(v.size());
+    for (size_t i = 0; i < v.size(); ++i) {
+        uint32_t u;
+        std::memcpy(&u, &v[i], 4);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        b[i] = static_cast<uint16_t>(u >> 16);
+    }
+    return b;
+}
+
+float bf16_round(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+Value bf16_leaf(const std::vector<float>& v, const std::vector<int64_t>& shape, const char* name,
+                bool req = true) {
+    std::vector<uint16_t> b = to_bf16_bits(v);
+    Tensor t = Tensor::from_host(b.data(), shape, Dtype::BFloat16);
+    t.set_requires_grad(req);
+    return make_tensor(t, name);
+}
+
+std::vector<float> rounded(const std::vector<float>& v) {
+    std::vector<float> o(v.size());
+    for (size_t i = 0; i < v.size(); ++i) o[i] = bf16_round(v[i]);
+    return o;
+}
+
+double rel_err(const std::vector<float>& got, const std::vector<double>& ref) {
+    double num = 0.0, den = 0.0;
+    for (size_t i = 0; i < ref.size(); ++i) {
+        num = std::max(num, std::fabs(double(got[i]) - ref[i]));
+        den = std::max(den, std::fabs(ref[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+// host fp64 restatements, row-major [R, D]
+using Vec = std::vector<double>;
+Vec to_d(const std::vector<float>& v) { return Vec(v.begin(), v.end()); }
+
+Vec host_rms_layer(const Vec& x, const Vec* g, int64_t R, int64_t D, double eps) {
+    Vec y(x.size());
+    for (int64_t i = 0; i < R; ++i) {
+        double ss = 0.0;
+        for (int64_t j = 0; j < D; ++j) ss += x[i * D + j] * x[i * D + j];
+        const double r = 1.0 / std::sqrt(ss / D + eps);
+        for (int64_t j = 0; j < D; ++j) y[i * D + j] = x[i * D + j] * r * (g ? (*g)[j] : 1.0);
+    }
+    return y;
+}
+
+Vec host_laynor(const Vec& x, int64_t R, int64_t D, double eps = 1e-5) {
+    Vec y(x.size());
+    for (int64_t i = 0; i < R; ++i) {
+        double m = 0.0, v = 0.0;
+        for (int64_t j = 0; j < D; ++j) m += x[i * D + j];
+        m /= D;
+        for (int64_t j = 0; j < D; ++j) v += (x[i * D + j] - m) * (x[i * D + j] - m);
+        v /= D;
+        for (int64_t j = 0; j < D; ++j) y[i * D + j] = (x[i * D + j] - m) / std::sqrt(v + eps);
+    }
+    return y;
+}
+
+Vec host_softmax(const Vec& z, int64_t R, int64_t D) {
+    Vec y(z.size());
+    for (int64_t i = 0; i < R; ++i) {
+        double m = -INFINITY, s = 0.0;
+        for (int64_t j = 0; j < D; ++j) m = std::max(m, z[i * D + j]);
+        for (int64_t j = 0; j < D; ++j) s += std::exp(z[i * D + j] - m);
+        for (int64_t j = 0; j < D; ++j) y[i * D + j] = std::exp(z[i * D + j] - m) / s;
+    }
+    return y;
+}
+
+Vec host_lse(const Vec& z, int64_t R, int64_t D) {
+    Vec y(R);
+    for (int64_t i = 0; i < R; ++i) {
+        double m = -INFINITY, s = 0.0;
+        for (int64_t j = 0; j < D; ++j) m = std::max(m, z[i * D + j]);
+        for (int64_t j = 0; j < D; ++j) s += std::exp(z[i * D + j] - m);
+        y[i] = std::log(s) + m;
+    }
+    return y;
+}
+
+Vec axpy(const Vec& x, const Vec& t, double h) {
+    Vec o(x.size());
+    for (size_t i = 0; i < x.size(); ++i) o[i] = x[i] + h * t[i];
+    return o;
+}
+
+Vec central(const std::function<Vec(double)>& f, double h = 1e-4) {
+    Vec p = f(h), m = f(-h), o(p.size());
+    for (size_t i = 0; i < p.size(); ++i) o[i] = (p[i] - m[i]) / (2 * h);
+    return o;
+}
+
+void test_row_ops_gradients() {
+    // the reference pattern: [4,10] input, numerical gradient of sum(f(a))
+    Value a = leaf(normal(40, 60), {4, 10}, "a");
+    auto fl = [&]() { return laynor(a); };
+    Tensor dy = Tensor::from_host_f32(normal(40, 61), {4, 10});
+    Value w = leaf(dy.to_host_f32(), {4, 10}, "w", false);
+    auto fw = [&]() { return laynor(a) * w; };
+    backward(fl(), &dy);
+    check_grad("laynor [4,10] numerical gradient", a, fw);
+    zero_grad(fl());
+    auto fs = [&]() { return softmax_row(a) * w; };
+    backward(softmax_row(a), &dy);
+    check_grad("softmax_row [4,10] numerical gradient", a, fs);
+    zero_grad(fs());
+    auto fz = [&]() { return logsumexp_row(a); };
+    backward(fz());
+    check_grad("logsumexp_row [4,10] numerical gradient", a, fz);
+    report("logsumexp_row output shape [4,1]",
+           fz().val().shape() == std::vector<int64_t>{4, 1});
+}
+
+void test_jvp() {
+    const int64_t R = 5, D = 24;
+    const double eps = 1e-5;
+    std::vector<float> xv = normal(R * D, 70), gv = uniform(D, 71, 0.5, 1.5),
+                       txv = normal(R * D, 72), tgv = normal(D, 73);
+    const Vec xd = to_d(xv), gd = to_d(gv), txd = to_d(txv), tgd = to_d(tgv);
+    Tensor tx = Tensor::from_host_f32(txv, {R, D}), tg = Tensor::from_host_f32(tgv, {D});
+
+    Value x = leaf(xv, {R, D}, "x"), g = leaf(gv, {D}, "g");
+    Tensor ty = jvp(rms_norm(x, g, 1e-5f), {{x.node.get(), tx}, {g.node.get(), tg}});
+    Vec fd = central([&](double h) {
+        Vec gh = axpy(gd, tgd, h);
+        return host_rms_layer(axpy(xd, txd, h), &gh, R, D, eps);
+    });
+    const double e1 = rel_err(ty.to_host_f32(), fd);
+    report("jvp rms_norm(x, g) along (tx, tg) == central differences", e1 <= 1e-4,
+           std::to_string(e1));
+
+    Value x2 = leaf(xv, {R, D}, "x2"), g2 = leaf(gv, {1, D}, "g2");
+    Tensor tg2 = Tensor::from_host_f32(tgv, {1, D});
+    Tensor ty2 = jvp(rms(x2) * g2, {{x2.node.get(), tx}, {g2.node.get(), tg2}});
+    const double e2 = rel_err(ty2.to_host_f32(), to_d(ty.to_host_f32()));
+    report("jvp rms(x) * g == jvp rms_norm(x, g)", e2 <= 1e-5, std::to_string(e2));
+
+    Value x3 = leaf(xv, {R, D}, "x3");
+    const double e3 = rel_err(jvp(rms(x3), {{x3.node.get(), tx}}).to_host_f32(),
+                              central([&](double h) {
+                                  return host_rms_layer(axpy(xd, txd, h), nullptr, R, D, eps);
+                              }));
+    report("jvp rms(x) (the corrected rule) == central differences", e3 <= 1e-4,
+           std::to_string(e3));
+
+    Value x4 = leaf(xv, {R, D}, "x4");
+    const double e4 = rel_err(jvp(laynor(x4), {{x4.node.get(), tx}}).to_host_f32(),
+                              central([&](double h) { return host_laynor(axpy(xd, txd, h), R, D); }));
+    report("jvp laynor == central differences", e4 <= 1e-4, std::to_string(e4));
+
+    Value x5 = leaf(xv, {R, D}, "x5");
+    const double e5 = rel_err(jvp(softmax_row(x5), {{x5.node.get(), tx}}).to_host_f32(),
+                              central([&](double h) { return host_softmax(axpy(xd, txd, h), R, D); }));
+    report("jvp softmax_row == central differences", e5 <= 1e-4, std::to_string(e5));
+
+    Value x6 = leaf(xv, {R, D}, "x6");
+    const double e6 = rel_err(jvp(logsumexp_row(x6), {{x6.node.get(), tx}}).to_host_f32(),
+                              central([&](double h) { return host_lse(axpy(xd, txd, h), R, D); }));
+    report("jvp logsumexp_row == central differences", e6 <= 1e-4, std::to_string(e6));
+
+    // a composition: softmax_row(laynor(rms_norm(x, g))) along tx only
+    Value x7 = leaf(xv, {R, D}, "x7"), g7 = leaf(gv, {D}, "g7");
+    Tensor ty7 = jvp(softmax_row(laynor(rms_norm(x7, g7, 1e-5f))), {{x7.node.get(), tx}});
+    const double e7 = rel_err(ty7.to_host_f32(), central([&](double h) {
+        return host_softmax(host_laynor(host_rms_layer(axpy(xd, txd, h), &gd, R, D, eps), R, D),
+                            R, D);
+    }));
+    report("jvp of softmax_row(laynor(rms_norm(x, g))) == central differences", e7 <= 1e-4,
+           std::to_string(e7));
+
+    // a seed that does not reach the root gives a zero tangent
+    Value x8 = leaf(xv, {R, D}, "x8"), other = leaf(xv, {R, D}, "other");
+    report("jvp without a seed on the path is zero",
+           max_abs(jvp(rms(x8), {{other.node.get(), tx}}).to_host_f32()) == 0.0);
+}
+
+void test_matmul_layer() {
+    const int64_t M = 64, K = 128, N = 96;
+    const double eps = 1e-5;
+    std::vector<float> xv = rounded(normal(M * K, 80)), gv = rounded(uniform(K, 81, 0.5, 1.5)),
+                       wv = rounded(normal(K * N, 82, 0.05)), dyv = rounded(normal(M * N, 83));
+    std::vector<uint16_t> dyb = to_bf16_bits(dyv);
+    Tensor dy = Tensor::from_host(dyb.data(), {M, N}, Dtype::BFloat16);
+    auto run = [&](bool parallel, std::vector<std::vector<float>>& out) {
+        Value x = bf16_leaf(xv, {M, K}, "x"), g = bf16_leaf(gv, {K}, "g"),
+              W = bf16_leaf(wv, {K, N}, "W");
+        Value y = matmul(rms_norm(x, g, 1e-5f), W);
+        backward(y, &dy, parallel);
+        out = {y.val().to_host_f32(), x.grad().to_host_f32(), g.grad().to_host_f32(),
+               W.grad().to_host_f32()};
+        report("matmul: dx bf16, dgamma and dW fp32",
+               x.grad().dtype() == Dtype::BFloat16 && g.grad().dtype() == Dtype::Float32 &&
+                   W.grad().dtype() == Dtype::Float32);
+    };
+    std::vector<std::vector<float>> seq, par;
+    run(false, seq);
+    run(true, par);
+    report("matmul(rms_norm(x, g), W): parallel backward == sequential (bitwise)", seq == par);
+    // host fp64 reference with bf16 rounding where the graph stores bf16 (h, dh)
+    Vec h(M * K), y(M * N, 0.0), dh(M * K, 0.0), dW(K * N, 0.0), dx(M * K), dg(K, 0.0);
+    std::vector<double> r(M);
+    for (int64_t i = 0; i < M; ++i) {
+        double ss = 0.0;
+        for (int64_t k = 0; k < K; ++k) ss += double(xv[i * K + k]) * xv[i * K + k];
+        r[i] = 1.0 / std::sqrt(ss / K + eps);
+        for (int64_t k = 0; k < K; ++k) h[i * K + k] = bf16_round(float(xv[i * K + k] * r[i] * gv[k]));
+    }
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t j = 0; j < N; ++j) {
+                y[i * N + j] += h[i * K + k] * wv[k * N + j];
+                dh[i * K + k] += double(dyv[i * N + j]) * wv[k * N + j];
+                dW[k * N + j] += h[i * K + k] * dyv[i * N + j];
+            }
+    for (auto& v : dh) v = bf16_round(float(v));
+    for (int64_t i = 0; i < M; ++i) {
+        double dot = 0.0;
+        for (int64_t k = 0; k < K; ++k) dot += dh[i * K + k] * gv[k] * xv[i * K + k];
+        for (int64_t k = 0; k < K; ++k) {
+            const double gk = dh[i * K + k] * gv[k];
+            dx[i * K + k] = r[i] * (gk - xv[i * K + k] * r[i] * r[i] * dot / K);
+            dg[k] += dh[i * K + k] * xv[i * K + k] * r[i];
+        }
+    }
+    const double ey = rel_err(seq[0], y), ex = rel_err(seq[1], dx), eg = rel_err(seq[2], dg),
+                 ew = rel_err(seq[3], dW);
+    report("matmul(rms_norm(x, g), W) vs host fp64 (y, dx, dgamma, dW)",
+           ey <= 1e-2 && ex <= 3e-2 && eg <= 1e-2 && ew <= 1e-2,
+           "y " + std::to_string(ey) + " dx " + std::to_string(ex) + " dgamma " +
+               std::to_string(eg) + " dW " + std::to_string(ew));
+    // forward mode through the product: tangent of W only
+    Value x = bf16_leaf(xv, {M, K}, "x"), W = bf16_leaf(wv, {K, N}, "W");
+    std::vector<float> twv = rounded(normal(K * N, 84, 0.05));
+    std::vector<uint16_t> twb = to_bf16_bits(twv);
+    Tensor tw = Tensor::from_host(twb.data(), {K, N}, Dtype::BFloat16);
+    Tensor ty = jvp(matmul(x, W), {{W.node.get(), tw}});
+    Vec tref(M * N, 0.0);
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t j = 0; j < N; ++j) tref[i * N + j] += double(xv[i * K + k]) * twv[k * N + j];
+    const double et = rel_err(ty.to_host_f32(), tref);
+    report("jvp matmul(x, W) along tW == x tW", et <= 1e-2, std::to_string(et));
+
+    bool threw = false;
+    try {
+        matmul(leaf(normal(64, 85), {8, 8}, "f32a"), leaf(normal(64, 86), {8, 8}, "f32b"));
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    report("matmul of fp32 operands throws", threw);
+    threw = false;
+    try {
+        matmul(bf16_leaf(normal(64, 87), {8, 8}, "a"), bf16_leaf(normal(128, 88), {16, 8}, "b"));
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    report("matmul with mismatched inner dimensions throws", threw);
+}
+
+// A captured forward + backward, replayed on changed inputs with eager work in
+// between, against eager runs of the same graph.
+void test_graph_capture(bool parallel) {
+    const int64_t R = 256, D = 1024;
+    std::vector<float> gv = uniform(D, 91, 0.5, 1.5);
+    GraphRunner runner(size_t(64) << 20);
+    StreamGuard guard(runner.get_stream());
+    Tensor xt = Tensor::from_host_f32(normal(R * D, 90), {R, D});
+    xt.set_requires_grad(true);
+    Tensor gt = Tensor::from_host_f32(gv, {D});
+    gt.set_requires_grad(true);
+    Tensor dyt = Tensor::from_host_f32(normal(R * D, 92), {R, D});
+    Value x = make_tensor(xt, "x"), g = make_tensor(gt, "g");
+    runner.begin_capture();
+    Value s = softmax_row(laynor(rms_norm(x, g, 1e-5f)));
+    backward(s, &dyt, parallel);
+    runner.end_capture();
+    const size_t used = runner.arena_bytes_used();
+    bool same = true;
+    for (int rep = 0; rep < 3; ++rep) {
+        std::vector<float> xv = normal(R * D, 100 + rep);
+        xt.copy_from(Tensor::from_host_f32(xv, {R, D}));
+        {  // eager work on the same stream between replays
+            Value e = leaf(normal(R * D, 200 + rep), {R, D}, "e"), ge = leaf(gv, {D}, "ge");
+            backward(rms_norm(e, ge, 1e-5f), &dyt);
+        }
+        if (!runner.replay()) same = false;
+        (void)hipStreamSynchronize(runner.get_stream());
+        Value xe = leaf(xv, {R, D}, "xe"), ge = leaf(gv, {D}, "ge");
+        Value se = softmax_row(laynor(rms_norm(xe, ge, 1e-5f)));
+        backward(se, &dyt, parallel);
+        same = same && s.val().to_host_f32() == se.val().to_host_f32() &&
+               x.grad().to_host_f32() == xe.grad().to_host_f32() &&
+               g.grad().to_host_f32() == ge.grad().to_host_f32();
+    }
+    report(parallel ? "graph replay == eager, 3 replays on new inputs (parallel backward)"
+                    : "graph replay == eager, 3 replays on new inputs",
+           same, "arena bytes used " + std::to_string(used));
+}
+
+void test_graph_capture_rules() {
+    GraphRunner runner(size_t(1) << 20);
+    StreamGuard guard(runner.get_stream());
+    std::vector<float> xv = normal(64, 95);
+    Value x = leaf(xv, {4, 16}, "x");
+    runner.begin_capture();
+    Value y = rms(x);
+    bool zeros_threw = false, seedless_threw = false, huge_threw = false;
+    try {
+        (void)Tensor::zeros({4});
+    } catch (const std::runtime_error&) {
+        zeros_threw = true;
+    }
+    try {
+        backward(y);  // a ones seed needs a fill
+    } catch (const std::runtime_error&) {
+        seedless_threw = true;
+    }
+    try {
+        (void)Tensor::empty({int64_t(1) << 20});  // 4 MiB > the 1 MiB arena
+    } catch (const std::runtime_error&) {
+        huge_threw = true;
+    }
+    runner.end_capture();
+    report("capture: zeros(), a seedless backward and arena overflow throw",
+           zeros_threw && seedless_threw && huge_threw);
+    const bool replayed = runner.replay();
+    (void)hipStreamSynchronize(runner.get_stream());
+    Value xe = leaf(xv, {4, 16}, "xe");
+    report("capture: the ops before the failures replay",
+           replayed && y.val().to_host_f32() == rms(xe).val().to_host_f32());
+    GraphRunner idle;
+    report("replay without a capture returns false", !idle.replay());
+}
+
 int selftest() {
     const std::pair<const char*, void (*)()> tests[] = {
         {"reference_pattern", test_reference_pattern},
@@ -369,6 +724,12 @@ int selftest() {
         {"bf16_layer", test_bf16_layer},
         {"seed_not_modified", test_seed_not_modified},
         {"user_stream", test_user_stream},
+        {"row_ops_gradients", test_row_ops_gradients},
+        {"jvp", test_jvp},
+        {"matmul_layer", test_matmul_layer},
+        {"graph_capture", [] { test_graph_capture(false); }},
+        {"graph_capture_parallel", [] { test_graph_capture(true); }},
+        {"graph_capture_rules", test_graph_capture_rules},
     };
     for (auto& [name, fn] : tests) {
         std::printf("-- %s\n", name);

@@ -1,9 +1,12 @@
-"""The C++ graph layer (ag::Value, rms, rms_norm, mul, backward) over the C ABI.
+"""The C++ graph layer (ag::Value, rms, rms_norm, mul, matmul, laynor, softmax_row,
+logsumexp_row, backward, jvp, GraphRunner) over the C ABI.
 
 CPU: libag.so and the test program resolve every dependency and export the
 reference's API surface.  GPU: the program's self-checks (numerical gradients
 in the reference's pattern, accumulation, zero_grad, parallel == sequential
-backward, tied gamma, errors, bf16, streams) and, through its dump mode, the
+backward, tied gamma, errors, bf16, streams, the row ops' numerical gradients,
+forward mode against central differences, matmul against a host fp64
+product, hipGraph capture and replay against eager runs) and, through its dump mode, the
 fused layer, the fused layer with parallel backward and the unfused graph
 rms(x) * gamma against the CPU oracle on seeded inputs.
 """
@@ -37,7 +40,13 @@ def test_graph_layer_links_and_exports():
                  "ag::zero_grad(ag::Value const&)", "ag::vjp_lookup(ag::Op)",
                  "ag::detail::vjp_RMSNorm(ag::Node*, ag::Tensor const&)",
                  "ag::detail::vjp_Mul(ag::Node*, ag::Tensor const&)",
-                 "ag::topo_from(ag::Node*)", "ag::nn::RMSNorm::RMSNorm(long, float, ag::Dtype)"):
+                 "ag::topo_from(ag::Node*)", "ag::nn::RMSNorm::RMSNorm(long, float, ag::Dtype)",
+                 "ag::matmul(ag::Value const&, ag::Value const&)", "ag::laynor(ag::Value const&)",
+                 "ag::softmax_row(ag::Value const&)", "ag::logsumexp_row(ag::Value const&)",
+                 "ag::jvp_lookup(ag::Op)", "ag::detail::vjp_MatMul(ag::Node*, ag::Tensor const&)",
+                 "ag::detail::jvp_RMSNorm(ag::Node*, std::function<ag::Tensor const& (ag::Node*)> const&)",
+                 "ag::GraphRunner::begin_capture()", "ag::GraphRunner::end_capture()",
+                 "ag::GraphRunner::replay()"):
         assert want in syms, want
 
 
