@@ -325,6 +325,145 @@ def run_c5(steps, warmup):
     }
 
 
+# ---- row ops on the same skeleton (include/agk_rowops.h) ---------------------------
+# Algorithmic bytes per kernel launch, s = storage bytes, R rows, D cols:
+#   layernorm    fwd 2RDs + 8R (mean, rstd)      bwd 3RDs + 8R
+#   softmax      fwd 2RDs                         bwd 3RDs
+#   logsumexp    fwd RDs + Rs                     bwd 2RDs + Rs      jvp 2RDs + Rs
+#   rmsnorm_jvp  jvp 3RDs + 2Ds + 4R
+ROWOPS = ("layernorm", "softmax", "logsumexp", "rmsnorm_jvp")
+
+
+def _rowop_bytes(op, R, D, s):
+    rd = R * D * s
+    return {
+        "layernorm": {"fwd": 2 * rd + 8 * R, "bwd": 3 * rd + 8 * R},
+        "softmax": {"fwd": 2 * rd, "bwd": 3 * rd},
+        "logsumexp": {"fwd": rd + R * s, "bwd": 2 * rd + R * s, "jvp": 2 * rd + R * s},
+        "rmsnorm_jvp": {"jvp": 3 * rd + 2 * D * s + 4 * R},
+    }[op]
+
+
+def _rowop_cpu_baseline(op, cfg, seconds):
+    """The oracle's restatement of the reference rule (numpy, materialising every
+    intermediate) on a bounded row sample, timed on this host."""
+    import numpy as np
+
+    from cgadimpl_amd import configs
+    from oracle import rowops as ro
+    rows = max(1, min(cfg.rows, (1 << 20) // cfg.cols))
+    x, g, dy = configs.config_inputs(cfg, (rows, cfg.cols))
+    if cfg.dtype == "bf16":
+        import oracle
+        x, g, dy = oracle.bf16_decode(x), oracle.bf16_decode(g), oracle.bf16_decode(dy)
+    fns = {
+        "layernorm": lambda: ro.layernorm_bwd(x, *ro.layernorm_fwd(x, cfg.eps)[1:], dy, cfg.eps),
+        "softmax": lambda: ro.softmax_bwd(ro.softmax_fwd(x), dy),
+        "logsumexp": lambda: (ro.logsumexp_fwd(x), ro.logsumexp_bwd(x, dy[:, :1]),
+                              ro.logsumexp_jvp(x, dy)),
+        "rmsnorm_jvp": lambda: ro.rmsnorm_jvp(x, g, dy, g[::-1] - 1.0, cfg.eps),
+    }
+    f = fns[op]
+    f()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        f()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    alg = sum(_rowop_bytes(op, rows, cfg.cols, cfg.storage_bytes).values())
+    return {"value": round(alg * reps / el / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{rows} of {cfg.rows} rows x {cfg.cols} ({cfg.dtype}), the oracle's "
+                      f"numpy restatement of the reference rules (fp32, every intermediate "
+                      f"materialised), {reps} reps in {el:.1f} s"}
+
+
+def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
+    import torch
+
+    import cgadimpl_amd as agk
+    from cgadimpl_amd import configs
+
+    cfg = configs.CONFIGS[cfg_name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    R, D = cfg.rows, cfg.cols
+    x, g, dy = _device_inputs(cfg, dev, cfg.seed)
+    if op in ("softmax", "logsumexp"):
+        x = (x * 4.0).contiguous()
+    f32 = torch.float32
+    out = torch.empty_like(x)
+    y = torch.empty_like(x)
+    mean = torch.empty(R, 1, dtype=f32, device=dev)
+    rstd = torch.empty(R, 1, dtype=f32, device=dev)
+    lse = torch.empty(R, 1, dtype=x.dtype, device=dev)
+    tl = torch.empty(R, 1, dtype=x.dtype, device=dev)
+    dl = dy[:, :1].contiguous()
+    tg = (torch.flip(g, [0]) - 1.0).contiguous()
+    _, inv = agk.rmsnorm_fwd(x, g, cfg.eps)
+    stream = torch.cuda.current_stream()
+    launches = {
+        "layernorm": [("fwd", lambda: agk.layernorm_fwd(x, cfg.eps, y=y, mean=mean, rstd=rstd,
+                                                        stream=stream)),
+                      ("bwd", lambda: agk.layernorm_bwd(x, mean, rstd, dy, dx=out,
+                                                        stream=stream))],
+        "softmax": [("fwd", lambda: agk.softmax_fwd(x, y=y, stream=stream)),
+                    ("bwd", lambda: agk.softmax_bwd(y, dy, dz=out, stream=stream))],
+        "logsumexp": [("fwd", lambda: agk.logsumexp_fwd(x, y=lse, stream=stream)),
+                      ("bwd", lambda: agk.logsumexp_bwd(x, dl, dz=out, stream=stream)),
+                      ("jvp", lambda: agk.logsumexp_jvp(x, dy, ty=tl, stream=stream))],
+        "rmsnorm_jvp": [("jvp", lambda: agk.rmsnorm_jvp(x, g, inv, dy, tg, ty=out,
+                                                        stream=stream))],
+    }[op]
+    for _ in range(warmup):
+        for _, f in launches:
+            f()
+    torch.cuda.synchronize()
+    n = len(launches)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        for k, (_, f) in enumerate(launches):
+            f()
+            ev[i][k + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    alg = _rowop_bytes(op, R, D, cfg.storage_bytes)
+    kernels = {}
+    for k, (name, _) in enumerate(launches):
+        ms = sum(e[k].elapsed_time(e[k + 1]) for e in ev) / steps
+        gbs = alg[name] / (ms * 1e-3) / 1e9
+        kernels[name] = {"avg_ms": round(ms, 5), "alg_bytes": alg[name], "gbs": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    dom = max(kernels, key=lambda k: kernels[k]["alg_bytes"])
+    ms_per_step = wall * 1e3 / steps
+    total = sum(alg.values())
+    rec = {
+        "metric": f"{op} ({'+'.join(alg)}) achieved HBM GB/s at {list(cfg.shape)}",
+        "value": round(total / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": cfg.dtype,
+        "data": "synthetic: inputs drawn on the device (torch Philox) with the configuration's "
+                "distributions" + (" (x scaled by 4 as logits)" if op in ("softmax", "logsumexp")
+                                   else ""),
+        "config": {"workload": f"{cfg.name}: {op} x{list(cfg.shape)} {cfg.dtype}", "rows": R,
+                   "cols": D, "algorithmic_bytes_per_step": total},
+        "roofline": {"kernel": f"agk_{op if op != 'rmsnorm_jvp' else 'rmsnorm'}_{dom}",
+                     "bound": "hbm", "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": None,
+                     "algorithmic_bytes_per_launch": alg[dom],
+                     "avg_launch_ms": kernels[dom]["avg_ms"]},
+        "kernels": kernels,
+        "cpu_baseline": _rowop_cpu_baseline(op, cfg, cpu_seconds) if cpu_seconds > 0 else None,
+    }
+    return rec
+
+
 def copy_probe(mib, steps):
     """Device-to-device copies of a known size (torch's copy kernel).
 
@@ -350,6 +489,9 @@ def main():
     ap.add_argument("--config", default=DEFAULT_CONFIG,
                     help="c1, c2 (default, the headline), c3, c4a, c4b, c4c, c5 (RMSNorm + "
                          "linear), or 'all'")
+    ap.add_argument("--op", default="rmsnorm",
+                    help="rmsnorm (default: the layer fwd + VJP), or a row op on the same "
+                         "skeleton: " + ", ".join(ROWOPS) + ", or 'rowops' for all four")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline budget in seconds (0 disables it)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -369,6 +511,14 @@ def main():
         sys.exit(2)
 
     from cgadimpl_amd import configs
+    if args.op != "rmsnorm":
+        ops = ROWOPS if args.op == "rowops" else [args.op]
+        names = ["c2", "c3"] if args.config == "all" else [args.config]
+        for name in names:
+            for op in ops:
+                print(json.dumps(run_rowop(op, name, args.steps, args.warmup,
+                                           min(args.cpu_seconds, 5.0))), flush=True)
+        return
     names = list(configs.CONFIGS) + ["c5"] if args.config == "all" else [args.config]
     for name in names:
         if name == "c5":

@@ -66,6 +66,15 @@ struct MaxR {
     __device__ static float op(float a, float b) { return fmaxf(a, b); }
 };
 
+// exp(x) = 2^(x * log2(e)) on the hardware exp2 instruction (v_exp_f32).  The
+// product x*log2(e) is rounded once, so the relative error is about
+// |x| * 2^-24 * ln(2) plus the instruction's 1 ulp: for the shifted logits of
+// softmax and log-sum-exp (x <= 0) the large terms (x near 0) are accurate to
+// ~1 ulp and the error of the small ones is far below them.  -inf gives 0.
+__device__ __forceinline__ float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
 // Reduction over the TPR (<= 64) lanes of a row group with the pairing of
 // group_sum: every pairing is symmetric, so all lanes of the group end with
 // the same bits.
@@ -124,6 +133,11 @@ __device__ __forceinline__ void row_reduce(float (&v)[N],
 //   ncols, inv_cols                  cols and 1 / cols as floats
 //   sum(f), max(f)                   reduce f(a, b) over the row
 //   sum2(f, s0, s1)                  f(a, b, o) fills o[2]; both summed
+//   sum_keep(f)                      sum of f(a, b) over the row, keeping the
+//                                    values where the row is held in registers
+//   store_kept(out, acc, f, g)       out[col] (+)= g(f(a, b)), f's values as
+//                                    kept by the last sum_keep (recomputed by
+//                                    the looped context)
 //   store(out, acc, c0, d0, c1, d1, f)
 //                                    out[col] (+)= f(a, b, u, v), u = c0[col]
 //                                    (d0 when c0 is null), v likewise
@@ -145,6 +159,7 @@ struct Resident {
     int cols;
     float ncols, inv_cols;
     u32x4 a[NV], b[NV];
+    float kept[NV][W];
 
     __device__ Resident(const RowArgs& p, int64_t rows, int cols_, float (*red_)[kSlots])
         : red(red_), cols(cols_) {
@@ -217,6 +232,54 @@ struct Resident {
         reduce<SumR>(r, f);
         s0 = r[0];
         s1 = r[1];
+    }
+
+    template <class F>
+    __device__ __forceinline__ float sum_keep(F f) {
+        float part[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) part[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            if ((t + k * TPR) * W < cols) {
+                float fa[W], fb[W];
+                S::unpack(a[k], fa);
+                if constexpr (NIN == 2) S::unpack(b[k], fb);
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    kept[k][e] = f(fa[e], NIN == 2 ? fb[e] : 0.0f);
+                    part[e] += kept[k][e];
+                }
+            }
+        }
+        float r[1] = {part[0]};
+#pragma unroll
+        for (int e = 1; e < W; ++e) r[0] += part[e];
+        row_reduce<TPR, G, 1, SumR>(r, red, parity);
+        parity ^= 1;
+        return r[0];
+    }
+
+    template <class F, class Gf>
+    __device__ __forceinline__ void store_kept(void* out, int acc, F, Gf g) const {
+        if (!active) return;
+        T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            if (col < cols) {
+                float r[W];
+#pragma unroll
+                for (int e = 0; e < W; ++e) r[e] = g(kept[k][e]);
+                if (acc) {
+                    float old[W];
+                    S::unpack(load16_stream<S>(o + col), old);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) r[e] = old[e] + r[e];
+                }
+                store16_stream<S>(o + col, S::pack(r));
+            }
+        }
     }
 
     template <class F>
@@ -325,6 +388,21 @@ struct Looped {
     }
 
     template <class F>
+    __device__ __forceinline__ float sum_keep(F f) {
+        return sum(f);
+    }
+
+    template <class F, class Gf>
+    __device__ __forceinline__ void store_kept(void* out, int acc, F f, Gf g) const {
+        T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
+        for (int c = threadIdx.x; c < cols; c += kBlock) {
+            float r = g(f(S::get(x + c), NIN == 2 ? S::get(y + c) : 0.0f));
+            if (acc) r = S::get(o + c) + r;
+            S::put(o + c, r);
+        }
+    }
+
+    template <class F>
     __device__ __forceinline__ void store(void* out, int acc, const void* c0, float d0,
                                           const void* c1, float d1, F f) const {
         T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
@@ -415,15 +493,16 @@ struct LnBwd {
     }
 };
 
-// Row softmax (in0 = z, out = y): y = exp(z - m) / sum(exp(z - m)), m = max(z).
+// Row softmax (in0 = z, out = y): y = e * (1 / sum(e)), e = exp(z - m), m = max(z);
+// each exponential is computed once and kept for the store.
 struct SmFwd {
     static constexpr int kIn = 1;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         const float m = c.max([](float z, float) { return z; });
-        const float s = c.sum([=](float z, float) { return expf(z - m); });
-        c.store(p.out, 0, nullptr, 0.0f, nullptr, 0.0f,
-                [=](float z, float, float, float) { return expf(z - m) / s; });
+        auto e = [=](float z, float) { return fast_exp(z - m); };
+        const float inv = 1.0f / c.sum_keep(e);
+        c.store_kept(p.out, 0, e, [=](float v) { return v * inv; });
     }
 };
 
@@ -445,22 +524,22 @@ struct LseFwd {
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         const float m = c.max([](float z, float) { return z; });
-        const float s = c.sum([=](float z, float) { return expf(z - m); });
+        const float s = c.sum([=](float z, float) { return fast_exp(z - m); });
         c.put_val(p.out_row, logf(s) + m);
     }
 };
 
 // Row log-sum-exp backward (in0 = z, rsv = dy, out = dz):
-//   dz (+)= dy * (exp(z - m) / sum(exp(z - m)))
+//   dz (+)= dy * (e * (1 / sum(e))),  e = exp(z - m), computed once
 struct LseBwd {
     static constexpr int kIn = 1;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         const float m = c.max([](float z, float) { return z; });
-        const float s = c.sum([=](float z, float) { return expf(z - m); });
+        auto e = [=](float z, float) { return fast_exp(z - m); };
+        const float inv = 1.0f / c.sum_keep(e);
         const float g = c.row_val(p.rsv);
-        c.store(p.out, p.acc, nullptr, 0.0f, nullptr, 0.0f,
-                [=](float z, float, float, float) { return g * (expf(z - m) / s); });
+        c.store_kept(p.out, p.acc, e, [=](float v) { return g * (v * inv); });
     }
 };
 
@@ -474,7 +553,7 @@ struct LseJvp {
         float s = 0.0f, d = 0.0f;
         c.sum2(
             [=](float z, float t, float (&o)[2]) {
-                const float e = expf(z - m);
+                const float e = fast_exp(z - m);
                 o[0] = e;
                 o[1] = e * t;
             },
