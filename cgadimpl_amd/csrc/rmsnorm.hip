@@ -106,9 +106,9 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
 }
 
 // ---- register-resident backward --------------------------------------------
-// Workgroup b owns rows [b*rpb, min(rows, (b+1)*rpb)); its G groups of TPR
-// lanes take rows round-robin (group q: rows b*rpb + q, + G, + 2G, ...).
-// Per row:
+// The grid has nblk workgroups (one fp32 partial row of dgamma each); group q
+// of workgroup b takes rows b*G + q + k*nblk*G, k = 0, 1, ... (about rows/nblk
+// rows per workgroup).  Per row:
 //   g = dy*gamma, dot = sum(g*x), dx (+)= r*(g - x*(r*r*dot/cols))
 // and, when partials != nullptr, each lane accumulates dy*(x*r) for the
 // columns it owns.  At the end the G groups' sums are added in group order
@@ -145,9 +145,15 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
 
     const int t = threadIdx.x % TPR;
     const int grp = threadIdx.x / TPR;
-    const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
-    const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
-    const int64_t niter = (row_end - row_begin + G - 1) / G;  // uniform in the block
+    // Rows are dealt to the workgroups round-robin, G at a time: workgroup b
+    // takes rows b*G .. b*G+G-1, then the same rows plus gridDim.x*G, and so
+    // on.  At any moment the whole grid works on one contiguous band of rows,
+    // which streams from HBM faster than one run of rows per workgroup.
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * G;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * G;
+    const int64_t row_end = rows;
+    const int64_t niter = first < rows ? (rows - first + stride - 1) / stride : 0;  // uniform
+    (void)rpb;
     const bool want_dg = partials != nullptr;
     const bool want_dx = dx != nullptr;
     const float inv_cols = 1.0f / static_cast<float>(cols);
@@ -165,7 +171,7 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
 #pragma unroll
         for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
 
-    int64_t row = row_begin + grp;
+    int64_t row = first + grp;
     bool active = row < row_end;
     u32x4 xv[NV], dv[NV];
     load_row_slots<S, TPR, NV, G>(x, dy, (active ? row : 0) * static_cast<int64_t>(cols), active,
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
 
     for (int64_t it = 0; it < niter; ++it) {
         // issue the next row's loads first
-        const int64_t nrow = row + G;
+        const int64_t nrow = row + stride;
         const bool nactive = nrow < row_end;
         u32x4 xn[NV], dn[NV];
         float rn = 0.0f;
@@ -501,11 +507,12 @@ inline Plan bwd_plan(int64_t nslot, int64_t rows) {
     return p;
 }
 
-// Backward row blocking: about kTargetBlocks workgroups, each owning a run of
-// consecutive rows and writing one partial row of dgamma (at least
-// kMinRowsPerBlockLarge rows once there are enough rows, so the partial rows
-// stay a small fraction of the traffic).  Depends only on rows, so the dgamma
-// summation order is fixed by the shape.
+// Backward row blocking: about kTargetBlocks workgroups, each summing about
+// rpb rows into one partial row of dgamma (at least kMinRowsPerBlockLarge
+// rows once there are enough rows, so the partial rows stay a small fraction
+// of the traffic).  The resident kernel deals rows to the workgroups
+// round-robin, the looped kernel gives each a run of rpb consecutive rows.
+// Depends only on rows, so the dgamma summation order is fixed by the shape.
 inline int64_t bwd_rows_per_block(int64_t rows) {
     int64_t rpb = (rows + kTargetBlocks - 1) / kTargetBlocks;
     if (rows >= kLargeRows / 8 && rpb < kMinRowsPerBlockLarge) rpb = kMinRowsPerBlockLarge;
