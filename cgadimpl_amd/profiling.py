@@ -14,8 +14,15 @@ scaled by what it reads for the copy kernel, whose true traffic is MIB MiB
 read and MIB MiB written, so the scaled figures are bytes that actually
 crossed the HBM interface.
 
+  MFMA use       rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_VALU_MFMA_BUSY_CYCLES ...
+                 -> per GEMM launch shape: flops (512 per MOPS_BF16 count), TFLOP/s,
+                 and MFMA-busy time (SQ_VALU_MFMA_BUSY_CYCLES summed over the 1024
+                 SIMDs, at the 2.4 GHz peak engine clock) as a share of the kernel time
+
 Usage:
   python -m cgadimpl_amd.profiling trace  <run_kernel_stats.csv> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling mfma <run_counter_collection.csv> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling bench <bench output (JSON lines)> <out.md> "<command>"
   python -m cgadimpl_amd.profiling traffic <fetch_dir> <write_dir> <copy_fetch_dir>
         <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
 """
@@ -153,9 +160,103 @@ def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, 
         fh.write("\n")
 
 
+def write_mfma_summary(counter_csv, out_md, command, simds=1024, clock_ghz=2.4):
+    per = defaultdict(lambda: defaultdict(float))
+    disp = defaultdict(dict)
+    for r in _rows(counter_csv):
+        d = disp[r["Dispatch_Id"]]
+        d["key"] = (short_name(r["Kernel_Name"]), r["Grid_Size"], r["Workgroup_Size"])
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+        d["ns"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+    for d in disp.values():
+        if d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0) <= 0:
+            continue
+        acc = per[d["key"]]
+        acc["n"] += 1
+        for c in ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_LDS_BANK_CONFLICT",
+                  "SQ_LDS_IDX_ACTIVE", "ns"):
+            acc[c] += d.get(c, 0.0)
+    lines = ["# MFMA use of the bf16 GEMM launches (rocprofv3 counters)", "", "Command:", "",
+             "```", command, "```", "",
+             f"flops = 512 x SQ_INSTS_VALU_MFMA_MOPS_BF16; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+             f"({simds} SIMDs x {clock_ghz} GHz) as a share of the kernel's duration in the "
+             "counter run; LDS conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.", "",
+             "| kernel | grid | workgroup | launches | avg us | GFLOP | TFLOP/s | MFMA busy | "
+             "LDS conflict |", "|---|---|---|---|---|---|---|---|---|"]
+    for (name, grid, wg), a in sorted(per.items(), key=lambda kv: (kv[0][0], kv[0][1])):
+        n = a["n"]
+        us = a["ns"] / n / 1e3
+        flops = 512.0 * a["SQ_INSTS_VALU_MFMA_MOPS_BF16"] / n
+        busy_us = a["SQ_VALU_MFMA_BUSY_CYCLES"] / n / simds / (clock_ghz * 1e3)
+        lds = a["SQ_LDS_BANK_CONFLICT"] / a["SQ_LDS_IDX_ACTIVE"] if a["SQ_LDS_IDX_ACTIVE"] else 0.0
+        lines.append(f"| {name} | {grid} | {wg} | {int(n)} | {us:.1f} | {flops / 1e9:.1f} | "
+                     f"{flops / (us * 1e-6) / 1e12:.0f} | {100 * busy_us / us:.1f} % | "
+                     f"{100 * lds:.2f} % |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
+def write_bench_summary(jsonl, out_md, command):
+    """Tables of bench.py's JSON lines (RMSNorm configurations, c5, row ops)."""
+    recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith("{")]
+    lines = ["# bench.py results (MI355X, one GPU)", "", "Command:", "", "```", command, "```", "",
+             "Kernel times are HIP events on the launch stream, averaged over the timed steps; "
+             "GB/s are algorithmic bytes over those times; % is of the 8 TB/s HBM peak.", ""]
+    norm = [r for r in recs if r.get("unit") == "GB/s" and "fwd" in r.get("kernels", {})
+            and r["metric"].startswith("RMSNorm")]
+    if norm:
+        lines += ["## RMSNorm layer fwd + VJP", "",
+                  "| config | fwd+bwd GB/s | % of peak | fwd us | fwd % | bwd+finalize us | bwd % |",
+                  "|---|---|---|---|---|---|---|"]
+        for r in norm:
+            k = r["kernels"]
+            lines.append(f"| {r['config']['workload'].split(':')[0]} {r['config']['rows']}x"
+                         f"{r['config']['cols']} {r['dtype']} | {r['value']:.0f} | "
+                         f"{100 * r['value'] / 8000:.1f} | {1e3 * k['fwd']['avg_ms']:.1f} | "
+                         f"{100 * k['fwd']['frac']:.1f} | {1e3 * k['bwd']['avg_ms']:.1f} | "
+                         f"{100 * k['bwd']['frac']:.1f} |")
+        lines.append("")
+    rows = [r for r in recs if r.get("unit") == "GB/s" and not r["metric"].startswith("RMSNorm")]
+    if rows:
+        lines += ["## Row ops on the same skeleton", "",
+                  "| workload | kernel | us | GB/s | % of peak | CPU oracle GB/s |",
+                  "|---|---|---|---|---|---|"]
+        for r in rows:
+            cpu = r.get("cpu_baseline")
+            for name, k in r["kernels"].items():
+                lines.append(f"| {r['config']['workload']} | {name} | {1e3 * k['avg_ms']:.1f} | "
+                             f"{k['gbs']:.0f} | {100 * k['frac']:.1f} | "
+                             f"{cpu['value'] if cpu else '-'} |")
+        lines.append("")
+    for r in recs:
+        if r.get("unit") != "TFLOP/s":
+            continue
+        st, tb = r["stages_ms"], r["torch_hipblaslt_ms"]
+        fl = r["config"]["gemm_flops_per_step"] / 3
+        lines += ["## RMSNorm + linear layer (c5)", "",
+                  f"M, K, N = {r['config']['M']}, {r['config']['K']}, {r['config']['N']}; "
+                  f"{r['value']} TFLOP/s over the three products "
+                  f"({100 * r['roofline']['frac']:.1f} % of 2.5 PFLOP/s dense bf16); "
+                  f"hipBLASLt on the same operands {r['torch_hipblaslt_tflops']} TFLOP/s.", "",
+                  "| stage | this build us | TFLOP/s | hipBLASLt us | TFLOP/s |", "|---|---|---|---|---|"]
+        for name, ms in st.items():
+            if name in tb:
+                lines.append(f"| {name} | {1e3 * ms:.1f} | {fl / (ms * 1e-3) / 1e12:.0f} | "
+                             f"{1e3 * tb[name]:.1f} | {fl / (tb[name] * 1e-3) / 1e12:.0f} |")
+            else:
+                lines.append(f"| {name} | {1e3 * ms:.1f} | - | - | - |")
+        lines.append("")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
 def main(argv):
     if len(argv) >= 4 and argv[0] == "trace":
         write_trace_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 4 and argv[0] == "bench":
+        write_bench_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 4 and argv[0] == "mfma":
+        write_mfma_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 9 and argv[0] == "traffic":
         write_traffic_summary(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6],
                               argv[7], argv[8])
