@@ -19,13 +19,14 @@
 // L2 into registers while the current step's tiles are multiplied out of LDS,
 // then written to the other half of a double-buffered LDS (one barrier per
 // step).  LDS rows are k-contiguous (each MFMA operand is 8 consecutive k of
-// one row or column, one 16-byte LDS read) and padded by 16 bytes against
-// bank conflicts.  An operand stored with k contiguous in memory ([rows][K])
+// one row or column, one 16-byte LDS read).  An operand stored with k
+// contiguous in memory ([rows][K])
 // is copied in 16-byte chunks; an operand stored with k strided ([K][rows])
 // is read 4 k-rows x 8 values per lane and transposed in registers
 // (v_perm_b32) into 8-byte LDS writes.
 //
-// LDS rows are 128 bytes with XOR-swizzled 16-byte chunks (lds_off), and the
+// LDS rows are 128 bytes, unpadded, with XOR-swizzled 16-byte chunks (lds_off:
+// no bank conflicts, measured with SQ_LDS_BANK_CONFLICT), and the
 // global loads are issued unconditionally at clamped in-range addresses (out
 // of range values are zeroed afterwards), so the compiler can keep the next
 // step's loads in flight across the MFMA block.

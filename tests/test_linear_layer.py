@@ -47,7 +47,8 @@ def test_layer_against_oracle(cuda, M, K, N):
     }
     print(f"[{M}x{K}x{N}] " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
     for k, v in errs.items():
-        assert v <= TOL_BF16, (k, v)
+        # dW is an fp32 product of bf16 operands: only the accumulation order differs
+        assert v <= (1e-5 if k == "dW" else TOL_BF16), (k, v)
 
 
 def test_layer_full_size(cuda):
