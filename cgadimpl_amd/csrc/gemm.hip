@@ -302,6 +302,8 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
                 const int col = n0 + wn * WN + j * 32 + col_l;
                 if (col >= N) continue;
                 float v = acc[i][j][e] * rs;
+                // accumulation rounds the product first (no fused multiply-add)
+                asm volatile("" : "+v"(v));
                 if constexpr (OUT_F32) {
                     float* p = static_cast<float*>(C) + static_cast<int64_t>(row) * ldc + col;
                     *p = accumulate ? *p + v : v;
@@ -409,6 +411,8 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
                 const int col = n0 + wn * WN + j * 32 + col_l;
                 if (col >= N) continue;
                 float v = acc[i][j][e] * rs;
+                // accumulation rounds the product first (no fused multiply-add)
+                asm volatile("" : "+v"(v));
                 if constexpr (OUT_F32) {
                     float* p = static_cast<float*>(C) + static_cast<int64_t>(row) * ldc + col;
                     *p = accumulate ? *p + v : v;

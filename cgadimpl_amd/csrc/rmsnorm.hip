@@ -108,174 +108,232 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
 // ---- register-resident backward --------------------------------------------
 // The grid has nblk workgroups (one fp32 partial row of dgamma each); group q
 // of workgroup b takes rows b*G + q + k*nblk*G, k = 0, 1, ... (about rows/nblk
-// rows per workgroup).  Per row:
+// rows per workgroup).  Rows are dealt round-robin so that at any moment the
+// whole grid works on one contiguous band of rows, which streams from HBM
+// faster than one run of rows per workgroup.  Per row:
 //   g = dy*gamma, dot = sum(g*x), dx (+)= r*(g - x*(r*r*dot/cols))
-// and, when partials != nullptr, each lane accumulates dy*(x*r) for the
-// columns it owns.  At the end the G groups' sums are added in group order
-// (through LDS) into partials[b][*], one fp32 row per workgroup.
-// With PF the loop is software-pipelined: the loads of a group's next row are
-// issued before the current row's reduction, so HBM traffic overlaps the
-// barrier and the arithmetic.  Without PF (wide rows, where the second set of
-// row registers would not fit) each row is loaded when it is processed.
-// gamma is read once per lane and kept in registers.
-template <class S, int TPR, int NV, int G>
-__device__ __forceinline__ void load_row_slots(const typename S::T* __restrict__ x,
-                                               const typename S::T* __restrict__ dy,
-                                               int64_t off, bool active, int cols, int t,
-                                               u32x4 (&xv)[NV], u32x4 (&dv)[NV]) {
+// and each lane accumulates dy*(x*r) for the columns it owns.  At the end the
+// G groups' sums are added in group order (through LDS) into partials[b][*],
+// one fp32 row per workgroup.  gamma is read once and kept in registers.
+//
+// Memory access is branch-free, through buffer resources: a wave's rows of a
+// step get a resource sized to the rows that exist (zero for a step past the
+// last row), and a slot past the row end gets an out-of-range offset.  Such
+// loads return zeros, which add nothing to dot or dgamma, and such stores are
+// dropped.  dx's old values (accumulate) are read the same way, through a
+// resource of size zero when dx is not wanted.  The old values are loaded
+// (and held in registers) only in the accumulating instantiation (ACC).
+//
+// With PF the loop is software-pipelined over two register sets A and B: the
+// loads of step s+2 go into a set as soon as step s has stored from it, so
+// two steps' loads are in flight while a step reduces and stores.  The first
+// pair of steps is peeled so that the loop is entered with the same memory
+// operations outstanding as at its back edge; the compiler then waits for
+// exactly the set being processed and never for the stores just issued or the
+// other set's loads.  Without PF (the widest shape, whose second set would not
+// fit in registers) each step loads and then processes one set.
+template <class S, int NV, bool ACC>
+struct BwdSet {
+    u32x4 xv[NV], dv[NV];   // x, dy
+    u32x4 ov[ACC ? NV : 1]; // old dx (accumulate)
+    float r;
+};
+
+template <class S, int TPR, int NV, int G, bool ACC>
+struct BwdCtx {
+    using T = typename S::T;
+    static constexpr int W = S::kVec;
+    static constexpr int RPW = TPR >= 64 ? 1 : 64 / TPR;  // rows a wave holds per step
+    const T* x;
+    const T* gamma;
+    const float* inv_rms;
+    const T* dy;
+    T* dx;
+    int64_t rows, first, stride;
+    int cols, wgrp0;
+    uint32_t row_bytes, old_bytes, dx_bytes, roff;
+    uint32_t off[NV];
+    float inv_cols;
+
+    // First row of the wave's rows at `step` (clamped into range) and how many exist.
+    __device__ __forceinline__ void wave_rows(int64_t step, int64_t& r0, uint32_t& n) const {
+        const int64_t w0 = first + wgrp0 + step * stride;
+        int64_t cnt = rows - w0;
+        cnt = cnt < 0 ? 0 : (cnt > RPW ? RPW : cnt);
+        r0 = w0 < rows ? w0 : rows - 1;
+        n = static_cast<uint32_t>(cnt);
+    }
+
+    __device__ __forceinline__ void issue(BwdSet<S, NV, ACC>& b, int64_t step) const {
+        int64_t r0;
+        uint32_t n;
+        wave_rows(step, r0, n);
+        const int64_t e0 = r0 * static_cast<int64_t>(cols);
+        const rsrc_t rx = make_rsrc(x + e0, n * row_bytes);
+        const rsrc_t rd = make_rsrc(dy + e0, n * row_bytes);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            b.xv[k] = bload16_stream(rx, off[k]);
+            b.dv[k] = bload16_stream(rd, off[k]);
+        }
+        if constexpr (ACC) {
+            const rsrc_t ro = make_rsrc(dx ? dx + e0 : dx, n * old_bytes);
+#pragma unroll
+            for (int k = 0; k < NV; ++k) b.ov[k] = bload16_stream(ro, off[k]);
+        }
+        b.r = bload_f32(make_rsrc(inv_rms + r0, n * 4u), roff);
+    }
+};
+
+template <class S, int TPR, int NV, int G, bool ACC>
+__device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC>& c,
+                                            BwdSet<S, NV, ACC>& b,
+                                            int64_t step, int parity, const u32x4 (&gv)[NV],
+                                            bool has_gamma, float (&dg)[NV][S::kVec],
+                                            float (*red)[TPR > 64 ? G * (TPR / 64) : 1]) {
     constexpr int W = S::kVec;
+    float part[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) part[e] = 0.0f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const int col = (t + k * TPR) * W;
-        const bool ok = active && col < cols;
-        xv[k] = ok ? load16_stream<S>(x + off + col) : u32x4{0u, 0u, 0u, 0u};
-        dv[k] = ok ? load16_stream<S>(dy + off + col) : u32x4{0u, 0u, 0u, 0u};
+        float fx[W], fd[W];
+        S::unpack(b.xv[k], fx);
+        S::unpack(b.dv[k], fd);
+        if (has_gamma) {
+            float gm[W];
+            S::unpack(gv[k], gm);
+#pragma unroll
+            for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+        }
+#pragma unroll
+        for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int e = 0; e < W; ++e) dot += part[e];
+    dot = row_sum<TPR, G>(dot, red, parity);
+    const float r = b.r;
+    const float s = (r * r * dot) * c.inv_cols;
+    // Re-derive the unpacked values from the raw slots after the reduction
+    // instead of keeping both copies live across it.
+#pragma unroll
+    for (int k = 0; k < NV; ++k) opaque(b.xv[k], b.dv[k]);
+
+    int64_t r0;
+    uint32_t n;
+    c.wave_rows(step, r0, n);
+    const rsrc_t rdx = make_rsrc(c.dx ? c.dx + r0 * static_cast<int64_t>(c.cols) : c.dx,
+                                 n * c.dx_bytes);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        float fx[W], fd[W], gk[W], o[W];
+        S::unpack(b.xv[k], fx);
+        S::unpack(b.dv[k], fd);
+        if (has_gamma) {
+            float gm[W];
+            S::unpack(gv[k], gm);
+#pragma unroll
+            for (int e = 0; e < W; ++e) gk[e] = fd[e] * gm[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < W; ++e) gk[e] = fd[e];
+        }
+#pragma unroll
+        for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
+        if constexpr (ACC) {
+            float old[W];
+            S::unpack(b.ov[k], old);
+#pragma unroll
+            for (int e = 0; e < W; ++e) o[e] = acc_add(old[e], o[e]);
+        }
+        bstore16_stream(rdx, c.off[k], S::pack(o));
+#pragma unroll
+        for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
     }
 }
 
-template <class S, int TPR, int NV, int G, bool PF>
+template <class S, int TPR, int NV, int G, bool PF, bool ACC>
 __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
     typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
     int64_t rpb, int acc_dx) {
+    using T = typename S::T;
     constexpr int W = S::kVec;
+    constexpr int RPW = TPR >= 64 ? 1 : 64 / TPR;
+    (void)acc_dx;  // ACC carries it
     __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
-    extern __shared__ float lds_part[];  // [cols] when G > 1 and partials
+    extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
+    (void)rpb;
 
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int t = threadIdx.x % TPR;
     const int grp = threadIdx.x / TPR;
-    // Rows are dealt to the workgroups round-robin, G at a time: workgroup b
-    // takes rows b*G .. b*G+G-1, then the same rows plus gridDim.x*G, and so
-    // on.  At any moment the whole grid works on one contiguous band of rows,
-    // which streams from HBM faster than one run of rows per workgroup.
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * G;
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * G;
-    const int64_t row_end = rows;
-    const int64_t niter = first < rows ? (rows - first + stride - 1) / stride : 0;  // uniform
-    (void)rpb;
-    const bool want_dg = partials != nullptr;
-    const bool want_dx = dx != nullptr;
-    const float inv_cols = 1.0f / static_cast<float>(cols);
+    const int sub = TPR >= 64 ? 0 : lane / TPR;  // the lane's row among the wave's rows
 
+    BwdCtx<S, TPR, NV, G, ACC> c;
+    c.x = x;
+    c.gamma = gamma;
+    c.inv_rms = inv_rms;
+    c.dy = dy;
+    c.dx = dx;
+    c.rows = rows;
+    c.first = static_cast<int64_t>(blockIdx.x) * G;
+    c.stride = static_cast<int64_t>(gridDim.x) * G;
+    c.cols = cols;
+    c.wgrp0 = TPR >= 64 ? wave / (TPR / 64) : wave * RPW;
+    c.row_bytes = static_cast<uint32_t>(cols) * static_cast<uint32_t>(sizeof(T));
+    c.old_bytes = dx ? c.row_bytes : 0u;
+    c.dx_bytes = dx ? c.row_bytes : 0u;
+    c.roff = static_cast<uint32_t>(sub) * 4u;
+    c.inv_cols = 1.0f / static_cast<float>(cols);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = (t + k * TPR) * W;
+        c.off[k] = col < cols ? (static_cast<uint32_t>(sub) * static_cast<uint32_t>(cols) +
+                                 static_cast<uint32_t>(col)) * static_cast<uint32_t>(sizeof(T))
+                              : kOffOut;
+    }
+    const int64_t steps = c.first < rows ? (rows - c.first + c.stride - 1) / c.stride : 0;
+
+    const bool has_gamma = gamma != nullptr;
     u32x4 gv[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int col = (t + k * TPR) * W;
-        gv[k] = (gamma && col < cols) ? load16<S>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
+        gv[k] = (has_gamma && col < cols) ? load16<S>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
     }
-
     float dg[NV][W];
 #pragma unroll
     for (int k = 0; k < NV; ++k)
 #pragma unroll
         for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
 
-    int64_t row = first + grp;
-    bool active = row < row_end;
-    u32x4 xv[NV], dv[NV];
-    load_row_slots<S, TPR, NV, G>(x, dy, (active ? row : 0) * static_cast<int64_t>(cols), active,
-                                  cols, t, xv, dv);
-    float r = active ? inv_rms[row] : 0.0f;
-
-    for (int64_t it = 0; it < niter; ++it) {
-        // issue the next row's loads first
-        const int64_t nrow = row + stride;
-        const bool nactive = nrow < row_end;
-        u32x4 xn[NV], dn[NV];
-        float rn = 0.0f;
-        if constexpr (PF) {
-            load_row_slots<S, TPR, NV, G>(x, dy,
-                                          (nactive ? nrow : 0) * static_cast<int64_t>(cols),
-                                          nactive, cols, t, xn, dn);
-            rn = nactive ? inv_rms[nrow] : 0.0f;
+    if constexpr (PF) {
+        BwdSet<S, NV, ACC> A, B;
+        c.issue(A, 0);
+        c.issue(B, 1);
+        bwd_process(c, A, 0, 0, gv, has_gamma, dg, red);
+        c.issue(A, 2);
+        bwd_process(c, B, 1, 1, gv, has_gamma, dg, red);
+        c.issue(B, 3);
+        for (int64_t s = 2; s < steps; s += 2) {  // steps is uniform
+            bwd_process(c, A, s, 0, gv, has_gamma, dg, red);
+            c.issue(A, s + 2);
+            bwd_process(c, B, s + 1, 1, gv, has_gamma, dg, red);
+            c.issue(B, s + 3);
         }
-
-        float s = 0.0f;
-        if (want_dx) {  // dot = sum(g*x) is only needed for dx (uniform branch)
-            float part[W];
-#pragma unroll
-            for (int e = 0; e < W; ++e) part[e] = 0.0f;
-#pragma unroll
-            for (int k = 0; k < NV; ++k) {
-                float fx[W], fd[W];
-                S::unpack(xv[k], fx);
-                S::unpack(dv[k], fd);
-                if (gamma) {
-                    float gm[W];
-                    S::unpack(gv[k], gm);
-#pragma unroll
-                    for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
-                }
-#pragma unroll
-                for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
-            }
-            float dot = 0.0f;
-#pragma unroll
-            for (int e = 0; e < W; ++e) dot += part[e];
-            dot = row_sum<TPR, G>(dot, red, static_cast<int>(it & 1));
-            s = (r * r * dot) * inv_cols;
-            // Re-derive the unpacked values from the raw slots after the
-            // reduction instead of keeping both copies live across it.
-#pragma unroll
-            for (int k = 0; k < NV; ++k) opaque(xv[k], dv[k]);
+    } else {
+        BwdSet<S, NV, ACC> A;
+        for (int64_t s = 0; s < steps; ++s) {
+            c.issue(A, s);
+            bwd_process(c, A, s, static_cast<int>(s & 1), gv, has_gamma, dg, red);
         }
-
-        if (active) {
-            const int64_t off = row * static_cast<int64_t>(cols);
-#pragma unroll
-            for (int k = 0; k < NV; ++k) {
-                const int col = (t + k * TPR) * W;
-                if (col < cols) {
-                    float fx[W], fd[W], gk[W];
-                    S::unpack(xv[k], fx);
-                    S::unpack(dv[k], fd);
-                    if (gamma) {
-                        float gm[W];
-                        S::unpack(gv[k], gm);
-#pragma unroll
-                        for (int e = 0; e < W; ++e) gk[e] = fd[e] * gm[e];
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < W; ++e) gk[e] = fd[e];
-                    }
-                    if (want_dx) {
-                        float o[W];
-#pragma unroll
-                        for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
-                        if (acc_dx) {
-                            float old[W];
-                            S::unpack(load16_stream<S>(dx + off + col), old);
-#pragma unroll
-                            for (int e = 0; e < W; ++e) o[e] = old[e] + o[e];
-                        }
-                        store16_stream<S>(dx + off + col, S::pack(o));
-                    }
-                    if (want_dg) {
-#pragma unroll
-                        for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
-                    }
-                }
-            }
-        }
-        if constexpr (PF) {
-#pragma unroll
-            for (int k = 0; k < NV; ++k) {
-                xv[k] = xn[k];
-                dv[k] = dn[k];
-            }
-            r = rn;
-        } else if (it + 1 < niter) {
-            load_row_slots<S, TPR, NV, G>(x, dy,
-                                          (nactive ? nrow : 0) * static_cast<int64_t>(cols),
-                                          nactive, cols, t, xv, dv);
-            r = nactive ? inv_rms[nrow] : 0.0f;
-        }
-        row = nrow;
-        active = nactive;
     }
 
-    if (!want_dg) return;
+    if (!partials) return;
     float* prow = partials + static_cast<int64_t>(blockIdx.x) * cols;
     if constexpr (G == 1) {
 #pragma unroll
@@ -287,23 +345,22 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
             }
         }
     } else {
-        // groups add their sums into one LDS row in group order
-#pragma unroll 1
-        for (int q = 0; q < G; ++q) {
-            if (grp == q) {
+        // each group's sums in its own LDS row; then the G rows are added in
+        // group order, column by column
 #pragma unroll
-                for (int k = 0; k < NV; ++k) {
-                    const int col = (t + k * TPR) * W;
-                    if (col < cols) {
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            if (col < cols) {
 #pragma unroll
-                        for (int e = 0; e < W; ++e)
-                            lds_part[col + e] = q == 0 ? dg[k][e] : lds_part[col + e] + dg[k][e];
-                    }
-                }
+                for (int e = 0; e < W; ++e) lds_part[grp * cols + col + e] = dg[k][e];
             }
-            __syncthreads();
         }
-        for (int c = threadIdx.x; c < cols; c += TPR * G) prow[c] = lds_part[c];
+        __syncthreads();
+        for (int c2 = threadIdx.x; c2 < cols; c2 += TPR * G) {
+            float v = lds_part[c2];
+            for (int q = 1; q < G; ++q) v += lds_part[q * cols + c2];
+            prow[c2] = v;
+        }
     }
 }
 
@@ -369,7 +426,7 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
             if (dx) {
                 const float g = gamma ? d * S::get(gamma + c) : d;
                 float o = r * (g - xv * s);
-                if (acc_dx) o = S::get(dx + off + c) + o;
+                if (acc_dx) o = acc_add(S::get(dx + off + c), o);
                 S::put(dx + off + c, o);
             }
             if (prow) {
@@ -421,7 +478,7 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
             const float g = S::get(gy + off + c);
             if (da) {
                 float o = g * S::get(b + c);
-                if (acc_da) o = S::get(da + off + c) + o;
+                if (acc_da) o = acc_add(S::get(da + off + c), o);
                 S::put(da + off + c, o);
             }
             if (prow) {
@@ -477,18 +534,18 @@ __global__ __launch_bounds__(kBlock) void fill_zero_f32(float* __restrict__ p, i
     if (i < n) p[i] = 0.0f;
 }
 
-// (TPR, NV, G, prefetch).  Prefetching shapes hold two rows' slots per lane;
-// the widest shapes hold one.
+// (TPR, NV, G, prefetch).  Every shape is a 1024-lane workgroup (TPR * G =
+// 1024).  Rows of up to 1024 slots take one slot per lane (TPR = the width
+// rounded up to a power of two, G = 1024 / TPR rows per step); wider rows take
+// 2 or 4 slots per lane on 1024 lanes.  Narrow rows (TPR <= 64) and the
+// widest shape process one register set at a time; the others prefetch.
+// Measured on MI355X (c2 f32 [65536, 4096], c3 bf16 [65536, 8192],
+// c4a [7161, 5120], c4b [1048576, 128]) against 256- to 1024-lane and
+// 1- to 4-slot alternatives, with and without prefetch.
 #define AGK_BWD_SHAPES(X)                                                                  \
-    X(1, 1, 256, 1) X(2, 1, 128, 1) X(4, 1, 64, 1) X(8, 1, 32, 1) X(16, 1, 16, 1)          \
-    X(32, 1, 32, 1) X(64, 1, 4, 1) X(64, 2, 4, 1) X(128, 2, 2, 1) X(256, 2, 2, 1)         \
-    X(512, 2, 2, 1) X(1024, 2, 1, 1) X(1024, 4, 1, 0)
-
-constexpr Shape3 kBwdShapes[] = {
-#define AGK_X(a, b, c, d) {a, b, c},
-    AGK_BWD_SHAPES(AGK_X)
-#undef AGK_X
-};
+    X(1, 1, 1024, 0) X(2, 1, 512, 0) X(4, 1, 256, 0) X(8, 1, 128, 0) X(16, 1, 64, 0)       \
+    X(32, 1, 32, 0) X(64, 1, 16, 0) X(128, 1, 8, 1) X(256, 1, 4, 1) X(512, 1, 2, 1)       \
+    X(1024, 1, 1, 1) X(1024, 2, 1, 1) X(1024, 4, 1, 0)
 
 // Backward shapes that are not built for a storage type: bf16 unpacks to
 // twice the floats per slot, and the widest shape would spill registers.
@@ -496,23 +553,48 @@ template <class S>
 constexpr bool bwd_shape_enabled(int tpr, int nv) {
     return !(std::is_same<S, BF16>::value && tpr == 1024 && nv == 4);
 }
+// Whether a shape prefetches for a storage type: bf16 with two slots per lane
+// holds one register set (two would spill).
+template <class S>
+constexpr bool bwd_prefetch(int nv, int pf) {
+    return pf != 0 && !(std::is_same<S, BF16>::value && nv >= 2);
+}
 
 template <class S>
-inline Plan bwd_plan(int64_t nslot, int64_t rows) {
-    Plan p = pick_plan(kBwdShapes, nslot, 2, 1024, 4);
-    // many rows: two rows per workgroup where that shape exists
-    if (p.tpr >= 256 && rows > kLargeRows && has_shape(kBwdShapes, Plan{p.tpr, p.nv, 2}))
-        p.g = 2;
-    if (p.tpr != 0 && !bwd_shape_enabled<S>(p.tpr, p.nv)) return Plan{};
+inline Plan bwd_plan(int64_t nslot) {
+    Plan p;
+    if (nslot <= 1024) {
+        p.tpr = pow2_at_least(nslot);
+        p.nv = 1;
+    } else if (nslot <= 2048) {
+        p.tpr = 1024;
+        p.nv = 2;
+    } else if (nslot <= 4096) {
+        p.tpr = 1024;
+        p.nv = 4;
+    } else {
+        return Plan{};
+    }
+    p.g = 1024 / p.tpr;
+    if (!bwd_shape_enabled<S>(p.tpr, p.nv)) return Plan{};
     return p;
 }
 
-// Backward row blocking: about kTargetBlocks workgroups, each summing about
-// rpb rows into one partial row of dgamma (at least kMinRowsPerBlockLarge
-// rows once there are enough rows, so the partial rows stay a small fraction
-// of the traffic).  The resident kernel deals rows to the workgroups
-// round-robin, the looped kernel gives each a run of rpb consecutive rows.
+// Row blocking of the resident backward: min(kBwdBlocks, rows) workgroups,
+// about one per CU, so the whole grid runs in one generation and finishes
+// together; workgroup b takes rows b*G + q + k*nblk*G (round-robin, so the
+// grid streams through one band of rows at a time) and writes one partial
+// row of dgamma.  A grid of more workgroups than fit at once finishes in a
+// ragged last generation, measured 3-15 % slower at the configurations above.
 // Depends only on rows, so the dgamma summation order is fixed by the shape.
+constexpr int64_t kBwdBlocks = 256;
+inline int64_t bwd_resident_blocks(int64_t rows) { return rows < kBwdBlocks ? rows : kBwdBlocks; }
+
+// Row blocking of the looped backward (unaligned or too-wide rows): about
+// kTargetBlocks workgroups, each summing a run of rpb consecutive rows into
+// one partial row (at least kMinRowsPerBlockLarge rows once there are enough
+// rows, so the partial rows stay a small fraction of the traffic).  Never
+// fewer blocks than the resident blocking, so it also sizes the workspace.
 inline int64_t bwd_rows_per_block(int64_t rows) {
     int64_t rpb = (rows + kTargetBlocks - 1) / kTargetBlocks;
     if (rows >= kLargeRows / 8 && rpb < kMinRowsPerBlockLarge) rpb = kMinRowsPerBlockLarge;
@@ -560,30 +642,22 @@ int launch_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_
     return launch_fwd_plan<S>(p, x, gamma, y, inv_rms, rows, cols, eps, st);
 }
 
-template <class S>
-int launch_bwd_plan(const Plan& p, int64_t rpb, const void* x, const void* gamma,
-                    const float* inv_rms, const void* dy, void* dx, float* partials,
-                    int64_t rows, int cols, int accumulate, hipStream_t st) {
+template <class S, bool ACC>
+int launch_bwd_resident(const Plan& p, int64_t nblk, const void* x, const void* gamma,
+                        const float* inv_rms, const void* dy, void* dx, float* partials,
+                        int64_t rows, int cols, hipStream_t st) {
     using T = typename S::T;
     const T* xp = static_cast<const T*>(x);
     const T* gp = static_cast<const T*>(gamma);
     const T* dyp = static_cast<const T*>(dy);
     T* dxp = static_cast<T*>(dx);
-    const int64_t nblk = (rows + rpb - 1) / rpb;
-    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
-    if (p.tpr == 0) {
-        hipLaunchKernelGGL(rms_bwd_looped<S>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0,
-                           st, xp, gp, inv_rms, dyp, dxp, partials, rows, cols, rpb, accumulate);
-        return check_launch();
-    }
-    const size_t lds = (partials && p.g > 1) ? static_cast<size_t>(cols) * 4 : 0;
+    const size_t lds = (partials && p.g > 1) ? static_cast<size_t>(p.g) * cols * 4 : 0;
 #define AGK_X(a, b, c, d)                                                                  \
     if constexpr (bwd_shape_enabled<S>(a, b)) {                                            \
         if (p.tpr == a && p.nv == b && p.g == c) {                                         \
-            hipLaunchKernelGGL((rms_bwd_resident<S, a, b, c, d>),                          \
+            hipLaunchKernelGGL((rms_bwd_resident<S, a, b, c, bwd_prefetch<S>(b, d), ACC>), \
                                dim3(static_cast<unsigned>(nblk)), dim3(a * c), lds, st, xp, \
-                               gp, inv_rms, dyp, dxp, partials, rows, cols, rpb,            \
-                               accumulate);                                                \
+                               gp, inv_rms, dyp, dxp, partials, rows, cols, 0, ACC);        \
             return check_launch();                                                         \
         }                                                                                  \
     }
@@ -592,18 +666,47 @@ int launch_bwd_plan(const Plan& p, int64_t rpb, const void* x, const void* gamma
     return AGK_EINVAL;
 }
 
+// The shape and row blocking a backward call of these sizes takes; nblk is
+// the number of dgamma partial rows it writes.
+template <class S>
+inline Plan bwd_plan_for(const void* x, const void* gamma, const void* dy, const void* dx,
+                         int64_t rows, int cols, int64_t& nblk, int64_t& rpb) {
+    const bool vec = (cols % S::kVec) == 0 && aligned16(x) && aligned16(dy) &&
+                     (dx == nullptr || aligned16(dx)) && (gamma == nullptr || aligned16(gamma));
+    Plan p;
+    if (vec) p = bwd_plan<S>(cols / S::kVec);
+    // the per-group partial rows must fit in LDS
+    if (p.tpr != 0 && p.g > 1 && static_cast<int64_t>(p.g) * cols * 4 > 64 * 1024) p = Plan{};
+    if (p.tpr != 0) {
+        nblk = bwd_resident_blocks(rows);
+        rpb = (rows + nblk - 1) / nblk;
+    } else {
+        rpb = bwd_rows_per_block(rows);
+        nblk = bwd_num_blocks(rows);
+    }
+    return p;
+}
+
 template <class S>
 int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
                void* dx, float* partials, int64_t rows, int cols, int accumulate,
-               hipStream_t st) {
-    const bool vec = (cols % S::kVec) == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) &&
-                     (gamma == nullptr || aligned16(gamma));
-    Plan p;
-    if (vec) p = bwd_plan<S>(cols / S::kVec, rows);
-    // the G-row combine buffer must fit in LDS
-    if (p.tpr != 0 && p.g > 1 && static_cast<int64_t>(cols) * 4 > 64 * 1024) p = Plan{};
-    return launch_bwd_plan<S>(p, bwd_rows_per_block(rows), x, gamma, inv_rms, dy, dx, partials,
-                              rows, cols, accumulate, st);
+               hipStream_t st, int64_t& nblk) {
+    using T = typename S::T;
+    int64_t rpb = 0;
+    const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    if (p.tpr == 0) {
+        hipLaunchKernelGGL(rms_bwd_looped<S>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0,
+                           st, static_cast<const T*>(x), static_cast<const T*>(gamma), inv_rms,
+                           static_cast<const T*>(dy), static_cast<T*>(dx), partials, rows, cols,
+                           rpb, accumulate);
+        return check_launch();
+    }
+    if (accumulate && dx)
+        return launch_bwd_resident<S, true>(p, nblk, x, gamma, inv_rms, dy, dx, partials, rows,
+                                            cols, st);
+    return launch_bwd_resident<S, false>(p, nblk, x, gamma, inv_rms, dy, dx, partials, rows,
+                                         cols, st);
 }
 
 inline int launch_finalize(const float* partials, float* dgamma, int64_t nblk, int cols,
@@ -672,11 +775,13 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
         partials = static_cast<float*>(workspace);
     }
     const int c = static_cast<int>(cols);
+    int64_t nblk = 0;
     int rc = dtype == AGK_F32
-                 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st)
-                 : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st);
+                 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st, nblk)
+                 : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st,
+                                    nblk);
     if (rc != AGK_OK || !dgamma) return rc;
-    return launch_finalize(partials, dgamma, bwd_num_blocks(rows), c, acc_dg, st);
+    return launch_finalize(partials, dgamma, nblk, c, acc_dg, st);
 }
 
 int agk_mul_rowbcast_fwd(const void* a, const void* b, void* y, int64_t rows, int64_t cols,
@@ -760,19 +865,21 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
     if (!plan) return AGK_EINVAL;
     const int w = dtype == AGK_F32 ? F32::kVec : BF16::kVec;
     Plan p;
-    if (cols > 0 && cols % w == 0) {
-        const int64_t nslot = cols / w;
-        if (!backward)
-            p = fwd_plan(nslot, rows);
-        else
-            p = dtype == AGK_F32 ? bwd_plan<F32>(nslot, rows) : bwd_plan<BF16>(nslot, rows);
-        if (backward && p.tpr != 0 && p.g > 1 && cols * 4 > 64 * 1024) p = Plan{};
+    int64_t nblk = 0, rpb = 0;
+    if (!backward) {
+        if (cols > 0 && cols % w == 0) p = fwd_plan(cols / w, rows);
+    } else if (cols > 0 && cols <= 0x7fffffffLL) {
+        // aligned stand-in pointers: the plan depends only on alignment
+        const void* a = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+        const int c = static_cast<int>(cols);
+        p = dtype == AGK_F32 ? bwd_plan_for<F32>(a, a, a, a, rows, c, nblk, rpb)
+                             : bwd_plan_for<BF16>(a, a, a, a, rows, c, nblk, rpb);
     }
     plan[0] = p.tpr;
     plan[1] = p.nv;
     plan[2] = p.g;
-    plan[3] = backward ? static_cast<int32_t>(bwd_rows_per_block(rows)) : 0;
-    plan[4] = backward ? static_cast<int32_t>(bwd_num_blocks(rows)) : 0;
+    plan[3] = static_cast<int32_t>(rpb);
+    plan[4] = static_cast<int32_t>(nblk);
     return AGK_OK;
 }
 

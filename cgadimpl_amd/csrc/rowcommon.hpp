@@ -78,6 +78,14 @@ struct BF16 {
     }
 };
 
+// `old + v` for gradient accumulation (`grad += g`): g is rounded on its own
+// first, then the sum.  The empty asm keeps the compiler from fusing the
+// multiply that produced v into this add, which would round only once.
+__device__ __forceinline__ float acc_add(float old, float v) {
+    asm volatile("" : "+v"(v));
+    return old + v;
+}
+
 // Makes v opaque to the optimiser at this point, so values derived from it
 // earlier are recomputed afterwards rather than held in registers.
 __device__ __forceinline__ void opaque(u32x4& a, u32x4& b) {
@@ -100,6 +108,33 @@ __device__ __forceinline__ u32x4 load16_stream(const typename S::T* p) {
 template <class S>
 __device__ __forceinline__ void store16_stream(typename S::T* p, u32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// ---- buffer resources ---------------------------------------------------------
+// A raw buffer resource (stride 0, no swizzle) over `bytes` bytes at `base`.
+// The hardware range-checks every access against `bytes`: a load at or past
+// the end returns zero and a store there is dropped, without touching memory.
+// Kernels use this to make tails and inactive rows branch-free: the same
+// instructions run on every path, so the compiler's s_waitcnt placement can
+// count exactly which loads are still in flight.  Base and size live in
+// scalar registers, so they must be wave-uniform.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;      // gfx9 family: 32-bit data format, raw
+constexpr int kCachePolicyNT = 2;           // non-temporal
+constexpr uint32_t kOffOut = 0x80000000u;   // an offset past any buffer this code makes
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 bload16_stream(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCachePolicyNT);
+}
+__device__ __forceinline__ void bstore16_stream(rsrc_t r, uint32_t off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCachePolicyNT);
+}
+__device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
 // ---- reductions -------------------------------------------------------------

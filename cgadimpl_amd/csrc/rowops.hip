@@ -275,7 +275,7 @@ struct Resident {
                     float old[W];
                     S::unpack(load16_stream<S>(o + col), old);
 #pragma unroll
-                    for (int e = 0; e < W; ++e) r[e] = old[e] + r[e];
+                    for (int e = 0; e < W; ++e) r[e] = acc_add(old[e], r[e]);
                 }
                 store16_stream<S>(o + col, S::pack(r));
             }
@@ -312,7 +312,7 @@ struct Resident {
                     float old[W];
                     S::unpack(load16_stream<S>(o + col), old);
 #pragma unroll
-                    for (int e = 0; e < W; ++e) r[e] = old[e] + r[e];
+                    for (int e = 0; e < W; ++e) r[e] = acc_add(old[e], r[e]);
                 }
                 store16_stream<S>(o + col, S::pack(r));
             }
@@ -397,7 +397,7 @@ struct Looped {
         T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
         for (int c = threadIdx.x; c < cols; c += kBlock) {
             float r = g(f(S::get(x + c), NIN == 2 ? S::get(y + c) : 0.0f));
-            if (acc) r = S::get(o + c) + r;
+            if (acc) r = acc_add(S::get(o + c), r);
             S::put(o + c, r);
         }
     }
@@ -411,7 +411,7 @@ struct Looped {
         for (int c = threadIdx.x; c < cols; c += kBlock) {
             float r = f(S::get(x + c), NIN == 2 ? S::get(y + c) : 0.0f, u ? S::get(u + c) : d0,
                         v ? S::get(v + c) : d1);
-            if (acc) r = S::get(o + c) + r;
+            if (acc) r = acc_add(S::get(o + c), r);
             S::put(o + c, r);
         }
     }

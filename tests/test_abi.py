@@ -80,10 +80,20 @@ def test_workspace_bytes_rule():
     assert ws(1048576, 128) == 1024 * 128 * 4
     assert ws(7161, 5120) == 1023 * 5120 * 4
     assert ws(2048, 64) == 512 * 64 * 4
-    for rows in (1, 2, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 65535, 10 ** 7):
+    for rows in (1, 2, 255, 256, 257, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097,
+                 65535, 10 ** 7):
         assert ws(rows, 8) == _blocks(rows) * 8 * 4, rows
-        plan = agk.launch_plan(rows, 8, agk.AGK_F32, True)
-        assert plan["nblk"] == _blocks(rows)
+        # resident kernels: min(256, rows) workgroups (one partial row each),
+        # never more than the workspace holds
+        for dt in (agk.AGK_F32, agk.AGK_BF16):
+            plan = agk.launch_plan(rows, 8 * 16, dt, True)
+            assert plan["tpr"] > 0
+            assert plan["nblk"] == min(256, rows) <= _blocks(rows)
+            assert plan["rpb"] == -(-rows // plan["nblk"])
+        # the looped kernel (cols not a whole number of 16-byte slots): runs of
+        # rpb consecutive rows, one partial row per run
+        plan = agk.launch_plan(rows, 9, agk.AGK_F32, True)
+        assert plan["tpr"] == 0 and plan["nblk"] == _blocks(rows)
         assert (plan["nblk"] - 1) * plan["rpb"] < rows <= plan["nblk"] * plan["rpb"]
     assert lib.agk_mul_rowbcast_bwd_workspace_bytes(65536, 4096) == ws(65536, 4096)
 
@@ -99,9 +109,12 @@ def test_launch_plans_are_well_formed():
             assert tpr * nv * w >= cols
             assert nv == 1 or tpr * nv * w // 2 < cols or tpr == 64, (tpr, nv, cols)
             assert 64 <= tpr * g <= 1024 and (tpr & (tpr - 1)) == 0
+            if direction == "bwd":
+                assert tpr * g == 1024
     # the headline shapes
     assert agk.launch_plan(65536, 4096, agk.AGK_F32, False)["tpr"] == 512
-    assert agk.launch_plan(65536, 4096, agk.AGK_F32, True)["g"] == 2
+    bwd = agk.launch_plan(65536, 4096, agk.AGK_F32, True)
+    assert (bwd["tpr"], bwd["nv"], bwd["g"], bwd["nblk"]) == (1024, 1, 1, 256)
     # rows that are not whole 16-byte slots take the looped kernels
     assert agk.launch_plan(64, 4098, agk.AGK_F32, False)["tpr"] == 0
     assert agk.launch_plan(64, 4100, agk.AGK_BF16, True)["tpr"] == 0
