@@ -35,6 +35,62 @@ HBM_PEAK_GBS = 8000.0
 DEFAULT_CONFIG = "c2"
 
 
+class TimingEvent:
+    """A HIP event for timing only, recorded on the stream the kernels run on.
+
+    Created with hipEventDisableSystemFence: recording it adds no system-scope
+    fence (cache writeback and invalidate), which with torch.cuda.Event leaves
+    the GPU idle for ~5 us around every record and would count against the
+    step.  It comes from the HIP runtime torch itself loaded (opening the same
+    file returns the loaded object), so torch's stream handles are valid for
+    it.  Same interface as torch.cuda.Event: record(stream), elapsed_time(end).
+    """
+
+    _hip = None
+    _DISABLE_SYSTEM_FENCE = 0x20000000
+
+    @classmethod
+    def _runtime(cls):
+        if cls._hip is None:
+            import ctypes
+
+            import torch
+            hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib",
+                                           "libamdhip64.so"))
+            hip.hipEventCreateWithFlags.argtypes = [ctypes.c_void_p, ctypes.c_uint]
+            hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            hip.hipEventElapsedTime.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_void_p]
+            hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            cls._hip = hip
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self._ctypes = ctypes
+        self._ev = ctypes.c_void_p()
+        rc = self._runtime().hipEventCreateWithFlags(ctypes.byref(self._ev),
+                                                     self._DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self, stream):
+        rc = self._runtime().hipEventRecord(self._ev, self._ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end):
+        ms = self._ctypes.c_float()
+        rc = self._runtime().hipEventElapsedTime(self._ctypes.byref(ms), self._ev, end._ev)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        if self._hip is not None and self._ev:
+            self._hip.hipEventDestroy(self._ev)
+
+
 def _device_inputs(cfg, dev, seed):
     import torch
     gen = torch.Generator(device=dev)
@@ -141,7 +197,7 @@ def run(cfg_name, steps, warmup, cpu_seconds):
         step(i)
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    events = [[TimingEvent() for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -269,7 +325,7 @@ def run_c5(steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(steps)]
+    events = [[TimingEvent() for _ in range(7)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
         step(events[i])
@@ -282,7 +338,7 @@ def run_c5(steps, warmup):
         for _ in range(2):
             f()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a, b = TimingEvent(), TimingEvent()
         a.record(stream)
         for _ in range(reps):
             f()
@@ -422,7 +478,7 @@ def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
             f()
     torch.cuda.synchronize()
     n = len(launches)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
+    ev = [[TimingEvent() for _ in range(n + 1)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
         ev[i][0].record(stream)

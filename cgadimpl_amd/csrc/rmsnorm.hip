@@ -124,14 +124,14 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
 // resource of size zero when dx is not wanted.  The old values are loaded
 // (and held in registers) only in the accumulating instantiation (ACC).
 //
-// With PF the loop is software-pipelined over two register sets A and B: the
-// loads of step s+2 go into a set as soon as step s has stored from it, so
-// two steps' loads are in flight while a step reduces and stores.  The first
-// pair of steps is peeled so that the loop is entered with the same memory
+// With NSET > 1 register sets the loop is software-pipelined: the loads of
+// step s+NSET go into a set as soon as step s has stored from it, so NSET
+// steps' loads are in flight while a step reduces and stores.  The first NSET
+// steps are peeled so that the loop is entered with the same memory
 // operations outstanding as at its back edge; the compiler then waits for
 // exactly the set being processed and never for the stores just issued or the
-// other set's loads.  Without PF (the widest shape, whose second set would not
-// fit in registers) each step loads and then processes one set.
+// other sets' loads.  With one set (narrow rows, and wide shapes whose second
+// set would not fit in registers) each step loads and then processes.
 template <class S, int NV, bool ACC>
 struct BwdSet {
     u32x4 xv[NV], dv[NV];   // x, dy
@@ -253,19 +253,85 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC>& c,
     }
 }
 
-template <class S, int TPR, int NV, int G, bool PF, bool ACC>
+// Runs steps 0 .. steps-1 of c's row sequence with NSET (1 or 2) register
+// sets, adding each lane's dgamma terms into dg.
+template <class S, int TPR, int NV, int G, int NSET, bool ACC>
+__device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC>& c, int64_t steps,
+                                            const u32x4 (&gv)[NV], bool has_gamma,
+                                            float (&dg)[NV][S::kVec],
+                                            float (*red)[TPR > 64 ? G * (TPR / 64) : 1]) {
+    if constexpr (NSET == 1) {
+        BwdSet<S, NV, ACC> A;
+        for (int64_t s = 0; s < steps; ++s) {
+            c.issue(A, s);
+            bwd_process(c, A, s, static_cast<int>(s & 1), gv, has_gamma, dg, red);
+        }
+    } else {
+        static_assert(NSET == 2, "one or two register sets");
+        BwdSet<S, NV, ACC> A, B;
+        c.issue(A, 0);
+        c.issue(B, 1);
+        bwd_process(c, A, 0, 0, gv, has_gamma, dg, red);
+        c.issue(A, 2);
+        bwd_process(c, B, 1, 1, gv, has_gamma, dg, red);
+        c.issue(B, 3);
+        for (int64_t s = 2; s < steps; s += 2) {  // steps is uniform
+            bwd_process(c, A, s, 0, gv, has_gamma, dg, red);
+            c.issue(A, s + 2);
+            bwd_process(c, B, s + 1, 1, gv, has_gamma, dg, red);
+            c.issue(B, s + 3);
+        }
+    }
+}
+
+// Writes one partial row of dgamma: the G groups' sums (each group's in its
+// own LDS row) added in group order, column by column.  Ends with a barrier
+// so the LDS rows can be written again.
+template <class S, int TPR, int NV, int G>
+__device__ __forceinline__ void bwd_write_partial(float* __restrict__ prow, int cols, int t,
+                                                  int grp, const float (&dg)[NV][S::kVec],
+                                                  float* lds_part) {
+    constexpr int W = S::kVec;
+    if constexpr (G == 1) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            if (col < cols) {
+#pragma unroll
+                for (int e = 0; e < W; ++e) prow[col + e] = dg[k][e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            if (col < cols) {
+#pragma unroll
+                for (int e = 0; e < W; ++e) lds_part[grp * cols + col + e] = dg[k][e];
+            }
+        }
+        __syncthreads();
+        for (int c2 = threadIdx.x; c2 < cols; c2 += TPR * G) {
+            float v = lds_part[c2];
+            for (int q = 1; q < G; ++q) v += lds_part[q * cols + c2];
+            prow[c2] = v;
+        }
+        __syncthreads();
+    }
+}
+
+// Rows are dealt round-robin to the gridDim.x workgroups; workgroup b writes
+// partial row b.
+template <class S, int TPR, int NV, int G, int NSET, bool ACC>
 __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
-    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
-    int64_t rpb, int acc_dx) {
+    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols) {
     using T = typename S::T;
     constexpr int W = S::kVec;
     constexpr int RPW = TPR >= 64 ? 1 : 64 / TPR;
-    (void)acc_dx;  // ACC carries it
     __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
     extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
-    (void)rpb;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -296,7 +362,6 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
                                  static_cast<uint32_t>(col)) * static_cast<uint32_t>(sizeof(T))
                               : kOffOut;
     }
-    const int64_t steps = c.first < rows ? (rows - c.first + c.stride - 1) / c.stride : 0;
 
     const bool has_gamma = gamma != nullptr;
     u32x4 gv[NV];
@@ -311,57 +376,11 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
 #pragma unroll
         for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
 
-    if constexpr (PF) {
-        BwdSet<S, NV, ACC> A, B;
-        c.issue(A, 0);
-        c.issue(B, 1);
-        bwd_process(c, A, 0, 0, gv, has_gamma, dg, red);
-        c.issue(A, 2);
-        bwd_process(c, B, 1, 1, gv, has_gamma, dg, red);
-        c.issue(B, 3);
-        for (int64_t s = 2; s < steps; s += 2) {  // steps is uniform
-            bwd_process(c, A, s, 0, gv, has_gamma, dg, red);
-            c.issue(A, s + 2);
-            bwd_process(c, B, s + 1, 1, gv, has_gamma, dg, red);
-            c.issue(B, s + 3);
-        }
-    } else {
-        BwdSet<S, NV, ACC> A;
-        for (int64_t s = 0; s < steps; ++s) {
-            c.issue(A, s);
-            bwd_process(c, A, s, static_cast<int>(s & 1), gv, has_gamma, dg, red);
-        }
-    }
-
-    if (!partials) return;
-    float* prow = partials + static_cast<int64_t>(blockIdx.x) * cols;
-    if constexpr (G == 1) {
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int col = (t + k * TPR) * W;
-            if (col < cols) {
-#pragma unroll
-                for (int e = 0; e < W; ++e) prow[col + e] = dg[k][e];
-            }
-        }
-    } else {
-        // each group's sums in its own LDS row; then the G rows are added in
-        // group order, column by column
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int col = (t + k * TPR) * W;
-            if (col < cols) {
-#pragma unroll
-                for (int e = 0; e < W; ++e) lds_part[grp * cols + col + e] = dg[k][e];
-            }
-        }
-        __syncthreads();
-        for (int c2 = threadIdx.x; c2 < cols; c2 += TPR * G) {
-            float v = lds_part[c2];
-            for (int q = 1; q < G; ++q) v += lds_part[q * cols + c2];
-            prow[c2] = v;
-        }
-    }
+    const int64_t steps = c.first < rows ? (rows - c.first + c.stride - 1) / c.stride : 0;
+    bwd_segment<S, TPR, NV, G, NSET, ACC>(c, steps, gv, has_gamma, dg, red);
+    if (partials)
+        bwd_write_partial<S, TPR, NV, G>(partials + static_cast<int64_t>(blockIdx.x) * cols, cols,
+                                         t, grp, dg, lds_part);
 }
 
 // ---- looped kernels (any alignment, any width) --------------------------------
@@ -534,7 +553,7 @@ __global__ __launch_bounds__(kBlock) void fill_zero_f32(float* __restrict__ p, i
     if (i < n) p[i] = 0.0f;
 }
 
-// (TPR, NV, G, prefetch).  Every shape is a 1024-lane workgroup (TPR * G =
+// (TPR, NV, G, register sets).  Every shape is a 1024-lane workgroup (TPR * G =
 // 1024).  Rows of up to 1024 slots take one slot per lane (TPR = the width
 // rounded up to a power of two, G = 1024 / TPR rows per step); wider rows take
 // 2 or 4 slots per lane on 1024 lanes.  Narrow rows (TPR <= 64) and the
@@ -543,9 +562,9 @@ __global__ __launch_bounds__(kBlock) void fill_zero_f32(float* __restrict__ p, i
 // c4a [7161, 5120], c4b [1048576, 128]) against 256- to 1024-lane and
 // 1- to 4-slot alternatives, with and without prefetch.
 #define AGK_BWD_SHAPES(X)                                                                  \
-    X(1, 1, 1024, 0) X(2, 1, 512, 0) X(4, 1, 256, 0) X(8, 1, 128, 0) X(16, 1, 64, 0)       \
-    X(32, 1, 32, 0) X(64, 1, 16, 0) X(128, 1, 8, 1) X(256, 1, 4, 1) X(512, 1, 2, 1)       \
-    X(1024, 1, 1, 1) X(1024, 2, 1, 1) X(1024, 4, 1, 0)
+    X(1, 1, 1024, 1) X(2, 1, 512, 1) X(4, 1, 256, 1) X(8, 1, 128, 1) X(16, 1, 64, 1)       \
+    X(32, 1, 32, 1) X(64, 1, 16, 1) X(128, 1, 8, 2) X(256, 1, 4, 2) X(512, 1, 2, 2)       \
+    X(1024, 1, 1, 2) X(1024, 2, 1, 2) X(1024, 4, 1, 1)
 
 // Backward shapes that are not built for a storage type: bf16 unpacks to
 // twice the floats per slot, and the widest shape would spill registers.
@@ -553,11 +572,11 @@ template <class S>
 constexpr bool bwd_shape_enabled(int tpr, int nv) {
     return !(std::is_same<S, BF16>::value && tpr == 1024 && nv == 4);
 }
-// Whether a shape prefetches for a storage type: bf16 with two slots per lane
-// holds one register set (two would spill).
+// Register sets of a shape for a storage type: bf16 with two slots per lane
+// holds one (two would spill).
 template <class S>
-constexpr bool bwd_prefetch(int nv, int pf) {
-    return pf != 0 && !(std::is_same<S, BF16>::value && nv >= 2);
+constexpr int bwd_sets(int nv, int sets) {
+    return (std::is_same<S, BF16>::value && nv >= 2) ? 1 : sets;
 }
 
 template <class S>
@@ -655,9 +674,9 @@ int launch_bwd_resident(const Plan& p, int64_t nblk, const void* x, const void* 
 #define AGK_X(a, b, c, d)                                                                  \
     if constexpr (bwd_shape_enabled<S>(a, b)) {                                            \
         if (p.tpr == a && p.nv == b && p.g == c) {                                         \
-            hipLaunchKernelGGL((rms_bwd_resident<S, a, b, c, bwd_prefetch<S>(b, d), ACC>), \
+            hipLaunchKernelGGL((rms_bwd_resident<S, a, b, c, bwd_sets<S>(b, d), ACC>),     \
                                dim3(static_cast<unsigned>(nblk)), dim3(a * c), lds, st, xp, \
-                               gp, inv_rms, dyp, dxp, partials, rows, cols, 0, ACC);        \
+                               gp, inv_rms, dyp, dxp, partials, rows, cols);                \
             return check_launch();                                                         \
         }                                                                                  \
     }
