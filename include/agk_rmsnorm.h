@@ -80,11 +80,12 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
                     agk_stream_t stream);
 
 /* Bytes of workspace agk_rmsnorm_bwd needs for these sizes: fp32 dgamma
- * partials, one row of cols floats per row block, where a row block is
- *   rpb = ceil(rows / 1024) rows, at least 4 once rows >= 2048,
- * so nblk = ceil(rows / rpb) and the size is nblk * cols * 4 bytes.  Depends
- * only on rows and cols, never on the device, so the dgamma summation order
- * is the same everywhere.                                                    */
+ * partials, one row of cols floats per workgroup.  The size is nblk * cols * 4
+ * bytes with nblk = ceil(rows / rpb), rpb = ceil(rows / 1024) rows (at least
+ * 4 once rows >= 2048): the count the looped kernel (unaligned or too-wide
+ * rows) uses, never fewer than the min(256, rows) rows the register-resident
+ * kernel uses.  Depends only on rows and cols, never on the device, so the
+ * dgamma summation order is the same everywhere.                            */
 size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
 /* Backward (VJP) of the RMSNorm layer.
@@ -167,7 +168,8 @@ int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_ds
  * library picks for a forward (backward = 0) or backward (backward != 0)
  * call of these sizes with 16-byte aligned pointers.  plan[5] receives
  *   {lanes per row, 16-byte slots per lane, rows per workgroup,
- *    rows per dgamma block (backward), dgamma blocks (backward)};
+ *    rows per dgamma partial row (backward; ceil(rows / partial rows)),
+ *    dgamma partial rows (backward)};
  * lanes per row == 0 means the looped kernel (rows that are not a whole
  * number of 16-byte slots, or too wide to keep in registers).  Used by the
  * tests to run every reachable shape.                                        */
