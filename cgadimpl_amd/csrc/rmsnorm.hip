@@ -26,8 +26,9 @@
 // is not a multiple of the vector width, or that are too wide for registers
 // take a looped kernel that re-reads the row (from cache) instead.
 //
-// dgamma is deterministic: each workgroup of the backward owns a contiguous
-// block of rows and sums dy*xhat for them in a fixed order into one row of
+// dgamma is deterministic: each workgroup of the backward owns a fixed set of
+// rows (dealt round-robin in the register-resident kernel, a contiguous run in
+// the looped one) and sums dy*xhat for them in a fixed order into one row of
 // fp32 partials; dgamma_finalize then sums the partial rows in a fixed order
 // in fp64.  No floating-point atomics are used anywhere.
 

@@ -19,12 +19,11 @@ namespace agk {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBlock = 256;          // threads per workgroup (TPR <= 256)
-constexpr int kTargetBlocks = 1024;  // backward row blocks (sets partial rows)
+constexpr int kBlock = 256;          // threads per workgroup of the looped kernels
+constexpr int kTargetBlocks = 1024;  // looped backward: row blocks (partial rows)
 constexpr int kMinRowsPerBlockLarge = 4;     // once rows >= kLargeRows / 8
-constexpr int64_t kLargeRows = 16384;        // plan switch: more rows than this
-                                             // keep enough workgroups with fewer
-                                             // lanes in flight per row
+constexpr int64_t kLargeRows = 16384;        // forward plan switch: more rows than
+                                             // this take fewer slots per lane
 
 // ---- storage types --------------------------------------------------------
 
