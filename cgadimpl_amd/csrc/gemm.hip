@@ -12,6 +12,12 @@
 // (kscale multiplies the A operand as it is staged, rounding to bf16 as a
 // stored h would be; rowscale multiplies the fp32 accumulator.)
 //
+// Two kernels share the tile shape.  With a workspace (and K a multiple of
+// 64) operands are first made k-contiguous and the product runs on the
+// direct-to-LDS kernel further below, which stages through four 32-deep LDS
+// stages without registers; otherwise the register-staged kernel described
+// here runs.
+//
 // Kernel shape.  A workgroup of 512 lanes (8 waves, 2 along M x 4 along N)
 // computes a 256 x 256 tile of C; each wave owns 128 x 64 of it as 4 x 2
 // v_mfma_f32_32x32x16_bf16 accumulators (128 fp32 registers per lane).  K is
@@ -317,80 +323,14 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
     }
 }
 
-// ---- direct-to-LDS kernel: both operands k-contiguous, K a multiple of BK ----
-// Staging without registers: global_load_lds_dwordx4 writes lane l's 16 bytes
-// to LDS at (wave-uniform base) + 16 * l (checked on MI355X), so one wave
-// instruction fills 8 LDS rows of 128 bytes; each lane fetches the global
-// chunk that belongs at its position of the swizzled layout (lds_off).  The
-// two stages are separate LDS objects and the k loop is unrolled by two, so
-// the compiler can tell the stage being multiplied from the one being filled
-// and does not wait for the DMA before the fragment reads.  Rows past M or N
-// are fetched from the last valid row (never stored); K must be a multiple
-// of BK, since a partial k-tile would multiply stale data.
+// ---- direct-to-LDS kernel: both operands k-contiguous, K a multiple of 64 ----
+// Staging without registers: buffer_load_dwordx4 ... lds writes lane l's 16
+// bytes to LDS at (wave-uniform base) + 16 * l, so one wave instruction fills
+// a contiguous kilobyte of LDS; each lane fetches the global chunk that belongs
+// at its position of the swizzled layout.  Rows past M or N are fetched from
+// the last valid row (never stored).  The epilogue store_c writes the wave's
+// 128 x 64 block of C.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// Per-lane element offsets (from the tile's first row) of the 4 A and 4 B
-// chunks a lane fetches per k-tile; the tile bases are wave-uniform.
-struct DirectStage {
-    const uint16_t* a_base;
-    const uint16_t* b_base;
-    uint32_t oa[4];
-    uint32_t ob[4];
-};
-
-__device__ __forceinline__ void direct_issue(const DirectStage& d, uint16_t* stage, int k0,
-                                             int wave) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(d.a_base + d.oa[j] + k0,
-                                         (lds_ptr_t)(stage + (wave * 32 + j * 8) * kStride), 16,
-                                         0, 0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(d.b_base + d.ob[j] + k0,
-                                         (lds_ptr_t)(stage + (BM + wave * 32 + j * 8) * kStride),
-                                         16, 0, 0);
-}
-
-// Instruction classes for __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
-
-// One BK-deep step of the wave's 128 x 64 tile out of one LDS stage.  The six
-// fragment reads of k-substep s + 1 are issued together ahead of the eight
-// MFMAs of substep s (scheduling groups), so they are in flight while the
-// matrix cores work and the two substeps' fragments stay in separate
-// registers.
-__device__ __forceinline__ void mfma_tile(const uint16_t* cur, f32x16 (&acc)[TM][TN], int wm,
-                                          int wn, int frow, int fk) {
-    bf16x8 af[2][TM], bf[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) af[0][i] = lds_frag(cur, wm * WM + i * 32 + frow, fk);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bf[0][j] = lds_frag(cur + BM * kStride, wn * WN + j * 32 + frow, fk);
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-        const int c = s & 1;
-        const bool next = s + 1 < BK / 16;
-        if (next) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[c ^ 1][i] = lds_frag(cur, wm * WM + i * 32 + frow, (s + 1) * 16 + fk);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bf[c ^ 1][j] = lds_frag(cur + BM * kStride, wn * WN + j * 32 + frow,
-                                        (s + 1) * 16 + fk);
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bf[c][j], acc[i][j],
-                                                                    0, 0, 0);
-        if (next) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, TM + TN, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, TM * TN, 0);
-    }
-}
 
 template <bool OUT_F32>
 __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
@@ -426,13 +366,104 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
     }
 }
 
+// The k loop walks 32-deep tiles through four LDS stages (the tile is the same
+// 256 x 256 over 8 waves of 128 x 64 as above): the loads of tile kt + 3
+// are issued as tile kt starts, so each tile's loads have three tiles' time to
+// land and a wave only ever waits for the oldest tile in flight
+// (s_waitcnt vmcnt(8): two younger tiles of 4 loads each stay outstanding).
+// With two 64-deep stages a tile's loads had one tile's time, and waves spent
+// over a third of their cycles waiting on them (SQ_WAIT_ANY, MI355X).
+// LDS rows are 64 bytes (four 16-byte k-chunks), XOR-swizzled by row / 4 so
+// that the eight rows a 16-byte fragment read serves at a time hit distinct
+// banks.  The four stages are separate LDS objects and the loop is unrolled by
+// four, so the compiler can tell the stage being read from those being filled.
+constexpr int BK2 = 32;
+constexpr int kStride2 = BK2;                       // bf16 per LDS row (64 bytes)
+constexpr int kStageElems2 = (BM + BN) * kStride2;  // 32 KiB per stage
+
+__device__ __forceinline__ int lds_off2(int row, int c) {
+    return row * kStride2 + ((c ^ ((row >> 2) & 3)) << 3);
+}
+
+// Per-wave staging state: buffer resources over the tile's A and B rows (base
+// and size in scalar registers) and each lane's byte offsets within them; the
+// k position is the scalar offset of each load.
+// Four direct loads per wave per tile: rows wave * 32 + j * 16 .. + 15 of A and
+// of B (one instruction fills 16 LDS rows of 64 bytes).
+struct DeepStage {
+    __amdgpu_buffer_rsrc_t ra, rb;
+    uint32_t oa[2], ob[2];
+};
+
+__device__ __forceinline__ void deep_issue(const DeepStage& d, uint16_t* stage, int k0, int wave) {
+    const int sk = k0 * 2;  // bytes
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            d.ra, (lds_ptr_t)(stage + (wave * 32 + j * 16) * kStride2), 16, d.oa[j], sk, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            d.rb, (lds_ptr_t)(stage + (BM + wave * 32 + j * 16) * kStride2), 16, d.ob[j], sk, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 lds_frag2(const uint16_t* lds, int row, int c) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + lds_off2(row, c)));
+}
+
+// The two 16-deep substeps of one 32-deep tile (fragments of substep 1 are read
+// while substep 0 multiplies).
+__device__ __forceinline__ void mfma_tile2(const uint16_t* cur, f32x16 (&acc)[TM][TN], int wm,
+                                           int wn, int frow, int fc) {
+    bf16x8 af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[s][i] = lds_frag2(cur, wm * WM + i * 32 + frow, 2 * s + fc);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            bf[s][j] = lds_frag2(cur + BM * kStride2, wn * WN + j * 32 + frow, 2 * s + fc);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bf[s][j], acc[i][j],
+                                                                    0, 0, 0);
+}
+
+// One tile step: wait until this wave's loads of tile kt have landed (the two
+// younger tiles stay in flight), make every wave's loads visible, start the
+// loads of tile kt + 3 into the stage tile kt - 1 used, multiply tile kt.
+// Steps run in groups of four; past the last tile a step re-loads the last
+// tile into a stage nothing reads again (so every step has the same loads in
+// flight and the same wait) and skips the multiply.
+__device__ __forceinline__ void deep_step(const DeepStage& d, const uint16_t* cur, uint16_t* fill,
+                                          int kt, int nk, f32x16 (&acc)[TM][TN], int wm, int wn,
+                                          int frow, int fc, int wave) {
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    // A bare barrier: __syncthreads()'s fence would wait for every load in
+    // flight (vmcnt(0)), the younger tiles' included.  Every wave's reads of
+    // the stage refilled below were consumed by its MFMAs of the previous step.
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    deep_issue(d, fill, (kt + 3 < nk ? kt + 3 : nk - 1) * BK2, wave);
+    if (kt < nk) mfma_tile2(cur, acc, wm, wn, frow, fc);  // uniform
+    // keep this step's MFMAs (and their fragment registers) inside the step
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <bool OUT_F32>
-__global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
+__global__ __launch_bounds__(kThreads) void gemm_nt_deep_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
     int accumulate, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint16_t stage0[kStageElems];
-    __shared__ __attribute__((aligned(16))) uint16_t stage1[kStageElems];
+    __shared__ __attribute__((aligned(16))) uint16_t st0[kStageElems2];
+    __shared__ __attribute__((aligned(16))) uint16_t st1[kStageElems2];
+    __shared__ __attribute__((aligned(16))) uint16_t st2[kStageElems2];
+    __shared__ __attribute__((aligned(16))) uint16_t st3[kStageElems2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -444,17 +475,24 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
-    DirectStage d;
-    d.a_base = A + static_cast<int64_t>(m0) * lda;
-    d.b_base = B + static_cast<int64_t>(n0) * ldb;
+    // rows past M or N are fetched from the last valid row (never stored)
+    const int rows_a = M - m0 < BM ? M - m0 : BM;
+    const int rows_b = N - n0 < BN ? N - n0 : BN;
+    DeepStage d;
+    d.ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(A + static_cast<int64_t>(m0) * lda), static_cast<short>(0),
+        static_cast<int>(((rows_a - 1) * lda + K) * 2), 0x00020000);
+    d.rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(B + static_cast<int64_t>(n0) * ldb), static_cast<short>(0),
+        static_cast<int>(((rows_b - 1) * ldb + K) * 2), 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = wave * 32 + j * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 7);
-        const int ra = m0 + row < M ? row : M - 1 - m0;
-        const int rb = n0 + row < N ? row : N - 1 - n0;
-        d.oa[j] = static_cast<uint32_t>(ra) * static_cast<uint32_t>(lda) + c * 8;
-        d.ob[j] = static_cast<uint32_t>(rb) * static_cast<uint32_t>(ldb) + c * 8;
+    for (int j = 0; j < 2; ++j) {
+        const int row = wave * 32 + j * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((row >> 2) & 3);
+        const int ra = row < rows_a ? row : rows_a - 1;
+        const int rb = row < rows_b ? row : rows_b - 1;
+        d.oa[j] = (static_cast<uint32_t>(ra) * static_cast<uint32_t>(lda) + c * 8) * 2;
+        d.ob[j] = (static_cast<uint32_t>(rb) * static_cast<uint32_t>(ldb) + c * 8) * 2;
     }
 
     f32x16 acc[TM][TN];
@@ -465,20 +503,20 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int nk = K / BK;
+    const int nk = K / BK2;  // >= 2: K is a positive multiple of 64
     const int frow = lane & 31;
-    const int fk = (lane >> 5) * 8;
-    direct_issue(d, stage0, 0, wave);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        uint16_t* cur = (kt & 1) ? stage1 : stage0;
-        uint16_t* nxt = (kt & 1) ? stage0 : stage1;
-        if (kt + 1 < nk) direct_issue(d, nxt, (kt + 1) * BK, wave);
-        mfma_tile(cur, acc, wm, wn, frow, fk);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+    const int fc = lane >> 5;
+    deep_issue(d, st0, 0, wave);
+    deep_issue(d, st1, BK2, wave);
+    deep_issue(d, st2, (nk > 2 ? 2 : nk - 1) * BK2, wave);
+    for (int kt = 0; kt < nk; kt += 4) {
+        deep_step(d, st0, st3, kt, nk, acc, wm, wn, frow, fc, wave);
+        deep_step(d, st1, st0, kt + 1, nk, acc, wm, wn, frow, fc, wave);
+        deep_step(d, st2, st1, kt + 2, nk, acc, wm, wn, frow, fc, wave);
+        deep_step(d, st3, st2, kt + 3, nk, acc, wm, wn, frow, fc, wave);
     }
+    // no load may still be writing this workgroup's LDS when it exits
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     store_c<OUT_F32>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale, accumulate);
 }
 
@@ -657,15 +695,17 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
             b_nt = ws;
             ldb_nt = K;
         }
-        if (lda_nt < (1 << 23) && ldb_nt < (1 << 23)) {
+        // the buffer resources span a tile's 256 rows in 31-bit byte offsets
+        auto fits = [&](int64_t ld) { return (255 * ld + K) * 2 <= 0x7fffffffLL; };
+        if (fits(lda_nt) && fits(ldb_nt)) {
             const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
             if (c_dtype == AGK_F32)
-                hipLaunchKernelGGL(gemm_nt_direct_kernel<true>, dim3(tiles_m * tiles_n),
+                hipLaunchKernelGGL(gemm_nt_deep_kernel<true>, dim3(tiles_m * tiles_n),
                                    dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
                                    lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
                                    n, k, rowscale, acc, tiles_m, tiles_n);
             else
-                hipLaunchKernelGGL(gemm_nt_direct_kernel<false>, dim3(tiles_m * tiles_n),
+                hipLaunchKernelGGL(gemm_nt_deep_kernel<false>, dim3(tiles_m * tiles_n),
                                    dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
                                    lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
                                    n, k, rowscale, acc, tiles_m, tiles_n);
