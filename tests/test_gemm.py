@@ -51,8 +51,10 @@ def _ref(a, b, ta, tb, ks, rs):
     return C
 
 
+# K / 32 = 2, 4, 6, 10, 14, 32 on the direct-to-LDS kernel (K a multiple of 64):
+# every remainder of its four-stage loop, with ragged M and N tiles.
 CASES = [(256, 256, 64), (264, 520, 72), (8, 8, 8), (1000, 1032, 520), (512, 768, 1024),
-         (136, 264, 192)]
+         (136, 264, 192), (264, 520, 128), (520, 264, 320), (200, 136, 448)]
 
 
 @pytest.mark.gpu
