@@ -7,7 +7,8 @@ Outputs (in-tree, git-ignored, shipped with the source tree):
   cgadimpl_amd/lib/libag.so            the C++ graph layer (ag::Value, rms, rms_norm,
                                        mul, backward) over the C ABI (host C++)
   cgadimpl_amd/lib/test_ag_layer       its GPU test program (tests/cpp/)
-  cgadimpl_amd/lib/rmsnorm_layer_bench the layer benchmark through the graph layer
+  cgadimpl_amd/lib/rmsnorm_layer       the RMSNorm layer benchmark through the graph layer
+                                       (cgadimpl_amd/ag/bench/rmsnorm_layer.cpp)
 
 Every HIP translation unit is compiled for gfx950 only, with packed-fp32
 instruction generation disabled.
@@ -122,6 +123,7 @@ def build_all(verbose: bool = True) -> list[str]:
     outs.append(ag_library())
     outs.append(ag_program("test_ag_layer", os.path.join(ROOT, "tests", "cpp",
                                                          "test_ag_layer.cpp")))
+    outs.append(ag_program("rmsnorm_layer", os.path.join(AG_DIR, "bench", "rmsnorm_layer.cpp")))
     if verbose:
         for o in outs:
             print(f"built {os.path.relpath(o, ROOT)}")

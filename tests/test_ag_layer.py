@@ -24,10 +24,11 @@ from tolerances import TOL_BF16, TOL_F32, dx_rel_err, row_rel_err, vec_rel_err
 
 PROGRAM = os.path.join(LIB_DIR, "test_ag_layer")
 LIBAG = os.path.join(LIB_DIR, "libag.so")
+LAYER_BENCH = os.path.join(LIB_DIR, "rmsnorm_layer")
 
 
 def test_graph_layer_links_and_exports():
-    for path in (PROGRAM, LIBAG):
+    for path in (PROGRAM, LIBAG, LAYER_BENCH):
         assert os.path.exists(path), "build first: python -c 'import __graft_entry__ as g; g.build()'"
         ldd = subprocess.run(["ldd", path], capture_output=True, text=True, check=True).stdout
         assert "not found" not in ldd, ldd
@@ -112,3 +113,23 @@ def test_graph_layer_against_oracle(cuda, name, shape):
         assert np.array_equal(load("dx_fused"), load("dx_fused_par"))
         assert np.array_equal(load("dg_fused", np.float32, (cols,)),
                               load("dg_fused_par", np.float32, (cols,)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_layer_benchmark_program_runs(cuda, dtype):
+    """The RMSNorm layer benchmark through the graph layer (the program the
+    reference's empty Benchmark/RMSNormLayer.cpp stands for) runs both the
+    fused layer and the unfused rms(x) * gamma graph and reports them."""
+    import json
+    proc = subprocess.run([LAYER_BENCH, "4", "128", "512", "3", "1", dtype, "both"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
+    lines = [json.loads(ln) for ln in proc.stdout.splitlines() if ln.startswith("{")]
+    assert [ln["path"].split(",")[1].split()[0] for ln in lines] == ["nn::RMSNorm", "ag::rms(x)"]
+    for ln in lines:
+        assert ln["shape"] == [4, 128, 512] and ln["dtype"] == dtype and ln["steps"] == 3
+        assert ln["ms_per_step"] > 0 and ln["gbs"] > 0
+    bad = subprocess.run([LAYER_BENCH, "4", "128", "512", "0"], capture_output=True, text=True,
+                         timeout=60)
+    assert bad.returncode == 1 and "usage" in bad.stderr
