@@ -98,9 +98,9 @@ int main(int argc, char** argv) {
 
         const double s = dt == ag::Dtype::Float32 ? 4.0 : 2.0;
         const double bytes = 5.0 * R * D * s + 2.0 * D * s + 2.0 * R * 4 + D * 4.0;
-        for (const std::string m : {std::string("fused"), std::string("unfused")}) {
+        for (const char* m : {"fused", "unfused"}) {
             if (mode != "both" && mode != m) continue;
-            const bool fused = m == "fused";
+            const bool fused = std::strcmp(m, "fused") == 0;
             auto step = [&]() {
                 ag::Value xv = ag::make_tensor(x, "x");
                 ag::Value y = fused ? layer(xv) : ag::rms(xv) * layer.gamma;

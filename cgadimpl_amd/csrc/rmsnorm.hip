@@ -140,7 +140,9 @@ struct BwdSet {
     float r;
 };
 
-template <class S, int TPR, int NV, int G, bool ACC>
+// MUL: the broadcast multiply's VJP on the same skeleton (x = a, gamma = b,
+// dy = gy): da = gy*b, db += gy*a, no row reduction and no inv_rms (r = 1).
+template <class S, int TPR, int NV, int G, bool ACC, bool MUL>
 struct BwdCtx {
     using T = typename S::T;
     static constexpr int W = S::kVec;
@@ -152,7 +154,7 @@ struct BwdCtx {
     T* dx;
     int64_t rows, first, stride;
     int cols, wgrp0;
-    uint32_t row_bytes, old_bytes, dx_bytes, roff;
+    uint32_t row_bytes, x_bytes, old_bytes, dx_bytes, roff;
     uint32_t off[NV];
     float inv_cols;
 
@@ -170,7 +172,7 @@ struct BwdCtx {
         uint32_t n;
         wave_rows(step, r0, n);
         const int64_t e0 = r0 * static_cast<int64_t>(cols);
-        const rsrc_t rx = make_rsrc(x + e0, n * row_bytes);
+        const rsrc_t rx = make_rsrc(x ? x + e0 : x, n * x_bytes);
         const rsrc_t rd = make_rsrc(dy + e0, n * row_bytes);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
@@ -182,44 +184,53 @@ struct BwdCtx {
 #pragma unroll
             for (int k = 0; k < NV; ++k) b.ov[k] = bload16_stream(ro, off[k]);
         }
-        b.r = bload_f32(make_rsrc(inv_rms + r0, n * 4u), roff);
+        if constexpr (MUL)
+            b.r = 1.0f;
+        else
+            b.r = bload_f32(make_rsrc(inv_rms + r0, n * 4u), roff);
     }
 };
 
-template <class S, int TPR, int NV, int G, bool ACC>
-__device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC>& c,
+template <class S, int TPR, int NV, int G, bool ACC, bool MUL>
+__device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL>& c,
                                             BwdSet<S, NV, ACC>& b,
                                             int64_t step, int parity, const u32x4 (&gv)[NV],
                                             bool has_gamma, float (&dg)[NV][S::kVec],
                                             float (*red)[TPR > 64 ? G * (TPR / 64) : 1]) {
     constexpr int W = S::kVec;
-    float part[W];
-#pragma unroll
-    for (int e = 0; e < W; ++e) part[e] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        float fx[W], fd[W];
-        S::unpack(b.xv[k], fx);
-        S::unpack(b.dv[k], fd);
-        if (has_gamma) {
-            float gm[W];
-            S::unpack(gv[k], gm);
-#pragma unroll
-            for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
-        }
-#pragma unroll
-        for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
-    }
-    float dot = 0.0f;
-#pragma unroll
-    for (int e = 0; e < W; ++e) dot += part[e];
-    dot = row_sum<TPR, G>(dot, red, parity);
     const float r = b.r;
-    const float s = (r * r * dot) * c.inv_cols;
-    // Re-derive the unpacked values from the raw slots after the reduction
-    // instead of keeping both copies live across it.
+    float s = 0.0f;
+    if constexpr (!MUL) {
+        float part[W];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) opaque(b.xv[k], b.dv[k]);
+        for (int e = 0; e < W; ++e) part[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fx[W], fd[W];
+            S::unpack(b.xv[k], fx);
+            S::unpack(b.dv[k], fd);
+            if (has_gamma) {
+                float gm[W];
+                S::unpack(gv[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < W; ++e) dot += part[e];
+        dot = row_sum<TPR, G>(dot, red, parity);
+        s = (r * r * dot) * c.inv_cols;
+        // Re-derive the unpacked values from the raw slots after the reduction
+        // instead of keeping both copies live across it.
+#pragma unroll
+        for (int k = 0; k < NV; ++k) opaque(b.xv[k], b.dv[k]);
+    } else {
+        (void)parity;
+        (void)red;
+    }
 
     int64_t r0;
     uint32_t n;
@@ -240,8 +251,13 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC>& c,
 #pragma unroll
             for (int e = 0; e < W; ++e) gk[e] = fd[e];
         }
+        if constexpr (MUL) {
 #pragma unroll
-        for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
+            for (int e = 0; e < W; ++e) o[e] = gk[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
+        }
         if constexpr (ACC) {
             float old[W];
             S::unpack(b.ov[k], old);
@@ -249,15 +265,20 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC>& c,
             for (int e = 0; e < W; ++e) o[e] = acc_add(old[e], o[e]);
         }
         bstore16_stream(rdx, c.off[k], S::pack(o));
+        if constexpr (MUL) {
 #pragma unroll
-        for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
+            for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * fx[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
+        }
     }
 }
 
 // Runs steps 0 .. steps-1 of c's row sequence with NSET (1 or 2) register
 // sets, adding each lane's dgamma terms into dg.
-template <class S, int TPR, int NV, int G, int NSET, bool ACC>
-__device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC>& c, int64_t steps,
+template <class S, int TPR, int NV, int G, int NSET, bool ACC, bool MUL>
+__device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC, MUL>& c, int64_t steps,
                                             const u32x4 (&gv)[NV], bool has_gamma,
                                             float (&dg)[NV][S::kVec],
                                             float (*red)[TPR > 64 ? G * (TPR / 64) : 1]) {
@@ -323,16 +344,15 @@ __device__ __forceinline__ void bwd_write_partial(float* __restrict__ prow, int 
 
 // Rows are dealt round-robin to the gridDim.x workgroups; workgroup b writes
 // partial row b.
-template <class S, int TPR, int NV, int G, int NSET, bool ACC>
-__global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
+template <class S, int TPR, int NV, int G, int NSET, bool ACC, bool MUL>
+__device__ __forceinline__ void bwd_resident_body(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
-    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols) {
+    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
+    float (*red)[TPR > 64 ? G * (TPR / 64) : 1], float* lds_part) {
     using T = typename S::T;
     constexpr int W = S::kVec;
     constexpr int RPW = TPR >= 64 ? 1 : 64 / TPR;
-    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
-    extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -340,7 +360,7 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     const int grp = threadIdx.x / TPR;
     const int sub = TPR >= 64 ? 0 : lane / TPR;  // the lane's row among the wave's rows
 
-    BwdCtx<S, TPR, NV, G, ACC> c;
+    BwdCtx<S, TPR, NV, G, ACC, MUL> c;
     c.x = x;
     c.gamma = gamma;
     c.inv_rms = inv_rms;
@@ -352,6 +372,7 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     c.cols = cols;
     c.wgrp0 = TPR >= 64 ? wave / (TPR / 64) : wave * RPW;
     c.row_bytes = static_cast<uint32_t>(cols) * static_cast<uint32_t>(sizeof(T));
+    c.x_bytes = x ? c.row_bytes : 0u;
     c.old_bytes = dx ? c.row_bytes : 0u;
     c.dx_bytes = dx ? c.row_bytes : 0u;
     c.roff = static_cast<uint32_t>(sub) * 4u;
@@ -378,10 +399,35 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
         for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
 
     const int64_t steps = c.first < rows ? (rows - c.first + c.stride - 1) / c.stride : 0;
-    bwd_segment<S, TPR, NV, G, NSET, ACC>(c, steps, gv, has_gamma, dg, red);
+    bwd_segment<S, TPR, NV, G, NSET, ACC, MUL>(c, steps, gv, has_gamma, dg, red);
     if (partials)
         bwd_write_partial<S, TPR, NV, G>(partials + static_cast<int64_t>(blockIdx.x) * cols, cols,
                                          t, grp, dg, lds_part);
+}
+
+// RMSNorm backward: dx (+)= r*(dy*gamma - x*r*r*dot/cols), dgamma partials.
+template <class S, int TPR, int NV, int G, int NSET, bool ACC>
+__global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
+    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols) {
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
+    extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
+    bwd_resident_body<S, TPR, NV, G, NSET, ACC, false>(x, gamma, inv_rms, dy, dx, partials, rows,
+                                                       cols, red, lds_part);
+}
+
+// Broadcast multiply backward (vjp_Mul with reduce_for_broadcast): da (+)=
+// gy*b, db partials of gy*a.  a, b, da may be null when not needed.
+template <class S, int TPR, int NV, int G, int NSET, bool ACC>
+__global__ __launch_bounds__(TPR * G) void mul_rowbcast_bwd_resident(
+    const typename S::T* __restrict__ a, const typename S::T* __restrict__ b,
+    const typename S::T* __restrict__ gy, typename S::T* __restrict__ da,
+    float* __restrict__ partials, int64_t rows, int cols) {
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
+    extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
+    bwd_resident_body<S, TPR, NV, G, NSET, ACC, true>(a, b, nullptr, gy, da, partials, rows, cols,
+                                                      red, lds_part);
 }
 
 // ---- looped kernels (any alignment, any width) --------------------------------
@@ -686,6 +732,31 @@ int launch_bwd_resident(const Plan& p, int64_t nblk, const void* x, const void* 
     return AGK_EINVAL;
 }
 
+template <class S, bool ACC>
+int launch_mul_bwd_resident(const Plan& p, int64_t nblk, const void* a, const void* b,
+                            const void* gy, void* da, float* partials, int64_t rows, int cols,
+                            hipStream_t st) {
+    using T = typename S::T;
+    const T* ap = static_cast<const T*>(a);
+    const T* bp = static_cast<const T*>(b);
+    const T* gp = static_cast<const T*>(gy);
+    T* dap = static_cast<T*>(da);
+    const size_t lds = (partials && p.g > 1) ? static_cast<size_t>(p.g) * cols * 4 : 0;
+#define AGK_X(a_, b_, c_, d_)                                                              \
+    if constexpr (bwd_shape_enabled<S>(a_, b_)) {                                          \
+        if (p.tpr == a_ && p.nv == b_ && p.g == c_) {                                      \
+            hipLaunchKernelGGL((mul_rowbcast_bwd_resident<S, a_, b_, c_,                   \
+                                                          bwd_sets<S>(b_, d_), ACC>),      \
+                               dim3(static_cast<unsigned>(nblk)), dim3(a_ * c_), lds, st,   \
+                               ap, bp, gp, dap, partials, rows, cols);                     \
+            return check_launch();                                                         \
+        }                                                                                  \
+    }
+    AGK_BWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
 // The shape and row blocking a backward call of these sizes takes; nblk is
 // the number of dgamma partial rows it writes.
 template <class S>
@@ -857,10 +928,25 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
         if (!workspace || workspace_bytes < need) return AGK_EWORKSPACE;
         partials = static_cast<float*>(workspace);
     }
-    const int64_t rpb = bwd_rows_per_block(rows);
-    const int64_t nblk = bwd_num_blocks(rows);
-    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
     const int c = static_cast<int>(cols);
+    int64_t nblk = 0, rpb = 0;
+    const Plan p = dtype == AGK_F32 ? bwd_plan_for<F32>(a, b, gy, da, rows, c, nblk, rpb)
+                                    : bwd_plan_for<BF16>(a, b, gy, da, rows, c, nblk, rpb);
+    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    if (p.tpr != 0) {  // register-resident, as the RMSNorm backward
+        const bool acc = acc_da && da;
+        int rc = dtype == AGK_F32
+                     ? (acc ? launch_mul_bwd_resident<F32, true>(p, nblk, a, b, gy, da, partials,
+                                                                 rows, c, st)
+                            : launch_mul_bwd_resident<F32, false>(p, nblk, a, b, gy, da, partials,
+                                                                  rows, c, st))
+                     : (acc ? launch_mul_bwd_resident<BF16, true>(p, nblk, a, b, gy, da,
+                                                                  partials, rows, c, st)
+                            : launch_mul_bwd_resident<BF16, false>(p, nblk, a, b, gy, da,
+                                                                   partials, rows, c, st));
+        if (rc != AGK_OK || !db) return rc;
+        return launch_finalize(partials, db, nblk, c, acc_db, st);
+    }
     if (dtype == AGK_F32) {
         hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, dim3(static_cast<unsigned>(nblk)),
                            dim3(kBlock), 0, st, static_cast<const float*>(gy),
