@@ -369,7 +369,7 @@ def run_c5(steps, warmup):
         "data": "synthetic: x~N(0,1), gamma~U(0.5,1.5), W~N(0,0.02^2), dy~N(0,1) (torch Philox)",
         "config": {"workload": "c5: rms_norm(x) * gamma -> matmul W, fwd + VJP (dx, dgamma, dW)",
                    "M": M, "K": K, "N": N, "gemm_flops_per_step": 3 * flops},
-        "roofline": {"kernel": "gemm_nt_deep (3 products)", "bound": "mfma",
+        "roofline": {"kernel": "gemm_nt_direct (3 products)", "bound": "mfma",
                      "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": None},

@@ -14,9 +14,9 @@
 //
 // Two kernels share the tile shape.  With a workspace (and K a multiple of
 // 64) operands are first made k-contiguous and the product runs on the
-// direct-to-LDS kernel further below, which stages through four 32-deep LDS
-// stages without registers; otherwise the register-staged kernel described
-// here runs.
+// direct-to-LDS kernel further below, which stages whole 128-byte rows through
+// two 64-deep LDS stages without registers; otherwise the register-staged
+// kernel described here runs.
 //
 // Kernel shape.  A workgroup of 512 lanes (8 waves, 2 along M x 4 along N)
 // computes a 256 x 256 tile of C; each wave owns 128 x 64 of it as 4 x 2
@@ -366,108 +366,117 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
     }
 }
 
-// The k loop walks 32-deep tiles through four LDS stages (the tile is the same
-// 256 x 256 over 8 waves of 128 x 64 as above): the loads of tile kt + 3
-// are issued as tile kt starts, so each tile's loads have three tiles' time to
-// land and a wave only ever waits for the oldest tile in flight
-// (s_waitcnt vmcnt(8): two younger tiles of 4 loads each stay outstanding).
-// With two 64-deep stages a tile's loads had one tile's time, and waves spent
-// over a third of their cycles waiting on them (SQ_WAIT_ANY, MI355X).
-// LDS rows are 64 bytes (four 16-byte k-chunks), XOR-swizzled by row / 4 so
-// that the eight rows a 16-byte fragment read serves at a time hit distinct
-// banks.  The four stages are separate LDS objects and the loop is unrolled by
-// four, so the compiler can tell the stage being read from those being filled.
-constexpr int BK2 = 32;
-constexpr int kStride2 = BK2;                       // bf16 per LDS row (64 bytes)
-constexpr int kStageElems2 = (BM + BN) * kStride2;  // 32 KiB per stage
-
-__device__ __forceinline__ int lds_off2(int row, int c) {
-    return row * kStride2 + ((c ^ ((row >> 2) & 3)) << 3);
-}
-
-// Per-wave staging state: buffer resources over the tile's A and B rows (base
-// and size in scalar registers) and each lane's byte offsets within them; the
-// k position is the scalar offset of each load.
-// Four direct loads per wave per tile: rows wave * 32 + j * 16 .. + 15 of A and
-// of B (one instruction fills 16 LDS rows of 64 bytes).
-struct DeepStage {
-    __amdgpu_buffer_rsrc_t ra, rb;
-    uint32_t oa[2], ob[2];
+// ---- direct-to-LDS kernel -----------------------------------------------------
+// The same 256 x 256 tile over 8 waves of 128 x 64, for operands whose k is
+// contiguous.  K is walked in 64-deep tiles through two LDS stages of 64 KiB
+// (rows of 128 bytes, 8 XOR-swizzled 16-byte chunks: lds_off above), filled by
+// `buffer_load_dwordx4 ... lds`, which writes each lane's 16 bytes straight
+// into LDS, so staging takes no registers.  One load instruction covers 8
+// whole rows (128 bytes each): every 128-byte line the vector L1 asks L2 for
+// is used whole.  With 32-deep tiles (64 bytes per row) each line was asked
+// for twice, half at a time, and the L1's queue of pending misses, not HBM,
+// set the pace (twice hipBLASLt's L2 request count for the same bytes,
+// TCP_TCC_READ_REQ on MI355X).
+//
+// Schedule of tile t (after the barrier that makes tile t visible and frees the
+// other stage): the loads of tile t + 1 go into the other stage, one per MFMA
+// of the first substep; the fragments run one 16-deep substep ahead of the
+// MFMAs, so the substep that straddles the barrier (the last of tile t - 1)
+// multiplies while tile t's first fragments are read.  At the end of the tile
+// each wave waits for its own loads and reads, then the barrier.
+struct DirectStage {
+    __amdgpu_buffer_rsrc_t ra, rb;  // tile rows of A and B (base and size in SGPRs)
+    uint32_t oa[4], ob[4];          // byte offset of each lane's chunk, per 8-row load
 };
 
-__device__ __forceinline__ void deep_issue(const DeepStage& d, uint16_t* stage, int k0, int wave) {
+// Load j of a wave (j = 0..3) fills rows wave * 32 + j * 8 .. + 7 of the A and
+// B halves of `stage`; lane l lands in row l / 8, physical chunk l % 8.
+__device__ __forceinline__ void direct_issue(const DirectStage& d, uint16_t* stage, int k0,
+                                             int wave) {
     const int sk = k0 * 2;  // bytes
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            d.ra, (lds_ptr_t)(stage + (wave * 32 + j * 16) * kStride2), 16, d.oa[j], sk, 0, 0);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
+            d.ra, (lds_ptr_t)(stage + (wave * 32 + j * 8) * kStride), 16, d.oa[j], sk, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            d.rb, (lds_ptr_t)(stage + (BM + wave * 32 + j * 16) * kStride2), 16, d.ob[j], sk, 0, 0);
+            d.rb, (lds_ptr_t)(stage + (BM + wave * 32 + j * 8) * kStride), 16, d.ob[j], sk, 0, 0);
+    }
 }
 
-__device__ __forceinline__ bf16x8 lds_frag2(const uint16_t* lds, int row, int c) {
-    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + lds_off2(row, c)));
+// The fragments of one 16-deep substep s (0..3) of a wave: 4 of A (128 rows),
+// 2 of B (64 columns).
+struct Frags {
+    bf16x8 a[TM], b[TN];
+};
+
+__device__ __forceinline__ void read_frags(Frags& f, const uint16_t* stage, int s, int wm, int wn,
+                                           int frow, int fk) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) f.a[i] = lds_frag(stage, wm * WM + i * 32 + frow, s * 16 + fk);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+        f.b[j] = lds_frag(stage + BM * kStride, wn * WN + j * 32 + frow, s * 16 + fk);
 }
 
-// The two 16-deep substeps of one 32-deep tile (fragments of substep 1 are read
-// while substep 0 multiplies).
-__device__ __forceinline__ void mfma_tile2(const uint16_t* cur, f32x16 (&acc)[TM][TN], int wm,
-                                           int wn, int frow, int fc) {
-    bf16x8 af[2][TM], bf[2][TN];
+__device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN]) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) af[s][i] = lds_frag2(cur, wm * WM + i * 32 + frow, 2 * s + fc);
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-            bf[s][j] = lds_frag2(cur + BM * kStride2, wn * WN + j * 32 + frow, 2 * s + fc);
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bf[s][j], acc[i][j],
-                                                                    0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
-// One tile step: wait until this wave's loads of tile kt have landed (the two
-// younger tiles stay in flight), make every wave's loads visible, start the
-// loads of tile kt + 3 into the stage tile kt - 1 used, multiply tile kt.
-// Steps run in groups of four; past the last tile a step re-loads the last
-// tile into a stage nothing reads again (so every step has the same loads in
-// flight and the same wait) and skips the multiply.
-__device__ __forceinline__ void deep_step(const DeepStage& d, const uint16_t* cur, uint16_t* fill,
-                                          int kt, int nk, f32x16 (&acc)[TM][TN], int wm, int wn,
-                                          int frow, int fc, int wave) {
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    // A bare barrier: __syncthreads()'s fence would wait for every load in
-    // flight (vmcnt(0)), the younger tiles' included.  Every wave's reads of
-    // the stage refilled below were consumed by its MFMAs of the previous step.
+// One load, then (for six of them) one fragment read, then one MFMA.
+#define AGK_LOAD_READ_MFMA(nread)                          \
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);     \
+    __builtin_amdgcn_sched_group_barrier(0x100, nread, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+
+// Tile t of nk; past the last tile (t == nk, when nk is odd) the step re-loads
+// the last tile into the stage it frees, multiplies only the straddling
+// substep and skips the rest.  Entering, f1 holds substep 3 of tile t - 1.
+__device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t* cur,
+                                            uint16_t* other, int t, int nk,
+                                            f32x16 (&acc)[TM][TN], Frags& f0, Frags& f1, int wm,
+                                            int wn, int frow, int fk, int wave) {
+    direct_issue(d, other, (t + 1 < nk ? t + 1 : nk - 1) * BK, wave);
+    read_frags(f0, cur, 0, wm, wn, frow, fk);
+    if (t > 0 && t <= nk) {  // uniform
+        mfma_sub(f1, acc);
+        AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1)
+        AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(0) AGK_LOAD_READ_MFMA(0)
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(f1, cur, 1, wm, wn, frow, fk);
+    if (t < nk) mfma_sub(f0, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(f0, cur, 2, wm, wn, frow, fk);
+    if (t < nk) mfma_sub(f1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(f1, cur, 3, wm, wn, frow, fk);
+    if (t < nk) mfma_sub(f0, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    // This wave's loads of tile t + 1 have landed and its reads of tile t are
+    // done; after the barrier every wave's are.  A bare barrier:
+    // __syncthreads()'s fence adds nothing here (vmcnt and lgkmcnt are zero).
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    deep_issue(d, fill, (kt + 3 < nk ? kt + 3 : nk - 1) * BK2, wave);
-    if (kt < nk) mfma_tile2(cur, acc, wm, wn, frow, fc);  // uniform
-    // keep this step's MFMAs (and their fragment registers) inside the step
     __builtin_amdgcn_sched_barrier(0);
 }
 
 template <bool OUT_F32>
-__global__ __launch_bounds__(kThreads) void gemm_nt_deep_kernel(
+__global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
     int accumulate, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint16_t st0[kStageElems2];
-    __shared__ __attribute__((aligned(16))) uint16_t st1[kStageElems2];
-    __shared__ __attribute__((aligned(16))) uint16_t st2[kStageElems2];
-    __shared__ __attribute__((aligned(16))) uint16_t st3[kStageElems2];
+    __shared__ __attribute__((aligned(16))) uint16_t st0[kStageElems];
+    __shared__ __attribute__((aligned(16))) uint16_t st1[kStageElems];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform, so kept in scalar registers (LDS destinations of the loads)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / kWavesN;
     const int wn = wave % kWavesN;
     int tm, tn;
@@ -478,7 +487,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_deep_kernel(
     // rows past M or N are fetched from the last valid row (never stored)
     const int rows_a = M - m0 < BM ? M - m0 : BM;
     const int rows_b = N - n0 < BN ? N - n0 : BN;
-    DeepStage d;
+    DirectStage d;
     d.ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(A + static_cast<int64_t>(m0) * lda), static_cast<short>(0),
         static_cast<int>(((rows_a - 1) * lda + K) * 2), 0x00020000);
@@ -486,9 +495,9 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_deep_kernel(
         const_cast<uint16_t*>(B + static_cast<int64_t>(n0) * ldb), static_cast<short>(0),
         static_cast<int>(((rows_b - 1) * ldb + K) * 2), 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = wave * 32 + j * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((row >> 2) & 3);
+    for (int j = 0; j < 4; ++j) {
+        const int row = wave * 32 + j * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 7);  // logical chunk of slot lane % 8
         const int ra = row < rows_a ? row : rows_a - 1;
         const int rb = row < rows_b ? row : rows_b - 1;
         d.oa[j] = (static_cast<uint32_t>(ra) * static_cast<uint32_t>(lda) + c * 8) * 2;
@@ -503,20 +512,20 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_deep_kernel(
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int nk = K / BK2;  // >= 2: K is a positive multiple of 64
+    const int nk = K / BK;  // >= 1: K is a positive multiple of 64
     const int frow = lane & 31;
-    const int fc = lane >> 5;
-    deep_issue(d, st0, 0, wave);
-    deep_issue(d, st1, BK2, wave);
-    deep_issue(d, st2, (nk > 2 ? 2 : nk - 1) * BK2, wave);
-    for (int kt = 0; kt < nk; kt += 4) {
-        deep_step(d, st0, st3, kt, nk, acc, wm, wn, frow, fc, wave);
-        deep_step(d, st1, st0, kt + 1, nk, acc, wm, wn, frow, fc, wave);
-        deep_step(d, st2, st1, kt + 2, nk, acc, wm, wn, frow, fc, wave);
-        deep_step(d, st3, st2, kt + 3, nk, acc, wm, wn, frow, fc, wave);
-    }
-    // no load may still be writing this workgroup's LDS when it exits
+    const int fk = (lane >> 5) * 8;  // MFMA operand lanes 32..63 hold k 8..15
+    direct_issue(d, st0, 0, wave);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    Frags f0, f1;
+    for (int t = 0; t < nk; t += 2) {
+        direct_step(d, st0, st1, t, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+        direct_step(d, st1, st0, t + 1, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+    }
+    // the last tile's substep 3 (with nk odd the extra step multiplied it)
+    if ((nk & 1) == 0) mfma_sub(f1, acc);
     store_c<OUT_F32>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale, accumulate);
 }
 
@@ -700,12 +709,12 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
         if (fits(lda_nt) && fits(ldb_nt)) {
             const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
             if (c_dtype == AGK_F32)
-                hipLaunchKernelGGL(gemm_nt_deep_kernel<true>, dim3(tiles_m * tiles_n),
+                hipLaunchKernelGGL(gemm_nt_direct_kernel<true>, dim3(tiles_m * tiles_n),
                                    dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
                                    lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
                                    n, k, rowscale, acc, tiles_m, tiles_n);
             else
-                hipLaunchKernelGGL(gemm_nt_deep_kernel<false>, dim3(tiles_m * tiles_n),
+                hipLaunchKernelGGL(gemm_nt_direct_kernel<false>, dim3(tiles_m * tiles_n),
                                    dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
                                    lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
                                    n, k, rowscale, acc, tiles_m, tiles_n);
