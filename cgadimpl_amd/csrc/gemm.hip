@@ -332,11 +332,14 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
 // 128 x 64 block of C.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <bool OUT_F32>
-__device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
-                                        int64_t ldc, int M, int N, int m0, int n0, int wm, int wn,
-                                        int lane, const float* __restrict__ rowscale,
-                                        int accumulate) {
+// GENERAL: rowscale and accumulate honoured; CHECK: rows past M and columns
+// past N skipped.  store_c picks the variant once per call (uniform values), so
+// the common plain, interior store has no per-element branches.
+template <bool OUT_F32, bool GENERAL, bool CHECK>
+__device__ __forceinline__ void store_c_impl(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
+                                             int64_t ldc, int M, int N, int m0, int n0, int wm,
+                                             int wn, int lane, const float* __restrict__ rowscale,
+                                             int accumulate) {
     const int col_l = lane & 31;
     const int row_l = 4 * (lane >> 5);
 #pragma unroll
@@ -344,21 +347,27 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int row = m0 + wm * WM + i * 32 + 8 * (e >> 2) + row_l + (e & 3);
-            if (row >= M) continue;
-            const float rs = rowscale ? rowscale[row] : 1.0f;
+            if (CHECK && row >= M) continue;
+            float rs = 1.0f;
+            if constexpr (GENERAL) rs = rowscale ? rowscale[row] : 1.0f;
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int col = n0 + wn * WN + j * 32 + col_l;
-                if (col >= N) continue;
-                float v = acc[i][j][e] * rs;
-                // accumulation rounds the product first (no fused multiply-add)
-                asm volatile("" : "+v"(v));
+                if (CHECK && col >= N) continue;
+                float v = acc[i][j][e];
+                if constexpr (GENERAL) {
+                    v *= rs;
+                    // accumulation rounds the product first (no fused multiply-add)
+                    asm volatile("" : "+v"(v));
+                }
                 if constexpr (OUT_F32) {
                     float* p = static_cast<float*>(C) + static_cast<int64_t>(row) * ldc + col;
-                    *p = accumulate ? *p + v : v;
+                    if constexpr (GENERAL) v = accumulate ? *p + v : v;
+                    *p = v;
                 } else {
                     uint16_t* p = static_cast<uint16_t*>(C) + static_cast<int64_t>(row) * ldc + col;
-                    if (accumulate) v = __uint_as_float(static_cast<uint32_t>(*p) << 16) + v;
+                    if constexpr (GENERAL)
+                        if (accumulate) v = __uint_as_float(static_cast<uint32_t>(*p) << 16) + v;
                     *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
                 }
             }
@@ -366,47 +375,74 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
     }
 }
 
-// ---- direct-to-LDS kernel -----------------------------------------------------
-// The same 256 x 256 tile over 8 waves of 128 x 64, for operands whose k is
-// contiguous.  K is walked in 64-deep tiles through two LDS stages of 64 KiB
-// (rows of 128 bytes, 8 XOR-swizzled 16-byte chunks: lds_off above), filled by
-// `buffer_load_dwordx4 ... lds`, which writes each lane's 16 bytes straight
-// into LDS, so staging takes no registers.  One load instruction covers 8
-// whole rows (128 bytes each): every 128-byte line the vector L1 asks L2 for
-// is used whole.  With 32-deep tiles (64 bytes per row) each line was asked
-// for twice, half at a time, and the L1's queue of pending misses, not HBM,
-// set the pace (twice hipBLASLt's L2 request count for the same bytes,
-// TCP_TCC_READ_REQ on MI355X).
-//
-// Schedule of tile t (after the barrier that makes tile t visible and frees the
-// other stage): the loads of tile t + 1 go into the other stage, one per MFMA
-// of the first substep; the fragments run one 16-deep substep ahead of the
-// MFMAs, so the substep that straddles the barrier (the last of tile t - 1)
-// multiplies while tile t's first fragments are read.  At the end of the tile
-// each wave waits for its own loads and reads, then the barrier.
-struct DirectStage {
-    __amdgpu_buffer_rsrc_t ra, rb;  // tile rows of A and B (base and size in SGPRs)
-    uint32_t oa[4], ob[4];          // byte offset of each lane's chunk, per 8-row load
-};
-
-// Load j of a wave (j = 0..3) fills rows wave * 32 + j * 8 .. + 7 of the A and
-// B halves of `stage`; lane l lands in row l / 8, physical chunk l % 8.
-__device__ __forceinline__ void direct_issue(const DirectStage& d, uint16_t* stage, int k0,
-                                             int wave) {
-    const int sk = k0 * 2;  // bytes
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            d.ra, (lds_ptr_t)(stage + (wave * 32 + j * 8) * kStride), 16, d.oa[j], sk, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            d.rb, (lds_ptr_t)(stage + (BM + wave * 32 + j * 8) * kStride), 16, d.ob[j], sk, 0, 0);
+template <bool OUT_F32>
+__device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
+                                        int64_t ldc, int M, int N, int m0, int n0, int wm, int wn,
+                                        int lane, const float* __restrict__ rowscale,
+                                        int accumulate) {
+    if (rowscale != nullptr || accumulate) {
+        store_c_impl<OUT_F32, true, true>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale,
+                                          accumulate);
+    } else if (m0 + BM <= M && n0 + BN <= N) {
+        store_c_impl<OUT_F32, false, false>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr, 0);
+    } else {
+        store_c_impl<OUT_F32, false, true>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr, 0);
     }
 }
 
+// ---- direct-to-LDS kernel -----------------------------------------------------
+// The same 256 x 256 tile, over 4 waves of 128 x 128 (2 x 2; 4 x 4 MFMA tiles
+// per wave, whose 256 accumulator registers live in AGPRs), for operands whose
+// k is contiguous.  K is walked in 64-deep tiles through two LDS stages of
+// 64 KiB (rows of 128 bytes, 8 XOR-swizzled 16-byte chunks: lds_off above),
+// filled by `buffer_load_dwordx4 ... lds`, so staging takes no registers.
+//
+// Why this shape (measured on MI355X, c5 products):
+// - One load instruction covers 8 whole rows of 128 bytes, so every 128-byte
+//   line the vector L1 asks L2 for is used whole.  32-deep tiles (64 bytes per
+//   row) asked for each line twice, half at a time, and the L1's queue of
+//   pending misses, not HBM, set the pace (twice hipBLASLt's L2 request count
+//   for the same bytes, TCP_TCC_READ_REQ).
+// - One wave per SIMD with a 128 x 128 block reads a third fewer LDS bytes per
+//   MFMA than two waves of 128 x 64, and its stream of 64 MFMAs per tile has
+//   the loads and fragment reads interleaved between them; it was 4-6 % faster
+//   than eight waves of 128 x 64 with the same stages.
+//
+// Schedule of tile t (after the barrier that makes tile t visible and frees the
+// other stage): the 16 loads of tile t + 1 go into the other stage, one per
+// two MFMAs of the first two substeps; the fragments run one 16-deep substep
+// ahead of the MFMAs, so the substep that straddles the barrier (the last of
+// tile t - 1) multiplies while tile t's first fragments are read.  At the end
+// of the tile each wave waits for its own loads and reads, then the barrier.
+constexpr int kDirectThreads = 256;
+constexpr int WN4 = 128, TN4 = WN4 / 32;  // per-wave columns, MFMA tiles along them
+
+struct DirectStage {
+    __amdgpu_buffer_rsrc_t ra, rb;  // tile rows of A and B (base and size in SGPRs)
+    uint32_t oa[8], ob[8];          // byte offset of each lane's chunk, per 8-row load
+};
+
+// Load j of a wave (j = 0..7) fills rows wave * 64 + j * 8 .. + 7 of one
+// operand's half of `stage`; lane l lands in row l / 8, physical chunk l % 8.
+__device__ __forceinline__ void direct_issue_a(const DirectStage& d, uint16_t* stage, int sk,
+                                               int wave) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            d.ra, (lds_ptr_t)(stage + (wave * 64 + j * 8) * kStride), 16, d.oa[j], sk, 0, 0);
+}
+__device__ __forceinline__ void direct_issue_b(const DirectStage& d, uint16_t* stage, int sk,
+                                               int wave) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            d.rb, (lds_ptr_t)(stage + (BM + wave * 64 + j * 8) * kStride), 16, d.ob[j], sk, 0, 0);
+}
+
 // The fragments of one 16-deep substep s (0..3) of a wave: 4 of A (128 rows),
-// 2 of B (64 columns).
+// 4 of B (128 columns).
 struct Frags {
-    bf16x8 a[TM], b[TN];
+    bf16x8 a[TM], b[TN4];
 };
 
 __device__ __forceinline__ void read_frags(Frags& f, const uint16_t* stage, int s, int wm, int wn,
@@ -414,47 +450,57 @@ __device__ __forceinline__ void read_frags(Frags& f, const uint16_t* stage, int 
 #pragma unroll
     for (int i = 0; i < TM; ++i) f.a[i] = lds_frag(stage, wm * WM + i * 32 + frow, s * 16 + fk);
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-        f.b[j] = lds_frag(stage + BM * kStride, wn * WN + j * 32 + frow, s * 16 + fk);
+    for (int j = 0; j < TN4; ++j)
+        f.b[j] = lds_frag(stage + BM * kStride, wn * WN4 + j * 32 + frow, s * 16 + fk);
 }
 
-__device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN]) {
+__device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN4]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN4; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
-// One load, then (for six of them) one fragment read, then one MFMA.
-#define AGK_LOAD_READ_MFMA(nread)                          \
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);     \
-    __builtin_amdgcn_sched_group_barrier(0x100, nread, 0); \
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+// Scheduling groups: one load, one fragment read, two MFMAs (AGK_LRM); one
+// fragment read, two MFMAs (AGK_RM).  Eight of them cover a substep's 16 MFMAs.
+#define AGK_LRM                                         \
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#define AGK_RM                                          \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#define AGK_X8(g) g g g g g g g g
 
-// Tile t of nk; past the last tile (t == nk, when nk is odd) the step re-loads
-// the last tile into the stage it frees, multiplies only the straddling
-// substep and skips the rest.  Entering, f1 holds substep 3 of tile t - 1.
+// Tile t of nk.  FIRST (tile 0) has no straddling substep; every step loads
+// tile t + 1 (the last tile again at the end, into the stage nothing reads
+// again).  Entering, f1 holds substep 3 of tile t - 1.
+template <bool FIRST>
 __device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t* cur,
                                             uint16_t* other, int t, int nk,
-                                            f32x16 (&acc)[TM][TN], Frags& f0, Frags& f1, int wm,
+                                            f32x16 (&acc)[TM][TN4], Frags& f0, Frags& f1, int wm,
                                             int wn, int frow, int fk, int wave) {
-    direct_issue(d, other, (t + 1 < nk ? t + 1 : nk - 1) * BK, wave);
+    const int sk = (t + 1 < nk ? t + 1 : nk - 1) * BK * 2;  // bytes
+    direct_issue_a(d, other, sk, wave);
     read_frags(f0, cur, 0, wm, wn, frow, fk);
-    if (t > 0 && t <= nk) {  // uniform
+    if constexpr (!FIRST) {
         mfma_sub(f1, acc);
-        AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1)
-        AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(1) AGK_LOAD_READ_MFMA(0) AGK_LOAD_READ_MFMA(0)
+        AGK_X8(AGK_LRM)
     }
     __builtin_amdgcn_sched_barrier(0);
+    direct_issue_b(d, other, sk, wave);
     read_frags(f1, cur, 1, wm, wn, frow, fk);
-    if (t < nk) mfma_sub(f0, acc);
+    mfma_sub(f0, acc);
+    AGK_X8(AGK_LRM)
     __builtin_amdgcn_sched_barrier(0);
     read_frags(f0, cur, 2, wm, wn, frow, fk);
-    if (t < nk) mfma_sub(f1, acc);
+    mfma_sub(f1, acc);
+    AGK_X8(AGK_RM)
     __builtin_amdgcn_sched_barrier(0);
     read_frags(f1, cur, 3, wm, wn, frow, fk);
-    if (t < nk) mfma_sub(f0, acc);
+    mfma_sub(f0, acc);
+    AGK_X8(AGK_RM)
     __builtin_amdgcn_sched_barrier(0);
     // This wave's loads of tile t + 1 have landed and its reads of tile t are
     // done; after the barrier every wave's are.  A bare barrier:
@@ -466,7 +512,7 @@ __device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t
 }
 
 template <bool OUT_F32>
-__global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
+__global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
     int accumulate, int tiles_m, int tiles_n) {
@@ -477,8 +523,8 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
     const int lane = tid & 63;
     // wave-uniform, so kept in scalar registers (LDS destinations of the loads)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / kWavesN;
-    const int wn = wave % kWavesN;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
     int tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM;
@@ -495,8 +541,8 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
         const_cast<uint16_t*>(B + static_cast<int64_t>(n0) * ldb), static_cast<short>(0),
         static_cast<int>(((rows_b - 1) * ldb + K) * 2), 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = wave * 32 + j * 8 + (lane >> 3);
+    for (int j = 0; j < 8; ++j) {
+        const int row = wave * 64 + j * 8 + (lane >> 3);
         const int c = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 7);  // logical chunk of slot lane % 8
         const int ra = row < rows_a ? row : rows_a - 1;
         const int rb = row < rows_b ? row : rows_b - 1;
@@ -504,29 +550,42 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_direct_kernel(
         d.ob[j] = (static_cast<uint32_t>(rb) * static_cast<uint32_t>(ldb) + c * 8) * 2;
     }
 
-    f32x16 acc[TM][TN];
+    f32x16 acc[TM][TN4];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     const int nk = K / BK;  // >= 1: K is a positive multiple of 64
     const int frow = lane & 31;
     const int fk = (lane >> 5) * 8;  // MFMA operand lanes 32..63 hold k 8..15
-    direct_issue(d, st0, 0, wave);
+    direct_issue_a(d, st0, 0, wave);
+    direct_issue_b(d, st0, 0, wave);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     Frags f0, f1;
-    for (int t = 0; t < nk; t += 2) {
-        direct_step(d, st0, st1, t, nk, acc, f0, f1, wm, wn, frow, fk, wave);
-        direct_step(d, st1, st0, t + 1, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+    direct_step<true>(d, st0, st1, 0, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+    int t = 1;
+    for (; t + 1 < nk; t += 2) {
+        direct_step<false>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+        direct_step<false>(d, st0, st1, t + 1, nk, acc, f0, f1, wm, wn, frow, fk, wave);
     }
-    // the last tile's substep 3 (with nk odd the extra step multiplied it)
-    if ((nk & 1) == 0) mfma_sub(f1, acc);
-    store_c<OUT_F32>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale, accumulate);
+    if (t < nk) direct_step<false>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+    mfma_sub(f1, acc);  // substep 3 of the last tile
+
+    // the wave's 128 x 128 block leaves as two 128 x 64 halves (store_c's layout)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        f32x16 half[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) half[i][j] = acc[i][h * TN + j];
+        store_c<OUT_F32>(half, C, ldc, M, N, m0, n0, wm, 2 * wn + h, lane, rowscale, accumulate);
+    }
 }
 
 // ---- transpose ----------------------------------------------------------------
@@ -710,12 +769,12 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
             const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
             if (c_dtype == AGK_F32)
                 hipLaunchKernelGGL(gemm_nt_direct_kernel<true>, dim3(tiles_m * tiles_n),
-                                   dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
+                                   dim3(kDirectThreads), 0, st, static_cast<const uint16_t*>(a_nt),
                                    lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
                                    n, k, rowscale, acc, tiles_m, tiles_n);
             else
                 hipLaunchKernelGGL(gemm_nt_direct_kernel<false>, dim3(tiles_m * tiles_n),
-                                   dim3(kThreads), 0, st, static_cast<const uint16_t*>(a_nt),
+                                   dim3(kDirectThreads), 0, st, static_cast<const uint16_t*>(a_nt),
                                    lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
                                    n, k, rowscale, acc, tiles_m, tiles_n);
             return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
