@@ -301,6 +301,12 @@ def run_c5(steps, warmup):
     ws_n = torch.empty(max(1, agk.rmsnorm_bwd_workspace_bytes(M, K)), dtype=torch.uint8, device=dev)
     ws_w = torch.empty(agk.gemm_bf16_workspace_bytes(K, N, M, True, False), dtype=torch.uint8,
                        device=dev)
+
+    def gemm_ws(m, n, k, ta, tb):  # the workspace each product's fast path asks for, or None
+        need = agk.gemm_bf16_workspace_bytes(m, n, k, ta, tb)
+        return torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+    ws_y = gemm_ws(M, N, K, False, True)
+    ws_dh = gemm_ws(M, K, N, False, True)
     stream = torch.cuda.current_stream()
     stages = ["rmsnorm_fwd", "transpose_W", "gemm_y", "gemm_dh", "gemm_dW", "rmsnorm_bwd"]
 
@@ -313,9 +319,9 @@ def run_c5(steps, warmup):
         mark(1)
         agk.transpose_bf16(W, wt, stream=stream)
         mark(2)
-        agk.gemm_bf16(h, wt, y, trans_b=True, workspace=None, stream=stream)
+        agk.gemm_bf16(h, wt, y, trans_b=True, workspace=ws_y, stream=stream)
         mark(3)
-        agk.gemm_bf16(dy, W, dh, trans_b=True, workspace=None, stream=stream)
+        agk.gemm_bf16(dy, W, dh, trans_b=True, workspace=ws_dh, stream=stream)
         mark(4)
         agk.gemm_bf16(h, dy, dW, trans_a=True, workspace=ws_w, stream=stream)
         mark(5)
