@@ -61,9 +61,18 @@ struct SumR {
     static constexpr float kId = 0.0f;
     __device__ static float op(float a, float b) { return a + b; }
 };
+// max(a, b) as one v_max_f32.  Written as fmaxf (or any form the compiler
+// recognises as a max) it costs three instructions per element here: in IEEE
+// mode the compiler first quiets possible signalling NaNs in both operands.  A
+// NaN in a row still reaches every result that uses the max, through
+// exp(z - max).
 struct MaxR {
     static constexpr float kId = -__builtin_inff();
-    __device__ static float op(float a, float b) { return fmaxf(a, b); }
+    __device__ static float op(float a, float b) {
+        float r;
+        asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+        return r;
+    }
 };
 
 // exp(x) = 2^(x * log2(e)) on the hardware exp2 instruction (v_exp_f32).  The
