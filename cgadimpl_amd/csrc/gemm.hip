@@ -12,11 +12,11 @@
 // (kscale multiplies the A operand as it is staged, rounding to bf16 as a
 // stored h would be; rowscale multiplies the fp32 accumulator.)
 //
-// Two kernels share the tile shape.  With a workspace (and K a multiple of
-// 64) operands are first made k-contiguous and the product runs on the
-// direct-to-LDS kernel further below, which stages whole 128-byte rows through
-// two 64-deep LDS stages without registers; otherwise the register-staged
-// kernel described here runs.
+// Two kernels share the tile shape.  When K is a multiple of 64 and there is
+// no k-scale, the product runs on the direct-to-LDS kernel further below,
+// which stages whole 128-byte lines of either operand layout through two
+// 64-deep LDS stages without registers; otherwise the register-staged kernel
+// described here runs.
 //
 // Kernel shape.  A workgroup of 512 lanes (8 waves, 2 along M x 4 along N)
 // computes a 256 x 256 tile of C; each wave owns 128 x 64 of it as 4 x 2
@@ -392,17 +392,28 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
 
 // ---- direct-to-LDS kernel -----------------------------------------------------
 // The same 256 x 256 tile, over 4 waves of 128 x 128 (2 x 2; 4 x 4 MFMA tiles
-// per wave, whose 256 accumulator registers live in AGPRs), for operands whose
-// k is contiguous.  K is walked in 64-deep tiles through two LDS stages of
-// 64 KiB (rows of 128 bytes, 8 XOR-swizzled 16-byte chunks: lds_off above),
-// filled by `buffer_load_dwordx4 ... lds`, so staging takes no registers.
+// per wave, whose 256 accumulator registers live in AGPRs).  K is walked in
+// 64-deep tiles through two LDS stages of 64 KiB (32 KiB per operand), filled by
+// `buffer_load_dwordx4 ... lds`, so staging takes no registers.  Each operand is
+// staged in the layout it has in memory:
+// - k-contiguous ([rows][K]): 256 LDS rows of 64 k (128 bytes, 8 XOR-swizzled
+//   16-byte chunks: lds_off above); a fragment is one 16-byte read.
+// - k-strided (TR; [K][cols], the columns contiguous): 64 LDS rows of one k
+//   each, 256 columns (512 bytes, 32 chunks whose 64-byte groups are XOR-
+//   swizzled by k % 4: tr_off); a fragment is two ds_read_b64_tr_b16.  Within
+//   each 16 lanes that instruction hands lane 4a + b, for e = 0..3, the element
+//   at offset b from the address of lane 4e + a (checked on MI355X), so lane s
+//   pointing at k0 + s / 4, column c0 + 4 (s % 4) gives lane j the four k
+//   k0 .. k0 + 3 of column c0 + j: the MFMA operand layout.  No transposed copy
+//   of the operand is made.
+// Either way one load instruction moves 1 KiB of whole 128-byte lines, and the
+// LDS destination of load j of wave w is the same kilobyte.
 //
 // Why this shape (measured on MI355X, c5 products):
-// - One load instruction covers 8 whole rows of 128 bytes, so every 128-byte
-//   line the vector L1 asks L2 for is used whole.  32-deep tiles (64 bytes per
-//   row) asked for each line twice, half at a time, and the L1's queue of
-//   pending misses, not HBM, set the pace (twice hipBLASLt's L2 request count
-//   for the same bytes, TCP_TCC_READ_REQ).
+// - Whole 128-byte rows per load: 32-deep tiles (64 bytes per row) asked L2 for
+//   each line twice, half at a time, and the L1's queue of pending misses, not
+//   HBM, set the pace (twice hipBLASLt's L2 request count for the same bytes,
+//   TCP_TCC_READ_REQ).
 // - One wave per SIMD with a 128 x 128 block reads a third fewer LDS bytes per
 //   MFMA than two waves of 128 x 64, and its stream of 64 MFMAs per tile has
 //   the loads and fragment reads interleaved between them; it was 4-6 % faster
@@ -416,27 +427,59 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
 // of the tile each wave waits for its own loads and reads, then the barrier.
 constexpr int kDirectThreads = 256;
 constexpr int WN4 = 128, TN4 = WN4 / 32;  // per-wave columns, MFMA tiles along them
+constexpr int kTrRow = 256;               // bf16 per LDS row of a k-strided operand
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
+
+// Element offset of column col (a multiple of 4) of k-row k in a k-strided stage.
+__device__ __forceinline__ int tr_off(int k, int col) {
+    return k * kTrRow + ((((col >> 3) ^ ((k & 3) << 2))) << 3) + (col & 7);
+}
 
 struct DirectStage {
-    __amdgpu_buffer_rsrc_t ra, rb;  // tile rows of A and B (base and size in SGPRs)
-    uint32_t oa[8], ob[8];          // byte offset of each lane's chunk, per 8-row load
+    __amdgpu_buffer_rsrc_t ra, rb;  // the tile's A and B (base and size in SGPRs)
+    uint32_t oa[8], ob[8];          // byte offset of each lane's chunk, per load
+    int step_a, step_b;             // bytes from one 64-deep k-tile to the next
 };
 
-// Load j of a wave (j = 0..7) fills rows wave * 64 + j * 8 .. + 7 of one
-// operand's half of `stage`; lane l lands in row l / 8, physical chunk l % 8.
-__device__ __forceinline__ void direct_issue_a(const DirectStage& d, uint16_t* stage, int sk,
+// Load j of a wave (j = 0..7) fills kilobyte wave * 8 + j of one operand's half
+// of `stage`; tile t's data starts t * step bytes into the operand.
+__device__ __forceinline__ void direct_issue_a(const DirectStage& d, uint16_t* stage, int t,
                                                int wave) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            d.ra, (lds_ptr_t)(stage + (wave * 64 + j * 8) * kStride), 16, d.oa[j], sk, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, (lds_ptr_t)(stage + (wave * 8 + j) * 512),
+                                                 16, d.oa[j], t * d.step_a, 0, 0);
 }
-__device__ __forceinline__ void direct_issue_b(const DirectStage& d, uint16_t* stage, int sk,
+__device__ __forceinline__ void direct_issue_b(const DirectStage& d, uint16_t* stage, int t,
                                                int wave) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            d.rb, (lds_ptr_t)(stage + (BM + wave * 64 + j * 8) * kStride), 16, d.ob[j], sk, 0, 0);
+            d.rb, (lds_ptr_t)(stage + BM * BK + (wave * 8 + j) * 512), 16, d.ob[j], t * d.step_b,
+            0, 0);
+}
+
+// Per-lane byte offsets of one operand's loads.  rows: valid rows (k-contiguous)
+// or columns (k-strided) of the tile; ld: leading dimension in elements.
+template <bool TR>
+__device__ __forceinline__ void direct_offsets(uint32_t (&o)[8], int wave, int lane, int rows,
+                                               int64_t ld) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if constexpr (!TR) {
+            const int row = wave * 64 + j * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 7);  // chunk of slot lane % 8
+            const int r = row < rows ? row : rows - 1;  // rows past M or N: the last valid row
+            o[j] = (static_cast<uint32_t>(r) * static_cast<uint32_t>(ld) + c * 8) * 2;
+        } else {
+            const int k = wave * 16 + j * 2 + (lane >> 5);
+            const int c = (lane & 31) ^ ((k & 3) << 2);  // chunk of slot lane % 32
+            const int col = c * 8 < rows ? c * 8 : rows - 8;  // columns past M or N: the last 8
+            o[j] = (static_cast<uint32_t>(k) * static_cast<uint32_t>(ld) + col) * 2;
+        }
+    }
 }
 
 // The fragments of one 16-deep substep s (0..3) of a wave: 4 of A (128 rows),
@@ -445,13 +488,32 @@ struct Frags {
     bf16x8 a[TM], b[TN4];
 };
 
+// MFMA operand lane l (row or column l % 32, k 8 (l / 32) .. + 7) of block
+// column base c0, substep s, from a k-strided stage: two transposing reads of
+// four k each.
+__device__ __forceinline__ bf16x8 tr_frag(const uint16_t* lds, int c0, int s, int lane) {
+    const int g = lane >> 4, sl = lane & 15;
+    const int k = s * 16 + (g >> 1) * 8 + (sl >> 2);
+    const int col = c0 + (g & 1) * 16 + 4 * (sl & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(lds + tr_off(k, col)));
+    const s16x4 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(lds + tr_off(k + 4, col)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <bool A_TR, bool B_TR>
 __device__ __forceinline__ void read_frags(Frags& f, const uint16_t* stage, int s, int wm, int wn,
-                                           int frow, int fk) {
+                                           int frow, int fk, int lane) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) f.a[i] = lds_frag(stage, wm * WM + i * 32 + frow, s * 16 + fk);
+    for (int i = 0; i < TM; ++i) {
+        if constexpr (A_TR) f.a[i] = tr_frag(stage, wm * WM + i * 32, s, lane);
+        else f.a[i] = lds_frag(stage, wm * WM + i * 32 + frow, s * 16 + fk);
+    }
 #pragma unroll
-    for (int j = 0; j < TN4; ++j)
-        f.b[j] = lds_frag(stage + BM * kStride, wn * WN4 + j * 32 + frow, s * 16 + fk);
+    for (int j = 0; j < TN4; ++j) {
+        if constexpr (B_TR) f.b[j] = tr_frag(stage + BM * BK, wn * WN4 + j * 32, s, lane);
+        else f.b[j] = lds_frag(stage + BM * kStride, wn * WN4 + j * 32 + frow, s * 16 + fk);
+    }
 }
 
 __device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN4]) {
@@ -476,29 +538,29 @@ __device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN4])
 // Tile t of nk.  FIRST (tile 0) has no straddling substep; every step loads
 // tile t + 1 (the last tile again at the end, into the stage nothing reads
 // again).  Entering, f1 holds substep 3 of tile t - 1.
-template <bool FIRST>
+template <bool FIRST, bool A_TR, bool B_TR>
 __device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t* cur,
                                             uint16_t* other, int t, int nk,
                                             f32x16 (&acc)[TM][TN4], Frags& f0, Frags& f1, int wm,
-                                            int wn, int frow, int fk, int wave) {
-    const int sk = (t + 1 < nk ? t + 1 : nk - 1) * BK * 2;  // bytes
-    direct_issue_a(d, other, sk, wave);
-    read_frags(f0, cur, 0, wm, wn, frow, fk);
+                                            int wn, int frow, int fk, int lane, int wave) {
+    const int tn = t + 1 < nk ? t + 1 : nk - 1;
+    direct_issue_a(d, other, tn, wave);
+    read_frags<A_TR, B_TR>(f0, cur, 0, wm, wn, frow, fk, lane);
     if constexpr (!FIRST) {
         mfma_sub(f1, acc);
         AGK_X8(AGK_LRM)
     }
     __builtin_amdgcn_sched_barrier(0);
-    direct_issue_b(d, other, sk, wave);
-    read_frags(f1, cur, 1, wm, wn, frow, fk);
+    direct_issue_b(d, other, tn, wave);
+    read_frags<A_TR, B_TR>(f1, cur, 1, wm, wn, frow, fk, lane);
     mfma_sub(f0, acc);
     AGK_X8(AGK_LRM)
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(f0, cur, 2, wm, wn, frow, fk);
+    read_frags<A_TR, B_TR>(f0, cur, 2, wm, wn, frow, fk, lane);
     mfma_sub(f1, acc);
     AGK_X8(AGK_RM)
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(f1, cur, 3, wm, wn, frow, fk);
+    read_frags<A_TR, B_TR>(f1, cur, 3, wm, wn, frow, fk, lane);
     mfma_sub(f0, acc);
     AGK_X8(AGK_RM)
     __builtin_amdgcn_sched_barrier(0);
@@ -511,7 +573,9 @@ __device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool OUT_F32>
+// A_TR: A stored [K][lda] (its m contiguous); B_TR: B stored [K][ldb] (its n
+// contiguous).  Otherwise the operand is [rows][ld] with k contiguous.
+template <bool OUT_F32, bool A_TR, bool B_TR>
 __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
@@ -530,25 +594,25 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
-    // rows past M or N are fetched from the last valid row (never stored)
     const int rows_a = M - m0 < BM ? M - m0 : BM;
     const int rows_b = N - n0 < BN ? N - n0 : BN;
     DirectStage d;
+    // the resources span the bytes the tile's loads can address (their k
+    // position is the scalar offset, always inside the operand)
     d.ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(A + static_cast<int64_t>(m0) * lda), static_cast<short>(0),
-        static_cast<int>(((rows_a - 1) * lda + K) * 2), 0x00020000);
+        const_cast<uint16_t*>(A_TR ? A + m0 : A + static_cast<int64_t>(m0) * lda),
+        static_cast<short>(0),
+        static_cast<int>(A_TR ? ((K - 1) * lda + rows_a) * 2 : ((rows_a - 1) * lda + K) * 2),
+        0x00020000);
     d.rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(B + static_cast<int64_t>(n0) * ldb), static_cast<short>(0),
-        static_cast<int>(((rows_b - 1) * ldb + K) * 2), 0x00020000);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int row = wave * 64 + j * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 7);  // logical chunk of slot lane % 8
-        const int ra = row < rows_a ? row : rows_a - 1;
-        const int rb = row < rows_b ? row : rows_b - 1;
-        d.oa[j] = (static_cast<uint32_t>(ra) * static_cast<uint32_t>(lda) + c * 8) * 2;
-        d.ob[j] = (static_cast<uint32_t>(rb) * static_cast<uint32_t>(ldb) + c * 8) * 2;
-    }
+        const_cast<uint16_t*>(B_TR ? B + n0 : B + static_cast<int64_t>(n0) * ldb),
+        static_cast<short>(0),
+        static_cast<int>(B_TR ? ((K - 1) * ldb + rows_b) * 2 : ((rows_b - 1) * ldb + K) * 2),
+        0x00020000);
+    d.step_a = A_TR ? static_cast<int>(BK * lda * 2) : BK * 2;
+    d.step_b = B_TR ? static_cast<int>(BK * ldb * 2) : BK * 2;
+    direct_offsets<A_TR>(d.oa, wave, lane, rows_a, lda);
+    direct_offsets<B_TR>(d.ob, wave, lane, rows_b, ldb);
 
     f32x16 acc[TM][TN4];
 #pragma unroll
@@ -567,13 +631,17 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     Frags f0, f1;
-    direct_step<true>(d, st0, st1, 0, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+    direct_step<true, A_TR, B_TR>(d, st0, st1, 0, nk, acc, f0, f1, wm, wn, frow, fk, lane, wave);
     int t = 1;
     for (; t + 1 < nk; t += 2) {
-        direct_step<false>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, wave);
-        direct_step<false>(d, st0, st1, t + 1, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+        direct_step<false, A_TR, B_TR>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, lane,
+                                       wave);
+        direct_step<false, A_TR, B_TR>(d, st0, st1, t + 1, nk, acc, f0, f1, wm, wn, frow, fk,
+                                       lane, wave);
     }
-    if (t < nk) direct_step<false>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, wave);
+    if (t < nk)
+        direct_step<false, A_TR, B_TR>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, lane,
+                                       wave);
     mfma_sub(f1, acc);  // substep 3 of the last tile
 
     // the wave's 128 x 128 block leaves as two 128 x 64 halves (store_c's layout)
@@ -692,14 +760,10 @@ inline bool direct_eligible(int64_t K, const float* kscale) {
     return kscale == nullptr && K % BK == 0;
 }
 
-inline size_t workspace_for(int64_t M, int64_t N, int64_t K, int a_trans, int b_trans,
-                            const float* kscale) {
-    if (!direct_eligible(K, kscale)) return 0;
-    size_t bytes = 0;
-    if (a_trans) bytes += static_cast<size_t>(M) * K * 2;
-    if (!b_trans) bytes += static_cast<size_t>(N) * K * 2;
-    return bytes;
-}
+// No layout needs a workspace: the direct kernel stages either layout of each
+// operand itself.  (The workspace arguments stay in the ABI for callers that
+// pass one.)
+inline size_t workspace_for(int64_t, int64_t, int64_t, int, int, const float*) { return 0; }
 
 }  // namespace agk_gemm
 
@@ -743,49 +807,39 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
     const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
     const int acc = accumulate != 0;
 
-    // With a workspace, operands stored with k strided are transposed into it
-    // (one HBM-bound pass each) so the GEMM runs on the direct-to-LDS kernel.
-    const size_t need = workspace_for(M, N, K, a_trans, b_trans, kscale);
-    if (direct_eligible(K, kscale) && (need == 0 || (workspace && workspace_bytes >= need &&
-                                                     aligned16(workspace)))) {
-        const void* a_nt = A;
-        const void* b_nt = B;
-        int64_t lda_nt = lda, ldb_nt = ldb;
-        char* ws = static_cast<char*>(workspace);
-        if (a_trans) {  // A stored [K][lda] -> [M][K]
-            if (int rc = launch_transpose(A, lda, ws, K, k, m, st)) return rc;
-            a_nt = ws;
-            lda_nt = K;
-            ws += static_cast<size_t>(M) * K * 2;
+    // The direct-to-LDS kernel reads either layout of each operand; the
+    // buffer resources span a tile's rows (or k-rows) in 31-bit byte offsets.
+    auto fits = [&](int64_t ld, bool tr) {
+        return (tr ? (K - 1) * ld + BM : (BM - 1) * ld + K) * 2 <= 0x7fffffffLL;
+    };
+    const bool a_tr = a_trans != 0, b_tr = b_trans == 0;
+    if (direct_eligible(K, kscale) && fits(lda, a_tr) && fits(ldb, b_tr)) {
+        const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+        const dim3 grid(tiles_m * tiles_n), block(kDirectThreads);
+        const uint16_t* a16 = static_cast<const uint16_t*>(A);
+        const uint16_t* b16 = static_cast<const uint16_t*>(B);
+#define AGK_DIRECT(F32, ATR, BTR)                                                              \
+    hipLaunchKernelGGL((gemm_nt_direct_kernel<F32, ATR, BTR>), grid, block, 0, st, a16, lda, b16, \
+                       ldb, C, ldc, m, n, k, rowscale, acc, tiles_m, tiles_n)
+        const bool f32 = c_dtype == AGK_F32;
+        if (f32) {
+            if (a_tr && b_tr) AGK_DIRECT(true, true, true);
+            else if (a_tr) AGK_DIRECT(true, true, false);
+            else if (b_tr) AGK_DIRECT(true, false, true);
+            else AGK_DIRECT(true, false, false);
+        } else {
+            if (a_tr && b_tr) AGK_DIRECT(false, true, true);
+            else if (a_tr) AGK_DIRECT(false, true, false);
+            else if (b_tr) AGK_DIRECT(false, false, true);
+            else AGK_DIRECT(false, false, false);
         }
-        if (!b_trans) {  // B stored [K][ldb] -> [N][K]
-            if (int rc = launch_transpose(B, ldb, ws, K, k, n, st)) return rc;
-            b_nt = ws;
-            ldb_nt = K;
-        }
-        // the buffer resources span a tile's 256 rows in 31-bit byte offsets
-        auto fits = [&](int64_t ld) { return (255 * ld + K) * 2 <= 0x7fffffffLL; };
-        if (fits(lda_nt) && fits(ldb_nt)) {
-            const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
-            if (c_dtype == AGK_F32)
-                hipLaunchKernelGGL(gemm_nt_direct_kernel<true>, dim3(tiles_m * tiles_n),
-                                   dim3(kDirectThreads), 0, st, static_cast<const uint16_t*>(a_nt),
-                                   lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
-                                   n, k, rowscale, acc, tiles_m, tiles_n);
-            else
-                hipLaunchKernelGGL(gemm_nt_direct_kernel<false>, dim3(tiles_m * tiles_n),
-                                   dim3(kDirectThreads), 0, st, static_cast<const uint16_t*>(a_nt),
-                                   lda_nt, static_cast<const uint16_t*>(b_nt), ldb_nt, C, ldc, m,
-                                   n, k, rowscale, acc, tiles_m, tiles_n);
-            return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
-        }
-        A = a_nt;  // leading dimensions too large for the direct kernel's offsets
-        B = b_nt;
-        lda = lda_nt;
-        ldb = ldb_nt;
-        a_trans = 0;
-        b_trans = 1;
+#undef AGK_DIRECT
+        return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
     }
+    // Leading dimensions too large for the direct kernel's offsets, K not a
+    // multiple of 64, or a k-scale: the register-staged kernel.
+    (void)workspace;
+    (void)workspace_bytes;
     const bool ak = !a_trans, bk = b_trans != 0, ks = kscale != nullptr;
     if (ak && bk) return dispatch_ks<true, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
     if (ak && !bk) return dispatch_ks<true, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);

@@ -140,11 +140,10 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
  *   kscale (nullable, fp32 [K]): multiplies A's column k as A is staged, the
  *      product rounded to bf16 (h = x * gamma without materialising h);
  *   rowscale (nullable, fp32 [M]): multiplies row m of the fp32 result.
- *   workspace (nullable): with at least agk_gemm_bf16_workspace_bytes(...)
- *      bytes, operands stored with k strided are first transposed into it
- *      and the product runs on the faster kernel for k-contiguous operands
- *      (used when kscale == NULL and K % 64 == 0); without it the operands
- *      are transposed while they are staged.
+ *   workspace (nullable, unused): every layout is staged as it lies (k-strided
+ *      operands read with transposing LDS reads when kscale == NULL and
+ *      K % 64 == 0; otherwise transposed in registers while staged), so
+ *      agk_gemm_bf16_workspace_bytes is 0; the argument stays for callers.
  * A, B, kscale, workspace 16-byte aligned; M, N, K, lda, ldb multiples of 8;
  * the result is deterministic (fixed accumulation order).                    */
 int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
@@ -152,8 +151,8 @@ int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_
                   int64_t K, const float* kscale, const float* rowscale, int accumulate,
                   void* workspace, size_t workspace_bytes, agk_stream_t stream);
 
-/* Bytes of workspace that let agk_gemm_bf16 use the k-contiguous kernel:
- * M*K*2 if a_trans, plus N*K*2 if !b_trans; 0 when K % 64 != 0. */
+/* Bytes of workspace agk_gemm_bf16 uses: 0 for every shape and layout (kept so
+ * that callers sizing a workspace from it need no change). */
 size_t agk_gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_trans, int b_trans);
 
 /* dst[c][r] = src[r][c] for a bf16 matrix of rows x cols (multiples of 8),

@@ -1,9 +1,11 @@
 """bf16 GEMM on MFMA (agk_gemm_bf16) and the bf16 transpose, through the C ABI.
 
-GPU: every operand layout, with and without workspace (the direct-to-LDS
-kernel and the staging kernel), the k- and row-scales, fp32 and bf16 output,
-accumulation and ragged sizes, each against a plain PyTorch fp32 product of
-the same bf16 operands; transposes bit-exact; repeated calls bit-identical.
+GPU: every operand layout (the direct-to-LDS kernel reads k-contiguous operands
+with 16-byte LDS reads and k-strided ones with transposing reads; K not a
+multiple of 64 and the k-scale take the register-staged kernel), the k- and
+row-scales, fp32 and bf16 output, accumulation and ragged sizes, each against a
+plain PyTorch fp32 product of the same bf16 operands; transposes bit-exact;
+repeated calls bit-identical; the four layouts of one product bit-identical.
 CPU: argument validation and the workspace rule.
 """
 import pytest
@@ -30,10 +32,11 @@ def test_gemm_argument_validation():
     assert call(ldc=32) == 1                           # ldc < N
     assert call(a=FAKE + 4) == 1                       # A not 16-byte aligned
     ws = lib.agk_gemm_bf16_workspace_bytes
-    assert ws(8192, 11008, 4096, 0, 1) == 0            # already k-contiguous
-    assert ws(8192, 11008, 4096, 0, 0) == 11008 * 4096 * 2
-    assert ws(4096, 11008, 8192, 1, 0) == (4096 + 11008) * 8192 * 2
-    assert ws(64, 64, 72, 1, 0) == 0                   # K % 64: staged kernel, no workspace
+    # the direct kernel stages either operand layout itself: no layout needs a workspace
+    for ta in (0, 1):
+        for tb in (0, 1):
+            assert ws(8192, 11008, 4096, ta, tb) == 0
+    assert ws(64, 64, 72, 1, 0) == 0                   # K % 64: staged kernel
     t = lib.agk_transpose_bf16
     assert t(FAKE, 64, FAKE, 64, 64, 60, None) == 1    # cols not a multiple of 8
     assert t(FAKE, 64, FAKE, 32, 64, 64, None) == 1    # ld_dst < rows
@@ -51,8 +54,8 @@ def _ref(a, b, ta, tb, ks, rs):
     return C
 
 
-# K / 32 = 2, 4, 6, 10, 14, 32 on the direct-to-LDS kernel (K a multiple of 64):
-# every remainder of its four-stage loop, with ragged M and N tiles.
+# K / 64 = 1, 2, 3, 5, 7, 16 on the direct-to-LDS kernel (K a multiple of 64):
+# odd and even tile counts of its peeled two-stage loop, with ragged M and N tiles.
 CASES = [(256, 256, 64), (264, 520, 72), (8, 8, 8), (1000, 1032, 520), (512, 768, 1024),
          (136, 264, 192), (264, 520, 128), (520, 264, 320), (200, 136, 448)]
 
@@ -120,3 +123,27 @@ def test_gemm_c5_shapes(cuda):
     cols = torch.randint(0, K, (16,), device=cuda)
     rdW = h[:, cols].float().t() @ dy.float()
     assert ((dW[cols] - rdW).abs().max() / rdW.abs().max()).item() <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(264, 520, 128), (520, 264, 320), (1000, 1032, 512)])
+@pytest.mark.parametrize("f32", [True, False])
+def test_gemm_layouts_bit_identical(cuda, M, N, K, f32):
+    """The same product with A and B in each storage layout: the k-strided operands are staged
+    as they lie and read with transposing LDS reads, the k-contiguous ones with plain reads; the
+    MFMAs see the same values in the same order, so all four results are bit-identical."""
+    import torch
+    torch.manual_seed(M + 3 * N + 7 * K)
+    a = torch.randn(M, K, device=cuda).bfloat16()      # [M, K]
+    b = torch.randn(N, K, device=cuda).bfloat16()      # [N, K]
+    at, bt = a.t().contiguous(), b.t().contiguous()    # [K, M], [K, N]
+    od = torch.float32 if f32 else torch.bfloat16
+    outs = [agk.gemm_bf16(a, b, trans_b=True, out_dtype=od),          # both k-contiguous
+            agk.gemm_bf16(at, b, trans_a=True, trans_b=True, out_dtype=od),
+            agk.gemm_bf16(a, bt, out_dtype=od),
+            agk.gemm_bf16(at, bt, trans_a=True, out_dtype=od)]          # both k-strided
+    torch.cuda.synchronize()
+    for c in outs[1:]:
+        assert torch.equal(c, outs[0])
+    r = a.float() @ b.float().t()
+    assert ((outs[0].float() - r).abs().max() / r.abs().max()).item() <= (1e-5 if f32 else 8e-3)
