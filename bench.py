@@ -544,8 +544,11 @@ def copy_probe(mib, steps):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed steps first (default 2000, ~1.8 s at c2): right after a "
+                         "high-power workload, such as the GEMM tests, the GPU needs a second or "
+                         "two of load to return to its steady clocks")
     ap.add_argument("--config", default=DEFAULT_CONFIG,
                     help="c1, c2 (default, the headline), c3, c4a, c4b, c4c, c5 (RMSNorm + "
                          "linear), or 'all'")
