@@ -56,10 +56,28 @@ def kernel_stats(stats_csv):
 
 
 def short_name(name):
-    """Library kernels (hipBLASLt's long tuned names) shortened for the tables."""
+    """Kernel names shortened for the tables: hipBLASLt's long tuned names, and full
+    (untruncated) device names cut to the kernel and its template arguments without
+    namespaces, e.g. "row_resident<BF16, 512, 2, 1, LseFwd>"."""
     if name.startswith(("Cijk_", "Custom_Cijk_")):
         return "hipBLASLt " + name.split("_MT")[0] + ("_MT" + name.split("_MT")[1][:12]
                                                       if "_MT" in name else "")
+    if name.startswith("void "):
+        name = name[len("void "):]
+    depth = 0
+    for i, ch in enumerate(name):  # drop the parameter list: the first '(' outside <...>
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    for ns in ("agk::rowops::", "agk_gemm::", "agk::", "at::native::"):
+        name = name.replace(ns, "")
+    if not name:
+        return "(torch, unnamed)"
+    if name.startswith(("vectorized_elementwise_kernel", "elementwise_kernel",
+                        "distribution_elementwise", "index_elementwise", "reduce_kernel")):
+        return "torch " + name.split("<")[0]  # input generation, not this build's kernels
     return name
 
 
