@@ -144,7 +144,7 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
  *      operands read with transposing LDS reads when kscale == NULL and
  *      K % 64 == 0; otherwise transposed in registers while staged), so
  *      agk_gemm_bf16_workspace_bytes is 0; the argument stays for callers.
- * A, B, kscale, workspace 16-byte aligned; M, N, K, lda, ldb multiples of 8;
+ * A, B, kscale 16-byte aligned; M, N, K, lda, ldb multiples of 8;
  * the result is deterministic (fixed accumulation order).                    */
 int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
                   int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
