@@ -656,6 +656,14 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     }
 }
 
+// C = 0 for an empty reduction (K == 0): rows of ldc, n columns of 4- or 2-byte
+// elements (a kernel, not a memset node, so that the call can be captured).
+__global__ __launch_bounds__(256) void zero_c_kernel(void* __restrict__ C, int64_t ldc, int n,
+                                                     int elem_bytes) {
+    char* p = static_cast<char*>(C) + static_cast<int64_t>(blockIdx.x) * ldc * elem_bytes;
+    for (int64_t i = threadIdx.x; i < static_cast<int64_t>(n) * elem_bytes; i += 256) p[i] = 0;
+}
+
 // ---- transpose ----------------------------------------------------------------
 // dst[c][r] = src[r][c] for a rows x cols bf16 matrix (rows, cols multiples of
 // 8).  A 256-lane workgroup moves a 128 x 128 tile: each lane reads an 8 x 8
@@ -795,7 +803,16 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
         return AGK_EINVAL;
     if (c_dtype != AGK_F32 && c_dtype != AGK_BF16) return AGK_EDTYPE;
     if (M == 0 || N == 0) return AGK_OK;
-    if (!A || !B || !C) return AGK_EINVAL;
+    if (!C || ldc < N) return AGK_EINVAL;
+    if (K == 0) {  // empty reduction (A and B may be null): C = 0, or C as it was
+        if (accumulate) return AGK_OK;
+        (void)hipGetLastError();
+        hipLaunchKernelGGL(zero_c_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(stream), C, ldc,
+                           static_cast<int>(N), c_dtype == AGK_F32 ? 4 : 2);
+        return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
+    }
+    if (!A || !B) return AGK_EINVAL;
     // 16-byte vector accesses along the contiguous dimension of each operand
     if ((M | N | K) % 8 != 0) return AGK_EINVAL;
     if (lda % 8 || ldb % 8 || ldc < N) return AGK_EINVAL;

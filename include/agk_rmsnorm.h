@@ -145,7 +145,9 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
  *      K % 64 == 0; otherwise transposed in registers while staged), so
  *      agk_gemm_bf16_workspace_bytes is 0; the argument stays for callers.
  * A, B, kscale 16-byte aligned; M, N, K, lda, ldb multiples of 8;
- * the result is deterministic (fixed accumulation order).                    */
+ * the result is deterministic (fixed accumulation order).
+ * M == 0 or N == 0 is a no-op; K == 0 (an empty sum, A and B may be NULL)
+ * writes zeros to C, or leaves C as it is when accumulating.                */
 int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
                   int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
                   int64_t K, const float* kscale, const float* rowscale, int accumulate,

@@ -31,6 +31,11 @@ def test_gemm_argument_validation():
     assert call(lda=60) == 1                           # lda < K
     assert call(ldc=32) == 1                           # ldc < N
     assert call(a=FAKE + 4) == 1                       # A not 16-byte aligned
+    # K == 0: an empty sum; accumulating into C leaves it as it is (no launch),
+    # C itself is still required and checked
+    assert g(None, 0, 0, None, 64, 0, FAKE, 64, 0, 64, 64, 0, None, None, 1, None, 0, None) == 0
+    assert g(None, 0, 0, None, 64, 0, None, 64, 0, 64, 64, 0, None, None, 1, None, 0, None) == 1
+    assert g(None, 0, 0, None, 64, 0, FAKE, 32, 0, 64, 64, 0, None, None, 0, None, 0, None) == 1
     ws = lib.agk_gemm_bf16_workspace_bytes
     # the direct kernel stages either operand layout itself: no layout needs a workspace
     for ta in (0, 1):
@@ -147,3 +152,22 @@ def test_gemm_layouts_bit_identical(cuda, M, N, K, f32):
         assert torch.equal(c, outs[0])
     r = a.float() @ b.float().t()
     assert ((outs[0].float() - r).abs().max() / r.abs().max()).item() <= (1e-5 if f32 else 8e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0)])
+def test_gemm_empty_reduction(cuda, ta, tb):
+    """K == 0: the product is zero; with accumulation C is left as it was."""
+    import torch
+    M, N = 264, 136
+    a = torch.empty((0, M) if ta else (M, 0), device=cuda, dtype=torch.bfloat16)
+    b = torch.empty((N, 0) if tb else (0, N), device=cuda, dtype=torch.bfloat16)
+    for od in (torch.float32, torch.bfloat16):
+        c = agk.gemm_bf16(a, b, c=torch.full((M, N), 7.0, device=cuda).to(od),
+                          trans_a=bool(ta), trans_b=bool(tb))
+        base = torch.randn(M, N, device=cuda).to(od)
+        c2 = agk.gemm_bf16(a, b, c=base.clone(), trans_a=bool(ta), trans_b=bool(tb),
+                           accumulate=True)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(c).item() == 0
+        assert torch.equal(c2, base)
