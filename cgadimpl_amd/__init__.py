@@ -43,6 +43,8 @@ SIGNATURES = {
     "agk_mul_rowbcast_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_mul_rowbcast_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
                                             ctypes.c_int, ctypes.c_int, _P]),
+    "agk_rms_mul_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64,
+                                       _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_gemm_bf16": (ctypes.c_int, [_P, _I64, ctypes.c_int, _P, _I64, ctypes.c_int, _P, _I64,
                                      ctypes.c_int, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P,
                                      ctypes.c_size_t, _P]),
@@ -288,6 +290,34 @@ def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate=False, want_da: bool
                                     ws_bytes, rows, cols, _dtype_code(a), acc, _stream(stream))
     _check(rc, "agk_mul_rowbcast_bwd")
     return da, db
+
+
+def rms_mul_bwd(x, gamma, inv_rms, gy, dx=None, dgamma=None, accumulate=False,
+                want_dx: bool = True, want_dgamma: bool = True, stream=None):
+    """Both VJPs of y = rms(x) * gamma in one pass (agk_rms_mul_bwd).
+
+    Returns (dr, dx, dgamma): dr = gy * gamma (the gradient of rms(x)), dx and
+    dgamma as mul_rowbcast_bwd followed by rmsnorm_bwd(gamma=None) on dr give
+    them, bit for bit.  inv_rms comes from rmsnorm_fwd(x, None, eps).
+    """
+    torch = _torch()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    acc = _accum_flags(accumulate)
+    dr = torch.empty_like(x)
+    if want_dx and dx is None:
+        dx = torch.empty_like(x) if not acc & AGK_ACCUM_DX else torch.zeros_like(x)
+    if want_dgamma and dgamma is None:
+        dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
+    ws = None
+    ws_bytes = int(lib().agk_rmsnorm_bwd_workspace_bytes(rows, cols)) if dgamma is not None else 0
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    rc = lib().agk_rms_mul_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(gy), _ptr(dr), _ptr(dx),
+                               _ptr(dgamma), _ptr(ws), ws_bytes, rows, cols, _dtype_code(x), acc,
+                               _stream(stream))
+    _check(rc, "agk_rms_mul_bwd")
+    return dr, dx, dgamma
 
 
 # ---- the RMSNorm + linear layer (configuration c5) --------------------------------

@@ -76,6 +76,9 @@ struct Node : std::enable_shared_from_this<Node> {
 
     std::atomic<int> child_grad_count{0};
     std::mutex grad_mutex;
+    // Set during backward by a consumer's VJP that ran this node's VJP too
+    // (vjp_Mul on rms(x) * gamma); backward then skips this node's VJP once.
+    bool vjp_done = false;
 
     std::vector<HookFn> post_acc_grad_hooks;
     void register_hook(HookFn hook) { post_acc_grad_hooks.push_back(std::move(hook)); }
@@ -116,6 +119,10 @@ namespace debug {
 using NodeCreatedHook = void (*)(const std::shared_ptr<Node>&);
 void set_on_node_created(NodeCreatedHook hook);
 void on_node_created(const std::shared_ptr<Node>& n);
+// How many times backward has run the two VJPs of rms(x) * gamma as one pass
+// (vjp_Mul with agk_rms_mul_bwd) in this process; no reference counterpart.
+uint64_t fused_rms_mul_vjps();
+void count_fused_rms_mul_vjp();
 }  // namespace debug
 
 }  // namespace ag

@@ -89,17 +89,31 @@ void zero_grad(const Value& root) {
 
 namespace {
 
+thread_local bool t_in_backward = false;
+
+struct InBackward {
+    InBackward() { t_in_backward = true; }
+    ~InBackward() { t_in_backward = false; }
+};
+
 void run_node(Node* n) {
-    if (n->grad.defined()) {
+    if (n->vjp_done) {  // a consumer's VJP already ran this one
+        n->vjp_done = false;
+    } else if (n->grad.defined()) {
         VjpFn fn = vjp_lookup(n->op);
         if (fn) fn(n, n->grad);
     }
     for (auto& hook : n->post_acc_grad_hooks) hook(n);
 }
 
-void backward_parallel(const std::vector<Node*>& order, Node* root, hipStream_t stream) {
-    // consumers of each node that still have to run (reference: autodiff.cpp:37-49)
-    for (Node* n : order) n->child_grad_count = 0;
+// Sets every node's child_grad_count to the number of its consumers in
+// `order` that will run a VJP (reference: autodiff.cpp:37-49); returns how
+// many nodes will run.
+size_t count_consumers(const std::vector<Node*>& order) {
+    for (Node* n : order) {
+        n->child_grad_count = 0;
+        n->vjp_done = false;
+    }
     size_t pending = 0;
     for (Node* n : order) {
         if (!n->requires_grad()) continue;
@@ -107,6 +121,11 @@ void backward_parallel(const std::vector<Node*>& order, Node* root, hipStream_t 
         for (auto& p : n->inputs)
             if (p && p->requires_grad()) p->child_grad_count++;
     }
+    return pending;
+}
+
+void backward_parallel(const std::vector<Node*>& order, Node* root, hipStream_t stream) {
+    const size_t pending = count_consumers(order);
 
     std::mutex mu;
     std::condition_variable cv;
@@ -116,6 +135,7 @@ void backward_parallel(const std::vector<Node*>& order, Node* root, hipStream_t 
 
     auto worker = [&]() {
         StreamGuard guard(stream);
+        InBackward in_backward;
         for (;;) {
             Node* n = nullptr;
             {
@@ -173,11 +193,22 @@ void backward(const Value& root, const Tensor* grad_seed, bool enable_parallel) 
     r->grad_is_materialized_zero = false;
 
     if (!enable_parallel) {
-        for (auto it = order.rbegin(); it != order.rend(); ++it)
-            if ((*it)->requires_grad()) run_node(*it);
+        count_consumers(order);
+        InBackward in_backward;
+        for (auto it = order.rbegin(); it != order.rend(); ++it) {
+            Node* n = *it;
+            if (!n->requires_grad()) continue;
+            run_node(n);
+            for (auto& p : n->inputs)
+                if (p && p->requires_grad()) p->child_grad_count--;
+        }
         return;
     }
     backward_parallel(order, r, current_stream());
 }
+
+namespace internal {
+bool in_backward() { return t_in_backward; }
+}  // namespace internal
 
 }  // namespace ag

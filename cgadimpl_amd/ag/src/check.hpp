@@ -27,4 +27,8 @@ inline void agk_check(int rc, const char* what) {
 
 [[noreturn]] inline void fail(const std::string& msg) { throw std::runtime_error(msg); }
 
+// True on a thread while it runs ag::backward's VJPs: only there may a VJP
+// also run its producer's VJP (backward knows which consumers are still due).
+bool in_backward();
+
 }  // namespace ag::internal

@@ -100,8 +100,11 @@ std::vector<Node*> topo_from(Node* root) {
 namespace debug {
 namespace {
 NodeCreatedHook g_hook = nullptr;
+std::atomic<uint64_t> g_fused_rms_mul{0};
 }
 void set_on_node_created(NodeCreatedHook hook) { g_hook = hook; }
+uint64_t fused_rms_mul_vjps() { return g_fused_rms_mul.load(); }
+void count_fused_rms_mul_vjp() { g_fused_rms_mul.fetch_add(1); }
 void on_node_created(const std::shared_ptr<Node>& n) {
     if (g_hook) g_hook(n);
 }

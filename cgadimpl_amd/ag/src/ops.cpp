@@ -23,6 +23,7 @@
 // tape, child_grad_count, the node-created hook); each VJP adds its
 // contribution into the inputs' gradients under their mutexes, with the
 // addition done by the kernel (see Node::grad_for_write).
+#include <algorithm>
 #include <mutex>
 
 #include "ag/autodiff.hpp"
@@ -74,15 +75,20 @@ void check_upstream(const Node* n, const Tensor& gy, const char* op) {
 
 // Locks the gradient mutexes of up to two (possibly identical) nodes.
 struct GradLocks {
-    std::unique_lock<std::mutex> a, b;
-    GradLocks(Node* x, Node* y) {
-        if (x == y || !y) {
-            a = std::unique_lock<std::mutex>(x->grad_mutex);
-        } else {
-            a = std::unique_lock<std::mutex>(x->grad_mutex, std::defer_lock);
-            b = std::unique_lock<std::mutex>(y->grad_mutex, std::defer_lock);
-            std::lock(a, b);
-        }
+    std::unique_lock<std::mutex> l[3];
+    GradLocks(Node* x, Node* y, Node* z = nullptr) {
+        Node* u[3];
+        int n = 0;
+        for (Node* p : {x, y, z})
+            if (p && std::find(u, u + n, p) == u + n) u[n++] = p;
+        for (int i = 0; i < n; ++i)
+            l[i] = std::unique_lock<std::mutex>(u[i]->grad_mutex, std::defer_lock);
+        if (n == 1)
+            l[0].lock();
+        else if (n == 2)
+            std::lock(l[0], l[1]);
+        else if (n == 3)
+            std::lock(l[0], l[1], l[2]);
     }
 };
 
@@ -309,6 +315,48 @@ void vjp_RMSNormAffine(Node* n, const Tensor& gy) {
     // ws returns to the pool on the same stream, after the kernels that use it
 }
 
+// The unfused layer y = rms(x) * gamma, from vjp_Mul with F = rms(x) (the full
+// operand) and Rw = gamma (the broadcast row).  During backward, when this Mul
+// is the last consumer of F still due and F has no gradient yet, F's gradient
+// is final once this VJP has written it, so F's own VJP (vjp_RMSNorm) can run
+// here in the same pass over the rows: agk_rms_mul_bwd reads x and gy once
+// and writes F.grad = gy*gamma, X.grad (+)= and Rw.grad (+)= exactly the
+// values the two VJPs write one after the other.  backward then skips F's
+// VJP.  Returns false (nothing done) when the pattern does not apply.
+static bool vjp_mul_of_rms(Node* F, Node* Rw, const Tensor& gy, bool want_row) {
+    if (!internal::in_backward() || F->op != Op::RMSNorm || F->inputs.size() != 1 ||
+        F->tape.empty() || F->vjp_done || F->child_grad_count.load() != 1)
+        return false;
+    Node* X = F->inputs[0].get();
+    if (!X || X == Rw || X == F || !X->requires_grad()) return false;
+    GradLocks lock(F, Rw, X);
+    if (F->grad.defined() && !F->grad_is_materialized_zero) return false;  // not the only one
+    const Tensor& x = X->value;
+    const Tensor& row = Rw->value;
+    const Tensor& inv = *F->tape[0];
+    bool a = false;
+    void* dr = F->grad_for_write(F->value.dtype(), &a).data();  // overwritten (a is false)
+    int acc = AGK_ACCUM_NONE;
+    void* dx = X->grad_for_write(x.dtype(), &a).data();
+    if (a) acc |= AGK_ACCUM_DX;
+    float* drow = nullptr;
+    std::unique_ptr<Storage> ws;
+    size_t ws_bytes = 0;
+    if (want_row) {
+        drow = static_cast<float*>(Rw->grad_for_write(Dtype::Float32, &a).data());
+        if (a) acc |= AGK_ACCUM_DGAMMA;
+        ws_bytes = agk_rmsnorm_bwd_workspace_bytes(x.rows(), x.cols());
+        ws = std::make_unique<Storage>(ws_bytes, current_stream());
+    }
+    agk_check(agk_rms_mul_bwd(x.data(), row.data(), static_cast<const float*>(inv.data()),
+                              gy.data(), dr, dx, drow, ws ? ws->data() : nullptr, ws_bytes,
+                              x.rows(), x.cols(), agk_dtype_of(x.dtype()), acc, stream_arg()),
+              "vjp_Mul (rms(x) * gamma)");
+    F->vjp_done = true;
+    debug::count_fused_rms_mul_vjp();
+    return true;
+}
+
 // A.grad += gy * B,  B.grad += reduce_for_broadcast(gy * A)   (autodiff_vjp_ops.cpp:54-59)
 void vjp_Mul(Node* n, const Tensor& gy) {
     Node* A = n->inputs[0].get();
@@ -320,8 +368,8 @@ void vjp_Mul(Node* n, const Tensor& gy) {
     const Tensor& av = A->value;
     const Tensor& bv = B->value;
     const int dt = agk_dtype_of(av.dtype());
-    GradLocks lock(A, B);
     if (av.shape() == bv.shape()) {
+        GradLocks lock(A, B);
         // equal shapes: dA = gy * B and dB = gy * A, both element-wise, each in
         // its operand's dtype (one launch per gradient; A == B adds twice)
         const int64_t cnt = av.numel();
@@ -351,6 +399,8 @@ void vjp_Mul(Node* n, const Tensor& gy) {
     const Tensor& row = Rw->value;
     const bool want_full = F->requires_grad();
     const bool want_row = Rw->requires_grad();
+    if (want_full && vjp_mul_of_rms(F, Rw, gy, want_row)) return;
+    GradLocks lock(F, Rw);
     int acc = AGK_ACCUM_NONE;
     void* dfull = nullptr;
     float* drow = nullptr;

@@ -48,7 +48,10 @@ namespace agk {
 // lane holds NV 16-byte slots of its row (columns (t + k*TPR)*W .. +W).
 // gamma == nullptr: no scale.  Requires 16-byte aligned x/y/gamma,
 // cols % S::kVec == 0 and cols <= TPR * NV * kVec.
-template <class S, int TPR, int NV, int G>
+//
+// MUL: the broadcast multiply y = x * gamma on the same launch shape (the
+// unfused layer's Mul): no row sum, no inv_rms.
+template <class S, int TPR, int NV, int G, bool MUL = false>
 __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     typename S::T* __restrict__ y, float* __restrict__ inv_rms, int64_t rows, int cols,
@@ -75,15 +78,20 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
 #pragma unroll
         for (int e = 0; e < W; ++e) part[e] += f[e] * f[e];
     }
-    float ss = 0.0f;
+    float r = 1.0f;
+    if constexpr (!MUL) {
+        float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < W; ++e) ss += part[e];
-    ss = row_sum<TPR, G>(ss, red, 0);
-
-    const float ms = ss / static_cast<float>(cols);
-    const float r = 1.0f / sqrtf(ms + eps);
+        for (int e = 0; e < W; ++e) ss += part[e];
+        ss = row_sum<TPR, G>(ss, red, 0);
+        const float ms = ss / static_cast<float>(cols);
+        r = 1.0f / sqrtf(ms + eps);
+    } else {
+        (void)red;
+        (void)eps;
+    }
     if (!active) return;
-    if (t == 0) inv_rms[row] = r;
+    if (!MUL && t == 0) inv_rms[row] = r;
 
     T* yr = y + row * static_cast<int64_t>(cols);
 #pragma unroll
@@ -92,7 +100,12 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
         if (col < cols) {
             float f[W];
             S::unpack(xv[k], f);
-            if (gamma) {
+            if (MUL) {
+                float gm[W];
+                S::unpack(load16<S>(gamma + col), gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) f[e] = f[e] * gm[e];
+            } else if (gamma) {
                 float gm[W];
                 S::unpack(load16<S>(gamma + col), gm);
 #pragma unroll
@@ -140,9 +153,19 @@ struct BwdSet {
     float r;
 };
 
-// MUL: the broadcast multiply's VJP on the same skeleton (x = a, gamma = b,
-// dy = gy): da = gy*b, db += gy*a, no row reduction and no inv_rms (r = 1).
-template <class S, int TPR, int NV, int G, bool ACC, bool MUL>
+// What one instantiation of the skeleton computes (template argument KIND):
+//   kBwdRms     the RMSNorm VJP above (gamma optional);
+//   kBwdMul     the broadcast multiply's VJP (x = a, gamma = b, dy = gy):
+//               da = gy*b, db += gy*a, no row reduction and no inv_rms (r = 1);
+//   kBwdRmsMul  both VJPs of the composition y = rms(x) * gamma, back to back:
+//               g = gy*gamma rounded to storage (written to dr, the gradient
+//               of rms(x)), dx (+)= r*(g - x*(r*r*sum(g*x)/cols)), and
+//               dgamma += gy*h with h = x*r rounded to storage (rms(x) as the
+//               forward stored it).  Every value and every summation order is
+//               the one the two separate calls produce.
+enum : int { kBwdRms = 0, kBwdMul = 1, kBwdRmsMul = 2 };
+
+template <class S, int TPR, int NV, int G, bool ACC, int KIND>
 struct BwdCtx {
     using T = typename S::T;
     static constexpr int W = S::kVec;
@@ -152,9 +175,10 @@ struct BwdCtx {
     const float* inv_rms;
     const T* dy;
     T* dx;
+    T* dr;  // kBwdRmsMul: the gradient of rms(x)
     int64_t rows, first, stride;
     int cols, wgrp0;
-    uint32_t row_bytes, x_bytes, old_bytes, dx_bytes, roff;
+    uint32_t row_bytes, x_bytes, old_bytes, dx_bytes, dr_bytes, roff;
     uint32_t off[NV];
     float inv_cols;
 
@@ -184,15 +208,29 @@ struct BwdCtx {
 #pragma unroll
             for (int k = 0; k < NV; ++k) b.ov[k] = bload16_stream(ro, off[k]);
         }
-        if constexpr (MUL)
+        if constexpr (KIND == kBwdMul)
             b.r = 1.0f;
         else
             b.r = bload_f32(make_rsrc(inv_rms + r0, n * 4u), roff);
     }
 };
 
-template <class S, int TPR, int NV, int G, bool ACC, bool MUL>
-__device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL>& c,
+// g = dy*gamma for kBwdRmsMul: rounded to storage and kept out of any fused
+// multiply-add, as the separate multiply's VJP stores it.
+template <class S>
+__device__ __forceinline__ void stored_product(float (&f)[S::kVec], const float (&gm)[S::kVec],
+                                               u32x4& q) {
+    constexpr int W = S::kVec;
+#pragma unroll
+    for (int e = 0; e < W; ++e) f[e] = f[e] * gm[e];
+    q = S::pack(f);
+    S::unpack(q, f);
+#pragma unroll
+    for (int e = 0; e < W; ++e) asm("" : "+v"(f[e]));
+}
+
+template <class S, int TPR, int NV, int G, bool ACC, int KIND>
+__device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, KIND>& c,
                                             BwdSet<S, NV, ACC>& b,
                                             int64_t step, int parity, const u32x4 (&gv)[NV],
                                             bool has_gamma, float (&dg)[NV][S::kVec],
@@ -200,6 +238,8 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL
     constexpr int W = S::kVec;
     const float r = b.r;
     float s = 0.0f;
+    constexpr bool MUL = KIND == kBwdMul;
+    constexpr bool COMP = KIND == kBwdRmsMul;
     if constexpr (!MUL) {
         float part[W];
 #pragma unroll
@@ -209,7 +249,12 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL
             float fx[W], fd[W];
             S::unpack(b.xv[k], fx);
             S::unpack(b.dv[k], fd);
-            if (has_gamma) {
+            if constexpr (COMP) {
+                float gm[W];
+                u32x4 q;
+                S::unpack(gv[k], gm);
+                stored_product<S>(fd, gm, q);
+            } else if (has_gamma) {
                 float gm[W];
                 S::unpack(gv[k], gm);
 #pragma unroll
@@ -237,12 +282,22 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL
     c.wave_rows(step, r0, n);
     const rsrc_t rdx = make_rsrc(c.dx ? c.dx + r0 * static_cast<int64_t>(c.cols) : c.dx,
                                  n * c.dx_bytes);
+    const rsrc_t rdr = make_rsrc(c.dr ? c.dr + r0 * static_cast<int64_t>(c.cols) : c.dr,
+                                 n * c.dr_bytes);  // used by kBwdRmsMul only
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         float fx[W], fd[W], gk[W], o[W];
         S::unpack(b.xv[k], fx);
         S::unpack(b.dv[k], fd);
-        if (has_gamma) {
+        if constexpr (COMP) {
+            float gm[W];
+            u32x4 q;
+            S::unpack(gv[k], gm);
+#pragma unroll
+            for (int e = 0; e < W; ++e) gk[e] = fd[e];
+            stored_product<S>(gk, gm, q);
+            bstore16_stream(rdr, c.off[k], q);
+        } else if (has_gamma) {
             float gm[W];
             S::unpack(gv[k], gm);
 #pragma unroll
@@ -268,6 +323,13 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL
         if constexpr (MUL) {
 #pragma unroll
             for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * fx[e];
+        } else if constexpr (COMP) {
+            float h[W];
+#pragma unroll
+            for (int e = 0; e < W; ++e) h[e] = fx[e] * r;
+            S::unpack(S::pack(h), h);
+#pragma unroll
+            for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * h[e];
         } else {
 #pragma unroll
             for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
@@ -277,8 +339,8 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, MUL
 
 // Runs steps 0 .. steps-1 of c's row sequence with NSET (1 or 2) register
 // sets, adding each lane's dgamma terms into dg.
-template <class S, int TPR, int NV, int G, int NSET, bool ACC, bool MUL>
-__device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC, MUL>& c, int64_t steps,
+template <class S, int TPR, int NV, int G, int NSET, bool ACC, int KIND>
+__device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC, KIND>& c, int64_t steps,
                                             const u32x4 (&gv)[NV], bool has_gamma,
                                             float (&dg)[NV][S::kVec],
                                             float (*red)[TPR > 64 ? G * (TPR / 64) : 1]) {
@@ -344,12 +406,12 @@ __device__ __forceinline__ void bwd_write_partial(float* __restrict__ prow, int 
 
 // Rows are dealt round-robin to the gridDim.x workgroups; workgroup b writes
 // partial row b.
-template <class S, int TPR, int NV, int G, int NSET, bool ACC, bool MUL>
+template <class S, int TPR, int NV, int G, int NSET, bool ACC, int KIND>
 __device__ __forceinline__ void bwd_resident_body(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
-    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
-    float (*red)[TPR > 64 ? G * (TPR / 64) : 1], float* lds_part) {
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ partials,
+    int64_t rows, int cols, float (*red)[TPR > 64 ? G * (TPR / 64) : 1], float* lds_part) {
     using T = typename S::T;
     constexpr int W = S::kVec;
     constexpr int RPW = TPR >= 64 ? 1 : 64 / TPR;
@@ -360,12 +422,13 @@ __device__ __forceinline__ void bwd_resident_body(
     const int grp = threadIdx.x / TPR;
     const int sub = TPR >= 64 ? 0 : lane / TPR;  // the lane's row among the wave's rows
 
-    BwdCtx<S, TPR, NV, G, ACC, MUL> c;
+    BwdCtx<S, TPR, NV, G, ACC, KIND> c;
     c.x = x;
     c.gamma = gamma;
     c.inv_rms = inv_rms;
     c.dy = dy;
     c.dx = dx;
+    c.dr = dr;
     c.rows = rows;
     c.first = static_cast<int64_t>(blockIdx.x) * G;
     c.stride = static_cast<int64_t>(gridDim.x) * G;
@@ -375,6 +438,7 @@ __device__ __forceinline__ void bwd_resident_body(
     c.x_bytes = x ? c.row_bytes : 0u;
     c.old_bytes = dx ? c.row_bytes : 0u;
     c.dx_bytes = dx ? c.row_bytes : 0u;
+    c.dr_bytes = dr ? c.row_bytes : 0u;
     c.roff = static_cast<uint32_t>(sub) * 4u;
     c.inv_cols = 1.0f / static_cast<float>(cols);
 #pragma unroll
@@ -399,7 +463,7 @@ __device__ __forceinline__ void bwd_resident_body(
         for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
 
     const int64_t steps = c.first < rows ? (rows - c.first + c.stride - 1) / c.stride : 0;
-    bwd_segment<S, TPR, NV, G, NSET, ACC, MUL>(c, steps, gv, has_gamma, dg, red);
+    bwd_segment<S, TPR, NV, G, NSET, ACC, KIND>(c, steps, gv, has_gamma, dg, red);
     if (partials)
         bwd_write_partial<S, TPR, NV, G>(partials + static_cast<int64_t>(blockIdx.x) * cols, cols,
                                          t, grp, dg, lds_part);
@@ -413,8 +477,22 @@ __global__ __launch_bounds__(TPR * G) void rms_bwd_resident(
     typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols) {
     __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
     extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
-    bwd_resident_body<S, TPR, NV, G, NSET, ACC, false>(x, gamma, inv_rms, dy, dx, partials, rows,
-                                                       cols, red, lds_part);
+    bwd_resident_body<S, TPR, NV, G, NSET, ACC, kBwdRms>(x, gamma, inv_rms, dy, dx, nullptr,
+                                                         partials, rows, cols, red, lds_part);
+}
+
+// The composition y = rms(x) * gamma (kBwdRmsMul): dr = gy*gamma, dx (+)=
+// the RMSNorm VJP of dr, dgamma partials of gy*rms(x).  gamma is required.
+template <class S, int TPR, int NV, int G, int NSET, bool ACC>
+__global__ __launch_bounds__(TPR * G) void rms_mul_bwd_resident(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ gy,
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ partials,
+    int64_t rows, int cols) {
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
+    extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
+    bwd_resident_body<S, TPR, NV, G, NSET, ACC, kBwdRmsMul>(x, gamma, inv_rms, gy, dx, dr,
+                                                            partials, rows, cols, red, lds_part);
 }
 
 // Broadcast multiply backward (vjp_Mul with reduce_for_broadcast): da (+)=
@@ -426,8 +504,8 @@ __global__ __launch_bounds__(TPR * G) void mul_rowbcast_bwd_resident(
     float* __restrict__ partials, int64_t rows, int cols) {
     __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
     extern __shared__ float lds_part[];  // [G][cols] when G > 1 and partials
-    bwd_resident_body<S, TPR, NV, G, NSET, ACC, true>(a, b, nullptr, gy, da, partials, rows, cols,
-                                                      red, lds_part);
+    bwd_resident_body<S, TPR, NV, G, NSET, ACC, kBwdMul>(a, b, nullptr, gy, da, nullptr, partials,
+                                                         rows, cols, red, lds_part);
 }
 
 // ---- looped kernels (any alignment, any width) --------------------------------
@@ -459,12 +537,15 @@ __global__ __launch_bounds__(kBlock) void rms_fwd_looped(
     }
 }
 
+// With dr (the composition y = rms(x) * gamma, gamma required): g = dy*gamma
+// rounded to storage is written to dr, and the dgamma term is dy*h with
+// h = x*r rounded to storage, as the separate multiply's VJP computes them.
 template <class S>
 __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
-    typename S::T* __restrict__ dx, float* __restrict__ partials, int64_t rows, int cols,
-    int64_t rpb, int acc_dx) {
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ partials,
+    int64_t rows, int cols, int64_t rpb, int acc_dx) {
     __shared__ float red[2][kBlock / 64];
     const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
@@ -480,6 +561,7 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
             for (int c = threadIdx.x; c < cols; c += kBlock) {
                 float g = S::get(dy + off + c);
                 if (gamma) g = g * S::get(gamma + c);
+                if (dr) g = S::stored(g);
                 dot += g * S::get(x + off + c);
             }
             dot = row_sum<kBlock, 1>(dot, red, parity);
@@ -489,14 +571,18 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
         for (int c = threadIdx.x; c < cols; c += kBlock) {
             const float xv = S::get(x + off + c);
             const float d = S::get(dy + off + c);
+            float g = gamma ? d * S::get(gamma + c) : d;
+            if (dr) {
+                g = S::stored(g);
+                S::put(dr + off + c, g);
+            }
             if (dx) {
-                const float g = gamma ? d * S::get(gamma + c) : d;
                 float o = r * (g - xv * s);
                 if (acc_dx) o = acc_add(S::get(dx + off + c), o);
                 S::put(dx + off + c, o);
             }
             if (prow) {
-                const float t = d * (xv * r);
+                const float t = d * (dr ? S::stored(xv * r) : xv * r);
                 prow[c] = first ? t : prow[c] + t;
             }
         }
@@ -708,6 +794,38 @@ int launch_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_
     return launch_fwd_plan<S>(p, x, gamma, y, inv_rms, rows, cols, eps, st);
 }
 
+// y = a * b (b broadcast over rows): the forward's resident launch shape when
+// rows are aligned and fit, else one workgroup per row.
+template <class S>
+int launch_mul_fwd(const void* a, const void* b, void* y, int64_t rows, int cols,
+                   hipStream_t st) {
+    using T = typename S::T;
+    const T* ap = static_cast<const T*>(a);
+    const T* bp = static_cast<const T*>(b);
+    T* yp = static_cast<T*>(y);
+    const bool vec = (cols % S::kVec) == 0 && aligned16(a) && aligned16(b) && aligned16(y);
+    Plan p;
+    if (vec) p = fwd_plan(cols / S::kVec, rows);
+    if (p.tpr == 0) {
+        if (rows > 0x7fffffffLL) return AGK_EINVAL;
+        hipLaunchKernelGGL(mul_rowbcast_fwd_kernel<S>, dim3(static_cast<unsigned>(rows)),
+                           dim3(kBlock), 0, st, ap, bp, yp, rows, cols, vec ? 1 : 0);
+        return check_launch();
+    }
+    const int64_t grid = (rows + p.g - 1) / p.g;
+    if (grid > 0x7fffffffLL) return AGK_EINVAL;
+#define AGK_X(a_, b_, c_)                                                                 \
+    if (p.tpr == a_ && p.nv == b_ && p.g == c_) {                                         \
+        hipLaunchKernelGGL((rms_fwd_resident<S, a_, b_, c_, true>),                       \
+                           dim3(static_cast<unsigned>(grid)), dim3(a_ * c_), 0, st, ap, bp, \
+                           yp, nullptr, rows, cols, 0.0f);                                \
+        return check_launch();                                                            \
+    }
+    AGK_FWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
 template <class S, bool ACC>
 int launch_bwd_resident(const Plan& p, int64_t nblk, const void* x, const void* gamma,
                         const float* inv_rms, const void* dy, void* dx, float* partials,
@@ -778,20 +896,59 @@ inline Plan bwd_plan_for(const void* x, const void* gamma, const void* dy, const
     return p;
 }
 
+template <class S, bool ACC>
+int launch_rms_mul_bwd_resident(const Plan& p, int64_t nblk, const void* x, const void* gamma,
+                                const float* inv_rms, const void* gy, void* dx, void* dr,
+                                float* partials, int64_t rows, int cols, hipStream_t st) {
+    using T = typename S::T;
+    const T* xp = static_cast<const T*>(x);
+    const T* gp = static_cast<const T*>(gamma);
+    const T* gyp = static_cast<const T*>(gy);
+    T* dxp = static_cast<T*>(dx);
+    T* drp = static_cast<T*>(dr);
+    const size_t lds = (partials && p.g > 1) ? static_cast<size_t>(p.g) * cols * 4 : 0;
+#define AGK_X(a, b, c, d)                                                                  \
+    if constexpr (bwd_shape_enabled<S>(a, b)) {                                            \
+        if (p.tpr == a && p.nv == b && p.g == c) {                                         \
+            hipLaunchKernelGGL((rms_mul_bwd_resident<S, a, b, c, bwd_sets<S>(b, d), ACC>), \
+                               dim3(static_cast<unsigned>(nblk)), dim3(a * c), lds, st, xp, \
+                               gp, inv_rms, gyp, dxp, drp, partials, rows, cols);           \
+            return check_launch();                                                         \
+        }                                                                                  \
+    }
+    AGK_BWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
+// dr == nullptr: the RMSNorm VJP (gamma optional); dr != nullptr: the
+// composition rms(x) * gamma (gamma required), dr receiving gy*gamma.
 template <class S>
 int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
-               void* dx, float* partials, int64_t rows, int cols, int accumulate,
+               void* dx, void* dr, float* partials, int64_t rows, int cols, int accumulate,
                hipStream_t st, int64_t& nblk) {
     using T = typename S::T;
     int64_t rpb = 0;
-    const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    if (dr && p.tpr != 0 && !aligned16(dr)) {  // the looped kernel, with its own row blocking
+        p = Plan{};
+        rpb = bwd_rows_per_block(rows);
+        nblk = bwd_num_blocks(rows);
+    }
     if (nblk > 0x7fffffffLL) return AGK_EINVAL;
     if (p.tpr == 0) {
         hipLaunchKernelGGL(rms_bwd_looped<S>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0,
                            st, static_cast<const T*>(x), static_cast<const T*>(gamma), inv_rms,
-                           static_cast<const T*>(dy), static_cast<T*>(dx), partials, rows, cols,
-                           rpb, accumulate);
+                           static_cast<const T*>(dy), static_cast<T*>(dx), static_cast<T*>(dr),
+                           partials, rows, cols, rpb, accumulate);
         return check_launch();
+    }
+    if (dr) {
+        if (accumulate && dx)
+            return launch_rms_mul_bwd_resident<S, true>(p, nblk, x, gamma, inv_rms, dy, dx, dr,
+                                                        partials, rows, cols, st);
+        return launch_rms_mul_bwd_resident<S, false>(p, nblk, x, gamma, inv_rms, dy, dx, dr,
+                                                     partials, rows, cols, st);
     }
     if (accumulate && dx)
         return launch_bwd_resident<S, true>(p, nblk, x, gamma, inv_rms, dy, dx, partials, rows,
@@ -867,10 +1024,42 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     }
     const int c = static_cast<int>(cols);
     int64_t nblk = 0;
-    int rc = dtype == AGK_F32
-                 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st, nblk)
-                 : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, partials, rows, c, acc_dx, st,
-                                    nblk);
+    int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, partials,
+                                                rows, c, acc_dx, st, nblk)
+                              : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
+                                                 rows, c, acc_dx, st, nblk);
+    if (rc != AGK_OK || !dgamma) return rc;
+    return launch_finalize(partials, dgamma, nblk, c, acc_dg, st);
+}
+
+int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms, const void* gy,
+                    void* dr, void* dx, float* dgamma, void* workspace, size_t workspace_bytes,
+                    int64_t rows, int64_t cols, int dtype, int accumulate, agk_stream_t stream) {
+    using namespace agk;
+    if (int rc = check_sizes(rows, cols)) return rc;
+    if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    clear_pending_error();
+    if (accumulate & ~AGK_ACCUM_ALL) return AGK_EINVAL;
+    const int acc_dx = (accumulate & AGK_ACCUM_DX) != 0;
+    const int acc_dg = (accumulate & AGK_ACCUM_DGAMMA) != 0;
+    if (rows == 0 || cols == 0) {
+        if (dgamma && !acc_dg && cols > 0) return zero_fill(dgamma, cols, st);
+        return AGK_OK;
+    }
+    if (!x || !gamma || !inv_rms || !gy || !dr) return AGK_EINVAL;
+    float* partials = nullptr;
+    if (dgamma) {
+        const size_t need = agk_rmsnorm_bwd_workspace_bytes(rows, cols);
+        if (!workspace || workspace_bytes < need) return AGK_EWORKSPACE;
+        partials = static_cast<float*>(workspace);
+    }
+    const int c = static_cast<int>(cols);
+    int64_t nblk = 0;
+    int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, gy, dx, dr, partials, rows, c,
+                                                acc_dx, st, nblk)
+                              : launch_bwd<BF16>(x, gamma, inv_rms, gy, dx, dr, partials, rows,
+                                                 c, acc_dx, st, nblk);
     if (rc != AGK_OK || !dgamma) return rc;
     return launch_finalize(partials, dgamma, nblk, c, acc_dg, st);
 }
@@ -886,19 +1075,8 @@ int agk_mul_rowbcast_fwd(const void* a, const void* b, void* y, int64_t rows, in
     clear_pending_error();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int c = static_cast<int>(cols);
-    if (dtype == AGK_F32) {
-        const int vec = (c % F32::kVec) == 0 && aligned16(a) && aligned16(b) && aligned16(y);
-        hipLaunchKernelGGL(mul_rowbcast_fwd_kernel<F32>, dim3(static_cast<unsigned>(rows)),
-                           dim3(kBlock), 0, st, static_cast<const float*>(a),
-                           static_cast<const float*>(b), static_cast<float*>(y), rows, c, vec);
-    } else {
-        const int vec = (c % BF16::kVec) == 0 && aligned16(a) && aligned16(b) && aligned16(y);
-        hipLaunchKernelGGL(mul_rowbcast_fwd_kernel<BF16>, dim3(static_cast<unsigned>(rows)),
-                           dim3(kBlock), 0, st, static_cast<const uint16_t*>(a),
-                           static_cast<const uint16_t*>(b), static_cast<uint16_t*>(y), rows, c,
-                           vec);
-    }
-    return check_launch();
+    return dtype == AGK_F32 ? launch_mul_fwd<F32>(a, b, y, rows, c, st)
+                            : launch_mul_fwd<BF16>(a, b, y, rows, c, st);
 }
 
 size_t agk_mul_rowbcast_bwd_workspace_bytes(int64_t rows, int64_t cols) {

@@ -44,6 +44,11 @@ struct F32 {
     static constexpr int kVec = 4;  // elements per 16-byte slot
     __device__ static float get(const T* p) { return *p; }
     __device__ static void put(T* p, float v) { *p = v; }
+    // v as storage holds it, kept out of any fused multiply-add
+    __device__ static float stored(float v) {
+        asm("" : "+v"(v));
+        return v;
+    }
     __device__ static void unpack(u32x4 v, float (&f)[4]) {
         f[0] = __uint_as_float(v.x);
         f[1] = __uint_as_float(v.y);
@@ -64,6 +69,11 @@ struct BF16 {
     }
     __device__ static void put(T* p, float v) {
         *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+    __device__ static float stored(float v) {
+        v = __uint_as_float(f32_to_bf16_bits(v) << 16);
+        asm("" : "+v"(v));
+        return v;
     }
     __device__ static void unpack(u32x4 v, float (&f)[8]) {
 #pragma unroll

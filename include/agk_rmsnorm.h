@@ -125,6 +125,25 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
                          size_t workspace_bytes, int64_t rows, int64_t cols,
                          int dtype, int accumulate, agk_stream_t stream);
 
+/* Both VJPs of the unfused layer y = ag::rms(x) * gamma in one pass over the
+ * rows: vjp_Mul with reduce_for_broadcast (autodiff_vjp_ops.cpp:54-59,
+ * :15-35) followed by vjp_RMSNorm (autodiff_vjp_ops.cpp:368-377) on the
+ * gradient it produced.  With h = rms(x) = x * inv_rms (inv_rms from
+ * agk_rmsnorm_fwd with gamma == NULL):
+ *   dr = gy * gamma                 (overwritten: the gradient of h)
+ *   dx (+)= RMSNorm VJP of dr       (NULL to skip)
+ *   dgamma (+)= sum_rows gy * h     (fp32, NULL to skip)
+ * Every output is bit-identical to agk_mul_rowbcast_bwd(gy, h, gamma, dr,
+ * dgamma) followed by agk_rmsnorm_bwd(x, NULL, inv_rms, dr, dx) on the same
+ * inputs (same rounding of dr and h to storage, same summation orders), with
+ * x and dy read once instead of h, gy and dr twice.  accumulate:
+ * AGK_ACCUM_DX adds into dx, AGK_ACCUM_DGAMMA into dgamma; workspace as for
+ * agk_rmsnorm_bwd when dgamma != NULL.                                      */
+int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms,
+                    const void* gy, void* dr, void* dx, float* dgamma,
+                    void* workspace, size_t workspace_bytes, int64_t rows,
+                    int64_t cols, int dtype, int accumulate, agk_stream_t stream);
+
 /* bf16 GEMM on MFMA with fp32 accumulation, for the RMSNorm + linear layer:
  *   C[m, n] (+)= rowscale[m] * sum_k (A[m, k] * kscale[k]) * B[k, n]
  * Replaces the tensor-library matmul behind the reference's matmul node and

@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "ag/ag.hpp"
+#include "agk_rmsnorm.h"
 
 using namespace ag;
 
@@ -172,6 +173,134 @@ void test_fused_matches_unfused() {
            y3.val().to_host_f32() == y2.val().to_host_f32() &&
                x3.grad().to_host_f32() == x2.grad().to_host_f32() &&
                g3.grad().to_host_f32() == g2.grad().to_host_f32());
+}
+
+std::vector<uint16_t> to_bf16_bits(const std::vector<float>& v) {
+    std::vector<uint16_t> b(v.size());
+    for (size_t i = 0; i < v.size(); ++i) {
+        uint32_t u;
+        std::memcpy(&u, &v[i], 4);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        b[i] = static_cast<uint16_t>(u >> 16);
+    }
+    return b;
+}
+
+Tensor device(const std::vector<float>& v, const std::vector<int64_t>& shape, Dtype dt) {
+    if (dt == Dtype::Float32) return Tensor::from_host_f32(v, shape);
+    const std::vector<uint16_t> b = to_bf16_bits(v);
+    return Tensor::from_host(b.data(), shape, dt);
+}
+
+std::vector<char> bytes_of(const Tensor& t) {
+    std::vector<char> b(t.nbytes());
+    if (!b.empty()) t.copy_to_host(b.data());
+    return b;
+}
+
+// backward of rms(x) * gamma runs both VJPs in one pass (agk_rms_mul_bwd,
+// from vjp_Mul); every gradient it leaves (x, gamma and rms(x) itself) must be
+// bit-identical to the two separate kernels, agk_mul_rowbcast_bwd and then
+// agk_rmsnorm_bwd, on the same tensors.
+void composition_case(const char* name, int64_t R, int64_t D, Dtype dt, bool parallel,
+                      bool gamma_first, bool gamma_2d) {
+    const int dtc = dt == Dtype::Float32 ? AGK_F32 : AGK_BF16;
+    Tensor xt = device(normal(R * D, 40 + D, 2.0), {R, D}, dt);
+    Tensor gt = device(uniform(D, 41 + D, 0.5, 1.5), gamma_2d ? std::vector<int64_t>{1, D}
+                                                               : std::vector<int64_t>{D}, dt);
+    Tensor dy = device(normal(R * D, 42 + D), {R, D}, dt);
+    xt.set_requires_grad(true);
+    gt.set_requires_grad(true);
+    Value x = make_tensor(xt, "x"), g = make_tensor(gt, "gamma");
+    Value h = rms(x);
+    Value y = gamma_first ? g * h : h * g;
+    const uint64_t fused_before = debug::fused_rms_mul_vjps();
+    backward(y, &dy, parallel);
+    const bool fused = debug::fused_rms_mul_vjps() == fused_before + 1;
+
+    agk_stream_t st = reinterpret_cast<agk_stream_t>(current_stream());
+    const Tensor& inv = *h.node->tape[0];
+    Tensor dr = Tensor::empty({R, D}, dt), dx = Tensor::empty({R, D}, dt);
+    Tensor dg = Tensor::empty({D}, Dtype::Float32);
+    const size_t wsb = agk_rmsnorm_bwd_workspace_bytes(R, D);
+    Tensor ws = Tensor::empty({static_cast<int64_t>(wsb / 4) + 1}, Dtype::Float32);
+    const int rc1 = agk_mul_rowbcast_bwd(dy.data(), h.val().data(), g.val().data(), dr.data(),
+                                         static_cast<float*>(dg.data()), ws.data(), wsb, R, D,
+                                         dtc, 0, st);
+    const int rc2 = agk_rmsnorm_bwd(x.val().data(), nullptr, static_cast<const float*>(inv.data()),
+                                    dr.data(), dx.data(), nullptr, nullptr, 0, R, D, dtc, 0, st);
+    const bool same = rc1 == AGK_OK && rc2 == AGK_OK && bytes_of(h.grad()) == bytes_of(dr) &&
+                      bytes_of(x.grad()) == bytes_of(dx) && bytes_of(g.grad()) == bytes_of(dg);
+    report(name, fused && same,
+           std::string(fused ? "one pass" : "NOT fused") + (same ? ", bit-identical" : ", DIFFER"));
+}
+
+void test_composition_backward() {
+    composition_case("rms(x) * gamma backward, one pass == two VJPs (f32 [64,256])", 64, 256,
+                     Dtype::Float32, false, false, false);
+    composition_case("... parallel backward, gamma * rms(x), gamma [1, D]", 64, 256,
+                     Dtype::Float32, true, true, true);
+    composition_case("... f32 [300,4096] (several rows per workgroup)", 300, 4096,
+                     Dtype::Float32, false, false, false);
+    composition_case("... bf16 [96,1024]", 96, 1024, Dtype::BFloat16, false, false, false);
+    composition_case("... bf16 [40,8192]", 40, 8192, Dtype::BFloat16, true, false, false);
+    composition_case("... f32 [33,250] (looped kernel: rows not a multiple of 16 bytes)", 33, 250,
+                     Dtype::Float32, false, false, false);
+    composition_case("... bf16 [17,100] (looped kernel)", 17, 100, Dtype::BFloat16, true, false,
+                     false);
+
+    // rms(x) with a second consumer: the one-pass rule must not fire (its
+    // gradient is not final when the Mul runs); checked numerically.
+    Value x = leaf(normal(24, 43), {4, 6}, "x");
+    Value g = leaf(uniform(6, 44, 0.5, 1.5), {6}, "g");
+    Tensor dy = Tensor::from_host_f32(normal(24, 45), {4, 6});
+    auto f = [&]() {
+        Value h = rms(x);
+        return ((h * g) * h) * make_tensor(dy);
+    };
+    const uint64_t before = debug::fused_rms_mul_vjps();
+    {
+        Value h = rms(x);
+        backward((h * g) * h, &dy);
+    }
+    report("rms(x) used twice: not fused", debug::fused_rms_mul_vjps() == before);
+    check_grad("rms(x) used twice: dx numerical gradient", x, f);
+    check_grad("rms(x) used twice: dgamma numerical gradient", g, f);
+
+    // Accumulation.  A new graph over the same leaves: the one-pass kernel adds
+    // into x's and gamma's gradients (its accumulating variant).
+    Value x2 = leaf(normal(64 * 128, 46), {64, 128}, "x2");
+    Value g2 = leaf(uniform(128, 47, 0.5, 1.5), {128}, "g2");
+    Tensor dy2 = Tensor::from_host_f32(normal(64 * 128, 48), {64, 128});
+    Value y2 = rms(x2) * g2;
+    backward(y2, &dy2);
+    const std::vector<float> dx1 = x2.grad().to_host_f32(), dg1 = g2.grad().to_host_f32();
+    const uint64_t f0 = debug::fused_rms_mul_vjps();
+    backward(rms(x2) * g2, &dy2);
+    const bool fused_again = debug::fused_rms_mul_vjps() == f0 + 1;
+    std::vector<float> dxa = x2.grad().to_host_f32(), dga = g2.grad().to_host_f32();
+    bool doubled = true;
+    for (size_t i = 0; i < dx1.size(); ++i) doubled &= dxa[i] == dx1[i] + dx1[i];
+    for (size_t i = 0; i < dg1.size(); ++i) doubled &= dga[i] == dg1[i] + dg1[i];
+    report("rms(x) * gamma, a second graph: one pass adds into x and gamma",
+           fused_again && doubled);
+    // A second backward over the same graph: rms(x)'s gradient from the first
+    // is still there, so the Mul's is not its only contribution and the rule
+    // stands aside; as in the reference, rms(x)'s VJP then propagates the
+    // accumulated 2*dr, so x.grad gains 2*dx1 (exact: scaling by 2) and
+    // gamma.grad gains dg1.
+    zero_grad(y2);
+    backward(y2, &dy2);
+    const uint64_t f1 = debug::fused_rms_mul_vjps();
+    backward(y2, &dy2);
+    const bool stood_aside = debug::fused_rms_mul_vjps() == f1;
+    dxa = x2.grad().to_host_f32();
+    dga = g2.grad().to_host_f32();
+    bool tripled = true;
+    for (size_t i = 0; i < dx1.size(); ++i) tripled &= dxa[i] == dx1[i] + 2.0f * dx1[i];
+    for (size_t i = 0; i < dg1.size(); ++i) tripled &= dga[i] == dg1[i] + dg1[i];
+    report("rms(x) * gamma, the same graph again: rms(x).grad accumulates (reference semantics)",
+           stood_aside && tripled);
 }
 
 void test_accumulation_and_zero_grad() {
@@ -362,17 +491,6 @@ void test_user_stream() {
 
 
 // ---- matmul, the row ops beside RMSNorm, forward mode, graph capture ----------
-
-std::vector<uint16_t> to_bf16_bits(const std::vector<float>& v) {
-    std::vector<uint16_t> b(v.size());
-    for (size_t i = 0; i < v.size(); ++i) {
-        uint32_t u;
-        std::memcpy(&u, &v[i], 4);
-        u += 0x7fffu + ((u >> 16) & 1u);
-        b[i] = static_cast<uint16_t>(u >> 16);
-    }
-    return b;
-}
 
 float bf16_round(float f) {
     uint32_t u;
@@ -715,6 +833,7 @@ int selftest() {
         {"reference_pattern", test_reference_pattern},
         {"fused_layer_gradients", test_fused_layer_gradients},
         {"fused_matches_unfused", test_fused_matches_unfused},
+        {"composition_backward", test_composition_backward},
         {"accumulation_and_zero_grad", test_accumulation_and_zero_grad},
         {"parallel_matches_sequential", test_parallel_matches_sequential},
         {"weight_tying", test_weight_tying},

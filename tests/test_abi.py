@@ -180,6 +180,15 @@ def test_mul_argument_validation():
     assert m(FAKE, FAKE, FAKE, None, FAKE, None, 0, 4, 4, 0, 0, None) == 3        # db needs ws
     assert m(FAKE, FAKE, FAKE, None, None, None, 0, 4, 4, 0, 0, None) == 0        # nothing asked
     assert m(FAKE, FAKE, FAKE, FAKE, None, None, 0, 4, 4, 0, 8, None) == 1        # bad accumulate
+    r = lib.agk_rms_mul_bwd  # x, gamma, inv, gy, dr, dx, dgamma, ws, wsb, rows, cols, dt, acc
+    for i in range(5):  # x, gamma, inv_rms, gy and dr are required
+        args = [FAKE] * 5
+        args[i] = None
+        assert r(*args, FAKE, None, None, 0, 4, 4, 0, 0, None) == 1
+    assert r(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, 4, 4, 0, 0, None) == 3  # ws
+    assert r(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, 0, 4, 4, 7, 0, None) == 2  # dtype
+    assert r(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, 0, 4, 4, 0, 4, None) == 1  # acc bits
+    assert r(None, None, None, None, None, None, None, None, 0, 0, 4, 0, 2, None) == 0  # empty
 
 
 def test_rowops_argument_validation():

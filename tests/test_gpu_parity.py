@@ -288,3 +288,45 @@ def test_mul_rowbcast(cuda, dtype, cols):
     assert row_rel_err(as_f32(to_host(y)), af * bf) <= tol
     assert row_rel_err(as_f32(to_host(da)), gf * bf) <= tol
     assert vec_rel_err(to_host(db), np.sum(gf * af, axis=0)) <= TOL_F32
+
+
+# ---- the unfused layer's two VJPs in one pass (agk_rms_mul_bwd) -------------------
+
+@pytest.mark.parametrize("dtype,shape", [("f32", (40, 4096)), ("f32", (33, 250)),
+                                         ("bf16", (96, 8192)), ("bf16", (17, 100)),
+                                         ("f32", (65536, 4096)), ("bf16", (16384, 8192))])
+def test_rms_mul_bwd(cuda, dtype, shape):
+    """Bit-identical to mul_rowbcast_bwd followed by rmsnorm_bwd(gamma=None) on
+    the same tensors, overwriting and accumulating; where the oracle is quick,
+    dx and dgamma also against the oracle's VJP of the fused layer (the same
+    gradients up to the storage rounding of rms(x) and of its gradient)."""
+    import torch
+    R, D = shape
+    print(f"rms_mul_bwd {dtype} {shape}", flush=True)
+    x, g, dy = device_inputs(shape, dtype, R * 7 + D, cuda)
+    h, inv = agk.rmsnorm_fwd(x, None, 1e-5)
+    for acc in (False, True):
+        gen = torch.Generator(device=cuda)
+        gen.manual_seed(R + D)
+        dx0 = torch.randn(shape, generator=gen, device=cuda).to(x.dtype)
+        dg0 = torch.randn(D, generator=gen, device=cuda)
+        dr, dx, dg = agk.rms_mul_bwd(x, g, inv, dy, dx=dx0.clone() if acc else None,
+                                     dgamma=dg0.clone() if acc else None, accumulate=acc)
+        dr2, dg2 = agk.mul_rowbcast_bwd(dy, h, g, db=dg0.clone() if acc else None,
+                                        accumulate=agk.AGK_ACCUM_DGAMMA if acc else 0)
+        dx2, _ = agk.rmsnorm_bwd(x, None, inv, dr2, dx=dx0.clone() if acc else None,
+                                 accumulate=agk.AGK_ACCUM_DX if acc else 0, want_dgamma=False)
+        torch.cuda.synchronize()
+        assert torch.equal(dr, dr2), "dr"
+        assert torch.equal(dx, dx2), "dx"
+        assert torch.equal(dg, dg2), "dgamma"
+    if R * D <= 1 << 20:
+        xh, gh, dyh = to_host(x), to_host(g), to_host(dy)
+        _, rinv = oracle.fwd(xh, gh, 1e-5)
+        rdx, rdg = oracle.bwd(xh, gh, rinv, dyh)
+        dr, dx, dg = agk.rms_mul_bwd(x, g, inv, dy)
+        torch.cuda.synchronize()
+        tol = _tol(xh)
+        assert row_rel_err(as_f32(to_host(dx)), as_f32(rdx)) <= tol
+        assert vec_rel_err(to_host(dg), rdg) <= tol
+        assert row_rel_err(as_f32(to_host(dr)), as_f32(dyh) * as_f32(gh)[None, :]) <= tol
