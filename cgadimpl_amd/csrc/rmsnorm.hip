@@ -590,17 +590,40 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
 }
 
 // ---- broadcast multiply (unfused ag::rms(x) * gamma) -------------------------
+// Both looped kernels split a row into column chunks of `chunk` elements
+// (blockIdx.y), so that few long rows (an equal-shape product is one row of
+// numel columns) still spread over many workgroups.  chunk is a multiple of
+// kBlock * kVec.
+__host__ __device__ inline int64_t chunk_end(int64_t c0, int64_t chunk, int cols) {
+    return c0 + chunk < cols ? c0 + chunk : cols;
+}
+
+// Column chunk for rows x cols: about kChunkBlocks workgroups in all, at most
+// 65535 chunks per row, a multiple of kBlock * vec elements.
+inline int64_t mul_chunk(int64_t rows_or_blocks, int cols, int vec) {
+    constexpr int64_t kChunkBlocks = 4096;
+    const int64_t step = static_cast<int64_t>(kBlock) * vec;
+    const int64_t per_row =
+        rows_or_blocks >= kChunkBlocks ? 1 : (kChunkBlocks + rows_or_blocks - 1) / rows_or_blocks;
+    int64_t chunk = (cols + per_row - 1) / per_row;
+    const int64_t min_chunk = (cols + 65534) / 65535;
+    if (chunk < min_chunk) chunk = min_chunk;
+    return (chunk + step - 1) / step * step;
+}
+
 template <class S>
 __global__ __launch_bounds__(kBlock) void mul_rowbcast_fwd_kernel(
     const typename S::T* __restrict__ a, const typename S::T* __restrict__ b,
-    typename S::T* __restrict__ y, int64_t rows, int cols, int vec) {
+    typename S::T* __restrict__ y, int64_t rows, int cols, int vec, int64_t chunk) {
     // vec: 1 when a/b/y are 16-byte aligned and cols % kVec == 0.
     constexpr int W = S::kVec;
     const int64_t row = blockIdx.x;
     if (row >= rows) return;
     const int64_t off = row * static_cast<int64_t>(cols);
+    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * chunk;
+    const int64_t c1 = chunk_end(c0, chunk, cols);
     if (vec) {
-        for (int c = threadIdx.x * W; c < cols; c += kBlock * W) {
+        for (int64_t c = c0 + threadIdx.x * W; c < c1; c += kBlock * W) {
             float fa[W], fb[W];
             S::unpack(load16_stream<S>(a + off + c), fa);
             S::unpack(load16<S>(b + c), fb);
@@ -609,24 +632,30 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_fwd_kernel(
             store16_stream<S>(y + off + c, S::pack(fa));
         }
     } else {
-        for (int c = threadIdx.x; c < cols; c += kBlock)
+        for (int64_t c = c0 + threadIdx.x; c < c1; c += kBlock)
             S::put(y + off + c, S::get(a + off + c) * S::get(b + c));
     }
 }
 
-// da (+)= gy*b; partial row of this block (+)= gy*a (owned-column RMW).
+// da (+)= gy*b; partial row of this row block (+)= gy*a for the block's
+// column chunk (owned-column RMW: the chunks are disjoint, and within one the
+// lane (c - c0) % kBlock owns column c).  Each column still sums the block's
+// rows in row order, whatever the chunking.
 template <class S>
 __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
     const typename S::T* __restrict__ gy, const typename S::T* __restrict__ a,
     const typename S::T* __restrict__ b, typename S::T* __restrict__ da,
-    float* __restrict__ partials, int64_t rows, int cols, int64_t rpb, int acc_da) {
+    float* __restrict__ partials, int64_t rows, int cols, int64_t rpb, int acc_da,
+    int64_t chunk) {
     const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
     float* prow = partials ? partials + static_cast<int64_t>(blockIdx.x) * cols : nullptr;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * chunk;
+    const int64_t c1 = chunk_end(c0, chunk, cols);
     for (int64_t row = row_begin; row < row_end; ++row) {
         const int64_t off = row * static_cast<int64_t>(cols);
         const bool first = row == row_begin;
-        for (int c = threadIdx.x; c < cols; c += kBlock) {
+        for (int64_t c = c0 + threadIdx.x; c < c1; c += kBlock) {
             const float g = S::get(gy + off + c);
             if (da) {
                 float o = g * S::get(b + c);
@@ -808,8 +837,11 @@ int launch_mul_fwd(const void* a, const void* b, void* y, int64_t rows, int cols
     if (vec) p = fwd_plan(cols / S::kVec, rows);
     if (p.tpr == 0) {
         if (rows > 0x7fffffffLL) return AGK_EINVAL;
-        hipLaunchKernelGGL(mul_rowbcast_fwd_kernel<S>, dim3(static_cast<unsigned>(rows)),
-                           dim3(kBlock), 0, st, ap, bp, yp, rows, cols, vec ? 1 : 0);
+        const int64_t chunk = mul_chunk(rows, cols, vec ? S::kVec : 1);
+        const int64_t nchunk = (cols + chunk - 1) / chunk;
+        hipLaunchKernelGGL(mul_rowbcast_fwd_kernel<S>,
+                           dim3(static_cast<unsigned>(rows), static_cast<unsigned>(nchunk)),
+                           dim3(kBlock), 0, st, ap, bp, yp, rows, cols, vec ? 1 : 0, chunk);
         return check_launch();
     }
     const int64_t grid = (rows + p.g - 1) / p.g;
@@ -1125,16 +1157,18 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
         if (rc != AGK_OK || !db) return rc;
         return launch_finalize(partials, db, nblk, c, acc_db, st);
     }
+    const int64_t chunk = mul_chunk(nblk, c, 1);
+    const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>((c + chunk - 1) / chunk));
     if (dtype == AGK_F32) {
-        hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, dim3(static_cast<unsigned>(nblk)),
-                           dim3(kBlock), 0, st, static_cast<const float*>(gy),
-                           static_cast<const float*>(a), static_cast<const float*>(b),
-                           static_cast<float*>(da), partials, rows, c, rpb, acc_da);
+        hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, grid, dim3(kBlock), 0, st,
+                           static_cast<const float*>(gy), static_cast<const float*>(a),
+                           static_cast<const float*>(b), static_cast<float*>(da), partials, rows,
+                           c, rpb, acc_da, chunk);
     } else {
-        hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<BF16>, dim3(static_cast<unsigned>(nblk)),
-                           dim3(kBlock), 0, st, static_cast<const uint16_t*>(gy),
-                           static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
-                           static_cast<uint16_t*>(da), partials, rows, c, rpb, acc_da);
+        hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<BF16>, grid, dim3(kBlock), 0, st,
+                           static_cast<const uint16_t*>(gy), static_cast<const uint16_t*>(a),
+                           static_cast<const uint16_t*>(b), static_cast<uint16_t*>(da), partials,
+                           rows, c, rpb, acc_da, chunk);
     }
     int rc = check_launch();
     if (rc != AGK_OK || !db) return rc;

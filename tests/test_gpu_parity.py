@@ -290,6 +290,29 @@ def test_mul_rowbcast(cuda, dtype, cols):
     assert vec_rel_err(to_host(db), np.sum(gf * af, axis=0)) <= TOL_F32
 
 
+
+@pytest.mark.parametrize("dtype,cols", [("f32", (1 << 24) + 8), ("bf16", (1 << 23) + 24),
+                                        ("f32", 1000003)])
+def test_mul_one_long_row(cuda, dtype, cols):
+    """An equal-shape product reaches the broadcast kernels as one row of numel
+    columns (ag::mul with equal shapes); the row is split over many workgroups.
+    Products are single roundings of the same operands, so torch's elementwise
+    product is bit-exact; db of one row is its gy * a in fp32."""
+    import torch
+    print(f"mul one row {dtype} {cols}", flush=True)
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(cols)
+    dt = torch.float32 if dtype == "f32" else torch.bfloat16
+    a, b, gy = (torch.randn((1, cols), generator=gen, device=cuda).to(dt) for _ in range(3))
+    b = b.view(cols)
+    y = agk.mul_rowbcast_fwd(a, b)
+    da, db = agk.mul_rowbcast_bwd(gy, a, b)
+    torch.cuda.synchronize()
+    assert torch.equal(y, a * b)
+    assert torch.equal(da, gy * b)
+    assert torch.equal(db, (gy.float() * a.float()).view(cols))
+
+
 # ---- the unfused layer's two VJPs in one pass (agk_rms_mul_bwd) -------------------
 
 @pytest.mark.parametrize("dtype,shape", [("f32", (40, 4096)), ("f32", (33, 250)),
