@@ -11,13 +11,17 @@
 //                                                 arithmetic.cpp:31-39): two
 //                                                 forward and two backward calls
 // Inputs live on the device before timing starts; the timed region is `steps`
-// steps on one stream between two device synchronisations, so it includes
-// the graph layer's host work (node creation, topological order, the pool
-// allocations of every output and gradient).  One JSON line per mode, with
-// algorithmic bytes per step 5*R*D*s + 2*D*s + 2*R*4 + D*4 (the fused layer's
-// traffic; the unfused graph moves more than that).
+// steps on one stream between two device synchronisations.  Eagerly, that
+// includes the graph layer's host work (node creation, topological order, the
+// pool allocations of every output and gradient); captured, one step is
+// recorded once with ag::GraphRunner (the reference's CudaGraphRunner) and
+// each timed step is one replay of the recorded forward + backward.  One JSON
+// line per graph and run mode, with algorithmic bytes per step
+// 5*R*D*s + 2*D*s + 2*R*4 + D*4 (the fused layer's traffic; the unfused graph
+// moves more than that).
 //
 // Usage: rmsnorm_layer [B T D] [steps] [warmup] [f32|bf16] [fused|unfused|both]
+//                      [eager|captured|all]
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -71,16 +75,19 @@ int main(int argc, char** argv) {
     try {
         std::vector<int64_t> shape = {32, 2048, 4096};
         int steps = 20, warmup = 5;
-        std::string dtype = "f32", mode = "both";
+        std::string dtype = "f32", mode = "both", run = "all";
         if (argc >= 4) shape = {std::atoll(argv[1]), std::atoll(argv[2]), std::atoll(argv[3])};
         if (argc >= 5) steps = std::atoi(argv[4]);
         if (argc >= 6) warmup = std::atoi(argv[5]);
         if (argc >= 7) dtype = argv[6];
         if (argc >= 8) mode = argv[7];
+        if (argc >= 9) run = argv[8];
         if (steps < 1 || warmup < 0 || (dtype != "f32" && dtype != "bf16") ||
-            (mode != "fused" && mode != "unfused" && mode != "both"))
+            (mode != "fused" && mode != "unfused" && mode != "both") ||
+            (run != "eager" && run != "captured" && run != "all"))
             throw std::runtime_error(
-                "usage: rmsnorm_layer [B T D] [steps] [warmup] [f32|bf16] [fused|unfused|both]");
+                "usage: rmsnorm_layer [B T D] [steps] [warmup] [f32|bf16] [fused|unfused|both] "
+                "[eager|captured|all]");
         const ag::Dtype dt = dtype == "f32" ? ag::Dtype::Float32 : ag::Dtype::BFloat16;
         const int64_t D = shape[2], R = shape[0] * shape[1];
         const size_t n = static_cast<size_t>(R * D);
@@ -98,9 +105,25 @@ int main(int argc, char** argv) {
 
         const double s = dt == ag::Dtype::Float32 ? 4.0 : 2.0;
         const double bytes = 5.0 * R * D * s + 2.0 * D * s + 2.0 * R * 4 + D * 4.0;
+        auto report = [&](const char* path, const char* how, double sec) {
+            const double ms = sec * 1e3 / steps;
+            const double gbs = bytes / (ms * 1e-3) / 1e9;
+            std::printf(
+                "{\"path\": \"graph layer, %s, %s\", \"shape\": [%lld, %lld, %lld], "
+                "\"dtype\": \"%s\", \"steps\": %d, \"warmup\": %d, \"ms_per_step\": %.5f, "
+                "\"gbs\": %.1f, \"pct_of_hbm_peak\": %.2f}\n",
+                path, how, static_cast<long long>(shape[0]), static_cast<long long>(shape[1]),
+                static_cast<long long>(shape[2]), dtype.c_str(), steps, warmup, ms, gbs,
+                100.0 * gbs / 8000.0);
+            std::fflush(stdout);
+        };
+        auto seconds_since = [](std::chrono::steady_clock::time_point t0) {
+            return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        };
         for (const char* m : {"fused", "unfused"}) {
             if (mode != "both" && mode != m) continue;
             const bool fused = std::strcmp(m, "fused") == 0;
+            const char* path = fused ? "nn::RMSNorm (fused)" : "ag::rms(x) * gamma (unfused)";
             auto step = [&]() {
                 ag::Value xv = ag::make_tensor(x, "x");
                 ag::Value y = fused ? layer(xv) : ag::rms(xv) * layer.gamma;
@@ -109,22 +132,26 @@ int main(int argc, char** argv) {
             };
             for (int i = 0; i < warmup; ++i) step();
             check(hipDeviceSynchronize(), "warm-up");
-            const auto t0 = std::chrono::steady_clock::now();
-            for (int i = 0; i < steps; ++i) step();
-            check(hipDeviceSynchronize(), "timed steps");
-            const double sec =
-                std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-            const double ms = sec * 1e3 / steps;
-            const double gbs = bytes / (ms * 1e-3) / 1e9;
-            std::printf(
-                "{\"path\": \"graph layer, %s\", \"shape\": [%lld, %lld, %lld], \"dtype\": \"%s\", "
-                "\"steps\": %d, \"warmup\": %d, \"ms_per_step\": %.5f, \"gbs\": %.1f, "
-                "\"pct_of_hbm_peak\": %.2f}\n",
-                fused ? "nn::RMSNorm (fused)" : "ag::rms(x) * gamma (unfused)",
-                static_cast<long long>(shape[0]), static_cast<long long>(shape[1]),
-                static_cast<long long>(shape[2]), dtype.c_str(), steps, warmup, ms, gbs,
-                100.0 * gbs / 8000.0);
-            std::fflush(stdout);
+            if (run != "captured") {
+                const auto t0 = std::chrono::steady_clock::now();
+                for (int i = 0; i < steps; ++i) step();
+                check(hipDeviceSynchronize(), "timed steps");
+                report(path, "eager", seconds_since(t0));
+            }
+            if (run != "eager") {
+                // every buffer of one step (outputs, saved tensors, gradients,
+                // workspaces) comes from the capture arena
+                ag::GraphRunner runner(static_cast<size_t>(4.5 * R * D * s) + (size_t(64) << 20));
+                runner.begin_capture();
+                step();
+                runner.end_capture();
+                for (int i = 0; i < warmup; ++i) runner.replay();
+                check(hipDeviceSynchronize(), "replay warm-up");
+                const auto t0 = std::chrono::steady_clock::now();
+                for (int i = 0; i < steps; ++i) runner.replay();
+                check(hipDeviceSynchronize(), "timed replays");
+                report(path, "captured", seconds_since(t0));
+            }
         }
         check(hipStreamSynchronize(stream), "hipStreamSynchronize");
         return 0;
