@@ -45,6 +45,10 @@ SIGNATURES = {
                                             ctypes.c_int, ctypes.c_int, _P]),
     "agk_rms_mul_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64,
                                        _I64, ctypes.c_int, ctypes.c_int, _P]),
+    "agk_sum_rows_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "agk_sum_rows": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _I64, _I64, ctypes.c_int,
+                                    ctypes.c_int, _P]),
+    "agk_linear_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "agk_gemm_bf16": (ctypes.c_int, [_P, _I64, ctypes.c_int, _P, _I64, ctypes.c_int, _P, _I64,
                                      ctypes.c_int, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P,
                                      ctypes.c_size_t, _P]),
@@ -318,6 +322,38 @@ def rms_mul_bwd(x, gamma, inv_rms, gy, dx=None, dgamma=None, accumulate=False,
                                _stream(stream))
     _check(rc, "agk_rms_mul_bwd")
     return dr, dx, dgamma
+
+
+def sum_rows(x, out=None, accumulate=False, stream=None):
+    """out[j] (+)= sum_i x[i, j] in fp32, deterministic (agk_sum_rows)."""
+    torch = _torch()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    if out is None:
+        out = torch.empty(cols, dtype=torch.float32, device=x.device)
+    wsb = int(lib().agk_sum_rows_workspace_bytes(rows, cols))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=x.device) if wsb else None
+    rc = lib().agk_sum_rows(_ptr(x), _ptr(out), _ptr(ws), wsb, rows, cols, _dtype_code(x),
+                            int(bool(accumulate)), _stream(stream))
+    _check(rc, "agk_sum_rows")
+    return out
+
+
+def linear_bf16(x, w, bias=None, y=None, stream=None):
+    """y = x @ w^T + bias (agk_linear_bf16): x [M, K], w [N, K], bias [N], bf16."""
+    torch = _torch()
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("linear_bf16 takes bfloat16 operands")
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError("x and w disagree on the input width")
+    if y is None:
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    rc = lib().agk_linear_bf16(_ptr(x), x.shape[1], _ptr(w), w.shape[1], _ptr(bias), _ptr(y),
+                               y.shape[1], M, N, K, _stream(stream))
+    _check(rc, "agk_linear_bf16")
+    return y
 
 
 # ---- the RMSNorm + linear layer (configuration c5) --------------------------------

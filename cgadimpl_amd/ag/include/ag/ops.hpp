@@ -37,6 +37,14 @@ inline Value operator*(const Value& a, const Value& b) { return mul(a, b); }
 // (a weight accumulates in fp32).  fp32 operands throw std::runtime_error.
 Value matmul(const Value& a, const Value& b);
 
+// x [..., K] times w [N, K] transposed, plus b [N] or [1, N] -> [..., N], all
+// bf16, on the MFMA GEMM with the bias added in its store
+// (cgadimpl/src/ops/linalg.cpp:21-33, `matmul(x, w.t()) + b`, with its two
+// bf16 roundings).  x's gradient is bf16; w's and b's are fp32.  Forward mode
+// uses the rule tx w^T + x tw^T + tb (the reference's jvp_Linear,
+// autodiff_jvp_ops.cpp:256-265, multiplies by w where w^T belongs).
+Value linear(const Value& x, const Value& w, const Value& b);
+
 // (x - mean) / sqrt(var + 1e-5) over the last axis (normalization.cpp:10-22;
 // eps fixed as there).  Tape: {mean, rstd}, fp32 [..., 1].
 Value laynor(const Value& x);
@@ -54,6 +62,9 @@ std::shared_ptr<Node> rms_norm_nodeops(const std::shared_ptr<Node>& x,
 std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a,
                                   const std::shared_ptr<Node>& b);
 std::shared_ptr<Node> matmul_nodeops(const std::shared_ptr<Node>& a,
+                                     const std::shared_ptr<Node>& b);
+std::shared_ptr<Node> linear_nodeops(const std::shared_ptr<Node>& x,
+                                     const std::shared_ptr<Node>& w,
                                      const std::shared_ptr<Node>& b);
 std::shared_ptr<Node> laynor_nodeops(const std::shared_ptr<Node>& x);
 std::shared_ptr<Node> softmax_row_nodeops(const std::shared_ptr<Node>& z);

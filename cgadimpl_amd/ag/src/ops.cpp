@@ -6,11 +6,13 @@
 //   rms_nodeops      cgadimpl/src/ops/normalization.cpp:23-35
 //   mul_nodeops      cgadimpl/src/ops/arithmetic.cpp:31-39
 //   matmul_nodeops   cgadimpl/src/ops/linalg.cpp:12-20
+//   linear_nodeops   cgadimpl/src/ops/linalg.cpp:21-33
 //   laynor_nodeops   normalization.cpp:10-22
 //   softmax_row_nodeops, logsumexp_row_nodeops  cgadimpl/src/ops/reduction.cpp:42-66
 //   vjp_RMSNorm      cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:368-377
 //   vjp_Mul          autodiff_vjp_ops.cpp:54-59, with reduce_for_broadcast :15-35
 //   vjp_MatMul       autodiff_vjp_ops.cpp:258-263
+//   vjp_Linear       autodiff_vjp_ops.cpp:272-279
 //   vjp_LayerNorm    autodiff_vjp_ops.cpp:351-365
 //   vjp_SoftmaxRow, vjp_LogSumExpRow  autodiff_vjp_ops.cpp:421-440
 //   jvp_* rules      cgadimpl/src/autodiff/autodiff_jvp_ops.cpp (Mul :24-31,
@@ -209,6 +211,35 @@ std::shared_ptr<Node> matmul_nodeops(const std::shared_ptr<Node>& a,
     auto n = std::make_shared<Node>(y, Op::MatMul, a->requires_grad() || b->requires_grad(),
                                     "matmul");
     link_inputs(n, {a, b});
+    return n;
+}
+
+std::shared_ptr<Node> linear_nodeops(const std::shared_ptr<Node>& x,
+                                     const std::shared_ptr<Node>& w,
+                                     const std::shared_ptr<Node>& b) {
+    require_value(x, "linear");
+    require_value(w, "linear");
+    require_value(b, "linear");
+    const Tensor& xv = x->value;
+    const Tensor& wv = w->value;
+    const Tensor& bv = b->value;
+    if (xv.dtype() != Dtype::BFloat16 || wv.dtype() != Dtype::BFloat16 ||
+        bv.dtype() != Dtype::BFloat16)
+        fail("linear: x, w and b must be bfloat16 (the product runs on the bf16 matrix cores)");
+    if (wv.dim() != 2 || xv.dim() < 1 || xv.cols() != wv.shape()[1])
+        fail("linear: expects x [..., K] and w [N, K]");
+    const int64_t M = xv.rows(), K = xv.cols(), N = wv.shape()[0];
+    if (!is_row_vector(bv, N)) fail("linear: b must have shape [N] or [1, N]");
+    if (M % 8 || N % 8 || K % 8) fail("linear: the batch, N and K must be multiples of 8");
+    std::vector<int64_t> ys = xv.shape();
+    ys.back() = N;
+    Tensor y = Tensor::empty(ys, Dtype::BFloat16);
+    agk_check(agk_linear_bf16(xv.data(), K, wv.data(), K, bv.data(), y.data(), N, M, N, K,
+                              stream_arg()),
+              "linear");
+    auto n = std::make_shared<Node>(
+        y, Op::Linear, x->requires_grad() || w->requires_grad() || b->requires_grad(), "linear");
+    link_inputs(n, {x, w, b});
     return n;
 }
 
@@ -456,6 +487,48 @@ void vjp_MatMul(Node* n, const Tensor& gy) {
     }
 }
 
+// X.grad += gy W (bf16), W.grad += gy^T X (fp32), b.grad += sum over rows of gy
+// (fp32, agk_sum_rows)   (autodiff_vjp_ops.cpp:272-279)
+void vjp_Linear(Node* n, const Tensor& gy) {
+    Node* X = n->inputs[0].get();
+    Node* Wn = n->inputs[1].get();
+    Node* Bn = n->inputs[2].get();
+    const bool want_x = X->requires_grad();
+    const bool want_w = Wn->requires_grad();
+    const bool want_b = Bn->requires_grad();
+    if (!want_x && !want_w && !want_b) return;
+    check_upstream(n, gy, "vjp_Linear");
+    const Tensor& xv = X->value;
+    const Tensor& wv = Wn->value;
+    const int64_t M = xv.rows(), K = xv.cols(), N = wv.shape()[0];
+    GradLocks lock(X, Wn, Bn);
+    if (want_x) {  // [M, K] = gy [M, N] . W [N, K]
+        bool acc = false;
+        Tensor& dx = X->grad_for_write(Dtype::BFloat16, &acc);
+        if (M && K)
+            gemm(gy.data(), N, false, wv.data(), K, false, dx.data(), K, Dtype::BFloat16, M, K,
+                 N, acc, "vjp_Linear dX");
+    }
+    if (want_w) {  // [N, K] = gy^T [N, M] . X [M, K]
+        bool acc = false;
+        Tensor& dw = Wn->grad_for_write(Dtype::Float32, &acc);
+        if (N && K)
+            gemm(gy.data(), N, true, xv.data(), K, false, dw.data(), K, Dtype::Float32, N, K, M,
+                 acc, "vjp_Linear dW");
+    }
+    if (want_b) {
+        bool acc = false;
+        Tensor& db = Bn->grad_for_write(Dtype::Float32, &acc);
+        const size_t wsb = agk_sum_rows_workspace_bytes(M, N);
+        std::unique_ptr<Storage> ws;
+        if (wsb) ws = std::make_unique<Storage>(wsb, current_stream());
+        agk_check(agk_sum_rows(gy.data(), static_cast<float*>(db.data()),
+                               ws ? ws->data() : nullptr, wsb, M, N, AGK_BF16, acc ? 1 : 0,
+                               stream_arg()),
+                  "vjp_Linear db");
+    }
+}
+
 // X.grad += rstd * (gy - mean(gy) - xhat * mean(gy * xhat))   (autodiff_vjp_ops.cpp:351-365)
 void vjp_LayerNorm(Node* n, const Tensor& gy) {
     Node* X = n->inputs[0].get();
@@ -621,6 +694,42 @@ Tensor jvp_RMSNormAffine(Node* n, const TangentOf& tan) {
 }
 
 // The LayerNorm Jacobian is symmetric: its VJP kernel applied to the tangent.
+// tx W^T + X tW^T + tb: the corrected rule (the reference's jvp_Linear,
+// autodiff_jvp_ops.cpp:256-265, multiplies by W and tW untransposed).  The
+// first product carries tb in its store; the second adds into it.
+Tensor jvp_Linear(Node* n, const TangentOf& tan) {
+    Node* X = n->inputs[0].get();
+    Node* Wn = n->inputs[1].get();
+    Node* Bn = n->inputs[2].get();
+    const Tensor& tx = tan(X);
+    const Tensor& tw = tan(Wn);
+    const Tensor& tb = tan(Bn);
+    if (!tx.defined() && !tw.defined() && !tb.defined()) return Tensor();
+    check_tangent(tx, X->value, "jvp_Linear");
+    check_tangent(tw, Wn->value, "jvp_Linear");
+    check_tangent(tb, Bn->value, "jvp_Linear");
+    const Tensor& xv = X->value;
+    const Tensor& wv = Wn->value;
+    const int64_t M = xv.rows(), K = xv.cols(), N = wv.shape()[0];
+    Tensor out = Tensor::empty(n->value.shape(), Dtype::BFloat16);
+    if (M == 0 || N == 0) return out;
+    const void* bias = tb.defined() ? tb.data() : nullptr;
+    if (tx.defined() || !tw.defined()) {  // tx W^T + tb (K = 0 when only tb: the bias rows)
+        const bool use_x = tx.defined();
+        agk_check(agk_linear_bf16(use_x ? tx.data() : nullptr, K, wv.data(), K, bias, out.data(),
+                                  N, M, N, use_x ? K : 0, stream_arg()),
+                  "jvp_Linear");
+        if (tw.defined())
+            gemm(xv.data(), K, false, tw.data(), K, true, out.data(), N, Dtype::BFloat16, M, N, K,
+                 true, "jvp_Linear");
+    } else {  // X tW^T + tb
+        agk_check(agk_linear_bf16(xv.data(), K, tw.data(), K, bias, out.data(), N, M, N, K,
+                                  stream_arg()),
+                  "jvp_Linear");
+    }
+    return out;
+}
+
 Tensor jvp_LayerNorm(Node* n, const TangentOf& tan) {
     Node* X = n->inputs[0].get();
     const Tensor& tx = tan(X);
@@ -676,6 +785,10 @@ Value mul(const Value& a, const Value& b) { return Value(detail::mul_nodeops(a.n
 
 Value matmul(const Value& a, const Value& b) {
     return Value(detail::matmul_nodeops(a.node, b.node));
+}
+
+Value linear(const Value& x, const Value& w, const Value& b) {
+    return Value(detail::linear_nodeops(x.node, w.node, b.node));
 }
 
 Value laynor(const Value& x) { return Value(detail::laynor_nodeops(x.node)); }

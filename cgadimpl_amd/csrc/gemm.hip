@@ -215,13 +215,22 @@ __device__ __forceinline__ void tile_of(int L, int tiles_m, int tiles_n, int& tm
     tn = in / gsize;
 }
 
+// The product rounded to bf16, plus a bf16 bias term (then rounded again when
+// stored): `matmul(X, W^T) + b` with its two roundings, as a bf16 product and
+// a bf16 sum give them.
+__device__ __forceinline__ float with_bias(float v, uint16_t b) {
+    v = __uint_as_float(f32_to_bf16_bits(v) << 16);
+    return v + __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
 // ---- the kernel ---------------------------------------------------------------
 
 template <bool A_KCONTIG, bool B_KCONTIG, bool KSCALE, bool OUT_F32>
 __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ kscale,
-    const float* __restrict__ rowscale, int accumulate, int tiles_m, int tiles_n) {
+    const float* __restrict__ rowscale, const uint16_t* __restrict__ colbias, int accumulate,
+    int tiles_m, int tiles_n) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStageElems];
 
     const int tid = threadIdx.x;
@@ -316,6 +325,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
                 } else {
                     uint16_t* p = static_cast<uint16_t*>(C) + static_cast<int64_t>(row) * ldc + col;
                     if (accumulate) v = __uint_as_float(static_cast<uint32_t>(*p) << 16) + v;
+                    if (colbias) v = with_bias(v, colbias[col]);
                     *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
                 }
             }
@@ -332,13 +342,15 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
 // 128 x 64 block of C.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// GENERAL: rowscale and accumulate honoured; CHECK: rows past M and columns
-// past N skipped.  store_c picks the variant once per call (uniform values), so
-// the common plain, interior store has no per-element branches.
+// GENERAL: rowscale, a column bias (bf16 output only) and accumulate
+// honoured; CHECK: rows past M and columns past N skipped.  store_c picks the
+// variant once per call (uniform values), so the common plain, interior store
+// has no per-element branches.
 template <bool OUT_F32, bool GENERAL, bool CHECK>
 __device__ __forceinline__ void store_c_impl(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
                                              int64_t ldc, int M, int N, int m0, int n0, int wm,
                                              int wn, int lane, const float* __restrict__ rowscale,
+                                             const uint16_t* __restrict__ colbias,
                                              int accumulate) {
     const int col_l = lane & 31;
     const int row_l = 4 * (lane >> 5);
@@ -366,8 +378,10 @@ __device__ __forceinline__ void store_c_impl(const f32x16 (&acc)[TM][TN], void* 
                     *p = v;
                 } else {
                     uint16_t* p = static_cast<uint16_t*>(C) + static_cast<int64_t>(row) * ldc + col;
-                    if constexpr (GENERAL)
+                    if constexpr (GENERAL) {
                         if (accumulate) v = __uint_as_float(static_cast<uint32_t>(*p) << 16) + v;
+                        if (colbias) v = with_bias(v, colbias[col]);
+                    }
                     *p = static_cast<uint16_t>(f32_to_bf16_bits(v));
                 }
             }
@@ -379,14 +393,16 @@ template <bool OUT_F32>
 __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
                                         int64_t ldc, int M, int N, int m0, int n0, int wm, int wn,
                                         int lane, const float* __restrict__ rowscale,
-                                        int accumulate) {
-    if (rowscale != nullptr || accumulate) {
+                                        const uint16_t* __restrict__ colbias, int accumulate) {
+    if (rowscale != nullptr || colbias != nullptr || accumulate) {
         store_c_impl<OUT_F32, true, true>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale,
-                                          accumulate);
+                                          colbias, accumulate);
     } else if (m0 + BM <= M && n0 + BN <= N) {
-        store_c_impl<OUT_F32, false, false>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr, 0);
+        store_c_impl<OUT_F32, false, false>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr,
+                                            nullptr, 0);
     } else {
-        store_c_impl<OUT_F32, false, true>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr, 0);
+        store_c_impl<OUT_F32, false, true>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr,
+                                           nullptr, 0);
     }
 }
 
@@ -579,7 +595,7 @@ template <bool OUT_F32, bool A_TR, bool B_TR>
 __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
-    int accumulate, int tiles_m, int tiles_n) {
+    const uint16_t* __restrict__ colbias, int accumulate, int tiles_m, int tiles_n) {
     __shared__ __attribute__((aligned(16))) uint16_t st0[kStageElems];
     __shared__ __attribute__((aligned(16))) uint16_t st1[kStageElems];
 
@@ -652,15 +668,23 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) half[i][j] = acc[i][h * TN + j];
-        store_c<OUT_F32>(half, C, ldc, M, N, m0, n0, wm, 2 * wn + h, lane, rowscale, accumulate);
+        store_c<OUT_F32>(half, C, ldc, M, N, m0, n0, wm, 2 * wn + h, lane, rowscale, colbias,
+                         accumulate);
     }
 }
 
-// C = 0 for an empty reduction (K == 0): rows of ldc, n columns of 4- or 2-byte
-// elements (a kernel, not a memset node, so that the call can be captured).
+// C for an empty reduction (K == 0): zeros, or the bf16 column bias in every
+// row; rows of ldc, n columns of 4- or 2-byte elements (a kernel, not a memset
+// node, so that the call can be captured).
 __global__ __launch_bounds__(256) void zero_c_kernel(void* __restrict__ C, int64_t ldc, int n,
-                                                     int elem_bytes) {
+                                                     int elem_bytes,
+                                                     const uint16_t* __restrict__ colbias) {
     char* p = static_cast<char*>(C) + static_cast<int64_t>(blockIdx.x) * ldc * elem_bytes;
+    if (colbias) {  // bf16 output
+        uint16_t* q = reinterpret_cast<uint16_t*>(p);
+        for (int64_t i = threadIdx.x; i < n; i += 256) q[i] = colbias[i];
+        return;
+    }
     for (int64_t i = threadIdx.x; i < static_cast<int64_t>(n) * elem_bytes; i += 256) p[i] = 0;
 }
 
@@ -728,35 +752,35 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 template <bool AK, bool BK_, bool KS, bool F32>
 int launch(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int M,
-           int N, int K, const float* kscale, const float* rowscale, int accumulate,
-           hipStream_t st) {
+           int N, int K, const float* kscale, const float* rowscale, const uint16_t* colbias,
+           int accumulate, hipStream_t st) {
     const int tiles_m = (M + BM - 1) / BM;
     const int tiles_n = (N + BN - 1) / BN;
     hipLaunchKernelGGL((gemm_bf16_kernel<AK, BK_, KS, F32>), dim3(tiles_m * tiles_n),
                        dim3(kThreads), 0, st, static_cast<const uint16_t*>(A), lda,
                        static_cast<const uint16_t*>(B), ldb, C, ldc, M, N, K, kscale, rowscale,
-                       accumulate, tiles_m, tiles_n);
+                       colbias, accumulate, tiles_m, tiles_n);
     return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
 }
 
 // Dispatch over (A k-contiguous, B k-contiguous, k-scale, fp32 output).
 template <bool AK, bool BK_, bool KS>
 int dispatch_out(int c_dtype, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
-                 int64_t ldc, int M, int N, int K, const float* ks, const float* rs, int acc,
-                 hipStream_t st) {
+                 int64_t ldc, int M, int N, int K, const float* ks, const float* rs,
+                 const uint16_t* cb, int acc, hipStream_t st) {
     return c_dtype == AGK_F32 ? launch<AK, BK_, KS, true>(A, lda, B, ldb, C, ldc, M, N, K, ks, rs,
-                                                          acc, st)
+                                                          cb, acc, st)
                               : launch<AK, BK_, KS, false>(A, lda, B, ldb, C, ldc, M, N, K, ks,
-                                                           rs, acc, st);
+                                                           rs, cb, acc, st);
 }
 template <bool AK, bool BK_>
 int dispatch_ks(bool has_ks, int c_dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                 void* C, int64_t ldc, int M, int N, int K, const float* ks, const float* rs,
-                int acc, hipStream_t st) {
+                const uint16_t* cb, int acc, hipStream_t st) {
     return has_ks ? dispatch_out<AK, BK_, true>(c_dtype, A, lda, B, ldb, C, ldc, M, N, K, ks, rs,
-                                                acc, st)
+                                                cb, acc, st)
                   : dispatch_out<AK, BK_, false>(c_dtype, A, lda, B, ldb, C, ldc, M, N, K, ks, rs,
-                                                 acc, st);
+                                                 cb, acc, st);
 }
 
 }  // namespace agk_gemm
@@ -793,23 +817,25 @@ extern "C" int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, in
                             static_cast<int>(cols), reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
-                             int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
-                             int64_t K, const float* kscale, const float* rowscale,
-                             int accumulate, void* workspace, size_t workspace_bytes,
-                             agk_stream_t stream) {
-    using namespace agk_gemm;
+namespace agk_gemm {
+
+// agk_gemm_bf16 with an optional bf16 column bias (bf16 output, no rowscale,
+// no accumulation: the caller has checked).
+int gemm_impl(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb, int b_trans,
+              void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N, int64_t K,
+              const float* kscale, const float* rowscale, const uint16_t* colbias, int accumulate,
+              agk_stream_t stream) {
     if (M < 0 || N < 0 || K < 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
         return AGK_EINVAL;
     if (c_dtype != AGK_F32 && c_dtype != AGK_BF16) return AGK_EDTYPE;
     if (M == 0 || N == 0) return AGK_OK;
     if (!C || ldc < N) return AGK_EINVAL;
-    if (K == 0) {  // empty reduction (A and B may be null): C = 0, or C as it was
+    if (K == 0) {  // empty reduction (A and B may be null): C = 0 (+ bias), or C as it was
         if (accumulate) return AGK_OK;
         (void)hipGetLastError();
         hipLaunchKernelGGL(zero_c_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0,
                            reinterpret_cast<hipStream_t>(stream), C, ldc,
-                           static_cast<int>(N), c_dtype == AGK_F32 ? 4 : 2);
+                           static_cast<int>(N), c_dtype == AGK_F32 ? 4 : 2, colbias);
         return hipGetLastError() == hipSuccess ? AGK_OK : AGK_EHIP;
     }
     if (!A || !B) return AGK_EINVAL;
@@ -837,7 +863,7 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
         const uint16_t* b16 = static_cast<const uint16_t*>(B);
 #define AGK_DIRECT(F32, ATR, BTR)                                                              \
     hipLaunchKernelGGL((gemm_nt_direct_kernel<F32, ATR, BTR>), grid, block, 0, st, a16, lda, b16, \
-                       ldb, C, ldc, m, n, k, rowscale, acc, tiles_m, tiles_n)
+                       ldb, C, ldc, m, n, k, rowscale, colbias, acc, tiles_m, tiles_n)
         const bool f32 = c_dtype == AGK_F32;
         if (f32) {
             if (a_tr && b_tr) AGK_DIRECT(true, true, true);
@@ -855,11 +881,32 @@ extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void
     }
     // Leading dimensions too large for the direct kernel's offsets, K not a
     // multiple of 64, or a k-scale: the register-staged kernel.
-    (void)workspace;
-    (void)workspace_bytes;
     const bool ak = !a_trans, bk = b_trans != 0, ks = kscale != nullptr;
-    if (ak && bk) return dispatch_ks<true, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
-    if (ak && !bk) return dispatch_ks<true, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
-    if (!ak && bk) return dispatch_ks<false, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
-    return dispatch_ks<false, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, acc, st);
+    const uint16_t* cb = colbias;
+    if (ak && bk) return dispatch_ks<true, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, cb, acc, st);
+    if (ak && !bk) return dispatch_ks<true, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, cb, acc, st);
+    if (!ak && bk) return dispatch_ks<false, true>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, cb, acc, st);
+    return dispatch_ks<false, false>(ks, c_dtype, A, lda, B, ldb, C, ldc, m, n, k, kscale, rowscale, cb, acc, st);
+}
+
+}  // namespace agk_gemm
+
+extern "C" int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_t ldb,
+                             int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
+                             int64_t K, const float* kscale, const float* rowscale,
+                             int accumulate, void* workspace, size_t workspace_bytes,
+                             agk_stream_t stream) {
+    (void)workspace;  // every layout is staged as it lies
+    (void)workspace_bytes;
+    return agk_gemm::gemm_impl(A, lda, a_trans, B, ldb, b_trans, C, ldc, c_dtype, M, N, K, kscale,
+                               rowscale, nullptr, accumulate, stream);
+}
+
+extern "C" int agk_linear_bf16(const void* X, int64_t ldx, const void* W, int64_t ldw,
+                               const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N,
+                               int64_t K, agk_stream_t stream) {
+    if (bias && (reinterpret_cast<uintptr_t>(bias) & 1u)) return AGK_EINVAL;
+    // Y [M][N] = X [M][K] * (W [N][K])^T: A k-contiguous, B stored as B^T
+    return agk_gemm::gemm_impl(X, ldx, 0, W, ldw, 1, Y, ldy, AGK_BF16, M, N, K, nullptr, nullptr,
+                               static_cast<const uint16_t*>(bias), 0, stream);
 }

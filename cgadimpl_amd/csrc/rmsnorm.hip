@@ -162,8 +162,10 @@ struct BwdSet {
 //               of rms(x)), dx (+)= r*(g - x*(r*r*sum(g*x)/cols)), and
 //               dgamma += gy*h with h = x*r rounded to storage (rms(x) as the
 //               forward stored it).  Every value and every summation order is
-//               the one the two separate calls produce.
-enum : int { kBwdRms = 0, kBwdMul = 1, kBwdRmsMul = 2 };
+//               the one the two separate calls produce;
+//   kBwdColSum  column sums of dy alone (the bias gradient of a linear
+//               layer): partials += dy, no row reduction, nothing stored.
+enum : int { kBwdRms = 0, kBwdMul = 1, kBwdRmsMul = 2, kBwdColSum = 3 };
 
 template <class S, int TPR, int NV, int G, bool ACC, int KIND>
 struct BwdCtx {
@@ -208,7 +210,7 @@ struct BwdCtx {
 #pragma unroll
             for (int k = 0; k < NV; ++k) b.ov[k] = bload16_stream(ro, off[k]);
         }
-        if constexpr (KIND == kBwdMul)
+        if constexpr (KIND == kBwdMul || KIND == kBwdColSum)
             b.r = 1.0f;
         else
             b.r = bload_f32(make_rsrc(inv_rms + r0, n * 4u), roff);
@@ -240,6 +242,22 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, KIN
     float s = 0.0f;
     constexpr bool MUL = KIND == kBwdMul;
     constexpr bool COMP = KIND == kBwdRmsMul;
+    if constexpr (KIND == kBwdColSum) {
+        (void)c;
+        (void)step;
+        (void)parity;
+        (void)red;
+        (void)gv;
+        (void)has_gamma;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fd[W];
+            S::unpack(b.dv[k], fd);
+#pragma unroll
+            for (int e = 0; e < W; ++e) dg[k][e] += fd[e];
+        }
+        return;
+    }
     if constexpr (!MUL) {
         float part[W];
 #pragma unroll
@@ -508,6 +526,18 @@ __global__ __launch_bounds__(TPR * G) void mul_rowbcast_bwd_resident(
                                                          rows, cols, red, lds_part);
 }
 
+// Column sums (kBwdColSum): partial rows of sum_rows x, as the backward's dgamma.
+template <class S, int TPR, int NV, int G, int NSET>
+__global__ __launch_bounds__(TPR * G) void sum_rows_resident(const typename S::T* __restrict__ x,
+                                                             float* __restrict__ partials,
+                                                             int64_t rows, int cols) {
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
+    extern __shared__ float lds_part[];  // [G][cols] when G > 1
+    bwd_resident_body<S, TPR, NV, G, NSET, false, kBwdColSum>(nullptr, nullptr, nullptr, x,
+                                                              nullptr, nullptr, partials, rows,
+                                                              cols, red, lds_part);
+}
+
 // ---- looped kernels (any alignment, any width) --------------------------------
 // One workgroup per row (forward) or per row block (backward); element-wise
 // accesses; the row is read twice (second read normally hits L2).  In the
@@ -662,8 +692,8 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
                 if (acc_da) o = acc_add(S::get(da + off + c), o);
                 S::put(da + off + c, o);
             }
-            if (prow) {
-                const float t = g * S::get(a + off + c);
+            if (prow) {  // a == nullptr: column sums of gy
+                const float t = a ? g * S::get(a + off + c) : g;
                 prow[c] = first ? t : prow[c] + t;
             }
         }
@@ -899,6 +929,26 @@ int launch_mul_bwd_resident(const Plan& p, int64_t nblk, const void* a, const vo
                                                           bwd_sets<S>(b_, d_), ACC>),      \
                                dim3(static_cast<unsigned>(nblk)), dim3(a_ * c_), lds, st,   \
                                ap, bp, gp, dap, partials, rows, cols);                     \
+            return check_launch();                                                         \
+        }                                                                                  \
+    }
+    AGK_BWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
+template <class S>
+int launch_sum_rows_resident(const Plan& p, int64_t nblk, const void* x, float* partials,
+                             int64_t rows, int cols, hipStream_t st) {
+    using T = typename S::T;
+    const T* xp = static_cast<const T*>(x);
+    const size_t lds = p.g > 1 ? static_cast<size_t>(p.g) * cols * 4 : 0;
+#define AGK_X(a_, b_, c_, d_)                                                              \
+    if constexpr (bwd_shape_enabled<S>(a_, b_)) {                                          \
+        if (p.tpr == a_ && p.nv == b_ && p.g == c_) {                                      \
+            hipLaunchKernelGGL((sum_rows_resident<S, a_, b_, c_, bwd_sets<S>(b_, d_)>),    \
+                               dim3(static_cast<unsigned>(nblk)), dim3(a_ * c_), lds, st,   \
+                               xp, partials, rows, cols);                                  \
             return check_launch();                                                         \
         }                                                                                  \
     }
@@ -1173,6 +1223,52 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
     int rc = check_launch();
     if (rc != AGK_OK || !db) return rc;
     return launch_finalize(partials, db, nblk, c, acc_db, st);
+}
+
+size_t agk_sum_rows_workspace_bytes(int64_t rows, int64_t cols) {
+    return agk_rmsnorm_bwd_workspace_bytes(rows, cols);
+}
+
+int agk_sum_rows(const void* x, float* out, void* workspace, size_t workspace_bytes,
+                 int64_t rows, int64_t cols, int dtype, int accumulate, agk_stream_t stream) {
+    using namespace agk;
+    if (int rc = check_sizes(rows, cols)) return rc;
+    if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    clear_pending_error();
+    if (accumulate != 0 && accumulate != 1) return AGK_EINVAL;
+    if (cols == 0) return AGK_OK;
+    if (!out) return AGK_EINVAL;
+    if (rows == 0) return accumulate ? AGK_OK : zero_fill(out, cols, st);
+    if (!x) return AGK_EINVAL;
+    const size_t need = agk_sum_rows_workspace_bytes(rows, cols);
+    if (!workspace || workspace_bytes < need) return AGK_EWORKSPACE;
+    float* partials = static_cast<float*>(workspace);
+    const int c = static_cast<int>(cols);
+    int64_t nblk = 0, rpb = 0;
+    const Plan p = dtype == AGK_F32 ? bwd_plan_for<F32>(x, nullptr, x, nullptr, rows, c, nblk, rpb)
+                                    : bwd_plan_for<BF16>(x, nullptr, x, nullptr, rows, c, nblk,
+                                                         rpb);
+    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    int rc;
+    if (p.tpr != 0) {
+        rc = dtype == AGK_F32 ? launch_sum_rows_resident<F32>(p, nblk, x, partials, rows, c, st)
+                              : launch_sum_rows_resident<BF16>(p, nblk, x, partials, rows, c, st);
+    } else {
+        const int64_t chunk = mul_chunk(nblk, c, 1);
+        const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>((c + chunk - 1) / chunk));
+        if (dtype == AGK_F32)
+            hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, grid, dim3(kBlock), 0, st,
+                               static_cast<const float*>(x), nullptr, nullptr, nullptr, partials,
+                               rows, c, rpb, 0, chunk);
+        else
+            hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<BF16>, grid, dim3(kBlock), 0, st,
+                               static_cast<const uint16_t*>(x), nullptr, nullptr, nullptr,
+                               partials, rows, c, rpb, 0, chunk);
+        rc = check_launch();
+    }
+    if (rc != AGK_OK) return rc;
+    return launch_finalize(partials, out, nblk, c, accumulate, st);
 }
 
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,

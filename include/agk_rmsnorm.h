@@ -125,6 +125,17 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
                          size_t workspace_bytes, int64_t rows, int64_t cols,
                          int dtype, int accumulate, agk_stream_t stream);
 
+/* Column sums out[j] (+)= sum_i x[i, j] of a rows x cols matrix, in fp32 and
+ * in a fixed order (the same two-stage partial-row reduction as dgamma; no
+ * float atomics, bit-identical run to run): OwnTensor::reduce_sum(gy, {0})
+ * in vjp_Linear (cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:272-279), the
+ * bias gradient.  accumulate: 0 overwrites out, 1 adds into it.  workspace:
+ * agk_sum_rows_workspace_bytes(rows, cols) bytes.                          */
+size_t agk_sum_rows_workspace_bytes(int64_t rows, int64_t cols);
+int agk_sum_rows(const void* x, float* out, void* workspace, size_t workspace_bytes,
+                 int64_t rows, int64_t cols, int dtype, int accumulate,
+                 agk_stream_t stream);
+
 /* Both VJPs of the unfused layer y = ag::rms(x) * gamma in one pass over the
  * rows: vjp_Mul with reduce_for_broadcast (autodiff_vjp_ops.cpp:54-59,
  * :15-35) followed by vjp_RMSNorm (autodiff_vjp_ops.cpp:368-377) on the
@@ -171,6 +182,19 @@ int agk_gemm_bf16(const void* A, int64_t lda, int a_trans, const void* B, int64_
                   int b_trans, void* C, int64_t ldc, int c_dtype, int64_t M, int64_t N,
                   int64_t K, const float* kscale, const float* rowscale, int accumulate,
                   void* workspace, size_t workspace_bytes, agk_stream_t stream);
+
+/* The linear layer's forward, Y = X W^T + bias, bf16 in and out with fp32
+ * accumulation: linear_nodeops (cgadimpl/src/ops/linalg.cpp:21-33,
+ * `matmul(X, W.t()) + b`).  X [M][ldx] (k contiguous), W [N][ldw] (the
+ * reference's (out, in) layout), bias bf16 [N] or NULL, Y [M][ldy].  Each
+ * element is the product rounded to bf16, plus the bias, rounded again: the
+ * two roundings of the reference's bf16 matmul and bf16 add.  The bias is
+ * added in the GEMM's store, with no extra pass over Y.  Sizes and alignment
+ * as agk_gemm_bf16 (M, N, K, ldx, ldw multiples of 8; X, W 16-byte aligned);
+ * K == 0 writes the bias (or zeros) to every row.                          */
+int agk_linear_bf16(const void* X, int64_t ldx, const void* W, int64_t ldw,
+                    const void* bias, void* Y, int64_t ldy, int64_t M, int64_t N,
+                    int64_t K, agk_stream_t stream);
 
 /* Bytes of workspace agk_gemm_bf16 uses: 0 for every shape and layout (kept so
  * that callers sizing a workspace from it need no change). */

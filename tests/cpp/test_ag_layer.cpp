@@ -29,6 +29,8 @@
 #include <random>
 #include <stdexcept>
 #include <string>
+#include <tuple>
+#include <unordered_map>
 #include <vector>
 
 #include "ag/ag.hpp"
@@ -755,6 +757,112 @@ void test_matmul_layer() {
 
 // A captured forward + backward, replayed on changed inputs with eager work in
 // between, against eager runs of the same graph.
+// linear(x, w, b) = x w^T + b (the reference's Linear test shapes, x [16, 32],
+// w [8, 32] (out, in), b [1, 8], and a wider one), in bf16: forward, the
+// three gradients and forward mode against host fp64 with the graph's bf16
+// roundings; sequential against parallel backward bitwise; errors.
+void test_linear_layer() {
+    for (auto [M, K, N] : {std::tuple<int64_t, int64_t, int64_t>{16, 32, 8}, {96, 136, 200}}) {
+        const std::string tag = "[" + std::to_string(M) + "," + std::to_string(K) + "] x [" +
+                                std::to_string(N) + "," + std::to_string(K) + "]^T";
+        std::vector<float> xv = rounded(normal(M * K, 90 + K)), wv = rounded(normal(N * K, 91 + K, 0.2)),
+                           bv = rounded(normal(N, 92 + K)), dyv = rounded(normal(M * N, 93 + K));
+        std::vector<uint16_t> dyb = to_bf16_bits(dyv);
+        Tensor dy = Tensor::from_host(dyb.data(), {M, N}, Dtype::BFloat16);
+        auto run = [&](bool parallel, std::vector<std::vector<float>>& out) {
+            Value x = bf16_leaf(xv, {M, K}, "x"), w = bf16_leaf(wv, {N, K}, "w"),
+                  b = bf16_leaf(bv, {1, N}, "b");
+            Value y = linear(x, w, b);
+            backward(y, &dy, parallel);
+            out = {y.val().to_host_f32(), x.grad().to_host_f32(), w.grad().to_host_f32(),
+                   b.grad().to_host_f32()};
+            report(("linear " + tag + ": dx bf16, dw and db fp32").c_str(),
+                   x.grad().dtype() == Dtype::BFloat16 && w.grad().dtype() == Dtype::Float32 &&
+                       b.grad().dtype() == Dtype::Float32 && b.grad().shape() == b.val().shape());
+        };
+        std::vector<std::vector<float>> seq, par;
+        run(false, seq);
+        run(true, par);
+        report(("linear " + tag + ": parallel backward == sequential (bitwise)").c_str(),
+               seq == par);
+        Vec y(M * N, 0.0), dx(M * K, 0.0), dw(N * K, 0.0), db(N, 0.0);
+        for (int64_t i = 0; i < M; ++i)
+            for (int64_t j = 0; j < N; ++j) {
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k) {
+                    acc += double(xv[i * K + k]) * wv[j * K + k];
+                    dx[i * K + k] += double(dyv[i * N + j]) * wv[j * K + k];
+                    dw[j * K + k] += double(dyv[i * N + j]) * xv[i * K + k];
+                }
+                // the product rounded to bf16, then the bf16 sum with b
+                y[i * N + j] = bf16_round(bf16_round(float(acc)) + bv[j]);
+                db[j] += dyv[i * N + j];
+            }
+        const double ey = rel_err(seq[0], y), ex = rel_err(seq[1], dx), ew = rel_err(seq[2], dw),
+                     eb = rel_err(seq[3], db);
+        report(("linear " + tag + " vs host fp64 (y, dx, dw, db)").c_str(),
+               ey <= 1e-2 && ex <= 1e-2 && ew <= 1e-5 && eb <= 1e-6,
+               "y " + std::to_string(ey) + " dx " + std::to_string(ex) + " dw " +
+                   std::to_string(ew) + " db " + std::to_string(eb));
+
+        // forward mode along (tx, tw, tb), each alone and all together
+        std::vector<float> txv = rounded(normal(M * K, 94 + K)), twv = rounded(normal(N * K, 95 + K, 0.2)),
+                           tbv = rounded(normal(N, 96 + K));
+        std::vector<uint16_t> txb = to_bf16_bits(txv), twb = to_bf16_bits(twv), tbb = to_bf16_bits(tbv);
+        Tensor tx = Tensor::from_host(txb.data(), {M, K}, Dtype::BFloat16);
+        Tensor tw = Tensor::from_host(twb.data(), {N, K}, Dtype::BFloat16);
+        Tensor tb = Tensor::from_host(tbb.data(), {1, N}, Dtype::BFloat16);
+        for (int mask = 1; mask < 8; ++mask) {
+            Value x = bf16_leaf(xv, {M, K}, "x"), w = bf16_leaf(wv, {N, K}, "w"),
+                  b = bf16_leaf(bv, {1, N}, "b");
+            std::unordered_map<Node*, Tensor> seed;
+            if (mask & 1) seed[x.node.get()] = tx;
+            if (mask & 2) seed[w.node.get()] = tw;
+            if (mask & 4) seed[b.node.get()] = tb;
+            Tensor ty = jvp(linear(x, w, b), seed);
+            Vec ref(M * N, 0.0);
+            for (int64_t i = 0; i < M; ++i)
+                for (int64_t j = 0; j < N; ++j) {
+                    double v = (mask & 4) ? tbv[j] : 0.0;
+                    for (int64_t k = 0; k < K; ++k) {
+                        if (mask & 1) v += double(txv[i * K + k]) * wv[j * K + k];
+                        if (mask & 2) v += double(xv[i * K + k]) * twv[j * K + k];
+                    }
+                    ref[i * N + j] = v;
+                }
+            const double et = rel_err(ty.to_host_f32(), ref);
+            report(("jvp linear " + tag + " along" + ((mask & 1) ? " tx" : "") +
+                    ((mask & 2) ? " tw" : "") + ((mask & 4) ? " tb" : ""))
+                       .c_str(),
+                   et <= 1e-2, std::to_string(et));
+        }
+    }
+    bool threw = false;
+    try {
+        linear(leaf(normal(64, 97), {8, 8}, "x32"), leaf(normal(64, 98), {8, 8}, "w32"),
+               leaf(normal(8, 99), {8}, "b32"));
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    report("linear of fp32 operands throws", threw);
+    threw = false;
+    try {
+        linear(bf16_leaf(normal(64, 100), {8, 8}, "x"), bf16_leaf(normal(128, 101), {8, 16}, "w"),
+               bf16_leaf(normal(8, 102), {8}, "b"));
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    report("linear with mismatched input widths throws", threw);
+    threw = false;
+    try {
+        linear(bf16_leaf(normal(64, 103), {8, 8}, "x"), bf16_leaf(normal(64, 104), {8, 8}, "w"),
+               bf16_leaf(normal(16, 105), {16}, "b"));
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    report("linear with a bias of the wrong width throws", threw);
+}
+
 void test_graph_capture(bool parallel) {
     const int64_t R = 256, D = 1024;
     std::vector<float> gv = uniform(D, 91, 0.5, 1.5);
@@ -846,6 +954,7 @@ int selftest() {
         {"row_ops_gradients", test_row_ops_gradients},
         {"jvp", test_jvp},
         {"matmul_layer", test_matmul_layer},
+        {"linear_layer", test_linear_layer},
         {"graph_capture", [] { test_graph_capture(false); }},
         {"graph_capture_parallel", [] { test_graph_capture(true); }},
         {"graph_capture_rules", test_graph_capture_rules},

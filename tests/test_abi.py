@@ -180,6 +180,20 @@ def test_mul_argument_validation():
     assert m(FAKE, FAKE, FAKE, None, FAKE, None, 0, 4, 4, 0, 0, None) == 3        # db needs ws
     assert m(FAKE, FAKE, FAKE, None, None, None, 0, 4, 4, 0, 0, None) == 0        # nothing asked
     assert m(FAKE, FAKE, FAKE, FAKE, None, None, 0, 4, 4, 0, 8, None) == 1        # bad accumulate
+    sr = lib.agk_sum_rows  # x, out, ws, wsb, rows, cols, dtype, accumulate
+    assert sr(None, FAKE, FAKE, 1 << 20, 4, 4, 0, 0, None) == 1                # x
+    assert sr(FAKE, None, FAKE, 1 << 20, 4, 4, 0, 0, None) == 1                # out
+    assert sr(FAKE, FAKE, None, 0, 4, 4, 0, 0, None) == 3                      # workspace
+    assert sr(FAKE, FAKE, FAKE, 1 << 20, 4, 4, 3, 0, None) == 2                # dtype
+    assert sr(FAKE, FAKE, FAKE, 1 << 20, 4, 4, 0, 2, None) == 1                # accumulate
+    assert sr(None, None, None, 0, 4, 0, 0, 0, None) == 0                      # no columns
+    assert lib.agk_sum_rows_workspace_bytes(65536, 4096) == lib.agk_rmsnorm_bwd_workspace_bytes(65536, 4096)
+    li = lib.agk_linear_bf16  # X, ldx, W, ldw, bias, Y, ldy, M, N, K
+    assert li(None, 64, FAKE, 64, FAKE, FAKE, 64, 64, 64, 64, None) == 1     # X
+    assert li(FAKE, 64, FAKE, 64, FAKE + 1, FAKE, 64, 64, 64, 64, None) == 1  # odd bias
+    assert li(FAKE, 60, FAKE, 64, None, FAKE, 64, 64, 64, 64, None) == 1     # ldx
+    assert li(FAKE, 64, FAKE, 64, None, FAKE, 32, 64, 64, 64, None) == 1     # ldy < N
+    assert li(None, 0, None, 0, None, None, 0, 0, 64, 64, None) == 0         # no rows
     r = lib.agk_rms_mul_bwd  # x, gamma, inv, gy, dr, dx, dgamma, ws, wsb, rows, cols, dt, acc
     for i in range(5):  # x, gamma, inv_rms, gy and dr are required
         args = [FAKE] * 5

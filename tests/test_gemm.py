@@ -171,3 +171,27 @@ def test_gemm_empty_reduction(cuda, ta, tb):
         torch.cuda.synchronize()
         assert torch.count_nonzero(c).item() == 0
         assert torch.equal(c2, base)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(16, 8, 32), (264, 520, 128), (200, 136, 72), (1000, 1032, 512),
+                                   (64, 64, 0)])
+def test_linear_bias_epilogue(cuda, M, N, K):
+    """agk_linear_bf16: y = bf16(bf16(x w^T) + b), the bias added in the GEMM's
+    store.  Bit-identical to the plain product (same kernel, no bias) followed
+    by a bf16 add of b; against a plain fp32 product + b within bf16 rounding.
+    K = 0 gives b in every row."""
+    import torch
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(M * 7 + N * 3 + K)
+    x = torch.randn(M, K, generator=gen, device=cuda).bfloat16()
+    w = (torch.randn(N, K, generator=gen, device=cuda) * 0.2).bfloat16()
+    b = torch.randn(N, generator=gen, device=cuda).bfloat16()
+    y = agk.linear_bf16(x, w, b)
+    y0 = agk.linear_bf16(x, w, None)
+    plain = agk.gemm_bf16(x, w, trans_b=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, plain)
+    assert torch.equal(y, (plain.float() + b.float()).bfloat16())
+    r = x.float() @ w.float().t() + b.float()
+    assert ((y.float() - r).abs().max() / r.abs().max()).item() <= 8e-3

@@ -313,6 +313,36 @@ def test_mul_one_long_row(cuda, dtype, cols):
     assert torch.equal(db, (gy.float() * a.float()).view(cols))
 
 
+
+@pytest.mark.parametrize("dtype,shape", [("f32", (65536, 4096)), ("bf16", (8192, 11008)),
+                                         ("f32", (333, 1001)), ("bf16", (7, 100)),
+                                         ("f32", (1, 4096)), ("f32", (0, 64))])
+def test_sum_rows(cuda, dtype, shape):
+    """agk_sum_rows (the linear layer's bias gradient): column sums in fp32
+    against fp64, bit-identical run to run, accumulate adds exactly the
+    fresh sum's rounding onto the old values' (old + new in fp32)."""
+    import torch
+    R, D = shape
+    print(f"sum_rows {dtype} {shape}", flush=True)
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(R + D)
+    x = torch.randn(shape, generator=gen, device=cuda)
+    if dtype == "bf16":
+        x = x.bfloat16()
+    s1 = agk.sum_rows(x)
+    s2 = agk.sum_rows(x)
+    old = torch.randn(D, generator=gen, device=cuda)
+    s3 = agk.sum_rows(x, out=old.clone(), accumulate=True)
+    torch.cuda.synchronize()
+    ref = x.double().sum(dim=0)
+    assert torch.equal(s1, s2)
+    assert torch.equal(s3, old + s1)
+    if R:
+        assert ((s1.double() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item() <= 1e-6
+    else:
+        assert torch.count_nonzero(s1).item() == 0
+
+
 # ---- the unfused layer's two VJPs in one pass (agk_rms_mul_bwd) -------------------
 
 @pytest.mark.parametrize("dtype,shape", [("f32", (40, 4096)), ("f32", (33, 250)),
