@@ -863,9 +863,11 @@ void test_linear_layer() {
     report("linear with a bias of the wrong width throws", threw);
 }
 
+// The captured graph holds the unfused composition rms(.) * g2 too, whose
+// backward runs as one pass (agk_rms_mul_bwd) inside the capture.
 void test_graph_capture(bool parallel) {
     const int64_t R = 256, D = 1024;
-    std::vector<float> gv = uniform(D, 91, 0.5, 1.5);
+    std::vector<float> gv = uniform(D, 91, 0.5, 1.5), g2v = uniform(D, 93, 0.5, 1.5);
     GraphRunner runner(size_t(64) << 20);
     StreamGuard guard(runner.get_stream());
     Tensor xt = Tensor::from_host_f32(normal(R * D, 90), {R, D});
@@ -873,11 +875,15 @@ void test_graph_capture(bool parallel) {
     Tensor gt = Tensor::from_host_f32(gv, {D});
     gt.set_requires_grad(true);
     Tensor dyt = Tensor::from_host_f32(normal(R * D, 92), {R, D});
-    Value x = make_tensor(xt, "x"), g = make_tensor(gt, "g");
+    Tensor g2t = Tensor::from_host_f32(g2v, {1, D});
+    g2t.set_requires_grad(true);
+    Value x = make_tensor(xt, "x"), g = make_tensor(gt, "g"), g2 = make_tensor(g2t, "g2");
+    const uint64_t fused_before = debug::fused_rms_mul_vjps();
     runner.begin_capture();
-    Value s = softmax_row(laynor(rms_norm(x, g, 1e-5f)));
+    Value s = softmax_row(laynor(rms(rms_norm(x, g, 1e-5f)) * g2));
     backward(s, &dyt, parallel);
     runner.end_capture();
+    const bool fused_in_capture = debug::fused_rms_mul_vjps() == fused_before + 1;
     const size_t used = runner.arena_bytes_used();
     bool same = true;
     for (int rep = 0; rep < 3; ++rep) {
@@ -889,16 +895,19 @@ void test_graph_capture(bool parallel) {
         }
         if (!runner.replay()) same = false;
         (void)hipStreamSynchronize(runner.get_stream());
-        Value xe = leaf(xv, {R, D}, "xe"), ge = leaf(gv, {D}, "ge");
-        Value se = softmax_row(laynor(rms_norm(xe, ge, 1e-5f)));
+        Value xe = leaf(xv, {R, D}, "xe"), ge = leaf(gv, {D}, "ge"), g2e = leaf(g2v, {1, D}, "g2e");
+        Value se = softmax_row(laynor(rms(rms_norm(xe, ge, 1e-5f)) * g2e));
         backward(se, &dyt, parallel);
         same = same && s.val().to_host_f32() == se.val().to_host_f32() &&
                x.grad().to_host_f32() == xe.grad().to_host_f32() &&
-               g.grad().to_host_f32() == ge.grad().to_host_f32();
+               g.grad().to_host_f32() == ge.grad().to_host_f32() &&
+               g2.grad().to_host_f32() == g2e.grad().to_host_f32();
     }
     report(parallel ? "graph replay == eager, 3 replays on new inputs (parallel backward)"
                     : "graph replay == eager, 3 replays on new inputs",
-           same, "arena bytes used " + std::to_string(used));
+           same && fused_in_capture,
+           "arena bytes used " + std::to_string(used) +
+               (fused_in_capture ? ", rms(.) * g2 backward in one pass" : ", NOT fused"));
 }
 
 void test_graph_capture_rules() {
