@@ -84,7 +84,13 @@ void set_capture_arena(hipStream_t stream, std::shared_ptr<CaptureArena> arena);
 std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream);
 
 // One device allocation: from the stream-ordered pool, or from the capture
-// arena of the stream when it is being captured.
+// arena of the stream when it is being captured.  A pool block goes, when its
+// Storage is destroyed, to a cache kept per stream (and device), and the next
+// allocation of a fitting size on the same stream takes it: the stream orders
+// the new user's work after the old user's, as the pool itself would, and no
+// hipFreeAsync is called (it blocks the calling thread on this runtime, which
+// kept the host from running ahead of the GPU).  Blocks never move between
+// streams.
 class Storage {
   public:
     Storage(size_t bytes, hipStream_t stream);
@@ -98,9 +104,19 @@ class Storage {
   private:
     void* ptr_ = nullptr;
     size_t bytes_ = 0;
+    size_t block_ = 0;  // bytes of the pool block behind ptr_ (>= bytes_)
+    int device_ = 0;
     hipStream_t stream_ = nullptr;
     std::shared_ptr<CaptureArena> arena_;  // set: the memory belongs to the arena
 };
+
+// Returns every cached pool block of the current device to HIP (after a
+// device synchronisation).  Call it before destroying a stream that graph-layer
+// tensors were allocated on while work on it may still be pending, or to give
+// the memory back.
+void release_cached_memory();
+// Bytes held in the cache on the current device (diagnostic).
+size_t cached_bytes();
 
 class Tensor {
   public:

@@ -22,6 +22,12 @@ GraphRunner::~GraphRunner() {
     destroy_graph();
     if (stream_) {
         (void)hipStreamSynchronize(stream_);
+        // blocks cached under this stream must not pass to a later stream
+        // that happens to reuse its handle
+        try {
+            release_cached_memory();
+        } catch (...) {
+        }
         (void)hipStreamDestroy(stream_);
     }
 }

@@ -3,6 +3,7 @@
 
 #include <atomic>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <numeric>
 #include <string>
@@ -119,14 +120,48 @@ std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream) {
 
 // ---- storage --------------------------------------------------------------------
 
+namespace {
+
+// Freed pool blocks by (device, stream), then by size.  A request takes the
+// smallest cached block of at least its size and at most 5/4 of it.  The cache
+// is never destroyed: freeing blocks at exit would race the runtime's teardown.
+struct BlockCache {
+    std::mutex mu;
+    std::map<std::pair<int, hipStream_t>, std::multimap<size_t, void*>> free;
+};
+BlockCache& block_cache() {
+    static BlockCache* c = new BlockCache;
+    return *c;
+}
+size_t block_size(size_t bytes) { return (bytes + 511) & ~size_t(511); }
+
+void* take_cached(int dev, hipStream_t stream, size_t need, size_t* got) {
+    BlockCache& c = block_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto list = c.free.find({dev, stream});
+    if (list == c.free.end()) return nullptr;
+    auto it = list->second.lower_bound(need);
+    if (it == list->second.end() || it->first > need + need / 4) return nullptr;
+    void* p = it->second;
+    *got = it->first;
+    list->second.erase(it);
+    return p;
+}
+
+}  // namespace
+
 Storage::Storage(size_t bytes, hipStream_t stream) : bytes_(bytes), stream_(stream) {
     if (bytes == 0) return;
     if ((arena_ = capture_arena(stream))) {
         ptr_ = arena_->take(bytes);
         return;
     }
+    hip_check(hipGetDevice(&device_), "hipGetDevice");
+    const size_t need = block_size(bytes);
+    if ((ptr_ = take_cached(device_, stream, need, &block_))) return;
     retain_pool_memory();
-    hip_check(hipMallocAsync(&ptr_, bytes, stream), "hipMallocAsync");
+    hip_check(hipMallocAsync(&ptr_, need, stream), "hipMallocAsync");
+    block_ = need;
 }
 
 Storage::~Storage() {
@@ -135,7 +170,42 @@ Storage::~Storage() {
         a->defer_free(ptr_);  // a free on a capturing stream would be recorded
         return;
     }
-    (void)hipFreeAsync(ptr_, stream_);
+    BlockCache& c = block_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    c.free[{device_, stream_}].emplace(block_, ptr_);
+}
+
+void release_cached_memory() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::vector<void*> blocks;
+    {
+        BlockCache& c = block_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        for (auto it = c.free.begin(); it != c.free.end();) {
+            if (it->first.first != dev) {
+                ++it;
+                continue;
+            }
+            for (auto& [size, p] : it->second) blocks.push_back(p);
+            it = c.free.erase(it);
+        }
+    }
+    if (blocks.empty()) return;
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    for (void* p : blocks) hip_check(hipFree(p), "hipFree");
+}
+
+size_t cached_bytes() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    BlockCache& c = block_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    size_t n = 0;
+    for (auto& [key, list] : c.free)
+        if (key.first == dev)
+            for (auto& [size, p] : list) n += size;
+    return n;
 }
 
 Tensor Tensor::empty(const std::vector<int64_t>& shape, Dtype dt) {

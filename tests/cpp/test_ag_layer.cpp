@@ -945,6 +945,42 @@ void test_graph_capture_rules() {
     report("replay without a capture returns false", !idle.replay());
 }
 
+// Storage's block cache: a freed block is handed to the next fitting
+// allocation on the same stream, never to another stream; release returns
+// everything.
+void test_block_cache() {
+    release_cached_memory();
+    const bool empty0 = cached_bytes() == 0;
+    void* p1 = nullptr;
+    {
+        Tensor t = Tensor::empty({1024, 1024});
+        p1 = t.data();
+    }
+    const bool cached = cached_bytes() >= (size_t(4) << 20);
+    Tensor t2 = Tensor::empty({1000, 1024});  // fits the cached 4 MiB block
+    const bool reused = t2.data() == p1 && cached_bytes() == 0;
+    Tensor t3 = Tensor::empty({2048, 1024});  // larger than anything cached
+    const bool fresh = t3.data() != p1;
+    report("block cache: a freed block is reused on its stream, a larger request is not served",
+           empty0 && cached && reused && fresh);
+
+    hipStream_t s = nullptr;
+    (void)hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    void* ps = nullptr;
+    {
+        StreamGuard guard(s);
+        Tensor ts = Tensor::empty({512, 1024});
+        ps = ts.data();
+    }
+    Tensor tn = Tensor::empty({512, 1024});  // the null stream: must not take s's block
+    const bool separate = tn.data() != ps;
+    release_cached_memory();
+    const bool released = cached_bytes() == 0;
+    (void)hipStreamDestroy(s);
+    report("block cache: blocks stay with their stream; release empties the cache",
+           separate && released);
+}
+
 int selftest() {
     const std::pair<const char*, void (*)()> tests[] = {
         {"reference_pattern", test_reference_pattern},
@@ -967,6 +1003,7 @@ int selftest() {
         {"graph_capture", [] { test_graph_capture(false); }},
         {"graph_capture_parallel", [] { test_graph_capture(true); }},
         {"graph_capture_rules", test_graph_capture_rules},
+        {"block_cache", test_block_cache},
     };
     for (auto& [name, fn] : tests) {
         std::printf("-- %s\n", name);

@@ -120,13 +120,16 @@ def test_graph_layer_against_oracle(cuda, name, shape):
 def test_layer_benchmark_program_runs(cuda, dtype):
     """The RMSNorm layer benchmark through the graph layer (the program the
     reference's empty Benchmark/RMSNormLayer.cpp stands for) runs both the
-    fused layer and the unfused rms(x) * gamma graph and reports them."""
+    fused layer and the unfused rms(x) * gamma graph, eagerly and as replays of
+    a captured step, and reports each."""
     import json
     proc = subprocess.run([LAYER_BENCH, "4", "128", "512", "3", "1", dtype, "both"],
                           capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
     lines = [json.loads(ln) for ln in proc.stdout.splitlines() if ln.startswith("{")]
-    assert [ln["path"].split(",")[1].split()[0] for ln in lines] == ["nn::RMSNorm", "ag::rms(x)"]
+    got = [(ln["path"].split(", ")[1].split()[0], ln["path"].split(", ")[-1]) for ln in lines]
+    assert got == [("nn::RMSNorm", "eager"), ("nn::RMSNorm", "captured"),
+                   ("ag::rms(x)", "eager"), ("ag::rms(x)", "captured")]
     for ln in lines:
         assert ln["shape"] == [4, 128, 512] and ln["dtype"] == dtype and ln["steps"] == 3
         assert ln["ms_per_step"] > 0 and ln["gbs"] > 0
