@@ -671,17 +671,59 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_fwd_kernel(
 // column chunk (owned-column RMW: the chunks are disjoint, and within one the
 // lane (c - c0) % kBlock owns column c).  Each column still sums the block's
 // rows in row order, whatever the chunking.
+// vec: every pointer 16-byte aligned and cols % kVec == 0 (chunk is then a
+// multiple of kBlock * kVec): each lane takes kVec consecutive columns, with
+// the same arithmetic per element and the same order per column.
 template <class S>
 __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
     const typename S::T* __restrict__ gy, const typename S::T* __restrict__ a,
     const typename S::T* __restrict__ b, typename S::T* __restrict__ da,
     float* __restrict__ partials, int64_t rows, int cols, int64_t rpb, int acc_da,
-    int64_t chunk) {
+    int64_t chunk, int vec) {
+    constexpr int W = S::kVec;
     const int64_t row_begin = static_cast<int64_t>(blockIdx.x) * rpb;
     const int64_t row_end = row_begin + rpb < rows ? row_begin + rpb : rows;
     float* prow = partials ? partials + static_cast<int64_t>(blockIdx.x) * cols : nullptr;
     const int64_t c0 = static_cast<int64_t>(blockIdx.y) * chunk;
     const int64_t c1 = chunk_end(c0, chunk, cols);
+    if (vec) {
+        for (int64_t row = row_begin; row < row_end; ++row) {
+            const int64_t off = row * static_cast<int64_t>(cols);
+            const bool first = row == row_begin;
+            for (int64_t c = c0 + threadIdx.x * W; c < c1; c += kBlock * W) {
+                float g[W];
+                S::unpack(load16_stream<S>(gy + off + c), g);
+                if (da) {
+                    float bb[W], o[W];
+                    S::unpack(load16<S>(b + c), bb);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) o[e] = g[e] * bb[e];
+                    if (acc_da) {
+                        float old[W];
+                        S::unpack(load16_stream<S>(da + off + c), old);
+#pragma unroll
+                        for (int e = 0; e < W; ++e) o[e] = acc_add(old[e], o[e]);
+                    }
+                    store16_stream<S>(da + off + c, S::pack(o));
+                }
+                if (prow) {
+                    float t[W];
+                    if (a) {
+                        float aa[W];
+                        S::unpack(load16_stream<S>(a + off + c), aa);
+#pragma unroll
+                        for (int e = 0; e < W; ++e) t[e] = g[e] * aa[e];
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < W; ++e) t[e] = g[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < W; ++e) prow[c + e] = first ? t[e] : prow[c + e] + t[e];
+                }
+            }
+        }
+        return;
+    }
     for (int64_t row = row_begin; row < row_end; ++row) {
         const int64_t off = row * static_cast<int64_t>(cols);
         const bool first = row == row_begin;
@@ -1207,18 +1249,21 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
         if (rc != AGK_OK || !db) return rc;
         return launch_finalize(partials, db, nblk, c, acc_db, st);
     }
-    const int64_t chunk = mul_chunk(nblk, c, 1);
+    const int w = dtype == AGK_F32 ? F32::kVec : BF16::kVec;
+    const int vec = c % w == 0 && aligned16(gy) && (!a || aligned16(a)) && (!b || aligned16(b)) &&
+                    (!da || aligned16(da));
+    const int64_t chunk = mul_chunk(nblk, c, vec ? w : 1);
     const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>((c + chunk - 1) / chunk));
     if (dtype == AGK_F32) {
         hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, grid, dim3(kBlock), 0, st,
                            static_cast<const float*>(gy), static_cast<const float*>(a),
                            static_cast<const float*>(b), static_cast<float*>(da), partials, rows,
-                           c, rpb, acc_da, chunk);
+                           c, rpb, acc_da, chunk, vec);
     } else {
         hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<BF16>, grid, dim3(kBlock), 0, st,
                            static_cast<const uint16_t*>(gy), static_cast<const uint16_t*>(a),
                            static_cast<const uint16_t*>(b), static_cast<uint16_t*>(da), partials,
-                           rows, c, rpb, acc_da, chunk);
+                           rows, c, rpb, acc_da, chunk, vec);
     }
     int rc = check_launch();
     if (rc != AGK_OK || !db) return rc;
@@ -1255,16 +1300,18 @@ int agk_sum_rows(const void* x, float* out, void* workspace, size_t workspace_by
         rc = dtype == AGK_F32 ? launch_sum_rows_resident<F32>(p, nblk, x, partials, rows, c, st)
                               : launch_sum_rows_resident<BF16>(p, nblk, x, partials, rows, c, st);
     } else {
-        const int64_t chunk = mul_chunk(nblk, c, 1);
+        const int w = dtype == AGK_F32 ? F32::kVec : BF16::kVec;
+        const int vec = c % w == 0 && aligned16(x);
+        const int64_t chunk = mul_chunk(nblk, c, vec ? w : 1);
         const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>((c + chunk - 1) / chunk));
         if (dtype == AGK_F32)
             hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<F32>, grid, dim3(kBlock), 0, st,
                                static_cast<const float*>(x), nullptr, nullptr, nullptr, partials,
-                               rows, c, rpb, 0, chunk);
+                               rows, c, rpb, 0, chunk, vec);
         else
             hipLaunchKernelGGL(mul_rowbcast_bwd_kernel<BF16>, grid, dim3(kBlock), 0, st,
                                static_cast<const uint16_t*>(x), nullptr, nullptr, nullptr,
-                               partials, rows, c, rpb, 0, chunk);
+                               partials, rows, c, rpb, 0, chunk, vec);
         rc = check_launch();
     }
     if (rc != AGK_OK) return rc;

@@ -316,6 +316,7 @@ def test_mul_one_long_row(cuda, dtype, cols):
 
 @pytest.mark.parametrize("dtype,shape", [("f32", (65536, 4096)), ("bf16", (8192, 11008)),
                                          ("f32", (333, 1001)), ("bf16", (7, 100)),
+                                         ("f32", (40, 16392)), ("bf16", (9, 32776)),
                                          ("f32", (1, 4096)), ("f32", (0, 64))])
 def test_sum_rows(cuda, dtype, shape):
     """agk_sum_rows (the linear layer's bias gradient): column sums in fp32
@@ -347,6 +348,7 @@ def test_sum_rows(cuda, dtype, shape):
 
 @pytest.mark.parametrize("dtype,shape", [("f32", (40, 4096)), ("f32", (33, 250)),
                                          ("bf16", (96, 8192)), ("bf16", (17, 100)),
+                                         ("f32", (24, 16392)), ("bf16", (9, 32776)),
                                          ("f32", (65536, 4096)), ("bf16", (16384, 8192))])
 def test_rms_mul_bwd(cuda, dtype, shape):
     """Bit-identical to mul_rowbcast_bwd followed by rmsnorm_bwd(gamma=None) on
