@@ -861,6 +861,21 @@ void test_linear_layer() {
         threw = true;
     }
     report("linear with a bias of the wrong width throws", threw);
+
+    // an empty batch: y is empty, dw = 0 (the GEMM's empty reduction) and db = 0
+    {
+        Tensor xe = Tensor::empty({0, 32}, Dtype::BFloat16);
+        xe.set_requires_grad(true);
+        Value x = make_tensor(xe, "x0"), w = bf16_leaf(normal(8 * 32, 106), {8, 32}, "w0"),
+              b = bf16_leaf(normal(8, 107), {8}, "b0");
+        Value y = linear(x, w, b);
+        Tensor seed = Tensor::empty({0, 8}, Dtype::BFloat16);
+        backward(y, &seed);
+        report("linear on an empty batch: dw and db are zero",
+               y.val().numel() == 0 && max_abs(w.grad().to_host_f32()) == 0.0 &&
+                   max_abs(b.grad().to_host_f32()) == 0.0 &&
+                   w.grad().dtype() == Dtype::Float32);
+    }
 }
 
 // The captured graph holds the unfused composition rms(.) * g2 too, whose
