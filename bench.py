@@ -182,31 +182,42 @@ def run(cfg_name, steps, warmup, cpu_seconds):
                      device=dev)
     stream = torch.cuda.current_stream()
 
-    def step(i, ev=None):
+    def step(i, ev_fwd=None, ev_bwd=None):
         x, g, dy, y, inv, dx, dg = sets[i % nsets]
-        if ev is not None:
-            ev[0].record(stream)
+        if ev_fwd is not None:
+            ev_fwd[0].record(stream)
         agk.rmsnorm_fwd(x, g, cfg.eps, y=y, inv_rms=inv, stream=stream)
-        if ev is not None:
-            ev[1].record(stream)
+        if ev_fwd is not None:
+            ev_fwd[1].record(stream)
+        if ev_bwd is not None:
+            ev_bwd[0].record(stream)
         agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=stream)
-        if ev is not None:
-            ev[2].record(stream)
+        if ev_bwd is not None:
+            ev_bwd[1].record(stream)
 
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
 
-    events = [[TimingEvent() for _ in range(3)] for _ in range(steps)]
+    # The timed region: K steps, two events per step around the backward (the
+    # roofline kernel), recorded on the stream the kernels run on.
+    events = [[TimingEvent() for _ in range(2)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        step(i, events[i])
+        step(i, ev_bwd=events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    bwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
 
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / steps
+    # Outside the timed region: the same steps again with the events around
+    # the forward instead, for the per-kernel breakdown.
+    fwd_events = [[TimingEvent() for _ in range(2)] for _ in range(steps)]
+    for i in range(steps):
+        step(i, ev_fwd=fwd_events[i])
+    torch.cuda.synchronize()
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in fwd_events) / steps
+
     ms_per_step = wall * 1e3 / steps
     alg = cfg.algorithmic_bytes()
     value = alg / (ms_per_step * 1e-3) / 1e9
@@ -541,6 +552,56 @@ def copy_probe(mib, steps):
     print(json.dumps({"copy_probe_bytes_each_way": n * 4, "dispatches": steps}), flush=True)
 
 
+STREAM_MIXES = (("copy (1 read + 1 write, as the forward)", 1, 1),
+                ("2 reads + 1 write (as the backward)", 2, 1),
+                ("read only", 1, 0))
+STREAM_GRIDS = (2048, 8192, 65536)
+
+
+def stream_probe(mib, steps):
+    """The practical HBM ceiling of this device for the path's traffic mixes.
+
+    A grid-stride streaming kernel (agk_probe_stream: 16-byte slots, four in
+    flight per lane) over MIB-MiB buffers, with plain and with non-temporal
+    accesses, at several grid sizes; HIP events on the launch stream.  Prints
+    one JSON line per (mix, cache policy) with the best grid's GB/s.
+    """
+    import torch
+
+    import cgadimpl_amd as agk
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    nbytes = mib << 20
+    a = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev)
+    b = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev)
+    c = torch.empty_like(a)
+    stream = torch.cuda.current_stream()
+    results = []
+    for name, reads, writes in STREAM_MIXES:
+        for nt in (False, True):
+            per_grid = {}
+            for grid in STREAM_GRIDS:
+                def launch():
+                    agk.probe_stream(a, b, c, nbytes, reads, writes, nt, grid, stream=stream)
+                for _ in range(3):
+                    launch()
+                e0, e1 = TimingEvent(), TimingEvent()
+                e0.record(stream)
+                for _ in range(steps):
+                    launch()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / steps
+                per_grid[grid] = round((reads + writes) * nbytes / (us * 1e-6) / 1e9, 1)
+            best = max(per_grid.values())
+            rec = {"stream_probe": name, "reads": reads, "writes": writes, "nontemporal": nt,
+                   "mib_per_buffer": mib, "launches": steps, "gbs_by_grid": per_grid,
+                   "best_gbs": best, "pct_of_hbm_peak": round(100.0 * best / HBM_PEAK_GBS, 2)}
+            results.append(rec)
+            print(json.dumps(rec), flush=True)
+    return results
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -559,9 +620,15 @@ def main():
                     help="CPU baseline budget in seconds (0 disables it)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run MIB-MiB device copies (counter calibration), then exit")
+    ap.add_argument("--stream-probe", type=int, default=0, metavar="MIB",
+                    help="only time the HBM streaming probe (copy, 2 reads + 1 write, read "
+                         "only; plain and non-temporal) over MIB-MiB buffers, then exit")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe(args.copy_probe, args.steps)
+        return
+    if args.stream_probe:
+        stream_probe(args.stream_probe, min(args.steps, 50))
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

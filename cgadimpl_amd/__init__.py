@@ -17,7 +17,7 @@ __all__ = [
     "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
     "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "rmsnorm_jvp", "layernorm_fwd",
     "layernorm_bwd", "softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
-    "logsumexp_jvp", "AGK_F32", "AGK_BF16", "STATUS",
+    "logsumexp_jvp", "probe_stream", "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -66,6 +66,8 @@ SIGNATURES = {
     "agk_logsumexp_fwd": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_logsumexp_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_logsumexp_jvp": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_probe_stream": (ctypes.c_int, [_P, _P, _P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
     "agk_version": (ctypes.c_char_p, []),
@@ -482,3 +484,12 @@ def logsumexp_jvp(z, tz, ty=None, stream=None):
                                  _stream(stream))
     _check(rc, "agk_logsumexp_jvp")
     return ty
+
+
+def probe_stream(a, b, c, nbytes: int, reads: int, writes: int, nontemporal: bool, grid: int,
+                 stream=None) -> None:
+    """HBM streaming probe (diagnostic): reads `reads` buffers, writes `writes`."""
+    rc = lib().agk_probe_stream(_ptr(a), _ptr(b) if b is not None else None, _ptr(c), int(nbytes),
+                                int(reads), int(writes), int(bool(nontemporal)), int(grid),
+                                _stream(stream))
+    _check(rc, "agk_probe_stream")

@@ -114,7 +114,8 @@ def build_all(verbose: bool = True) -> list[str]:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(LIB, exist_ok=True)
     jobs = [
-        lambda: hip_library("libagk_rmsnorm.so", ["rmsnorm.hip", "gemm.hip", "rowops.hip"]),
+        lambda: hip_library("libagk_rmsnorm.so",
+                            ["rmsnorm.hip", "gemm.hip", "rowops.hip", "probe.hip"]),
         lambda: host_library("libagk_synth.so", ["synth.cpp"]),
     ]
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:

@@ -1,0 +1,113 @@
+// probe.hip -- HBM streaming probe: the bandwidth a plain streaming kernel
+// reaches on this device for the RMSNorm path's traffic mixes (one read + one
+// write, as the forward; two reads + one write, as the backward; reads only),
+// with and without the non-temporal cache policy the row kernels use.  It is
+// the practical ceiling the row kernels are measured against, next to the
+// vendor peak.  No reference counterpart; a diagnostic of this library.
+//
+// Each lane moves 16-byte slots in a grid-stride loop.  Four independent
+// slots per lane are in flight per iteration, so a wave issues four loads
+// before it waits; the sizes are multiples of 64 slots per lane group.
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "agk_rmsnorm.h"
+#include "rowcommon.hpp"
+
+namespace agk {
+
+constexpr int kProbeBlock = 256;
+constexpr int kProbeUnroll = 4;
+
+template <bool NT>
+__device__ __forceinline__ u32x4 probe_load(const u32x4* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    return *p;
+}
+template <bool NT>
+__device__ __forceinline__ void probe_store(u32x4* p, u32x4 v) {
+    if constexpr (NT)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
+}
+
+// READS in {1, 2}, WRITES in {0, 1}.  n = slots per buffer, a multiple of
+// kProbeUnroll * kProbeBlock * gridDim.x is not required: the tail is guarded.
+template <int READS, int WRITES, bool NT>
+__global__ __launch_bounds__(kProbeBlock) void probe_stream_kernel(const u32x4* __restrict__ a,
+                                                                   const u32x4* __restrict__ b,
+                                                                   u32x4* __restrict__ c,
+                                                                   int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kProbeBlock;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * kProbeBlock + threadIdx.x;
+    u32x4 sink = u32x4{0u, 0u, 0u, 0u};
+    for (; i + (kProbeUnroll - 1) * stride < n; i += kProbeUnroll * stride) {
+        u32x4 v[kProbeUnroll];
+#pragma unroll
+        for (int u = 0; u < kProbeUnroll; ++u) v[u] = probe_load<NT>(a + i + u * stride);
+        if constexpr (READS == 2) {
+#pragma unroll
+            for (int u = 0; u < kProbeUnroll; ++u) v[u] ^= probe_load<NT>(b + i + u * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < kProbeUnroll; ++u) {
+            if constexpr (WRITES == 1)
+                probe_store<NT>(c + i + u * stride, v[u]);
+            else
+                sink ^= v[u];
+        }
+    }
+    for (; i < n; i += stride) {
+        u32x4 v = probe_load<NT>(a + i);
+        if constexpr (READS == 2) v ^= probe_load<NT>(b + i);
+        if constexpr (WRITES == 1)
+            probe_store<NT>(c + i, v);
+        else
+            sink ^= v;
+    }
+    if constexpr (WRITES == 0) {
+        // Keeps the loads: a store that the data decides on (all-ones XOR of
+        // every slot this lane read), written to slot 0 of c, which the
+        // caller provides.
+        if (sink.x == 0xffffffffu && sink.y == 0xffffffffu && sink.z == 0xffffffffu &&
+            sink.w == 0xffffffffu)
+            c[0] = sink;
+    }
+}
+
+}  // namespace agk
+
+extern "C" int agk_probe_stream(const void* a, const void* b, void* c, int64_t bytes, int reads,
+                                int writes, int nontemporal, int grid, agk_stream_t stream) {
+    using namespace agk;
+    if (bytes < 0 || (bytes & 15) != 0 || grid <= 0) return AGK_EINVAL;
+    if (reads != 1 && reads != 2) return AGK_EINVAL;
+    if (writes != 0 && writes != 1) return AGK_EINVAL;
+    if (!a || !c || (reads == 2 && !b)) return AGK_EINVAL;
+    if (bytes == 0) return AGK_OK;
+    clear_pending_error();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const u32x4* pa = static_cast<const u32x4*>(a);
+    const u32x4* pb = static_cast<const u32x4*>(b);
+    u32x4* pc = static_cast<u32x4*>(c);
+    const int64_t n = bytes / 16;
+    const dim3 g(static_cast<unsigned>(grid)), blk(kProbeBlock);
+#define AGK_PROBE(R, W, NT) \
+    hipLaunchKernelGGL((probe_stream_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, n)
+    const int key = (reads - 1) * 4 + writes * 2 + (nontemporal ? 1 : 0);
+    switch (key) {
+        case 0: AGK_PROBE(1, 0, false); break;
+        case 1: AGK_PROBE(1, 0, true); break;
+        case 2: AGK_PROBE(1, 1, false); break;
+        case 3: AGK_PROBE(1, 1, true); break;
+        case 4: AGK_PROBE(2, 0, false); break;
+        case 5: AGK_PROBE(2, 0, true); break;
+        case 6: AGK_PROBE(2, 1, false); break;
+        default: AGK_PROBE(2, 1, true); break;
+    }
+#undef AGK_PROBE
+    return check_launch();
+}

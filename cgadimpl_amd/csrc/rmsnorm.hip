@@ -422,25 +422,22 @@ __device__ __forceinline__ void bwd_write_partial(float* __restrict__ prow, int 
     }
 }
 
-// Rows are dealt round-robin to the gridDim.x workgroups; workgroup b writes
-// partial row b.
-template <class S, int TPR, int NV, int G, int NSET, bool ACC, int KIND>
-__device__ __forceinline__ void bwd_resident_body(
-    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
-    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
-    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ partials,
-    int64_t rows, int cols, float (*red)[TPR > 64 ? G * (TPR / 64) : 1], float* lds_part) {
+// The skeleton's per-lane context for workgroup blk of a grid of nblk row
+// workgroups (group q of workgroup blk takes rows blk*G + q + k*nblk*G), and
+// the lane's slots of gamma.
+template <class S, int TPR, int NV, int G, bool ACC, int KIND>
+__device__ __forceinline__ void bwd_setup(BwdCtx<S, TPR, NV, G, ACC, KIND>& c, u32x4 (&gv)[NV],
+                                          const typename S::T* x, const typename S::T* gamma,
+                                          const float* inv_rms, const typename S::T* dy,
+                                          typename S::T* dx, typename S::T* dr, int64_t rows,
+                                          int cols, int64_t blk, int64_t nblk) {
     using T = typename S::T;
     constexpr int W = S::kVec;
     constexpr int RPW = TPR >= 64 ? 1 : 64 / TPR;
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int t = threadIdx.x % TPR;
-    const int grp = threadIdx.x / TPR;
     const int sub = TPR >= 64 ? 0 : lane / TPR;  // the lane's row among the wave's rows
-
-    BwdCtx<S, TPR, NV, G, ACC, KIND> c;
     c.x = x;
     c.gamma = gamma;
     c.inv_rms = inv_rms;
@@ -448,8 +445,8 @@ __device__ __forceinline__ void bwd_resident_body(
     c.dx = dx;
     c.dr = dr;
     c.rows = rows;
-    c.first = static_cast<int64_t>(blockIdx.x) * G;
-    c.stride = static_cast<int64_t>(gridDim.x) * G;
+    c.first = blk * G;
+    c.stride = nblk * G;
     c.cols = cols;
     c.wgrp0 = TPR >= 64 ? wave / (TPR / 64) : wave * RPW;
     c.row_bytes = static_cast<uint32_t>(cols) * static_cast<uint32_t>(sizeof(T));
@@ -466,14 +463,29 @@ __device__ __forceinline__ void bwd_resident_body(
                                  static_cast<uint32_t>(col)) * static_cast<uint32_t>(sizeof(T))
                               : kOffOut;
     }
-
-    const bool has_gamma = gamma != nullptr;
-    u32x4 gv[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int col = (t + k * TPR) * W;
-        gv[k] = (has_gamma && col < cols) ? load16<S>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
+        gv[k] = (gamma != nullptr && col < cols) ? load16<S>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
     }
+}
+
+// Rows are dealt round-robin to the gridDim.x workgroups; workgroup b writes
+// partial row b.
+template <class S, int TPR, int NV, int G, int NSET, bool ACC, int KIND>
+__device__ __forceinline__ void bwd_resident_body(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ partials,
+    int64_t rows, int cols, float (*red)[TPR > 64 ? G * (TPR / 64) : 1], float* lds_part) {
+    constexpr int W = S::kVec;
+    const int t = threadIdx.x % TPR;
+    const int grp = threadIdx.x / TPR;
+
+    BwdCtx<S, TPR, NV, G, ACC, KIND> c;
+    u32x4 gv[NV];
+    bwd_setup(c, gv, x, gamma, inv_rms, dy, dx, dr, rows, cols, blockIdx.x, gridDim.x);
+    const bool has_gamma = gamma != nullptr;
     float dg[NV][W];
 #pragma unroll
     for (int k = 0; k < NV; ++k)
@@ -536,6 +548,131 @@ __global__ __launch_bounds__(TPR * G) void sum_rows_resident(const typename S::T
     bwd_resident_body<S, TPR, NV, G, NSET, false, kBwdColSum>(nullptr, nullptr, nullptr, x,
                                                               nullptr, nullptr, partials, rows,
                                                               cols, red, lds_part);
+}
+
+// ---- few rows: row workgroups beside column workgroups -------------------------
+// With fewer rows than the resident backward has workgroups (kBwdBlocks), most
+// CUs would sit idle and the dgamma partial rows plus their finalize launch
+// would cost as much as the rows themselves.  Here one launch runs two kinds
+// of workgroup side by side:
+//  - row workgroups [0, nrow_blocks): one step of the resident skeleton over
+//    G rows (dx, and dr for the composition; the same arithmetic as the
+//    resident kernel, so dx is bit-identical to it);
+//  - column workgroups: 64 slots of columns each (kFewQuads lanes x kVec
+//    columns), split over kFewGroups row groups of one wave.  Row group q sums
+//    rows q, q + kFewGroups, ... in increasing order in fp64; the groups' sums
+//    are then added in group order and written to dgamma directly.  dgamma
+//    needs no row dot product, so these workgroups do not wait for the rows.
+// No partial rows, no finalize launch, no atomics; the summation order
+// depends only on rows.  The column term per KIND is the one the resident
+// kernel adds: dy*(x*r), dy*stored(x*r) (composition), gy*a (broadcast
+// multiply) or dy (column sums).
+constexpr int64_t kFewRowsMax = 255;  // rows below the resident backward's kBwdBlocks
+constexpr int kFewQuads = 64;         // column slots per column workgroup
+constexpr int kFewGroups = 16;        // row groups of a 1024-lane column workgroup
+constexpr int kFewBatch = 8;          // rows per group loaded before they are added
+
+template <class S, int TPR, int NV, int G, bool ACC, int KIND>
+__global__ __launch_bounds__(TPR * G) void bwd_fewrows(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ dgamma,
+    int64_t rows, int cols, int64_t nrow_blocks, int acc_dg) {
+    static_assert(TPR * G == kFewGroups * 64, "column workgroups are 16 waves");
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    __shared__ float red[2][TPR > 64 ? G * (TPR / 64) : 1];
+    __shared__ double cred[kFewGroups][kFewQuads * 4];
+    if (static_cast<int64_t>(blockIdx.x) < nrow_blocks) {  // workgroup-uniform
+        BwdCtx<S, TPR, NV, G, ACC, KIND> c;
+        u32x4 gv[NV];
+        bwd_setup(c, gv, x, gamma, inv_rms, dy, dx, dr, rows, cols, blockIdx.x, nrow_blocks);
+        float dg[NV][W];  // unused: dgamma comes from the column workgroups
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+#pragma unroll
+            for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
+        BwdSet<S, NV, ACC> A;
+        c.issue(A, 0);
+        bwd_process(c, A, 0, 0, gv, gamma != nullptr, dg, red);
+        return;
+    }
+    // column workgroup
+    const int lane = threadIdx.x & 63;
+    const int grp = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t cb = static_cast<int64_t>(blockIdx.x) - nrow_blocks;
+    const int col = static_cast<int>((cb * kFewQuads + lane) * W);
+    const uint32_t off = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    double acc[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) acc[e] = 0.0;
+    for (int64_t r0 = grp; r0 < rows; r0 += static_cast<int64_t>(kFewGroups) * kFewBatch) {
+        u32x4 xv[kFewBatch], dv[kFewBatch];
+        float rr[kFewBatch];
+#pragma unroll
+        for (int u = 0; u < kFewBatch; ++u) {
+            // The wave's row of this batch entry: a resource of zero bytes past
+            // the last row, so its loads return zeros and its terms add +0.0.
+            const int64_t row = r0 + static_cast<int64_t>(u) * kFewGroups;
+            const uint32_t n = row < rows ? 1u : 0u;
+            const int64_t e0 = (row < rows ? row : 0) * static_cast<int64_t>(cols);
+            dv[u] = bload16_stream(make_rsrc(dy + e0, n * row_bytes), off);
+            if constexpr (KIND != kBwdColSum)
+                xv[u] = bload16_stream(make_rsrc(x + e0, n * row_bytes), off);
+            if constexpr (KIND == kBwdRms || KIND == kBwdRmsMul)
+                rr[u] = bload_f32(make_rsrc(inv_rms + (row < rows ? row : 0), n * 4u), 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kFewBatch; ++u) {
+            float fd[W];
+            S::unpack(dv[u], fd);
+            float term[W];
+            if constexpr (KIND == kBwdColSum) {
+#pragma unroll
+                for (int e = 0; e < W; ++e) term[e] = fd[e];
+            } else {
+                float fx[W];
+                S::unpack(xv[u], fx);
+                if constexpr (KIND == kBwdMul) {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) term[e] = fd[e] * fx[e];
+                } else if constexpr (KIND == kBwdRmsMul) {
+                    float h[W];
+#pragma unroll
+                    for (int e = 0; e < W; ++e) h[e] = fx[e] * rr[u];
+                    S::unpack(S::pack(h), h);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) term[e] = fd[e] * h[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) term[e] = fd[e] * (fx[e] * rr[u]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) acc[e] += static_cast<double>(term[e]);
+        }
+    }
+    // Groups' sums in group order, 4 columns per lane at a time (bf16 lanes
+    // hold 8 columns: two rounds).
+#pragma unroll
+    for (int h = 0; h < W; h += 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cred[grp][lane * 4 + i] = acc[h + i];
+        __syncthreads();
+        if (threadIdx.x < kFewQuads * 4) {
+            const int l = static_cast<int>(threadIdx.x) >> 2, i = static_cast<int>(threadIdx.x) & 3;
+            double tot = cred[0][threadIdx.x];
+#pragma unroll
+            for (int q = 1; q < kFewGroups; ++q) tot += cred[q][threadIdx.x];
+            const int64_t c = (cb * kFewQuads + l) * W + h + i;
+            if (c < cols) {
+                const float v = static_cast<float>(tot);
+                dgamma[c] = acc_dg ? dgamma[c] + v : v;
+            }
+        }
+        __syncthreads();
+    }
 }
 
 // ---- looped kernels (any alignment, any width) --------------------------------
@@ -743,42 +880,77 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
 }
 
 // ---- dgamma: fixed-order column sum of the partial rows ------------------------
-// Workgroup: 64 columns x kFinSplits row splits.  Split s sums partial rows
-// s, s + kFinSplits, ... in increasing order in fp64; the split sums are then
-// added in split order.  The order depends only on nblk, never on timing.
-constexpr int kFinSplits = 16;
+// Workgroup: kFinCols columns x kFinSplits row splits.  Split s sums partial
+// rows s, s + kFinSplits, ... in increasing order in fp64; the split sums are
+// then added in split order.  The order depends only on nblk, never on timing
+// or on the path taken.  Each lane loads kFinBatch partial rows before it adds
+// any of them: the partials were just written by other XCDs' workgroups, so
+// every load misses this XCD's L2, and at the resident backward's 256 partial
+// rows one round trip covers all of them.  Narrow column chunks give one
+// workgroup per 16 columns (256 at 4096 columns), so the partials stream in
+// over most of the CUs rather than a quarter of them.
+// VEC: a lane sums 4 adjacent columns with 16-byte loads (cols % 4 == 0 and
+// partials 16-byte aligned, so every partial row's quads are aligned);
+// otherwise a lane sums one column with 4-byte loads.  Same order either way.
+constexpr int kFinSplits = 64;
+constexpr int kFinBatch = 4;
+constexpr int kFinCols = 16;  // columns per workgroup
 
-__global__ __launch_bounds__(64 * kFinSplits) void dgamma_finalize(
+template <bool VEC>
+__global__ __launch_bounds__((VEC ? kFinCols / 4 : kFinCols) * kFinSplits) void dgamma_finalize(
     const float* __restrict__ partials, float* __restrict__ dgamma, int64_t nblk, int cols,
     int accumulate) {
-    __shared__ double red[kFinSplits][64];
-    const int lane = threadIdx.x & 63;
-    const int split = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + lane;
-    double acc = 0.0;
-    if (c < cols) {
-        int64_t b = split;
-        // four independent loads in flight per step, added in row order
-        for (; b + 3 * kFinSplits < nblk; b += 4 * kFinSplits) {
-            const float p0 = partials[b * cols + c];
-            const float p1 = partials[(b + kFinSplits) * cols + c];
-            const float p2 = partials[(b + 2 * kFinSplits) * cols + c];
-            const float p3 = partials[(b + 3 * kFinSplits) * cols + c];
-            acc += p0;
-            acc += p1;
-            acc += p2;
-            acc += p3;
-        }
-        for (; b < nblk; b += kFinSplits) acc += partials[b * cols + c];
-    }
-    red[split][lane] = acc;
-    __syncthreads();
-    if (split == 0 && c < cols) {
-        double tot = red[0][lane];
+    constexpr int CPL = VEC ? 4 : 1;              // columns per lane
+    constexpr int LANES = kFinCols / CPL;         // lanes per split
+    __shared__ double red[kFinSplits][kFinCols];
+    const int q = threadIdx.x % LANES;
+    const int split = threadIdx.x / LANES;
+    const int c0 = blockIdx.x * kFinCols + q * CPL;
+    const bool in = c0 < cols;  // VEC: the whole quad is in (cols % 4 == 0)
+    // Loads are unconditional (a row or column past the end reads the last
+    // valid one instead) and the values are selected afterwards: loads behind
+    // branches would each wait for all earlier loads to return.  A skipped
+    // term adds +0.0, which leaves the sum unchanged (it starts at +0.0 and
+    // round-to-nearest never makes it -0.0).
+    const int cl = in ? c0 : cols - CPL;
+    double acc[CPL];
 #pragma unroll
-        for (int q = 1; q < kFinSplits; ++q) tot += red[q][lane];
-        const float v = static_cast<float>(tot);
-        dgamma[c] = accumulate ? dgamma[c] + v : v;
+    for (int i = 0; i < CPL; ++i) acc[i] = 0.0;
+    for (int64_t base = split; base < nblk; base += static_cast<int64_t>(kFinSplits) * kFinBatch) {
+        float v[kFinBatch][CPL];
+#pragma unroll
+        for (int u = 0; u < kFinBatch; ++u) {
+            const int64_t b = base + static_cast<int64_t>(u) * kFinSplits;
+            const float* p = partials + (b < nblk ? b : nblk - 1) * cols + cl;
+            if constexpr (VEC) {
+                const float4 t = *reinterpret_cast<const float4*>(p);
+                v[u][0] = t.x;
+                v[u][CPL > 1 ? 1 : 0] = t.y;
+                v[u][CPL > 2 ? 2 : 0] = t.z;
+                v[u][CPL > 3 ? 3 : 0] = t.w;
+            } else {
+                v[u][0] = *p;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kFinBatch; ++u) {
+            const bool take = in && base + static_cast<int64_t>(u) * kFinSplits < nblk;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) acc[i] += take ? v[u][i] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) red[split][q * CPL + i] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < kFinCols) {
+        const int c = blockIdx.x * kFinCols + static_cast<int>(threadIdx.x);
+        if (c < cols) {
+            double tot = red[0][threadIdx.x];
+#pragma unroll
+            for (int s2 = 1; s2 < kFinSplits; ++s2) tot += red[s2][threadIdx.x];
+            const float v = static_cast<float>(tot);
+            dgamma[c] = accumulate ? dgamma[c] + v : v;
+        }
     }
 }
 
@@ -1045,12 +1217,61 @@ int launch_rms_mul_bwd_resident(const Plan& p, int64_t nblk, const void* x, cons
     return AGK_EINVAL;
 }
 
+// The few-rows backward (bwd_fewrows) of KIND for a resident plan p with
+// rows <= kFewRowsMax: row workgroups when dx or dr is wanted, column
+// workgroups when dgamma is; dgamma is written (or added into, acc_dg)
+// directly.
+template <class S, int KIND>
+int launch_fewrows(const Plan& p, const void* x, const void* gamma, const float* inv_rms,
+                   const void* dy, void* dx, void* dr, float* dgamma, int64_t rows, int cols,
+                   int acc_dx, int acc_dg, hipStream_t st) {
+    using T = typename S::T;
+    const int64_t nrow_blocks = (dx != nullptr || dr != nullptr) ? (rows + p.g - 1) / p.g : 0;
+    const int64_t ncol_blocks =
+        dgamma != nullptr ? (cols / S::kVec + kFewQuads - 1) / kFewQuads : 0;
+    const int64_t grid = nrow_blocks + ncol_blocks;
+    if (grid == 0) return AGK_OK;
+    if (grid > 0x7fffffffLL) return AGK_EINVAL;
+    const bool acc = acc_dx && dx != nullptr;
+    const T* xp = static_cast<const T*>(x);
+    const T* gp = static_cast<const T*>(gamma);
+    const T* dyp = static_cast<const T*>(dy);
+    T* dxp = static_cast<T*>(dx);
+    T* drp = static_cast<T*>(dr);
+#define AGK_X(a, b, c, d)                                                                   \
+    if constexpr (bwd_shape_enabled<S>(a, b)) {                                             \
+        if (p.tpr == a && p.nv == b && p.g == c) {                                          \
+            if constexpr (KIND != kBwdColSum) {                                             \
+                if (acc) {                                                                  \
+                    hipLaunchKernelGGL((bwd_fewrows<S, a, b, c, true, KIND>),               \
+                                       dim3(static_cast<unsigned>(grid)), dim3(a * c), 0, st, \
+                                       xp, gp, inv_rms, dyp, dxp, drp, dgamma, rows, cols,  \
+                                       nrow_blocks, acc_dg);                                \
+                    return check_launch();                                                  \
+                }                                                                           \
+            }                                                                               \
+            hipLaunchKernelGGL((bwd_fewrows<S, a, b, c, false, KIND>),                      \
+                               dim3(static_cast<unsigned>(grid)), dim3(a * c), 0, st, xp, gp, \
+                               inv_rms, dyp, dxp, drp, dgamma, rows, cols, nrow_blocks,     \
+                               acc_dg);                                                     \
+            return check_launch();                                                          \
+        }                                                                                   \
+    }
+    AGK_BWD_SHAPES(AGK_X)
+#undef AGK_X
+    return AGK_EINVAL;
+}
+
 // dr == nullptr: the RMSNorm VJP (gamma optional); dr != nullptr: the
 // composition rms(x) * gamma (gamma required), dr receiving gy*gamma.
+// Rows that fit the resident shapes but are fewer than kFewRowsMax take the
+// few-rows kernel, which writes dgamma itself: nblk is then 0 (no partial
+// rows to finalize).  Otherwise nblk is the number of dgamma partial rows
+// written to `partials`.
 template <class S>
 int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
-               void* dx, void* dr, float* partials, int64_t rows, int cols, int accumulate,
-               hipStream_t st, int64_t& nblk) {
+               void* dx, void* dr, float* partials, float* dgamma, int64_t rows, int cols,
+               int accumulate, int acc_dg, hipStream_t st, int64_t& nblk) {
     using T = typename S::T;
     int64_t rpb = 0;
     Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
@@ -1058,6 +1279,13 @@ int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const voi
         p = Plan{};
         rpb = bwd_rows_per_block(rows);
         nblk = bwd_num_blocks(rows);
+    }
+    if (p.tpr != 0 && rows <= kFewRowsMax) {
+        nblk = 0;
+        return dr ? launch_fewrows<S, kBwdRmsMul>(p, x, gamma, inv_rms, dy, dx, dr, dgamma, rows,
+                                                  cols, accumulate, acc_dg, st)
+                  : launch_fewrows<S, kBwdRms>(p, x, gamma, inv_rms, dy, dx, nullptr, dgamma,
+                                               rows, cols, accumulate, acc_dg, st);
     }
     if (nblk > 0x7fffffffLL) return AGK_EINVAL;
     if (p.tpr == 0) {
@@ -1083,9 +1311,13 @@ int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const voi
 
 inline int launch_finalize(const float* partials, float* dgamma, int64_t nblk, int cols,
                            int accumulate, hipStream_t st) {
-    const unsigned grid = static_cast<unsigned>((cols + 63) / 64);
-    hipLaunchKernelGGL(dgamma_finalize, dim3(grid), dim3(64 * kFinSplits), 0, st, partials,
-                       dgamma, nblk, cols, accumulate);
+    const unsigned grid = static_cast<unsigned>((cols + kFinCols - 1) / kFinCols);
+    if (cols % 4 == 0 && aligned16(partials))
+        hipLaunchKernelGGL(dgamma_finalize<true>, dim3(grid), dim3(kFinCols / 4 * kFinSplits), 0,
+                           st, partials, dgamma, nblk, cols, accumulate);
+    else
+        hipLaunchKernelGGL(dgamma_finalize<false>, dim3(grid), dim3(kFinCols * kFinSplits), 0, st,
+                           partials, dgamma, nblk, cols, accumulate);
     return check_launch();
 }
 
@@ -1149,10 +1381,10 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     const int c = static_cast<int>(cols);
     int64_t nblk = 0;
     int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, partials,
-                                                rows, c, acc_dx, st, nblk)
+                                                dgamma, rows, c, acc_dx, acc_dg, st, nblk)
                               : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
-                                                 rows, c, acc_dx, st, nblk);
-    if (rc != AGK_OK || !dgamma) return rc;
+                                                 dgamma, rows, c, acc_dx, acc_dg, st, nblk);
+    if (rc != AGK_OK || !dgamma || nblk == 0) return rc;
     return launch_finalize(partials, dgamma, nblk, c, acc_dg, st);
 }
 
@@ -1180,11 +1412,11 @@ int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     }
     const int c = static_cast<int>(cols);
     int64_t nblk = 0;
-    int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, gy, dx, dr, partials, rows, c,
-                                                acc_dx, st, nblk)
-                              : launch_bwd<BF16>(x, gamma, inv_rms, gy, dx, dr, partials, rows,
-                                                 c, acc_dx, st, nblk);
-    if (rc != AGK_OK || !dgamma) return rc;
+    int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, gy, dx, dr, partials, dgamma,
+                                                rows, c, acc_dx, acc_dg, st, nblk)
+                              : launch_bwd<BF16>(x, gamma, inv_rms, gy, dx, dr, partials, dgamma,
+                                                 rows, c, acc_dx, acc_dg, st, nblk);
+    if (rc != AGK_OK || !dgamma || nblk == 0) return rc;
     return launch_finalize(partials, dgamma, nblk, c, acc_dg, st);
 }
 
@@ -1235,6 +1467,12 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b, void* da,
     const Plan p = dtype == AGK_F32 ? bwd_plan_for<F32>(a, b, gy, da, rows, c, nblk, rpb)
                                     : bwd_plan_for<BF16>(a, b, gy, da, rows, c, nblk, rpb);
     if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    if (p.tpr != 0 && rows <= kFewRowsMax)  // few rows: db written directly
+        return dtype == AGK_F32
+                   ? launch_fewrows<F32, kBwdMul>(p, a, b, nullptr, gy, da, nullptr, db, rows, c,
+                                                  acc_da, acc_db, st)
+                   : launch_fewrows<BF16, kBwdMul>(p, a, b, nullptr, gy, da, nullptr, db, rows, c,
+                                                   acc_da, acc_db, st);
     if (p.tpr != 0) {  // register-resident, as the RMSNorm backward
         const bool acc = acc_da && da;
         int rc = dtype == AGK_F32
@@ -1295,6 +1533,12 @@ int agk_sum_rows(const void* x, float* out, void* workspace, size_t workspace_by
                                     : bwd_plan_for<BF16>(x, nullptr, x, nullptr, rows, c, nblk,
                                                          rpb);
     if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    if (p.tpr != 0 && rows <= kFewRowsMax)  // few rows: out written directly
+        return dtype == AGK_F32
+                   ? launch_fewrows<F32, kBwdColSum>(p, nullptr, nullptr, nullptr, x, nullptr,
+                                                     nullptr, out, rows, c, 0, accumulate, st)
+                   : launch_fewrows<BF16, kBwdColSum>(p, nullptr, nullptr, nullptr, x, nullptr,
+                                                      nullptr, out, rows, c, 0, accumulate, st);
     int rc;
     if (p.tpr != 0) {
         rc = dtype == AGK_F32 ? launch_sum_rows_resident<F32>(p, nblk, x, partials, rows, c, st)
@@ -1335,6 +1579,7 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
         const int c = static_cast<int>(cols);
         p = dtype == AGK_F32 ? bwd_plan_for<F32>(a, a, a, a, rows, c, nblk, rpb)
                              : bwd_plan_for<BF16>(a, a, a, a, rows, c, nblk, rpb);
+        if (p.tpr != 0 && rows <= kFewRowsMax) rpb = nblk = 0;  // few rows: no partial rows
     }
     plan[0] = p.tpr;
     plan[1] = p.nv;

@@ -108,8 +108,9 @@ __device__ __forceinline__ void opaque(u32x4& a, u32x4& b) {
 // 16-byte accesses.  load16 is for data that is reused (gamma); the
 // stream variants set the non-temporal bit, for row data that each kernel
 // touches exactly once, so it does not displace reused lines in L2 and the
-// Infinity Cache (measured on MI355X: a plain 16-byte copy kernel moves
-// 6.2 TB/s, the same kernel with non-temporal loads and stores 6.5 TB/s).
+// Infinity Cache (measured on MI355X with the RMSNorm backward at
+// [65536, 4096] fp32: non-temporal loads and stores 521-525 us; plain stores
+// 586-589 us, plain loads 577 us, write-through stores (sc1) 533-538 us).
 template <class S>
 __device__ __forceinline__ u32x4 load16(const typename S::T* p) {
     return *reinterpret_cast<const u32x4*>(p);
@@ -217,7 +218,7 @@ struct Plan {
 // storage types (hipcc -Rpass-analysis=kernel-resource-usage); wider rows
 // take the looped kernels.
 #define AGK_FWD_SHAPES(X)                                                                  \
-    X(1, 1, 256) X(2, 1, 128) X(4, 1, 64) X(8, 1, 32) X(16, 1, 16) X(32, 1, 16) X(64, 1, 8) \
+    X(1, 1, 512) X(1, 2, 512) X(2, 2, 256) X(4, 2, 128) X(8, 2, 64) X(16, 2, 32) X(32, 2, 16) \
     X(64, 2, 4) X(64, 4, 4) X(128, 2, 2) X(128, 4, 2) X(256, 2, 1) X(256, 4, 1)            \
     X(512, 2, 1) X(512, 4, 1) X(1024, 2, 1) X(1024, 4, 1) X(1024, 8, 1)
 
@@ -243,8 +244,13 @@ inline int pow2_at_least(int64_t v) {
 
 // Resident shapes, chosen from the row width in 16-byte slots (nslot) and the
 // row count (measured on MI355X with a sweep of every instantiated shape):
-//  - rows of at most 64 slots: one slot per lane, TPR = nslot rounded up to a
-//    power of two, several rows per workgroup;
+//  - rows of at most 64 slots: two slots per lane (one for a one-slot row),
+//    TPR = nslot / 2 rounded up to a power of two (at most 32 lanes, so a row
+//    never spans waves and needs no barrier), and 512-lane workgroups of
+//    512 / TPR rows.  Swept at 1 GiB over fp32 widths 64-512 and bf16 widths
+//    128-1024 against 1- and 4-slot shapes and 256-lane workgroups: within
+//    1 % of the best shape at every width, up to 3 % ahead of one slot per
+//    lane (bf16 rows of 128-512 columns);
 //  - wider rows: NV slots per lane, TPR = nslot / NV rounded up.  With many
 //    rows NV = 2 (more lanes in flight per row); with fewer rows NV = 4, so
 //    the grid still has enough workgroups.  NV doubles when a row would need
@@ -255,9 +261,9 @@ inline Plan pick_plan(const Shape3 (&shapes)[N], int64_t nslot, int nv0, int sma
                       int max_nv) {
     Plan p;
     if (nslot <= 64) {
-        p.tpr = pow2_at_least(nslot);
-        p.nv = 1;
-        p.g = p.tpr >= 32 ? small_threads / p.tpr : 256 / p.tpr;
+        p.nv = nslot >= 2 ? 2 : 1;
+        p.tpr = pow2_at_least((nslot + p.nv - 1) / p.nv);
+        p.g = small_threads / p.tpr;
     } else {
         int nv = nv0;
         int64_t tpr = pow2_at_least((nslot + nv - 1) / nv);

@@ -215,10 +215,22 @@ int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_ds
  *    rows per dgamma partial row (backward; ceil(rows / partial rows)),
  *    dgamma partial rows (backward)};
  * lanes per row == 0 means the looped kernel (rows that are not a whole
- * number of 16-byte slots, or too wide to keep in registers).  Used by the
+ * number of 16-byte slots, or too wide to keep in registers).  A resident
+ * backward of at most 255 rows reports 0 partial rows: it runs row and
+ * column workgroups in one launch and writes dgamma directly.  Used by the
  * tests to run every reachable shape.                                        */
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan);
+
+/* Diagnostic, with no counterpart in the reference: an HBM streaming probe,
+ * the practical ceiling the row kernels are measured against.  A grid-stride
+ * kernel of `grid` 256-lane workgroups moves `bytes` (a multiple of 16) per
+ * buffer in 16-byte slots: reads == 1 reads a, reads == 2 reads a and b;
+ * writes == 1 writes c (a, or a ^ b), writes == 0 writes nothing (c must
+ * still point at 16 writable bytes).  nontemporal != 0 sets the
+ * non-temporal cache policy on every access, as the row kernels do.       */
+int agk_probe_stream(const void* a, const void* b, void* c, int64_t bytes, int reads,
+                     int writes, int nontemporal, int grid, agk_stream_t stream);
 
 /* Human-readable name of a status code (static storage). */
 const char* agk_status_str(int status);

@@ -83,13 +83,17 @@ def test_workspace_bytes_rule():
     for rows in (1, 2, 255, 256, 257, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097,
                  65535, 10 ** 7):
         assert ws(rows, 8) == _blocks(rows) * 8 * 4, rows
-        # resident kernels: min(256, rows) workgroups (one partial row each),
-        # never more than the workspace holds
+        # resident kernels: 256 workgroups (one partial row each), never more
+        # than the workspace holds; below 256 rows, row and column workgroups
+        # in one launch and no partial rows
         for dt in (agk.AGK_F32, agk.AGK_BF16):
             plan = agk.launch_plan(rows, 8 * 16, dt, True)
             assert plan["tpr"] > 0
-            assert plan["nblk"] == min(256, rows) <= _blocks(rows)
-            assert plan["rpb"] == -(-rows // plan["nblk"])
+            if rows < 256:
+                assert plan["nblk"] == 0 and plan["rpb"] == 0
+            else:
+                assert plan["nblk"] == 256 <= _blocks(rows)
+                assert plan["rpb"] == -(-rows // plan["nblk"])
         # the looped kernel (cols not a whole number of 16-byte slots): runs of
         # rpb consecutive rows, one partial row per run
         plan = agk.launch_plan(rows, 9, agk.AGK_F32, True)
