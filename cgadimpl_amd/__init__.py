@@ -39,6 +39,8 @@ SIGNATURES = {
     "agk_rmsnorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_rmsnorm_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
                                        ctypes.c_int, ctypes.c_int, _P]),
+    "agk_rmsnorm_bwd_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_int,
+                                               ctypes.c_int, _P]),
     "agk_mul_rowbcast_fwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_mul_rowbcast_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_mul_rowbcast_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,

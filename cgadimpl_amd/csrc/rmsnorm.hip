@@ -35,6 +35,8 @@
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
+
+#include <mutex>
 #include <type_traits>
 
 #include "agk_rmsnorm.h"
@@ -1329,6 +1331,81 @@ inline int zero_fill(float* p, int64_t n, hipStream_t st) {
     return check_launch();
 }
 
+// Bytes of dgamma partial rows the backward writes for these pointers and
+// sizes (the path launch_bwd takes): none for the few-rows kernel, 256 rows
+// for the resident kernel, the looped kernel's row blocks otherwise.
+template <class S>
+inline size_t bwd_partials_bytes(const void* x, const void* gamma, const void* dy,
+                                 const void* dx, int64_t rows, int cols) {
+    int64_t nblk = 0, rpb = 0;
+    const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    if (p.tpr != 0 && rows <= kFewRowsMax) return 0;
+    return static_cast<size_t>(nblk) * static_cast<size_t>(cols) * sizeof(float);
+}
+
+// The RMSNorm backward with validated arguments and dgamma partials at
+// `partials` (which must hold bwd_partials_bytes when dgamma != NULL).
+inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rms,
+                           const void* dy, void* dx, float* dgamma, float* partials, int64_t rows,
+                           int cols, int dtype, int acc_dx, int acc_dg, hipStream_t st) {
+    int64_t nblk = 0;
+    int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, partials,
+                                                dgamma, rows, cols, acc_dx, acc_dg, st, nblk)
+                              : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
+                                                 dgamma, rows, cols, acc_dx, acc_dg, st, nblk);
+    if (rc != AGK_OK || !dgamma || nblk == 0) return rc;
+    return launch_finalize(partials, dgamma, nblk, cols, acc_dg, st);
+}
+
+}  // namespace agk
+
+// ---- scratch of the entry point that allocates nothing ---------------------------
+// agk_rmsnorm_bwd_noalloc keeps its dgamma partial rows here instead of in a
+// caller workspace.  Every device the library runs on holds one copy for the
+// life of the process; every call on that device shares it (overlapping calls
+// on one device race).  The kernels write every partial row they later read,
+// so nothing in it needs clearing between calls.  Host code must not pass the
+// name to a kernel (on the host it is a stand-in, not a device address): it
+// uses the address hipGetSymbolAddress gives for the device, kept per device.
+static __device__ __align__(256) float scratch[AGK_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace agk {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the device `stream` runs on (the current
+// device for the null stream), looked up once per device with that device
+// current.
+inline int scratch_on_device(hipStream_t stream, float** out) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return status_from_hip(e);
+    int dev = cur;
+    if (stream != nullptr) {
+        hipDevice_t d = 0;
+        e = hipStreamGetDevice(stream, &d);
+        if (e != hipSuccess) return status_from_hip(e);
+        dev = static_cast<int>(d);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return AGK_EINVAL;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return status_from_hip(e);
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) {
+            const hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess) return status_from_hip(e);
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return AGK_OK;
+}
+
 }  // namespace agk
 
 // ---- C ABI ----------------------------------------------------------------------
@@ -1378,14 +1455,39 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
         if (!workspace || workspace_bytes < need) return AGK_EWORKSPACE;
         partials = static_cast<float*>(workspace);
     }
+    return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, partials, rows,
+                           static_cast<int>(cols), dtype, acc_dx, acc_dg, st);
+}
+
+int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_rms,
+                            const void* dy, void* dx, float* dgamma, int64_t rows, int64_t cols,
+                            int dtype, int accumulate, agk_stream_t stream) {
+    using namespace agk;
+    if (int rc = check_sizes(rows, cols)) return rc;
+    if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    clear_pending_error();
+    if (accumulate & ~AGK_ACCUM_ALL) return AGK_EINVAL;
+    const int acc_dx = (accumulate & AGK_ACCUM_DX) != 0;
+    const int acc_dg = (accumulate & AGK_ACCUM_DGAMMA) != 0;
+    if (rows == 0 || cols == 0) {
+        if (dgamma && !acc_dg && cols > 0) return zero_fill(dgamma, cols, st);
+        return AGK_OK;
+    }
+    if (!x || !inv_rms || !dy) return AGK_EINVAL;
+    if (!dx && !dgamma) return AGK_OK;  // nothing requested
     const int c = static_cast<int>(cols);
-    int64_t nblk = 0;
-    int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, partials,
-                                                dgamma, rows, c, acc_dx, acc_dg, st, nblk)
-                              : launch_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
-                                                 dgamma, rows, c, acc_dx, acc_dg, st, nblk);
-    if (rc != AGK_OK || !dgamma || nblk == 0) return rc;
-    return launch_finalize(partials, dgamma, nblk, c, acc_dg, st);
+    float* partials = nullptr;
+    if (dgamma) {
+        const size_t need = dtype == AGK_F32 ? bwd_partials_bytes<F32>(x, gamma, dy, dx, rows, c)
+                                             : bwd_partials_bytes<BF16>(x, gamma, dy, dx, rows, c);
+        if (need > AGK_NOALLOC_SCRATCH_BYTES) return AGK_EWORKSPACE;
+        if (need > 0) {
+            if (int rc = scratch_on_device(st, &partials)) return rc;
+        }
+    }
+    return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, partials, rows, c, dtype, acc_dx,
+                           acc_dg, st);
 }
 
 int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms, const void* gy,

@@ -107,6 +107,23 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms,
                     size_t workspace_bytes, int64_t rows, int64_t cols,
                     int dtype, int accumulate, agk_stream_t stream);
 
+/* The backward above without a workspace: no counterpart in the reference.
+ * For callers that cannot allocate device memory around the call (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and accumulate bits as agk_rmsnorm_bwd; the dgamma
+ * partial rows go to a scratch array the library holds in each device's
+ * memory (AGK_NOALLOC_SCRATCH_BYTES per device, for the life of the process)
+ * instead of a caller workspace, and the call allocates nothing.  Sizes whose
+ * partial rows exceed the array (more than 256 * cols * 4 bytes on the
+ * register-resident path: cols > 32768; the looped path's row blocks
+ * otherwise) return AGK_EWORKSPACE.  Every call on a device shares that
+ * device's array: calls that overlap in time on one device race, so callers
+ * serialise them (one stream per device, or their own ordering).           */
+#define AGK_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_rms,
+                            const void* dy, void* dx, float* dgamma, int64_t rows,
+                            int64_t cols, int dtype, int accumulate, agk_stream_t stream);
+
 /* Broadcast multiply y[i, j] = a[i, j] * b[j]: mul_nodeops with b of shape
  * [1, cols] or [cols] (cgadimpl/src/ops/arithmetic.cpp:31-39).  Used when the
  * layer is written unfused, as `ag::rms(x) * gamma`.                         */
