@@ -110,49 +110,142 @@ def _device_inputs(cfg, dev, seed):
 
 def _traffic(config_name):
     """HBM bytes per backward call (FETCH_SIZE + WRITE_SIZE, scaled by a copy of
-    known size) from the committed rocprofv3 summary, if there is one."""
+    known size) from the committed rocprofv3 summary of this configuration, and
+    where it came from.  A summary whose kernel-source hash differs from the
+    current sources describes other kernels: its figure is not used (None)."""
+    from cgadimpl_amd import profiling
     path = os.path.join(ROOT, "profiles", f"rmsnorm_{config_name}_hbm_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, "no rocprofv3 traffic summary for this configuration"
     with open(path) as fh:
         rec = json.load(fh)
-    return rec.get("bwd_hbm_bytes_per_launch")
+    rel = os.path.relpath(path, ROOT)
+    if rec.get("kernel_source_sha256") != profiling.kernel_source_hash(ROOT):
+        return None, f"{rel} was measured on other kernel sources (stale, not used)"
+    return rec.get("bwd_hbm_bytes_per_launch"), f"{rel} (kernel sources match)"
 
 
-def cpu_baseline(cfg, seconds):
-    import numpy as np
+def _bwd_kernels(agk, rows, cols, dtype):
+    """The kernels one agk_rmsnorm_bwd call of these sizes launches."""
+    p = agk.launch_plan(rows, cols, agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16, True)
+    if p["tpr"] == 0:
+        return "rms_bwd_looped + dgamma_finalize"
+    if p["nblk"] == 0:
+        return "bwd_fewrows: row and column workgroups, one launch"
+    return "rms_bwd_resident + dgamma_finalize"
 
+
+def host_info():
+    """The host's CPU: model string, logical CPU count (what C++'s
+    std::thread::hardware_concurrency() reports), the CPUs this process may run
+    on, and the last-level cache size, read from /proc and /sys."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    llc = None
+    base = "/sys/devices/system/cpu/cpu0/cache"
+    try:
+        for idx in sorted(os.listdir(base)):
+            try:
+                with open(os.path.join(base, idx, "level")) as fh:
+                    level = int(fh.read())
+                with open(os.path.join(base, idx, "size")) as fh:
+                    txt = fh.read().strip().upper()
+                size = int(txt.rstrip("KMG")) * {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(
+                    txt[-1], 1)
+                if llc is None or level >= llc[0]:
+                    llc = (level, size)
+            except (OSError, ValueError):
+                continue
+    except OSError:
+        pass
+    return {"cpu_model": model, "hardware_concurrency": os.cpu_count(),
+            "usable_cpus": len(os.sched_getaffinity(0)),
+            "llc_bytes": llc[1] if llc else None}
+
+
+CPU_SAMPLE_MIN_BYTES = 64 << 20  # per tensor, and at least the last-level cache
+CPU_RUNS = 5                     # timed runs per mode; the median is reported
+
+
+def _keep_freed_memory():
+    """Asks glibc malloc to serve large blocks from its heap and keep freed
+    memory (mallopt M_MMAP_MAX = 0, M_TRIM_THRESHOLD = max), so the
+    restatement's per-call intermediates are not re-faulted from the kernel on
+    every run: that would time page faults (half the run time on the build
+    host), not the CPU path."""
+    import ctypes
+    try:
+        libc = ctypes.CDLL("libc.so.6")
+        libc.mallopt(-4, 0)            # M_MMAP_MAX
+        libc.mallopt(-1, 0x7fffffff)   # M_TRIM_THRESHOLD
+    except OSError:
+        pass
+
+
+def cpu_baseline(cfg, seconds=None):
+    """The CPU oracle on a bounded sample of the configuration, timed on this host.
+
+    What is timed is the oracle's restatement of the reference's CPU op
+    sequence (normalization.cpp:24-27, arithmetic.cpp:32, autodiff_vjp_ops.cpp:
+    15-35,54-59,368-377, graph.cpp:46), every intermediate materialised as the
+    reference graph does: the reference itself cannot be built here (its
+    tensor library is an empty submodule), so this times a restatement, not
+    OwnTensor.  The sample is whole rows of the configuration's inputs (same
+    generator and distributions), at least the host's last-level cache and
+    CPU_SAMPLE_MIN_BYTES per tensor, so the restatement's working set (about
+    ten tensors) streams from DRAM.  Two modes: one thread, and every CPU this
+    process may use (OpenMP); each reports the median of CPU_RUNS timed runs
+    after one untimed run.  (`seconds` is unused: the sample, not a time
+    budget, fixes the work.)
+    """
     import oracle
     from cgadimpl_amd import configs
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    oracle.set_threads(threads)
-    sample_rows = max(1, min(cfg.rows, (4 << 20) // cfg.cols))  # ~4M elements
-    shape = (sample_rows, cfg.cols)
-    x, g, dy = configs.config_inputs(cfg, shape)
+    info = host_info()
+    R, D, s = cfg.rows, cfg.cols, cfg.storage_bytes
+    per_tensor = max(CPU_SAMPLE_MIN_BYTES, info["llc_bytes"] or 0)
+    rows = max(1, min(R, -(-per_tensor // (D * s))))
+    x, g, dy = configs.config_inputs(cfg, (rows, D))
+    _keep_freed_memory()
+    sample_bytes = 5 * rows * D * s + 2 * D * s + 2 * rows * 4 + D * 4
+
     def one():
         _, inv = oracle.fwd(x, g, cfg.eps)
         oracle.bwd(x, g, inv, dy)
-    one()  # warm-up (page-in, thread pool)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        one()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    s = cfg.storage_bytes
-    R, D = sample_rows, cfg.cols
-    sample_bytes = 5 * R * D * s + 2 * D * s + 2 * R * 4 + D * 4
-    gbs = sample_bytes * reps / el / 1e9
+
+    modes = {}
+    for mode, threads in (("single_thread", 1), ("all_cpus", info["usable_cpus"])):
+        oracle.set_threads(threads)
+        one()  # untimed: page-in, thread pool
+        times = []
+        for _ in range(CPU_RUNS):
+            t0 = time.perf_counter()
+            one()
+            times.append(time.perf_counter() - t0)
+        med = sorted(times)[len(times) // 2]
+        modes[mode] = {"threads": threads, "median_s": round(med, 4),
+                       "gbs": round(sample_bytes / med / 1e9, 3),
+                       "rows_per_s": round(rows / med, 1)}
+    best = modes["all_cpus"]
     return {
-        "value": round(gbs, 3),
+        "value": best["gbs"],
         "unit": "GB/s",
-        "cores": threads,
+        "cores": best["threads"],
         "kind": "port",
-        "sample": (f"{R} of {cfg.rows} rows x {D} {cfg.dtype}, fwd+bwd of the oracle's "
-                   f"op-by-op restatement of the reference path (every intermediate "
-                   f"materialised), {reps} reps in {el:.1f} s; rows/s "
-                   f"{R * reps / el:.4g}"),
+        "sample": (f"{rows} of {R} rows x {D} {cfg.dtype} "
+                   f"({rows * D * s / 2**20:.0f} MiB per tensor), fwd+VJP of the "
+                   f"oracle's op-by-op restatement of the reference CPU path (every "
+                   f"intermediate materialised; a restatement, not OwnTensor), median of "
+                   f"{CPU_RUNS} runs on {best['threads']} OpenMP threads; rows/s "
+                   f"{best['rows_per_s']:.4g}"),
+        "modes": modes,
+        "host": info,
     }
 
 
@@ -223,7 +316,7 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     value = alg / (ms_per_step * 1e-3) / 1e9
     bwd_gbs = cfg.bwd_bytes() / (bwd_ms * 1e-3) / 1e9
     fwd_gbs = cfg.fwd_bytes() / (fwd_ms * 1e-3) / 1e9
-    traffic = _traffic(cfg_name)
+    traffic, traffic_src = _traffic(cfg_name)
 
     out = {
         "metric": METRIC,
@@ -249,13 +342,14 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "rows_per_s": round(R / (ms_per_step * 1e-3), 1),
         },
         "roofline": {
-            "kernel": "agk_rmsnorm_bwd (rms_bwd_resident + dgamma_finalize)",
+            "kernel": "agk_rmsnorm_bwd (" + _bwd_kernels(agk, R, D, cfg.dtype) + ")",
             "bound": "hbm",
             "achieved": round(bwd_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": cfg.bwd_bytes(),
             "avg_launch_ms": round(bwd_ms, 5),
         },
@@ -274,11 +368,46 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     return out
 
 
+def cpu_baseline_c5(sample_rows=256):
+    """The CPU oracle of the RMSNorm + linear layer (oracle.rmsnorm_linear_layer:
+    the reference's rms_norm(x) * gamma -> matmul W forward and VJP restated,
+    bf16 storage, products in float64 through numpy's BLAS) on sample_rows of
+    the M = 8192 rows, with the full W [4096, 11008]; median of CPU_RUNS runs.
+    Reported as the three products' TFLOP/s, the GPU line's unit."""
+    import numpy as np
+
+    import oracle
+    _, K, N = C5_SHAPE
+    info = host_info()
+    rng = np.random.default_rng(0)
+    x = oracle.bf16_encode(rng.standard_normal((sample_rows, K), dtype=np.float32))
+    g = oracle.bf16_encode(rng.uniform(0.5, 1.5, K).astype(np.float32))
+    w = oracle.bf16_encode((rng.standard_normal((K, N), dtype=np.float32) * 0.02))
+    dy = oracle.bf16_encode(rng.standard_normal((sample_rows, N), dtype=np.float32))
+    oracle.set_threads(info["usable_cpus"])
+    _keep_freed_memory()
+    oracle.rmsnorm_linear_layer(x, g, w, dy, 1e-5)  # untimed
+    times = []
+    for _ in range(CPU_RUNS):
+        t0 = time.perf_counter()
+        oracle.rmsnorm_linear_layer(x, g, w, dy, 1e-5)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    flops = 3 * 2.0 * sample_rows * K * N
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s",
+            "cores": info["usable_cpus"], "kind": "port",
+            "sample": (f"{sample_rows} of {C5_SHAPE[0]} rows of x with the full W "
+                       f"[{K}, {N}]: the oracle's restatement of the layer's forward + VJP "
+                       f"(bf16 storage, float64 products through numpy's BLAS), median of "
+                       f"{CPU_RUNS} runs {med:.3f} s"),
+            "host": info}
+
+
 C5_SHAPE = (8192, 4096, 11008)   # x [M, K], W [K, N], dy [M, N]
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 
 
-def run_c5(steps, warmup):
+def run_c5(steps, warmup, cpu=True):
     """RMSNorm + linear layer (configuration c5): forward + full VJP on one GPU.
 
     fwd: agk_rmsnorm_fwd (h, inv_rms) -> GEMM y = h W
@@ -392,7 +521,7 @@ def run_c5(steps, warmup):
         "rmsnorm_gbs": round(norm_bytes / (norm_ms * 1e-3) / 1e9, 1),
         "torch_hipblaslt_ms": {k: round(v, 4) for k, v in torch_ms.items()},
         "torch_hipblaslt_tflops": round(3 * flops / (sum(torch_ms.values()) * 1e-3) / 1e12, 1),
-        "cpu_baseline": None,
+        "cpu_baseline": cpu_baseline_c5() if cpu else None,
     }
 
 
@@ -555,16 +684,18 @@ def copy_probe(mib, steps):
 STREAM_MIXES = (("copy (1 read + 1 write, as the forward)", 1, 1),
                 ("2 reads + 1 write (as the backward)", 2, 1),
                 ("read only", 1, 0))
-STREAM_GRIDS = (2048, 8192, 65536)
+STREAM_GRIDS = (0, 1024, 8192, 65536)  # 0: one workgroup per 16 KiB chunk
 
 
 def stream_probe(mib, steps):
     """The practical HBM ceiling of this device for the path's traffic mixes.
 
-    A grid-stride streaming kernel (agk_probe_stream: 16-byte slots, four in
-    flight per lane) over MIB-MiB buffers, with plain and with non-temporal
-    accesses, at several grid sizes; HIP events on the launch stream.  Prints
-    one JSON line per (mix, cache policy) with the best grid's GB/s.
+    A streaming kernel (agk_probe_stream: 16-byte slots, four in flight per
+    lane) over MIB-MiB buffers, with plain and with non-temporal accesses, one
+    workgroup per 16 KiB chunk (grid 0, how the row kernels touch memory) and
+    grid-stride at several grid sizes; HIP events on the launch stream.
+    Prints one JSON line per (mix, cache policy) with each grid's GB/s and the
+    best.
     """
     import torch
 
@@ -617,7 +748,8 @@ def main():
                     help="rmsnorm (default: the layer fwd + VJP), or a row op on the same "
                          "skeleton: " + ", ".join(ROWOPS) + ", or 'rowops' for all four")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="CPU baseline budget in seconds (0 disables it)")
+                    help="0 disables the CPU baseline; any other value runs it (its sample "
+                         "size, at least the host's last-level cache per tensor, fixes its work)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run MIB-MiB device copies (counter calibration), then exit")
     ap.add_argument("--stream-probe", type=int, default=0, metavar="MIB",
@@ -652,10 +784,9 @@ def main():
     names = list(configs.CONFIGS) + ["c5"] if args.config == "all" else [args.config]
     for name in names:
         if name == "c5":
-            rec = run_c5(args.steps, args.warmup)
+            rec = run_c5(args.steps, args.warmup, cpu=args.cpu_seconds > 0)
         else:
-            rec = run(name, args.steps, args.warmup,
-                      args.cpu_seconds if name == DEFAULT_CONFIG or args.config != "all" else 0)
+            rec = run(name, args.steps, args.warmup, args.cpu_seconds)
         print(json.dumps(rec), flush=True)
 
 

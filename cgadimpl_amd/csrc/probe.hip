@@ -5,9 +5,12 @@
 // the practical ceiling the row kernels are measured against, next to the
 // vendor peak.  No reference counterpart; a diagnostic of this library.
 //
-// Each lane moves 16-byte slots in a grid-stride loop.  Four independent
-// slots per lane are in flight per iteration, so a wave issues four loads
-// before it waits; the sizes are multiples of 64 slots per lane group.
+// Two access patterns.  Grid-stride: each lane moves 16-byte slots in a
+// grid-stride loop with four independent slots in flight per iteration.
+// Chunked: each workgroup moves one contiguous 16 KiB chunk of each buffer
+// (four slots per lane, all loads issued before any store), one workgroup per
+// chunk, which is how the row kernels touch memory (a row or a band of rows
+// per workgroup).
 
 #include <hip/hip_runtime.h>
 
@@ -78,12 +81,43 @@ __global__ __launch_bounds__(kProbeBlock) void probe_stream_kernel(const u32x4* 
     }
 }
 
+template <int READS, int WRITES, bool NT>
+__global__ __launch_bounds__(kProbeBlock) void probe_chunk_kernel(const u32x4* __restrict__ a,
+                                                                  const u32x4* __restrict__ b,
+                                                                  u32x4* __restrict__ c,
+                                                                  int64_t n) {
+    constexpr int64_t kChunk = static_cast<int64_t>(kProbeBlock) * kProbeUnroll;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
+    u32x4 v[kProbeUnroll];
+    u32x4 sink = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) {
+        const int64_t i = base + u * kProbeBlock;
+        v[u] = i < n ? probe_load<NT>(a + i) : u32x4{0u, 0u, 0u, 0u};
+        if constexpr (READS == 2) v[u] ^= i < n ? probe_load<NT>(b + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) {
+        const int64_t i = base + u * kProbeBlock;
+        if constexpr (WRITES == 1) {
+            if (i < n) probe_store<NT>(c + i, v[u]);
+        } else {
+            sink ^= v[u];
+        }
+    }
+    if constexpr (WRITES == 0) {
+        if (sink.x == 0xffffffffu && sink.y == 0xffffffffu && sink.z == 0xffffffffu &&
+            sink.w == 0xffffffffu)
+            c[0] = sink;
+    }
+}
+
 }  // namespace agk
 
 extern "C" int agk_probe_stream(const void* a, const void* b, void* c, int64_t bytes, int reads,
                                 int writes, int nontemporal, int grid, agk_stream_t stream) {
     using namespace agk;
-    if (bytes < 0 || (bytes & 15) != 0 || grid <= 0) return AGK_EINVAL;
+    if (bytes < 0 || (bytes & 15) != 0 || grid < 0) return AGK_EINVAL;
     if (reads != 1 && reads != 2) return AGK_EINVAL;
     if (writes != 0 && writes != 1) return AGK_EINVAL;
     if (!a || !c || (reads == 2 && !b)) return AGK_EINVAL;
@@ -94,9 +128,16 @@ extern "C" int agk_probe_stream(const void* a, const void* b, void* c, int64_t b
     const u32x4* pb = static_cast<const u32x4*>(b);
     u32x4* pc = static_cast<u32x4*>(c);
     const int64_t n = bytes / 16;
-    const dim3 g(static_cast<unsigned>(grid)), blk(kProbeBlock);
-#define AGK_PROBE(R, W, NT) \
-    hipLaunchKernelGGL((probe_stream_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, n)
+    const int64_t chunks = (n + kProbeBlock * kProbeUnroll - 1) / (kProbeBlock * kProbeUnroll);
+    if (grid == 0 && chunks > 0x7fffffffLL) return AGK_EINVAL;
+    const dim3 g(static_cast<unsigned>(grid == 0 ? chunks : grid)), blk(kProbeBlock);
+#define AGK_PROBE(R, W, NT)                                                                    \
+    do {                                                                                       \
+        if (grid == 0)                                                                         \
+            hipLaunchKernelGGL((probe_chunk_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, n);  \
+        else                                                                                   \
+            hipLaunchKernelGGL((probe_stream_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, n); \
+    } while (0)
     const int key = (reads - 1) * 4 + writes * 2 + (nontemporal ? 1 : 0);
     switch (key) {
         case 0: AGK_PROBE(1, 0, false); break;

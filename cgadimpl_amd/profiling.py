@@ -23,6 +23,7 @@ Usage:
   python -m cgadimpl_amd.profiling trace  <run_kernel_stats.csv> <out.md> "<command>"
   python -m cgadimpl_amd.profiling mfma <run_counter_collection.csv> <out.md> "<command>"
   python -m cgadimpl_amd.profiling bench <bench output (JSON lines)> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling probe <bench --stream-probe output> <out.md> "<command>"
   python -m cgadimpl_amd.profiling traffic <fetch_dir> <write_dir> <copy_fetch_dir>
         <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
 """
@@ -37,8 +38,32 @@ from collections import defaultdict
 # Kernels that make up one call of each C-ABI entry point.
 ENTRY_KERNELS = {
     "agk_rmsnorm_fwd": ("rms_fwd_resident", "rms_fwd_looped"),
-    "agk_rmsnorm_bwd": ("rms_bwd_resident", "rms_bwd_looped", "dgamma_finalize"),
+    "agk_rmsnorm_bwd": ("rms_bwd_resident", "rms_bwd_looped", "bwd_fewrows", "dgamma_finalize"),
 }
+
+# The files the RMSNorm kernels are compiled from.  A traffic summary records a
+# hash of them, and bench.py uses a summary only while the hash still matches.
+KERNEL_SOURCES = ("cgadimpl_amd/csrc/rmsnorm.hip", "cgadimpl_amd/csrc/rowcommon.hpp")
+
+
+def kernel_source_hash(root=None):
+    """sha256 over the RMSNorm kernel sources (KERNEL_SOURCES, in order)."""
+    import hashlib
+    root = root or os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(root, rel), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
+def _git_head(root):
+    import subprocess
+    try:
+        return subprocess.run(["git", "-C", root, "rev-parse", "--short=12", "HEAD"],
+                              capture_output=True, text=True, check=True).stdout.strip()
+    except (OSError, subprocess.CalledProcessError):
+        return None
 
 
 def _rows(path):
@@ -165,12 +190,17 @@ def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, 
     for k, (rd, wr) in sorted(per_kernel.items()):
         if any(k in ks for ks in ENTRY_KERNELS.values()):
             lines.append(f"| {k} | {rd / 1e6:.1f} | {wr / 1e6:.1f} |")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = kernel_source_hash(root)
+    rec = {"config": config, "fetch_scale": fs, "write_scale": ws,
+           "kernel_source_sha256": src, "git_head": _git_head(root)}
     lines += ["", "| entry point | HBM bytes | algorithmic bytes | ratio |", "|---|---|---|---|"]
-    rec = {"config": config, "fetch_scale": fs, "write_scale": ws}
     for entry, kernels in ENTRY_KERNELS.items():
         tot = sum(sum(per_kernel[k]) for k in kernels if k in per_kernel)
         lines.append(f"| {entry} | {tot:.4g} | {alg[entry]:.4g} | {tot / alg[entry]:.4f} |")
         rec[entry.replace("agk_rmsnorm_", "") + "_hbm_bytes_per_launch"] = round(tot)
+    lines += ["", f"Kernel sources ({', '.join(KERNEL_SOURCES)}) sha256 {src[:16]}; git HEAD "
+              f"{rec['git_head']} when summarised (uncommitted changes are in the hash)."]
     with open(out_stem + ".md", "w") as fh:
         fh.write("\n".join(lines) + "\n")
     with open(out_stem + ".json", "w") as fh:
@@ -224,16 +254,32 @@ def write_bench_summary(jsonl, out_md, command):
             and r["metric"].startswith("RMSNorm")]
     if norm:
         lines += ["## RMSNorm layer fwd + VJP", "",
-                  "| config | fwd+bwd GB/s | % of peak | fwd us | fwd % | bwd+finalize us | bwd % |",
-                  "|---|---|---|---|---|---|---|"]
+                  "| config | fwd+bwd GB/s | % of peak | step us | fwd us | fwd % | bwd us | bwd % "
+                  "| CPU GB/s (threads) | CPU 1-thread GB/s |",
+                  "|---|---|---|---|---|---|---|---|---|---|"]
         for r in norm:
             k = r["kernels"]
+            cpu = r.get("cpu_baseline") or {}
+            one = (cpu.get("modes") or {}).get("single_thread") or {}
             lines.append(f"| {r['config']['workload'].split(':')[0]} {r['config']['rows']}x"
                          f"{r['config']['cols']} {r['dtype']} | {r['value']:.0f} | "
-                         f"{100 * r['value'] / 8000:.1f} | {1e3 * k['fwd']['avg_ms']:.1f} | "
+                         f"{100 * r['value'] / 8000:.1f} | {1e3 * r['ms_per_step']:.1f} | "
+                         f"{1e3 * k['fwd']['avg_ms']:.1f} | "
                          f"{100 * k['fwd']['frac']:.1f} | {1e3 * k['bwd']['avg_ms']:.1f} | "
-                         f"{100 * k['bwd']['frac']:.1f} |")
+                         f"{100 * k['bwd']['frac']:.1f} | "
+                         f"{cpu.get('value', '-')} ({cpu.get('cores', '-')}) | "
+                         f"{one.get('gbs', '-')} |")
         lines.append("")
+        hosts = {json.dumps(r["cpu_baseline"]["host"], sort_keys=True) for r in norm
+                 if r.get("cpu_baseline") and r["cpu_baseline"].get("host")}
+        for h in hosts:
+            h = json.loads(h)
+            lines += [f"CPU baseline host: {h.get('cpu_model')}, hardware_concurrency "
+                      f"{h.get('hardware_concurrency')}, {h.get('usable_cpus')} usable CPUs, "
+                      f"last-level cache {h.get('llc_bytes')} bytes. The CPU figure times the "
+                      "oracle's op-by-op restatement of the reference path (a restatement, not "
+                      "OwnTensor) on a row sample of at least the last-level cache per tensor, "
+                      "median of 5 runs.", ""]
     rows = [r for r in recs if r.get("unit") == "GB/s" and not r["metric"].startswith("RMSNorm")]
     if rows:
         lines += ["## Row ops on the same skeleton", "",
@@ -251,11 +297,14 @@ def write_bench_summary(jsonl, out_md, command):
             continue
         st, tb = r["stages_ms"], r["torch_hipblaslt_ms"]
         fl = r["config"]["gemm_flops_per_step"] / 3
+        cpu = r.get("cpu_baseline") or {}
         lines += ["## RMSNorm + linear layer (c5)", "",
                   f"M, K, N = {r['config']['M']}, {r['config']['K']}, {r['config']['N']}; "
                   f"{r['value']} TFLOP/s over the three products "
                   f"({100 * r['roofline']['frac']:.1f} % of 2.5 PFLOP/s dense bf16); "
-                  f"hipBLASLt on the same operands {r['torch_hipblaslt_tflops']} TFLOP/s.", "",
+                  f"hipBLASLt on the same operands {r['torch_hipblaslt_tflops']} TFLOP/s; "
+                  f"CPU oracle {cpu.get('value', '-')} TFLOP/s on {cpu.get('cores', '-')} "
+                  f"threads.", "",
                   "| stage | this build us | TFLOP/s | hipBLASLt us | TFLOP/s |", "|---|---|---|---|---|"]
         for name, ms in st.items():
             if name in tb:
@@ -268,9 +317,33 @@ def write_bench_summary(jsonl, out_md, command):
         fh.write("\n".join(lines) + "\n")
 
 
+def write_probe_summary(jsonl, out_md, command):
+    """Table of bench.py --stream-probe lines: GB/s per traffic mix, cache policy
+    and grid (0 = one workgroup per 16 KiB chunk)."""
+    recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith("{")]
+    recs = [r for r in recs if "stream_probe" in r]
+    grids = sorted({g for r in recs for g in r["gbs_by_grid"]}, key=int)
+    lines = ["# HBM streaming probe (bench.py --stream-probe)", "", "Command:", "", "```",
+             command, "```", "",
+             f"{recs[0]['mib_per_buffer'] if recs else '?'} MiB per buffer, 16-byte slots; GB/s "
+             "counts every byte read and written; HIP events on the launch stream. Grid 0 is "
+             "one 256-lane workgroup per contiguous 16 KiB chunk (how the row kernels touch "
+             "memory); the others are grid-stride loops of that many workgroups.", "",
+             "| mix | non-temporal | " + " | ".join(f"grid {g}" for g in grids) +
+             " | best % of 8 TB/s |", "|---|---|" + "---|" * len(grids) + "---|"]
+    for r in recs:
+        lines.append(f"| {r['stream_probe']} | {'yes' if r['nontemporal'] else 'no'} | " +
+                     " | ".join(f"{r['gbs_by_grid'].get(g, '-')}" for g in grids) +
+                     f" | {r['pct_of_hbm_peak']} |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
 def main(argv):
     if len(argv) >= 4 and argv[0] == "trace":
         write_trace_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 4 and argv[0] == "probe":
+        write_probe_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "bench":
         write_bench_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "mfma":

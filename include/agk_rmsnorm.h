@@ -240,9 +240,11 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan);
 
 /* Diagnostic, with no counterpart in the reference: an HBM streaming probe,
- * the practical ceiling the row kernels are measured against.  A grid-stride
- * kernel of `grid` 256-lane workgroups moves `bytes` (a multiple of 16) per
- * buffer in 16-byte slots: reads == 1 reads a, reads == 2 reads a and b;
+ * the practical ceiling the row kernels are measured against.  grid > 0: a
+ * grid-stride kernel of `grid` 256-lane workgroups; grid == 0: one 256-lane
+ * workgroup per contiguous 16 KiB chunk of each buffer.  It moves `bytes`
+ * (a multiple of 16) per buffer in 16-byte slots: reads == 1 reads a,
+ * reads == 2 reads a and b;
  * writes == 1 writes c (a, or a ^ b), writes == 0 writes nothing (c must
  * still point at 16 writable bytes).  nontemporal != 0 sets the
  * non-temporal cache policy on every access, as the row kernels do.       */
