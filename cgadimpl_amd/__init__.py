@@ -348,12 +348,21 @@ def linear_bf16(x, w, bias=None, y=None, stream=None):
     torch = _torch()
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise TypeError("linear_bf16 takes bfloat16 operands")
+    if x.dim() != 2 or w.dim() != 2:
+        raise ValueError("linear_bf16 takes a 2-D x [M, K] and w [N, K]")
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError("x and w disagree on the input width")
+    if bias is not None:
+        if bias.dtype != torch.bfloat16:
+            raise TypeError("the bias must be bfloat16 (it is added as bf16 values)")
+        if bias.numel() != N or not bias.is_contiguous():
+            raise ValueError(f"the bias must be a contiguous tensor of N = {N} values")
     if y is None:
         y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    elif y.dtype != torch.bfloat16 or tuple(y.shape) != (M, N):
+        raise ValueError(f"y must be a bfloat16 [{M}, {N}] tensor")
     rc = lib().agk_linear_bf16(_ptr(x), x.shape[1], _ptr(w), w.shape[1], _ptr(bias), _ptr(y),
                                y.shape[1], M, N, K, _stream(stream))
     _check(rc, "agk_linear_bf16")
@@ -362,16 +371,16 @@ def linear_bf16(x, w, bias=None, y=None, stream=None):
 
 # ---- the RMSNorm + linear layer (configuration c5) --------------------------------
 
-def rmsnorm_linear_fwd(x, gamma, W, eps: float, wt=None, stream=None):
+def rmsnorm_linear_fwd(x, gamma, W, eps: float, stream=None):
     """h = rms_norm(x) * gamma, y = h @ W.  bf16 x [M, K], gamma [K], W [K, N].
 
-    W is transposed once (wt, [N, K]) so the product runs with both operands
-    k-contiguous.  Returns (y, h, inv_rms, wt).
+    W is read as it lies ([K, N], n contiguous): the GEMM stages it with its
+    transposing LDS reads, the same product path bench.py times for c5.
+    Returns (y, h, inv_rms).
     """
     h, inv = rmsnorm_fwd(x, gamma, eps, stream=stream)
-    wt = transpose_bf16(W, wt, stream=stream)
-    y = gemm_bf16(h, wt, trans_b=True, workspace=None, stream=stream)
-    return y, h, inv, wt
+    y = gemm_bf16(h, W, workspace=None, stream=stream)
+    return y, h, inv
 
 
 def rmsnorm_linear_bwd(x, gamma, inv_rms, h, W, dy, dw_dtype=None, stream=None):

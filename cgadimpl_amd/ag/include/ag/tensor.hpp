@@ -88,9 +88,12 @@ std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream);
 // Storage is destroyed, to a cache kept per stream (and device), and the next
 // allocation of a fitting size on the same stream takes it: the stream orders
 // the new user's work after the old user's, as the pool itself would, and no
-// hipFreeAsync is called (it blocks the calling thread on this runtime, which
-// kept the host from running ahead of the GPU).  Blocks never move between
-// streams.
+// hipFreeAsync is called on the hot path (it blocks the calling thread on this
+// runtime, which kept the host from running ahead of the GPU).  Blocks never
+// move between streams.  The cache holds at most cache_limit() bytes per
+// device: a block freed past the limit sends the device's oldest cached blocks
+// back to the pool (hipFreeAsync on their own streams).  When the pool cannot
+// serve a request, the cache is emptied and the request retried once.
 class Storage {
   public:
     Storage(size_t bytes, hipStream_t stream);
@@ -111,12 +114,20 @@ class Storage {
 };
 
 // Returns every cached pool block of the current device to HIP (after a
-// device synchronisation).  Call it before destroying a stream that graph-layer
-// tensors were allocated on while work on it may still be pending, or to give
-// the memory back.
+// device synchronisation), to give the memory back.
 void release_cached_memory();
+// Returns the cached blocks of `stream` (current device) to the pool, ordered
+// on that stream.  Call it before destroying a stream that graph-layer tensors
+// were allocated on: a later stream created with the same handle would
+// otherwise take blocks whose last users it is not ordered after.
+void release_stream_cache(hipStream_t stream);
 // Bytes held in the cache on the current device (diagnostic).
 size_t cached_bytes();
+// The most bytes the cache holds per device (default kDefaultCacheLimit).
+// Lowering it evicts the oldest blocks at once.
+constexpr size_t kDefaultCacheLimit = size_t(4) << 30;
+void set_cache_limit(size_t bytes);
+size_t cache_limit();
 
 class Tensor {
   public:

@@ -203,11 +203,9 @@ std::shared_ptr<Node> matmul_nodeops(const std::shared_ptr<Node>& a,
     std::vector<int64_t> ys = av.shape();
     ys.back() = N;
     Tensor y = Tensor::empty(ys, Dtype::BFloat16);
-    if (M && N) {
-        if (K == 0) fail("matmul: K must be positive");
+    if (M && N)  // K == 0: the GEMM's empty sum writes zeros
         gemm(av.data(), K, false, bv.data(), N, false, y.data(), N, Dtype::BFloat16, M, N, K,
              false, "matmul");
-    }
     auto n = std::make_shared<Node>(y, Op::MatMul, a->requires_grad() || b->requires_grad(),
                                     "matmul");
     link_inputs(n, {a, b});
@@ -470,20 +468,16 @@ void vjp_MatMul(Node* n, const Tensor& gy) {
     if (want_a) {
         bool acc = false;
         Tensor& da = A->grad_for_write(Dtype::BFloat16, &acc);
-        if (M && K) {
-            if (N == 0) fail("vjp_MatMul: N must be positive");
+        if (M && K)  // N == 0: an empty sum (zeros, or da unchanged when accumulating)
             gemm(gy.data(), N, false, bv.data(), N, true, da.data(), K, Dtype::BFloat16, M, K, N,
                  acc, "vjp_MatMul dA");
-        }
     }
     if (want_b) {
         bool acc = false;
         Tensor& db = B->grad_for_write(Dtype::Float32, &acc);
-        if (K && N) {
-            if (M == 0) fail("vjp_MatMul: the batch must not be empty");
+        if (K && N)  // M == 0: an empty sum over the batch
             gemm(av.data(), K, true, gy.data(), N, false, db.data(), N, Dtype::Float32, K, N, M,
                  acc, "vjp_MatMul dB");
-        }
     }
 }
 

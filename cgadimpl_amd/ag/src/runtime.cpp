@@ -25,7 +25,7 @@ GraphRunner::~GraphRunner() {
         // blocks cached under this stream must not pass to a later stream
         // that happens to reuse its handle
         try {
-            release_cached_memory();
+            release_stream_cache(stream_);
         } catch (...) {
         }
         (void)hipStreamDestroy(stream_);

@@ -3,10 +3,13 @@
 
 #include <atomic>
 #include <cstring>
+#include <iterator>
+#include <list>
 #include <map>
 #include <mutex>
 #include <numeric>
 #include <string>
+#include <vector>
 
 #include "check.hpp"
 
@@ -123,17 +126,47 @@ std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream) {
 namespace {
 
 // Freed pool blocks by (device, stream), then by size.  A request takes the
-// smallest cached block of at least its size and at most 5/4 of it.  The cache
-// is never destroyed: freeing blocks at exit would race the runtime's teardown.
+// smallest cached block of at least its size and at most 5/4 of it.  The bytes
+// held per device are capped (cache_limit): a block freed past the cap pushes
+// out the device's oldest cached blocks, which go back to the pool with a
+// stream-ordered hipFreeAsync on the stream they were used on.  The cache is
+// never destroyed: freeing blocks at exit would race the runtime's teardown.
+struct CachedBlock {
+    int dev;
+    hipStream_t stream;
+    size_t bytes;
+    void* ptr;
+};
+using BlockList = std::list<CachedBlock>;  // oldest first
 struct BlockCache {
     std::mutex mu;
-    std::map<std::pair<int, hipStream_t>, std::multimap<size_t, void*>> free;
+    BlockList order;
+    std::map<std::pair<int, hipStream_t>, std::multimap<size_t, BlockList::iterator>> free;
+    std::map<int, size_t> held;  // bytes cached per device
+    size_t limit = kDefaultCacheLimit;
 };
 BlockCache& block_cache() {
     static BlockCache* c = new BlockCache;
     return *c;
 }
 size_t block_size(size_t bytes) { return (bytes + 511) & ~size_t(511); }
+
+// Unlinks one cached block (the cache's mutex held).
+void unlink_block(BlockCache& c, BlockList::iterator it) {
+    auto key = std::make_pair(it->dev, it->stream);
+    auto list = c.free.find(key);
+    if (list != c.free.end()) {
+        auto range = list->second.equal_range(it->bytes);
+        for (auto m = range.first; m != range.second; ++m)
+            if (m->second == it) {
+                list->second.erase(m);
+                break;
+            }
+        if (list->second.empty()) c.free.erase(list);
+    }
+    c.held[it->dev] -= it->bytes;
+    c.order.erase(it);
+}
 
 void* take_cached(int dev, hipStream_t stream, size_t need, size_t* got) {
     BlockCache& c = block_cache();
@@ -142,10 +175,25 @@ void* take_cached(int dev, hipStream_t stream, size_t need, size_t* got) {
     if (list == c.free.end()) return nullptr;
     auto it = list->second.lower_bound(need);
     if (it == list->second.end() || it->first > need + need / 4) return nullptr;
-    void* p = it->second;
-    *got = it->first;
-    list->second.erase(it);
+    BlockList::iterator b = it->second;
+    void* p = b->ptr;
+    *got = b->bytes;
+    unlink_block(c, b);
     return p;
+}
+
+// Returns blocks to the pool: stream-ordered on the stream each was used on,
+// with that stream's device current (the null stream means that device's).
+void free_blocks(const std::vector<CachedBlock>& blocks) {
+    if (blocks.empty()) return;
+    int cur = 0;
+    hip_check(hipGetDevice(&cur), "hipGetDevice");
+    int dev = cur;
+    for (const CachedBlock& b : blocks) {
+        if (b.dev != dev) hip_check(hipSetDevice(dev = b.dev), "hipSetDevice");
+        hip_check(hipFreeAsync(b.ptr, b.stream), "hipFreeAsync");
+    }
+    if (dev != cur) hip_check(hipSetDevice(cur), "hipSetDevice");
 }
 
 }  // namespace
@@ -160,7 +208,15 @@ Storage::Storage(size_t bytes, hipStream_t stream) : bytes_(bytes), stream_(stre
     const size_t need = block_size(bytes);
     if ((ptr_ = take_cached(device_, stream, need, &block_))) return;
     retain_pool_memory();
-    hip_check(hipMallocAsync(&ptr_, need, stream), "hipMallocAsync");
+    hipError_t e = hipMallocAsync(&ptr_, need, stream);
+    if (e == hipErrorOutOfMemory) {
+        // The pool is out of memory, possibly to blocks this cache holds for
+        // other sizes or streams: hand them all back and try once more.
+        (void)hipGetLastError();
+        release_cached_memory();
+        e = hipMallocAsync(&ptr_, need, stream);
+    }
+    hip_check(e, "hipMallocAsync");
     block_ = need;
 }
 
@@ -170,9 +226,34 @@ Storage::~Storage() {
         a->defer_free(ptr_);  // a free on a capturing stream would be recorded
         return;
     }
-    BlockCache& c = block_cache();
-    std::lock_guard<std::mutex> lock(c.mu);
-    c.free[{device_, stream_}].emplace(block_, ptr_);
+    std::vector<CachedBlock> evicted;
+    {
+        BlockCache& c = block_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        if (block_ > c.limit && g_narenas.load() == 0) {  // too big to cache: back to the pool
+            evicted.push_back({device_, stream_, block_, ptr_});
+        } else {
+            c.order.push_back({device_, stream_, block_, ptr_});
+            c.free[{device_, stream_}].emplace(block_, std::prev(c.order.end()));
+            size_t& held = c.held[device_];
+            held += block_;
+            // No frees while a capture is recorded anywhere (a free call can
+            // invalidate it); the next free after the capture trims the cache.
+            const bool capturing = g_narenas.load() != 0;
+            for (auto it = c.order.begin(); !capturing && held > c.limit && it != c.order.end();) {
+                auto next = std::next(it);
+                if (it->dev == device_) {
+                    evicted.push_back(*it);
+                    unlink_block(c, it);
+                }
+                it = next;
+            }
+        }
+    }
+    try {
+        free_blocks(evicted);
+    } catch (...) {  // a destructor must not throw; the block is lost to the pool
+    }
 }
 
 void release_cached_memory() {
@@ -182,13 +263,13 @@ void release_cached_memory() {
     {
         BlockCache& c = block_cache();
         std::lock_guard<std::mutex> lock(c.mu);
-        for (auto it = c.free.begin(); it != c.free.end();) {
-            if (it->first.first != dev) {
-                ++it;
-                continue;
+        for (auto it = c.order.begin(); it != c.order.end();) {
+            auto next = std::next(it);
+            if (it->dev == dev) {
+                blocks.push_back(it->ptr);
+                unlink_block(c, it);
             }
-            for (auto& [size, p] : it->second) blocks.push_back(p);
-            it = c.free.erase(it);
+            it = next;
         }
     }
     if (blocks.empty()) return;
@@ -196,16 +277,58 @@ void release_cached_memory() {
     for (void* p : blocks) hip_check(hipFree(p), "hipFree");
 }
 
+void release_stream_cache(hipStream_t stream) {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::vector<CachedBlock> blocks;
+    {
+        BlockCache& c = block_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        for (auto it = c.order.begin(); it != c.order.end();) {
+            auto next = std::next(it);
+            // a created stream's handle names one device; the null stream is
+            // the current device's
+            if (it->stream == stream && (stream != nullptr || it->dev == dev)) {
+                blocks.push_back(*it);
+                unlink_block(c, it);
+            }
+            it = next;
+        }
+    }
+    free_blocks(blocks);
+}
+
 size_t cached_bytes() {
     int dev = 0;
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     BlockCache& c = block_cache();
     std::lock_guard<std::mutex> lock(c.mu);
-    size_t n = 0;
-    for (auto& [key, list] : c.free)
-        if (key.first == dev)
-            for (auto& [size, p] : list) n += size;
-    return n;
+    auto it = c.held.find(dev);
+    return it == c.held.end() ? 0 : it->second;
+}
+
+void set_cache_limit(size_t bytes) {
+    std::vector<CachedBlock> evicted;
+    {
+        BlockCache& c = block_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        c.limit = bytes;
+        for (auto it = c.order.begin(); it != c.order.end();) {
+            auto next = std::next(it);
+            if (c.held[it->dev] > c.limit) {
+                evicted.push_back(*it);
+                unlink_block(c, it);
+            }
+            it = next;
+        }
+    }
+    free_blocks(evicted);
+}
+
+size_t cache_limit() {
+    BlockCache& c = block_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    return c.limit;
 }
 
 Tensor Tensor::empty(const std::vector<int64_t>& shape, Dtype dt) {

@@ -21,6 +21,7 @@
 // each op, matmul against a host fp64 product, and hipGraph capture by
 // replaying a captured forward + backward on changed inputs, with eager work
 // in between, against eager runs (bitwise: the kernels are deterministic).
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -878,6 +879,48 @@ void test_linear_layer() {
     }
 }
 
+// matmul with an empty dimension: the forward gives an empty or zero result and
+// the backward leaves the gradients at the GEMM's empty-sum values (zero), as
+// the reference's matmul of empty tensors does.
+void test_matmul_empty() {
+    {  // empty batch: y [0, 16]; dB = A^T gy is an empty sum, so zero
+        Tensor ae = Tensor::empty({0, 32}, Dtype::BFloat16);
+        ae.set_requires_grad(true);
+        Value a = make_tensor(ae, "a0"), b = bf16_leaf(normal(32 * 16, 108), {32, 16}, "b0");
+        Value y = matmul(a, b);
+        Tensor seed = Tensor::empty({0, 16}, Dtype::BFloat16);
+        backward(y, &seed);
+        report("matmul on an empty batch: dB is zero",
+               y.val().numel() == 0 && max_abs(b.grad().to_host_f32()) == 0.0 &&
+                   b.grad().dtype() == Dtype::Float32 && a.grad().numel() == 0);
+    }
+    {  // K == 0: y = 0 [8, 16]; dA and dB are empty
+        Tensor ae = Tensor::empty({8, 0}, Dtype::BFloat16), be = Tensor::empty({0, 16}, Dtype::BFloat16);
+        ae.set_requires_grad(true);
+        be.set_requires_grad(true);
+        Value a = make_tensor(ae, "a1"), b = make_tensor(be, "b1");
+        Value y = matmul(a, b);
+        std::vector<uint16_t> sb = to_bf16_bits(rounded(normal(8 * 16, 109)));
+        Tensor seed = Tensor::from_host(sb.data(), {8, 16}, Dtype::BFloat16);
+        backward(y, &seed);
+        report("matmul with an empty reduction: y is zero, dA and dB are empty",
+               y.val().numel() == 128 && max_abs(y.val().to_host_f32()) == 0.0 &&
+                   a.grad().numel() == 0 && b.grad().numel() == 0);
+    }
+    {  // N == 0: y [8, 0]; dA = gy B^T is an empty sum, so zero
+        Value a = bf16_leaf(normal(8 * 32, 110), {8, 32}, "a2");
+        Tensor be = Tensor::empty({32, 0}, Dtype::BFloat16);
+        be.set_requires_grad(true);
+        Value b = make_tensor(be, "b2");
+        Value y = matmul(a, b);
+        Tensor seed = Tensor::empty({8, 0}, Dtype::BFloat16);
+        backward(y, &seed);
+        report("matmul with no output columns: dA is zero",
+               y.val().numel() == 0 && max_abs(a.grad().to_host_f32()) == 0.0 &&
+                   a.grad().numel() == 8 * 32);
+    }
+}
+
 // The captured graph holds the unfused composition rms(.) * g2 too, whose
 // backward runs as one pass (agk_rms_mul_bwd) inside the capture.
 void test_graph_capture(bool parallel) {
@@ -994,6 +1037,40 @@ void test_block_cache() {
     (void)hipStreamDestroy(s);
     report("block cache: blocks stay with their stream; release empties the cache",
            separate && released);
+
+    // many distinct sizes under a small cap: the cache never holds more than
+    // the cap, the oldest blocks go back to the pool first
+    const size_t cap = size_t(64) << 20;
+    set_cache_limit(cap);
+    bool under = cache_limit() == cap;
+    uint64_t state = 12345;
+    size_t peak = 0;
+    for (int i = 0; i < 300; ++i) {
+        state = state * 6364136223846793005ull + 1442695040888963407ull;
+        const int64_t floats = 1024 + static_cast<int64_t>((state >> 33) % (4u << 20));
+        { Tensor t = Tensor::empty({floats}); }
+        peak = std::max(peak, cached_bytes());
+        under = under && cached_bytes() <= cap;
+    }
+    report("block cache: 300 distinct sizes stay under a 64 MiB cap",
+           under && peak > cap / 2, "peak " + std::to_string(peak));
+
+    // a stream's blocks are dropped when the stream is retired
+    hipStream_t s2 = nullptr;
+    (void)hipStreamCreateWithFlags(&s2, hipStreamNonBlocking);
+    const size_t before = cached_bytes();
+    {
+        StreamGuard guard(s2);
+        Tensor ts = Tensor::empty({256, 1024});
+    }
+    const bool held = cached_bytes() >= before + (size_t(1) << 20);
+    release_stream_cache(s2);
+    const bool dropped = cached_bytes() == before;
+    (void)hipStreamSynchronize(s2);
+    (void)hipStreamDestroy(s2);
+    set_cache_limit(kDefaultCacheLimit);
+    release_cached_memory();
+    report("block cache: release_stream_cache drops that stream's blocks only", held && dropped);
 }
 
 int selftest() {
@@ -1015,6 +1092,7 @@ int selftest() {
         {"jvp", test_jvp},
         {"matmul_layer", test_matmul_layer},
         {"linear_layer", test_linear_layer},
+        {"matmul_empty", test_matmul_empty},
         {"graph_capture", [] { test_graph_capture(false); }},
         {"graph_capture_parallel", [] { test_graph_capture(true); }},
         {"graph_capture_rules", test_graph_capture_rules},

@@ -256,3 +256,22 @@ def test_python_binding_raises_without_gpu_tensors():
     x = torch.zeros(4, 8)
     with pytest.raises(ValueError):
         agk.rmsnorm_fwd(x, None, 1e-6, y=x, inv_rms=torch.zeros(4))
+
+
+def test_linear_bf16_rejects_bad_bias_and_output():
+    """Checked before any device call: an fp32 bias would be read as pairs of
+    bf16 values, a short bias or a mis-shaped y would be read or written out
+    of bounds by the kernel."""
+    import torch
+    x = torch.zeros(16, 32, dtype=torch.bfloat16)
+    w = torch.zeros(8, 32, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        agk.linear_bf16(x, w, torch.zeros(8, dtype=torch.float32))
+    with pytest.raises(ValueError):
+        agk.linear_bf16(x, w, torch.zeros(4, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        agk.linear_bf16(x, w, torch.zeros(16, dtype=torch.bfloat16)[::2])
+    with pytest.raises(ValueError):
+        agk.linear_bf16(x, w, None, y=torch.zeros(16, 4, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        agk.linear_bf16(x, w, None, y=torch.zeros(16, 8, dtype=torch.float32))

@@ -34,7 +34,7 @@ def test_layer_against_oracle(cuda, M, K, N):
     eps = 1e-5
     ref = oracle.rmsnorm_linear_layer(x, g, w, dy, eps)
     xd, gd, wd, dyd = (to_dev(a, cuda) for a in (x, g, w, dy))
-    y, h, inv, _ = agk.rmsnorm_linear_fwd(xd, gd, wd, eps)
+    y, h, inv = agk.rmsnorm_linear_fwd(xd, gd, wd, eps)
     dx, dgamma, dW = agk.rmsnorm_linear_bwd(xd, gd, inv, h, wd, dyd)
     torch.cuda.synchronize()
     errs = {
@@ -62,7 +62,7 @@ def test_layer_full_size(cuda):
     W = (torch.randn(K, N, generator=gen, device=cuda) * 0.02).bfloat16()
     dy = torch.randn(M, N, generator=gen, device=cuda).bfloat16()
     eps = 1e-5
-    y, h, inv, _ = agk.rmsnorm_linear_fwd(x, g, W, eps)
+    y, h, inv = agk.rmsnorm_linear_fwd(x, g, W, eps)
     dx, dgamma, dW = agk.rmsnorm_linear_bwd(x, g, inv, h, W, dy)
     torch.cuda.synchronize()
     rows = torch.randint(0, M, (48,), generator=gen, device=cuda)
@@ -79,6 +79,13 @@ def test_layer_full_size(cuda):
     e = dx_rel_err(as_f32(to_host(dx[rows].contiguous())), as_f32(rdx), as_f32(xs),
                    as_f32(to_host(g)), as_f32(dhs), eps)
     assert e <= TOL_BF16, e
+    # dgamma over all 8192 rows against an fp64 reduction of the same dh (the
+    # GEMM is deterministic, so a second dh = dy W^T is the one the backward
+    # used): dgamma[j] = sum_i dh[i, j] * x[i, j] * inv_rms[i]
+    dh_all = agk.gemm_bf16(dy, W, trans_b=True)
+    rdg = (dh_all.double() * x.double() * inv.double().view(M, 1)).sum(dim=0)
+    e = ((dgamma.double() - rdg).abs().max() / rdg.abs().max()).item()
+    assert e <= 1e-5, e
     # determinism of the whole backward
     dx2, dg2, dW2 = agk.rmsnorm_linear_bwd(x, g, inv, h, W, dy)
     torch.cuda.synchronize()
