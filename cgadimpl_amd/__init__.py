@@ -21,7 +21,9 @@ __all__ = [
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(_PKG, "lib")
+# AGK_LIB_DIR selects another build of the libraries (tests/run_sanitized.py
+# points it at the host-sanitised build); the default is the in-tree build.
+LIB_DIR = os.environ.get("AGK_LIB_DIR") or os.path.join(_PKG, "lib")
 
 AGK_F32 = 0
 AGK_BF16 = 1

@@ -94,19 +94,59 @@ HOST_HIP_LIBS = [f"-L{LIB}", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN"
                  f"-Wl,-rpath,{ROCM}/lib"]
 
 
-def ag_library() -> str:
+def ag_library(cxx: str = "g++", extra: list[str] | None = None) -> str:
     out = os.path.join(LIB, "libag.so")
     srcs = [os.path.join(AG_DIR, "src", s) for s in AG_SOURCES]
-    _atomic_build(out, lambda o: ["g++", *HOST_HIP_FLAGS, "-shared", *srcs, "-o", o,
-                                  "-lagk_rmsnorm", *HOST_HIP_LIBS])
+    _atomic_build(out, lambda o: [cxx, *HOST_HIP_FLAGS, *(extra or []), "-shared", *srcs, "-o",
+                                  o, f"-L{LIB}", "-lagk_rmsnorm", *HOST_HIP_LIBS])
     return out
 
 
-def ag_program(name: str, source: str) -> str:
+def ag_program(name: str, source: str, cxx: str = "g++", extra: list[str] | None = None) -> str:
     out = os.path.join(LIB, name)
-    _atomic_build(out, lambda o: ["g++", *HOST_HIP_FLAGS, source, "-o", o, "-lag",
-                                  "-lagk_rmsnorm", *HOST_HIP_LIBS, "-pthread"])
+    _atomic_build(out, lambda o: [cxx, *HOST_HIP_FLAGS, *(extra or []), source, "-o", o,
+                                  f"-L{LIB}", "-lag", "-lagk_rmsnorm", *HOST_HIP_LIBS,
+                                  "-pthread"])
     return out
+
+
+SAN_HOST_FLAGS = ["-fsanitize=address", "-fsanitize=undefined", "-fno-sanitize-recover=undefined",
+                  "-shared-libsan", "-fno-omit-frame-pointer"]
+
+
+def build_sanitized(out_dir: str, verbose: bool = True) -> list[str]:
+    """The kernel library and the input generator with AddressSanitizer and
+    UndefinedBehaviorSanitizer on their host code only (every -fsanitize= goes
+    behind -Xarch_host: the gfx950 code is built as usual), into out_dir.  The
+    process that loads them must preload the shared sanitizer runtime."""
+    global LIB
+    saved = LIB
+    os.makedirs(out_dir, exist_ok=True)
+    host = [f for flag in SAN_HOST_FLAGS for f in ("-Xarch_host", flag)]
+    try:
+        LIB = out_dir
+        outs = [hip_library("libagk_rmsnorm.so",
+                            ["rmsnorm.hip", "gemm.hip", "rowops.hip", "probe.hip"],
+                            extra=[*host, "-g"])]
+        clang = os.path.join(ROCM, "llvm", "bin", "clang++")
+        out = os.path.join(out_dir, "libagk_synth.so")
+        _atomic_build(out, lambda o: [clang, *SAN_HOST_FLAGS, "-g", "-O1", "-fPIC", "-shared",
+                                      "-std=c++17", os.path.join(CSRC, "synth.cpp"), "-o", o])
+        outs.append(out)
+        # the graph layer and its programs (host C++ over the HIP runtime API)
+        outs.append(ag_library(clang, [*SAN_HOST_FLAGS, "-g"]))
+        outs.append(ag_program("test_ag_layer", os.path.join(ROOT, "tests", "cpp",
+                                                             "test_ag_layer.cpp"),
+                               clang, [*SAN_HOST_FLAGS, "-g"]))
+        outs.append(ag_program("rmsnorm_layer", os.path.join(AG_DIR, "bench",
+                                                             "rmsnorm_layer.cpp"),
+                               clang, [*SAN_HOST_FLAGS, "-g"]))
+    finally:
+        LIB = saved
+    if verbose:
+        for o in outs:
+            print(f"built {os.path.relpath(o, ROOT)} (host code sanitised)")
+    return outs
 
 
 def build_all(verbose: bool = True) -> list[str]:

@@ -275,3 +275,21 @@ def test_linear_bf16_rejects_bad_bias_and_output():
         agk.linear_bf16(x, w, None, y=torch.zeros(16, 4, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         agk.linear_bf16(x, w, None, y=torch.zeros(16, 8, dtype=torch.float32))
+
+
+def test_sanitized_builds_are_the_ones_loaded():
+    """Under tests/run_sanitized.py (ORACLE_SANITIZE=1): the libraries the bindings
+    load are the sanitised builds, whose host code calls the AddressSanitizer
+    runtime.  Skipped in an ordinary run."""
+    if os.environ.get("ORACLE_SANITIZE") != "1":
+        pytest.skip("not a sanitised run")
+    import oracle
+    paths = [agk.lib_path(), os.path.join(agk.LIB_DIR, "libagk_synth.so"),
+             os.path.join(agk.LIB_DIR, "libag.so"), oracle.build.lib_path()]
+    assert agk.lib_path().startswith(os.environ["AGK_LIB_DIR"])
+    assert oracle.build.lib_path().startswith(os.environ["ORACLE_LIB_DIR"])
+    for p in paths:
+        syms = subprocess.run(["nm", "-D", p], capture_output=True, text=True, check=True).stdout
+        assert "__asan_" in syms and "__ubsan_" in syms, p
+    agk.lib()
+    oracle.load()
