@@ -531,7 +531,10 @@ def run_c5(steps, warmup, cpu=True):
 #   softmax      fwd 2RDs                         bwd 3RDs
 #   logsumexp    fwd RDs + Rs                     bwd 2RDs + Rs      jvp 2RDs + Rs
 #   rmsnorm_jvp  jvp 3RDs + 2Ds + 4R
-ROWOPS = ("layernorm", "softmax", "logsumexp", "rmsnorm_jvp")
+#   rms_mul      the reference's unfused layer ag::rms(x) * gamma: rms fwd 2RDs + 4R,
+#                mul fwd 2RDs + Ds, one-pass bwd (agk_rms_mul_bwd: read x, gy; write
+#                dr = gy*gamma and dx; gamma, inv_rms, dgamma) 4RDs + Ds + 4R + 4D
+ROWOPS = ("layernorm", "softmax", "logsumexp", "rmsnorm_jvp", "rms_mul")
 
 
 def _rowop_bytes(op, R, D, s):
@@ -541,7 +544,17 @@ def _rowop_bytes(op, R, D, s):
         "softmax": {"fwd": 2 * rd, "bwd": 3 * rd},
         "logsumexp": {"fwd": rd + R * s, "bwd": 2 * rd + R * s, "jvp": 2 * rd + R * s},
         "rmsnorm_jvp": {"jvp": 3 * rd + 2 * D * s + 4 * R},
+        "rms_mul": {"rms": 2 * rd + 4 * R, "mul": 2 * rd + D * s,
+                    "bwd": 4 * rd + D * s + 4 * R + 4 * D},
     }[op]
+
+
+def _oracle_rms_mul(x, g, dy, eps):
+    """The oracle's restatement of rms(x) * gamma forward and both VJPs (the
+    C oracle with gamma applied, as the reference composes them)."""
+    import oracle
+    _, inv = oracle.fwd(x, g, eps)
+    oracle.bwd(x, g, inv, dy)
 
 
 def _rowop_cpu_baseline(op, cfg, seconds):
@@ -562,6 +575,7 @@ def _rowop_cpu_baseline(op, cfg, seconds):
         "logsumexp": lambda: (ro.logsumexp_fwd(x), ro.logsumexp_bwd(x, dy[:, :1]),
                               ro.logsumexp_jvp(x, dy)),
         "rmsnorm_jvp": lambda: ro.rmsnorm_jvp(x, g, dy, g[::-1] - 1.0, cfg.eps),
+        "rms_mul": lambda: _oracle_rms_mul(x, g, dy, cfg.eps),
     }
     f = fns[op]
     f()
@@ -603,6 +617,9 @@ def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
     dl = dy[:, :1].contiguous()
     tg = (torch.flip(g, [0]) - 1.0).contiguous()
     _, inv = agk.rmsnorm_fwd(x, g, cfg.eps)
+    inv1 = torch.empty(R, dtype=f32, device=dev)
+    dxo = torch.empty_like(x)
+    dgo = torch.empty(D, dtype=f32, device=dev)
     stream = torch.cuda.current_stream()
     launches = {
         "layernorm": [("fwd", lambda: agk.layernorm_fwd(x, cfg.eps, y=y, mean=mean, rstd=rstd,
@@ -616,6 +633,11 @@ def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
                       ("jvp", lambda: agk.logsumexp_jvp(x, dy, ty=tl, stream=stream))],
         "rmsnorm_jvp": [("jvp", lambda: agk.rmsnorm_jvp(x, g, inv, dy, tg, ty=out,
                                                         stream=stream))],
+        "rms_mul": [("rms", lambda: agk.rmsnorm_fwd(x, None, cfg.eps, y=y, inv_rms=inv1,
+                                                    stream=stream)),
+                    ("mul", lambda: agk.mul_rowbcast_fwd(y, g, y=out, stream=stream)),
+                    ("bwd", lambda: agk.rms_mul_bwd(x, g, inv1, dy, dx=dxo, dgamma=dgo,
+                                                    stream=stream))],
     }[op]
     for _ in range(warmup):
         for _, f in launches:
@@ -653,7 +675,8 @@ def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
                                    else ""),
         "config": {"workload": f"{cfg.name}: {op} x{list(cfg.shape)} {cfg.dtype}", "rows": R,
                    "cols": D, "algorithmic_bytes_per_step": total},
-        "roofline": {"kernel": f"agk_{op if op != 'rmsnorm_jvp' else 'rmsnorm'}_{dom}",
+        "roofline": {"kernel": {"rmsnorm_jvp": "agk_rmsnorm_jvp",
+                                "rms_mul": "agk_rms_mul_bwd"}.get(op, f"agk_{op}_{dom}"),
                      "bound": "hbm", "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": kernels[dom]["frac"], "traffic": None,
                      "algorithmic_bytes_per_launch": alg[dom],
@@ -683,6 +706,7 @@ def copy_probe(mib, steps):
 
 STREAM_MIXES = (("copy (1 read + 1 write, as the forward)", 1, 1),
                 ("2 reads + 1 write (as the backward)", 2, 1),
+                ("2 reads + 2 writes (as the rms(x) * gamma backward)", 2, 2),
                 ("read only", 1, 0))
 STREAM_GRIDS = (0, 1024, 8192, 65536)  # 0: one workgroup per 16 KiB chunk
 
@@ -706,6 +730,7 @@ def stream_probe(mib, steps):
     a = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev)
     b = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev)
     c = torch.empty_like(a)
+    d = torch.empty_like(a)
     stream = torch.cuda.current_stream()
     results = []
     for name, reads, writes in STREAM_MIXES:
@@ -713,7 +738,7 @@ def stream_probe(mib, steps):
             per_grid = {}
             for grid in STREAM_GRIDS:
                 def launch():
-                    agk.probe_stream(a, b, c, nbytes, reads, writes, nt, grid, stream=stream)
+                    agk.probe_stream(a, b, c, d, nbytes, reads, writes, nt, grid, stream=stream)
                 for _ in range(3):
                     launch()
                 e0, e1 = TimingEvent(), TimingEvent()

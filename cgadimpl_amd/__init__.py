@@ -70,8 +70,8 @@ SIGNATURES = {
     "agk_logsumexp_fwd": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_logsumexp_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_logsumexp_jvp": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
-    "agk_probe_stream": (ctypes.c_int, [_P, _P, _P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                        ctypes.c_int, _P]),
+    "agk_probe_stream": (ctypes.c_int, [_P, _P, _P, _P, _I64, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
     "agk_version": (ctypes.c_char_p, []),
@@ -499,10 +499,10 @@ def logsumexp_jvp(z, tz, ty=None, stream=None):
     return ty
 
 
-def probe_stream(a, b, c, nbytes: int, reads: int, writes: int, nontemporal: bool, grid: int,
+def probe_stream(a, b, c, d, nbytes: int, reads: int, writes: int, nontemporal: bool, grid: int,
                  stream=None) -> None:
     """HBM streaming probe (diagnostic): reads `reads` buffers, writes `writes`."""
-    rc = lib().agk_probe_stream(_ptr(a), _ptr(b) if b is not None else None, _ptr(c), int(nbytes),
-                                int(reads), int(writes), int(bool(nontemporal)), int(grid),
-                                _stream(stream))
+    rc = lib().agk_probe_stream(_ptr(a), _ptr(b) if b is not None else None, _ptr(c),
+                                _ptr(d) if d is not None else None, int(nbytes), int(reads),
+                                int(writes), int(bool(nontemporal)), int(grid), _stream(stream))
     _check(rc, "agk_probe_stream")

@@ -37,12 +37,13 @@ __device__ __forceinline__ void probe_store(u32x4* p, u32x4 v) {
         *p = v;
 }
 
-// READS in {1, 2}, WRITES in {0, 1}.  n = slots per buffer, a multiple of
+// READS in {1, 2}, WRITES in {0, 1, 2} (c = the value, d = the value + 1).  n = slots per buffer, a multiple of
 // kProbeUnroll * kProbeBlock * gridDim.x is not required: the tail is guarded.
 template <int READS, int WRITES, bool NT>
 __global__ __launch_bounds__(kProbeBlock) void probe_stream_kernel(const u32x4* __restrict__ a,
                                                                    const u32x4* __restrict__ b,
                                                                    u32x4* __restrict__ c,
+                                                                   u32x4* __restrict__ d,
                                                                    int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kProbeBlock;
     int64_t i = static_cast<int64_t>(blockIdx.x) * kProbeBlock + threadIdx.x;
@@ -57,19 +58,21 @@ __global__ __launch_bounds__(kProbeBlock) void probe_stream_kernel(const u32x4* 
         }
 #pragma unroll
         for (int u = 0; u < kProbeUnroll; ++u) {
-            if constexpr (WRITES == 1)
+            if constexpr (WRITES >= 1)
                 probe_store<NT>(c + i + u * stride, v[u]);
             else
                 sink ^= v[u];
+            if constexpr (WRITES == 2) probe_store<NT>(d + i + u * stride, v[u] + 1u);
         }
     }
     for (; i < n; i += stride) {
         u32x4 v = probe_load<NT>(a + i);
         if constexpr (READS == 2) v ^= probe_load<NT>(b + i);
-        if constexpr (WRITES == 1)
+        if constexpr (WRITES >= 1)
             probe_store<NT>(c + i, v);
         else
             sink ^= v;
+        if constexpr (WRITES == 2) probe_store<NT>(d + i, v + 1u);
     }
     if constexpr (WRITES == 0) {
         // Keeps the loads: a store that the data decides on (all-ones XOR of
@@ -85,6 +88,7 @@ template <int READS, int WRITES, bool NT>
 __global__ __launch_bounds__(kProbeBlock) void probe_chunk_kernel(const u32x4* __restrict__ a,
                                                                   const u32x4* __restrict__ b,
                                                                   u32x4* __restrict__ c,
+                                                                  u32x4* __restrict__ d,
                                                                   int64_t n) {
     constexpr int64_t kChunk = static_cast<int64_t>(kProbeBlock) * kProbeUnroll;
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
@@ -99,10 +103,13 @@ __global__ __launch_bounds__(kProbeBlock) void probe_chunk_kernel(const u32x4* _
 #pragma unroll
     for (int u = 0; u < kProbeUnroll; ++u) {
         const int64_t i = base + u * kProbeBlock;
-        if constexpr (WRITES == 1) {
+        if constexpr (WRITES >= 1) {
             if (i < n) probe_store<NT>(c + i, v[u]);
         } else {
             sink ^= v[u];
+        }
+        if constexpr (WRITES == 2) {
+            if (i < n) probe_store<NT>(d + i, v[u] + 1u);
         }
     }
     if constexpr (WRITES == 0) {
@@ -114,41 +121,50 @@ __global__ __launch_bounds__(kProbeBlock) void probe_chunk_kernel(const u32x4* _
 
 }  // namespace agk
 
-extern "C" int agk_probe_stream(const void* a, const void* b, void* c, int64_t bytes, int reads,
-                                int writes, int nontemporal, int grid, agk_stream_t stream) {
+extern "C" int agk_probe_stream(const void* a, const void* b, void* c, void* d, int64_t bytes,
+                                int reads, int writes, int nontemporal, int grid,
+                                agk_stream_t stream) {
     using namespace agk;
     if (bytes < 0 || (bytes & 15) != 0 || grid < 0) return AGK_EINVAL;
     if (reads != 1 && reads != 2) return AGK_EINVAL;
-    if (writes != 0 && writes != 1) return AGK_EINVAL;
-    if (!a || !c || (reads == 2 && !b)) return AGK_EINVAL;
+    if (writes < 0 || writes > 2) return AGK_EINVAL;
+    if (!a || !c || (reads == 2 && !b) || (writes == 2 && !d)) return AGK_EINVAL;
     if (bytes == 0) return AGK_OK;
     clear_pending_error();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const u32x4* pa = static_cast<const u32x4*>(a);
     const u32x4* pb = static_cast<const u32x4*>(b);
     u32x4* pc = static_cast<u32x4*>(c);
+    u32x4* pd = static_cast<u32x4*>(d);
     const int64_t n = bytes / 16;
     const int64_t chunks = (n + kProbeBlock * kProbeUnroll - 1) / (kProbeBlock * kProbeUnroll);
     if (grid == 0 && chunks > 0x7fffffffLL) return AGK_EINVAL;
     const dim3 g(static_cast<unsigned>(grid == 0 ? chunks : grid)), blk(kProbeBlock);
-#define AGK_PROBE(R, W, NT)                                                                    \
-    do {                                                                                       \
-        if (grid == 0)                                                                         \
-            hipLaunchKernelGGL((probe_chunk_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, n);  \
-        else                                                                                   \
-            hipLaunchKernelGGL((probe_stream_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, n); \
+#define AGK_PROBE(R, W, NT)                                                                   \
+    do {                                                                                      \
+        if (grid == 0)                                                                        \
+            hipLaunchKernelGGL((probe_chunk_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, pd,  \
+                               n);                                                            \
+        else                                                                                  \
+            hipLaunchKernelGGL((probe_stream_kernel<R, W, NT>), g, blk, 0, st, pa, pb, pc, pd, \
+                               n);                                                            \
     } while (0)
-    const int key = (reads - 1) * 4 + writes * 2 + (nontemporal ? 1 : 0);
-    switch (key) {
-        case 0: AGK_PROBE(1, 0, false); break;
-        case 1: AGK_PROBE(1, 0, true); break;
-        case 2: AGK_PROBE(1, 1, false); break;
-        case 3: AGK_PROBE(1, 1, true); break;
-        case 4: AGK_PROBE(2, 0, false); break;
-        case 5: AGK_PROBE(2, 0, true); break;
-        case 6: AGK_PROBE(2, 1, false); break;
-        default: AGK_PROBE(2, 1, true); break;
+#define AGK_PROBE_NT(R, W)          \
+    do {                            \
+        if (nontemporal)            \
+            AGK_PROBE(R, W, true);  \
+        else                        \
+            AGK_PROBE(R, W, false); \
+    } while (0)
+    switch ((reads - 1) * 3 + writes) {
+        case 0: AGK_PROBE_NT(1, 0); break;
+        case 1: AGK_PROBE_NT(1, 1); break;
+        case 2: AGK_PROBE_NT(1, 2); break;
+        case 3: AGK_PROBE_NT(2, 0); break;
+        case 4: AGK_PROBE_NT(2, 1); break;
+        default: AGK_PROBE_NT(2, 2); break;
     }
+#undef AGK_PROBE_NT
 #undef AGK_PROBE
     return check_launch();
 }

@@ -244,11 +244,11 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
  * grid-stride kernel of `grid` 256-lane workgroups; grid == 0: one 256-lane
  * workgroup per contiguous 16 KiB chunk of each buffer.  It moves `bytes`
  * (a multiple of 16) per buffer in 16-byte slots: reads == 1 reads a,
- * reads == 2 reads a and b;
- * writes == 1 writes c (a, or a ^ b), writes == 0 writes nothing (c must
- * still point at 16 writable bytes).  nontemporal != 0 sets the
- * non-temporal cache policy on every access, as the row kernels do.       */
-int agk_probe_stream(const void* a, const void* b, void* c, int64_t bytes, int reads,
+ * reads == 2 reads a and b; writes == 1 writes c (a, or a ^ b), writes == 2
+ * writes c and d, writes == 0 writes nothing (c must still point at 16
+ * writable bytes).  nontemporal != 0 sets the non-temporal cache policy on
+ * every access, as the row kernels do.                                     */
+int agk_probe_stream(const void* a, const void* b, void* c, void* d, int64_t bytes, int reads,
                      int writes, int nontemporal, int grid, agk_stream_t stream);
 
 /* Human-readable name of a status code (static storage). */
