@@ -193,23 +193,25 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t* lds, int row, int k) 
 // ---- tile order ----------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup L runs on
 // XCD L % 8), each XCD with its own L2.  The tile order below gives each XCD
-// a contiguous chunk of a grouped ordering (kGroupM m-tiles x all n-tiles,
+// a contiguous chunk of a grouped ordering (group_m m-tiles x all n-tiles,
 // column by column), so the ~32 workgroups resident on one XCD at a time
-// cover about kGroupM x 8 tiles and share their A row-panels and B column-
-// panels in that XCD's L2, instead of every neighbouring tile landing on a
-// different XCD.
+// cover about group_m x 32 / group_m tiles and share their A row-panels and B
+// column-panels in that XCD's L2, instead of every neighbouring tile landing
+// on a different XCD.  group_m = 4 unless a measured order is known for the
+// shape (tuned_group_m).
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
-__device__ __forceinline__ void tile_of(int L, int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_of(int L, int tiles_m, int tiles_n, int group_m, int& tm,
+                                        int& tn) {
     const int T = tiles_m * tiles_n;
     const int x = L % kXcds, s = L / kXcds;
     const int q = T / kXcds, r = T % kXcds;  // XCDs below r get q + 1 tiles
     const int g = x < r ? x * (q + 1) + s : r * (q + 1) + (x - r) * q + s;
-    const int per_group = kGroupM * tiles_n;
+    const int per_group = group_m * tiles_n;
     const int group = g / per_group;
-    const int gm0 = group * kGroupM;
-    const int gsize = tiles_m - gm0 < kGroupM ? tiles_m - gm0 : kGroupM;
+    const int gm0 = group * group_m;
+    const int gsize = tiles_m - gm0 < group_m ? tiles_m - gm0 : group_m;
     const int in = g - group * per_group;
     tm = gm0 + in % gsize;
     tn = in / gsize;
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bf16_kernel(
     const int wm = wave / kWavesN;
     const int wn = wave % kWavesN;
     int tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    tile_of(blockIdx.x, tiles_m, tiles_n, kGroupM, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
@@ -595,7 +597,7 @@ template <bool OUT_F32, bool A_TR, bool B_TR>
 __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
-    const uint16_t* __restrict__ colbias, int accumulate, int tiles_m, int tiles_n) {
+    const uint16_t* __restrict__ colbias, int accumulate, int tiles_m, int tiles_n, int group_m) {
     __shared__ __attribute__((aligned(16))) uint16_t st0[kStageElems];
     __shared__ __attribute__((aligned(16))) uint16_t st1[kStageElems];
 
@@ -606,7 +608,7 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const int wm = wave >> 1;
     const int wn = wave & 1;
     int tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
@@ -787,7 +789,46 @@ int dispatch_ks(bool has_ks, int c_dtype, const void* A, int64_t lda, const void
 
 namespace agk_gemm {
 
-// Whether a call takes the direct-to-LDS kernel once its operands are k-contiguous.
+// Tile orders measured on MI355X for the products of the RMSNorm + linear
+// layer at its headline size (M = 8192 rows, K = 4096, N = 11008), with
+// random bf16 operands; every other shape takes kGroupM.  The best group size
+// depends on the shape in ways no simple rule captured (the same y layout
+// with K = 8192 is fastest at 4, with 16384 rows at 2), so only shapes that
+// were measured are listed.  Microseconds per product, group size 2 / 4 / 8:
+//   y  = h W     (32 x 43 tiles, 64 k-steps, A k-contiguous, B k-strided):
+//                 531-537 / 551-561 / 549-558
+//   dh = dy W^T  (32 x 16 tiles, 172 k-steps, both k-contiguous):
+//                 565-570 / 506-516 / 493-499
+// (dW = h^T dy, 16 x 43 tiles, measured 524-550 at every group size: 4.)
+// The order changes only which workgroup computes which tile: results are
+// bit-identical.
+struct TunedOrder {
+    int tiles_m, tiles_n, nk;
+    bool a_tr, b_tr;
+    int group_m;
+};
+constexpr TunedOrder kTunedOrders[] = {
+    {32, 43, 64, false, true, 2},     // y
+    {32, 16, 172, false, false, 8},   // dh
+};
+
+inline int tuned_group_m(int tiles_m, int tiles_n, int nk, bool a_tr, bool b_tr) {
+    for (const TunedOrder& t : kTunedOrders)
+        if (t.tiles_m == tiles_m && t.tiles_n == tiles_n && t.nk == nk && t.a_tr == a_tr &&
+            t.b_tr == b_tr)
+            return t.group_m;
+    return kGroupM;
+}
+
+// Whether a call takes the direct-to-LDS kernel.  A k-scale keeps the call on
+// the register-staged kernel: the direct kernel's loads go from memory to LDS
+// without passing registers, so the scale would have to be applied to every A
+// fragment after its LDS read (unpack, multiply, round, repack: about 20 VALU
+// operations per fragment).  Measured on MI355X for y (8192 x 11008 x 4096,
+// A k-contiguous, the scale staged in LDS), that variant was bit-identical to
+// the staged kernel's but ran 759-819 us against 551 us without the scale,
+// while all it saves the RMSNorm + linear layer is writing and reading h
+// (about 15 us).
 inline bool direct_eligible(int64_t K, const float* kscale) {
     return kscale == nullptr && K % BK == 0;
 }
@@ -858,12 +899,13 @@ int gemm_impl(const void* A, int64_t lda, int a_trans, const void* B, int64_t ld
     const bool a_tr = a_trans != 0, b_tr = b_trans == 0;
     if (direct_eligible(K, kscale) && fits(lda, a_tr) && fits(ldb, b_tr)) {
         const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+        const int gm = tuned_group_m(tiles_m, tiles_n, k / BK, a_tr, b_tr);
         const dim3 grid(tiles_m * tiles_n), block(kDirectThreads);
         const uint16_t* a16 = static_cast<const uint16_t*>(A);
         const uint16_t* b16 = static_cast<const uint16_t*>(B);
 #define AGK_DIRECT(F32, ATR, BTR)                                                              \
     hipLaunchKernelGGL((gemm_nt_direct_kernel<F32, ATR, BTR>), grid, block, 0, st, a16, lda, b16, \
-                       ldb, C, ldc, m, n, k, rowscale, colbias, acc, tiles_m, tiles_n)
+                       ldb, C, ldc, m, n, k, rowscale, colbias, acc, tiles_m, tiles_n, gm)
         const bool f32 = c_dtype == AGK_F32;
         if (f32) {
             if (a_tr && b_tr) AGK_DIRECT(true, true, true);
