@@ -49,6 +49,13 @@ SIGNATURES = {
                                             ctypes.c_int, ctypes.c_int, _P]),
     "agk_rms_mul_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64,
                                        _I64, ctypes.c_int, ctypes.c_int, _P]),
+    "agk_mul_bcast_shape": (ctypes.c_int, [_P, ctypes.c_int, _P, ctypes.c_int, _P, _P]),
+    "agk_mul_bcast_fwd": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P, ctypes.c_int, _P,
+                                         ctypes.c_int, ctypes.c_int, _P]),
+    "agk_mul_bcast_bwd": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, _P, _P,
+                                         ctypes.c_int, ctypes.c_int, _P]),
+    "agk_gemm_f32": (ctypes.c_int, [_P, _I64, ctypes.c_int, _P, _I64, ctypes.c_int, _P, _I64,
+                                    _I64, _I64, _I64, ctypes.c_int, _P]),
     "agk_sum_rows_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_sum_rows": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _I64, _I64, ctypes.c_int,
                                     ctypes.c_int, _P]),
@@ -262,6 +269,24 @@ def gemm_bf16(a, b, c=None, trans_a: bool = False, trans_b: bool = False, out_dt
     return c
 
 
+def gemm_f32(a, b, c=None, trans_a: bool = False, trans_b: bool = False, accumulate=False,
+             stream=None):
+    """C (+)= op(A) op(B) in fp32 (agk_gemm_f32, rocBLAS sgemm, deterministic).
+
+    a: [M, K] (or [K, M] with trans_a), b: [K, N] (or [N, K] with trans_b),
+    row-major contiguous float32; c [M, N] float32."""
+    torch = _torch()
+    M = a.shape[1] if trans_a else a.shape[0]
+    K = a.shape[0] if trans_a else a.shape[1]
+    N = b.shape[0] if trans_b else b.shape[1]
+    if c is None:
+        c = torch.empty(M, N, dtype=torch.float32, device=a.device)
+    rc = lib().agk_gemm_f32(_ptr(a), a.shape[1], int(trans_a), _ptr(b), b.shape[1], int(trans_b),
+                            _ptr(c), c.shape[1], M, N, K, int(bool(accumulate)), _stream(stream))
+    _check(rc, "agk_gemm_f32")
+    return c
+
+
 def launch_plan(rows: int, cols: int, dtype: int, backward: bool) -> dict:
     """The launch shape agk_rmsnorm_{fwd,bwd} picks for these sizes (diagnostic)."""
     out = (ctypes.c_int32 * 5)()
@@ -328,6 +353,66 @@ def rms_mul_bwd(x, gamma, inv_rms, gy, dx=None, dgamma=None, accumulate=False,
                                _stream(stream))
     _check(rc, "agk_rms_mul_bwd")
     return dr, dx, dgamma
+
+
+def _shape_arg(shape):
+    n = len(shape)
+    return (ctypes.c_int64 * max(1, n))(*shape), n
+
+
+def mul_bcast_shape(a_shape, b_shape) -> tuple:
+    """The broadcast output shape of a * b (numpy rules; agk_mul_bcast_shape)."""
+    ab, an = _shape_arg(tuple(a_shape))
+    bb, bn = _shape_arg(tuple(b_shape))
+    out = (ctypes.c_int64 * 8)()
+    nd = ctypes.c_int(0)
+    _check(lib().agk_mul_bcast_shape(ab, an, bb, bn, out, ctypes.byref(nd)), "agk_mul_bcast_shape")
+    return tuple(out[i] for i in range(nd.value))
+
+
+def mul_bcast_fwd(a, b, y=None, accumulate=False, stream=None):
+    """y (+)= a * b under numpy broadcasting (agk_mul_bcast_fwd)."""
+    torch = _torch()
+    shape = mul_bcast_shape(a.shape, b.shape)
+    if y is None:
+        y = torch.empty(shape, dtype=a.dtype, device=a.device)
+    ab, an = _shape_arg(tuple(a.shape))
+    bb, bn = _shape_arg(tuple(b.shape))
+    rc = lib().agk_mul_bcast_fwd(_ptr(a), ab, an, _ptr(b), bb, bn, _ptr(y), _dtype_code(a),
+                                 int(bool(accumulate)), _stream(stream))
+    _check(rc, "agk_mul_bcast_fwd")
+    return y
+
+
+def mul_bcast_grad_dtype(operand_shape, out_shape, dtype):
+    """The dtype agk_mul_bcast_bwd writes an operand's gradient in: the storage
+    dtype when the operand covers the output, fp32 when it was broadcast."""
+    torch = _torch()
+    n = len(out_shape)
+    aligned = (1,) * (n - len(operand_shape)) + tuple(operand_shape)
+    return dtype if aligned == tuple(out_shape) else torch.float32
+
+
+def mul_bcast_bwd(gy, a, b, da=None, db=None, accumulate=False, want_da: bool = True,
+                  want_db: bool = True, stream=None):
+    """vjp_Mul with reduce_for_broadcast (agk_mul_bcast_bwd): da (+)= the sum of
+    gy * b over a's broadcast axes, db likewise; gradients of broadcast operands
+    in fp32, of full-shape operands in the storage dtype."""
+    torch = _torch()
+    out_shape = mul_bcast_shape(a.shape, b.shape)
+    acc = _accum_flags(accumulate)
+    if want_da and da is None:
+        da = torch.empty(tuple(a.shape), dtype=mul_bcast_grad_dtype(a.shape, out_shape, a.dtype),
+                         device=a.device)
+    if want_db and db is None:
+        db = torch.empty(tuple(b.shape), dtype=mul_bcast_grad_dtype(b.shape, out_shape, b.dtype),
+                         device=b.device)
+    ab, an = _shape_arg(tuple(a.shape))
+    bb, bn = _shape_arg(tuple(b.shape))
+    rc = lib().agk_mul_bcast_bwd(_ptr(gy), _ptr(a), ab, an, _ptr(b), bb, bn, _ptr(da), _ptr(db),
+                                 _dtype_code(a), acc, _stream(stream))
+    _check(rc, "agk_mul_bcast_bwd")
+    return da, db
 
 
 def sum_rows(x, out=None, accumulate=False, stream=None):

@@ -28,6 +28,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -58,7 +59,8 @@ def _atomic_build(out: str, cmd_for: callable) -> None:
     os.replace(tmp, out)
 
 
-def hip_library(name: str, sources: list[str], extra: list[str] | None = None) -> str:
+def hip_library(name: str, sources: list[str], extra: list[str] | None = None,
+                libs: list[str] | None = None) -> str:
     """Compiles each source to an object (in parallel), then links the library."""
     out = os.path.join(LIB, name)
     objdir = os.path.join(LIB, "obj")
@@ -72,7 +74,7 @@ def hip_library(name: str, sources: list[str], extra: list[str] | None = None) -
 
     with ThreadPoolExecutor(max_workers=len(sources)) as ex:
         objs = list(ex.map(compile_one, sources))
-    _atomic_build(out, lambda o: [HIPCC, *HIP_FLAGS, "-shared", *objs, "-o", o])
+    _atomic_build(out, lambda o: [HIPCC, *HIP_FLAGS, "-shared", *objs, "-o", o, *(libs or [])])
     return out
 
 
@@ -84,9 +86,14 @@ def host_library(name: str, sources: list[str], compiler: str = "g++") -> str:
     return out
 
 
+# The kernel library's sources, and what it links beyond the HIP runtime
+# (rocBLAS for the graph layer's fp32 matmul, gemm_f32.hip).
+KERNEL_SOURCES = ["rmsnorm.hip", "gemm.hip", "gemm_f32.hip", "rowops.hip", "bcast.hip",
+                  "probe.hip"]
+KERNEL_LIBS = [f"-L{ROCM}/lib", "-lrocblas", f"-Wl,-rpath,{ROCM}/lib"]
+
 AG_DIR = os.path.join(PKG, "ag")
 AG_SOURCES = ["tensor.cpp", "graph.cpp", "ops.cpp", "autodiff.cpp", "nn.cpp", "runtime.cpp"]
-ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 # Host C++ against the HIP runtime API (no device code in these files).
 HOST_HIP_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
                   f"-I{ROCM}/include", f"-I{os.path.join(AG_DIR, 'include')}", f"-I{INCLUDE}"]
@@ -125,9 +132,8 @@ def build_sanitized(out_dir: str, verbose: bool = True) -> list[str]:
     host = [f for flag in SAN_HOST_FLAGS for f in ("-Xarch_host", flag)]
     try:
         LIB = out_dir
-        outs = [hip_library("libagk_rmsnorm.so",
-                            ["rmsnorm.hip", "gemm.hip", "rowops.hip", "probe.hip"],
-                            extra=[*host, "-g"])]
+        outs = [hip_library("libagk_rmsnorm.so", KERNEL_SOURCES, extra=[*host, "-g"],
+                            libs=KERNEL_LIBS)]
         clang = os.path.join(ROCM, "llvm", "bin", "clang++")
         out = os.path.join(out_dir, "libagk_synth.so")
         _atomic_build(out, lambda o: [clang, *SAN_HOST_FLAGS, "-g", "-O1", "-fPIC", "-shared",
@@ -154,8 +160,7 @@ def build_all(verbose: bool = True) -> list[str]:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(LIB, exist_ok=True)
     jobs = [
-        lambda: hip_library("libagk_rmsnorm.so",
-                            ["rmsnorm.hip", "gemm.hip", "rowops.hip", "probe.hip"]),
+        lambda: hip_library("libagk_rmsnorm.so", KERNEL_SOURCES, libs=KERNEL_LIBS),
         lambda: host_library("libagk_synth.so", ["synth.cpp"]),
     ]
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:

@@ -52,6 +52,51 @@ bool is_row_vector(const Tensor& t, int64_t cols) {
     return true;
 }
 
+// The output shape of a * b under the tensor library's broadcasting (numpy
+// rules: shapes aligned at the trailing axis, extents equal or 1).
+std::vector<int64_t> mul_out_shape(const Tensor& a, const Tensor& b, const char* op) {
+    int64_t out[8];
+    int nd = 0;
+    const std::vector<int64_t>& as = a.shape();
+    const std::vector<int64_t>& bs = b.shape();
+    if (agk_mul_bcast_shape(as.data(), static_cast<int>(as.size()), bs.data(),
+                            static_cast<int>(bs.size()), out, &nd) != AGK_OK) {
+        auto str = [](const std::vector<int64_t>& s) {
+            std::string r = "[";
+            for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+            return r + "]";
+        };
+        fail(std::string(op) + ": shapes " + str(as) + " and " + str(bs) +
+             " do not broadcast (or have more than 8 axes)");
+    }
+    return std::vector<int64_t>(out, out + nd);
+}
+
+// Which kernels a product takes: equal shapes and a row vector broadcast over
+// the other operand's rows have their own; every other broadcast the general
+// ones (agk_mul_bcast_*).
+enum class MulForm { Equal, RowB, RowA, General };
+
+MulForm mul_form(const Tensor& av, const Tensor& bv, const std::vector<int64_t>& out) {
+    if (av.shape() == bv.shape()) return MulForm::Equal;
+    int64_t n = 1;
+    for (int64_t e : out) n *= e;
+    if (av.dim() >= 1 && is_row_vector(bv, av.cols()) && n == av.numel()) return MulForm::RowB;
+    if (bv.dim() >= 1 && is_row_vector(av, bv.cols()) && n == bv.numel()) return MulForm::RowA;
+    return MulForm::General;
+}
+
+// Whether an operand covers the whole output (its gradient then keeps its dtype).
+bool covers_output(const Tensor& t, const std::vector<int64_t>& out) {
+    if (t.dim() > static_cast<int64_t>(out.size())) return false;
+    const size_t pad = out.size() - static_cast<size_t>(t.dim());
+    for (size_t i = 0; i < out.size(); ++i) {
+        const int64_t e = i < pad ? 1 : t.shape()[i - pad];
+        if (e != out[i]) return false;
+    }
+    return true;
+}
+
 std::vector<int64_t> row_stat_shape(const Tensor& x) {
     std::vector<int64_t> s = x.shape();
     if (s.empty()) s.push_back(1);
@@ -104,6 +149,35 @@ void gemm(const void* A, int64_t lda, bool at, const void* B, int64_t ldb, bool 
     agk_check(agk_gemm_bf16(A, lda, at, B, ldb, bt, C, ldc, agk_dtype_of(cdt), M, N, K, nullptr,
                             nullptr, acc ? 1 : 0, ws ? ws->data() : nullptr, wsb, stream_arg()),
               what);
+}
+
+// The same product on fp32 operands (rocBLAS sgemm through agk_gemm_f32).
+void gemm_f32(const void* A, int64_t lda, bool at, const void* B, int64_t ldb, bool bt, void* C,
+              int64_t ldc, int64_t M, int64_t N, int64_t K, bool acc, const char* what) {
+    agk_check(agk_gemm_f32(static_cast<const float*>(A), lda, at, static_cast<const float*>(B),
+                           ldb, bt, static_cast<float*>(C), ldc, M, N, K, acc ? 1 : 0,
+                           stream_arg()),
+              what);
+}
+
+// C (+)= op(A) op(B) in the operands' dtype family: bf16 operands on the MFMA
+// kernel (C in cdt), fp32 operands through gemm_f32 (C fp32).
+void product(bool f32, const void* A, int64_t lda, bool at, const void* B, int64_t ldb, bool bt,
+             void* C, int64_t ldc, Dtype cdt, int64_t M, int64_t N, int64_t K, bool acc,
+             const char* what) {
+    if (f32)
+        gemm_f32(A, lda, at, B, ldb, bt, C, ldc, M, N, K, acc, what);
+    else
+        gemm(A, lda, at, B, ldb, bt, C, ldc, cdt, M, N, K, acc, what);
+}
+
+// The rows of a matmul operand [..., K]: the product of its leading axes.
+// (Tensor::rows() divides numel by the last axis and so reports 0 rows for
+// K == 0, where the product still has rows: zeros.)
+int64_t lead_rows(const Tensor& t) {
+    int64_t r = 1;
+    for (int64_t i = 0; i + 1 < t.dim(); ++i) r *= t.shape()[i];
+    return r;
 }
 
 // A tangent of `like`'s shape and dtype that is all zeros.
@@ -163,25 +237,31 @@ std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a,
     const Tensor& bv = b->value;
     if (av.dtype() != bv.dtype()) fail("mul: operands must have the same dtype");
     const int dt = agk_dtype_of(av.dtype());
-    Tensor y;
-    if (av.shape() == bv.shape()) {
-        y = Tensor::empty(av.shape(), av.dtype());
-        agk_check(agk_mul_rowbcast_fwd(av.data(), bv.data(), y.data(), 1, av.numel(), dt,
-                                       stream_arg()),
-                  "mul");
-    } else if (av.dim() >= 1 && is_row_vector(bv, av.cols())) {
-        y = Tensor::empty(av.shape(), av.dtype());
-        agk_check(agk_mul_rowbcast_fwd(av.data(), bv.data(), y.data(), av.rows(), av.cols(), dt,
-                                       stream_arg()),
-                  "mul");
-    } else if (bv.dim() >= 1 && is_row_vector(av, bv.cols())) {
-        y = Tensor::empty(bv.shape(), bv.dtype());
-        agk_check(agk_mul_rowbcast_fwd(bv.data(), av.data(), y.data(), bv.rows(), bv.cols(), dt,
-                                       stream_arg()),
-                  "mul");
-    } else {
-        fail("mul: only equal shapes or a row vector broadcast over the leading axes are "
-             "supported");
+    const std::vector<int64_t> out = mul_out_shape(av, bv, "mul");
+    Tensor y = Tensor::empty(out, av.dtype());
+    switch (mul_form(av, bv, out)) {
+        case MulForm::Equal:
+            agk_check(agk_mul_rowbcast_fwd(av.data(), bv.data(), y.data(), 1, av.numel(), dt,
+                                           stream_arg()),
+                      "mul");
+            break;
+        case MulForm::RowB:
+            agk_check(agk_mul_rowbcast_fwd(av.data(), bv.data(), y.data(), av.rows(), av.cols(),
+                                           dt, stream_arg()),
+                      "mul");
+            break;
+        case MulForm::RowA:
+            agk_check(agk_mul_rowbcast_fwd(bv.data(), av.data(), y.data(), bv.rows(), bv.cols(),
+                                           dt, stream_arg()),
+                      "mul");
+            break;
+        case MulForm::General:
+            agk_check(agk_mul_bcast_fwd(av.data(), av.shape().data(),
+                                        static_cast<int>(av.dim()), bv.data(), bv.shape().data(),
+                                        static_cast<int>(bv.dim()), y.data(), dt, 0,
+                                        stream_arg()),
+                      "mul");
+            break;
     }
     auto n = std::make_shared<Node>(y, Op::Mul, a->requires_grad() || b->requires_grad(), "*");
     link_inputs(n, {a, b});
@@ -194,18 +274,21 @@ std::shared_ptr<Node> matmul_nodeops(const std::shared_ptr<Node>& a,
     require_value(b, "matmul");
     const Tensor& av = a->value;
     const Tensor& bv = b->value;
-    if (av.dtype() != Dtype::BFloat16 || bv.dtype() != Dtype::BFloat16)
-        fail("matmul: operands must be bfloat16 (the product runs on the bf16 matrix cores)");
+    const bool f32 = av.dtype() == Dtype::Float32 && bv.dtype() == Dtype::Float32;
+    if (!f32 && (av.dtype() != Dtype::BFloat16 || bv.dtype() != Dtype::BFloat16))
+        fail("matmul: operands must both be bfloat16 (the bf16 matrix-core kernel) or both "
+             "float32 (a library sgemm)");
     if (bv.dim() != 2 || av.dim() < 1 || av.cols() != bv.shape()[0])
         fail("matmul: expects a [..., K] and b [K, N]");
-    const int64_t M = av.rows(), K = av.cols(), N = bv.shape()[1];
-    if (M % 8 || N % 8 || K % 8) fail("matmul: M, N and K must be multiples of 8");
+    const int64_t M = lead_rows(av), K = av.cols(), N = bv.shape()[1];
+    if (!f32 && (M % 8 || N % 8 || K % 8))
+        fail("matmul: bfloat16 operands need M, N and K multiples of 8");
     std::vector<int64_t> ys = av.shape();
     ys.back() = N;
-    Tensor y = Tensor::empty(ys, Dtype::BFloat16);
+    Tensor y = Tensor::empty(ys, av.dtype());
     if (M && N)  // K == 0: the GEMM's empty sum writes zeros
-        gemm(av.data(), K, false, bv.data(), N, false, y.data(), N, Dtype::BFloat16, M, N, K,
-             false, "matmul");
+        product(f32, av.data(), K, false, bv.data(), N, false, y.data(), N, av.dtype(), M, N, K,
+                false, "matmul");
     auto n = std::make_shared<Node>(y, Op::MatMul, a->requires_grad() || b->requires_grad(),
                                     "matmul");
     link_inputs(n, {a, b});
@@ -226,7 +309,7 @@ std::shared_ptr<Node> linear_nodeops(const std::shared_ptr<Node>& x,
         fail("linear: x, w and b must be bfloat16 (the product runs on the bf16 matrix cores)");
     if (wv.dim() != 2 || xv.dim() < 1 || xv.cols() != wv.shape()[1])
         fail("linear: expects x [..., K] and w [N, K]");
-    const int64_t M = xv.rows(), K = xv.cols(), N = wv.shape()[0];
+    const int64_t M = lead_rows(xv), K = xv.cols(), N = wv.shape()[0];
     if (!is_row_vector(bv, N)) fail("linear: b must have shape [N] or [1, N]");
     if (M % 8 || N % 8 || K % 8) fail("linear: the batch, N and K must be multiples of 8");
     std::vector<int64_t> ys = xv.shape();
@@ -397,7 +480,33 @@ void vjp_Mul(Node* n, const Tensor& gy) {
     const Tensor& av = A->value;
     const Tensor& bv = B->value;
     const int dt = agk_dtype_of(av.dtype());
-    if (av.shape() == bv.shape()) {
+    const std::vector<int64_t>& out = n->value.shape();
+    const MulForm form = mul_form(av, bv, out);
+    if (form == MulForm::General) {
+        // any other broadcast: each gradient summed over its operand's
+        // broadcast axes (fp32), or the element-wise product (dtype) for an
+        // operand that covers the output
+        GradLocks lock(A, B);
+        int acc = AGK_ACCUM_NONE;
+        void* da = nullptr;
+        void* db = nullptr;
+        if (want_a) {
+            bool a = false;
+            da = A->grad_for_write(covers_output(av, out) ? av.dtype() : Dtype::Float32, &a).data();
+            if (a) acc |= AGK_ACCUM_DX;
+        }
+        if (want_b) {
+            bool a = false;
+            db = B->grad_for_write(covers_output(bv, out) ? bv.dtype() : Dtype::Float32, &a).data();
+            if (a) acc |= AGK_ACCUM_DGAMMA;
+        }
+        agk_check(agk_mul_bcast_bwd(gy.data(), av.data(), av.shape().data(),
+                                    static_cast<int>(av.dim()), bv.data(), bv.shape().data(),
+                                    static_cast<int>(bv.dim()), da, db, dt, acc, stream_arg()),
+                  "vjp_Mul");
+        return;
+    }
+    if (form == MulForm::Equal) {
         GradLocks lock(A, B);
         // equal shapes: dA = gy * B and dB = gy * A, both element-wise, each in
         // its operand's dtype (one launch per gradient; A == B adds twice)
@@ -421,7 +530,7 @@ void vjp_Mul(Node* n, const Tensor& gy) {
         return;
     }
     // row-vector broadcast: `full` is [..., D], `row` is [D] / [1, D]
-    const bool b_is_row = is_row_vector(bv, av.cols()) && av.dim() >= 1;
+    const bool b_is_row = form == MulForm::RowB;
     Node* F = b_is_row ? A : B;
     Node* Rw = b_is_row ? B : A;
     const Tensor& full = F->value;
@@ -463,21 +572,24 @@ void vjp_MatMul(Node* n, const Tensor& gy) {
     check_upstream(n, gy, "vjp_MatMul");
     const Tensor& av = A->value;
     const Tensor& bv = B->value;
-    const int64_t M = av.rows(), K = av.cols(), N = bv.shape()[1];
+    const int64_t M = lead_rows(av), K = av.cols(), N = bv.shape()[1];
+    // bf16: dA in bf16, dB in fp32; fp32 operands: both fp32
+    const bool f32 = av.dtype() == Dtype::Float32;
+    const Dtype da_dt = f32 ? Dtype::Float32 : Dtype::BFloat16;
     GradLocks lock(A, B);
     if (want_a) {
         bool acc = false;
-        Tensor& da = A->grad_for_write(Dtype::BFloat16, &acc);
+        Tensor& da = A->grad_for_write(da_dt, &acc);
         if (M && K)  // N == 0: an empty sum (zeros, or da unchanged when accumulating)
-            gemm(gy.data(), N, false, bv.data(), N, true, da.data(), K, Dtype::BFloat16, M, K, N,
-                 acc, "vjp_MatMul dA");
+            product(f32, gy.data(), N, false, bv.data(), N, true, da.data(), K, da_dt, M, K, N,
+                    acc, "vjp_MatMul dA");
     }
     if (want_b) {
         bool acc = false;
         Tensor& db = B->grad_for_write(Dtype::Float32, &acc);
         if (K && N)  // M == 0: an empty sum over the batch
-            gemm(av.data(), K, true, gy.data(), N, false, db.data(), N, Dtype::Float32, K, N, M,
-                 acc, "vjp_MatMul dB");
+            product(f32, av.data(), K, true, gy.data(), N, false, db.data(), N, Dtype::Float32, K,
+                    N, M, acc, "vjp_MatMul dB");
     }
 }
 
@@ -494,7 +606,7 @@ void vjp_Linear(Node* n, const Tensor& gy) {
     check_upstream(n, gy, "vjp_Linear");
     const Tensor& xv = X->value;
     const Tensor& wv = Wn->value;
-    const int64_t M = xv.rows(), K = xv.cols(), N = wv.shape()[0];
+    const int64_t M = lead_rows(xv), K = xv.cols(), N = wv.shape()[0];
     GradLocks lock(X, Wn, Bn);
     if (want_x) {  // [M, K] = gy [M, N] . W [N, K]
         bool acc = false;
@@ -597,10 +709,24 @@ Tensor jvp_Mul(Node* n, const TangentOf& tan) {
     const Tensor& bv = B->value;
     Tensor out = Tensor::empty(n->value.shape(), n->value.dtype());
     const int dt = agk_dtype_of(av.dtype());
+    const MulForm form = mul_form(av, bv, n->value.shape());
+    if (form == MulForm::General) {  // out = tA * B + A * tB, each broadcast
+        bool first = true;
+        auto add = [&](const Tensor& x, const Tensor& y) {
+            agk_check(agk_mul_bcast_fwd(x.data(), x.shape().data(), static_cast<int>(x.dim()),
+                                        y.data(), y.shape().data(), static_cast<int>(y.dim()),
+                                        out.data(), dt, first ? 0 : 1, stream_arg()),
+                      "jvp_Mul");
+            first = false;
+        };
+        if (ta.defined()) add(ta, bv);
+        if (tb.defined()) add(av, tb);
+        return out;
+    }
     // full [..., D] times row [D]: out (+)= t_full * row and full * t_row, each
     // through the broadcast multiply's da path (equal shapes: one row of numel)
-    const bool equal = av.shape() == bv.shape();
-    const bool b_is_row = !equal && av.dim() >= 1 && is_row_vector(bv, av.cols());
+    const bool equal = form == MulForm::Equal;
+    const bool b_is_row = form == MulForm::RowB;
     const Tensor& full = equal || b_is_row ? av : bv;
     const int64_t rows = equal ? 1 : full.rows();
     const int64_t cols = equal ? full.numel() : full.cols();
@@ -637,18 +763,19 @@ Tensor jvp_MatMul(Node* n, const TangentOf& tan) {
     check_tangent(tb, B->value, "jvp_MatMul");
     const Tensor& av = A->value;
     const Tensor& bv = B->value;
-    const int64_t M = av.rows(), K = av.cols(), N = bv.shape()[1];
-    Tensor out = Tensor::empty(n->value.shape(), Dtype::BFloat16);
+    const int64_t M = lead_rows(av), K = av.cols(), N = bv.shape()[1];
+    const bool f32 = av.dtype() == Dtype::Float32;
+    Tensor out = Tensor::empty(n->value.shape(), n->value.dtype());
     if (M == 0 || N == 0) return out;
     bool acc = false;
     if (ta.defined()) {
-        gemm(ta.data(), K, false, bv.data(), N, false, out.data(), N, Dtype::BFloat16, M, N, K,
-             false, "jvp_MatMul");
+        product(f32, ta.data(), K, false, bv.data(), N, false, out.data(), N, out.dtype(), M, N,
+                K, false, "jvp_MatMul");
         acc = true;
     }
     if (tb.defined())
-        gemm(av.data(), K, false, tb.data(), N, false, out.data(), N, Dtype::BFloat16, M, N, K,
-             acc, "jvp_MatMul");
+        product(f32, av.data(), K, false, tb.data(), N, false, out.data(), N, out.dtype(), M, N,
+                K, acc, "jvp_MatMul");
     return out;
 }
 
@@ -704,7 +831,7 @@ Tensor jvp_Linear(Node* n, const TangentOf& tan) {
     check_tangent(tb, Bn->value, "jvp_Linear");
     const Tensor& xv = X->value;
     const Tensor& wv = Wn->value;
-    const int64_t M = xv.rows(), K = xv.cols(), N = wv.shape()[0];
+    const int64_t M = lead_rows(xv), K = xv.cols(), N = wv.shape()[0];
     Tensor out = Tensor::empty(n->value.shape(), Dtype::BFloat16);
     if (M == 0 || N == 0) return out;
     const void* bias = tb.defined() ? tb.data() : nullptr;

@@ -142,6 +142,47 @@ int agk_mul_rowbcast_bwd(const void* gy, const void* a, const void* b,
                          size_t workspace_bytes, int64_t rows, int64_t cols,
                          int dtype, int accumulate, agk_stream_t stream);
 
+/* Element-wise multiply under numpy broadcasting, for every shape pair the
+ * row-vector kernels above do not cover: mul_nodeops's `a->value * b->value`
+ * (cgadimpl/src/ops/arithmetic.cpp:31-39) with the tensor library's
+ * broadcasting.  Shapes (row-major, contiguous, at most 8 axes each) align at
+ * the trailing axis; each aligned axis pair must be equal or contain a 1.
+ * agk_mul_bcast_shape writes the output shape (out_shape may be NULL to get
+ * only out_ndim); AGK_EINVAL for incompatible shapes.
+ * agk_mul_bcast_fwd: y (+)= a * b in dtype (accumulate != 0 adds into y, the
+ * product rounded to storage first).  An empty output is a no-op.          */
+int agk_mul_bcast_shape(const int64_t* a_shape, int a_ndim, const int64_t* b_shape,
+                        int b_ndim, int64_t* out_shape, int* out_ndim);
+int agk_mul_bcast_fwd(const void* a, const int64_t* a_shape, int a_ndim,
+                      const void* b, const int64_t* b_shape, int b_ndim, void* y,
+                      int dtype, int accumulate, agk_stream_t stream);
+
+/* vjp_Mul with reduce_for_broadcast for those shapes
+ * (cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:54-59, :15-35):
+ *   da (+)= sum over a's broadcast axes of gy * b,  db (+)= ... of gy * a.
+ * gy has the output's shape.  The gradient of an operand whose aligned shape
+ * is the output's is the element-wise product in dtype; the gradient of a
+ * broadcast operand is an fp32 array of the operand's shape, summed from
+ * exact products in fp64 in a fixed order (bit-identical run to run).
+ * da or db NULL skips that gradient.  accumulate: AGK_ACCUM_DX adds into da,
+ * AGK_ACCUM_DGAMMA adds into db.  An empty output gives zero gradients (or
+ * leaves them when accumulating).                                          */
+int agk_mul_bcast_bwd(const void* gy, const void* a, const int64_t* a_shape, int a_ndim,
+                      const void* b, const int64_t* b_shape, int b_ndim, void* da,
+                      void* db, int dtype, int accumulate, agk_stream_t stream);
+
+/* fp32 GEMM for the graph layer's matmul on float32 tensors
+ * (cgadimpl/src/ops/linalg.cpp:12-20; VJP autodiff_vjp_ops.cpp:258-263):
+ *   C[M][ldc] (+)= op(A) op(B), all fp32, row-major,
+ *   A: a_trans == 0 -> [M][lda], else [K][lda];  B: b_trans == 0 -> [K][ldb],
+ *   else [N][ldb].  A plain library GEMM (rocBLAS sgemm, atomics disallowed:
+ *   deterministic), not on the RMSNorm layer's bf16 path.  M == 0 or N == 0
+ *   is a no-op; K == 0 writes zeros (or leaves C when accumulating).  No
+ *   alignment or multiple-of-8 requirements.                                */
+int agk_gemm_f32(const float* A, int64_t lda, int a_trans, const float* B, int64_t ldb,
+                 int b_trans, float* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                 int accumulate, agk_stream_t stream);
+
 /* Column sums out[j] (+)= sum_i x[i, j] of a rows x cols matrix, in fp32 and
  * in a fixed order (the same two-stage partial-row reduction as dgamma; no
  * float atomics, bit-identical run to run): OwnTensor::reduce_sum(gy, {0})

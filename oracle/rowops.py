@@ -23,6 +23,10 @@ to the reference tree):
       rms_nodeops fills with 1/sqrt(mean(x^2)+eps) (normalization.cpp:26-29);
       the derivative of y = x*r is T*r - y*r*dot/N with dot = sum(T*y)
   jvp_Mul                 autodiff_jvp_ops.cpp:24-31     (tA * B) + (A * tB), for gamma
+  mul_nodeops             cgadimpl/src/ops/arithmetic.cpp:31-39  y = a * b (broadcasting)
+  vjp_Mul                 autodiff_vjp_ops.cpp:54-59     dA += reduce_for_broadcast(gy * B, A)
+  reduce_for_broadcast    autodiff_vjp_ops.cpp:15-35     sum over the grad axes whose aligned
+      target axis is missing, or is 1 where the grad's is not (keepdim), then reshape
 
 Arithmetic is done in `dt` (float32 for the parity tests, float64 for the
 pinning checks); each op materialises its result as the reference graph does.
@@ -38,6 +42,8 @@ runs, and outputs are rounded to bf16 (round to nearest even).
   7  log-sum-exp drops the + max               8  log-sum-exp VJP: no / sum
   9  RMSNorm JVP as the reference wrote it (T / r instead of T * r)
  10  RMSNorm JVP: gamma tangent term dropped
+ 11  reduce_for_broadcast sums only the missing leading axes, not the extent-1 ones
+ 12  reduce_for_broadcast aligns the shapes at the leading axis instead of the trailing one
 """
 from __future__ import annotations
 
@@ -206,3 +212,55 @@ def logsumexp_jvp_bf16(z_bits, tz_bits):
 def rmsnorm_jvp_bf16(x_bits, gamma_bits, tx_bits, tgamma_bits=None, eps=1e-5):
     return bf16_encode(rmsnorm_jvp(_dec(x_bits), _dec(gamma_bits), _dec(tx_bits),
                                    _dec(tgamma_bits), eps))
+
+
+# ---- broadcast multiply ------------------------------------------------------------
+
+def reduce_for_broadcast(g, target_shape, mut=0):
+    """autodiff_vjp_ops.cpp:15-35: sum g over the axes where the target, aligned
+    at the trailing axis, is missing or has extent 1 (and g's extent is not),
+    keeping those axes, then reshape to the target.  Summed in float64."""
+    target_shape = tuple(target_shape)
+    if g.shape == target_shape:
+        return g
+    gnd, tnd = g.ndim, len(target_shape)
+    axes = []
+    for i in range(gnd):
+        t = i + tnd - gnd if mut != 12 else i
+        if t < 0 or t >= tnd:
+            axes.append(i)
+        elif target_shape[t] == 1 and g.shape[i] > 1 and mut != 11:
+            axes.append(i)
+    out = np.sum(g, axis=tuple(axes), keepdims=True, dtype=np.float64) if axes else g
+    return out.reshape(target_shape)
+
+
+def mul_bcast_fwd(a, b, dt=np.float32):
+    """mul_nodeops (arithmetic.cpp:31-39): a * b with numpy broadcasting, one rounding."""
+    return np.multiply(a.astype(dt), b.astype(dt), dtype=dt)
+
+
+def mul_bcast_vjp(gy, a, b, mut=0):
+    """vjp_Mul (autodiff_vjp_ops.cpp:54-59) in float64: (dA, dB), each
+    reduce_for_broadcast(gy * other, operand).  Products of float32 or bf16
+    values are exact in float64; the caller rounds (to storage for an operand
+    of the output's shape, to float32 for a broadcast one)."""
+    g = gy.astype(np.float64)
+    da = reduce_for_broadcast(g * b.astype(np.float64), a.shape, mut)
+    db = reduce_for_broadcast(g * a.astype(np.float64), b.shape, mut)
+    return da, db
+
+
+def mul_bcast_vjp_bf16(gy_bits, a_bits, b_bits, mut=0):
+    """The same on bf16 storage: a gradient with the output's shape is the
+    product rounded to bf16 bits; a broadcast operand's is a float32 sum."""
+    gy, a, b = _dec(gy_bits), _dec(a_bits), _dec(b_bits)
+    da, db = mul_bcast_vjp(gy, a, b, mut)
+    out_ndim = gy.ndim
+
+    def finish(d, shape):
+        aligned = (1,) * (out_ndim - len(shape)) + tuple(shape)
+        if aligned == gy.shape:
+            return bf16_encode(d.astype(np.float32))
+        return d.astype(np.float32)
+    return finish(da, a.shape), finish(db, b.shape)

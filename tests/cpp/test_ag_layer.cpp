@@ -2,8 +2,10 @@
 // matmul, laynor, softmax_row, logsumexp_row, backward, jvp, GraphRunner) on
 // the GPU.
 //
-//   test_ag_layer selftest     checks below; prints PASS/FAIL per check and
-//                              exits with the number of failures
+//   test_ag_layer selftest [name ...]
+//                              checks below (all, or the named groups); prints
+//                              PASS/FAIL per check and exits with the number
+//                              of failures
 //   test_ag_layer dump <dir>   reads <dir>/meta.txt ("rows cols dtype eps",
 //                              dtype 0 = f32, 1 = bf16) and x.bin, gamma.bin,
 //                              dy.bin; writes the outputs of the fused layer
@@ -408,6 +410,127 @@ void test_errors() {
     report("backward with a seed of the wrong shape throws", threw);
 }
 
+// mul under general broadcasting: gradients against numerical gradients (the
+// reference pattern) and the tangent against tA * B + A * tB on the host.
+void test_broadcast_mul() {
+    struct Case {
+        std::vector<int64_t> sa, sb, out;
+    };
+    const Case cases[] = {{{2, 3, 4}, {2, 1, 4}, {2, 3, 4}},
+                          {{3, 1}, {1, 5}, {3, 5}},
+                          {{2, 3, 4}, {3, 1}, {2, 3, 4}},
+                          {{1}, {2, 3}, {2, 3}}};
+    uint64_t seed = 80;
+    for (const Case& c : cases) {
+        auto numel = [](const std::vector<int64_t>& s) {
+            int64_t n = 1;
+            for (int64_t e : s) n *= e;
+            return static_cast<size_t>(n);
+        };
+        const std::string tag = "[" + std::to_string(c.sa.size()) + "-d]*[" +
+                                std::to_string(c.sb.size()) + "-d] -> " +
+                                std::to_string(numel(c.out)) + " elements";
+        Value a = leaf(normal(numel(c.sa), seed++), c.sa, "a");
+        Value b = leaf(normal(numel(c.sb), seed++), c.sb, "b");
+        Value w = leaf(normal(numel(c.out), seed++), c.out, "w", false);
+        auto f = [&]() { return (a * b) * w; };
+        report(("broadcast mul output shape " + tag).c_str(), (a * b).val().shape() == c.out);
+        backward(f());
+        check_grad(("broadcast mul da == numerical gradient " + tag).c_str(), a, f);
+        check_grad(("broadcast mul db == numerical gradient " + tag).c_str(), b, f);
+        // forward mode: tA * B + A * tB, on the host by explicit broadcasting
+        Tensor ta = Tensor::from_host_f32(normal(numel(c.sa), seed++), c.sa);
+        Tensor tb = Tensor::from_host_f32(normal(numel(c.sb), seed++), c.sb);
+        Value a2 = leaf(a.val().to_host_f32(), c.sa, "a2"), b2 = leaf(b.val().to_host_f32(), c.sb, "b2");
+        std::vector<float> ty = jvp(a2 * b2, {{a2.node.get(), ta}, {b2.node.get(), tb}}).to_host_f32();
+        const std::vector<float> av = a.val().to_host_f32(), bv = b.val().to_host_f32(),
+                                 tav = ta.to_host_f32(), tbv = tb.to_host_f32();
+        const size_t nd = c.out.size();
+        auto src = [&](const std::vector<int64_t>& s, const std::vector<int64_t>& idx) {
+            size_t off = 0;
+            const size_t pad = nd - s.size();
+            for (size_t i = pad; i < nd; ++i)
+                off = off * s[i - pad] + (s[i - pad] == 1 ? 0 : idx[i]);
+            return off;
+        };
+        double err = 0.0;
+        std::vector<int64_t> idx(nd, 0);
+        for (size_t o = 0; o < ty.size(); ++o) {
+            size_t r = o;
+            for (size_t i = nd; i-- > 0;) {
+                idx[i] = static_cast<int64_t>(r % c.out[i]);
+                r /= c.out[i];
+            }
+            const size_t ia = src(c.sa, idx), ib = src(c.sb, idx);
+            const double t1 = double(tav[ia]) * bv[ib], t2 = double(av[ia]) * tbv[ib];
+            // relative to the terms' size: the two may cancel
+            err = std::max(err, std::fabs(ty[o] - (t1 + t2)) / (std::fabs(t1) + std::fabs(t2) + 1e-6));
+        }
+        report(("broadcast mul jvp == tA * B + A * tB " + tag).c_str(), err <= 1e-6,
+               std::to_string(err));
+    }
+}
+
+// matmul on float32 operands (the library sgemm path): gradients against
+// numerical gradients, values against a host fp64 product, the tangent
+// against tA B + A tB, with sizes that are not multiples of 8.
+void test_matmul_f32() {
+    const int64_t M = 5, K = 7, N = 3;
+    Value a = leaf(normal(M * K, 90), {M, K}, "a");
+    Value b = leaf(normal(K * N, 91), {K, N}, "b");
+    Value w = leaf(normal(M * N, 92), {M, N}, "w", false);
+    auto f = [&]() { return matmul(a, b) * w; };
+    const std::vector<float> y = matmul(a, b).val().to_host_f32();
+    const std::vector<float> av = a.val().to_host_f32(), bv = b.val().to_host_f32();
+    double err = 0.0;
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            double s = 0.0, mag = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                s += double(av[i * K + k]) * bv[k * N + j];
+                mag += std::fabs(double(av[i * K + k]) * bv[k * N + j]);
+            }
+            err = std::max(err, std::fabs(y[i * N + j] - s) / (mag + 1e-30));
+        }
+    report("matmul f32 [5,7] x [7,3] == host fp64 product", err <= 1e-6, std::to_string(err));
+    report("matmul f32: output is float32",
+           matmul(a, b).val().dtype() == Dtype::Float32 &&
+               matmul(a, b).val().shape() == std::vector<int64_t>{M, N});
+    backward(f());
+    report("matmul f32: da and db are float32",
+           a.grad().dtype() == Dtype::Float32 && b.grad().dtype() == Dtype::Float32);
+    check_grad("matmul f32 da == numerical gradient", a, f);
+    check_grad("matmul f32 db == numerical gradient", b, f);
+    Tensor ta = Tensor::from_host_f32(normal(M * K, 93), {M, K});
+    Tensor tb = Tensor::from_host_f32(normal(K * N, 94), {K, N});
+    Value a2 = leaf(av, {M, K}, "a2"), b2 = leaf(bv, {K, N}, "b2");
+    const std::vector<float> ty =
+        jvp(matmul(a2, b2), {{a2.node.get(), ta}, {b2.node.get(), tb}}).to_host_f32();
+    const std::vector<float> tav = ta.to_host_f32(), tbv = tb.to_host_f32();
+    double ej = 0.0;
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            double s = 0.0, mag = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                const double t1 = double(tav[i * K + k]) * bv[k * N + j];
+                const double t2 = double(av[i * K + k]) * tbv[k * N + j];
+                s += t1 + t2;
+                mag += std::fabs(t1) + std::fabs(t2);
+            }
+            ej = std::max(ej, std::fabs(ty[i * N + j] - s) / (mag + 1e-30));
+        }
+    report("matmul f32 jvp == tA B + A tB", ej <= 1e-6, std::to_string(ej));
+    bool threw = false;
+    try {
+        const std::vector<uint16_t> hb(static_cast<size_t>(M * K), 0x3f80);  // ones
+        Value h = make_tensor(Tensor::from_host(hb.data(), {M, K}, Dtype::BFloat16), "h");
+        matmul(h, b);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    report("matmul of bf16 by f32 throws", threw);
+}
+
 void test_empty_batch() {
     Value x = make_tensor(Tensor::empty({0, 16}).set_requires_grad(true), "x");
     Value g = leaf(uniform(16, 23, 0.5, 1.5), {16}, "g");
@@ -742,11 +865,11 @@ void test_matmul_layer() {
 
     bool threw = false;
     try {
-        matmul(leaf(normal(64, 85), {8, 8}, "f32a"), leaf(normal(64, 86), {8, 8}, "f32b"));
+        matmul(bf16_leaf(normal(64, 85), {8, 8}, "bf16a"), leaf(normal(64, 86), {8, 8}, "f32b"));
     } catch (const std::runtime_error&) {
         threw = true;
     }
-    report("matmul of fp32 operands throws", threw);
+    report("matmul of a bf16 by an fp32 operand throws", threw);
     threw = false;
     try {
         matmul(bf16_leaf(normal(64, 87), {8, 8}, "a"), bf16_leaf(normal(128, 88), {16, 8}, "b"));
@@ -903,9 +1026,38 @@ void test_matmul_empty() {
         std::vector<uint16_t> sb = to_bf16_bits(rounded(normal(8 * 16, 109)));
         Tensor seed = Tensor::from_host(sb.data(), {8, 16}, Dtype::BFloat16);
         backward(y, &seed);
+        const double ymax = max_abs(y.val().to_host_f32());
         report("matmul with an empty reduction: y is zero, dA and dB are empty",
-               y.val().numel() == 128 && max_abs(y.val().to_host_f32()) == 0.0 &&
-                   a.grad().numel() == 0 && b.grad().numel() == 0);
+               y.val().numel() == 128 && ymax == 0.0 && a.grad().numel() == 0 &&
+                   b.grad().numel() == 0,
+               "y numel " + std::to_string(y.val().numel()) + " max|y| " + std::to_string(ymax) +
+                   ", dA numel " + std::to_string(a.grad().numel()) + ", dB numel " +
+                   std::to_string(b.grad().numel()));
+    }
+    {  // linear with K == 0: y = the bias in every row; db = column sums of gy
+        Tensor xe = Tensor::empty({8, 0}, Dtype::BFloat16), we = Tensor::empty({16, 0}, Dtype::BFloat16);
+        xe.set_requires_grad(true);
+        we.set_requires_grad(true);
+        const std::vector<float> bvals = rounded(normal(16, 111));
+        Value x = make_tensor(xe, "x3"), w = make_tensor(we, "w3"), b = bf16_leaf(bvals, {16}, "b3");
+        Value y = linear(x, w, b);
+        const std::vector<float> gv = rounded(normal(8 * 16, 112));
+        std::vector<uint16_t> sb = to_bf16_bits(gv);
+        Tensor seed = Tensor::from_host(sb.data(), {8, 16}, Dtype::BFloat16);
+        backward(y, &seed);
+        const std::vector<float> yv = y.val().to_host_f32(), db = b.grad().to_host_f32();
+        double ey = 0.0, eb = 0.0;
+        for (int64_t j = 0; j < 16; ++j) {
+            double s = 0.0;
+            for (int64_t i = 0; i < 8; ++i) {
+                ey = std::max(ey, std::fabs(double(yv[i * 16 + j]) - bvals[j]));
+                s += gv[i * 16 + j];
+            }
+            eb = std::max(eb, std::fabs(db[j] - s));
+        }
+        report("linear with an empty reduction: y is the bias rows, db the column sums of gy",
+               ey == 0.0 && eb <= 1e-5 && x.grad().numel() == 0 && w.grad().numel() == 0,
+               "max |y - b| " + std::to_string(ey) + ", max |db - sum gy| " + std::to_string(eb));
     }
     {  // N == 0: y [8, 0]; dA = gy B^T is an empty sum, so zero
         Value a = bf16_leaf(normal(8 * 32, 110), {8, 32}, "a2");
@@ -1073,7 +1225,8 @@ void test_block_cache() {
     report("block cache: release_stream_cache drops that stream's blocks only", held && dropped);
 }
 
-int selftest() {
+// Runs the named checks (all of them when `only` is empty).
+int selftest(const std::vector<std::string>& only) {
     const std::pair<const char*, void (*)()> tests[] = {
         {"reference_pattern", test_reference_pattern},
         {"fused_layer_gradients", test_fused_layer_gradients},
@@ -1084,6 +1237,8 @@ int selftest() {
         {"weight_tying", test_weight_tying},
         {"module", test_module},
         {"errors", test_errors},
+        {"broadcast_mul", test_broadcast_mul},
+        {"matmul_f32", test_matmul_f32},
         {"empty_batch", test_empty_batch},
         {"bf16_layer", test_bf16_layer},
         {"seed_not_modified", test_seed_not_modified},
@@ -1099,6 +1254,7 @@ int selftest() {
         {"block_cache", test_block_cache},
     };
     for (auto& [name, fn] : tests) {
+        if (!only.empty() && std::find(only.begin(), only.end(), name) == only.end()) continue;
         std::printf("-- %s\n", name);
         std::fflush(stdout);
         try {
@@ -1170,7 +1326,8 @@ int dump(const std::string& dir) {
 
 int main(int argc, char** argv) {
     try {
-        if (argc >= 2 && std::string(argv[1]) == "selftest") return selftest();
+        if (argc >= 2 && std::string(argv[1]) == "selftest")
+            return selftest(std::vector<std::string>(argv + 2, argv + argc));
         if (argc >= 3 && std::string(argv[1]) == "dump") return dump(argv[2]);
         std::fprintf(stderr, "usage: %s selftest | dump <dir>\n", argv[0]);
         return 2;
