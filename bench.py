@@ -490,6 +490,15 @@ def run_c5(steps, warmup, cpu=True):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps
 
+    # each product alone, back to back, as hipBLASLt is timed below (the
+    # timed step above runs them in the layer's order, between the RMSNorm
+    # kernels, which costs a few percent of clock)
+    alone_ms = {
+        "gemm_y": lib_ms(lambda: agk.gemm_bf16(h, W, y, workspace=ws_y, stream=stream)),
+        "gemm_dh": lib_ms(lambda: agk.gemm_bf16(dy, W, dh, trans_b=True, workspace=ws_dh,
+                                                stream=stream)),
+        "gemm_dW": lib_ms(lambda: agk.gemm_bf16(h, dy, dW, trans_a=True, workspace=ws_w,
+                                                stream=stream))}
     torch_ms = {"gemm_y": lib_ms(lambda: h @ W), "gemm_dh": lib_ms(lambda: dy @ W.t()),
                 "gemm_dW": lib_ms(lambda: h.t() @ dy)}
     flops = 2.0 * M * N * K
@@ -519,6 +528,7 @@ def run_c5(steps, warmup, cpu=True):
                      "traffic": None},
         "stages_ms": {k: round(v, 4) for k, v in per.items()},
         "rmsnorm_gbs": round(norm_bytes / (norm_ms * 1e-3) / 1e9, 1),
+        "alone_ms": {k: round(v, 4) for k, v in alone_ms.items()},
         "torch_hipblaslt_ms": {k: round(v, 4) for k, v in torch_ms.items()},
         "torch_hipblaslt_tflops": round(3 * flops / (sum(torch_ms.values()) * 1e-3) / 1e12, 1),
         "cpu_baseline": cpu_baseline_c5() if cpu else None,

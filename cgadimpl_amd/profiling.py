@@ -305,13 +305,21 @@ def write_bench_summary(jsonl, out_md, command):
                   f"hipBLASLt on the same operands {r['torch_hipblaslt_tflops']} TFLOP/s; "
                   f"CPU oracle {cpu.get('value', '-')} TFLOP/s on {cpu.get('cores', '-')} "
                   f"threads.", "",
-                  "| stage | this build us | TFLOP/s | hipBLASLt us | TFLOP/s |", "|---|---|---|---|---|"]
+                  "In the layer step: each stage as the timed step runs it (products between "
+                  "the RMSNorm kernels). Alone: the product repeated back to back, the way "
+                  "hipBLASLt is timed.", "",
+                  "| stage | in the layer step us | TFLOP/s | alone us | TFLOP/s | "
+                  "hipBLASLt us | TFLOP/s |", "|---|---|---|---|---|---|---|"]
+        alone = r.get("alone_ms", {})
         for name, ms in st.items():
             if name in tb:
+                al = alone.get(name)
+                al_cols = (f"{1e3 * al:.1f} | {fl / (al * 1e-3) / 1e12:.0f}" if al else "- | -")
                 lines.append(f"| {name} | {1e3 * ms:.1f} | {fl / (ms * 1e-3) / 1e12:.0f} | "
+                             f"{al_cols} | "
                              f"{1e3 * tb[name]:.1f} | {fl / (tb[name] * 1e-3) / 1e12:.0f} |")
             else:
-                lines.append(f"| {name} | {1e3 * ms:.1f} | - | - | - |")
+                lines.append(f"| {name} | {1e3 * ms:.1f} | - | - | - | - | - |")
         lines.append("")
     with open(out_md, "w") as fh:
         fh.write("\n".join(lines) + "\n")
