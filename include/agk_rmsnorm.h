@@ -83,9 +83,12 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
  * partials, one row of cols floats per workgroup.  The size is nblk * cols * 4
  * bytes with nblk = ceil(rows / rpb), rpb = ceil(rows / 1024) rows (at least
  * 4 once rows >= 2048): the count the looped kernel (unaligned or too-wide
- * rows) uses, never fewer than the min(256, rows) rows the register-resident
- * kernel uses.  Depends only on rows and cols, never on the device, so the
- * dgamma summation order is the same everywhere.                            */
+ * rows) uses, never fewer than the 256 rows the register-resident kernel
+ * uses from 256 rows up.  Below 256 rows the register-resident path sums
+ * dgamma down the columns in the same launch and uses no partial rows (the
+ * size is still returned, for the looped kernel).  Depends only on rows and
+ * cols, never on the device, so the dgamma summation order is the same
+ * everywhere.                                                               */
 size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
 /* Backward (VJP) of the RMSNorm layer.
