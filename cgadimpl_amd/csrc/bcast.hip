@@ -353,6 +353,7 @@ extern "C" int agk_mul_bcast_bwd(const void* gy, const void* a, const int64_t* a
                                  agk_stream_t stream) {
     using namespace agk;
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    if (accumulate & ~AGK_ACCUM_ALL) return AGK_EINVAL;
     int nd = 0;
     Aligned al, bl;
     int64_t osize[kBcastMaxDims];

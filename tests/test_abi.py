@@ -209,6 +209,76 @@ def test_mul_argument_validation():
     assert r(None, None, None, None, None, None, None, None, 0, 0, 4, 0, 2, None) == 0  # empty
 
 
+def _shape(*dims):
+    return (ctypes.c_int64 * max(1, len(dims)))(*dims), len(dims)
+
+
+def test_broadcast_shape_rule():
+    """agk_mul_bcast_shape follows numpy's rules (compared with numpy itself)."""
+    import numpy as np
+    lib = agk.lib()
+    pairs = [((3, 4), (4,)), ((2, 3, 4), (3, 1)), ((1,), (5, 6)), ((), (2,)), ((), ()),
+             ((2, 1, 3, 1), (1, 4, 1, 5)), ((0, 4), (1, 4)), ((7,), (1, 7)), ((3, 4), (2, 4)),
+             ((3,), (4,)), ((2, 0), (2, 3))]
+    for sa, sb in pairs:
+        a, an = _shape(*sa)
+        b, bn = _shape(*sb)
+        out = (ctypes.c_int64 * 8)()
+        nd = ctypes.c_int(-1)
+        rc = lib.agk_mul_bcast_shape(a, an, b, bn, out, ctypes.byref(nd))
+        try:
+            want = np.broadcast_shapes(sa, sb)
+        except ValueError:
+            assert rc == 1, (sa, sb)
+            continue
+        assert rc == 0 and tuple(out[i] for i in range(nd.value)) == want, (sa, sb)
+    nine, n9 = _shape(*([1] * 9))
+    one, n1 = _shape(1)
+    nd = ctypes.c_int(0)
+    assert lib.agk_mul_bcast_shape(nine, n9, one, n1, None, ctypes.byref(nd)) == 1  # > 8 axes
+    neg, nn = _shape(-1, 4)
+    assert lib.agk_mul_bcast_shape(neg, nn, one, n1, None, ctypes.byref(nd)) == 1   # negative
+    assert lib.agk_mul_bcast_shape(one, n1, one, n1, None, None) == 1               # no out_ndim
+
+
+def test_broadcast_mul_argument_validation():
+    lib = agk.lib()
+    a, an = _shape(3, 4)
+    b, bn = _shape(4)
+    bad, badn = _shape(2, 4)
+    e, en = _shape(0, 4)
+    f = lib.agk_mul_bcast_fwd  # a, a_shape, a_ndim, b, b_shape, b_ndim, y, dtype, acc
+    assert f(FAKE, a, an, FAKE, bad, badn, FAKE, 0, 0, None) == 1    # shapes do not broadcast
+    assert f(FAKE, a, an, FAKE, b, bn, FAKE, 3, 0, None) == 2        # dtype
+    assert f(None, a, an, FAKE, b, bn, FAKE, 0, 0, None) == 1        # a
+    assert f(FAKE, a, an, FAKE, b, bn, None, 0, 0, None) == 1        # y
+    assert f(None, e, en, None, b, bn, None, 0, 0, None) == 0        # empty output
+    g = lib.agk_mul_bcast_bwd  # gy, a, a_shape, a_ndim, b, b_shape, b_ndim, da, db, dt, acc
+    assert g(FAKE, FAKE, a, an, FAKE, bad, badn, FAKE, FAKE, 0, 0, None) == 1  # shapes
+    assert g(FAKE, FAKE, a, an, FAKE, b, bn, FAKE, FAKE, 5, 0, None) == 2      # dtype
+    assert g(FAKE, FAKE, a, an, FAKE, b, bn, FAKE, FAKE, 0, 4, None) == 1      # accumulate bits
+    assert g(None, FAKE, a, an, FAKE, b, bn, FAKE, None, 0, 0, None) == 1      # gy
+    assert g(FAKE, FAKE, a, an, None, b, bn, FAKE, None, 0, 0, None) == 1      # da needs b
+    assert g(FAKE, None, a, an, FAKE, b, bn, None, FAKE, 0, 0, None) == 1      # db needs a
+    assert g(FAKE, FAKE, a, an, FAKE, b, bn, None, None, 0, 0, None) == 0      # nothing asked
+    assert g(None, None, e, en, None, b, bn, None, FAKE, 0, 3, None) == 0      # empty, accumulate
+
+
+def test_gemm_f32_argument_validation():
+    lib = agk.lib()
+    g = lib.agk_gemm_f32  # A, lda, a_trans, B, ldb, b_trans, C, ldc, M, N, K, accumulate
+    assert g(FAKE, 8, 0, FAKE, 8, 0, FAKE, 8, -1, 8, 8, 0, None) == 1          # negative M
+    assert g(FAKE, 8, 0, FAKE, 8, 0, FAKE, 8, 8, 8, 1 << 31, 0, None) == 1     # K past int32
+    assert g(None, 8, 0, None, 8, 0, None, 8, 0, 8, 8, 0, None) == 0           # no rows
+    assert g(FAKE, 8, 0, FAKE, 8, 0, None, 8, 8, 8, 8, 0, None) == 1           # C
+    assert g(FAKE, 8, 0, FAKE, 8, 0, FAKE, 7, 8, 8, 8, 0, None) == 1           # ldc < N
+    assert g(None, 8, 0, FAKE, 8, 0, FAKE, 8, 8, 8, 8, 0, None) == 1           # A with K > 0
+    assert g(FAKE, 7, 0, FAKE, 8, 0, FAKE, 8, 8, 8, 8, 0, None) == 1           # lda < K
+    assert g(FAKE, 7, 1, FAKE, 8, 0, FAKE, 8, 8, 8, 8, 0, None) == 1           # lda < M (A^T)
+    assert g(FAKE, 8, 0, FAKE, 7, 0, FAKE, 8, 8, 8, 8, 0, None) == 1           # ldb < N
+    assert g(FAKE, 8, 0, FAKE, 7, 1, FAKE, 8, 8, 8, 8, 0, None) == 1           # ldb < K (B^T)
+
+
 def test_rowops_argument_validation():
     lib = agk.lib()
     j = lib.agk_rmsnorm_jvp
