@@ -26,6 +26,8 @@ Usage:
   python -m cgadimpl_amd.profiling probe <bench --stream-probe output> <out.md> "<command>"
   python -m cgadimpl_amd.profiling traffic <fetch_dir> <write_dir> <copy_fetch_dir>
         <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
+  python -m cgadimpl_amd.profiling gemm-traffic <fetch_dir> <write_dir> <copy_fetch_dir>
+        <copy_write_dir> <copy_mib> <out.md> "<command>"
 """
 from __future__ import annotations
 
@@ -208,6 +210,53 @@ def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, 
         fh.write("\n")
 
 
+def _counter_by_launch(run_dir, counter, name_part):
+    """{grid size: [per-dispatch values]} of one counter for the kernels whose
+    name contains name_part (the c5 products share one kernel name and differ
+    in their grids)."""
+    vals = defaultdict(list)
+    for r in _rows(os.path.join(run_dir, "run_counter_collection.csv")):
+        if r["Counter_Name"] == counter and name_part in r["Kernel_Name"]:
+            vals[int(r["Grid_Size"])].append(float(r["Counter_Value"]))
+    return vals
+
+
+# The c5 products by grid size (256 lanes per 256 x 256 tile): their
+# algorithmic bytes, A + B read once and C written once.
+C5_PRODUCTS = {
+    32 * 43 * 256: ("y = h W", 8192 * 4096 * 2 + 4096 * 11008 * 2, 8192 * 11008 * 2),
+    32 * 16 * 256: ("dh = dy W^T", 8192 * 11008 * 2 + 4096 * 11008 * 2, 8192 * 4096 * 2),
+    16 * 43 * 256: ("dW = h^T dy", 8192 * 4096 * 2 + 8192 * 11008 * 2, 4096 * 11008 * 4),
+}
+
+
+def write_gemm_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib,
+                               out_md, command, name_part="gemm_nt_direct"):
+    """HBM bytes per launch of each c5 product (median over its dispatches),
+    against the bytes of its operands and result."""
+    _, fs, ws = traffic(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib)
+    f = _counter_by_launch(fetch_dir, "FETCH_SIZE", name_part)
+    w = _counter_by_launch(write_dir, "WRITE_SIZE", name_part)
+    lines = ["# HBM traffic per launch of the c5 products (bf16 GEMM)", "",
+             "Commands (each counter in its own run):", "", "```", command, "```", "",
+             f"Counter scale from a {copy_mib} MiB device copy (`bench.py --copy-probe "
+             f"{copy_mib}`): FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {ws:.4f}. Algorithmic bytes: "
+             "A and B read once, C written once.", "",
+             "| product | grid | launches | read MB | write MB | algorithmic read MB | "
+             "algorithmic write MB | read ratio | write ratio |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for grid in sorted(set(f) | set(w)):
+        name, ar, aw = C5_PRODUCTS.get(grid, (f"grid {grid}", 0, 0))
+        rd = _median(f[grid]) * fs * 1024.0 if grid in f else 0.0
+        wr = _median(w[grid]) * ws * 1024.0 if grid in w else 0.0
+        n = max(len(f.get(grid, [])), len(w.get(grid, [])))
+        lines.append(f"| {name} | {grid} | {n} | {rd / 1e6:.1f} | {wr / 1e6:.1f} | "
+                     f"{ar / 1e6:.1f} | {aw / 1e6:.1f} | {rd / ar if ar else 0:.3f} | "
+                     f"{wr / aw if aw else 0:.3f} |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
 def write_mfma_summary(counter_csv, out_md, command, simds=1024, clock_ghz=2.4):
     per = defaultdict(lambda: defaultdict(float))
     disp = defaultdict(dict)
@@ -356,6 +405,9 @@ def main(argv):
         write_bench_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "mfma":
         write_mfma_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 8 and argv[0] == "gemm-traffic":
+        write_gemm_traffic_summary(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6],
+                                   argv[7])
     elif len(argv) >= 9 and argv[0] == "traffic":
         write_traffic_summary(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6],
                               argv[7], argv[8])
