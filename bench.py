@@ -301,7 +301,8 @@ def run(cfg_name, steps, warmup, cpu_seconds):
         step(i, ev_bwd=events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    bwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / steps
+    bwd_each = sorted(e[0].elapsed_time(e[1]) for e in events)
+    bwd_ms = sum(bwd_each) / steps
 
     # Outside the timed region: the same steps again with the events around
     # the forward instead, for the per-kernel breakdown.
@@ -309,7 +310,8 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     for i in range(steps):
         step(i, ev_fwd=fwd_events[i])
     torch.cuda.synchronize()
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in fwd_events) / steps
+    fwd_each = sorted(e[0].elapsed_time(e[1]) for e in fwd_events)
+    fwd_ms = sum(fwd_each) / steps
 
     ms_per_step = wall * 1e3 / steps
     alg = cfg.algorithmic_bytes()
@@ -354,9 +356,11 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "avg_launch_ms": round(bwd_ms, 5),
         },
         "kernels": {
-            "fwd": {"avg_ms": round(fwd_ms, 5), "alg_bytes": cfg.fwd_bytes(),
+            "fwd": {"avg_ms": round(fwd_ms, 5), "median_ms": round(fwd_each[steps // 2], 5),
+                    "alg_bytes": cfg.fwd_bytes(),
                     "gbs": round(fwd_gbs, 2), "frac": round(fwd_gbs / HBM_PEAK_GBS, 4)},
-            "bwd": {"avg_ms": round(bwd_ms, 5), "alg_bytes": cfg.bwd_bytes(),
+            "bwd": {"avg_ms": round(bwd_ms, 5), "median_ms": round(bwd_each[steps // 2], 5),
+                    "alg_bytes": cfg.bwd_bytes(),
                     "gbs": round(bwd_gbs, 2), "frac": round(bwd_gbs / HBM_PEAK_GBS, 4)},
         },
         "cpu_baseline": None,
