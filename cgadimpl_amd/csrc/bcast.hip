@@ -17,15 +17,21 @@
 //
 // Forward / full-shape gradient (y (+)= a * b): one workgroup row per run of
 // the innermost output axis; its base offsets into a and b are decomposed once
-// per run, the lanes walk the run.  HBM-bound: reads a and b (b often from
-// cache), writes y.
+// per run, the lanes walk the run, 16 bytes at a time when the innermost axis
+// is contiguous or broadcast in both operands and aligned (element by element
+// otherwise).  HBM-bound: reads a and b (b often from cache), writes y.
 //
-// Reduced gradient (d[j] (+)= sum over the broadcast positions of gy * other):
-// one wave (short sums) or one 256-lane workgroup (long sums) per element of
-// d.  Lane l takes positions l, l + lanes, ... of the reduced index space in
-// row-major order and accumulates exact products in fp64; the lanes' partials
-// are combined by a fixed tree in LDS, then rounded to fp32 once.  The order
-// depends only on the shapes: results are identical run to run.
+// Reduced gradient (d[j] (+)= sum over the broadcast positions of gy * other),
+// accumulating exact products in fp64 and rounding to fp32 once, in an order
+// fixed by the shapes (results identical run to run):
+//  - the output keeps the innermost axis ([B, T, D] -> [B, 1, D]): a lane per
+//    output element, 64 consecutive ones per workgroup, each of its four waves
+//    summing a contiguous quarter of the reduced positions (loads contiguous
+//    across the lanes); the quarters are added in order;
+//  - otherwise (the innermost axis is reduced: [R, C] -> [R, 1]): one wave
+//    (short sums) or one 256-lane workgroup (long sums) per output element;
+//    lane l takes positions l, l + lanes, ... of the reduced index space in
+//    row-major order, and the lanes' partials meet in a fixed tree in LDS.
 
 #include <hip/hip_runtime.h>
 
@@ -112,15 +118,32 @@ __global__ __launch_bounds__(kBcastBlock) void bcast_reduce_kernel(
                 og += c * r.kgy[k];
                 oo += c * r.ko[k];
             }
-            for (int64_t q = lane; q < r.rtotal; q += LANES) {
-                int64_t pg = og, po = oo, qr = q;
-                for (int k = r.nr - 1; k >= 0; --k) {
-                    const int64_t c = qr % r.rsize[k];
-                    qr /= r.rsize[k];
-                    pg += c * r.rgy[k];
-                    po += c * r.ro[k];
+            // position q = oq * inner_r + i (oq over the outer reduced axes, i
+            // along the innermost one); q steps by LANES, and the outer offsets
+            // are re-derived only when i leaves the innermost axis
+            const int ia = r.nr - 1;
+            const int64_t inner_r = r.rsize[ia], sg = r.rgy[ia], so = r.ro[ia];
+            auto outer = [&](int64_t oq, int64_t& bg, int64_t& bo) {
+                bg = og;
+                bo = oo;
+                for (int k = ia - 1; k >= 0; --k) {
+                    const int64_t c = oq % r.rsize[k];
+                    oq /= r.rsize[k];
+                    bg += c * r.rgy[k];
+                    bo += c * r.ro[k];
                 }
-                acc += static_cast<double>(S::get(gy + pg)) * static_cast<double>(S::get(other + po));
+            };
+            int64_t oq = lane / inner_r, i = lane - oq * inner_r, bg, bo;
+            outer(oq, bg, bo);
+            for (int64_t q = lane; q < r.rtotal; q += LANES) {
+                acc += static_cast<double>(S::get(gy + bg + i * sg)) *
+                       static_cast<double>(S::get(other + bo + i * so));
+                i += LANES;
+                if (i >= inner_r) {
+                    oq += i / inner_r;
+                    i %= inner_r;
+                    outer(oq, bg, bo);
+                }
             }
         }
         part[threadIdx.x] = acc;
@@ -133,6 +156,123 @@ __global__ __launch_bounds__(kBcastBlock) void bcast_reduce_kernel(
         if (lane == 0 && j < n_out) {
             const double old = accumulate ? static_cast<double>(d[j]) : 0.0;
             d[j] = static_cast<float>(old + part[threadIdx.x]);
+        }
+        __syncthreads();
+    }
+}
+
+// The same product with 16-byte accesses, when the innermost axis is
+// contiguous (stride 1) or broadcast (stride 0) in both operands, its extent a
+// multiple of the slot width and every base 16-byte aligned.  A run's base
+// offsets are computed once per workgroup and a broadcast operand's value once
+// per run; the lanes walk the run's slots.  Same roundings as the element-wise
+// kernel, so the results are the same bits.
+template <class S>
+__global__ __launch_bounds__(kBcastBlock) void bcast_mul_vec_kernel(
+    const typename S::T* __restrict__ a, const typename S::T* __restrict__ b,
+    typename S::T* __restrict__ y, const BcastGeom g, int64_t runs, int accumulate) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    const int last = g.nd - 1;
+    const int64_t inner = g.size[last];
+    const int64_t nvec = inner / W;
+    const bool a_vec = g.sa[last] != 0;
+    const bool b_vec = g.sb[last] != 0;
+    for (int64_t run = blockIdx.y; run < runs; run += gridDim.y) {
+        int64_t oa = 0, ob = 0, rem = run;
+        for (int d = last - 1; d >= 0; --d) {
+            const int64_t c = rem % g.size[d];
+            rem /= g.size[d];
+            oa += c * g.sa[d];
+            ob += c * g.sb[d];
+        }
+        const T* ar = a + oa;
+        const T* br = b + ob;
+        T* yr = y + run * inner;
+        const float as = a_vec ? 0.0f : S::get(ar);
+        const float bs = b_vec ? 0.0f : S::get(br);
+        for (int64_t v = static_cast<int64_t>(blockIdx.x) * kBcastBlock + threadIdx.x; v < nvec;
+             v += static_cast<int64_t>(gridDim.x) * kBcastBlock) {
+            float fa[W], fb[W], p[W];
+            if (a_vec) {
+                S::unpack(load16<S>(ar + v * W), fa);
+            } else {
+#pragma unroll
+                for (int e = 0; e < W; ++e) fa[e] = as;
+            }
+            if (b_vec) {
+                S::unpack(load16<S>(br + v * W), fb);
+            } else {
+#pragma unroll
+                for (int e = 0; e < W; ++e) fb[e] = bs;
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) p[e] = fa[e] * fb[e];
+            if (accumulate) {
+                float old[W];
+                S::unpack(load16<S>(yr + v * W), old);
+#pragma unroll
+                for (int e = 0; e < W; ++e) p[e] = acc_add(old[e], S::stored(p[e]));
+            }
+            store16_stream<S>(yr + v * W, S::pack(p));
+        }
+    }
+}
+
+// A reduction whose output keeps the innermost axis (e.g. [B, T, D] summed to
+// [B, 1, D]): each workgroup takes 64 consecutive outputs, one per lane, so a
+// wave's loads are contiguous in gy.  The reduced index space is cut into four
+// contiguous quarters, one per wave; a wave walks its quarter along the
+// innermost reduced axis (divisions only when it moves to the next outer
+// reduced position), accumulating exact products in fp64.  The quarters'
+// partials are added in quarter order: a fixed order for the shapes.
+template <class S>
+__global__ __launch_bounds__(kBcastBlock) void bcast_reduce_cols_kernel(
+    const typename S::T* __restrict__ gy, const typename S::T* __restrict__ other,
+    float* __restrict__ d, const BcastRed r, int64_t n_out, int accumulate) {
+    __shared__ double part[4][64];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int inner_ax = r.nr - 1;
+    const int64_t inner_r = r.rsize[inner_ax];
+    const int64_t sg = r.rgy[inner_ax], so = r.ro[inner_ax];
+    const int64_t q0 = r.rtotal * w / 4, q1 = r.rtotal * (w + 1) / 4;
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * 64; base < n_out;
+         base += static_cast<int64_t>(gridDim.x) * 64) {
+        const int64_t j = base + lane;
+        double acc = 0.0;
+        if (j < n_out) {
+            int64_t og = 0, oo = 0, rem = j;
+            for (int k = r.nk - 1; k >= 0; --k) {
+                const int64_t c = rem % r.ksize[k];
+                rem /= r.ksize[k];
+                og += c * r.kgy[k];
+                oo += c * r.ko[k];
+            }
+            for (int64_t q = q0; q < q1;) {
+                const int64_t oq = q / inner_r;
+                const int64_t i0 = q - oq * inner_r;
+                int64_t pg = og, po = oo, qr = oq;
+                for (int k = inner_ax - 1; k >= 0; --k) {
+                    const int64_t c = qr % r.rsize[k];
+                    qr /= r.rsize[k];
+                    pg += c * r.rgy[k];
+                    po += c * r.ro[k];
+                }
+                const int64_t i1 = inner_r - i0 < q1 - q ? inner_r : i0 + (q1 - q);
+#pragma unroll 4
+                for (int64_t i = i0; i < i1; ++i)
+                    acc += static_cast<double>(S::get(gy + pg + i * sg)) *
+                           static_cast<double>(S::get(other + po + i * so));
+                q += i1 - i0;
+            }
+        }
+        part[w][lane] = acc;
+        __syncthreads();
+        if (w == 0 && j < n_out) {
+            const double s = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+            const double old = accumulate ? static_cast<double>(d[j]) : 0.0;
+            d[j] = static_cast<float>(old + s);
         }
         __syncthreads();
     }
@@ -226,12 +366,23 @@ int launch_bcast_mul(const void* a, const void* b, void* y, const BcastGeom& g, 
     const int64_t inner = g.size[g.nd - 1];
     int64_t runs = 1;
     for (int d = 0; d + 1 < g.nd; ++d) runs *= g.size[d];
-    const int64_t bx = (inner + kBcastBlock - 1) / kBcastBlock;
+    const int last = g.nd - 1;
+    const bool vec = inner % S::kVec == 0 && (g.sa[last] == 0 || g.sa[last] == 1) &&
+                     (g.sb[last] == 0 || g.sb[last] == 1) && aligned16(a) && aligned16(b) &&
+                     aligned16(y);
+    const int64_t per_run = vec ? inner / S::kVec : inner;
+    const int64_t bx = (per_run + kBcastBlock - 1) / kBcastBlock;
     const dim3 grid(static_cast<unsigned>(bx < 1024 ? bx : 1024),
                     static_cast<unsigned>(runs < 65535 ? runs : 65535));
-    hipLaunchKernelGGL(bcast_mul_kernel<S>, grid, dim3(kBcastBlock), 0, st,
-                       static_cast<const typename S::T*>(a), static_cast<const typename S::T*>(b),
-                       static_cast<typename S::T*>(y), g, runs, accumulate);
+    const auto* ap = static_cast<const typename S::T*>(a);
+    const auto* bp = static_cast<const typename S::T*>(b);
+    auto* yp = static_cast<typename S::T*>(y);
+    if (vec)
+        hipLaunchKernelGGL(bcast_mul_vec_kernel<S>, grid, dim3(kBcastBlock), 0, st, ap, bp, yp, g,
+                           runs, accumulate);
+    else
+        hipLaunchKernelGGL(bcast_mul_kernel<S>, grid, dim3(kBcastBlock), 0, st, ap, bp, yp, g, runs,
+                           accumulate);
     return check_launch();
 }
 
@@ -271,12 +422,19 @@ inline BcastRed make_red(int nd, const int64_t* osize, const Aligned& t, const A
 template <class S>
 int launch_bcast_reduce(const void* gy, const void* other, float* d, const BcastRed& r,
                         int64_t n_out, int accumulate, hipStream_t st) {
+    const auto* g = static_cast<const typename S::T*>(gy);
+    const auto* o = static_cast<const typename S::T*>(other);
+    if (r.nk >= 1 && r.kgy[r.nk - 1] == 1) {  // the output keeps the innermost axis
+        const int64_t blocks = (n_out + 63) / 64;
+        hipLaunchKernelGGL(bcast_reduce_cols_kernel<S>,
+                           dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),
+                           dim3(kBcastBlock), 0, st, g, o, d, r, n_out, accumulate);
+        return check_launch();
+    }
     const bool wide = r.rtotal >= 4096;
     const int per = wide ? 1 : kBcastBlock / 64;
     const int64_t blocks = (n_out + per - 1) / per;
     const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
-    const auto* g = static_cast<const typename S::T*>(gy);
-    const auto* o = static_cast<const typename S::T*>(other);
     if (wide)
         hipLaunchKernelGGL((bcast_reduce_kernel<S, kBcastBlock>), grid, dim3(kBcastBlock), 0, st,
                            g, o, d, r, n_out, accumulate);

@@ -40,6 +40,9 @@ PAIRS = [
     ((6, 700, 3), (1, 700, 1)),        # long sums for b (256-lane reduction)
     ((1, 1), (5000, 3)),               # a summed over 15000 products
     ((64, 1, 96), (64, 40, 1)),
+    ((8, 64, 96), (1, 1, 96)),         # column sums whose quarters cross outer positions
+    ((6, 5, 4, 32), (6, 1, 1, 32)),    # two reduced axes between kept ones
+    ((4, 33, 128), (4, 1, 128)),       # 16-byte forward in bf16 too
 ]
 REL = 2.0 ** -22
 
