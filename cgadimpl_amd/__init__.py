@@ -17,7 +17,9 @@ __all__ = [
     "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
     "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "rmsnorm_jvp", "layernorm_fwd",
     "layernorm_bwd", "softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
-    "logsumexp_jvp", "probe_stream", "AGK_F32", "AGK_BF16", "STATUS",
+    "logsumexp_jvp", "probe_stream", "rms_mul_bwd", "sum_rows", "linear_bf16",
+    "mul_bcast_shape", "mul_bcast_fwd", "mul_bcast_bwd",
+    "mul_bcast_grad_dtype", "gemm_f32", "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
