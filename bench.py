@@ -91,6 +91,34 @@ class TimingEvent:
             self._hip.hipEventDestroy(self._ev)
 
 
+def graph_replay_ms(body, n, reps=5):
+    """Milliseconds per body() when n calls of it are captured once into a HIP
+    graph (torch.cuda.CUDAGraph) and the graph is replayed: the GPU's time for
+    the calls without the host's per-call launch cost.  body(i, stream) issues
+    call i on `stream`.  Best of `reps` replays, timed with HIP events on the
+    replay stream after one untimed replay."""
+    import torch
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream()
+        for i in range(n):
+            body(i, cs)
+    stream = torch.cuda.current_stream()
+    graph.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = TimingEvent(), TimingEvent()
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1))
+    del graph
+    return best / n
+
+
 def _device_inputs(cfg, dev, seed):
     import torch
     gen = torch.Generator(device=dev)
@@ -275,16 +303,23 @@ def run(cfg_name, steps, warmup, cpu_seconds):
                      device=dev)
     stream = torch.cuda.current_stream()
 
-    def step(i, ev_fwd=None, ev_bwd=None):
+    def fwd(i, st):
         x, g, dy, y, inv, dx, dg = sets[i % nsets]
+        agk.rmsnorm_fwd(x, g, cfg.eps, y=y, inv_rms=inv, stream=st)
+
+    def bwd(i, st):
+        x, g, dy, y, inv, dx, dg = sets[i % nsets]
+        agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=st)
+
+    def step(i, ev_fwd=None, ev_bwd=None):
         if ev_fwd is not None:
             ev_fwd[0].record(stream)
-        agk.rmsnorm_fwd(x, g, cfg.eps, y=y, inv_rms=inv, stream=stream)
+        fwd(i, stream)
         if ev_fwd is not None:
             ev_fwd[1].record(stream)
         if ev_bwd is not None:
             ev_bwd[0].record(stream)
-        agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=stream)
+        bwd(i, stream)
         if ev_bwd is not None:
             ev_bwd[1].record(stream)
 
@@ -312,6 +347,14 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     torch.cuda.synchronize()
     fwd_each = sorted(e[0].elapsed_time(e[1]) for e in fwd_events)
     fwd_ms = sum(fwd_each) / steps
+
+    # Also outside it: the same calls captured once into HIP graphs and
+    # replayed, the GPU's own time for them.  At the small configurations a
+    # call launched from Python costs the host longer than its kernels take,
+    # so the eager step above is the host's launch rate there, not the GPU's.
+    graph_step_ms = graph_replay_ms(lambda i, st: (fwd(i, st), bwd(i, st)), steps)
+    graph_fwd_ms = graph_replay_ms(fwd, steps)
+    graph_bwd_ms = graph_replay_ms(bwd, steps)
 
     ms_per_step = wall * 1e3 / steps
     alg = cfg.algorithmic_bytes()
@@ -362,6 +405,16 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "bwd": {"avg_ms": round(bwd_ms, 5), "median_ms": round(bwd_each[steps // 2], 5),
                     "alg_bytes": cfg.bwd_bytes(),
                     "gbs": round(bwd_gbs, 2), "frac": round(bwd_gbs / HBM_PEAK_GBS, 4)},
+        },
+        "graph": {
+            "how": (f"the {steps} steps (then {steps} forwards, then {steps} backwards) "
+                    "captured once into a HIP graph and replayed, best of 5 replays: the "
+                    "GPU's time without the host's per-call launch cost"),
+            "ms_per_step": round(graph_step_ms, 5),
+            "gbs": round(alg / (graph_step_ms * 1e-3) / 1e9, 2),
+            "pct_of_hbm_peak": round(100.0 * alg / (graph_step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "fwd_ms": round(graph_fwd_ms, 5),
+            "bwd_ms": round(graph_bwd_ms, 5),
         },
         "cpu_baseline": None,
     }

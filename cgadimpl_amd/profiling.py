@@ -293,6 +293,11 @@ def write_mfma_summary(counter_csv, out_md, command, simds=1024, clock_ghz=2.4):
         fh.write("\n".join(lines) + "\n")
 
 
+def _cfg_label(r):
+    return (f"{r['config']['workload'].split(':')[0]} {r['config']['rows']}x"
+            f"{r['config']['cols']} {r['dtype']}")
+
+
 def write_bench_summary(jsonl, out_md, command):
     """Tables of bench.py's JSON lines (RMSNorm configurations, c5, row ops)."""
     recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith("{")]
@@ -310,8 +315,7 @@ def write_bench_summary(jsonl, out_md, command):
             k = r["kernels"]
             cpu = r.get("cpu_baseline") or {}
             one = (cpu.get("modes") or {}).get("single_thread") or {}
-            lines.append(f"| {r['config']['workload'].split(':')[0]} {r['config']['rows']}x"
-                         f"{r['config']['cols']} {r['dtype']} | {r['value']:.0f} | "
+            lines.append(f"| {_cfg_label(r)} | {r['value']:.0f} | "
                          f"{100 * r['value'] / 8000:.1f} | {1e3 * r['ms_per_step']:.1f} | "
                          f"{1e3 * k['fwd']['avg_ms']:.1f} | "
                          f"{100 * k['fwd']['frac']:.1f} | {1e3 * k['bwd']['avg_ms']:.1f} | "
@@ -319,6 +323,21 @@ def write_bench_summary(jsonl, out_md, command):
                          f"{cpu.get('value', '-')} ({cpu.get('cores', '-')}) | "
                          f"{one.get('gbs', '-')} |")
         lines.append("")
+        graphed = [r for r in norm if r.get("graph")]
+        if graphed:
+            lines += ["The same calls captured once into a HIP graph and replayed (best of 5 "
+                      "replays of the timed number of steps): the GPU's own time, without the "
+                      "host's cost of launching each call from Python. Where the two tables "
+                      "differ, the eager step above is bound by the host's launch rate.", "",
+                      "| config | step us | GB/s | % of peak | fwd us | bwd us | fwd+bwd us "
+                      "(separate graphs) |", "|---|---|---|---|---|---|---|"]
+            for r in graphed:
+                gr = r["graph"]
+                lines.append(f"| {_cfg_label(r)} | {1e3 * gr['ms_per_step']:.1f} | "
+                             f"{gr['gbs']:.0f} | {gr['pct_of_hbm_peak']:.1f} | "
+                             f"{1e3 * gr['fwd_ms']:.1f} | {1e3 * gr['bwd_ms']:.1f} | "
+                             f"{1e3 * (gr['fwd_ms'] + gr['bwd_ms']):.1f} |")
+            lines.append("")
         hosts = {json.dumps(r["cpu_baseline"]["host"], sort_keys=True) for r in norm
                  if r.get("cpu_baseline") and r["cpu_baseline"].get("host")}
         for h in hosts:
