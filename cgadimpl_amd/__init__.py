@@ -32,6 +32,7 @@ AGK_BF16 = 1
 AGK_ACCUM_DX = 1
 AGK_ACCUM_DGAMMA = 2
 AGK_ACCUM_ALL = 3
+AGK_WIDE_MIN_COLS = 16385  # rows this wide and wider can take the split paths
 STATUS = {0: "AGK_OK", 1: "AGK_EINVAL", 2: "AGK_EDTYPE", 3: "AGK_EWORKSPACE", 4: "AGK_EHIP"}
 
 # Every symbol include/agk_rmsnorm.h and include/agk_rowops.h declare, with its
@@ -214,8 +215,11 @@ def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate=False,
         dx = torch.empty_like(x) if not acc & AGK_ACCUM_DX else torch.zeros_like(x)
     if want_dgamma and dgamma is None:
         dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
-    ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols) if dgamma is not None else 0
-    if dgamma is not None and workspace is None and ws_bytes:
+    # a workspace is required for dgamma, and lets dx alone take the split
+    # path on wide rows
+    wants_ws = dgamma is not None or cols >= AGK_WIDE_MIN_COLS
+    ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols) if wants_ws else 0
+    if wants_ws and workspace is None and ws_bytes:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     ws_have = workspace.numel() * workspace.element_size() if workspace is not None else 0
     rc = lib().agk_rmsnorm_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(dy), _ptr(dx),
@@ -290,7 +294,11 @@ def gemm_f32(a, b, c=None, trans_a: bool = False, trans_b: bool = False, accumul
 
 
 def launch_plan(rows: int, cols: int, dtype: int, backward: bool) -> dict:
-    """The launch shape agk_rmsnorm_{fwd,bwd} picks for these sizes (diagnostic)."""
+    """The launch shape agk_rmsnorm_{fwd,bwd} picks for these sizes (diagnostic).
+
+    tpr == 0 with nv > 0 is the split path: nv segments and g chunks per
+    row, rpb rows per backward tile, nblk dgamma partial rows (0: the tiles
+    write dgamma directly)."""
     out = (ctypes.c_int32 * 5)()
     _check(lib().agk_rmsnorm_launch_plan(rows, cols, dtype, int(bool(backward)), out),
            "agk_rmsnorm_launch_plan")
@@ -347,7 +355,8 @@ def rms_mul_bwd(x, gamma, inv_rms, gy, dx=None, dgamma=None, accumulate=False,
     if want_dgamma and dgamma is None:
         dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
     ws = None
-    ws_bytes = int(lib().agk_rmsnorm_bwd_workspace_bytes(rows, cols)) if dgamma is not None else 0
+    wants_ws = dgamma is not None or cols >= AGK_WIDE_MIN_COLS  # as rmsnorm_bwd
+    ws_bytes = int(lib().agk_rmsnorm_bwd_workspace_bytes(rows, cols)) if wants_ws else 0
     if ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     rc = lib().agk_rms_mul_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(gy), _ptr(dr), _ptr(dx),

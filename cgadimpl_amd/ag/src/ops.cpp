@@ -384,10 +384,18 @@ void vjp_RMSNorm(Node* n, const Tensor& gy) {
     GradLocks lock(X, nullptr);
     bool acc = false;
     Tensor& dx = X->grad_for_write(x.dtype(), &acc);
+    // no dgamma, so no workspace is required; wide rows take the split path
+    // with one
+    std::unique_ptr<Storage> ws;
+    size_t ws_bytes = 0;
+    if (x.cols() >= AGK_WIDE_MIN_COLS) {
+        ws_bytes = agk_rmsnorm_bwd_workspace_bytes(x.rows(), x.cols());
+        ws = std::make_unique<Storage>(ws_bytes, current_stream());
+    }
     agk_check(agk_rmsnorm_bwd(x.data(), nullptr, static_cast<const float*>(inv.data()), gy.data(),
-                              dx.data(), nullptr, nullptr, 0, x.rows(), x.cols(),
-                              agk_dtype_of(x.dtype()), acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE,
-                              stream_arg()),
+                              dx.data(), nullptr, ws ? ws->data() : nullptr, ws_bytes, x.rows(),
+                              x.cols(), agk_dtype_of(x.dtype()),
+                              acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE, stream_arg()),
               "vjp_RMSNorm");
 }
 
@@ -457,6 +465,10 @@ static bool vjp_mul_of_rms(Node* F, Node* Rw, const Tensor& gy, bool want_row) {
     if (want_row) {
         drow = static_cast<float*>(Rw->grad_for_write(Dtype::Float32, &a).data());
         if (a) acc |= AGK_ACCUM_DGAMMA;
+    }
+    // a workspace for the row gradient, and for wide rows (the split path,
+    // as vjp_RMSNorm takes it)
+    if (want_row || x.cols() >= AGK_WIDE_MIN_COLS) {
         ws_bytes = agk_rmsnorm_bwd_workspace_bytes(x.rows(), x.cols());
         ws = std::make_unique<Storage>(ws_bytes, current_stream());
     }

@@ -752,7 +752,7 @@ __global__ __launch_bounds__(kBlock) void rms_bwd_looped(
             }
             if (prow) {
                 const float t = d * (dr ? S::stored(xv * r) : xv * r);
-                prow[c] = first ? t : prow[c] + t;
+                prow[c] = first ? t : acc_add(prow[c], t);
             }
         }
     }
@@ -857,7 +857,7 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
                         for (int e = 0; e < W; ++e) t[e] = g[e];
                     }
 #pragma unroll
-                    for (int e = 0; e < W; ++e) prow[c + e] = first ? t[e] : prow[c + e] + t[e];
+                    for (int e = 0; e < W; ++e) prow[c + e] = first ? t[e] : acc_add(prow[c + e], t[e]);
                 }
             }
         }
@@ -875,7 +875,7 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
             }
             if (prow) {  // a == nullptr: column sums of gy
                 const float t = a ? g * S::get(a + off + c) : g;
-                prow[c] = first ? t : prow[c] + t;
+                prow[c] = first ? t : acc_add(prow[c], t);
             }
         }
     }
@@ -961,6 +961,7 @@ __global__ __launch_bounds__(kBlock) void fill_zero_f32(float* __restrict__ p, i
     if (i < n) p[i] = 0.0f;
 }
 
+
 // (TPR, NV, G, register sets).  Every shape is a 1024-lane workgroup (TPR * G =
 // 1024).  Rows of up to 1024 slots take one slot per lane (TPR = the width
 // rounded up to a power of two, G = 1024 / TPR rows per step); wider rows take
@@ -1033,6 +1034,8 @@ inline int64_t bwd_num_blocks(int64_t rows) {
     return (rows + rpb - 1) / rpb;
 }
 
+#include "rmsnorm_wide.hpp"
+
 template <class S>
 int launch_fwd_plan(const Plan& p, const void* x, const void* gamma, void* y, float* inv_rms,
                     int64_t rows, int cols, float eps, hipStream_t st) {
@@ -1066,6 +1069,8 @@ int launch_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_
                      (gamma == nullptr || aligned16(gamma));
     Plan p;
     if (vec) p = fwd_plan(cols / S::kVec, rows);
+    if (wide_fwd_eligible<S>(x, gamma, y, rows, cols, p.tpr != 0))
+        return launch_wide_fwd<S>(x, gamma, y, inv_rms, rows, cols, eps, st);
     return launch_fwd_plan<S>(p, x, gamma, y, inv_rms, rows, cols, eps, st);
 }
 
@@ -1343,11 +1348,36 @@ inline size_t bwd_partials_bytes(const void* x, const void* gamma, const void* d
     return static_cast<size_t>(nblk) * static_cast<size_t>(cols) * sizeof(float);
 }
 
-// The RMSNorm backward with validated arguments and dgamma partials at
-// `partials` (which must hold bwd_partials_bytes when dgamma != NULL).
+// Whether the backward takes the wide path for these arguments, given a
+// 16-byte aligned workspace of at least wide_ws_bytes(rows, cols, false).
+template <class S>
+inline bool bwd_wide_possible(const void* x, const void* gamma, const void* dy, const void* dx,
+                              int64_t rows, int cols) {
+    int64_t nblk = 0, rpb = 0;
+    const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    return wide_bwd_eligible<S>(x, gamma, dy, dx, cols, p.tpr != 0);
+}
+inline bool bwd_takes_wide(const void* x, const void* gamma, const void* dy, const void* dx,
+                           int64_t rows, int cols, int dtype, const void* ws, size_t ws_bytes) {
+    if (!ws || !aligned16(ws) || ws_bytes < wide_ws_bytes(rows, cols, false)) return false;
+    return dtype == AGK_F32 ? bwd_wide_possible<F32>(x, gamma, dy, dx, rows, cols)
+                            : bwd_wide_possible<BF16>(x, gamma, dy, dx, rows, cols);
+}
+
+// The RMSNorm backward with validated arguments.  Rows too wide for the
+// resident shapes take the wide path when `ws` (16-byte aligned, ws_bytes
+// long) holds wide_ws_bytes(rows, cols, false); otherwise dgamma partials go
+// to `partials` (which must hold bwd_partials_bytes when dgamma != NULL).
 inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rms,
-                           const void* dy, void* dx, float* dgamma, float* partials, int64_t rows,
-                           int cols, int dtype, int acc_dx, int acc_dg, hipStream_t st) {
+                           const void* dy, void* dx, float* dgamma, float* partials, void* ws,
+                           size_t ws_bytes, int64_t rows, int cols, int dtype, int acc_dx,
+                           int acc_dg, hipStream_t st) {
+    if (bwd_takes_wide(x, gamma, dy, dx, rows, cols, dtype, ws, ws_bytes))
+        return dtype == AGK_F32
+                   ? launch_wide_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, dgamma, ws, rows,
+                                          cols, acc_dx, acc_dg, st)
+                   : launch_wide_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, dgamma, ws, rows,
+                                           cols, acc_dx, acc_dg, st);
     int64_t nblk = 0;
     int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, partials,
                                                 dgamma, rows, cols, acc_dx, acc_dg, st, nblk)
@@ -1428,7 +1458,12 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms, i
 
 size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
     if (agk::check_sizes(rows, cols) != AGK_OK || rows == 0 || cols == 0) return 0;
-    return static_cast<size_t>(agk::bwd_num_blocks(rows)) * static_cast<size_t>(cols) * 4u;
+    const size_t looped =
+        static_cast<size_t>(agk::bwd_num_blocks(rows)) * static_cast<size_t>(cols) * 4u;
+    const size_t wide = agk::wide_ws_bytes(rows, cols, false);
+    const size_t comp = agk::wide_ws_bytes(rows, cols, true);
+    const size_t split = wide > comp ? wide : comp;
+    return split > looped ? split : looped;
 }
 
 int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
@@ -1455,8 +1490,9 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms, cons
         if (!workspace || workspace_bytes < need) return AGK_EWORKSPACE;
         partials = static_cast<float*>(workspace);
     }
-    return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, partials, rows,
-                           static_cast<int>(cols), dtype, acc_dx, acc_dg, st);
+    return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, partials, workspace,
+                           workspace ? workspace_bytes : 0, rows, static_cast<int>(cols), dtype,
+                           acc_dx, acc_dg, st);
 }
 
 int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_rms,
@@ -1477,6 +1513,18 @@ int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_r
     if (!x || !inv_rms || !dy) return AGK_EINVAL;
     if (!dx && !dgamma) return AGK_OK;  // nothing requested
     const int c = static_cast<int>(cols);
+    // Rows too wide for the resident shapes: the wide path with the scratch
+    // array as its workspace, as agk_rmsnorm_bwd takes it with the workspace
+    // agk_rmsnorm_bwd_workspace_bytes asks for.
+    const bool wide = dtype == AGK_F32 ? bwd_wide_possible<F32>(x, gamma, dy, dx, rows, c)
+                                       : bwd_wide_possible<BF16>(x, gamma, dy, dx, rows, c);
+    if (wide) {
+        if (wide_ws_bytes(rows, c, false) > AGK_NOALLOC_SCRATCH_BYTES) return AGK_EWORKSPACE;
+        float* ws = nullptr;
+        if (int rc = scratch_on_device(st, &ws)) return rc;
+        return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, ws, ws,
+                               AGK_NOALLOC_SCRATCH_BYTES, rows, c, dtype, acc_dx, acc_dg, st);
+    }
     float* partials = nullptr;
     if (dgamma) {
         const size_t need = dtype == AGK_F32 ? bwd_partials_bytes<F32>(x, gamma, dy, dx, rows, c)
@@ -1486,8 +1534,8 @@ int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_r
             if (int rc = scratch_on_device(st, &partials)) return rc;
         }
     }
-    return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, partials, rows, c, dtype, acc_dx,
-                           acc_dg, st);
+    return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, partials, nullptr, 0, rows, c,
+                           dtype, acc_dx, acc_dg, st);
 }
 
 int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms, const void* gy,
@@ -1513,6 +1561,16 @@ int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms, cons
         partials = static_cast<float*>(workspace);
     }
     const int c = static_cast<int>(cols);
+    // Rows too wide for the resident shapes, with a workspace: the split
+    // path, whose outputs are the two separate calls' on their split paths.
+    if (workspace && aligned16(workspace) && aligned16(dr) &&
+        workspace_bytes >= wide_ws_bytes(rows, c, true) &&
+        (dtype == AGK_F32 ? bwd_wide_possible<F32>(x, gamma, gy, dx, rows, c)
+                          : bwd_wide_possible<BF16>(x, gamma, gy, dx, rows, c)))
+        return dtype == AGK_F32 ? launch_wide_bwd<F32>(x, gamma, inv_rms, gy, dx, dr, dgamma,
+                                                       workspace, rows, c, acc_dx, acc_dg, st)
+                                : launch_wide_bwd<BF16>(x, gamma, inv_rms, gy, dx, dr, dgamma,
+                                                        workspace, rows, c, acc_dx, acc_dg, st);
     int64_t nblk = 0;
     int rc = dtype == AGK_F32 ? launch_bwd<F32>(x, gamma, inv_rms, gy, dx, dr, partials, dgamma,
                                                 rows, c, acc_dx, acc_dg, st, nblk)
@@ -1688,6 +1746,23 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
     plan[2] = p.g;
     plan[3] = static_cast<int32_t>(rpb);
     plan[4] = static_cast<int32_t>(nblk);
+    if (p.tpr == 0 && cols > 0 && cols <= 0x7fffffffLL) {
+        // aligned stand-in pointers, and for the forward a y apart from x
+        const void* a = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+        const int c = static_cast<int>(cols);
+        const bool split =
+            backward ? (dtype == AGK_F32 ? wide_bwd_eligible<F32>(a, a, a, a, c, false)
+                                         : wide_bwd_eligible<BF16>(a, a, a, a, c, false))
+                     : (dtype == AGK_F32 ? wide_fwd_shape_ok<F32>(rows, c, false)
+                                         : wide_fwd_shape_ok<BF16>(rows, c, false));
+        if (split) {
+            const WidePlan w = wide_plan(rows, c);
+            plan[1] = static_cast<int32_t>(w.nseg);
+            plan[2] = static_cast<int32_t>(w.nch);
+            plan[3] = backward ? static_cast<int32_t>(w.rb) : 0;
+            plan[4] = backward && w.nrb > 1 ? static_cast<int32_t>(w.nrb) : 0;
+        }
+    }
     return AGK_OK;
 }
 

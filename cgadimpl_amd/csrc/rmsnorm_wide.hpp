@@ -1,0 +1,529 @@
+// rmsnorm_wide.hpp -- the RMSNorm forward and backward for rows wider than the
+// register-resident shapes hold (more than 4096 16-byte slots: 16384 fp32 or
+// 32768 bf16 columns; 16384 bf16 columns and up for the backward), with every
+// row 16-byte aligned.  Included by rmsnorm.hip inside namespace agk.
+//
+// A row is cut into segments of kWideSegCols columns for its statistics and
+// into chunks of kWideChunkCols columns for the element-wise pass, so a few
+// long rows still spread over the whole GPU:
+//
+//   forward   wide_row_stats<S, kWideSumSq>  per (row, segment): sum of x^2
+//             wide_row_finish<kWideSumSq>    per row: partials in segment
+//                                            order -> inv_rms[row]
+//             wide_fwd_scale<S>              per (row, chunk): y = (x*r)*gamma
+//   backward  wide_row_stats<S, kWideDot>    per (row, segment): sum of g*x,
+//                                            g = dy*gamma          (dx only)
+//             wide_row_finish<kWideDot>      per row: s = r*r*dot/cols
+//             wide_bwd_tiles<S, ACC>         per (row block, chunk): dx =
+//                                            r*(g - x*s) and one fp32 dgamma
+//                                            partial row per row block
+//             dgamma_finalize                partial rows in fixed fp64 order
+//                                            (more than one row block only)
+//
+// The formulas are the resident kernels' (same products, same association);
+// only the order of the row sums differs (segment trees summed in segment
+// order), and it depends only on cols.  Every launch shape depends only on
+// rows and cols, so results are bit-identical run to run.
+//
+// The composition rms(x) * gamma (COMP: agk_rms_mul_bwd) runs the same
+// kernels with g = gy*gamma rounded to storage (and written to dr) and the
+// dgamma term gy * h, h = x*r rounded to storage.  Its dx is then the plain
+// path's dx of dr with no gamma, and its tiles take the looped kernels' row
+// blocking (bwd_rows_per_block), so its dgamma partial rows are the ones
+// agk_mul_rowbcast_bwd writes for gy and h: both outputs bit-identical to the
+// two calls it replaces.
+//
+// Scratch: the forward keeps its per-segment partial sums in the first
+// nseg * 4 bytes of each row of y (y is written in full by the last kernel;
+// x and y must not overlap -- the caller checks and takes the one-workgroup-
+// per-row kernel when they do).  The backward keeps its partials and per-row
+// coefficients in the caller's workspace (wide_ws_layout).
+
+constexpr int kWideLanes = 256;         // lanes per workgroup of every wide kernel
+constexpr int kWideSegCols = 4096;      // columns per segment of the row statistics
+constexpr int kWideChunkCols = 2048;    // columns per chunk of the element-wise pass
+constexpr int64_t kWideTiles = 2048;    // backward tiles aimed for (8 per CU)
+constexpr int64_t kWideFwdRowsMax = 1023;  // forward: more rows fill the GPU one per workgroup
+constexpr int kWideMinCols = 16385;     // narrowest row the wide paths take (either dtype)
+constexpr int kWideSumSq = 0;
+constexpr int kWideDot = 1;
+constexpr int kWideDotComp = 2;  // g rounded to storage (the composition)
+
+inline int launch_finalize(const float* partials, float* dgamma, int64_t nblk, int cols,
+                           int accumulate, hipStream_t st);
+
+struct WidePlan {
+    int64_t nseg = 0;  // segments per row
+    int64_t nch = 0;   // chunks per row
+    int64_t rb = 0;    // rows per backward tile
+    int64_t nrb = 0;   // backward row blocks = dgamma partial rows
+};
+
+// Depends only on rows and cols (never on the dtype or the device), so the
+// workspace size and the dgamma summation order are fixed by the shape.
+inline WidePlan wide_plan(int64_t rows, int cols) {
+    WidePlan p;
+    p.nseg = (cols + kWideSegCols - 1) / kWideSegCols;
+    p.nch = (cols + kWideChunkCols - 1) / kWideChunkCols;
+    int64_t nrb = (kWideTiles + p.nch - 1) / p.nch;
+    if (nrb > rows) nrb = rows;
+    if (nrb < 1) nrb = 1;
+    p.rb = (rows + nrb - 1) / nrb;
+    p.nrb = (rows + p.rb - 1) / p.rb;
+    return p;
+}
+
+inline size_t round256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// Row blocking of the wide tiles: the plan's for the RMSNorm backward, the
+// looped kernels' for the composition (see above).
+inline void wide_blocking(int64_t rows, int cols, bool comp, int64_t& rb, int64_t& nrb) {
+    if (comp) {
+        rb = bwd_rows_per_block(rows);
+        nrb = bwd_num_blocks(rows);
+    } else {
+        const WidePlan p = wide_plan(rows, cols);
+        rb = p.rb;
+        nrb = p.nrb;
+    }
+}
+
+// Workspace layout of the wide backward: [dgamma partial rows: prows x cols
+// fp32] [segment partials: rows x nseg fp32] [coefficients: rows fp32], each
+// region 256-byte aligned.
+struct WideWs {
+    size_t partials = 0, segs = 0, coefs = 0, total = 0;
+};
+inline WideWs wide_ws_layout(int64_t rows, int cols, int64_t prows) {
+    const WidePlan p = wide_plan(rows, cols);
+    WideWs w;
+    w.partials = 0;
+    w.segs = round256(static_cast<size_t>(prows) * static_cast<size_t>(cols) * 4u);
+    w.coefs = w.segs + round256(static_cast<size_t>(rows) * static_cast<size_t>(p.nseg) * 4u);
+    w.total = w.coefs + round256(static_cast<size_t>(rows) * 4u);
+    return w;
+}
+inline WideWs wide_ws_layout(int64_t rows, int cols, bool comp) {
+    int64_t rb = 0, nrb = 0;
+    wide_blocking(rows, cols, comp, rb, nrb);
+    return wide_ws_layout(rows, cols, nrb);
+}
+// Bytes the wide backward (comp false) or the composition (comp true) needs.
+inline size_t wide_ws_bytes(int64_t rows, int64_t cols, bool comp) {
+    if (cols < kWideMinCols || rows <= 0) return 0;
+    return wide_ws_layout(rows, static_cast<int>(cols), comp).total;
+}
+
+// Per (row, segment): the segment's sum of x^2 (kWideSumSq) or of g*x with
+// g = dy*gamma (kWideDot; kWideDotComp: g rounded to storage, gamma
+// required), summed per lane over its slots in order, then over the wave's
+// lanes (DPP tree) and the four waves in order.  Blocks are row-major over
+// (row, segment).  Loads past the row end return zeros.
+template <class S, int KIND>
+__global__ __launch_bounds__(kWideLanes) void wide_row_stats(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ dy,
+    const typename S::T* __restrict__ gamma, float* __restrict__ out, int64_t out_row_stride,
+    int64_t rows, int cols, int64_t nseg) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    constexpr int NV = kWideSegCols / (W * kWideLanes);  // slots per lane
+    __shared__ float red[2][kWideLanes / 64];
+    const int64_t row = static_cast<int64_t>(blockIdx.x) / nseg;
+    const int seg = static_cast<int>(static_cast<int64_t>(blockIdx.x) - row * nseg);
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    const rsrc_t rx = make_rsrc(x + row * static_cast<int64_t>(cols), row_bytes);
+    const rsrc_t rd = make_rsrc(KIND != kWideSumSq ? dy + row * static_cast<int64_t>(cols) : x,
+                                KIND != kWideSumSq ? row_bytes : 0u);
+    const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
+    uint32_t off[NV];
+    u32x4 xv[NV], dv[NV], gv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = seg * kWideSegCols + (static_cast<int>(threadIdx.x) + k * kWideLanes) * W;
+        off[k] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+        xv[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off[k], 0, 0);
+        if constexpr (KIND != kWideSumSq) {
+            dv[k] = __builtin_amdgcn_raw_buffer_load_b128(rd, off[k], 0, 0);
+            if (gamma) gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[k], 0, 0);
+        }
+    }
+    float part[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) part[e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        float fx[W];
+        S::unpack(xv[k], fx);
+        if constexpr (KIND == kWideSumSq) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[e] += fx[e] * fx[e];
+        } else {
+            float fd[W];
+            S::unpack(dv[k], fd);
+            if constexpr (KIND == kWideDotComp) {
+                float gm[W];
+                u32x4 q;
+                S::unpack(gv[k], gm);
+                stored_product<S>(fd, gm, q);
+            } else if (gamma) {
+                float gm[W];
+                S::unpack(gv[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
+        }
+    }
+    float v = 0.0f;
+#pragma unroll
+    for (int e = 0; e < W; ++e) v += part[e];
+    v = row_sum<kWideLanes, 1>(v, red, 0);
+    if (threadIdx.x == 0) out[row * out_row_stride + seg] = v;
+    (void)rows;
+}
+
+// Per row: the segment partials added in segment order, then
+//   kWideSumSq: out[row] = 1/sqrt(sum/cols + eps)            (inv_rms)
+//   kWideDot:   out[row] = (r*r*dot) * (1/cols), r = inv_rms[row]
+template <int KIND>
+__global__ __launch_bounds__(kWideLanes) void wide_row_finish(
+    const float* __restrict__ partials, int64_t part_row_stride, const float* __restrict__ inv_rms,
+    float* __restrict__ out, int64_t rows, int cols, int64_t nseg, float eps) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWideLanes + threadIdx.x;
+    if (row >= rows) return;
+    const float* p = partials + row * part_row_stride;
+    float v = 0.0f;
+    for (int64_t s = 0; s < nseg; ++s) v += p[s];
+    if constexpr (KIND == kWideSumSq) {
+        out[row] = 1.0f / sqrtf(v / static_cast<float>(cols) + eps);
+        (void)inv_rms;
+    } else {
+        (void)eps;
+        const float r = inv_rms[row];
+        out[row] = (r * r * v) * (1.0f / static_cast<float>(cols));
+    }
+}
+
+// Per (row, chunk): y = (x * r) * gamma (x * r without gamma), as the resident
+// forward computes it.  Blocks are row-major over (row, chunk).
+template <class S>
+__global__ __launch_bounds__(kWideLanes) void wide_fwd_scale(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, typename S::T* __restrict__ y, int64_t rows, int cols,
+    int64_t nch) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    constexpr int NV = kWideChunkCols / (W * kWideLanes);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) / nch;
+    const int ch = static_cast<int>(static_cast<int64_t>(blockIdx.x) - row * nch);
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    const rsrc_t rx = make_rsrc(x + row * static_cast<int64_t>(cols), row_bytes);
+    const rsrc_t ry = make_rsrc(y + row * static_cast<int64_t>(cols), row_bytes);
+    const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
+    const float r = inv_rms[row];
+    uint32_t off[NV];
+    u32x4 xv[NV], gv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = ch * kWideChunkCols + (static_cast<int>(threadIdx.x) + k * kWideLanes) * W;
+        off[k] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+        xv[k] = bload16_stream(rx, off[k]);
+        if (gamma) gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[k], 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        float f[W];
+        S::unpack(xv[k], f);
+        if (gamma) {
+            float gm[W];
+            S::unpack(gv[k], gm);
+#pragma unroll
+            for (int e = 0; e < W; ++e) f[e] = (f[e] * r) * gm[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < W; ++e) f[e] = f[e] * r;
+        }
+        bstore16_stream(ry, off[k], S::pack(f));
+    }
+    (void)rows;
+}
+
+// Per (row block, chunk): rows rb*RB .. of the block in order, each
+//   g = dy*gamma, dx (+)= r*(g - x*s)     (s from wide_row_finish<kWideDot>)
+// and each lane's dgamma terms dy*(x*r) added row by row in fp32, as the
+// resident backward does (COMP: g rounded to storage and written to dr, the
+// dgamma term dy*h with h = x*r rounded to storage).  The block's sums go to partial row rb (nrb > 1) or
+// straight to dgamma (one row block: dgamma (+)= the sums).  The next row's
+// slots are loaded while the current row is processed (a row past the block
+// reads through a zero-size resource and returns zeros).  Blocks are
+// row-major over (row block, chunk).  coefs == nullptr: no dx.
+template <class S, bool ACC, bool COMP>
+__global__ __launch_bounds__(kWideLanes) void wide_bwd_tiles(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr,
+    const float* __restrict__ coefs, float* __restrict__ partials, float* __restrict__ dgamma,
+    int64_t rows, int cols, int64_t nch, int64_t rb, int64_t nrb, int acc_dg) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    constexpr int NV = kWideChunkCols / (W * kWideLanes);
+    const int64_t blk = static_cast<int64_t>(blockIdx.x) / nch;
+    const int ch = static_cast<int>(static_cast<int64_t>(blockIdx.x) - blk * nch);
+    const int64_t r0 = blk * rb;
+    const int64_t r1 = r0 + rb < rows ? r0 + rb : rows;
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    const bool want_dx = coefs != nullptr;
+    uint32_t off[NV];
+    u32x4 gv[NV];
+    const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = ch * kWideChunkCols + (static_cast<int>(threadIdx.x) + k * kWideLanes) * W;
+        off[k] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+        gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[k], 0, 0);
+    }
+    float dg[NV][W];
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < W; ++e) dg[k][e] = 0.0f;
+
+    struct Set {
+        u32x4 xv[NV], dv[NV], ov[NV];
+        float r, s;
+    };
+    auto issue = [&](Set& b, int64_t row) {
+        const uint32_t n = row < r1 ? 1u : 0u;
+        const int64_t rr = row < r1 ? row : r0;
+        const int64_t e0 = rr * static_cast<int64_t>(cols);
+        const rsrc_t rx = make_rsrc(x + e0, n * row_bytes);
+        const rsrc_t rd = make_rsrc(dy + e0, n * row_bytes);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            b.xv[k] = bload16_stream(rx, off[k]);
+            b.dv[k] = bload16_stream(rd, off[k]);
+        }
+        if constexpr (ACC) {
+            const rsrc_t ro = make_rsrc(dx ? dx + e0 : dx, dx ? n * row_bytes : 0u);
+#pragma unroll
+            for (int k = 0; k < NV; ++k) b.ov[k] = bload16_stream(ro, off[k]);
+        }
+        b.r = inv_rms[rr];
+        b.s = want_dx ? coefs[rr] : 0.0f;
+    };
+    Set cur, nxt;
+    issue(cur, r0);
+    for (int64_t row = r0; row < r1; ++row) {
+        issue(nxt, row + 1);
+        const float r = cur.r, s = cur.s;
+        const rsrc_t rdx = make_rsrc(dx ? dx + row * static_cast<int64_t>(cols) : dx,
+                                     (dx && want_dx) ? row_bytes : 0u);
+        const rsrc_t rdr = make_rsrc(COMP ? dr + row * static_cast<int64_t>(cols) : dr,
+                                     COMP ? row_bytes : 0u);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fx[W], fd[W], gk[W];
+            S::unpack(cur.xv[k], fx);
+            S::unpack(cur.dv[k], fd);
+            if constexpr (COMP) {
+                float gm[W];
+                u32x4 q;
+                S::unpack(gv[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) gk[e] = fd[e];
+                stored_product<S>(gk, gm, q);
+                bstore16_stream(rdr, off[k], q);
+            } else if (gamma) {
+                float gm[W];
+                S::unpack(gv[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) gk[e] = fd[e] * gm[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < W; ++e) gk[e] = fd[e];
+            }
+            if (want_dx) {
+                float o[W];
+#pragma unroll
+                for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * s);
+                if constexpr (ACC) {
+                    float old[W];
+                    S::unpack(cur.ov[k], old);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) o[e] = acc_add(old[e], o[e]);
+                }
+                bstore16_stream(rdx, off[k], S::pack(o));
+            }
+            if constexpr (COMP) {
+                // as agk_mul_rowbcast_bwd's looped kernel: the product, then
+                // an unfused add (the first row's term taken as it is)
+                float h[W];
+#pragma unroll
+                for (int e = 0; e < W; ++e) h[e] = fx[e] * r;
+                S::unpack(S::pack(h), h);
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const float t = fd[e] * h[e];
+                    dg[k][e] = row == r0 ? t : acc_add(dg[k][e], t);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < W; ++e) dg[k][e] += fd[e] * (fx[e] * r);
+            }
+        }
+        cur = nxt;
+    }
+    if (partials == nullptr && dgamma == nullptr) return;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        if (off[k] == kOffOut) continue;
+        const int col = static_cast<int>(off[k] / sizeof(T));
+        if (nrb > 1) {
+            float* p = partials + blk * static_cast<int64_t>(cols) + col;
+#pragma unroll
+            for (int e = 0; e < W; e += 4)
+                *reinterpret_cast<float4*>(p + e) =
+                    make_float4(dg[k][e], dg[k][e + 1], dg[k][e + 2], dg[k][e + 3]);
+        } else {
+            // +0.0 + sum, as the finalize's fp64 sum from +0.0 gives it (a
+            // lone -0.0 term becomes +0.0)
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const float v = 0.0f + dg[k][e];
+                dgamma[col + e] = acc_dg ? dgamma[col + e] + v : v;
+            }
+        }
+    }
+}
+
+// A row of cols elements the wide kernels can take: a multiple of the slot
+// width, at least kWideMinCols, and short enough for 32-bit buffer offsets.
+template <class S>
+inline bool wide_cols_ok(int cols) {
+    return cols >= kWideMinCols && (cols % S::kVec) == 0 &&
+           static_cast<uint64_t>(cols) * sizeof(typename S::T) < 0x80000000ull;
+}
+
+// Whether [a, a+bytes) and [b, b+bytes) share a byte.
+inline bool overlaps(const void* a, const void* b, size_t bytes) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return pa < pb + bytes && pb < pa + bytes;
+}
+
+// The wide forward's sizes: rows too wide for a resident shape
+// (resident_plan false), few enough that one workgroup per row would leave
+// CUs idle.
+template <class S>
+inline bool wide_fwd_shape_ok(int64_t rows, int cols, bool resident_plan) {
+    return !resident_plan && rows <= kWideFwdRowsMax && wide_cols_ok<S>(cols);
+}
+
+// ... and its pointers: 16-byte aligned, y not overlapping x (y holds the
+// partial sums meanwhile).
+template <class S>
+inline bool wide_fwd_eligible(const void* x, const void* gamma, const void* y, int64_t rows,
+                              int cols, bool resident_plan) {
+    return wide_fwd_shape_ok<S>(rows, cols, resident_plan) && aligned16(x) && aligned16(y) &&
+           (gamma == nullptr || aligned16(gamma)) &&
+           !overlaps(x, y, static_cast<size_t>(rows) * static_cast<size_t>(cols) *
+                               sizeof(typename S::T));
+}
+
+// The wide backward's arguments without the workspace: rows too wide for a
+// resident shape, x, dy, dx (when given) and gamma (when given) 16-byte
+// aligned.  The caller also needs a 16-byte aligned workspace of
+// wide_ws_bytes(rows, cols).
+template <class S>
+inline bool wide_bwd_eligible(const void* x, const void* gamma, const void* dy, const void* dx,
+                              int cols, bool resident_plan) {
+    return !resident_plan && wide_cols_ok<S>(cols) && aligned16(x) && aligned16(dy) &&
+           (dx == nullptr || aligned16(dx)) && (gamma == nullptr || aligned16(gamma));
+}
+
+template <class S>
+int launch_wide_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_t rows,
+                    int cols, float eps, hipStream_t st) {
+    using T = typename S::T;
+    const WidePlan p = wide_plan(rows, cols);
+    const int64_t nstat = rows * p.nseg, nscale = rows * p.nch;
+    if (nstat > 0x7fffffffLL || nscale > 0x7fffffffLL) return AGK_EINVAL;
+    const T* xp = static_cast<const T*>(x);
+    T* yp = static_cast<T*>(y);
+    // per-segment partials in the first nseg floats of each row of y
+    float* part = static_cast<float*>(y);
+    const int64_t stride = static_cast<int64_t>(cols) * static_cast<int64_t>(sizeof(T)) / 4;
+    hipLaunchKernelGGL((wide_row_stats<S, kWideSumSq>), dim3(static_cast<unsigned>(nstat)),
+                       dim3(kWideLanes), 0, st, xp, static_cast<const T*>(nullptr),
+                       static_cast<const T*>(nullptr), part, stride, rows, cols, p.nseg);
+    if (int rc = check_launch()) return rc;
+    hipLaunchKernelGGL(wide_row_finish<kWideSumSq>,
+                       dim3(static_cast<unsigned>((rows + kWideLanes - 1) / kWideLanes)),
+                       dim3(kWideLanes), 0, st, part, stride, static_cast<const float*>(nullptr),
+                       inv_rms, rows, cols, p.nseg, eps);
+    if (int rc = check_launch()) return rc;
+    hipLaunchKernelGGL((wide_fwd_scale<S>), dim3(static_cast<unsigned>(nscale)), dim3(kWideLanes),
+                       0, st, xp, static_cast<const T*>(gamma), inv_rms, yp, rows, cols, p.nch);
+    return check_launch();
+}
+
+// ws: at least wide_ws_bytes(rows, cols, dr != nullptr) bytes, 16-byte
+// aligned (checked by the caller).  dr != nullptr: the composition (gamma
+// required), dr receiving g = gy*gamma rounded to storage.
+template <class S>
+int launch_wide_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
+                    void* dx, void* dr, float* dgamma, void* ws, int64_t rows, int cols,
+                    int acc_dx, int acc_dg, hipStream_t st) {
+    using T = typename S::T;
+    const bool comp = dr != nullptr;
+    WidePlan p = wide_plan(rows, cols);
+    wide_blocking(rows, cols, comp, p.rb, p.nrb);
+    const WideWs w = wide_ws_layout(rows, cols, p.nrb);
+    const int64_t nstat = rows * p.nseg, ntile = p.nrb * p.nch;
+    if (nstat > 0x7fffffffLL || ntile > 0x7fffffffLL) return AGK_EINVAL;
+    char* base = static_cast<char*>(ws);
+    float* partials = reinterpret_cast<float*>(base + w.partials);
+    float* segs = reinterpret_cast<float*>(base + w.segs);
+    float* coefs = reinterpret_cast<float*>(base + w.coefs);
+    const T* xp = static_cast<const T*>(x);
+    const T* gp = static_cast<const T*>(gamma);
+    const T* dyp = static_cast<const T*>(dy);
+    T* dxp = static_cast<T*>(dx);
+    T* drp = static_cast<T*>(dr);
+    if (dx) {
+        if (comp)
+            hipLaunchKernelGGL((wide_row_stats<S, kWideDotComp>),
+                               dim3(static_cast<unsigned>(nstat)), dim3(kWideLanes), 0, st, xp,
+                               dyp, gp, segs, p.nseg, rows, cols, p.nseg);
+        else
+            hipLaunchKernelGGL((wide_row_stats<S, kWideDot>), dim3(static_cast<unsigned>(nstat)),
+                               dim3(kWideLanes), 0, st, xp, dyp, gp, segs, p.nseg, rows, cols,
+                               p.nseg);
+        if (int rc = check_launch()) return rc;
+        hipLaunchKernelGGL(wide_row_finish<kWideDot>,
+                           dim3(static_cast<unsigned>((rows + kWideLanes - 1) / kWideLanes)),
+                           dim3(kWideLanes), 0, st, segs, p.nseg, inv_rms, coefs, rows, cols,
+                           p.nseg, 0.0f);
+        if (int rc = check_launch()) return rc;
+    }
+    float* part_arg = dgamma && p.nrb > 1 ? partials : nullptr;
+    float* dg_arg = dgamma && p.nrb == 1 ? dgamma : nullptr;
+    const float* coef_arg = dx ? coefs : nullptr;
+    const dim3 grid(static_cast<unsigned>(ntile));
+#define AGK_TILES(ACC_, COMP_)                                                               \
+    hipLaunchKernelGGL((wide_bwd_tiles<S, ACC_, COMP_>), grid, dim3(kWideLanes), 0, st, xp, gp, \
+                       inv_rms, dyp, dxp, drp, coef_arg, part_arg, dg_arg, rows, cols, p.nch,   \
+                       p.rb, p.nrb, acc_dg)
+    const bool acc = acc_dx && dx;
+    if (comp) {
+        if (acc) AGK_TILES(true, true);
+        else AGK_TILES(false, true);
+    } else {
+        if (acc) AGK_TILES(true, false);
+        else AGK_TILES(false, false);
+    }
+#undef AGK_TILES
+    if (int rc = check_launch()) return rc;
+    if (part_arg) return launch_finalize(partials, dgamma, p.nrb, cols, acc_dg, st);
+    return AGK_OK;
+}

@@ -67,6 +67,12 @@ typedef enum {
     AGK_ACCUM_ALL = 3
 } agk_accumulate;
 
+/* Narrowest row (in elements, either dtype) that can take the split paths:
+ * rows too wide for the register-resident kernels, 16-byte aligned, are cut
+ * into 4096-column segments and 2048-column chunks, each its own workgroup,
+ * so that a few long rows still spread over the whole GPU.                  */
+#define AGK_WIDE_MIN_COLS 16385
+
 /* Forward of the RMSNorm layer.
  * Replaces the eager forward of `ag::rms(x) * gamma`:
  *   rms_nodeops   cgadimpl/src/ops/normalization.cpp:23-35
@@ -74,7 +80,11 @@ typedef enum {
  *   mul_nodeops   cgadimpl/src/ops/arithmetic.cpp:31-39  (broadcast * gamma)
  * gamma == NULL means no scale (ag::rms alone).  inv_rms[rows] receives
  * r = 1/sqrt(mean(x^2)+eps) per row, which the backward reads (the reference
- * keeps the same tensor on the node's tape, normalization.cpp:29).           */
+ * keeps the same tensor on the node's tape, normalization.cpp:29).
+ * y may be x itself (in place).  Fewer than 1024 rows too wide for the
+ * resident kernels use y's first bytes of each row for partial sums until
+ * the last of the call's kernels overwrites them; an in-place call takes the
+ * one-workgroup-per-row kernel instead.                                      */
 int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
                     int64_t rows, int64_t cols, float eps, int dtype,
                     agk_stream_t stream);
@@ -86,9 +96,13 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
  * rows) uses, never fewer than the 256 rows the register-resident kernel
  * uses from 256 rows up.  Below 256 rows the register-resident path sums
  * dgamma down the columns in the same launch and uses no partial rows (the
- * size is still returned, for the looped kernel).  Depends only on rows and
- * cols, never on the device, so the dgamma summation order is the same
- * everywhere.                                                               */
+ * size is still returned, for the looped kernel).  From AGK_WIDE_MIN_COLS
+ * columns on it is at least what the split backward uses: about 16 MiB of
+ * dgamma partial rows (nrb = ceil(rows / ceil(rows / min(rows,
+ * ceil(2048 / ceil(cols / 2048))))) rows of cols floats), rows *
+ * ceil(cols / 4096) segment partials and rows coefficients, each region
+ * rounded up to 256 bytes.  Depends only on rows and cols, never on the
+ * device or the dtype, so the dgamma summation order is the same everywhere. */
 size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
 /* Backward (VJP) of the RMSNorm layer.
@@ -104,7 +118,10 @@ size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
  * dgamma == NULL skips the dgamma reduction; both NULL is a no-op.
  * accumulate is a set of agk_accumulate bits (AGK_ACCUM_DX, AGK_ACCUM_DGAMMA).
  * workspace must hold at least agk_rmsnorm_bwd_workspace_bytes(rows, cols)
- * bytes when dgamma != NULL.                                                 */
+ * bytes when dgamma != NULL.  With dgamma == NULL it may be NULL; rows of at
+ * least AGK_WIDE_MIN_COLS columns then take the one-workgroup-per-row-block
+ * kernel, and take the split path only when a 16-byte aligned workspace of
+ * that size is given.                                                        */
 int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms,
                     const void* dy, void* dx, float* dgamma, void* workspace,
                     size_t workspace_bytes, int64_t rows, int64_t cols,
@@ -118,7 +135,9 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms,
  * memory (AGK_NOALLOC_SCRATCH_BYTES per device, for the life of the process)
  * instead of a caller workspace, and the call allocates nothing.  Sizes whose
  * partial rows exceed the array (more than 256 * cols * 4 bytes on the
- * register-resident path: cols > 32768; the looped path's row blocks
+ * register-resident path; the split path's partial rows, segment sums and
+ * coefficients for aligned rows of AGK_WIDE_MIN_COLS columns and more, about
+ * 16 MiB + rows * ceil(cols / 4096) * 4 bytes; the looped path's row blocks
  * otherwise) return AGK_EWORKSPACE.  Every call on a device shares that
  * device's array: calls that overlap in time on one device race, so callers
  * serialise them (one stream per device, or their own ordering).           */
@@ -208,9 +227,11 @@ int agk_sum_rows(const void* x, float* out, void* workspace, size_t workspace_by
  * Every output is bit-identical to agk_mul_rowbcast_bwd(gy, h, gamma, dr,
  * dgamma) followed by agk_rmsnorm_bwd(x, NULL, inv_rms, dr, dx) on the same
  * inputs (same rounding of dr and h to storage, same summation orders), with
- * x and dy read once instead of h, gy and dr twice.  accumulate:
- * AGK_ACCUM_DX adds into dx, AGK_ACCUM_DGAMMA into dgamma; workspace as for
- * agk_rmsnorm_bwd when dgamma != NULL.                                      */
+ * x and dy read once instead of h, gy and dr twice; for rows of at least
+ * AGK_WIDE_MIN_COLS columns, when this call and that agk_rmsnorm_bwd call
+ * both have a workspace (both take the split path) or neither has.
+ * accumulate: AGK_ACCUM_DX adds into dx, AGK_ACCUM_DGAMMA into dgamma;
+ * workspace as for agk_rmsnorm_bwd (required when dgamma != NULL).          */
 int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms,
                     const void* gy, void* dr, void* dx, float* dgamma,
                     void* workspace, size_t workspace_bytes, int64_t rows,
@@ -275,11 +296,15 @@ int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_ds
  *   {lanes per row, 16-byte slots per lane, rows per workgroup,
  *    rows per dgamma partial row (backward; ceil(rows / partial rows)),
  *    dgamma partial rows (backward)};
- * lanes per row == 0 means the looped kernel (rows that are not a whole
- * number of 16-byte slots, or too wide to keep in registers).  A resident
- * backward of at most 255 rows reports 0 partial rows: it runs row and
- * column workgroups in one launch and writes dgamma directly.  Used by the
- * tests to run every reachable shape.                                        */
+ * lanes per row == 0 means a path that does not keep rows in registers:
+ * the split path when slots per lane > 0 (then plan[1] = 4096-column
+ * segments per row, plan[2] = 2048-column chunks per row, and for the
+ * backward plan[3] = rows per tile, plan[4] = dgamma partial rows, 0 when
+ * the tiles write dgamma directly), else the looped kernel (rows that are
+ * not a whole number of 16-byte slots, or too wide for registers and not
+ * split).  A resident backward of at most 255 rows reports 0 partial rows:
+ * it runs row and column workgroups in one launch and writes dgamma
+ * directly.  Used by the tests to run every reachable shape.                 */
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan);
 

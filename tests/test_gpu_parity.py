@@ -349,6 +349,7 @@ def test_sum_rows(cuda, dtype, shape):
 @pytest.mark.parametrize("dtype,shape", [("f32", (40, 4096)), ("f32", (33, 250)),
                                          ("bf16", (96, 8192)), ("bf16", (17, 100)),
                                          ("f32", (24, 16392)), ("bf16", (9, 32776)),
+                                         ("f32", (1100, 20480)), ("bf16", (2, 262144)),
                                          ("f32", (65536, 4096)), ("bf16", (16384, 8192))])
 def test_rms_mul_bwd(cuda, dtype, shape):
     """Bit-identical to mul_rowbcast_bwd followed by rmsnorm_bwd(gamma=None) on

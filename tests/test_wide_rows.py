@@ -1,0 +1,200 @@
+"""Rows wider than the register-resident shapes (the split paths: several
+workgroups per row for the row statistics, row-block x column-chunk tiles for
+dx and dgamma).
+
+Against the CPU oracle (fp64 accumulation) at sizes it finishes in seconds,
+through the size-independent properties at full sizes, bit-identical across
+runs, with accumulation and the one-output modes bit-identical to the full
+call, and the fallbacks that keep the one-workgroup-per-row kernels (an
+in-place forward, a dx-only call without workspace, rows that are not whole
+16-byte slots) within the same bars.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import cgadimpl_amd as agk
+import oracle
+from cgadimpl_amd import configs
+from gpu_util import as_f32, check_on_device, device_inputs, gpu_layer, to_dev, to_host
+from tolerances import TOL_BF16, TOL_F32, dx_rel_err, row_rel_err, vec_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _tol(x):
+    return TOL_BF16 if x.dtype == np.uint16 else TOL_F32
+
+
+def _compare(x, gamma, dy, eps, got, label, check_dg=True):
+    y, inv, dx, dg = got
+    ry, rinv = oracle.fwd(x, gamma, eps)
+    rdx, rdg = oracle.bwd(x, gamma, rinv, dy)
+    tol = _tol(x)
+    e = {"y": row_rel_err(as_f32(y), as_f32(ry)), "inv_rms": vec_rel_err(inv, rinv),
+         "dx": dx_rel_err(as_f32(dx), as_f32(rdx), as_f32(x), as_f32(gamma), as_f32(dy), eps)}
+    if check_dg:
+        e["dgamma"] = vec_rel_err(dg, rdg)
+    print(f"[{label}] " + " ".join(f"{k}={v:.2e}" for k, v in e.items()), flush=True)
+    assert e["inv_rms"] <= TOL_F32, (label, e)
+    for k in ("y", "dx", "dgamma"):
+        if k in e:
+            assert e[k] <= tol, (label, k, e[k])
+
+
+def _dt(dtype):
+    return agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16
+
+
+# (dtype, rows, cols): few very long rows (one row block: dgamma written by the
+# tiles), ragged last segment and chunk, and enough rows for several row
+# blocks (partial rows + finalize) with the forward still split (< 1024 rows)
+# or back on one workgroup per row (>= 1024 rows).
+WIDE_CASES = [
+    ("f32", 8, 262144),
+    ("f32", 1, 1 << 20),
+    ("f32", 3, 40000),
+    ("f32", 2, 131076),
+    ("bf16", 3, 65544),
+    ("bf16", 5, 131080),
+    ("bf16", 7, 24576),
+    ("f32", 300, 65536),
+    ("f32", 1100, 20480),
+    ("bf16", 1030, 40000),
+]
+
+
+@pytest.mark.parametrize("dtype,rows,cols", WIDE_CASES, ids=str)
+def test_wide_parity(cuda, dtype, rows, cols):
+    fp = agk.launch_plan(rows, cols, _dt(dtype), False)
+    bp = agk.launch_plan(rows, cols, _dt(dtype), True)
+    label = f"wide {dtype} {rows}x{cols} fwd {fp} bwd {bp}"
+    print(label, flush=True)
+    assert bp["tpr"] == 0 and bp["nv"] > 0, "backward should take the split path"
+    if fp["tpr"] == 0 and rows < 1024 and (cols % 4 == 0):
+        assert fp["nv"] > 0, "forward should take the split path"
+    x, g, dy = configs.make_inputs((rows, cols), dtype=dtype, seed=rows * 7 + cols)
+    got = gpu_layer(x, g, dy, 1e-6, cuda)
+    _compare(x, g, dy, 1e-6, got, label)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("dtype,rows,cols", [("f32", 4096, 32768), ("bf16", 1024, 65536),
+                                             ("f32", 64, 1 << 21)], ids=str)
+def test_wide_full_size_properties(cuda, dtype, rows, cols):
+    label = f"wide {dtype} {rows}x{cols}"
+    print(label, flush=True)
+    x, g, dy = device_inputs((rows, cols), dtype, rows + cols, cuda)
+    check_on_device(x, g, dy, 1e-6, label, _compare, sample=16)
+
+
+def test_wide_no_gamma(cuda):
+    x, _, dy = configs.make_inputs((3, 65536), with_gamma=False, seed=21)
+    got = gpu_layer(x, None, dy, 1e-5, cuda)
+    _compare(x, None, dy, 1e-5, got, "wide no gamma")
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [("f32", 5, 40000), ("bf16", 4, 65536),
+                                             ("f32", 1, 1 << 20)], ids=str)
+@pytest.mark.parametrize("flags", [agk.AGK_ACCUM_DX, agk.AGK_ACCUM_DGAMMA, agk.AGK_ACCUM_ALL])
+def test_wide_accumulate(cuda, dtype, rows, cols, flags):
+    """Each output accumulates on its own (several row blocks through the
+    finalize, and one row block whose tiles add into dgamma directly): fp32
+    dx and dgamma bit-identical to pre + fresh.  bf16 dx is rounded once from
+    pre + the fp32 term, which pre + the bf16-rounded fresh dx cannot
+    reproduce bit for bit: within those two roundings (2^-8 relative each)."""
+    import torch
+    xd, gd, dyd = device_inputs((rows, cols), dtype, rows * 3 + cols + flags, cuda)
+    _, inv = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    fresh_dx, fresh_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    pre_dx = torch.full_like(xd, 0.25)
+    pre_dg = torch.full((cols,), -0.5, device=cuda)
+    dx, dg = agk.rmsnorm_bwd(xd, gd, inv, dyd, dx=pre_dx.clone(), dgamma=pre_dg.clone(),
+                             accumulate=flags)
+    torch.cuda.synchronize()
+    want_dg = (pre_dg + fresh_dg) if flags & agk.AGK_ACCUM_DGAMMA else fresh_dg
+    assert torch.equal(dg, want_dg)
+    if not flags & agk.AGK_ACCUM_DX:
+        assert torch.equal(dx, fresh_dx)
+    elif dtype == "f32":
+        assert torch.equal(dx, pre_dx + fresh_dx)
+    else:
+        p, f = pre_dx.float(), fresh_dx.float()
+        bound = 2.0 ** -7 * (p.abs() + f.abs())
+        assert bool(((dx.float() - (p + f)).abs() <= bound).all())
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [("f32", 6, 65536), ("bf16", 300, 40000)], ids=str)
+def test_wide_one_output(cuda, dtype, rows, cols):
+    """dx alone (with a workspace) and dgamma alone: bit-identical to the full
+    call's outputs; dx alone without a workspace takes the looped kernel,
+    within the oracle's bar."""
+    import torch
+    x, g, dy = configs.make_inputs((rows, cols), dtype=dtype, seed=31 + rows)
+    xd, gd, dyd = to_dev(x, cuda), to_dev(g, cuda), to_dev(dy, cuda)
+    _, inv = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    full_dx, full_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    dx_only, none_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd, want_dgamma=False)
+    none_dx, dg_only = agk.rmsnorm_bwd(xd, gd, inv, dyd, want_dx=False)
+    torch.cuda.synchronize()
+    assert none_dg is None and none_dx is None
+    assert torch.equal(dx_only, full_dx)
+    assert torch.equal(dg_only, full_dg)
+    # no workspace: the C ABI with a NULL workspace and dgamma == NULL
+    dx_loop = torch.empty_like(xd)
+    rc = agk.lib().agk_rmsnorm_bwd(xd.data_ptr(), gd.data_ptr(), inv.data_ptr(), dyd.data_ptr(),
+                                   dx_loop.data_ptr(), None, None, 0, rows, cols,
+                                   _dt(dtype), 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    _, rinv = oracle.fwd(x, g, 1e-6)
+    rdx, _ = oracle.bwd(x, g, rinv, dy)
+    for name, t in (("split", full_dx), ("looped", dx_loop)):
+        e = dx_rel_err(as_f32(to_host(t)), as_f32(rdx), as_f32(x), as_f32(g), as_f32(dy), 1e-6)
+        print(f"[{dtype} {rows}x{cols} dx {name}] {e:.2e}", flush=True)
+        assert e <= _tol(x)
+
+
+def test_wide_forward_in_place(cuda):
+    """y == x: the one-workgroup-per-row kernel (the split forward would
+    overwrite x with its partial sums), same bars as out of place."""
+    import torch
+    rows, cols = 4, 65536
+    x, g, dy = configs.make_inputs((rows, cols), seed=41)
+    xd, gd = to_dev(x, cuda), to_dev(g, cuda)
+    y_out, inv_out = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    buf = xd.clone()
+    y_in, inv_in = agk.rmsnorm_fwd(buf, gd, 1e-6, y=buf)
+    torch.cuda.synchronize()
+    assert y_in.data_ptr() == buf.data_ptr()
+    ry, rinv = oracle.fwd(x, g, 1e-6)
+    for name, y, inv in (("split", y_out, inv_out), ("in place", y_in, inv_in)):
+        ey = row_rel_err(to_host(y), ry)
+        ei = vec_rel_err(to_host(inv), rinv)
+        print(f"[in-place test {name}] y={ey:.2e} inv={ei:.2e}", flush=True)
+        assert ey <= TOL_F32 and ei <= TOL_F32
+
+
+@pytest.mark.parametrize("cols", [40002, 65537])
+def test_wide_unaligned_rows(cuda, cols):
+    """Rows that are not whole 16-byte slots keep the looped kernels."""
+    assert agk.launch_plan(3, cols, agk.AGK_F32, True)["nv"] == 0
+    x, g, dy = configs.make_inputs((3, cols), seed=cols)
+    got = gpu_layer(x, g, dy, 1e-6, cuda)
+    _compare(x, g, dy, 1e-6, got, f"wide unaligned 3x{cols}")
+
+
+def test_wide_workspace_size(cuda):
+    """The workspace query covers the split path's regions, and a call with a
+    workspace one byte short of it is refused when dgamma is wanted."""
+    import torch
+    rows, cols = 300, 65536
+    need = agk.rmsnorm_bwd_workspace_bytes(rows, cols)
+    assert need >= 16 << 20
+    x = torch.randn(rows, cols, device=cuda)
+    _, inv = agk.rmsnorm_fwd(x, None, 1e-6)
+    ws = torch.empty(need - 1, dtype=torch.uint8, device=cuda)
+    with pytest.raises(agk.AgkError) as ei:
+        agk.rmsnorm_bwd(x, None, inv, x, workspace=ws)
+    assert ei.value.status == 3

@@ -48,13 +48,17 @@ def _pair(cuda, rows, cols, dtype, accumulate, seed):
 
 
 # (rows, cols, dtype, accumulate bits): each call smaller than the one before it;
-# the register-resident kernel (256 partial rows), the looped kernel (unaligned
-# rows, one partial row per row block) and the few-rows kernel (no partials).
+# the register-resident kernel (256 partial rows), the split path for wide rows
+# (partial rows, segment sums and coefficients; then one row block writing
+# dgamma directly), the looped kernel (unaligned rows, one partial row per row
+# block) and the few-rows kernel (no partials).
 CALLS = [
     (16384, 4096, "f32", 0),
+    (300, 65536, "f32", agk.AGK_ACCUM_ALL),
     (1000, 1536, "bf16", agk.AGK_ACCUM_ALL),
     (600, 1001, "f32", agk.AGK_ACCUM_DGAMMA),
     (51, 13824, "f32", 0),
+    (1, 131072, "bf16", agk.AGK_ACCUM_DX),
 ]
 
 
@@ -68,7 +72,7 @@ def test_noalloc_matches_workspace_backward_across_calls(cuda):
 
 def test_noalloc_rejects_partials_beyond_the_scratch_array(cuda):
     import torch
-    rows, cols = 300, 40000  # looped kernel: 300 row blocks x 40000 fp32 partials = 48 MB
+    rows, cols = 300, 40001  # looped kernel: 300 row blocks x 40001 fp32 partials = 48 MB
     x = torch.zeros((rows, cols), dtype=torch.float32, device=cuda)
     inv = torch.ones(rows, dtype=torch.float32, device=cuda)
     dg = torch.zeros(cols, dtype=torch.float32, device=cuda)
