@@ -156,6 +156,9 @@ def _traffic(config_name):
 def _bwd_kernels(agk, rows, cols, dtype):
     """The kernels one agk_rmsnorm_bwd call of these sizes launches."""
     p = agk.launch_plan(rows, cols, agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16, True)
+    if p["tpr"] == 0 and p["nv"] > 0:
+        return ("wide_row_stats + wide_row_finish + wide_bwd_tiles"
+                + (" + dgamma_finalize" if p["nblk"] else ""))
     if p["tpr"] == 0:
         return "rms_bwd_looped + dgamma_finalize"
     if p["nblk"] == 0:
@@ -825,6 +828,82 @@ def stream_probe(mib, steps):
     return results
 
 
+WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
+               ("f32", 256, 65536), ("f32", 4096, 32768), ("bf16", 8, 262144),
+               ("bf16", 51, 32768), ("bf16", 1024, 65536))
+
+
+def run_wide(steps):
+    """Rows wider than the register-resident kernels: the split paths against
+    the one-workgroup-per-row kernels on the same build, each call captured
+    `steps` times into a HIP graph and replayed (GPU time per call).
+
+    forward: out of place (split when fewer than 1024 rows) against in place
+    (y = x, which keeps one workgroup per row); dx alone: with a workspace
+    (split) against without one (looped); and the full backward (dx and
+    dgamma, split).  One JSON line per shape; GB/s are algorithmic bytes
+    (forward 2 tensors, backward 3) over the time.
+    """
+    import torch
+
+    import cgadimpl_amd as agk
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    out = []
+    for dtype, rows, cols in WIDE_SHAPES:
+        dt = agk.AGK_F32 if dtype == "f32" else agk.AGK_BF16
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(rows * 31 + cols)
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        x = torch.randn(rows, cols, generator=gen, device=dev).to(tdt)
+        g = (torch.rand(cols, generator=gen, device=dev) + 0.5).to(tdt)
+        dy = torch.randn(rows, cols, generator=gen, device=dev).to(tdt)
+        y, dx = torch.empty_like(x), torch.empty_like(x)
+        xin = x.clone()
+        inv = torch.empty(rows, dtype=torch.float32, device=dev)
+        dg = torch.empty(cols, dtype=torch.float32, device=dev)
+        ws = torch.empty(agk.rmsnorm_bwd_workspace_bytes(rows, cols), dtype=torch.uint8,
+                         device=dev)
+        agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv)
+        fn = agk.lib().agk_rmsnorm_bwd
+
+        def dx_only(workspace):
+            def body(i, st):
+                rc = fn(x.data_ptr(), g.data_ptr(), inv.data_ptr(), dy.data_ptr(), dx.data_ptr(),
+                        None, workspace.data_ptr() if workspace is not None else None,
+                        workspace.numel() if workspace is not None else 0, rows, cols, dt, 0,
+                        st.cuda_stream)
+                if rc:
+                    raise agk.AgkError(rc, "agk_rmsnorm_bwd")
+            return body
+        n = max(1, steps)
+        t = {
+            "fwd_split": graph_replay_ms(
+                lambda i, st: agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, stream=st), n),
+            "fwd_in_place": graph_replay_ms(
+                lambda i, st: agk.rmsnorm_fwd(xin, g, 1e-6, y=xin, inv_rms=inv, stream=st), n),
+            "bwd_split": graph_replay_ms(
+                lambda i, st: agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws,
+                                              stream=st), n),
+            "bwd_dx_split": graph_replay_ms(dx_only(ws), n),
+            "bwd_dx_looped": graph_replay_ms(dx_only(None), n),
+        }
+        es = x.element_size()
+        fb, bb = 2.0 * rows * cols * es, 3.0 * rows * cols * es
+        fp, bp = agk.launch_plan(rows, cols, dt, False), agk.launch_plan(rows, cols, dt, True)
+        rec = {"wide_rows": f"{dtype} {rows}x{cols}", "dtype": dtype, "rows": rows,
+               "cols": cols, "calls_per_graph": n,
+               "fwd_plan": fp, "bwd_plan": bp,
+               "us": {k: round(v * 1e3, 2) for k, v in t.items()},
+               "gbs": {k: round((fb if k.startswith("fwd") else bb) / (v * 1e-3) / 1e9, 1)
+                       for k, v in t.items()}}
+        print(json.dumps(rec), flush=True)
+        out.append(rec)
+        del x, g, dy, y, dx, xin, inv, dg, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -847,12 +926,18 @@ def main():
     ap.add_argument("--stream-probe", type=int, default=0, metavar="MIB",
                     help="only time the HBM streaming probe (copy, 2 reads + 1 write, read "
                          "only; plain and non-temporal) over MIB-MiB buffers, then exit")
+    ap.add_argument("--wide", action="store_true",
+                    help="only time rows wider than the register-resident kernels: the split "
+                         "paths against the one-workgroup-per-row kernels, then exit")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe(args.copy_probe, args.steps)
         return
     if args.stream_probe:
         stream_probe(args.stream_probe, min(args.steps, 50))
+        return
+    if args.wide:
+        run_wide(min(args.steps, 20))
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -956,6 +956,35 @@ __global__ __launch_bounds__((VEC ? kFinCols / 4 : kFinCols) * kFinSplits) void 
     }
 }
 
+// dgamma from at most kFinSplits partial rows: one lane per column, the
+// partial rows added in order in fp64 from +0.0, kFewFinBatch rows loaded
+// before any is added.  With nblk <= kFinSplits every split of
+// dgamma_finalize holds at most one row, so its sum is this sum bit for bit
+// (its split sums are +0.0 + p_s, added in split order, and the empty splits
+// add +0.0 to a sum that is never -0.0); this kernel spreads over the columns
+// instead of launching a workgroup per 16 columns for a few rows.
+constexpr int kFewFinBatch = 16;
+__global__ __launch_bounds__(kBlock) void dgamma_finalize_few(
+    const float* __restrict__ partials, float* __restrict__ dgamma, int64_t nblk, int cols,
+    int accumulate) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    double tot = 0.0;
+    for (int64_t b0 = 0; b0 < nblk; b0 += kFewFinBatch) {
+        float v[kFewFinBatch];
+#pragma unroll
+        for (int u = 0; u < kFewFinBatch; ++u) {
+            const int64_t b = b0 + u < nblk ? b0 + u : nblk - 1;  // in range; dropped below
+            v[u] = partials[b * cols + c];
+        }
+#pragma unroll
+        for (int u = 0; u < kFewFinBatch; ++u)
+            if (b0 + u < nblk) tot += v[u];
+    }
+    const float v = static_cast<float>(tot);
+    dgamma[c] = accumulate ? dgamma[c] + v : v;
+}
+
 __global__ __launch_bounds__(kBlock) void fill_zero_f32(float* __restrict__ p, int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -1318,6 +1347,12 @@ int launch_bwd(const void* x, const void* gamma, const float* inv_rms, const voi
 
 inline int launch_finalize(const float* partials, float* dgamma, int64_t nblk, int cols,
                            int accumulate, hipStream_t st) {
+    if (nblk <= kFinSplits) {  // same sums, spread over the columns
+        const unsigned g = static_cast<unsigned>((cols + kBlock - 1) / kBlock);
+        hipLaunchKernelGGL(dgamma_finalize_few, dim3(g), dim3(kBlock), 0, st, partials, dgamma,
+                           nblk, cols, accumulate);
+        return check_launch();
+    }
     const unsigned grid = static_cast<unsigned>((cols + kFinCols - 1) / kFinCols);
     if (cols % 4 == 0 && aligned16(partials))
         hipLaunchKernelGGL(dgamma_finalize<true>, dim3(grid), dim3(kFinCols / 4 * kFinSplits), 0,

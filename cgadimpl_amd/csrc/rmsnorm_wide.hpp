@@ -8,7 +8,7 @@
 // long rows still spread over the whole GPU:
 //
 //   forward   wide_row_stats<S, kWideSumSq>  per (row, segment): sum of x^2
-//             wide_row_finish<kWideSumSq>    per row: partials in segment
+//             wide_row_finish<kWideSumSq>    per row: partials in a fixed
 //                                            order -> inv_rms[row]
 //             wide_fwd_scale<S>              per (row, chunk): y = (x*r)*gamma
 //   backward  wide_row_stats<S, kWideDot>    per (row, segment): sum of g*x,
@@ -21,8 +21,8 @@
 //                                            (more than one row block only)
 //
 // The formulas are the resident kernels' (same products, same association);
-// only the order of the row sums differs (segment trees summed in segment
-// order), and it depends only on cols.  Every launch shape depends only on
+// only the order of the row sums differs (segment trees, then the segments
+// over a fixed lane tree), and it depends only on cols.  Every launch shape depends only on
 // rows and cols, so results are bit-identical run to run.
 //
 // The composition rms(x) * gamma (COMP: agk_rms_mul_bwd) runs the same
@@ -183,18 +183,36 @@ __global__ __launch_bounds__(kWideLanes) void wide_row_stats(
     (void)rows;
 }
 
-// Per row: the segment partials added in segment order, then
+// Per row (one wave of 64 lanes each, four rows per workgroup): the segment
+// partials summed in a fixed order -- lane l adds partials l, l+64, l+128, ...
+// in turn, then the lanes are added over the DPP tree of group_sum -- then
 //   kWideSumSq: out[row] = 1/sqrt(sum/cols + eps)            (inv_rms)
-//   kWideDot:   out[row] = (r*r*dot) * (1/cols), r = inv_rms[row]
+//   otherwise:  out[row] = (r*r*dot) * (1/cols), r = inv_rms[row]
+// Each lane's loads are issued before any is added, so a row of up to 256
+// segments (1M columns) costs one round trip.
+constexpr int kFinishRowsPerBlock = kWideLanes / 64;
 template <int KIND>
 __global__ __launch_bounds__(kWideLanes) void wide_row_finish(
     const float* __restrict__ partials, int64_t part_row_stride, const float* __restrict__ inv_rms,
     float* __restrict__ out, int64_t rows, int cols, int64_t nseg, float eps) {
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWideLanes + threadIdx.x;
-    if (row >= rows) return;
+    constexpr int kBatch = 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kFinishRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform: the whole wave takes this row or none
     const float* p = partials + row * part_row_stride;
     float v = 0.0f;
-    for (int64_t s = 0; s < nseg; ++s) v += p[s];
+    for (int64_t base = lane; base < nseg; base += 64 * kBatch) {
+        float t[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int64_t i = base + 64 * u;
+            t[u] = i < nseg ? p[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v += t[u];
+    }
+    v = group_sum<64>(v);
+    if (lane != 0) return;
     if constexpr (KIND == kWideSumSq) {
         out[row] = 1.0f / sqrtf(v / static_cast<float>(cols) + eps);
         (void)inv_rms;
@@ -458,7 +476,8 @@ int launch_wide_fwd(const void* x, const void* gamma, void* y, float* inv_rms, i
                        static_cast<const T*>(nullptr), part, stride, rows, cols, p.nseg);
     if (int rc = check_launch()) return rc;
     hipLaunchKernelGGL(wide_row_finish<kWideSumSq>,
-                       dim3(static_cast<unsigned>((rows + kWideLanes - 1) / kWideLanes)),
+                       dim3(static_cast<unsigned>((rows + kFinishRowsPerBlock - 1) /
+                                                  kFinishRowsPerBlock)),
                        dim3(kWideLanes), 0, st, part, stride, static_cast<const float*>(nullptr),
                        inv_rms, rows, cols, p.nseg, eps);
     if (int rc = check_launch()) return rc;
@@ -501,7 +520,8 @@ int launch_wide_bwd(const void* x, const void* gamma, const float* inv_rms, cons
                                p.nseg);
         if (int rc = check_launch()) return rc;
         hipLaunchKernelGGL(wide_row_finish<kWideDot>,
-                           dim3(static_cast<unsigned>((rows + kWideLanes - 1) / kWideLanes)),
+                           dim3(static_cast<unsigned>((rows + kFinishRowsPerBlock - 1) /
+                                                  kFinishRowsPerBlock)),
                            dim3(kWideLanes), 0, st, segs, p.nseg, inv_rms, coefs, rows, cols,
                            p.nseg, 0.0f);
         if (int rc = check_launch()) return rc;

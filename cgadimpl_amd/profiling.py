@@ -24,6 +24,7 @@ Usage:
   python -m cgadimpl_amd.profiling mfma <run_counter_collection.csv> <out.md> "<command>"
   python -m cgadimpl_amd.profiling bench <bench output (JSON lines)> <out.md> "<command>"
   python -m cgadimpl_amd.profiling probe <bench --stream-probe output> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling wide <bench --wide output> <out.md> "<command>"
   python -m cgadimpl_amd.profiling traffic <fetch_dir> <write_dir> <copy_fetch_dir>
         <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
   python -m cgadimpl_amd.profiling gemm-traffic <fetch_dir> <write_dir> <copy_fetch_dir>
@@ -45,7 +46,8 @@ ENTRY_KERNELS = {
 
 # The files the RMSNorm kernels are compiled from.  A traffic summary records a
 # hash of them, and bench.py uses a summary only while the hash still matches.
-KERNEL_SOURCES = ("cgadimpl_amd/csrc/rmsnorm.hip", "cgadimpl_amd/csrc/rowcommon.hpp")
+KERNEL_SOURCES = ("cgadimpl_amd/csrc/rmsnorm.hip", "cgadimpl_amd/csrc/rowcommon.hpp",
+                  "cgadimpl_amd/csrc/rmsnorm_wide.hpp")
 
 
 def kernel_source_hash(root=None):
@@ -415,8 +417,35 @@ def write_probe_summary(jsonl, out_md, command):
         fh.write("\n".join(lines) + "\n")
 
 
+def write_wide_summary(jsonl, out_md, command):
+    """Table of bench.py --wide lines: the split paths against the
+    one-workgroup-per-row kernels per shape (graph-replayed us and GB/s)."""
+    recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"wide_rows"')]
+    lines = ["# Rows wider than the register-resident kernels (MI355X, one GPU)", "",
+             "Command:", "", "```", command, "```", "",
+             "Each call captured into a HIP graph and replayed (GPU time per call, best of 5 "
+             "replays). Forward: out of place (the split path below 1024 rows) against in "
+             "place (y = x keeps one workgroup per row). dx alone: with a workspace (split) "
+             "against without (looped). Backward: dx and dgamma (split). GB/s: algorithmic "
+             "bytes (forward 2 tensors, backward 3) over the time; % of 8 TB/s in brackets.",
+             "",
+             "| shape | fwd split us | fwd in place us | bwd dx split us | bwd dx looped us | "
+             "bwd (dx, dgamma) split us | fwd split GB/s | bwd split GB/s |",
+             "|---|---|---|---|---|---|---|---|"]
+    for r in recs:
+        u, g = r["us"], r["gbs"]
+        lines.append(f"| {r['wide_rows']} | {u['fwd_split']} | {u['fwd_in_place']} | "
+                     f"{u['bwd_dx_split']} | {u['bwd_dx_looped']} | {u['bwd_split']} | "
+                     f"{g['fwd_split']:.0f} ({g['fwd_split'] / 80:.1f} %) | "
+                     f"{g['bwd_split']:.0f} ({g['bwd_split'] / 80:.1f} %) |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
 def main(argv):
-    if len(argv) >= 4 and argv[0] == "trace":
+    if len(argv) >= 4 and argv[0] == "wide":
+        write_wide_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 4 and argv[0] == "trace":
         write_trace_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "probe":
         write_probe_summary(argv[1], argv[2], argv[3])
