@@ -161,6 +161,8 @@ def _bwd_kernels(agk, rows, cols, dtype):
                 + (" + dgamma_finalize" if p["nblk"] else ""))
     if p["tpr"] == 0:
         return "rms_bwd_looped + dgamma_finalize"
+    if cols > 16384 and p["tpr"] == 1024 and p["nv"] * (4 if dtype == "f32" else 8) * 1024 > 16384:
+        return "wide_bwd_resident + dgamma_finalize"
     if p["nblk"] == 0:
         return "bwd_fewrows: row and column workgroups, one launch"
     return "rms_bwd_resident + dgamma_finalize"
@@ -830,7 +832,7 @@ def stream_probe(mib, steps):
 
 WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
                ("f32", 256, 65536), ("f32", 4096, 32768), ("bf16", 8, 262144),
-               ("bf16", 51, 32768), ("bf16", 1024, 65536))
+               ("bf16", 51, 32768), ("bf16", 1024, 65536), ("bf16", 16384, 20480))
 
 
 def run_wide(steps):

@@ -1392,6 +1392,27 @@ inline bool bwd_wide_possible(const void* x, const void* gamma, const void* dy, 
     const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
     return wide_bwd_eligible<S>(x, gamma, dy, dx, cols, p.tpr != 0);
 }
+// Whether the one-pass kernel for rows of up to 32768 columns takes these
+// arguments (dr: the composition's output, or nullptr).
+template <class S>
+inline bool bwd_res_wide_possible(const void* x, const void* gamma, const void* dy,
+                                  const void* dx, const void* dr, int64_t rows, int cols) {
+    int64_t nblk = 0, rpb = 0;
+    const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    return wide_res_eligible<S>(x, gamma, dy, dx, dr, rows, cols, p.tpr != 0);
+}
+inline bool bwd_takes_res_wide(const void* x, const void* gamma, const void* dy, const void* dx,
+                               const void* dr, int64_t rows, int cols, int dtype) {
+    return dtype == AGK_F32 ? bwd_res_wide_possible<F32>(x, gamma, dy, dx, dr, rows, cols)
+                            : bwd_res_wide_possible<BF16>(x, gamma, dy, dx, dr, rows, cols);
+}
+// dgamma partial rows the one-pass kernel writes (its workspace need).
+inline size_t bwd_res_wide_bytes(int64_t rows, int cols, bool comp) {
+    int64_t nblk = 0, rpb = 0;
+    wide_res_blocking(rows, comp, nblk, rpb);
+    return static_cast<size_t>(nblk) * static_cast<size_t>(cols) * 4u;
+}
+
 inline bool bwd_takes_wide(const void* x, const void* gamma, const void* dy, const void* dx,
                            int64_t rows, int cols, int dtype, const void* ws, size_t ws_bytes) {
     if (!ws || !aligned16(ws) || ws_bytes < wide_ws_bytes(rows, cols, false)) return false;
@@ -1407,6 +1428,12 @@ inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rm
                            const void* dy, void* dx, float* dgamma, float* partials, void* ws,
                            size_t ws_bytes, int64_t rows, int cols, int dtype, int acc_dx,
                            int acc_dg, hipStream_t st) {
+    if (bwd_takes_res_wide(x, gamma, dy, dx, nullptr, rows, cols, dtype))
+        return dtype == AGK_F32
+                   ? launch_wide_res_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, partials, dgamma,
+                                              rows, cols, acc_dx, acc_dg, st)
+                   : launch_wide_res_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
+                                               dgamma, rows, cols, acc_dx, acc_dg, st);
     if (bwd_takes_wide(x, gamma, dy, dx, rows, cols, dtype, ws, ws_bytes))
         return dtype == AGK_F32
                    ? launch_wide_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, dgamma, ws, rows,
@@ -1548,6 +1575,18 @@ int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_r
     if (!x || !inv_rms || !dy) return AGK_EINVAL;
     if (!dx && !dgamma) return AGK_OK;  // nothing requested
     const int c = static_cast<int>(cols);
+    // Rows of up to 32768 columns, at least 256 of them: the one-pass kernel,
+    // its partial rows in the scratch array.
+    if (bwd_takes_res_wide(x, gamma, dy, dx, nullptr, rows, c, dtype)) {
+        float* ws = nullptr;
+        if (dgamma) {
+            if (bwd_res_wide_bytes(rows, c, false) > AGK_NOALLOC_SCRATCH_BYTES)
+                return AGK_EWORKSPACE;
+            if (int rc = scratch_on_device(st, &ws)) return rc;
+        }
+        return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, ws, nullptr, 0, rows, c, dtype,
+                               acc_dx, acc_dg, st);
+    }
     // Rows too wide for the resident shapes: the wide path with the scratch
     // array as its workspace, as agk_rmsnorm_bwd takes it with the workspace
     // agk_rmsnorm_bwd_workspace_bytes asks for.
@@ -1596,6 +1635,15 @@ int agk_rms_mul_bwd(const void* x, const void* gamma, const float* inv_rms, cons
         partials = static_cast<float*>(workspace);
     }
     const int c = static_cast<int>(cols);
+    // Rows of up to 32768 columns and at least 256 rows: the one-pass kernel,
+    // whose outputs are the two separate calls' (agk_rmsnorm_bwd takes the
+    // same kernel for them, agk_mul_rowbcast_bwd the looped one).
+    if (bwd_takes_res_wide(x, gamma, gy, dx, dr, rows, c, dtype))
+        return dtype == AGK_F32 ? launch_wide_res_bwd<F32>(x, gamma, inv_rms, gy, dx, dr, partials,
+                                                           dgamma, rows, c, acc_dx, acc_dg, st)
+                                : launch_wide_res_bwd<BF16>(x, gamma, inv_rms, gy, dx, dr,
+                                                            partials, dgamma, rows, c, acc_dx,
+                                                            acc_dg, st);
     // Rows too wide for the resident shapes, with a workspace: the split
     // path, whose outputs are the two separate calls' on their split paths.
     if (workspace && aligned16(workspace) && aligned16(dr) &&
@@ -1781,6 +1829,24 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
     plan[2] = p.g;
     plan[3] = static_cast<int32_t>(rpb);
     plan[4] = static_cast<int32_t>(nblk);
+    if (p.tpr == 0 && backward && cols > 0 && cols <= 0x7fffffffLL) {
+        // the one-pass kernel for rows of up to 32768 columns
+        const void* a = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+        const int c = static_cast<int>(cols);
+        const bool res = dtype == AGK_F32
+                             ? wide_res_eligible<F32>(a, a, a, a, nullptr, rows, c, false)
+                             : wide_res_eligible<BF16>(a, a, a, a, nullptr, rows, c, false);
+        if (res) {
+            int64_t wb = 0, wr = 0;
+            wide_res_blocking(rows, false, wb, wr);
+            plan[0] = kWideResLanes;
+            plan[1] = kWideResMaxCols / (w * kWideResLanes);
+            plan[2] = 1;
+            plan[3] = static_cast<int32_t>((rows + wb - 1) / wb);
+            plan[4] = static_cast<int32_t>(wb);
+            return AGK_OK;
+        }
+    }
     if (p.tpr == 0 && cols > 0 && cols <= 0x7fffffffLL) {
         // aligned stand-in pointers, and for the forward a y apart from x
         const void* a = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));

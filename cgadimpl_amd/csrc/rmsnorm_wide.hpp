@@ -547,3 +547,233 @@ int launch_wide_bwd(const void* x, const void* gamma, const float* inv_rms, cons
     if (part_arg) return launch_finalize(partials, dgamma, p.nrb, cols, acc_dg, st);
     return AGK_OK;
 }
+
+// ---- one pass over rows of up to 32768 columns ----------------------------------
+// Aligned rows of kWideMinCols..kWideResMaxCols columns and at least
+// kWideResMinRows rows: one 1024-lane workgroup per row at a time, the row's x
+// and dy in registers (NV 16-byte slots per lane: 8 fp32, 4 bf16), gamma
+// re-read per row from L2, and each lane's dgamma columns in LDS (dgl,
+// 128 KiB) instead of registers, which the row would not leave room for.
+// Each lane adds to LDS only the columns it owns, so the accumulators need no
+// barrier.  Before the row sum each slot yields g = dy*gamma, its share of
+// the dot, the composition's dr and the dgamma term (which needs r, not the
+// sum), so only x and g stay live across the sum.  x and dy are read once:
+// the split path's second read disappears.
+//   RMSNorm backward (COMP false): rows dealt round-robin to min(rows, 256)
+//     workgroups (as the resident backward), the dgamma term dy*(x*r);
+//   composition (COMP true): g rounded to storage and written to dr, the term
+//     gy*h with h = x*r rounded to storage, added unfused in row order over
+//     the looped kernels' contiguous row blocks (bwd_rows_per_block), so the
+//     partial rows are agk_mul_rowbcast_bwd's.
+// Both end with one fp32 partial row per workgroup (dgamma_finalize after);
+// the dx arithmetic and its row sum are the same in both.
+constexpr int kWideResLanes = 1024;
+constexpr int kWideResMaxCols = 32768;
+constexpr int64_t kWideResMinRows = 256;
+constexpr int64_t kWideResBlocks = 256;
+
+template <class S>
+inline bool wide_res_eligible(const void* x, const void* gamma, const void* dy, const void* dx,
+                              const void* dr, int64_t rows, int cols, bool resident_plan) {
+    return !resident_plan && rows >= kWideResMinRows && cols <= kWideResMaxCols &&
+           wide_cols_ok<S>(cols) && aligned16(x) && aligned16(dy) &&
+           (dx == nullptr || aligned16(dx)) && (dr == nullptr || aligned16(dr)) &&
+           (gamma == nullptr || aligned16(gamma));
+}
+
+// Row blocking of the one-pass kernel: (workgroups, contiguous rows per
+// workgroup, 0 = round-robin).
+inline void wide_res_blocking(int64_t rows, bool comp, int64_t& nblk, int64_t& rpb) {
+    if (comp) {
+        rpb = bwd_rows_per_block(rows);
+        nblk = bwd_num_blocks(rows);
+    } else {
+        nblk = rows < kWideResBlocks ? rows : kWideResBlocks;
+        rpb = 0;
+    }
+}
+
+template <class S, bool ACC, bool COMP>
+__global__ __launch_bounds__(kWideResLanes) void wide_bwd_resident(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
+    typename S::T* __restrict__ dx, typename S::T* __restrict__ dr, float* __restrict__ partials,
+    int64_t rows, int cols, int64_t rpb) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    constexpr int NV = kWideResMaxCols / (W * kWideResLanes);
+    __shared__ float red[2][kWideResLanes / 64];
+    __shared__ __align__(16) float dgl[kWideResMaxCols];
+    const int t = threadIdx.x;
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    const bool want_dg = partials != nullptr;
+    const bool want_dx = dx != nullptr;
+    const float inv_cols = 1.0f / static_cast<float>(cols);
+    // Slot k of lane t: columns (t + k*1024)*W ..  Offsets past the row end
+    // read zeros and drop stores through the row's buffer resource.
+    const uint32_t off0 = static_cast<uint32_t>(t * W) * sizeof(T);
+    constexpr uint32_t kSlotStride = kWideResLanes * W * sizeof(T);
+    const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
+    if (want_dg) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * kWideResLanes) * W;
+            if (col < cols) {
+#pragma unroll
+                for (int e = 0; e < W; e += 4)
+                    *reinterpret_cast<float4*>(dgl + col + e) = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+    int64_t row, step, end;
+    if (rpb > 0) {
+        row = static_cast<int64_t>(blockIdx.x) * rpb;
+        end = row + rpb < rows ? row + rpb : rows;
+        step = 1;
+    } else {
+        row = blockIdx.x;
+        end = rows;
+        step = gridDim.x;
+    }
+    // The row's slots, and the next row's loaded into them slot by slot as
+    // the dx loop frees them (a row past the end reads through a zero-size
+    // resource).
+    u32x4 xv[NV], dv[NV], gv[NV];
+    float r_next = 0.0f;
+    auto issue_slot = [&](int64_t rr, int k) {
+        const uint32_t n = rr < end ? row_bytes : 0u;
+        const int64_t e = (rr < end ? rr : 0) * static_cast<int64_t>(cols);
+        xv[k] = bload16_stream(make_rsrc(x + e, n), off0 + k * kSlotStride);
+        dv[k] = bload16_stream(make_rsrc(dy + e, n), off0 + k * kSlotStride);
+        gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off0 + k * kSlotStride, 0, 0);
+    };
+    auto issue_r = [&](int64_t rr) { r_next = rr < end ? inv_rms[rr] : 0.0f; };
+#pragma unroll
+    for (int k = 0; k < NV; ++k) issue_slot(row, k);
+    issue_r(row);
+    int parity = 0;
+    for (const int64_t first = row; row < end; row += step, parity ^= 1) {
+        const int64_t e0 = row * static_cast<int64_t>(cols);
+        const int64_t next = row + step;
+        const rsrc_t rdr = make_rsrc(COMP ? dr + e0 : dr, COMP ? row_bytes : 0u);
+        const float r = r_next;
+        // Before the row sum: g = dy*gamma (kept for dx), its dot with x, the
+        // composition's dr, and the dgamma terms (they need r, not the sum).
+        float g[NV][W];
+        float part[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) part[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fx[W], fd[W];
+            S::unpack(xv[k], fx);
+            S::unpack(dv[k], fd);
+#pragma unroll
+            for (int e = 0; e < W; ++e) g[k][e] = fd[e];
+            if constexpr (COMP) {
+                float gm[W];
+                u32x4 q;
+                S::unpack(gv[k], gm);
+                stored_product<S>(g[k], gm, q);
+                bstore16_stream(rdr, off0 + k * kSlotStride, q);
+            } else if (gamma) {
+                float gm[W];
+                S::unpack(gv[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) g[k][e] = fd[e] * gm[e];
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[e] += g[k][e] * fx[e];
+            const int col = (t + k * kWideResLanes) * W;
+            if (want_dg && col < cols) {
+                float* a = dgl + col;
+                if constexpr (COMP) {
+                    float h[W];
+#pragma unroll
+                    for (int e = 0; e < W; ++e) h[e] = fx[e] * r;
+                    S::unpack(S::pack(h), h);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) {
+                        const float term = fd[e] * h[e];
+                        a[e] = row == first ? term : acc_add(a[e], term);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) a[e] += fd[e] * (fx[e] * r);
+                }
+            }
+        }
+        if (!want_dx) {  // workgroup-uniform
+#pragma unroll
+            for (int k = 0; k < NV; ++k) issue_slot(next, k);
+            issue_r(next);
+            continue;
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < W; ++e) dot += part[e];
+        dot = row_sum<kWideResLanes, 1>(dot, red, parity);
+        const float s = (r * r * dot) * inv_cols;
+        const rsrc_t rdx = make_rsrc(dx + e0, row_bytes);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fx[W], o[W];
+            S::unpack(xv[k], fx);
+#pragma unroll
+            for (int e = 0; e < W; ++e) o[e] = r * (g[k][e] - fx[e] * s);
+            if constexpr (ACC) {
+                float old[W];
+                S::unpack(bload16_stream(rdx, off0 + k * kSlotStride), old);
+#pragma unroll
+                for (int e = 0; e < W; ++e) o[e] = acc_add(old[e], o[e]);
+            }
+            bstore16_stream(rdx, off0 + k * kSlotStride, S::pack(o));
+            issue_slot(next, k);
+        }
+        issue_r(next);
+    }
+    if (!want_dg) return;
+    float* prow = partials + static_cast<int64_t>(blockIdx.x) * cols;  // any 4-byte alignment
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int col = (t + k * kWideResLanes) * W;
+        if (col < cols) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) prow[col + e] = dgl[col + e];
+        }
+    }
+}
+
+// partials: nblk rows of cols floats when dgamma != nullptr (wide_res_blocking).
+template <class S>
+int launch_wide_res_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
+                        void* dx, void* dr, float* partials, float* dgamma, int64_t rows,
+                        int cols, int acc_dx, int acc_dg, hipStream_t st) {
+    using T = typename S::T;
+    const bool comp = dr != nullptr;
+    int64_t nblk = 0, rpb = 0;
+    wide_res_blocking(rows, comp, nblk, rpb);
+    if (nblk > 0x7fffffffLL) return AGK_EINVAL;
+    const T* xp = static_cast<const T*>(x);
+    const T* gp = static_cast<const T*>(gamma);
+    const T* dyp = static_cast<const T*>(dy);
+    T* dxp = static_cast<T*>(dx);
+    T* drp = static_cast<T*>(dr);
+    float* part = dgamma ? partials : nullptr;
+    const dim3 grid(static_cast<unsigned>(nblk));
+#define AGK_RES(ACC_, COMP_)                                                                  \
+    hipLaunchKernelGGL((wide_bwd_resident<S, ACC_, COMP_>), grid, dim3(kWideResLanes), 0, st, \
+                       xp, gp, inv_rms, dyp, dxp, drp, part, rows, cols, rpb)
+    const bool acc = acc_dx && dx;
+    if (comp) {
+        if (acc) AGK_RES(true, true);
+        else AGK_RES(false, true);
+    } else {
+        if (acc) AGK_RES(true, false);
+        else AGK_RES(false, false);
+    }
+#undef AGK_RES
+    if (int rc = check_launch()) return rc;
+    if (dgamma) return launch_finalize(partials, dgamma, nblk, cols, acc_dg, st);
+    return AGK_OK;
+}

@@ -1,6 +1,7 @@
-"""Rows wider than the register-resident shapes (the split paths: several
+"""Rows wider than the register-resident shapes: the split paths (several
 workgroups per row for the row statistics, row-block x column-chunk tiles for
-dx and dgamma).
+dx and dgamma) and, from 256 rows of at most 32768 columns, the one-pass
+backward (x and dy in registers, dgamma in LDS).
 
 Against the CPU oracle (fp64 accumulation) at sizes it finishes in seconds,
 through the size-independent properties at full sizes, bit-identical across
@@ -50,7 +51,8 @@ def _dt(dtype):
 # (dtype, rows, cols): few very long rows (one row block: dgamma written by the
 # tiles), ragged last segment and chunk, and enough rows for several row
 # blocks (partial rows + finalize) with the forward still split (< 1024 rows)
-# or back on one workgroup per row (>= 1024 rows).
+# or back on one workgroup per row (>= 1024 rows); from 256 rows of at most
+# 32768 columns the one-pass kernel (x and dy in registers, dgamma in LDS).
 WIDE_CASES = [
     ("f32", 8, 262144),
     ("f32", 1, 1 << 20),
@@ -60,9 +62,19 @@ WIDE_CASES = [
     ("bf16", 5, 131080),
     ("bf16", 7, 24576),
     ("f32", 300, 65536),
-    ("f32", 1100, 20480),
     ("bf16", 1030, 40000),
+    ("f32", 255, 32768),
+    ("f32", 1100, 20480),
+    ("f32", 256, 16388),
+    ("f32", 300, 32768),
+    ("bf16", 257, 16392),
+    ("bf16", 1024, 24576),
+    ("bf16", 300, 32768),
 ]
+
+
+def _one_pass(rows, cols):
+    return rows >= 256 and cols <= 32768
 
 
 @pytest.mark.parametrize("dtype,rows,cols", WIDE_CASES, ids=str)
@@ -71,7 +83,11 @@ def test_wide_parity(cuda, dtype, rows, cols):
     bp = agk.launch_plan(rows, cols, _dt(dtype), True)
     label = f"wide {dtype} {rows}x{cols} fwd {fp} bwd {bp}"
     print(label, flush=True)
-    assert bp["tpr"] == 0 and bp["nv"] > 0, "backward should take the split path"
+    if _one_pass(rows, cols):
+        assert bp["tpr"] == 1024 and bp["nv"] == (8 if dtype == "f32" else 4), \
+            "backward should take the one-pass kernel"
+    else:
+        assert bp["tpr"] == 0 and bp["nv"] > 0, "backward should take the split path"
     if fp["tpr"] == 0 and rows < 1024 and (cols % 4 == 0):
         assert fp["nv"] > 0, "forward should take the split path"
     x, g, dy = configs.make_inputs((rows, cols), dtype=dtype, seed=rows * 7 + cols)
@@ -81,7 +97,8 @@ def test_wide_parity(cuda, dtype, rows, cols):
 
 @pytest.mark.slow
 @pytest.mark.parametrize("dtype,rows,cols", [("f32", 4096, 32768), ("bf16", 1024, 65536),
-                                             ("f32", 64, 1 << 21)], ids=str)
+                                             ("f32", 64, 1 << 21), ("bf16", 16384, 20480)],
+                         ids=str)
 def test_wide_full_size_properties(cuda, dtype, rows, cols):
     label = f"wide {dtype} {rows}x{cols}"
     print(label, flush=True)
@@ -96,7 +113,8 @@ def test_wide_no_gamma(cuda):
 
 
 @pytest.mark.parametrize("dtype,rows,cols", [("f32", 5, 40000), ("bf16", 4, 65536),
-                                             ("f32", 1, 1 << 20)], ids=str)
+                                             ("f32", 1, 1 << 20), ("f32", 300, 20480),
+                                             ("bf16", 512, 32768)], ids=str)
 @pytest.mark.parametrize("flags", [agk.AGK_ACCUM_DX, agk.AGK_ACCUM_DGAMMA, agk.AGK_ACCUM_ALL])
 def test_wide_accumulate(cuda, dtype, rows, cols, flags):
     """Each output accumulates on its own (several row blocks through the
@@ -125,11 +143,13 @@ def test_wide_accumulate(cuda, dtype, rows, cols, flags):
         assert bool(((dx.float() - (p + f)).abs() <= bound).all())
 
 
-@pytest.mark.parametrize("dtype,rows,cols", [("f32", 6, 65536), ("bf16", 300, 40000)], ids=str)
+@pytest.mark.parametrize("dtype,rows,cols", [("f32", 6, 65536), ("bf16", 300, 40000),
+                                             ("f32", 400, 24576)], ids=str)
 def test_wide_one_output(cuda, dtype, rows, cols):
     """dx alone (with a workspace) and dgamma alone: bit-identical to the full
-    call's outputs; dx alone without a workspace takes the looped kernel,
-    within the oracle's bar."""
+    call's outputs; dx alone without a workspace takes the looped kernel (the
+    split path needs the workspace; the one-pass kernel does not, and takes
+    it), within the oracle's bar."""
     import torch
     x, g, dy = configs.make_inputs((rows, cols), dtype=dtype, seed=31 + rows)
     xd, gd, dyd = to_dev(x, cuda), to_dev(g, cuda), to_dev(dy, cuda)
@@ -150,7 +170,9 @@ def test_wide_one_output(cuda, dtype, rows, cols):
     torch.cuda.synchronize()
     _, rinv = oracle.fwd(x, g, 1e-6)
     rdx, _ = oracle.bwd(x, g, rinv, dy)
-    for name, t in (("split", full_dx), ("looped", dx_loop)):
+    if _one_pass(rows, cols):
+        assert torch.equal(dx_loop, full_dx)
+    for name, t in (("with workspace", full_dx), ("without", dx_loop)):
         e = dx_rel_err(as_f32(to_host(t)), as_f32(rdx), as_f32(x), as_f32(g), as_f32(dy), 1e-6)
         print(f"[{dtype} {rows}x{cols} dx {name}] {e:.2e}", flush=True)
         assert e <= _tol(x)

@@ -50,11 +50,12 @@ def _pair(cuda, rows, cols, dtype, accumulate, seed):
 # (rows, cols, dtype, accumulate bits): each call smaller than the one before it;
 # the register-resident kernel (256 partial rows), the split path for wide rows
 # (partial rows, segment sums and coefficients; then one row block writing
-# dgamma directly), the looped kernel (unaligned rows, one partial row per row
+# dgamma directly), the one-pass kernel for 256+ rows of up to 32768 columns, the looped kernel (unaligned rows, one partial row per row
 # block) and the few-rows kernel (no partials).
 CALLS = [
     (16384, 4096, "f32", 0),
     (300, 65536, "f32", agk.AGK_ACCUM_ALL),
+    (512, 24576, "bf16", agk.AGK_ACCUM_DGAMMA),
     (1000, 1536, "bf16", agk.AGK_ACCUM_ALL),
     (600, 1001, "f32", agk.AGK_ACCUM_DGAMMA),
     (51, 13824, "f32", 0),
