@@ -1,6 +1,6 @@
 // rmsnorm_wide.hpp -- the RMSNorm forward and backward for rows wider than the
-// register-resident shapes hold (more than 4096 16-byte slots: 16384 fp32 or
-// 32768 bf16 columns; 16384 bf16 columns and up for the backward), with every
+// register-resident shapes hold (forward: more than 8192 16-byte slots, 32768
+// fp32 or 65536 bf16 columns; backward: more than 16384 columns), with every
 // row 16-byte aligned.  Included by rmsnorm.hip inside namespace agk.
 //
 // A row is cut into segments of kWideSegCols columns for its statistics and
