@@ -144,6 +144,9 @@ __device__ __forceinline__ void row_reduce(float (&v)[N],
 //   sum2(f, s0, s1)                  f(a, b, o) fills o[2]; both summed
 //   sum_keep(f)                      sum of f(a, b) over the row, keeping the
 //                                    values where the row is held in registers
+//   max_sumexp<KEEP>(m, s)           m = max over the row of a, s = sum of
+//                                    fast_exp(a - m) (KEEP: kept as sum_keep
+//                                    keeps them); one online pass in LoopedVec
 //   store_kept(out, acc, f, g)       out[col] (+)= g(f(a, b)), f's values as
 //                                    kept by the last sum_keep (recomputed by
 //                                    the looped context)
@@ -241,6 +244,17 @@ struct Resident {
         reduce<SumR>(r, f);
         s0 = r[0];
         s1 = r[1];
+    }
+
+    template <bool KEEP>
+    __device__ __forceinline__ void max_sumexp(float& m, float& s) {
+        m = max([](float z, float) { return z; });
+        const float mm = m;
+        auto e = [=](float z, float) { return fast_exp(z - mm); };
+        if constexpr (KEEP)
+            s = sum_keep(e);
+        else
+            s = sum(e);
     }
 
     template <class F>
@@ -396,6 +410,17 @@ struct Looped {
         s1 = r[1];
     }
 
+    template <bool KEEP>
+    __device__ __forceinline__ void max_sumexp(float& m, float& s) {
+        m = max([](float z, float) { return z; });
+        const float mm = m;
+        auto e = [=](float z, float) { return fast_exp(z - mm); };
+        if constexpr (KEEP)
+            s = sum_keep(e);
+        else
+            s = sum(e);
+    }
+
     template <class F>
     __device__ __forceinline__ float sum_keep(F f) {
         return sum(f);
@@ -423,6 +448,217 @@ struct Looped {
             if (acc) r = acc_add(S::get(o + c), r);
             S::put(o + c, r);
         }
+    }
+
+    __device__ float row_f32(const float* p) const { return p[row]; }
+    __device__ float row_val(const void* p) const {
+        return S::get(static_cast<const T*>(p) + row);
+    }
+    __device__ void put_f32(float* p, float v) const {
+        if (threadIdx.x == 0) p[row] = v;
+    }
+    __device__ void put_val(void* p, float v) const {
+        if (threadIdx.x == 0) S::put(static_cast<T*>(p) + row, v);
+    }
+};
+
+// Rows too wide for the resident shapes but whole 16-byte slots, with every
+// pointer 16-byte aligned: one 1024-lane workgroup per row, as Looped, but each
+// pass streams the row in 16-byte slots, four slots per lane in flight, through
+// buffer resources (a slot past the row end reads zeros and is skipped).  Each
+// pass re-reads the row: with 1024-lane workgroups only a few hundred rows are
+// in flight, so the re-reads of a row mostly hit the Infinity Cache.  The
+// per-lane order is slot by slot, element by element, then the row tree, fixed
+// by cols.
+constexpr int kVecLanes = 1024;
+constexpr int kVecBatch = 4;
+
+template <class S, int NIN>
+struct LoopedVec {
+    using T = typename S::T;
+    static constexpr int W = S::kVec;
+    static constexpr int kSlots = red_slots<kVecLanes, 1>();
+
+    float (*red)[kSlots];
+    int parity = 0;
+    int64_t row;
+    int cols, nslot;
+    float ncols, inv_cols;
+    const T* x;
+    const T* y;
+    uint32_t row_bytes;
+
+    __device__ LoopedVec(const RowArgs& p, int64_t row_, int cols_, float (*red_)[kSlots])
+        : red(red_), row(row_), cols(cols_) {
+        ncols = static_cast<float>(cols);
+        inv_cols = 1.0f / ncols;
+        nslot = cols / W;
+        row_bytes = static_cast<uint32_t>(cols) * static_cast<uint32_t>(sizeof(T));
+        const int64_t off = row * static_cast<int64_t>(cols);
+        x = static_cast<const T*>(p.in0) + off;
+        y = NIN == 2 ? static_cast<const T*>(p.in1) + off : nullptr;
+    }
+
+    template <class R, int N, class F>
+    __device__ __forceinline__ void reduce(float (&res)[N], F f) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) res[i] = R::kId;
+        const rsrc_t rx = make_rsrc(x, row_bytes);
+        const rsrc_t ry = make_rsrc(NIN == 2 ? y : x, NIN == 2 ? row_bytes : 0u);
+        for (int base = threadIdx.x; base < nslot; base += kVecLanes * kVecBatch) {
+            u32x4 va[kVecBatch], vb[kVecBatch];
+#pragma unroll
+            for (int k = 0; k < kVecBatch; ++k) {
+                const uint32_t o = static_cast<uint32_t>(base + k * kVecLanes) * 16u;
+                va[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+                if constexpr (NIN == 2) vb[k] = __builtin_amdgcn_raw_buffer_load_b128(ry, o, 0, 0);
+            }
+#pragma unroll
+            for (int k = 0; k < kVecBatch; ++k) {
+                if (base + k * kVecLanes >= nslot) break;
+                float fa[W], fb[W];
+                S::unpack(va[k], fa);
+                if constexpr (NIN == 2) {
+                    S::unpack(vb[k], fb);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) fb[e] = 0.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    float o[N];
+                    f(fa[e], fb[e], o);
+#pragma unroll
+                    for (int i = 0; i < N; ++i) res[i] = R::op(res[i], o[i]);
+                }
+            }
+        }
+        row_reduce<kVecLanes, 1, N, R>(res, red, parity);
+        parity ^= 1;
+    }
+
+    template <class F>
+    __device__ __forceinline__ float sum(F f) {
+        float r[1];
+        reduce<SumR>(r, [&](float a, float b, float (&o)[1]) { o[0] = f(a, b); });
+        return r[0];
+    }
+    template <class F>
+    __device__ __forceinline__ float max(F f) {
+        float r[1];
+        reduce<MaxR>(r, [&](float a, float b, float (&o)[1]) { o[0] = f(a, b); });
+        return r[0];
+    }
+    template <class F>
+    __device__ __forceinline__ void sum2(F f, float& s0, float& s1) {
+        float r[2];
+        reduce<SumR>(r, f);
+        s0 = r[0];
+        s1 = r[1];
+    }
+
+    // One pass: per lane, each slot's maximum mn = max(m, slot max) and
+    // s = s * exp(m - mn) + sum over the slot of exp(a - mn) (a slot that
+    // leaves mn at -inf changes nothing); then M = the row maximum of m and
+    // s = the row sum of s * exp(m - M), both over the row tree.
+    template <bool KEEP>
+    __device__ __forceinline__ void max_sumexp(float& m_out, float& s_out) {
+        float m = -__builtin_inff(), s = 0.0f;
+        const rsrc_t rx = make_rsrc(x, row_bytes);
+        for (int base = threadIdx.x; base < nslot; base += kVecLanes * kVecBatch) {
+            u32x4 va[kVecBatch];
+#pragma unroll
+            for (int k = 0; k < kVecBatch; ++k)
+                va[k] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rx, static_cast<uint32_t>(base + k * kVecLanes) * 16u, 0, 0);
+#pragma unroll
+            for (int k = 0; k < kVecBatch; ++k) {
+                if (base + k * kVecLanes >= nslot) break;
+                float f[W];
+                S::unpack(va[k], f);
+                float sm = f[0];
+#pragma unroll
+                for (int e = 1; e < W; ++e) sm = fmaxf(sm, f[e]);
+                const float mn = fmaxf(m, sm);
+                if (mn != -__builtin_inff()) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < W; ++e) t += fast_exp(f[e] - mn);
+                    s = s * fast_exp(m - mn) + t;
+                    m = mn;
+                }
+            }
+        }
+        float r[1] = {m};
+        row_reduce<kVecLanes, 1, 1, MaxR>(r, red, parity);
+        parity ^= 1;
+        const float M = r[0];
+        float q[1] = {M == -__builtin_inff() ? 0.0f : s * fast_exp(m - M)};
+        row_reduce<kVecLanes, 1, 1, SumR>(q, red, parity);
+        parity ^= 1;
+        m_out = M;
+        s_out = q[0];
+    }
+
+    template <class F>
+    __device__ __forceinline__ float sum_keep(F f) {
+        return sum(f);
+    }
+
+    // out (+)= h(a, b, u, v) per element, u and v from the column vectors c0,
+    // c1 (d0, d1 when null), the row's slots streamed as in reduce.
+    template <class H>
+    __device__ __forceinline__ void store_each(void* out, int acc, const void* c0, float d0,
+                                               const void* c1, float d1, H h) const {
+        T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
+        const rsrc_t rx = make_rsrc(x, row_bytes);
+        const rsrc_t ry = make_rsrc(NIN == 2 ? y : x, NIN == 2 ? row_bytes : 0u);
+        const rsrc_t ro = make_rsrc(o, row_bytes);
+        const rsrc_t ru = make_rsrc(c0 ? c0 : x, c0 ? row_bytes : 0u);
+        const rsrc_t rv = make_rsrc(c1 ? c1 : x, c1 ? row_bytes : 0u);
+        for (int base = threadIdx.x; base < nslot; base += kVecLanes * kVecBatch) {
+            u32x4 va[kVecBatch], vb[kVecBatch], vu[kVecBatch], vv[kVecBatch], vo[kVecBatch];
+#pragma unroll
+            for (int k = 0; k < kVecBatch; ++k) {
+                const uint32_t off = static_cast<uint32_t>(base + k * kVecLanes) * 16u;
+                va[k] = bload16_stream(rx, off);
+                if constexpr (NIN == 2) vb[k] = bload16_stream(ry, off);
+                if (c0) vu[k] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0);
+                if (c1) vv[k] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+                if (acc) vo[k] = bload16_stream(ro, off);
+            }
+#pragma unroll
+            for (int k = 0; k < kVecBatch; ++k) {
+                const uint32_t off = static_cast<uint32_t>(base + k * kVecLanes) * 16u;
+                float fa[W], fb[W], fu[W], fv[W], r[W];
+                S::unpack(va[k], fa);
+                if constexpr (NIN == 2) S::unpack(vb[k], fb);
+                if (c0) S::unpack(vu[k], fu);
+                if (c1) S::unpack(vv[k], fv);
+#pragma unroll
+                for (int e = 0; e < W; ++e)
+                    r[e] = h(fa[e], NIN == 2 ? fb[e] : 0.0f, c0 ? fu[e] : d0, c1 ? fv[e] : d1);
+                if (acc) {
+                    float old[W];
+                    S::unpack(vo[k], old);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) r[e] = acc_add(old[e], r[e]);
+                }
+                bstore16_stream(ro, off, S::pack(r));  // past the row end: dropped
+            }
+        }
+    }
+
+    template <class F, class Gf>
+    __device__ __forceinline__ void store_kept(void* out, int acc, F f, Gf g) const {
+        store_each(out, acc, nullptr, 0.0f, nullptr, 0.0f,
+                   [&](float a, float b, float, float) { return g(f(a, b)); });
+    }
+
+    template <class F>
+    __device__ __forceinline__ void store(void* out, int acc, const void* c0, float d0,
+                                          const void* c1, float d1, F f) const {
+        store_each(out, acc, c0, d0, c1, d1, f);
     }
 
     __device__ float row_f32(const float* p) const { return p[row]; }
@@ -508,9 +744,10 @@ struct SmFwd {
     static constexpr int kIn = 1;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
-        const float m = c.max([](float z, float) { return z; });
+        float m, s;
+        c.template max_sumexp<true>(m, s);
         auto e = [=](float z, float) { return fast_exp(z - m); };
-        const float inv = 1.0f / c.sum_keep(e);
+        const float inv = 1.0f / s;
         c.store_kept(p.out, 0, e, [=](float v) { return v * inv; });
     }
 };
@@ -532,8 +769,8 @@ struct LseFwd {
     static constexpr int kIn = 1;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
-        const float m = c.max([](float z, float) { return z; });
-        const float s = c.sum([=](float z, float) { return fast_exp(z - m); });
+        float m, s;
+        c.template max_sumexp<false>(m, s);
         c.put_val(p.out_row, logf(s) + m);
     }
 };
@@ -544,9 +781,10 @@ struct LseBwd {
     static constexpr int kIn = 1;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
-        const float m = c.max([](float z, float) { return z; });
+        float m, s;
+        c.template max_sumexp<true>(m, s);
         auto e = [=](float z, float) { return fast_exp(z - m); };
-        const float inv = 1.0f / c.sum_keep(e);
+        const float inv = 1.0f / s;
         const float g = c.row_val(p.rsv);
         c.store_kept(p.out, p.acc, e, [=](float v) { return g * (v * inv); });
     }
@@ -582,6 +820,17 @@ __global__ __launch_bounds__(TPR * G) void row_resident(const RowArgs p, int64_t
 }
 
 template <class S, class Op>
+__global__ __launch_bounds__(kVecLanes) void row_looped_vec(const RowArgs p, int64_t rows,
+                                                           int cols) {
+    using Ctx = LoopedVec<S, Op::kIn>;
+    __shared__ float red[2][Ctx::kSlots];
+    const int64_t row = blockIdx.x;
+    if (row >= rows) return;  // workgroup-uniform
+    Ctx c(p, row, cols, red);
+    Op::run(c, p);
+}
+
+template <class S, class Op>
 __global__ __launch_bounds__(kBlock) void row_looped(const RowArgs p, int64_t rows, int cols) {
     using Ctx = Looped<S, Op::kIn>;
     __shared__ float red[2][Ctx::kSlots];
@@ -602,8 +851,13 @@ int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
     if (vec) pl = fwd_plan(cols / S::kVec, rows);
     if (pl.tpr == 0) {
         if (rows > 0x7fffffffLL) return AGK_EINVAL;
-        hipLaunchKernelGGL((row_looped<S, Op>), dim3(static_cast<unsigned>(rows)), dim3(kBlock),
-                           0, st, p, rows, cols);
+        // whole 16-byte slots, aligned, rows short enough for 32-bit buffer offsets
+        if (vec && static_cast<uint64_t>(cols) * sizeof(typename S::T) < 0x80000000ull)
+            hipLaunchKernelGGL((row_looped_vec<S, Op>), dim3(static_cast<unsigned>(rows)),
+                               dim3(kVecLanes), 0, st, p, rows, cols);
+        else
+            hipLaunchKernelGGL((row_looped<S, Op>), dim3(static_cast<unsigned>(rows)),
+                               dim3(kBlock), 0, st, p, rows, cols);
         return check_launch();
     }
     const int64_t grid = (rows + pl.g - 1) / pl.g;

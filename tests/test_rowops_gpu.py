@@ -12,7 +12,7 @@ fp32 storage 1e-5, bf16 storage 1e-2, per row, relative to the row's scale:
   - per-row statistics (mean, rstd): 1e-5 (fp32 arithmetic either way).
 Also covered: every resident launch shape (at its narrowest and widest
 width, below and above the large-batch threshold), widths that take the
-looped kernel, misaligned pointers, masked (-inf) entries, accumulation,
+looped kernels (16-byte and element-wise), misaligned pointers, masked (-inf) entries, accumulation,
 run-to-run determinism and full-size configurations through properties.
 """
 from __future__ import annotations
@@ -28,8 +28,12 @@ from tolerances import TOL_BF16, TOL_F32
 pytestmark = pytest.mark.gpu
 
 OPS = ("rmsnorm_jvp", "layernorm", "softmax", "logsumexp")
+# ... including vocabulary widths past the resident shapes (128256 = Llama 3's
+# vocabulary): aligned rows take the 16-byte looped kernel, 131076 bf16 (not a
+# whole number of 8-element slots) the element-wise one.
 SHAPES = [(5, 1), (3, 3), (17, 13), (9, 100), (33, 127), (65, 129), (8, 1000), (37, 4096),
-          (4, 4099), (2, 40000), (300, 64), (1000, 128), (512, 512), (64, 5120), (3, 65536)]
+          (4, 4099), (2, 40000), (300, 64), (1000, 128), (512, 512), (64, 5120), (3, 65536),
+          (4, 128256), (2, 131076), (1, 262144)]
 EPS = 1e-5
 
 
@@ -269,9 +273,10 @@ def test_misaligned_pointers_take_the_looped_kernel(cuda, op, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_backward_accumulates(cuda, dtype):
+@pytest.mark.parametrize("shape", [(40, 384), (3, 131072)], ids=str)
+def test_backward_accumulates(cuda, dtype, shape):
     import torch
-    x, g, dy = device_inputs((40, 384), dtype, 5, cuda)
+    x, g, dy = device_inputs(shape, dtype, 5, cuda)
     pre = torch.randn(x.shape, device=cuda).to(x.dtype)
     y, mean, rstd = agk.layernorm_fwd(x)
     outs = {
@@ -294,26 +299,28 @@ def test_backward_accumulates(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_masked_entries(cuda, dtype):
+@pytest.mark.parametrize("cols", [96, 131072])
+def test_masked_entries(cuda, dtype, cols):
     """-inf entries (masked logits) get probability 0 and drop out of the log-sum-exp."""
     import torch
-    z = torch.randn(16, 96, device=cuda) * 3
+    z = torch.randn(16, cols, device=cuda) * 3
     z[:, ::3] = float("-inf")
     z = z.to(torch.bfloat16 if dtype == "bf16" else torch.float32).contiguous()
     y = agk.softmax_fwd(z)
     lse = agk.logsumexp_fwd(z)
     torch.cuda.synchronize()
     assert torch.all(y[:, ::3] == 0)
-    keep = z.float()[:, [j for j in range(96) if j % 3]]
+    keep = z.float()[:, [j for j in range(cols) if j % 3]]
     want = torch.logsumexp(keep.double(), -1, keepdim=True)
     assert float((lse.double() - want).abs().max()) <= _tol(dtype == "bf16") * float(
         want.abs().max())
     assert float((y.double().sum(-1) - 1).abs().max()) <= 2 * _tol(dtype == "bf16")
 
 
-def test_results_are_deterministic(cuda):
+@pytest.mark.parametrize("shape", [(4099, 1000), (7, 131072)], ids=str)
+def test_results_are_deterministic(cuda, shape):
     import torch
-    x, g, dy = device_inputs((4099, 1000), "f32", 3, cuda)
+    x, g, dy = device_inputs(shape, "f32", 3, cuda)
     first = None
     for _ in range(3):
         y, mean, rstd = agk.layernorm_fwd(x)
