@@ -906,6 +906,68 @@ def run_wide(steps):
     return out
 
 
+WIDE_ROWOP_SHAPES = (("bf16", 8192, 128256), ("f32", 8192, 128256), ("bf16", 4096, 151936),
+                     ("bf16", 16, 128256))
+
+
+def run_wide_rowops(steps):
+    """Softmax and log-sum-exp over vocabulary-wide rows (past the resident
+    shapes): on 16-byte aligned tensors (the 16-byte looped kernel, online
+    max/sum pass) against the same values in views one element off a 16-byte
+    boundary (the element-wise looped kernel), graph-replayed.  GB/s are
+    algorithmic bytes: softmax forward 2 tensors, backward 3, log-sum-exp
+    forward 1, backward 2 (the [rows] vectors aside)."""
+    import torch
+
+    import cgadimpl_amd as agk
+    dev = torch.device("cuda:0")
+    out = []
+    for dtype, rows, cols in WIDE_ROWOP_SHAPES:
+        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(rows + cols)
+
+        def tensors(shift):
+            def make(vals):
+                buf = torch.empty(rows * cols + 8, dtype=tdt, device=dev)
+                v = buf[shift:shift + rows * cols].view(rows, cols)
+                v.copy_(vals)
+                return v
+            z = make((torch.randn(rows, cols, generator=gen, device=dev) * 4).to(tdt))
+            dy = make(torch.randn(rows, cols, generator=gen, device=dev).to(tdt))
+            y, dz = make(torch.zeros(rows, cols, dtype=tdt, device=dev)), make(
+                torch.zeros(rows, cols, dtype=tdt, device=dev))
+            lse = torch.empty(rows, 1, dtype=tdt, device=dev)
+            dl = torch.randn(rows, 1, generator=gen, device=dev).to(tdt)
+            return z, dy, y, dz, lse, dl
+
+        n = max(1, steps)
+        rec = {"wide_rowops": f"{dtype} {rows}x{cols}", "dtype": dtype, "rows": rows,
+               "cols": cols, "calls_per_graph": n, "us": {}, "gbs": {}}
+        es = 4 if dtype == "f32" else 2
+        tb = rows * cols * es
+        for tag, shift in (("vec", 0), ("scalar", 1)):
+            z, dy, y, dz, lse, dl = tensors(shift)
+            t = {
+                "softmax_fwd": (graph_replay_ms(
+                    lambda i, st: agk.softmax_fwd(z, y=y, stream=st), n), 2),
+                "softmax_bwd": (graph_replay_ms(
+                    lambda i, st: agk.softmax_bwd(y, dy, dz=dz, stream=st), n), 3),
+                "logsumexp_fwd": (graph_replay_ms(
+                    lambda i, st: agk.logsumexp_fwd(z, y=lse, stream=st), n), 1),
+                "logsumexp_bwd": (graph_replay_ms(
+                    lambda i, st: agk.logsumexp_bwd(z, dl, dz=dz, stream=st), n), 2),
+            }
+            for k, (ms, passes) in t.items():
+                rec["us"][f"{k}_{tag}"] = round(ms * 1e3, 1)
+                rec["gbs"][f"{k}_{tag}"] = round(passes * tb / (ms * 1e-3) / 1e9, 1)
+            del z, dy, y, dz, lse, dl
+            torch.cuda.empty_cache()
+        print(json.dumps(rec), flush=True)
+        out.append(rec)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -930,7 +992,9 @@ def main():
                          "only; plain and non-temporal) over MIB-MiB buffers, then exit")
     ap.add_argument("--wide", action="store_true",
                     help="only time rows wider than the register-resident kernels: the split "
-                         "paths against the one-workgroup-per-row kernels, then exit")
+                         "paths against the one-workgroup-per-row kernels, and softmax / "
+                         "log-sum-exp at vocabulary widths (16-byte against element-wise "
+                         "looped kernels), then exit")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe(args.copy_probe, args.steps)
@@ -940,6 +1004,7 @@ def main():
         return
     if args.wide:
         run_wide(min(args.steps, 20))
+        run_wide_rowops(min(args.steps, 10))
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -578,8 +578,8 @@ struct LoopedVec {
                 S::unpack(va[k], f);
                 float sm = f[0];
 #pragma unroll
-                for (int e = 1; e < W; ++e) sm = fmaxf(sm, f[e]);
-                const float mn = fmaxf(m, sm);
+                for (int e = 1; e < W; ++e) sm = MaxR::op(sm, f[e]);
+                const float mn = MaxR::op(m, sm);
                 if (mn != -__builtin_inff()) {
                     float t = 0.0f;
 #pragma unroll

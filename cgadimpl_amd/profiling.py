@@ -438,6 +438,24 @@ def write_wide_summary(jsonl, out_md, command):
                      f"{u['bwd_dx_split']} | {u['bwd_dx_looped']} | {u['bwd_split']} | "
                      f"{g['fwd_split']:.0f} ({g['fwd_split'] / 80:.1f} %) | "
                      f"{g['bwd_split']:.0f} ({g['bwd_split'] / 80:.1f} %) |")
+    ro = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"wide_rowops"')]
+    if ro:
+        lines += ["", "## Softmax and log-sum-exp at vocabulary widths", "",
+                  "16-byte aligned tensors (the 16-byte looped kernel, with one online pass "
+                  "for the row maximum and sum of exponentials) against views of the same "
+                  "values one element off a 16-byte boundary (the element-wise looped "
+                  "kernel), graph-replayed µs per call; % of 8 TB/s for the aligned call "
+                  "(algorithmic bytes: softmax forward 2 tensors, backward 3, log-sum-exp "
+                  "forward 1, backward 2).", "",
+                  "| shape | softmax fwd | softmax bwd | log-sum-exp fwd | log-sum-exp bwd |",
+                  "|---|---|---|---|---|"]
+        for r in ro:
+            u, g = r["us"], r["gbs"]
+            cells = []
+            for k in ("softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd"):
+                cells.append(f"{u[k + '_vec']} / {u[k + '_scalar']} "
+                             f"({g[k + '_vec'] / 80:.1f} %)")
+            lines.append(f"| {r['wide_rowops']} | " + " | ".join(cells) + " |")
     with open(out_md, "w") as fh:
         fh.write("\n".join(lines) + "\n")
 
