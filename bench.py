@@ -832,7 +832,8 @@ def stream_probe(mib, steps):
 
 WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
                ("f32", 256, 65536), ("f32", 4096, 32768), ("bf16", 8, 262144),
-               ("bf16", 51, 32768), ("bf16", 1024, 65536), ("bf16", 16384, 20480))
+               ("bf16", 51, 32768), ("bf16", 1024, 65536), ("bf16", 16384, 20480),
+               ("f32", 2048, 65536), ("bf16", 8192, 131072))
 
 
 def run_wide(steps):
@@ -840,8 +841,8 @@ def run_wide(steps):
     the one-workgroup-per-row kernels on the same build, each call captured
     `steps` times into a HIP graph and replayed (GPU time per call).
 
-    forward: out of place (split when fewer than 1024 rows) against in place
-    (y = x, which keeps one workgroup per row); dx alone: with a workspace
+    forward: out of place (split when the row is too wide for registers)
+    against in place (y = x, which keeps one workgroup per row); dx alone: with a workspace
     (split) against without one (looped); and the full backward (dx and
     dgamma, split).  One JSON line per shape; GB/s are algorithmic bytes
     (forward 2 tensors, backward 3) over the time.

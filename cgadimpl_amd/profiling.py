@@ -424,8 +424,8 @@ def write_wide_summary(jsonl, out_md, command):
     lines = ["# Rows wider than the register-resident kernels (MI355X, one GPU)", "",
              "Command:", "", "```", command, "```", "",
              "Each call captured into a HIP graph and replayed (GPU time per call, best of 5 "
-             "replays). Forward: out of place (the split path below 1024 rows) against in "
-             "place (y = x keeps one workgroup per row). dx alone: with a workspace (split) "
+             "replays). Forward: out of place (the split path for rows too wide for "
+             "registers) against in place (y = x keeps one workgroup per row). dx alone: with a workspace (split) "
              "against without (looped). Backward: dx and dgamma (split). GB/s: algorithmic "
              "bytes (forward 2 tensors, backward 3) over the time; % of 8 TB/s in brackets.",
              "",

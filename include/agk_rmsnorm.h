@@ -81,9 +81,9 @@ typedef enum {
  * gamma == NULL means no scale (ag::rms alone).  inv_rms[rows] receives
  * r = 1/sqrt(mean(x^2)+eps) per row, which the backward reads (the reference
  * keeps the same tensor on the node's tape, normalization.cpp:29).
- * y may be x itself (in place).  Fewer than 1024 rows too wide for the
- * resident kernels use y's first bytes of each row for partial sums until
- * the last of the call's kernels overwrites them; an in-place call takes the
+ * y may be x itself (in place).  Rows too wide for the resident kernels
+ * use y's first bytes of each row for partial sums until the last of the
+ * call's kernels overwrites them; an in-place call takes the
  * one-workgroup-per-row kernel instead.                                      */
 int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
                     int64_t rows, int64_t cols, float eps, int dtype,

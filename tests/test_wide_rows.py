@@ -50,9 +50,8 @@ def _dt(dtype):
 
 # (dtype, rows, cols): few very long rows (one row block: dgamma written by the
 # tiles), ragged last segment and chunk, and enough rows for several row
-# blocks (partial rows + finalize) with the forward still split (< 1024 rows)
-# or back on one workgroup per row (>= 1024 rows); from 256 rows of at most
-# 32768 columns the one-pass kernel (x and dy in registers, dgamma in LDS).
+# blocks (partial rows + finalize); from 256 rows of at most 32768 columns the
+# one-pass backward (x and dy in registers, dgamma in LDS).
 WIDE_CASES = [
     ("f32", 8, 262144),
     ("f32", 1, 1 << 20),
@@ -63,6 +62,8 @@ WIDE_CASES = [
     ("bf16", 7, 24576),
     ("f32", 300, 65536),
     ("bf16", 1030, 40000),
+    ("f32", 1100, 40000),
+    ("bf16", 1030, 65544),
     ("f32", 255, 32768),
     ("f32", 1100, 20480),
     ("f32", 256, 16388),
@@ -88,7 +89,7 @@ def test_wide_parity(cuda, dtype, rows, cols):
             "backward should take the one-pass kernel"
     else:
         assert bp["tpr"] == 0 and bp["nv"] > 0, "backward should take the split path"
-    if fp["tpr"] == 0 and rows < 1024 and (cols % 4 == 0):
+    if fp["tpr"] == 0:
         assert fp["nv"] > 0, "forward should take the split path"
     x, g, dy = configs.make_inputs((rows, cols), dtype=dtype, seed=rows * 7 + cols)
     got = gpu_layer(x, g, dy, 1e-6, cuda)
