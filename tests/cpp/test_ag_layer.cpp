@@ -151,8 +151,15 @@ void test_fused_layer_gradients() {
     check_grad("rms_norm dgamma numerical gradient", g, f);
 }
 
+void fused_matches_unfused_case(int64_t R, int64_t D);
+
 void test_fused_matches_unfused() {
-    const int64_t R = 64, D = 256;
+    fused_matches_unfused_case(64, 256);
+    fused_matches_unfused_case(3, 40000);  // split paths for wide rows
+    fused_matches_unfused_case(260, 20480);  // one-pass backward for wide rows
+}
+
+void fused_matches_unfused_case(int64_t R, int64_t D) {
     std::vector<float> xv = normal(R * D, 5), gv = uniform(D, 6, 0.5, 1.5), dyv = normal(R * D, 7);
     Tensor dy = Tensor::from_host_f32(dyv, {R, D});
     Value x1 = leaf(xv, {R, D}, "x1"), g1 = leaf(gv, {1, D}, "g1");
@@ -167,14 +174,15 @@ void test_fused_matches_unfused() {
                       max_abs(x2.grad().to_host_f32());
     const double eg = max_abs_diff(g1.grad().to_host_f32(), g2.grad().to_host_f32()) /
                       max_abs(g2.grad().to_host_f32());
-    report("rms_norm(x, g) == rms(x) * g", ey <= 1e-5 && ex <= 1e-5 && eg <= 1e-5,
+    const std::string shape = " [" + std::to_string(R) + "," + std::to_string(D) + "]";
+    report(("rms_norm(x, g) == rms(x) * g" + shape).c_str(), ey <= 1e-5 && ex <= 1e-5 && eg <= 1e-5,
            "y " + std::to_string(ey) + " dx " + std::to_string(ex) + " dgamma " +
                std::to_string(eg));
     // gamma * rms(x): the broadcast operand first
     Value x3 = leaf(xv, {R, D}, "x3"), g3 = leaf(gv, {D}, "g3");
     Value y3 = g3 * rms(x3);
     backward(y3, &dy);
-    report("gamma * rms(x) == rms(x) * gamma",
+    report(("gamma * rms(x) == rms(x) * gamma" + shape).c_str(),
            y3.val().to_host_f32() == y2.val().to_host_f32() &&
                x3.grad().to_host_f32() == x2.grad().to_host_f32() &&
                g3.grad().to_host_f32() == g2.grad().to_host_f32());
@@ -232,8 +240,11 @@ void composition_case(const char* name, int64_t R, int64_t D, Dtype dt, bool par
     const int rc1 = agk_mul_rowbcast_bwd(dy.data(), h.val().data(), g.val().data(), dr.data(),
                                          static_cast<float*>(dg.data()), ws.data(), wsb, R, D,
                                          dtc, 0, st);
+    // as vjp_RMSNorm calls it: a workspace for rows of AGK_WIDE_MIN_COLS or more
+    const bool wide = D >= AGK_WIDE_MIN_COLS;
     const int rc2 = agk_rmsnorm_bwd(x.val().data(), nullptr, static_cast<const float*>(inv.data()),
-                                    dr.data(), dx.data(), nullptr, nullptr, 0, R, D, dtc, 0, st);
+                                    dr.data(), dx.data(), nullptr, wide ? ws.data() : nullptr,
+                                    wide ? wsb : 0, R, D, dtc, 0, st);
     const bool same = rc1 == AGK_OK && rc2 == AGK_OK && bytes_of(h.grad()) == bytes_of(dr) &&
                       bytes_of(x.grad()) == bytes_of(dx) && bytes_of(g.grad()) == bytes_of(dg);
     report(name, fused && same,
@@ -253,6 +264,10 @@ void test_composition_backward() {
                      Dtype::Float32, false, false, false);
     composition_case("... bf16 [17,100] (looped kernel)", 17, 100, Dtype::BFloat16, true, false,
                      false);
+    composition_case("... f32 [3,40000] (split path for wide rows)", 3, 40000, Dtype::Float32,
+                     false, false, false);
+    composition_case("... bf16 [300,24576] (one-pass kernel for wide rows)", 300, 24576,
+                     Dtype::BFloat16, true, false, false);
 
     // rms(x) with a second consumer: the one-pass rule must not fire (its
     // gradient is not final when the Mul runs); checked numerically.
