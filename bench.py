@@ -908,16 +908,18 @@ def run_wide(steps):
 
 
 WIDE_ROWOP_SHAPES = (("bf16", 8192, 128256), ("f32", 8192, 128256), ("bf16", 4096, 151936),
-                     ("bf16", 16, 128256))
+                     ("bf16", 16, 128256), ("bf16", 8192, 50257), ("f32", 8192, 50257))
 
 
 def run_wide_rowops(steps):
     """Softmax and log-sum-exp over vocabulary-wide rows (past the resident
-    shapes): on 16-byte aligned tensors (the 16-byte looped kernel, online
-    max/sum pass) against the same values in views one element off a 16-byte
-    boundary (the element-wise looped kernel), graph-replayed.  GB/s are
-    algorithmic bytes: softmax forward 2 tensors, backward 3, log-sum-exp
-    forward 1, backward 2 (the [rows] vectors aside)."""
+    shapes, or not whole 16-byte slots), graph-replayed, on the same values in
+    three layouts: 16-byte aligned tensors ("vec"); every tensor one element
+    off a 16-byte boundary ("offset": the head/body/tail form of the 16-byte
+    looped kernel); the inputs one element off and the outputs aligned
+    ("scalar": the element-wise looped kernel; log-sum-exp forward has no row
+    output, so it has no such layout).  GB/s are algorithmic bytes: softmax
+    forward 2 tensors, backward 3, log-sum-exp forward 1, backward 2."""
     import torch
 
     import cgadimpl_amd as agk
@@ -928,16 +930,16 @@ def run_wide_rowops(steps):
         gen = torch.Generator(device=dev)
         gen.manual_seed(rows + cols)
 
-        def tensors(shift):
-            def make(vals):
+        def tensors(shift_in, shift_out):
+            def make(vals, shift):
                 buf = torch.empty(rows * cols + 8, dtype=tdt, device=dev)
                 v = buf[shift:shift + rows * cols].view(rows, cols)
                 v.copy_(vals)
                 return v
-            z = make((torch.randn(rows, cols, generator=gen, device=dev) * 4).to(tdt))
-            dy = make(torch.randn(rows, cols, generator=gen, device=dev).to(tdt))
-            y, dz = make(torch.zeros(rows, cols, dtype=tdt, device=dev)), make(
-                torch.zeros(rows, cols, dtype=tdt, device=dev))
+            z = make((torch.randn(rows, cols, generator=gen, device=dev) * 4).to(tdt), shift_in)
+            dy = make(torch.randn(rows, cols, generator=gen, device=dev).to(tdt), shift_in)
+            zero = torch.zeros(rows, cols, dtype=tdt, device=dev)
+            y, dz = make(zero, shift_out), make(zero, shift_out)
             lse = torch.empty(rows, 1, dtype=tdt, device=dev)
             dl = torch.randn(rows, 1, generator=gen, device=dev).to(tdt)
             return z, dy, y, dz, lse, dl
@@ -947,18 +949,20 @@ def run_wide_rowops(steps):
                "cols": cols, "calls_per_graph": n, "us": {}, "gbs": {}}
         es = 4 if dtype == "f32" else 2
         tb = rows * cols * es
-        for tag, shift in (("vec", 0), ("scalar", 1)):
-            z, dy, y, dz, lse, dl = tensors(shift)
+        for tag, shift_in, shift_out in (("vec", 0, 0), ("offset", 1, 1), ("scalar", 1, 0)):
+            z, dy, y, dz, lse, dl = tensors(shift_in, shift_out)
             t = {
                 "softmax_fwd": (graph_replay_ms(
                     lambda i, st: agk.softmax_fwd(z, y=y, stream=st), n), 2),
                 "softmax_bwd": (graph_replay_ms(
-                    lambda i, st: agk.softmax_bwd(y, dy, dz=dz, stream=st), n), 3),
-                "logsumexp_fwd": (graph_replay_ms(
-                    lambda i, st: agk.logsumexp_fwd(z, y=lse, stream=st), n), 1),
+                    # y takes the outputs' layout: the inputs' here
+                    lambda i, st: agk.softmax_bwd(z, dy, dz=y, stream=st), n), 3),
                 "logsumexp_bwd": (graph_replay_ms(
                     lambda i, st: agk.logsumexp_bwd(z, dl, dz=dz, stream=st), n), 2),
             }
+            if tag != "scalar":  # no row output: no element-wise layout
+                t["logsumexp_fwd"] = (graph_replay_ms(
+                    lambda i, st: agk.logsumexp_fwd(z, y=lse, stream=st), n), 1)
             for k, (ms, passes) in t.items():
                 rec["us"][f"{k}_{tag}"] = round(ms * 1e3, 1)
                 rec["gbs"][f"{k}_{tag}"] = round(passes * tb / (ms * 1e-3) / 1e9, 1)

@@ -462,18 +462,29 @@ struct Looped {
     }
 };
 
-// Rows too wide for the resident shapes but whole 16-byte slots, with every
-// pointer 16-byte aligned: one 1024-lane workgroup per row, as Looped, but each
-// pass streams the row in 16-byte slots, four slots per lane in flight, through
-// buffer resources (a slot past the row end reads zeros and is skipped).  Each
-// pass re-reads the row: with 1024-lane workgroups only a few hundred rows are
-// in flight, so the re-reads of a row mostly hit the Infinity Cache.  The
-// per-lane order is slot by slot, element by element, then the row tree, fixed
-// by cols.
+// One 1024-lane workgroup per row, each pass streaming the row in 16-byte
+// slots, four slots per lane in flight, through buffer resources (a slot past
+// the row's body reads zeros and is skipped).  Each pass re-reads the row:
+// with 1024-lane workgroups only a few hundred rows are in flight, so the
+// re-reads mostly hit the Infinity Cache.  The per-lane order is slot by slot,
+// element by element, then the row tree, fixed by cols and the row's offset.
+//   ALIGNED: rows of whole 16-byte slots, every pointer 16-byte aligned (rows
+//     too wide for the resident shapes);
+//   otherwise: rows that start anywhere (cols not a multiple of the slot
+//     width, or 16-byte misaligned tensors), every row tensor at the same
+//     offset from a 16-byte boundary.  A row is a head of up to W-1 elements
+//     before its first boundary, a body of 16-byte slots and a tail of up to
+//     W-1 elements; lane t adds head element t and tail element t (scalar
+//     accesses) besides its body slots.  Column vectors, whose offset from a
+//     boundary then differs from row to row, are read element by element.
 constexpr int kVecLanes = 1024;
 constexpr int kVecBatch = 4;
+// Narrower misaligned rows keep row_looped: a 1024-lane workgroup over a few
+// thousand columns leaves most lanes idle (4097 bf16 columns: level forward,
+// 15 % slower backward).
+constexpr int kVecMinCols = 8192;
 
-template <class S, int NIN>
+template <class S, int NIN, bool ALIGNED>
 struct LoopedVec {
     using T = typename S::T;
     static constexpr int W = S::kVec;
@@ -482,29 +493,57 @@ struct LoopedVec {
     float (*red)[kSlots];
     int parity = 0;
     int64_t row;
-    int cols, nslot;
+    int cols, nslot, head, tail0, ntail;
     float ncols, inv_cols;
     const T* x;
     const T* y;
-    uint32_t row_bytes;
+    uint32_t body_bytes;
 
     __device__ LoopedVec(const RowArgs& p, int64_t row_, int cols_, float (*red_)[kSlots])
         : red(red_), row(row_), cols(cols_) {
         ncols = static_cast<float>(cols);
         inv_cols = 1.0f / ncols;
-        nslot = cols / W;
-        row_bytes = static_cast<uint32_t>(cols) * static_cast<uint32_t>(sizeof(T));
         const int64_t off = row * static_cast<int64_t>(cols);
         x = static_cast<const T*>(p.in0) + off;
         y = NIN == 2 ? static_cast<const T*>(p.in1) + off : nullptr;
+        if constexpr (ALIGNED) {
+            head = 0;
+        } else {
+            const uint32_t mis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(x) & 15u);
+            head = mis ? static_cast<int>((16u - mis) / sizeof(T)) : 0;
+            if (head > cols) head = cols;
+        }
+        nslot = (cols - head) / W;
+        tail0 = head + nslot * W;
+        ntail = cols - tail0;
+        body_bytes = static_cast<uint32_t>(nslot) * 16u;
     }
+
+    // f over the head and tail elements this lane owns (lane t: element t of
+    // each), then over its body slots.
+    template <class G>
+    __device__ __forceinline__ void edges(G g) const {
+        if constexpr (!ALIGNED) {
+            const int t = threadIdx.x;
+            if (t < head) g(t);
+            if (t < ntail) g(tail0 + t);
+        }
+    }
+    __device__ __forceinline__ float xa(int c) const { return S::get(x + c); }
+    __device__ __forceinline__ float yb(int c) const { return NIN == 2 ? S::get(y + c) : 0.0f; }
 
     template <class R, int N, class F>
     __device__ __forceinline__ void reduce(float (&res)[N], F f) {
 #pragma unroll
         for (int i = 0; i < N; ++i) res[i] = R::kId;
-        const rsrc_t rx = make_rsrc(x, row_bytes);
-        const rsrc_t ry = make_rsrc(NIN == 2 ? y : x, NIN == 2 ? row_bytes : 0u);
+        edges([&](int c) {
+            float o[N];
+            f(xa(c), yb(c), o);
+#pragma unroll
+            for (int i = 0; i < N; ++i) res[i] = R::op(res[i], o[i]);
+        });
+        const rsrc_t rx = make_rsrc(x + head, body_bytes);
+        const rsrc_t ry = make_rsrc(NIN == 2 ? y + head : x, NIN == 2 ? body_bytes : 0u);
         for (int base = threadIdx.x; base < nslot; base += kVecLanes * kVecBatch) {
             u32x4 va[kVecBatch], vb[kVecBatch];
 #pragma unroll
@@ -557,14 +596,23 @@ struct LoopedVec {
         s1 = r[1];
     }
 
-    // One pass: per lane, each slot's maximum mn = max(m, slot max) and
-    // s = s * exp(m - mn) + sum over the slot of exp(a - mn) (a slot that
-    // leaves mn at -inf changes nothing); then M = the row maximum of m and
-    // s = the row sum of s * exp(m - M), both over the row tree.
+    // One pass: per lane, each slot (or edge element) updates the running
+    // maximum mn = max(m, its maximum) and s = s * exp(m - mn) + the sum of
+    // its exp(a - mn) (an update that leaves mn at -inf changes nothing); then
+    // M = the row maximum of m and s = the row sum of s * exp(m - M), both over
+    // the row tree.
     template <bool KEEP>
     __device__ __forceinline__ void max_sumexp(float& m_out, float& s_out) {
         float m = -__builtin_inff(), s = 0.0f;
-        const rsrc_t rx = make_rsrc(x, row_bytes);
+        edges([&](int c) {
+            const float v = xa(c);
+            const float mn = MaxR::op(m, v);
+            if (mn != -__builtin_inff()) {
+                s = s * fast_exp(m - mn) + fast_exp(v - mn);
+                m = mn;
+            }
+        });
+        const rsrc_t rx = make_rsrc(x + head, body_bytes);
         for (int base = threadIdx.x; base < nslot; base += kVecLanes * kVecBatch) {
             u32x4 va[kVecBatch];
 #pragma unroll
@@ -606,16 +654,23 @@ struct LoopedVec {
     }
 
     // out (+)= h(a, b, u, v) per element, u and v from the column vectors c0,
-    // c1 (d0, d1 when null), the row's slots streamed as in reduce.
+    // c1 (d0, d1 when null).
     template <class H>
     __device__ __forceinline__ void store_each(void* out, int acc, const void* c0, float d0,
                                                const void* c1, float d1, H h) const {
         T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
-        const rsrc_t rx = make_rsrc(x, row_bytes);
-        const rsrc_t ry = make_rsrc(NIN == 2 ? y : x, NIN == 2 ? row_bytes : 0u);
-        const rsrc_t ro = make_rsrc(o, row_bytes);
-        const rsrc_t ru = make_rsrc(c0 ? c0 : x, c0 ? row_bytes : 0u);
-        const rsrc_t rv = make_rsrc(c1 ? c1 : x, c1 ? row_bytes : 0u);
+        const T* u = static_cast<const T*>(c0);
+        const T* v = static_cast<const T*>(c1);
+        edges([&](int c) {
+            float r = h(xa(c), yb(c), u ? S::get(u + c) : d0, v ? S::get(v + c) : d1);
+            if (acc) r = acc_add(S::get(o + c), r);
+            S::put(o + c, r);
+        });
+        const rsrc_t rx = make_rsrc(x + head, body_bytes);
+        const rsrc_t ry = make_rsrc(NIN == 2 ? y + head : x, NIN == 2 ? body_bytes : 0u);
+        const rsrc_t ro = make_rsrc(o + head, body_bytes);
+        const rsrc_t ru = make_rsrc(c0 ? u + head : x, (ALIGNED && c0) ? body_bytes : 0u);
+        const rsrc_t rv = make_rsrc(c1 ? v + head : x, (ALIGNED && c1) ? body_bytes : 0u);
         for (int base = threadIdx.x; base < nslot; base += kVecLanes * kVecBatch) {
             u32x4 va[kVecBatch], vb[kVecBatch], vu[kVecBatch], vv[kVecBatch], vo[kVecBatch];
 #pragma unroll
@@ -623,28 +678,48 @@ struct LoopedVec {
                 const uint32_t off = static_cast<uint32_t>(base + k * kVecLanes) * 16u;
                 va[k] = bload16_stream(rx, off);
                 if constexpr (NIN == 2) vb[k] = bload16_stream(ry, off);
-                if (c0) vu[k] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0);
-                if (c1) vv[k] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+                if constexpr (ALIGNED) {
+                    if (c0) vu[k] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0);
+                    if (c1) vv[k] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+                }
                 if (acc) vo[k] = bload16_stream(ro, off);
             }
 #pragma unroll
             for (int k = 0; k < kVecBatch; ++k) {
-                const uint32_t off = static_cast<uint32_t>(base + k * kVecLanes) * 16u;
+                const int slot = base + k * kVecLanes;
+                const uint32_t off = static_cast<uint32_t>(slot) * 16u;
                 float fa[W], fb[W], fu[W], fv[W], r[W];
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    fu[e] = d0;
+                    fv[e] = d1;
+                }
                 S::unpack(va[k], fa);
                 if constexpr (NIN == 2) S::unpack(vb[k], fb);
-                if (c0) S::unpack(vu[k], fu);
-                if (c1) S::unpack(vv[k], fv);
+                if constexpr (ALIGNED) {
+                    if (c0) S::unpack(vu[k], fu);
+                    if (c1) S::unpack(vv[k], fv);
+                } else if (slot < nslot) {  // column values element by element
+                    const int c = head + slot * W;
 #pragma unroll
-                for (int e = 0; e < W; ++e)
-                    r[e] = h(fa[e], NIN == 2 ? fb[e] : 0.0f, c0 ? fu[e] : d0, c1 ? fv[e] : d1);
+                    for (int e = 0; e < W; ++e) {
+                        fu[e] = u ? S::get(u + c + e) : d0;
+                        fv[e] = v ? S::get(v + c + e) : d1;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const float uu = ALIGNED ? (c0 ? fu[e] : d0) : fu[e];
+                    const float vvv = ALIGNED ? (c1 ? fv[e] : d1) : fv[e];
+                    r[e] = h(fa[e], NIN == 2 ? fb[e] : 0.0f, uu, vvv);
+                }
                 if (acc) {
                     float old[W];
                     S::unpack(vo[k], old);
 #pragma unroll
                     for (int e = 0; e < W; ++e) r[e] = acc_add(old[e], r[e]);
                 }
-                bstore16_stream(ro, off, S::pack(r));  // past the row end: dropped
+                bstore16_stream(ro, off, S::pack(r));  // past the body: dropped
             }
         }
     }
@@ -819,10 +894,10 @@ __global__ __launch_bounds__(TPR * G) void row_resident(const RowArgs p, int64_t
     Op::run(c, p);
 }
 
-template <class S, class Op>
+template <class S, class Op, bool ALIGNED>
 __global__ __launch_bounds__(kVecLanes) void row_looped_vec(const RowArgs p, int64_t rows,
                                                            int cols) {
-    using Ctx = LoopedVec<S, Op::kIn>;
+    using Ctx = LoopedVec<S, Op::kIn, ALIGNED>;
     __shared__ float red[2][Ctx::kSlots];
     const int64_t row = blockIdx.x;
     if (row >= rows) return;  // workgroup-uniform
@@ -842,6 +917,20 @@ __global__ __launch_bounds__(kBlock) void row_looped(const RowArgs p, int64_t ro
 
 inline bool aligned_or_null(const void* p) { return p == nullptr || aligned16(p); }
 
+// Every row tensor (in0, in1, out) element-aligned and at in0's offset from a
+// 16-byte boundary, so that each row's head, body and tail line up in all of
+// them.  Column vectors and per-row vectors may sit anywhere.
+template <class T>
+inline bool same_offset(const RowArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.in0);
+    auto ok = [&](const void* q) {
+        if (q == nullptr) return true;
+        const uintptr_t b = reinterpret_cast<uintptr_t>(q);
+        return (b % sizeof(T)) == 0 && ((b - a) & 15u) == 0;
+    };
+    return (a % sizeof(T)) == 0 && ok(p.in1) && ok(p.out);
+}
+
 template <class Op, class S>
 int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
     const bool vec = (cols % S::kVec) == 0 && aligned16(p.in0) && aligned_or_null(p.in1) &&
@@ -851,9 +940,15 @@ int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
     if (vec) pl = fwd_plan(cols / S::kVec, rows);
     if (pl.tpr == 0) {
         if (rows > 0x7fffffffLL) return AGK_EINVAL;
-        // whole 16-byte slots, aligned, rows short enough for 32-bit buffer offsets
-        if (vec && static_cast<uint64_t>(cols) * sizeof(typename S::T) < 0x80000000ull)
-            hipLaunchKernelGGL((row_looped_vec<S, Op>), dim3(static_cast<unsigned>(rows)),
+        // rows short enough for 32-bit buffer offsets: whole 16-byte slots and
+        // aligned pointers, or (from kVecMinCols columns) every row tensor at
+        // the same offset from a 16-byte boundary
+        const bool fits = static_cast<uint64_t>(cols) * sizeof(typename S::T) < 0x80000000ull;
+        if (vec && fits)
+            hipLaunchKernelGGL((row_looped_vec<S, Op, true>), dim3(static_cast<unsigned>(rows)),
+                               dim3(kVecLanes), 0, st, p, rows, cols);
+        else if (fits && cols >= kVecMinCols && same_offset<typename S::T>(p))
+            hipLaunchKernelGGL((row_looped_vec<S, Op, false>), dim3(static_cast<unsigned>(rows)),
                                dim3(kVecLanes), 0, st, p, rows, cols);
         else
             hipLaunchKernelGGL((row_looped<S, Op>), dim3(static_cast<unsigned>(rows)),

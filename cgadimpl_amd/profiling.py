@@ -441,19 +441,23 @@ def write_wide_summary(jsonl, out_md, command):
     ro = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"wide_rowops"')]
     if ro:
         lines += ["", "## Softmax and log-sum-exp at vocabulary widths", "",
-                  "16-byte aligned tensors (the 16-byte looped kernel, with one online pass "
-                  "for the row maximum and sum of exponentials) against views of the same "
-                  "values one element off a 16-byte boundary (the element-wise looped "
-                  "kernel), graph-replayed µs per call; % of 8 TB/s for the aligned call "
-                  "(algorithmic bytes: softmax forward 2 tensors, backward 3, log-sum-exp "
-                  "forward 1, backward 2).", "",
+                  "Graph-replayed µs per call on the same values in three layouts: 16-byte "
+                  "aligned tensors / every tensor one element off a 16-byte boundary (the "
+                  "16-byte looped kernel's head/body/tail form; at 50257 columns every row "
+                  "is off a boundary, so both take it) / inputs off and outputs aligned (the "
+                  "element-wise looped kernel; log-sum-exp forward has no row output, so "
+                  "'-'). % of 8 TB/s for the first layout (algorithmic bytes: softmax forward "
+                  "2 tensors, backward 3, log-sum-exp forward 1, backward 2). The 16-byte "
+                  "kernel computes the row maximum and the sum of exponentials in one online "
+                  "pass.", "",
                   "| shape | softmax fwd | softmax bwd | log-sum-exp fwd | log-sum-exp bwd |",
                   "|---|---|---|---|---|"]
         for r in ro:
             u, g = r["us"], r["gbs"]
             cells = []
             for k in ("softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd"):
-                cells.append(f"{u[k + '_vec']} / {u[k + '_scalar']} "
+                sc = u.get(k + "_scalar", "-")
+                cells.append(f"{u[k + '_vec']} / {u[k + '_offset']} / {sc} "
                              f"({g[k + '_vec'] / 80:.1f} %)")
             lines.append(f"| {r['wide_rowops']} | " + " | ".join(cells) + " |")
     with open(out_md, "w") as fh:

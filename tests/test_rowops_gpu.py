@@ -29,11 +29,13 @@ pytestmark = pytest.mark.gpu
 
 OPS = ("rmsnorm_jvp", "layernorm", "softmax", "logsumexp")
 # ... including vocabulary widths past the resident shapes (128256 = Llama 3's
-# vocabulary): aligned rows take the 16-byte looped kernel, 131076 bf16 (not a
-# whole number of 8-element slots) the element-wise one.
+# vocabulary): aligned rows take the 16-byte looped kernel; rows that are not
+# whole 16-byte slots from 8192 columns (8193, 131076 bf16, 50257 = GPT-2's
+# vocabulary, where every row starts at another offset) its head/body/tail
+# form; narrower ones the element-wise kernel.
 SHAPES = [(5, 1), (3, 3), (17, 13), (9, 100), (33, 127), (65, 129), (8, 1000), (37, 4096),
           (4, 4099), (2, 40000), (300, 64), (1000, 128), (512, 512), (64, 5120), (3, 65536),
-          (4, 128256), (2, 131076), (1, 262144)]
+          (4, 128256), (2, 131076), (1, 262144), (9, 50257), (5, 8193)]
 EPS = 1e-5
 
 
@@ -270,6 +272,50 @@ def test_misaligned_pointers_take_the_looped_kernel(cuda, op, dtype):
     e_mis = run_op(op, shifted(x), shifted(g), shifted(dy), label)
     assert_ok(e_mis, _tol(dtype == "bf16"), label)
     assert_ok(e_al, _tol(dtype == "bf16"), label + " (aligned)")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("cols", [40000, 50257])
+def test_same_offset_tensors_take_the_16_byte_kernel(cuda, dtype, cols):
+    """Every tensor one element off a 16-byte boundary (inputs and outputs at
+    the same offset), at a width past the resident shapes: softmax and
+    log-sum-exp forward and backward through the head/body/tail form of the
+    16-byte looped kernel, against the oracle with check_softmax's and
+    check_logsumexp's bars."""
+    import torch
+    rows = 5
+    x, _, dy = device_inputs((rows, cols), dtype, 79 + cols, cuda)
+
+    def shifted(t):  # same values, one element past a 16-byte boundary
+        buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+        v = buf[1:1 + t.numel()].view(t.shape)
+        v.copy_(t)
+        return v
+
+    z, d = shifted(x * 4.0), shifted(dy)
+    y, dz, dlz = shifted(torch.zeros_like(x)), shifted(torch.zeros_like(x)), \
+        shifted(torch.zeros_like(x))
+    assert z.data_ptr() % 16 != 0 and (y.data_ptr() - z.data_ptr()) % 16 == 0
+    agk.softmax_fwd(z, y=y)
+    agk.softmax_bwd(y, d, dz=dz)
+    dl = dy[:, :1].contiguous()
+    lse = agk.logsumexp_fwd(z)
+    agk.logsumexp_bwd(z, dl, dz=dlz)
+    torch.cuda.synchronize()
+    zs, ds, ys, dls = to_host(z), to_host(d), to_host(y), to_host(dl)
+    bf16 = dtype == "bf16"
+    if bf16:
+        ry, rdz = ro.softmax_fwd_bf16(zs), ro.softmax_bwd_bf16(ys, ds)
+        rl, rdl = ro.logsumexp_fwd_bf16(zs), ro.logsumexp_bwd_bf16(zs, dls)
+    else:
+        ry, rdz = ro.softmax_fwd(zs), ro.softmax_bwd(ys, ds)
+        rl, rdl = ro.logsumexp_fwd(zs), ro.logsumexp_bwd(zs, dls)
+    yf, gf = _f64(ys), _f64(ds)
+    scale = _rowmax(yf) * (_rowmax(gf) + np.abs(np.sum(yf * gf, -1)))
+    e = {"softmax y": _row_rel(ys, ry), "softmax dz": _scaled_err(to_host(dz), rdz, scale),
+         "lse y": _scaled_err(to_host(lse), rl, np.maximum(np.abs(_f64(rl))[:, 0], 1.0)),
+         "lse dz": _row_rel(to_host(dlz), rdl)}
+    assert_ok(e, _tol(bf16), f"same-offset {dtype} {rows}x{cols}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
