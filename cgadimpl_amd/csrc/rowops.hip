@@ -32,6 +32,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "agk_rowops.h"
 #include "rowcommon.hpp"
 
@@ -842,6 +844,10 @@ struct SmBwd {
 // Row log-sum-exp (in0 = z, out_row = y): y = log(sum(exp(z - m))) + m.
 struct LseFwd {
     static constexpr int kIn = 1;
+    // bf16 rows of 8 slots per lane (32769-65536 columns) stream faster through
+    // the 16-byte looped kernel's one online pass (GPT-2-sized vocabularies:
+    // 52-61 % of HBM peak resident, 78 % streamed)
+    static constexpr bool kStreamWideBf16 = true;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         float m, s;
@@ -917,6 +923,15 @@ __global__ __launch_bounds__(kBlock) void row_looped(const RowArgs p, int64_t ro
 
 inline bool aligned_or_null(const void* p) { return p == nullptr || aligned16(p); }
 
+// Op::kStreamWideBf16 when the op declares it, else false.
+template <class Op, class = void>
+struct StreamWideBf16 : std::false_type {};
+template <class Op>
+struct StreamWideBf16<Op, std::void_t<decltype(Op::kStreamWideBf16)>>
+    : std::integral_constant<bool, Op::kStreamWideBf16> {};
+template <class Op>
+constexpr bool stream_wide_bf16() { return StreamWideBf16<Op>::value; }
+
 // Every row tensor (in0, in1, out) element-aligned and at in0's offset from a
 // 16-byte boundary, so that each row's head, body and tail line up in all of
 // them.  Column vectors and per-row vectors may sit anywhere.
@@ -938,6 +953,7 @@ int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
                      aligned_or_null(p.col1);
     Plan pl;
     if (vec) pl = fwd_plan(cols / S::kVec, rows);
+    if (stream_wide_bf16<Op>() && std::is_same<S, BF16>::value && pl.nv == 8) pl = Plan{};
     if (pl.tpr == 0) {
         if (rows > 0x7fffffffLL) return AGK_EINVAL;
         // rows short enough for 32-bit buffer offsets: whole 16-byte slots and
