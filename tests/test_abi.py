@@ -102,6 +102,64 @@ def test_workspace_bytes_rule():
     assert lib.agk_mul_rowbcast_bwd_workspace_bytes(65536, 4096) == ws(65536, 4096)
 
 
+def _r256(b):
+    return (b + 255) // 256 * 256
+
+
+def _split_blocks(rows, cols):
+    """(row blocks, rows per block) of the split backward: about 2048 tiles of
+    2048 columns."""
+    nch = -(-cols // 2048)
+    nrb = min(max(-(-2048 // nch), 1), rows)
+    rb = -(-rows // nrb)
+    return -(-rows // rb), rb
+
+
+def _split_ws(rows, cols, prows):
+    """Partial rows, segment sums (4096 columns each), coefficients."""
+    return _r256(prows * cols * 4) + _r256(rows * -(-cols // 4096) * 4) + _r256(rows * 4)
+
+
+def test_wide_row_plans_and_workspace():
+    """Rows of AGK_WIDE_MIN_COLS (16385) columns and more: the workspace covers
+    the split path's regions (its own row blocks, and the looped blocking the
+    composition uses) as well as the looped kernel's partial rows, the same for
+    both dtypes; the plan diagnostic reports the one-pass backward from 256
+    rows of at most 32768 columns, the split paths otherwise (aligned rows),
+    the looped kernels for rows that are not whole 16-byte slots."""
+    lib = agk.lib()
+    ws = lib.agk_rmsnorm_bwd_workspace_bytes
+    assert agk.AGK_WIDE_MIN_COLS == 16385
+    for rows in (1, 7, 300, 5000):
+        assert ws(rows, 16384) == _blocks(rows) * 16384 * 4  # narrower: unchanged
+    for rows, cols in [(1, 1 << 20), (8, 262144), (51, 32768), (255, 32768), (256, 16388),
+                       (300, 65536), (4096, 32768), (1100, 20480), (7, 16385), (3, 40002)]:
+        nrb, rb = _split_blocks(rows, cols)
+        want = max(_blocks(rows) * cols * 4, _split_ws(rows, cols, nrb),
+                   _split_ws(rows, cols, _blocks(rows)))
+        assert ws(rows, cols) == want, (rows, cols)
+        for dt, w in ((agk.AGK_F32, 4), (agk.AGK_BF16, 8)):
+            label = (rows, cols, dt)
+            bp = agk.launch_plan(rows, cols, dt, True)
+            fp = agk.launch_plan(rows, cols, dt, False)
+            if cols % w:
+                assert bp["tpr"] == 0 and bp["nv"] == 0, label
+                assert fp["tpr"] == 0 and fp["nv"] == 0, label
+                continue
+            if rows >= 256 and cols <= 32768:
+                assert (bp["tpr"], bp["nv"], bp["g"]) == (1024, 32768 // (w * 1024), 1), label
+                assert bp["nblk"] == 256 and bp["rpb"] == -(-rows // 256), label
+            else:
+                assert bp["tpr"] == 0, label
+                assert (bp["nv"], bp["g"]) == (-(-cols // 4096), -(-cols // 2048)), label
+                assert bp["rpb"] == rb and bp["nblk"] == (nrb if nrb > 1 else 0), label
+            if cols // w <= 8192:
+                assert fp["tpr"] > 0, label  # the resident forward holds the row
+            else:
+                assert fp["tpr"] == 0, label
+                assert (fp["nv"], fp["g"]) == (-(-cols // 4096), -(-cols // 2048)), label
+
+
 def test_launch_plans_are_well_formed():
     """Every reachable resident shape holds its row: lanes * slots * width >= cols."""
     from plans import reachable_plans

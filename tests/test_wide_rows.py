@@ -221,3 +221,42 @@ def test_wide_workspace_size(cuda):
     with pytest.raises(agk.AgkError) as ei:
         agk.rmsnorm_bwd(x, None, inv, x, workspace=ws)
     assert ei.value.status == 3
+
+
+@pytest.mark.parametrize("rows,cols", [(6, 65536), (300, 24576)], ids=str)
+def test_wide_paths_under_graph_capture(cuda, rows, cols):
+    """A forward and backward call (the split forward; the split or the one-pass
+    backward, with their partial sums in y and the workspace) captured once into
+    a HIP graph: three replays on new inputs, with eager calls and
+    synchronisations between them, each bit-identical to the eager calls on the
+    same inputs."""
+    import torch
+    x = torch.empty(rows, cols, device=cuda)
+    dy = torch.empty_like(x)
+    g = torch.rand(cols, device=cuda) + 0.5
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    inv = torch.empty(rows, device=cuda)
+    dg = torch.empty(cols, device=cuda)
+    ws = torch.empty(agk.rmsnorm_bwd_workspace_bytes(rows, cols), dtype=torch.uint8, device=cuda)
+    x.normal_()
+    dy.normal_()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = torch.cuda.current_stream()
+        agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, stream=st)
+        agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=st)
+    gen = torch.Generator(device=cuda)
+    for k in range(3):
+        gen.manual_seed(100 + k)
+        x.copy_(torch.randn(rows, cols, generator=gen, device=cuda))
+        dy.copy_(torch.randn(rows, cols, generator=gen, device=cuda))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (y, inv, dx, dg)]
+        ey, einv = agk.rmsnorm_fwd(x, g, 1e-6)
+        edx, edg = agk.rmsnorm_bwd(x, g, einv, dy)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "inv_rms", "dx", "dgamma"), got, (ey, einv, edx, edg)):
+            assert torch.equal(a, b), (k, name)
+    del graph
