@@ -146,18 +146,26 @@ def _check(status: int, where: str) -> None:
 
 # ---- torch plumbing ------------------------------------------------------------
 
+_torch_mod = None
+_dtype_codes: dict = {}
+
+
 def _torch():
-    import torch
-    return torch
+    global _torch_mod
+    if _torch_mod is None:
+        import torch
+        _torch_mod = torch
+    return _torch_mod
 
 
 def _dtype_code(t) -> int:
-    torch = _torch()
-    if t.dtype == torch.float32:
-        return AGK_F32
-    if t.dtype == torch.bfloat16:
-        return AGK_BF16
-    raise TypeError(f"unsupported storage dtype {t.dtype} (float32 or bfloat16)")
+    if not _dtype_codes:
+        torch = _torch()
+        _dtype_codes.update({torch.float32: AGK_F32, torch.bfloat16: AGK_BF16})
+    code = _dtype_codes.get(t.dtype)
+    if code is None:
+        raise TypeError(f"unsupported storage dtype {t.dtype} (float32 or bfloat16)")
+    return code
 
 
 def _ptr(t) -> Optional[int]:
@@ -217,10 +225,10 @@ def rmsnorm_bwd(x, gamma, inv_rms, dy, dx=None, dgamma=None, accumulate=False,
         dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
     # a workspace is required for dgamma, and lets dx alone take the split
     # path on wide rows
-    wants_ws = dgamma is not None or cols >= AGK_WIDE_MIN_COLS
-    ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols) if wants_ws else 0
-    if wants_ws and workspace is None and ws_bytes:
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    if workspace is None and (dgamma is not None or cols >= AGK_WIDE_MIN_COLS):
+        ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols)
+        if ws_bytes:
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     ws_have = workspace.numel() * workspace.element_size() if workspace is not None else 0
     rc = lib().agk_rmsnorm_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(dy), _ptr(dx),
                                _ptr(dgamma), _ptr(workspace), ws_have, rows, cols,
