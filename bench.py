@@ -692,6 +692,9 @@ def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
     inv1 = torch.empty(R, dtype=f32, device=dev)
     dxo = torch.empty_like(x)
     dgo = torch.empty(D, dtype=f32, device=dev)
+    dro = torch.empty_like(x) if op == "rms_mul" else None
+    wso = (torch.empty(max(1, agk.rmsnorm_bwd_workspace_bytes(R, D)), dtype=torch.uint8,
+                       device=dev) if op == "rms_mul" else None)
     stream = torch.cuda.current_stream()
     launches = {
         "layernorm": [("fwd", lambda: agk.layernorm_fwd(x, cfg.eps, y=y, mean=mean, rstd=rstd,
@@ -709,7 +712,7 @@ def run_rowop(op, cfg_name, steps, warmup, cpu_seconds):
                                                     stream=stream)),
                     ("mul", lambda: agk.mul_rowbcast_fwd(y, g, y=out, stream=stream)),
                     ("bwd", lambda: agk.rms_mul_bwd(x, g, inv1, dy, dx=dxo, dgamma=dgo,
-                                                    stream=stream))],
+                                                    dr=dro, workspace=wso, stream=stream))],
     }[op]
     for _ in range(warmup):
         for _, f in launches:

@@ -346,30 +346,33 @@ def mul_rowbcast_bwd(gy, a, b, da=None, db=None, accumulate=False, want_da: bool
 
 
 def rms_mul_bwd(x, gamma, inv_rms, gy, dx=None, dgamma=None, accumulate=False,
-                want_dx: bool = True, want_dgamma: bool = True, stream=None):
+                want_dx: bool = True, want_dgamma: bool = True, dr=None, workspace=None,
+                stream=None):
     """Both VJPs of y = rms(x) * gamma in one pass (agk_rms_mul_bwd).
 
     Returns (dr, dx, dgamma): dr = gy * gamma (the gradient of rms(x)), dx and
     dgamma as mul_rowbcast_bwd followed by rmsnorm_bwd(gamma=None) on dr give
-    them, bit for bit.  inv_rms comes from rmsnorm_fwd(x, None, eps).
+    them, bit for bit.  inv_rms comes from rmsnorm_fwd(x, None, eps).  dr and
+    the workspace (rmsnorm_bwd_workspace_bytes) are allocated when not given.
     """
     torch = _torch()
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
     acc = _accum_flags(accumulate)
-    dr = torch.empty_like(x)
+    if dr is None:
+        dr = torch.empty_like(x)
     if want_dx and dx is None:
         dx = torch.empty_like(x) if not acc & AGK_ACCUM_DX else torch.zeros_like(x)
     if want_dgamma and dgamma is None:
         dgamma = torch.empty(cols, dtype=torch.float32, device=x.device)
-    ws = None
-    wants_ws = dgamma is not None or cols >= AGK_WIDE_MIN_COLS  # as rmsnorm_bwd
-    ws_bytes = int(lib().agk_rmsnorm_bwd_workspace_bytes(rows, cols)) if wants_ws else 0
-    if ws_bytes:
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    if workspace is None and (dgamma is not None or cols >= AGK_WIDE_MIN_COLS):
+        ws_bytes = rmsnorm_bwd_workspace_bytes(rows, cols)  # as rmsnorm_bwd
+        if ws_bytes:
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    ws_have = workspace.numel() * workspace.element_size() if workspace is not None else 0
     rc = lib().agk_rms_mul_bwd(_ptr(x), _ptr(gamma), _ptr(inv_rms), _ptr(gy), _ptr(dr), _ptr(dx),
-                               _ptr(dgamma), _ptr(ws), ws_bytes, rows, cols, _dtype_code(x), acc,
-                               _stream(stream))
+                               _ptr(dgamma), _ptr(workspace), ws_have, rows, cols, _dtype_code(x),
+                               acc, _stream(stream))
     _check(rc, "agk_rms_mul_bwd")
     return dr, dx, dgamma
 
