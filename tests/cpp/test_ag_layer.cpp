@@ -1241,6 +1241,88 @@ void test_block_cache() {
 }
 
 // Runs the named checks (all of them when `only` is empty).
+// The reference's integration test (Tests/test_kitchen_sink_mlp.cpp:14-29, 111-113) trains a
+// small MLP with rms() inside on the GPU and asserts that the loss goes down and stays finite.
+// The same on this path's ops: linear -> laynor -> rms(.) * gamma -> linear, all bf16 on the
+// device; the softmax cross-entropy and its gradient (the backward seed) are taken on the host,
+// and plain gradient descent updates fp32 master weights that are written back as bf16 each
+// step.  Labels come from a fixed random linear teacher, so the classes are learnable.
+void test_mlp_training() {
+    const int64_t B = 64, IN = 64, H = 32, OUT = 8;
+    const int epochs = 30;
+    const float lr = 0.5f;
+    auto bits = [](const std::vector<float>& v) {
+        std::vector<uint16_t> b(v.size());
+        for (size_t i = 0; i < v.size(); ++i) {
+            uint32_t u;
+            std::memcpy(&u, &v[i], 4);
+            u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
+            b[i] = static_cast<uint16_t>(u >> 16);
+        }
+        return b;
+    };
+    auto param = [&](const std::vector<float>& v, std::vector<int64_t> shape, const char* name) {
+        std::vector<uint16_t> b = bits(v);
+        Tensor t = Tensor::from_host(b.data(), shape, Dtype::BFloat16);
+        t.set_requires_grad(true);
+        return make_tensor(t, name);
+    };
+    const std::vector<float> xv = normal(B * IN, 40), teacher = normal(IN * OUT, 41);
+    std::vector<int> label(B);
+    for (int64_t b = 0; b < B; ++b) {
+        double best = -1e300;
+        for (int64_t o = 0; o < OUT; ++o) {
+            double z = 0.0;
+            for (int64_t i = 0; i < IN; ++i) z += double(xv[b * IN + i]) * teacher[i * OUT + o];
+            if (z > best) best = z, label[b] = static_cast<int>(o);
+        }
+    }
+    std::vector<float> W1 = normal(H * IN, 42, 0.1), b1(H, 0.0f), gam(H, 1.0f),
+                       W2 = normal(OUT * H, 43, 0.1), b2(OUT, 0.0f);
+    const std::vector<uint16_t> xb = bits(xv);
+    const Tensor xt = Tensor::from_host(xb.data(), {B, IN}, Dtype::BFloat16);
+    std::vector<double> losses;
+    bool finite = true;
+    for (int ep = 0; ep < epochs; ++ep) {
+        Value x = make_tensor(xt, "x");
+        Value w1 = param(W1, {H, IN}, "W1"), c1 = param(b1, {H}, "b1"), g = param(gam, {H}, "g");
+        Value w2 = param(W2, {OUT, H}, "W2"), c2 = param(b2, {OUT}, "b2");
+        Value logits = linear(rms(laynor(linear(x, w1, c1))) * g, w2, c2);
+        const std::vector<float> z = logits.val().to_host_f32();
+        std::vector<float> dz(z.size());
+        double loss = 0.0;
+        for (int64_t b = 0; b < B; ++b) {
+            double m = -1e300, se = 0.0;
+            for (int64_t o = 0; o < OUT; ++o) m = std::max(m, double(z[b * OUT + o]));
+            for (int64_t o = 0; o < OUT; ++o) se += std::exp(double(z[b * OUT + o]) - m);
+            loss += m + std::log(se) - z[b * OUT + label[b]];
+            for (int64_t o = 0; o < OUT; ++o)
+                dz[b * OUT + o] = static_cast<float>(
+                    (std::exp(double(z[b * OUT + o]) - m) / se - (o == label[b] ? 1.0 : 0.0)) / B);
+        }
+        loss /= B;
+        losses.push_back(loss);
+        finite = finite && std::isfinite(loss);
+        const std::vector<uint16_t> sb = bits(dz);
+        const Tensor seed = Tensor::from_host(sb.data(), {B, OUT}, Dtype::BFloat16);
+        backward(logits, &seed);
+        const std::pair<std::vector<float>*, Value*> ps[] = {
+            {&W1, &w1}, {&b1, &c1}, {&gam, &g}, {&W2, &w2}, {&b2, &c2}};
+        for (auto& [master, v] : ps) {
+            const std::vector<float> gr = v->grad().to_host_f32();
+            for (size_t i = 0; i < master->size(); ++i) {
+                finite = finite && std::isfinite(gr[i]);
+                (*master)[i] -= lr * gr[i];
+            }
+        }
+    }
+    char detail[160];
+    std::snprintf(detail, sizeof detail, "loss %.4f -> %.4f (epoch 10: %.4f)", losses.front(),
+                  losses.back(), losses[10]);
+    report("MLP with rms(.) * gamma trains (linear, laynor, rms, mul, linear)",
+           finite && losses[10] < losses.front() && losses.back() < 0.25 * losses.front(), detail);
+}
+
 int selftest(const std::vector<std::string>& only) {
     const std::pair<const char*, void (*)()> tests[] = {
         {"reference_pattern", test_reference_pattern},
@@ -1267,6 +1349,7 @@ int selftest(const std::vector<std::string>& only) {
         {"graph_capture_parallel", [] { test_graph_capture(true); }},
         {"graph_capture_rules", test_graph_capture_rules},
         {"block_cache", test_block_cache},
+        {"mlp_training", test_mlp_training},
     };
     for (auto& [name, fn] : tests) {
         if (!only.empty() && std::find(only.begin(), only.end(), name) == only.end()) continue;
