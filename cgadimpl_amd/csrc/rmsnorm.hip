@@ -889,19 +889,24 @@ __global__ __launch_bounds__(kBlock) void mul_rowbcast_bwd_kernel(
 // any of them: the partials were just written by other XCDs' workgroups, so
 // every load misses this XCD's L2, and at the resident backward's 256 partial
 // rows one round trip covers all of them.  Narrow column chunks give one
-// workgroup per 16 columns (256 at 4096 columns), so the partials stream in
-// over most of the CUs rather than a quarter of them.
+// workgroup per 32 columns (128 at 4096 columns), so the partials stream in
+// over half the CUs rather than a few of them, and each workgroup reads whole
+// 128-byte lines of every partial row: with 16 columns, two workgroups on
+// different XCDs each fetched half of every line, doubling the bytes read and
+// costing c2's finalize 0.8 us, 1.3 us at 5120 columns and 2.6 us at 11008.
 // VEC: a lane sums 4 adjacent columns with 16-byte loads (cols % 4 == 0 and
 // partials 16-byte aligned, so every partial row's quads are aligned);
-// otherwise a lane sums one column with 4-byte loads.  Same order either way.
+// otherwise a lane sums one column with 4-byte loads (16 columns per
+// workgroup, 1024 lanes).  Same order either way.
 constexpr int kFinSplits = 64;
 constexpr int kFinBatch = 4;
-constexpr int kFinCols = 16;  // columns per workgroup
+constexpr int fin_cols(bool vec) { return vec ? 32 : 16; }  // columns per workgroup
 
 template <bool VEC>
-__global__ __launch_bounds__((VEC ? kFinCols / 4 : kFinCols) * kFinSplits) void dgamma_finalize(
-    const float* __restrict__ partials, float* __restrict__ dgamma, int64_t nblk, int cols,
-    int accumulate) {
+__global__ __launch_bounds__((VEC ? fin_cols(VEC) / 4 : fin_cols(VEC)) * kFinSplits) void
+dgamma_finalize(const float* __restrict__ partials, float* __restrict__ dgamma, int64_t nblk,
+                int cols, int accumulate) {
+    constexpr int kFinCols = fin_cols(VEC);
     constexpr int CPL = VEC ? 4 : 1;              // columns per lane
     constexpr int LANES = kFinCols / CPL;         // lanes per split
     __shared__ double red[kFinSplits][kFinCols];
@@ -1353,13 +1358,17 @@ inline int launch_finalize(const float* partials, float* dgamma, int64_t nblk, i
                            nblk, cols, accumulate);
         return check_launch();
     }
-    const unsigned grid = static_cast<unsigned>((cols + kFinCols - 1) / kFinCols);
-    if (cols % 4 == 0 && aligned16(partials))
-        hipLaunchKernelGGL(dgamma_finalize<true>, dim3(grid), dim3(kFinCols / 4 * kFinSplits), 0,
-                           st, partials, dgamma, nblk, cols, accumulate);
-    else
-        hipLaunchKernelGGL(dgamma_finalize<false>, dim3(grid), dim3(kFinCols * kFinSplits), 0, st,
-                           partials, dgamma, nblk, cols, accumulate);
+    if (cols % 4 == 0 && aligned16(partials)) {
+        constexpr int fc = fin_cols(true);
+        hipLaunchKernelGGL(dgamma_finalize<true>, dim3(static_cast<unsigned>((cols + fc - 1) / fc)),
+                           dim3(fc / 4 * kFinSplits), 0, st, partials, dgamma, nblk, cols,
+                           accumulate);
+    } else {
+        constexpr int fc = fin_cols(false);
+        hipLaunchKernelGGL(dgamma_finalize<false>,
+                           dim3(static_cast<unsigned>((cols + fc - 1) / fc)),
+                           dim3(fc * kFinSplits), 0, st, partials, dgamma, nblk, cols, accumulate);
+    }
     return check_launch();
 }
 

@@ -39,9 +39,12 @@ import sys
 from collections import defaultdict
 
 # Kernels that make up one call of each C-ABI entry point.
+# entry point: (its main kernels, kernels a call adds after one of them)
 ENTRY_KERNELS = {
-    "agk_rmsnorm_fwd": ("rms_fwd_resident", "rms_fwd_looped"),
-    "agk_rmsnorm_bwd": ("rms_bwd_resident", "rms_bwd_looped", "bwd_fewrows", "dgamma_finalize"),
+    "agk_rmsnorm_fwd": (("rms_fwd_resident", "rms_fwd_looped"), ()),
+    "agk_rmsnorm_bwd": (("rms_bwd_resident", "rms_bwd_looped", "bwd_fewrows"),
+                        ("dgamma_finalize", "dgamma_finalize_few")),
+    "agk_rms_mul_bwd": (("rms_mul_bwd_resident",), ("dgamma_finalize", "dgamma_finalize_few")),
 }
 
 # The files the RMSNorm kernels are compiled from.  A traffic summary records a
@@ -139,11 +142,12 @@ def write_trace_summary(stats_csv, out_md, command):
             lines.append(f"| {short_name(name)} | {grid} | {wg} | {len(v)} | "
                          f"{sum(v) / len(v) / 1e3:.1f} |")
         lines.append("")
-    for entry, kernels in ENTRY_KERNELS.items():
-        tot = sum(st[k][1] for k in kernels if k in st)
-        if tot:
-            lines.append(f"- one `{entry}` call: {tot / 1e3:.1f} us "
-                         f"({' + '.join(k for k in kernels if k in st)})")
+    for entry, (main, extra) in ENTRY_KERNELS.items():
+        if not any(k in st for k in main):
+            continue
+        kernels = [k for k in main + extra if k in st]
+        tot = sum(st[k][1] for k in kernels)
+        lines.append(f"- one `{entry}` call: {tot / 1e3:.1f} us ({' + '.join(kernels)})")
     with open(out_md, "w") as fh:
         fh.write("\n".join(lines) + "\n")
 
@@ -191,15 +195,16 @@ def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, 
              f"Counter scale from a {copy_mib} MiB device copy (`bench.py --copy-probe "
              f"{copy_mib}`): FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {ws:.4f}.", "",
              "| kernel | read MB | write MB |", "|---|---|---|"]
+    layer = {e: ENTRY_KERNELS[e][0] + ENTRY_KERNELS[e][1] for e in alg}
     for k, (rd, wr) in sorted(per_kernel.items()):
-        if any(k in ks for ks in ENTRY_KERNELS.values()):
+        if any(k in ks for ks in layer.values()):
             lines.append(f"| {k} | {rd / 1e6:.1f} | {wr / 1e6:.1f} |")
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     src = kernel_source_hash(root)
     rec = {"config": config, "fetch_scale": fs, "write_scale": ws,
            "kernel_source_sha256": src, "git_head": _git_head(root)}
     lines += ["", "| entry point | HBM bytes | algorithmic bytes | ratio |", "|---|---|---|---|"]
-    for entry, kernels in ENTRY_KERNELS.items():
+    for entry, kernels in layer.items():
         tot = sum(sum(per_kernel[k]) for k in kernels if k in per_kernel)
         lines.append(f"| {entry} | {tot:.4g} | {alg[entry]:.4g} | {tot / alg[entry]:.4f} |")
         rec[entry.replace("agk_rmsnorm_", "") + "_hbm_bytes_per_launch"] = round(tot)
