@@ -360,6 +360,11 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     graph_step_ms = graph_replay_ms(lambda i, st: (fwd(i, st), bwd(i, st)), steps)
     graph_fwd_ms = graph_replay_ms(fwd, steps)
     graph_bwd_ms = graph_replay_ms(bwd, steps)
+    # The same replay on one set of tensors: what a step costs when its inputs
+    # are still in L2 and the Infinity Cache (a layer whose input the previous
+    # op has just written).  Differs from the rotating sets only for the small
+    # configurations.
+    graph_step_one_set_ms = graph_replay_ms(lambda i, st: (fwd(0, st), bwd(0, st)), steps)
 
     ms_per_step = wall * 1e3 / steps
     alg = cfg.algorithmic_bytes()
@@ -420,6 +425,7 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "pct_of_hbm_peak": round(100.0 * alg / (graph_step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
             "fwd_ms": round(graph_fwd_ms, 5),
             "bwd_ms": round(graph_bwd_ms, 5),
+            "ms_per_step_one_set": round(graph_step_one_set_ms, 5),
         },
         "cpu_baseline": None,
     }

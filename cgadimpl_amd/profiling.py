@@ -337,14 +337,20 @@ def write_bench_summary(jsonl, out_md, command):
                       "host's cost of launching each call from Python. Where the two tables "
                       "differ, the eager step above is bound by the host's launch rate.", "",
                       "| config | step us | GB/s | % of peak | fwd us | bwd us | fwd+bwd us "
-                      "(separate graphs) |", "|---|---|---|---|---|---|---|"]
+                      "(separate graphs) | step us, one set |", "|---|---|---|---|---|---|---|---|"]
             for r in graphed:
                 gr = r["graph"]
+                one = gr.get("ms_per_step_one_set")
                 lines.append(f"| {_cfg_label(r)} | {1e3 * gr['ms_per_step']:.1f} | "
                              f"{gr['gbs']:.0f} | {gr['pct_of_hbm_peak']:.1f} | "
                              f"{1e3 * gr['fwd_ms']:.1f} | {1e3 * gr['bwd_ms']:.1f} | "
-                             f"{1e3 * (gr['fwd_ms'] + gr['bwd_ms']):.1f} |")
-            lines.append("")
+                             f"{1e3 * (gr['fwd_ms'] + gr['bwd_ms']):.1f} | "
+                             f"{'-' if one is None else f'{1e3 * one:.1f}'} |")
+            lines += ["", "The steps rotate over min(8, ceil(2 GiB / one set's bytes)) sets of "
+                      "tensors, so a small configuration's call does not find its inputs in L2 "
+                      "(4 MB per XCD). \"One set\" replays the same steps on a single set, "
+                      "whose tensors then stay in L2 and the Infinity Cache, as a layer's input "
+                      "does when the previous op has just written it.", ""]
         hosts = {json.dumps(r["cpu_baseline"]["host"], sort_keys=True) for r in norm
                  if r.get("cpu_baseline") and r["cpu_baseline"].get("host")}
         for h in hosts:
