@@ -1027,7 +1027,7 @@ def main():
         if rank == 0:
             print(f"bench.py: this build runs the RMSNorm path on one GPU; --gpus {args.gpus} "
                   f"(WORLD_SIZE {world}) is not supported. Rows shard across GPUs with no "
-                  "communication except one dgamma reduction; see DESIGN.md.", file=sys.stderr)
+                  "communication except one dgamma reduction, in rank order.", file=sys.stderr)
         sys.exit(2)
 
     from cgadimpl_amd import configs
