@@ -164,6 +164,12 @@ struct Resident {
     using T = typename S::T;
     static constexpr int W = S::kVec;
     static constexpr int kSlots = red_slots<TPR, G>();
+    // 16 slots per lane (rows of 8193-16384 slots, one row per 1024-lane
+    // workgroup): the packed row fills 64 registers, so nothing derived from
+    // it is kept across a row reduction -- the exponentials are recomputed
+    // when stored, and the slots are made opaque after each reduction so the
+    // compiler re-unpacks them instead of holding 128 unpacked values.
+    static constexpr bool kBig = NV >= 16;
 
     float (*red)[kSlots];
     int parity = 0;
@@ -173,7 +179,7 @@ struct Resident {
     int cols;
     float ncols, inv_cols;
     u32x4 a[NV], b[NV];
-    float kept[NV][W];
+    float kept[kBig ? 1 : NV][W];
 
     __device__ Resident(const RowArgs& p, int64_t rows, int cols_, float (*red_)[kSlots])
         : red(red_), cols(cols_) {
@@ -226,6 +232,17 @@ struct Resident {
         }
         row_reduce<TPR, G, N, R>(res, red, parity);
         parity ^= 1;
+        refresh();
+    }
+
+    __device__ __forceinline__ void refresh() {
+        if constexpr (kBig) {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                if constexpr (NIN == 2) opaque(a[k], b[k]);
+                else asm volatile("" : "+v"(a[k]));
+            }
+        }
     }
 
     template <class F>
@@ -253,7 +270,7 @@ struct Resident {
         m = max([](float z, float) { return z; });
         const float mm = m;
         auto e = [=](float z, float) { return fast_exp(z - mm); };
-        if constexpr (KEEP)
+        if constexpr (KEEP && !kBig)
             s = sum_keep(e);
         else
             s = sum(e);
@@ -286,7 +303,7 @@ struct Resident {
     }
 
     template <class F, class Gf>
-    __device__ __forceinline__ void store_kept(void* out, int acc, F, Gf g) const {
+    __device__ __forceinline__ void store_kept(void* out, int acc, F f, Gf g) const {
         if (!active) return;
         T* o = static_cast<T*>(out) + row * static_cast<int64_t>(cols);
 #pragma unroll
@@ -294,8 +311,16 @@ struct Resident {
             const int col = (t + k * TPR) * W;
             if (col < cols) {
                 float r[W];
+                if constexpr (kBig) {  // recomputed: the same function of the same value
+                    float fa[W], fb[W];
+                    S::unpack(a[k], fa);
+                    if constexpr (NIN == 2) S::unpack(b[k], fb);
 #pragma unroll
-                for (int e = 0; e < W; ++e) r[e] = g(kept[k][e]);
+                    for (int e = 0; e < W; ++e) r[e] = g(f(fa[e], NIN == 2 ? fb[e] : 0.0f));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) r[e] = g(kept[k][e]);
+                }
                 if (acc) {
                     float old[W];
                     S::unpack(load16_stream<S>(o + col), old);
@@ -819,6 +844,7 @@ struct LnBwd {
 // each exponential is computed once and kept for the store.
 struct SmFwd {
     static constexpr int kIn = 1;
+    static constexpr bool kResident16 = true;  // rows of 8193-16384 slots stay resident
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         float m, s;
@@ -860,6 +886,7 @@ struct LseFwd {
 //   dz (+)= dy * (e * (1 / sum(e))),  e = exp(z - m), computed once
 struct LseBwd {
     static constexpr int kIn = 1;
+    static constexpr bool kResident16 = true;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         float m, s;
@@ -932,6 +959,21 @@ struct StreamWideBf16<Op, std::void_t<decltype(Op::kStreamWideBf16)>>
 template <class Op>
 constexpr bool stream_wide_bf16() { return StreamWideBf16<Op>::value; }
 
+// Op::kResident16 when the op declares it, else false: rows of 8193-16384
+// 16-byte slots (65537-131072 bf16 or 32769-65536 fp32 columns) take a
+// 1024-lane workgroup of 16 slots per lane, the row read once, instead of the
+// looped kernels' two reads.  Only ops that read one row tensor and write
+// one: two packed inputs would not fit beside the arithmetic.  Measured on
+// MI355X at bf16 [8192, 128256]: softmax forward 846 against 878 us, log-sum-
+// exp backward 863 against 878 us; the row fills a CU's registers, so a CU
+// holds one row at a time (512 lanes x 32 slots: the same), which is what
+// keeps both near 60 % of HBM peak rather than the two-pass bytes.
+template <class Op, class = void>
+struct Resident16 : std::false_type {};
+template <class Op>
+struct Resident16<Op, std::void_t<decltype(Op::kResident16)>>
+    : std::integral_constant<bool, Op::kResident16> {};
+
 // Every row tensor (in0, in1, out) element-aligned and at in0's offset from a
 // 16-byte boundary, so that each row's head, body and tail line up in all of
 // them.  Column vectors and per-row vectors may sit anywhere.
@@ -954,6 +996,15 @@ int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
     Plan pl;
     if (vec) pl = fwd_plan(cols / S::kVec, rows);
     if (stream_wide_bf16<Op>() && std::is_same<S, BF16>::value && pl.nv == 8) pl = Plan{};
+    if constexpr (Resident16<Op>::value) {
+        const int64_t nslot = cols / S::kVec;
+        if (vec && pl.tpr == 0 && nslot > 8192 && nslot <= 16384) {
+            if (rows > 0x7fffffffLL) return AGK_EINVAL;
+            hipLaunchKernelGGL((row_resident<S, 1024, 16, 1, Op>), dim3(static_cast<unsigned>(rows)),
+                               dim3(1024), 0, st, p, rows, cols);
+            return check_launch();
+        }
+    }
     if (pl.tpr == 0) {
         if (rows > 0x7fffffffLL) return AGK_EINVAL;
         // rows short enough for 32-bit buffer offsets: whole 16-byte slots and
