@@ -479,8 +479,11 @@ def run_c5(steps, warmup, cpu=True):
     """RMSNorm + linear layer (configuration c5): forward + full VJP on one GPU.
 
     fwd: agk_rmsnorm_fwd (h, inv_rms) -> GEMM y = h W
-    bwd: GEMM dh = dy W^T -> GEMM dW = h^T dy (fp32 result) -> agk_rmsnorm_bwd (dx,
+    bwd: GEMM dW = h^T dy (fp32 result) -> GEMM dh = dy W^T -> agk_rmsnorm_bwd (dx,
          dgamma from dh)
+    dW runs before dh: dh then feeds the RMSNorm backward straight from the
+    caches, and the step measured about 8 us shorter that way (1725-1729 us
+    against 1733-1737 us with dh first).
     Every operand is read in the layout it has (W [K, N], h^T and dy with their k
     strided): the GEMM stages either layout itself, so no transposed copy is made.
     The three products are 3 * 2*M*N*K flops; torch.matmul (hipBLASLt) is timed
@@ -516,7 +519,7 @@ def run_c5(steps, warmup, cpu=True):
     ws_dh = gemm_ws(M, K, N, False, True)
     ws_w = gemm_ws(K, N, M, True, False)
     stream = torch.cuda.current_stream()
-    stages = ["rmsnorm_fwd", "gemm_y", "gemm_dh", "gemm_dW", "rmsnorm_bwd"]
+    stages = ["rmsnorm_fwd", "gemm_y", "gemm_dW", "gemm_dh", "rmsnorm_bwd"]
 
     def step(ev=None):
         def mark(i):
@@ -527,9 +530,9 @@ def run_c5(steps, warmup, cpu=True):
         mark(1)
         agk.gemm_bf16(h, W, y, workspace=ws_y, stream=stream)
         mark(2)
-        agk.gemm_bf16(dy, W, dh, trans_b=True, workspace=ws_dh, stream=stream)
-        mark(3)
         agk.gemm_bf16(h, dy, dW, trans_a=True, workspace=ws_w, stream=stream)
+        mark(3)
+        agk.gemm_bf16(dy, W, dh, trans_b=True, workspace=ws_dh, stream=stream)
         mark(4)
         agk.rmsnorm_bwd(x, g, inv, dh, dx=dx, dgamma=dg, workspace=ws_n, stream=stream)
         mark(5)
