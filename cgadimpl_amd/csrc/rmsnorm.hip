@@ -357,7 +357,7 @@ __device__ __forceinline__ void bwd_process(const BwdCtx<S, TPR, NV, G, ACC, KIN
     }
 }
 
-// Runs steps 0 .. steps-1 of c's row sequence with NSET (1 or 2) register
+// Runs steps 0 .. steps-1 of c's row sequence with NSET (1, 2 or 3) register
 // sets, adding each lane's dgamma terms into dg.
 template <class S, int TPR, int NV, int G, int NSET, bool ACC, int KIND>
 __device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC, KIND>& c, int64_t steps,
@@ -370,8 +370,7 @@ __device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC, KIN
             c.issue(A, s);
             bwd_process(c, A, s, static_cast<int>(s & 1), gv, has_gamma, dg, red);
         }
-    } else {
-        static_assert(NSET == 2, "one or two register sets");
+    } else if constexpr (NSET == 2) {
         BwdSet<S, NV, ACC> A, B;
         c.issue(A, 0);
         c.issue(B, 1);
@@ -384,6 +383,29 @@ __device__ __forceinline__ void bwd_segment(const BwdCtx<S, TPR, NV, G, ACC, KIN
             c.issue(A, s + 2);
             bwd_process(c, B, s + 1, 1, gv, has_gamma, dg, red);
             c.issue(B, s + 3);
+        }
+    } else {
+        // Three sets: the parity of the LDS reduction row still alternates
+        // step by step, so it is taken from the step, not from the set.
+        static_assert(NSET == 3, "one, two or three register sets");
+        BwdSet<S, NV, ACC> A, B, C;
+        c.issue(A, 0);
+        c.issue(B, 1);
+        c.issue(C, 2);
+        bwd_process(c, A, 0, 0, gv, has_gamma, dg, red);
+        c.issue(A, 3);
+        bwd_process(c, B, 1, 1, gv, has_gamma, dg, red);
+        c.issue(B, 4);
+        bwd_process(c, C, 2, 0, gv, has_gamma, dg, red);
+        c.issue(C, 5);
+        for (int64_t s = 3; s < steps; s += 3) {  // steps is uniform
+            const int par = static_cast<int>(s & 1);
+            bwd_process(c, A, s, par, gv, has_gamma, dg, red);
+            c.issue(A, s + 3);
+            bwd_process(c, B, s + 1, par ^ 1, gv, has_gamma, dg, red);
+            c.issue(B, s + 4);
+            bwd_process(c, C, s + 2, par, gv, has_gamma, dg, red);
+            c.issue(C, s + 5);
         }
     }
 }
@@ -1021,6 +1043,13 @@ template <class S>
 constexpr int bwd_sets(int nv, int sets) {
     return (std::is_same<S, BF16>::value && nv >= 2) ? 1 : sets;
 }
+// The composition's backward (kBwdRmsMul) does more arithmetic per slot than
+// the others (two products rounded to storage, an extra store stream), so its
+// one-slot shapes keep a third row's loads in flight while a row computes.
+template <class S>
+constexpr int rms_mul_sets(int nv, int sets) {
+    return (nv == 1 && sets == 2) ? 3 : bwd_sets<S>(nv, sets);
+}
 
 template <class S>
 inline Plan bwd_plan(int64_t nslot) {
@@ -1247,7 +1276,8 @@ int launch_rms_mul_bwd_resident(const Plan& p, int64_t nblk, const void* x, cons
 #define AGK_X(a, b, c, d)                                                                  \
     if constexpr (bwd_shape_enabled<S>(a, b)) {                                            \
         if (p.tpr == a && p.nv == b && p.g == c) {                                         \
-            hipLaunchKernelGGL((rms_mul_bwd_resident<S, a, b, c, bwd_sets<S>(b, d), ACC>), \
+            hipLaunchKernelGGL((rms_mul_bwd_resident<S, a, b, c, rms_mul_sets<S>(b, d),    \
+                                                     ACC>),                                \
                                dim3(static_cast<unsigned>(nblk)), dim3(a * c), lds, st, xp, \
                                gp, inv_rms, gyp, dxp, drp, partials, rows, cols);           \
             return check_launch();                                                         \
