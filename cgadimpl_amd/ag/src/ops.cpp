@@ -589,19 +589,21 @@ void vjp_MatMul(Node* n, const Tensor& gy) {
     const bool f32 = av.dtype() == Dtype::Float32;
     const Dtype da_dt = f32 ? Dtype::Float32 : Dtype::BFloat16;
     GradLocks lock(A, B);
-    if (want_a) {
-        bool acc = false;
-        Tensor& da = A->grad_for_write(da_dt, &acc);
-        if (M && K)  // N == 0: an empty sum (zeros, or da unchanged when accumulating)
-            product(f32, gy.data(), N, false, bv.data(), N, true, da.data(), K, da_dt, M, K, N,
-                    acc, "vjp_MatMul dA");
-    }
+    // dB first: dA is what the producer of A's VJP reads next, so it is the
+    // product left in the caches.  The two products are independent.
     if (want_b) {
         bool acc = false;
         Tensor& db = B->grad_for_write(Dtype::Float32, &acc);
         if (K && N)  // M == 0: an empty sum over the batch
             product(f32, av.data(), K, true, gy.data(), N, false, db.data(), N, Dtype::Float32, K,
                     N, M, acc, "vjp_MatMul dB");
+    }
+    if (want_a) {
+        bool acc = false;
+        Tensor& da = A->grad_for_write(da_dt, &acc);
+        if (M && K)  // N == 0: an empty sum (zeros, or da unchanged when accumulating)
+            product(f32, gy.data(), N, false, bv.data(), N, true, da.data(), K, da_dt, M, K, N,
+                    acc, "vjp_MatMul dA");
     }
 }
 
@@ -620,13 +622,6 @@ void vjp_Linear(Node* n, const Tensor& gy) {
     const Tensor& wv = Wn->value;
     const int64_t M = lead_rows(xv), K = xv.cols(), N = wv.shape()[0];
     GradLocks lock(X, Wn, Bn);
-    if (want_x) {  // [M, K] = gy [M, N] . W [N, K]
-        bool acc = false;
-        Tensor& dx = X->grad_for_write(Dtype::BFloat16, &acc);
-        if (M && K)
-            gemm(gy.data(), N, false, wv.data(), K, false, dx.data(), K, Dtype::BFloat16, M, K,
-                 N, acc, "vjp_Linear dX");
-    }
     if (want_w) {  // [N, K] = gy^T [N, M] . X [M, K]
         bool acc = false;
         Tensor& dw = Wn->grad_for_write(Dtype::Float32, &acc);
@@ -644,6 +639,14 @@ void vjp_Linear(Node* n, const Tensor& gy) {
                                ws ? ws->data() : nullptr, wsb, M, N, AGK_BF16, acc ? 1 : 0,
                                stream_arg()),
                   "vjp_Linear db");
+    }
+    // dX last, as in vjp_MatMul: the producer of X's VJP reads it next.
+    if (want_x) {  // [M, K] = gy [M, N] . W [N, K]
+        bool acc = false;
+        Tensor& dx = X->grad_for_write(Dtype::BFloat16, &acc);
+        if (M && K)
+            gemm(gy.data(), N, false, wv.data(), K, false, dx.data(), K, Dtype::BFloat16, M, K,
+                 N, acc, "vjp_Linear dX");
     }
 }
 
