@@ -493,13 +493,14 @@ def rmsnorm_linear_fwd(x, gamma, W, eps: float, stream=None):
 
 
 def rmsnorm_linear_bwd(x, gamma, inv_rms, h, W, dy, dw_dtype=None, stream=None):
-    """VJP of the layer: dh = dy @ W^T, dW = h^T @ dy, then the RMSNorm VJP of dh.
+    """VJP of the layer: dW = h^T @ dy, dh = dy @ W^T, then the RMSNorm VJP of dh.
 
+    dW runs first so that dh is still in the caches when the RMSNorm VJP reads it.
     Returns (dx, dgamma, dW); dW is float32 unless dw_dtype says otherwise.
     """
     torch = _torch()
-    dh = gemm_bf16(dy, W, trans_b=True, workspace=None, stream=stream)
     dW = gemm_bf16(h, dy, trans_a=True, out_dtype=dw_dtype or torch.float32, stream=stream)
+    dh = gemm_bf16(dy, W, trans_b=True, workspace=None, stream=stream)
     dx, dgamma = rmsnorm_bwd(x, gamma, inv_rms, dh, stream=stream)
     return dx, dgamma, dW
 
