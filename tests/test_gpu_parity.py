@@ -350,7 +350,12 @@ def test_sum_rows(cuda, dtype, shape):
                                          ("bf16", (96, 8192)), ("bf16", (17, 100)),
                                          ("f32", (24, 16392)), ("bf16", (9, 32776)),
                                          ("f32", (1100, 20480)), ("bf16", (2, 262144)),
-                                         ("f32", (65536, 4096)), ("bf16", (16384, 8192))])
+                                         ("f32", (65536, 4096)), ("bf16", (16384, 8192)),
+                                         # 1-3 steps per workgroup of the three-set
+                                         # pipeline, ragged row counts, 1-4 rows per step
+                                         ("f32", (300, 4096)), ("bf16", (700, 8192)),
+                                         ("f32", (1000, 1024)), ("bf16", (5000, 2048)),
+                                         ("f32", (2311, 512))])
 def test_rms_mul_bwd(cuda, dtype, shape):
     """Bit-identical to mul_rowbcast_bwd followed by rmsnorm_bwd(gamma=None) on
     the same tensors, overwriting and accumulating; where the oracle is quick,
