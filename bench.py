@@ -91,6 +91,113 @@ class TimingEvent:
             self._hip.hipEventDestroy(self._ev)
 
 
+def _bench_lib():
+    """libagk_bench.so: the benchmark's measurement probes (agk_probe_stream,
+    agk_probe_mfma; cgadimpl_amd/csrc/agk_bench.h), built beside the kernel
+    library but not part of it."""
+    import ctypes
+
+    import cgadimpl_amd as agk
+    global _BENCH_LIB
+    if _BENCH_LIB is None:
+        path = os.path.join(agk.LIB_DIR, "libagk_bench.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+        agk.lib()  # loads torch's HIP runtime first (see cgadimpl_amd.lib)
+        h = ctypes.CDLL(path)
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        h.agk_probe_stream.restype = I
+        h.agk_probe_stream.argtypes = [P, P, P, P, I64, I, I, I, I, P]
+        h.agk_probe_mfma.restype = I
+        h.agk_probe_mfma.argtypes = [P, P, P, I, I, I, P]
+        _BENCH_LIB = h
+    return _BENCH_LIB
+
+
+_BENCH_LIB = None
+
+
+def probe_stream(a, b, c, d, nbytes, reads, writes, nontemporal, grid, stream):
+    """agk_probe_stream: reads `reads` buffers, writes `writes` (a diagnostic)."""
+    rc = _bench_lib().agk_probe_stream(
+        a.data_ptr(), b.data_ptr() if b is not None else None, c.data_ptr(),
+        d.data_ptr() if d is not None else None, int(nbytes), int(reads), int(writes),
+        int(bool(nontemporal)), int(grid), stream.cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"agk_probe_stream failed ({rc})")
+
+
+def gpu_state():
+    """The GPU's shader and memory clocks, board power and temperatures from
+    sysfs (amdgpu's hwmon and pp_dpm files) at the moment of the call, for the
+    device torch runs on; None for what this host does not expose.  Read before
+    and after a timed region, so a slow box shows up as a slow box."""
+    import glob
+    import torch
+    out = {"sclk_mhz": None, "mclk_mhz": None, "power_w": None, "temp_edge_c": None,
+           "temp_junction_c": None, "temp_mem_c": None, "source": None}
+    dev_dir = None
+    try:
+        p = torch.cuda.get_device_properties(torch.cuda.current_device())
+        dom = getattr(p, "pci_domain_id", None)
+        bus = getattr(p, "pci_bus_id", None)
+        slot = getattr(p, "pci_device_id", None)
+        if bus is not None and slot is not None:
+            cand = "/sys/bus/pci/devices/%04x:%02x:%02x.0" % (dom or 0, bus, slot)
+            if os.path.isdir(cand):
+                dev_dir = cand
+    except Exception:  # noqa: BLE001 - diagnostic only
+        pass
+    if dev_dir is None:  # one AMD GPU visible in sysfs: take it
+        cards = [d for d in glob.glob("/sys/class/drm/card*/device")
+                 if os.path.exists(os.path.join(d, "pp_dpm_sclk"))]
+        if len(set(os.path.realpath(c) for c in cards)) == 1:
+            dev_dir = cards[0]
+    if dev_dir is None:
+        out["source"] = "no sysfs device matched"
+        return out
+    out["source"] = os.path.realpath(dev_dir)
+
+    def read(path):
+        try:
+            with open(path) as f:
+                return f.read().strip()
+        except OSError:
+            return None
+
+    def dpm_current(name):
+        txt = read(os.path.join(dev_dir, name))
+        if not txt:
+            return None
+        for ln in txt.splitlines():
+            if ln.rstrip().endswith("*"):
+                num = "".join(ch for ch in ln.split(":", 1)[-1] if ch.isdigit())
+                return int(num) if num else None
+        return None
+
+    hw = sorted(glob.glob(os.path.join(dev_dir, "hwmon", "hwmon*")))
+    h = hw[0] if hw else None
+    if h:
+        f1 = read(os.path.join(h, "freq1_input"))
+        f2 = read(os.path.join(h, "freq2_input"))
+        out["sclk_mhz"] = round(int(f1) / 1e6) if f1 and f1.isdigit() else None
+        out["mclk_mhz"] = round(int(f2) / 1e6) if f2 and f2.isdigit() else None
+        for name in ("power1_average", "power1_input"):
+            v = read(os.path.join(h, name))
+            if v and v.isdigit():
+                out["power_w"] = round(int(v) / 1e6, 1)
+                break
+        for key, name in (("temp_edge_c", "temp1_input"), ("temp_junction_c", "temp2_input"),
+                          ("temp_mem_c", "temp3_input")):
+            v = read(os.path.join(h, name))
+            out[key] = round(int(v) / 1e3, 1) if v and v.lstrip("-").isdigit() else None
+    if out["sclk_mhz"] is None:
+        out["sclk_mhz"] = dpm_current("pp_dpm_sclk")
+    if out["mclk_mhz"] is None:
+        out["mclk_mhz"] = dpm_current("pp_dpm_mclk")
+    return out
+
+
 def graph_replay_ms(body, n, reps=5):
     """Milliseconds per body() when n calls of it are captured once into a HIP
     graph (torch.cuda.CUDAGraph) and the graph is replayed: the GPU's time for
@@ -336,11 +443,13 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     # roofline kernel), recorded on the stream the kernels run on.
     events = [[TimingEvent() for _ in range(2)] for _ in range(steps)]
     torch.cuda.synchronize()
+    state_before = gpu_state()
     t0 = time.perf_counter()
     for i in range(steps):
         step(i, ev_bwd=events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    state_after = gpu_state()
     bwd_each = sorted(e[0].elapsed_time(e[1]) for e in events)
     bwd_ms = sum(bwd_each) / steps
 
@@ -415,6 +524,7 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "bwd": {"avg_ms": round(bwd_ms, 5), "median_ms": round(bwd_each[steps // 2], 5),
                     "alg_bytes": cfg.bwd_bytes(),
                     "gbs": round(bwd_gbs, 2), "frac": round(bwd_gbs / HBM_PEAK_GBS, 4)},
+            "gpu_state": {"before_timed": state_before, "after_timed": state_after},
         },
         "graph": {
             "how": (f"the {steps} steps (then {steps} forwards, then {steps} backwards) "
@@ -541,11 +651,13 @@ def run_c5(steps, warmup, cpu=True):
         step()
     torch.cuda.synchronize()
     events = [[TimingEvent() for _ in range(len(stages) + 1)] for _ in range(steps)]
+    state_before = gpu_state()
     t0 = time.perf_counter()
     for i in range(steps):
         step(events[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    state_after = gpu_state()
     per = {name: sum(e[i].elapsed_time(e[i + 1]) for e in events) / steps
            for i, name in enumerate(stages)}
 
@@ -598,6 +710,7 @@ def run_c5(steps, warmup, cpu=True):
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": None},
         "stages_ms": {k: round(v, 4) for k, v in per.items()},
+        "gpu_state": {"before_timed": state_before, "after_timed": state_after},
         "rmsnorm_gbs": round(norm_bytes / (norm_ms * 1e-3) / 1e9, 1),
         "alone_ms": {k: round(v, 4) for k, v in alone_ms.items()},
         "torch_hipblaslt_ms": {k: round(v, 4) for k, v in torch_ms.items()},
@@ -798,7 +911,7 @@ STREAM_GRIDS = (0, 1024, 8192, 65536)  # 0: one workgroup per 16 KiB chunk
 def stream_probe(mib, steps):
     """The practical HBM ceiling of this device for the path's traffic mixes.
 
-    A streaming kernel (agk_probe_stream: 16-byte slots, four in flight per
+    A streaming kernel (agk_probe_stream in libagk_bench.so: 16-byte slots, four in flight per
     lane) over MIB-MiB buffers, with plain and with non-temporal accesses, one
     workgroup per 16 KiB chunk (grid 0, how the row kernels touch memory) and
     grid-stride at several grid sizes; HIP events on the launch stream.
@@ -822,7 +935,7 @@ def stream_probe(mib, steps):
             per_grid = {}
             for grid in STREAM_GRIDS:
                 def launch():
-                    agk.probe_stream(a, b, c, d, nbytes, reads, writes, nt, grid, stream=stream)
+                    probe_stream(a, b, c, d, nbytes, reads, writes, nt, grid, stream)
                 for _ in range(3):
                     launch()
                 e0, e1 = TimingEvent(), TimingEvent()
@@ -840,6 +953,83 @@ def stream_probe(mib, steps):
             results.append(rec)
             print(json.dumps(rec), flush=True)
     return results
+
+
+def mfma_probe(reps):
+    """What the matrix cores sustain on this device: the bf16 GEMM's inner loop
+    without its global loads and barriers (agk_probe_mfma in libagk_bench.so),
+    256 workgroups of 4 waves (one wave per SIMD, as the GEMM), each wave 16
+    v_mfma_f32_32x32x16_bf16 accumulators.  Mode "lds": the GEMM's fragment
+    reads from LDS one substep ahead of the MFMAs; mode "registers": MFMAs
+    only.  Operand contents: the c5 products' distributions (A ~ N(0,1),
+    B ~ N(0,0.02^2) in bf16), uniform +-[0.5, 2), and zeros.  HIP events give
+    TFLOP/s; wave 0 of every workgroup reads s_memtime and s_memrealtime
+    (100 MHz) around its loop, which give the shader clock it ran at and its
+    cycles per 64-deep k-step (64 MFMAs: 2048 cycles at the full rate).  One
+    JSON line per (mode, data)."""
+    import ctypes
+
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _bench_lib()
+    wg, ksteps = 256, 20000
+    flop = wg * 4 * ksteps * 64 * 32768
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    half = 256 * 64  # bf16 per operand half of the 64 KiB tile
+
+    def uniform_pm():
+        mag = torch.rand(2 * half, generator=gen, device=dev) * 1.5 + 0.5
+        sign = torch.randint(0, 2, (2 * half,), generator=gen, device=dev) * 2 - 1
+        return (mag * sign).bfloat16()
+    datas = (
+        ("c5 operands (A ~ N(0,1), B ~ N(0,0.02^2))",
+         torch.cat([torch.randn(half, generator=gen, device=dev),
+                    torch.randn(half, generator=gen, device=dev) * 0.02]).bfloat16()),
+        ("uniform +-[0.5, 2)", uniform_pm()),
+        ("zeros", torch.zeros(2 * half, dtype=torch.bfloat16, device=dev)),
+    )
+    out = torch.empty(wg * 4, dtype=torch.float32, device=dev)
+    clocks = torch.zeros(wg * 4, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream()
+    recs = []
+    for mode, mode_name in ((0, "lds"), (1, "registers")):
+        for name, src in datas:
+            src = src.contiguous()
+
+            def launch(ck=None):
+                rc = lib.agk_probe_mfma(src.data_ptr(), out.data_ptr(),
+                                        ck.data_ptr() if ck is not None else None, wg, ksteps,
+                                        mode, stream.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"agk_probe_mfma failed ({rc})")
+            for _ in range(2):
+                launch()
+            e0, e1 = TimingEvent(), TimingEvent()
+            e0.record(stream)
+            for _ in range(reps):
+                launch()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            launch(clocks)
+            torch.cuda.synchronize()
+            c = clocks.view(wg, 4).cpu().double()
+            shader = c[:, 1] - c[:, 0]
+            real = c[:, 3] - c[:, 2]
+            ghz = (shader / real * 0.1).median().item()
+            cyc = (shader / ksteps).median().item()
+            tflops = flop / (ms * 1e-3) / 1e12
+            rec = {"mfma_probe": mode_name, "data": name, "workgroups": wg,
+                   "k_steps_per_wave": ksteps, "launches": reps, "ms_per_launch": round(ms, 3),
+                   "tflops": round(tflops, 1),
+                   "pct_of_dense_peak": round(100.0 * tflops / MFMA_BF16_PEAK_TFLOPS, 1),
+                   "shader_ghz": round(ghz, 3), "cycles_per_k_step": round(cyc, 1),
+                   "ideal_cycles_per_k_step": 2048}
+            recs.append(rec)
+            print(json.dumps(rec), flush=True)
+    return recs
 
 
 WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
@@ -1007,6 +1197,10 @@ def main():
     ap.add_argument("--stream-probe", type=int, default=0, metavar="MIB",
                     help="only time the HBM streaming probe (copy, 2 reads + 1 write, read "
                          "only; plain and non-temporal) over MIB-MiB buffers, then exit")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only run the MFMA probe (the bf16 GEMM's inner loop without loads or "
+                         "barriers, by operand content, with the shader clock it ran at), then "
+                         "exit")
     ap.add_argument("--wide", action="store_true",
                     help="only time rows wider than the register-resident kernels: the split "
                          "paths against the one-workgroup-per-row kernels, and softmax / "
@@ -1018,6 +1212,9 @@ def main():
         return
     if args.stream_probe:
         stream_probe(args.stream_probe, min(args.steps, 50))
+        return
+    if args.mfma_probe:
+        mfma_probe(min(args.steps, 5))
         return
     if args.wide:
         run_wide(min(args.steps, 20))

@@ -17,7 +17,7 @@ __all__ = [
     "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
     "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "rmsnorm_jvp", "layernorm_fwd",
     "layernorm_bwd", "softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
-    "logsumexp_jvp", "probe_stream", "rms_mul_bwd", "sum_rows", "linear_bf16",
+    "logsumexp_jvp", "rms_mul_bwd", "sum_rows", "linear_bf16",
     "mul_bcast_shape", "mul_bcast_fwd", "mul_bcast_bwd",
     "mul_bcast_grad_dtype", "gemm_f32", "AGK_F32", "AGK_BF16", "STATUS",
 ]
@@ -80,8 +80,7 @@ SIGNATURES = {
     "agk_logsumexp_fwd": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_logsumexp_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_logsumexp_jvp": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
-    "agk_probe_stream": (ctypes.c_int, [_P, _P, _P, _P, _I64, ctypes.c_int, ctypes.c_int,
-                                        ctypes.c_int, ctypes.c_int, _P]),
+    "agk_fill": (ctypes.c_int, [_P, _I64, ctypes.c_float, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
     "agk_version": (ctypes.c_char_p, []),
@@ -605,12 +604,3 @@ def logsumexp_jvp(z, tz, ty=None, stream=None):
                                  _stream(stream))
     _check(rc, "agk_logsumexp_jvp")
     return ty
-
-
-def probe_stream(a, b, c, d, nbytes: int, reads: int, writes: int, nontemporal: bool, grid: int,
-                 stream=None) -> None:
-    """HBM streaming probe (diagnostic): reads `reads` buffers, writes `writes`."""
-    rc = lib().agk_probe_stream(_ptr(a), _ptr(b) if b is not None else None, _ptr(c),
-                                _ptr(d) if d is not None else None, int(nbytes), int(reads),
-                                int(writes), int(bool(nontemporal)), int(grid), _stream(stream))
-    _check(rc, "agk_probe_stream")

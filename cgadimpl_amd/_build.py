@@ -3,6 +3,8 @@
 Outputs (in-tree, git-ignored, shipped with the source tree):
   cgadimpl_amd/lib/libagk_rmsnorm.so   HIP kernels + C ABI (include/agk_rmsnorm.h,
                                        include/agk_rowops.h)
+  cgadimpl_amd/lib/libagk_bench.so     bench.py's measurement probes (csrc/agk_bench.h;
+                                       not product ABI)
   cgadimpl_amd/lib/libagk_synth.so     seeded synthetic input generator (host)
   cgadimpl_amd/lib/libag.so            the C++ graph layer (ag::Value, rms, rms_norm,
                                        mul, backward) over the C ABI (host C++)
@@ -88,9 +90,11 @@ def host_library(name: str, sources: list[str], compiler: str = "g++") -> str:
 
 # The kernel library's sources, and what it links beyond the HIP runtime
 # (rocBLAS for the graph layer's fp32 matmul, gemm_f32.hip).
-KERNEL_SOURCES = ["rmsnorm.hip", "gemm.hip", "gemm_f32.hip", "rowops.hip", "bcast.hip",
-                  "probe.hip"]
+KERNEL_SOURCES = ["rmsnorm.hip", "gemm.hip", "gemm_f32.hip", "rowops.hip", "bcast.hip"]
 KERNEL_LIBS = [f"-L{ROCM}/lib", "-lrocblas", f"-Wl,-rpath,{ROCM}/lib"]
+# The benchmark's own measurement probes (csrc/agk_bench.h): loaded by bench.py
+# only, not part of the product ABI.
+BENCH_SOURCES = ["probe.hip", "mfma_probe.hip"]
 
 AG_DIR = os.path.join(PKG, "ag")
 AG_SOURCES = ["tensor.cpp", "graph.cpp", "ops.cpp", "autodiff.cpp", "nn.cpp", "runtime.cpp"]
@@ -161,6 +165,7 @@ def build_all(verbose: bool = True) -> list[str]:
     os.makedirs(LIB, exist_ok=True)
     jobs = [
         lambda: hip_library("libagk_rmsnorm.so", KERNEL_SOURCES, libs=KERNEL_LIBS),
+        lambda: hip_library("libagk_bench.so", BENCH_SOURCES),
         lambda: host_library("libagk_synth.so", ["synth.cpp"]),
     ]
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:

@@ -47,6 +47,13 @@ struct Value {
 
     Value() = default;
     explicit Value(std::shared_ptr<Node> n) : node(std::move(n)) {}
+    // A scalar literal (cgadimpl/include/ad/core/graph.hpp:22,
+    // cgadimpl/src/core/graph.cpp:91-105): a leaf holding a one-element [1]
+    // float32 tensor, named "scalar_literal", that requires no gradient.  Not
+    // explicit, as in the reference, so `rms(x) * 0.5f` and `0.5f * rms(x)`
+    // convert the float.  Used with a bfloat16 operand, mul takes the literal
+    // in bfloat16 (rounded to nearest even).
+    Value(float v);
 
     const std::vector<int64_t>& shape() const;
     Tensor& val();
@@ -73,6 +80,9 @@ struct Node : std::enable_shared_from_this<Node> {
     Op op = Op::Leaf;
     bool is_leaf = false;
     float eps = 0.0f;  // RMSNorm / RMSNormAffine: the eps of the forward pass
+    // Value(float): the literal's value, so an op can take it in another dtype
+    bool is_scalar_literal = false;
+    float literal_value = 0.0f;
 
     std::atomic<int> child_grad_count{0};
     std::mutex grad_mutex;

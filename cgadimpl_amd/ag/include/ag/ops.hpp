@@ -25,16 +25,21 @@ Value rms(const Value& x);
 // gradient of gamma is fp32 whatever gamma's storage type.
 Value rms_norm(const Value& x, const Value& gamma, float eps = 1e-5f);
 
-// Element-wise product where one operand is a row vector ([D] or [1, D])
-// broadcast over the other's leading axes, or both have the same shape
-// (cgadimpl/src/ops/arithmetic.cpp:31-39).  The gradient of a broadcast
-// operand is fp32.  Other broadcasts throw std::runtime_error.
+// Element-wise product under numpy broadcasting (cgadimpl/src/ops/arithmetic.cpp:31-39):
+// equal shapes and a row vector ([D] or [1, D]) over the other's leading axes
+// take the row kernels, every other broadcast (e.g. [B, T, D] * [B, 1, D], a
+// 0-d or [1] scalar) the general broadcast kernels.  The output has the
+// broadcast shape.  The gradient of a broadcast operand is fp32, summed over
+// its broadcast axes; an operand that covers the output gets its gradient in
+// its own dtype.  Shapes that do not broadcast, or operands of different
+// dtypes, throw std::runtime_error.
 Value mul(const Value& a, const Value& b);
 inline Value operator*(const Value& a, const Value& b) { return mul(a, b); }
 
-// a [..., K] (bf16) times b [K, N] (bf16) -> [..., N] (bf16), on the MFMA GEMM
-// (cgadimpl/src/ops/linalg.cpp:12-20).  a's gradient is bf16, b's is fp32
-// (a weight accumulates in fp32).  fp32 operands throw std::runtime_error.
+// a [..., K] times b [K, N] -> [..., N] (cgadimpl/src/ops/linalg.cpp:12-20).
+// bf16 operands run on the MFMA GEMM; a's gradient is bf16, b's is fp32 (a
+// weight accumulates in fp32).  fp32 operands run on the fp32 GEMM, with fp32
+// gradients.  Operands of different dtypes throw std::runtime_error.
 Value matmul(const Value& a, const Value& b);
 
 // x [..., K] times w [N, K] transposed, plus b [N] or [1, N] -> [..., N], all

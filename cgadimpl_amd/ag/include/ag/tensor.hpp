@@ -92,8 +92,10 @@ std::shared_ptr<CaptureArena> capture_arena(hipStream_t stream);
 // runtime, which kept the host from running ahead of the GPU).  Blocks never
 // move between streams.  The cache holds at most cache_limit() bytes per
 // device: a block freed past the limit sends the device's oldest cached blocks
-// back to the pool (hipFreeAsync on their own streams).  When the pool cannot
-// serve a request, the cache is emptied and the request retried once.
+// back to HIP (one device synchronisation, then hipFree; the streams they were
+// cached under are never called, so a destroyed stream's blocks are safe to
+// evict).  When the pool cannot serve a request, the cache is emptied and the
+// request retried once, unless a stream is being captured.
 class Storage {
   public:
     Storage(size_t bytes, hipStream_t stream);
@@ -116,9 +118,9 @@ class Storage {
 // Returns every cached pool block of the current device to HIP (after a
 // device synchronisation), to give the memory back.
 void release_cached_memory();
-// Returns the cached blocks of `stream` (current device) to the pool, ordered
-// on that stream.  Call it before destroying a stream that graph-layer tensors
-// were allocated on: a later stream created with the same handle would
+// Returns the cached blocks of `stream` (current device) to HIP, after a
+// device synchronisation.  Call it before destroying a stream that graph-layer
+// tensors were allocated on: a later stream created with the same handle would
 // otherwise take blocks whose last users it is not ordered after.
 void release_stream_cache(hipStream_t stream);
 // Bytes held in the cache on the current device (diagnostic).
@@ -140,6 +142,10 @@ class Tensor {
     static Tensor empty(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
     static Tensor zeros(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
     static Tensor ones(const std::vector<int64_t>& shape, Dtype dt = Dtype::Float32);
+    // Every element `value` (stored in dt), written by a kernel (agk_fill), so
+    // it may be called while the current stream is captured.
+    static Tensor full(const std::vector<int64_t>& shape, float value,
+                       Dtype dt = Dtype::Float32);
     // Copies `shape`-many elements of `dt` from host memory (bf16 as raw bits).
     static Tensor from_host(const void* src, const std::vector<int64_t>& shape,
                             Dtype dt = Dtype::Float32);

@@ -60,6 +60,13 @@ Tensor& Node::grad_for_write(Dtype dt, bool* accumulate) {
     return grad;
 }
 
+Value::Value(float v)
+    : node(std::make_shared<Node>(Tensor::full({1}, v, Dtype::Float32), Op::Leaf, false,
+                                  "scalar_literal")) {
+    node->is_scalar_literal = true;
+    node->literal_value = v;
+}
+
 const std::vector<int64_t>& Value::shape() const { return node->value.shape(); }
 Tensor& Value::val() { return node->value; }
 const Tensor& Value::val() const { return node->value; }

@@ -229,10 +229,23 @@ std::shared_ptr<Node> rms_norm_nodeops(const std::shared_ptr<Node>& x,
     return n;
 }
 
-std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a,
-                                  const std::shared_ptr<Node>& b) {
-    require_value(a, "mul");
-    require_value(b, "mul");
+// A scalar literal (Value(float)) next to an operand of another dtype: the
+// same literal in that dtype (a new leaf; the caller's literal is unchanged).
+std::shared_ptr<Node> literal_like(const std::shared_ptr<Node>& lit, const Tensor& other) {
+    if (!lit->is_scalar_literal || lit->value.dtype() == other.dtype()) return lit;
+    auto n = std::make_shared<Node>(Tensor::full({1}, lit->literal_value, other.dtype()),
+                                    Op::Leaf, false, "scalar_literal");
+    n->is_scalar_literal = true;
+    n->literal_value = lit->literal_value;
+    return n;
+}
+
+std::shared_ptr<Node> mul_nodeops(const std::shared_ptr<Node>& a_in,
+                                  const std::shared_ptr<Node>& b_in) {
+    require_value(a_in, "mul");
+    require_value(b_in, "mul");
+    const std::shared_ptr<Node> a = literal_like(a_in, b_in->value);
+    const std::shared_ptr<Node> b = literal_like(b_in, a->value);
     const Tensor& av = a->value;
     const Tensor& bv = b->value;
     if (av.dtype() != bv.dtype()) fail("mul: operands must have the same dtype");

@@ -1,6 +1,7 @@
 // tensor.cpp -- device tensors on HIP's stream-ordered memory pool.
 #include "ag/tensor.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <iterator>
@@ -128,9 +129,12 @@ namespace {
 // Freed pool blocks by (device, stream), then by size.  A request takes the
 // smallest cached block of at least its size and at most 5/4 of it.  The bytes
 // held per device are capped (cache_limit): a block freed past the cap pushes
-// out the device's oldest cached blocks, which go back to the pool with a
-// stream-ordered hipFreeAsync on the stream they were used on.  The cache is
-// never destroyed: freeing blocks at exit would race the runtime's teardown.
+// out the device's oldest cached blocks.  A block's stream is used only as a
+// key: the stream may have been destroyed since the block was cached (a caller
+// that skipped release_stream_cache), so blocks leave the cache through
+// return_blocks, which synchronises the device and frees them without naming
+// any stream.  The cache is never destroyed: freeing blocks at exit would race
+// the runtime's teardown.
 struct CachedBlock {
     int dev;
     hipStream_t stream;
@@ -182,20 +186,61 @@ void* take_cached(int dev, hipStream_t stream, size_t need, size_t* got) {
     return p;
 }
 
-// Returns blocks to the pool: stream-ordered on the stream each was used on,
-// with that stream's device current (the null stream means that device's).
-void free_blocks(const std::vector<CachedBlock>& blocks) {
-    if (blocks.empty()) return;
-    int cur = 0;
-    hip_check(hipGetDevice(&cur), "hipGetDevice");
-    int dev = cur;
-    for (const CachedBlock& b : blocks) {
-        if (b.dev != dev) hip_check(hipSetDevice(dev = b.dev), "hipSetDevice");
-        hip_check(hipFreeAsync(b.ptr, b.stream), "hipFreeAsync");
+// Makes `dev` current for a scope and restores the caller's device after it,
+// also when a HIP call in between throws.
+class DeviceGuard {
+  public:
+    DeviceGuard() {
+        hip_check(hipGetDevice(&saved_), "hipGetDevice");
+        current_ = saved_;
     }
-    if (dev != cur) hip_check(hipSetDevice(cur), "hipSetDevice");
-}
+    ~DeviceGuard() {
+        if (current_ != saved_) (void)hipSetDevice(saved_);
+    }
+    void set(int dev) {
+        if (dev == current_) return;
+        hip_check(hipSetDevice(dev), "hipSetDevice");
+        current_ = dev;
+    }
+    DeviceGuard(const DeviceGuard&) = delete;
+    DeviceGuard& operator=(const DeviceGuard&) = delete;
 
+  private:
+    int saved_ = 0;
+    int current_ = 0;
+};
+
+// Hands blocks back to HIP: per device, one device synchronisation (every
+// user of a block, on whatever stream, has then finished) and a hipFree per
+// block.  No stream handle is used, so blocks of destroyed streams are freed
+// like any other.  Every block is attempted; the first failure is thrown after
+// the caller's device is restored.
+void return_blocks(std::vector<CachedBlock> blocks) {
+    if (blocks.empty()) return;
+    std::stable_sort(blocks.begin(), blocks.end(),
+                     [](const CachedBlock& a, const CachedBlock& b) { return a.dev < b.dev; });
+    DeviceGuard guard;
+    std::string first_error;
+    auto note = [&](hipError_t e, const char* what) {
+        if (e != hipSuccess && first_error.empty())
+            first_error = std::string(what) + ": " + hipGetErrorString(e);
+    };
+    int synced = -1;
+    for (const CachedBlock& b : blocks) {
+        try {
+            guard.set(b.dev);
+        } catch (const std::exception& e) {
+            if (first_error.empty()) first_error = e.what();
+            continue;
+        }
+        if (synced != b.dev) {
+            note(hipDeviceSynchronize(), "hipDeviceSynchronize");
+            synced = b.dev;
+        }
+        note(hipFree(b.ptr), "hipFree");
+    }
+    if (!first_error.empty()) fail(first_error);
+}
 }  // namespace
 
 Storage::Storage(size_t bytes, hipStream_t stream) : bytes_(bytes), stream_(stream) {
@@ -209,9 +254,11 @@ Storage::Storage(size_t bytes, hipStream_t stream) : bytes_(bytes), stream_(stre
     if ((ptr_ = take_cached(device_, stream, need, &block_))) return;
     retain_pool_memory();
     hipError_t e = hipMallocAsync(&ptr_, need, stream);
-    if (e == hipErrorOutOfMemory) {
+    if (e == hipErrorOutOfMemory && g_narenas.load() == 0) {
         // The pool is out of memory, possibly to blocks this cache holds for
-        // other sizes or streams: hand them all back and try once more.
+        // other sizes or streams: hand them all back and try once more.  Not
+        // while any stream is being captured: the device synchronisation and
+        // frees of release_cached_memory would invalidate that capture.
         (void)hipGetLastError();
         release_cached_memory();
         e = hipMallocAsync(&ptr_, need, stream);
@@ -251,30 +298,28 @@ Storage::~Storage() {
         }
     }
     try {
-        free_blocks(evicted);
-    } catch (...) {  // a destructor must not throw; the block is lost to the pool
+        return_blocks(std::move(evicted));
+    } catch (...) {  // a destructor must not throw; a block that failed is lost to the pool
     }
 }
 
 void release_cached_memory() {
     int dev = 0;
     hip_check(hipGetDevice(&dev), "hipGetDevice");
-    std::vector<void*> blocks;
+    std::vector<CachedBlock> blocks;
     {
         BlockCache& c = block_cache();
         std::lock_guard<std::mutex> lock(c.mu);
         for (auto it = c.order.begin(); it != c.order.end();) {
             auto next = std::next(it);
             if (it->dev == dev) {
-                blocks.push_back(it->ptr);
+                blocks.push_back(*it);
                 unlink_block(c, it);
             }
             it = next;
         }
     }
-    if (blocks.empty()) return;
-    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
-    for (void* p : blocks) hip_check(hipFree(p), "hipFree");
+    return_blocks(std::move(blocks));
 }
 
 void release_stream_cache(hipStream_t stream) {
@@ -295,7 +340,7 @@ void release_stream_cache(hipStream_t stream) {
             it = next;
         }
     }
-    free_blocks(blocks);
+    return_blocks(std::move(blocks));
 }
 
 size_t cached_bytes() {
@@ -322,7 +367,7 @@ void set_cache_limit(size_t bytes) {
             it = next;
         }
     }
-    free_blocks(evicted);
+    return_blocks(std::move(evicted));
 }
 
 size_t cache_limit() {
@@ -369,6 +414,14 @@ Tensor Tensor::ones(const std::vector<int64_t>& shape, Dtype dt) {
         hip_check(hipMemsetD16Async(reinterpret_cast<hipDeviceptr_t>(t.data()), 0x3f80u, n,
                                     current_stream()),
                   "hipMemsetD16Async");
+    return t;
+}
+
+Tensor Tensor::full(const std::vector<int64_t>& shape, float value, Dtype dt) {
+    Tensor t = empty(shape, dt);
+    const int rc = agk_fill(t.data(), t.numel(), value, dt == Dtype::Float32 ? AGK_F32 : AGK_BF16,
+                            reinterpret_cast<agk_stream_t>(current_stream()));
+    internal::agk_check(rc, "ag::Tensor::full");
     return t;
 }
 

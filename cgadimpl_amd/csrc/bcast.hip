@@ -468,6 +468,38 @@ int bcast_bwd_one(const void* gy, const void* other, const Aligned& t, const Ali
 
 }  // namespace agk
 
+namespace agk {
+
+// dst[i] = value for i < n (a grid-stride loop of 256-lane workgroups).
+template <class S>
+__global__ __launch_bounds__(256) void fill_kernel(typename S::T* __restrict__ dst, int64_t n,
+                                                   float value) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+        S::put(dst + i, value);
+}
+
+}  // namespace agk
+
+extern "C" int agk_fill(void* dst, int64_t n, float value, int dtype, agk_stream_t stream) {
+    using namespace agk;
+    if (n < 0) return AGK_EINVAL;
+    if (dtype != AGK_F32 && dtype != AGK_BF16) return AGK_EDTYPE;
+    if (n == 0) return AGK_OK;
+    if (!dst) return AGK_EINVAL;
+    clear_pending_error();
+    const int64_t blocks64 = (n + 255) / 256;
+    const unsigned blocks = static_cast<unsigned>(blocks64 < 4096 ? blocks64 : 4096);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (dtype == AGK_F32)
+        hipLaunchKernelGGL(fill_kernel<F32>, dim3(blocks), dim3(256), 0, st,
+                           static_cast<float*>(dst), n, value);
+    else
+        hipLaunchKernelGGL(fill_kernel<BF16>, dim3(blocks), dim3(256), 0, st,
+                           static_cast<uint16_t*>(dst), n, value);
+    return check_launch();
+}
+
 extern "C" int agk_mul_bcast_shape(const int64_t* a_shape, int a_ndim, const int64_t* b_shape,
                                    int b_ndim, int64_t* out_shape, int* out_ndim) {
     using namespace agk;

@@ -3,7 +3,8 @@
 // write, as the forward; two reads + one write, as the backward; reads only),
 // with and without the non-temporal cache policy the row kernels use.  It is
 // the practical ceiling the row kernels are measured against, next to the
-// vendor peak.  No reference counterpart; a diagnostic of this library.
+// vendor peak.  No reference counterpart; part of the benchmark's own library
+// (libagk_bench.so), not of the kernel library.
 //
 // Two access patterns.  Grid-stride: each lane moves 16-byte slots in a
 // grid-stride loop with four independent slots in flight per iteration.
@@ -16,7 +17,7 @@
 
 #include <stdint.h>
 
-#include "agk_rmsnorm.h"
+#include "agk_bench.h"
 #include "rowcommon.hpp"
 
 namespace agk {

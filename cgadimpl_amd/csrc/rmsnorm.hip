@@ -1452,16 +1452,21 @@ inline size_t bwd_res_wide_bytes(int64_t rows, int cols, bool comp) {
     return static_cast<size_t>(nblk) * static_cast<size_t>(cols) * 4u;
 }
 
+// The workspace must hold the dgamma partial rows only when dgamma is wanted.
 inline bool bwd_takes_wide(const void* x, const void* gamma, const void* dy, const void* dx,
-                           int64_t rows, int cols, int dtype, const void* ws, size_t ws_bytes) {
-    if (!ws || !aligned16(ws) || ws_bytes < wide_ws_bytes(rows, cols, false)) return false;
+                           int64_t rows, int cols, int dtype, const void* ws, size_t ws_bytes,
+                           bool want_dgamma) {
+    const size_t need =
+        want_dgamma ? wide_ws_bytes(rows, cols, false) : wide_ws_stats_bytes(rows, cols);
+    if (!ws || !aligned16(ws) || ws_bytes < need) return false;
     return dtype == AGK_F32 ? bwd_wide_possible<F32>(x, gamma, dy, dx, rows, cols)
                             : bwd_wide_possible<BF16>(x, gamma, dy, dx, rows, cols);
 }
 
 // The RMSNorm backward with validated arguments.  Rows too wide for the
 // resident shapes take the wide path when `ws` (16-byte aligned, ws_bytes
-// long) holds wide_ws_bytes(rows, cols, false); otherwise dgamma partials go
+// long) holds wide_ws_bytes(rows, cols, false) (wide_ws_stats_bytes when
+// dgamma is NULL); otherwise dgamma partials go
 // to `partials` (which must hold bwd_partials_bytes when dgamma != NULL).
 inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rms,
                            const void* dy, void* dx, float* dgamma, float* partials, void* ws,
@@ -1473,7 +1478,7 @@ inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rm
                                               rows, cols, acc_dx, acc_dg, st)
                    : launch_wide_res_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
                                                dgamma, rows, cols, acc_dx, acc_dg, st);
-    if (bwd_takes_wide(x, gamma, dy, dx, rows, cols, dtype, ws, ws_bytes))
+    if (bwd_takes_wide(x, gamma, dy, dx, rows, cols, dtype, ws, ws_bytes, dgamma != nullptr))
         return dtype == AGK_F32
                    ? launch_wide_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, dgamma, ws, rows,
                                           cols, acc_dx, acc_dg, st)
@@ -1628,11 +1633,13 @@ int agk_rmsnorm_bwd_noalloc(const void* x, const void* gamma, const float* inv_r
     }
     // Rows too wide for the resident shapes: the wide path with the scratch
     // array as its workspace, as agk_rmsnorm_bwd takes it with the workspace
-    // agk_rmsnorm_bwd_workspace_bytes asks for.
+    // agk_rmsnorm_bwd_workspace_bytes asks for (with dgamma NULL, only the
+    // row statistics must fit).
     const bool wide = dtype == AGK_F32 ? bwd_wide_possible<F32>(x, gamma, dy, dx, rows, c)
                                        : bwd_wide_possible<BF16>(x, gamma, dy, dx, rows, c);
     if (wide) {
-        if (wide_ws_bytes(rows, c, false) > AGK_NOALLOC_SCRATCH_BYTES) return AGK_EWORKSPACE;
+        const size_t need = dgamma ? wide_ws_bytes(rows, c, false) : wide_ws_stats_bytes(rows, c);
+        if (need > AGK_NOALLOC_SCRATCH_BYTES) return AGK_EWORKSPACE;
         float* ws = nullptr;
         if (int rc = scratch_on_device(st, &ws)) return rc;
         return rmsnorm_bwd_run(x, gamma, inv_rms, dy, dx, dgamma, ws, ws,

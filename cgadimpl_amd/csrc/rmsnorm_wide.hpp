@@ -87,19 +87,20 @@ inline void wide_blocking(int64_t rows, int cols, bool comp, int64_t& rb, int64_
     }
 }
 
-// Workspace layout of the wide backward: [dgamma partial rows: prows x cols
-// fp32] [segment partials: rows x nseg fp32] [coefficients: rows fp32], each
-// region 256-byte aligned.
+// Workspace layout of the wide backward: [segment partials: rows x nseg fp32]
+// [coefficients: rows fp32] [dgamma partial rows: prows x cols fp32], each
+// region 256-byte aligned.  The row statistics come first, so a dx-only call
+// needs only the bytes before the partial rows (wide_ws_stats_bytes).
 struct WideWs {
     size_t partials = 0, segs = 0, coefs = 0, total = 0;
 };
 inline WideWs wide_ws_layout(int64_t rows, int cols, int64_t prows) {
     const WidePlan p = wide_plan(rows, cols);
     WideWs w;
-    w.partials = 0;
-    w.segs = round256(static_cast<size_t>(prows) * static_cast<size_t>(cols) * 4u);
-    w.coefs = w.segs + round256(static_cast<size_t>(rows) * static_cast<size_t>(p.nseg) * 4u);
-    w.total = w.coefs + round256(static_cast<size_t>(rows) * 4u);
+    w.segs = 0;
+    w.coefs = round256(static_cast<size_t>(rows) * static_cast<size_t>(p.nseg) * 4u);
+    w.partials = w.coefs + round256(static_cast<size_t>(rows) * 4u);
+    w.total = w.partials + round256(static_cast<size_t>(prows) * static_cast<size_t>(cols) * 4u);
     return w;
 }
 inline WideWs wide_ws_layout(int64_t rows, int cols, bool comp) {
@@ -111,6 +112,12 @@ inline WideWs wide_ws_layout(int64_t rows, int cols, bool comp) {
 inline size_t wide_ws_bytes(int64_t rows, int64_t cols, bool comp) {
     if (cols < kWideMinCols || rows <= 0) return 0;
     return wide_ws_layout(rows, static_cast<int>(cols), comp).total;
+}
+// Bytes the wide RMSNorm backward needs when it writes no dgamma: the row
+// statistics only.
+inline size_t wide_ws_stats_bytes(int64_t rows, int64_t cols) {
+    if (cols < kWideMinCols || rows <= 0) return 0;
+    return wide_ws_layout(rows, static_cast<int>(cols), int64_t{0}).partials;
 }
 
 // Per (row, segment): the segment's sum of x^2 (kWideSumSq) or of g*x with

@@ -627,7 +627,9 @@ struct LoopedVec {
     // maximum mn = max(m, its maximum) and s = s * exp(m - mn) + the sum of
     // its exp(a - mn) (an update that leaves mn at -inf changes nothing); then
     // M = the row maximum of m and s = the row sum of s * exp(m - M), both over
-    // the row tree.
+    // the row tree.  A row that is -inf throughout gives s = NaN, as the
+    // two-pass rule does (its exp(-inf - -inf) terms are NaN), so such a row
+    // comes out NaN on every path.
     template <bool KEEP>
     __device__ __forceinline__ void max_sumexp(float& m_out, float& s_out) {
         float m = -__builtin_inff(), s = 0.0f;
@@ -672,7 +674,7 @@ struct LoopedVec {
         row_reduce<kVecLanes, 1, 1, SumR>(q, red, parity);
         parity ^= 1;
         m_out = M;
-        s_out = q[0];
+        s_out = M == -__builtin_inff() ? __builtin_nanf("") : q[0];
     }
 
     template <class F>

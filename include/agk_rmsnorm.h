@@ -120,8 +120,10 @@ size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
  * workspace must hold at least agk_rmsnorm_bwd_workspace_bytes(rows, cols)
  * bytes when dgamma != NULL.  With dgamma == NULL it may be NULL; rows of at
  * least AGK_WIDE_MIN_COLS columns then take the one-workgroup-per-row-block
- * kernel, and take the split path only when a 16-byte aligned workspace of
- * that size is given.                                                        */
+ * kernel, and take the split path only when a 16-byte aligned workspace is
+ * given that holds the split path's row statistics (rows * ceil(cols / 4096)
+ * segment partials and rows coefficients, fp32, each region rounded up to
+ * 256 bytes; agk_rmsnorm_bwd_workspace_bytes(rows, cols) always does).      */
 int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms,
                     const void* dy, void* dx, float* dgamma, void* workspace,
                     size_t workspace_bytes, int64_t rows, int64_t cols,
@@ -138,7 +140,10 @@ int agk_rmsnorm_bwd(const void* x, const void* gamma, const float* inv_rms,
  * register-resident path; the split path's partial rows, segment sums and
  * coefficients for aligned rows of AGK_WIDE_MIN_COLS columns and more, about
  * 16 MiB + rows * ceil(cols / 4096) * 4 bytes; the looped path's row blocks
- * otherwise) return AGK_EWORKSPACE.  Every call on a device shares that
+ * otherwise) return AGK_EWORKSPACE.  With dgamma == NULL only the split
+ * path's row statistics must fit, and the split path is taken: dx equals
+ * agk_rmsnorm_bwd's given a workspace of agk_rmsnorm_bwd_workspace_bytes
+ * (what the reference-shaped callers pass).  Every call on a device shares that
  * device's array: calls that overlap in time on one device race, so callers
  * serialise them (one stream per device, or their own ordering).           */
 #define AGK_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
@@ -192,6 +197,13 @@ int agk_mul_bcast_fwd(const void* a, const int64_t* a_shape, int a_ndim,
 int agk_mul_bcast_bwd(const void* gy, const void* a, const int64_t* a_shape, int a_ndim,
                       const void* b, const int64_t* b_shape, int b_ndim, void* da,
                       void* db, int dtype, int accumulate, agk_stream_t stream);
+
+/* dst[0 .. n) = value, stored in dtype (bf16: rounded to nearest even):
+ * OwnTensor::Tensor::full, which the reference's scalar literal
+ * Value(float) uses (cgadimpl/src/core/graph.cpp:91-105).  A kernel, not a
+ * memset, so that it can be captured into a HIP graph (the value travels as
+ * a kernel argument).  n == 0 is a no-op.                                  */
+int agk_fill(void* dst, int64_t n, float value, int dtype, agk_stream_t stream);
 
 /* fp32 GEMM for the graph layer's matmul on float32 tensors
  * (cgadimpl/src/ops/linalg.cpp:12-20; VJP autodiff_vjp_ops.cpp:258-263):
@@ -307,18 +319,6 @@ int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_ds
  * directly.  Used by the tests to run every reachable shape.                 */
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan);
-
-/* Diagnostic, with no counterpart in the reference: an HBM streaming probe,
- * the practical ceiling the row kernels are measured against.  grid > 0: a
- * grid-stride kernel of `grid` 256-lane workgroups; grid == 0: one 256-lane
- * workgroup per contiguous 16 KiB chunk of each buffer.  It moves `bytes`
- * (a multiple of 16) per buffer in 16-byte slots: reads == 1 reads a,
- * reads == 2 reads a and b; writes == 1 writes c (a, or a ^ b), writes == 2
- * writes c and d, writes == 0 writes nothing (c must still point at 16
- * writable bytes).  nontemporal != 0 sets the non-temporal cache policy on
- * every access, as the row kernels do.                                     */
-int agk_probe_stream(const void* a, const void* b, void* c, void* d, int64_t bytes, int reads,
-                     int writes, int nontemporal, int grid, agk_stream_t stream);
 
 /* Human-readable name of a status code (static storage). */
 const char* agk_status_str(int status);

@@ -627,6 +627,7 @@ void test_user_stream() {
                x.grad().to_host_f32() == ref_dx && g.grad().to_host_f32() == ref_dg);
     }
     (void)hipStreamSynchronize(s);
+    release_stream_cache(s);  // before the handle dies (a new stream may reuse it)
     (void)hipStreamDestroy(s);
 }
 
@@ -648,6 +649,85 @@ Value bf16_leaf(const std::vector<float>& v, const std::vector<int64_t>& shape, 
     Tensor t = Tensor::from_host(b.data(), shape, Dtype::BFloat16);
     t.set_requires_grad(req);
     return make_tensor(t, name);
+}
+
+// A broadcast operand's gradient is fp32 (summed over the broadcast axes),
+// while an operand that covers a product's output gets its gradient in its own
+// dtype.  A bf16 node that receives both kinds cannot add them: backward
+// throws (a documented restriction), naming the gradient that did not match.
+void test_bf16_mixed_gradient_dtypes() {
+    const int64_t B = 2, T = 3, D = 8;
+    Value x = bf16_leaf(normal(B * T * D, 95), {B, T, D}, "x");
+    Value s = bf16_leaf(normal(B * D, 96), {B, 1, D}, "s");
+    bool threw = false;
+    std::string what;
+    try {
+        Value root = (x * s) * (s * s);  // s: fp32 from the first product, bf16 from s * s
+        backward(root);
+    } catch (const std::runtime_error& e) {
+        threw = true;
+        what = e.what();
+    }
+    report("bf16 node with fp32 and bf16 gradient contributions: backward throws", threw &&
+           (what.find("gradient") != std::string::npos), what);
+    // the same graph in fp32 has one gradient dtype throughout and runs
+    Value xf = leaf(normal(B * T * D, 95), {B, T, D}, "xf");
+    Value sf = leaf(normal(B * D, 96), {B, 1, D}, "sf");
+    bool ran = true;
+    try {
+        backward((xf * sf) * (sf * sf));
+    } catch (const std::runtime_error& e) {
+        ran = false;
+        what = e.what();
+    }
+    report("the same graph in fp32 runs", ran && sf.grad().dtype() == Dtype::Float32, what);
+}
+
+// Scalar literals (Value(float), as cgadimpl/include/ad/core/graph.hpp:22 and
+// cgadimpl/src/core/graph.cpp:91-105): `rms(x) * s` and `s * rms(x)` compile,
+// give rms(x) scaled by s, and differentiate to the rms VJP of s * dy.  The
+// reference products are taken on the host in the same IEEE arithmetic, so
+// the comparisons are bitwise.
+void test_scalar_literal() {
+    const int64_t R = 37, D = 1030;
+    const std::vector<float> xv = normal(R * D, 97), dyv = normal(R * D, 98);
+    Tensor dy = Tensor::from_host_f32(dyv, {R, D});
+    for (const float sc : {0.75f, -1.5f}) {
+        Value xa = leaf(xv, {R, D}, "xa");
+        Value ya = rms(xa) * sc;  // float converts to a scalar literal
+        backward(ya, &dy);
+        Value xb = leaf(xv, {R, D}, "xb");
+        Value yb = sc * rms(xb);  // the literal first
+        backward(yb, &dy);
+        Value xr = leaf(xv, {R, D}, "xr");
+        Value yr = rms(xr);
+        std::vector<float> dys = dyv;
+        for (float& v : dys) v *= sc;
+        Tensor dy_scaled = Tensor::from_host_f32(dys, {R, D});
+        backward(yr, &dy_scaled);
+        std::vector<float> want_y = yr.val().to_host_f32();
+        for (float& v : want_y) v *= sc;
+        const std::vector<float> want_dx = xr.grad().to_host_f32();
+        const std::string tag = " (s = " + std::to_string(sc) + ")";
+        report(("rms(x) * s == s * rms(x) == rms(x) scaled, dx == rms VJP of s * dy" + tag).c_str(),
+               ya.val().to_host_f32() == want_y && yb.val().to_host_f32() == want_y &&
+                   xa.grad().to_host_f32() == want_dx && xb.grad().to_host_f32() == want_dx);
+    }
+    // a literal is a [1] fp32 leaf that takes no gradient
+    Value lit(0.5f);
+    report("Value(float) is a [1] float32 leaf named scalar_literal, no gradient",
+           lit.shape() == std::vector<int64_t>{1} && lit.val().dtype() == Dtype::Float32 &&
+               !lit.node->requires_grad() && std::string(lit.node->debug_name) == "scalar_literal" &&
+               lit.val().to_host_f32() == std::vector<float>{0.5f});
+    // bf16: the literal is taken in bf16 (0.75 is exact), the product rounded
+    Value xh = bf16_leaf(xv, {R, D}, "xh");
+    Value yh = rms(xh) * 0.75f;
+    Value xh2 = bf16_leaf(xv, {R, D}, "xh2");
+    std::vector<float> want = rms(xh2).val().to_host_f32();
+    for (float& v : want) v = bf16_round(v * 0.75f);
+    report("bf16 rms(x) * 0.75f: the literal in bf16, the product rounded",
+           yh.val().dtype() == Dtype::BFloat16 && yh.val().to_host_f32() == want &&
+               lit.val().dtype() == Dtype::Float32);
 }
 
 std::vector<float> rounded(const std::vector<float>& v) {
@@ -1238,6 +1318,38 @@ void test_block_cache() {
     set_cache_limit(kDefaultCacheLimit);
     release_cached_memory();
     report("block cache: release_stream_cache drops that stream's blocks only", held && dropped);
+
+    // blocks of a stream destroyed without release_stream_cache: evicting them
+    // (by lowering the cap, then by a free past it) names no dead stream
+    bool evicted_ok = true;
+    std::string why;
+    try {
+        for (int round = 0; round < 2; ++round) {
+            hipStream_t s3 = nullptr;
+            (void)hipStreamCreateWithFlags(&s3, hipStreamNonBlocking);
+            {
+                StreamGuard guard(s3);
+                Tensor a = Tensor::empty({512, 1024});
+                Tensor b = Tensor::empty({300, 1024});
+            }
+            (void)hipStreamSynchronize(s3);
+            (void)hipStreamDestroy(s3);
+            if (round == 0) {
+                set_cache_limit(0);
+            } else {
+                set_cache_limit(size_t(1) << 20);
+                { Tensor big = Tensor::empty({1024, 1024}); }  // 4 MiB freed past the cap
+            }
+            evicted_ok = evicted_ok && cached_bytes() <= cache_limit();
+        }
+    } catch (const std::exception& e) {
+        evicted_ok = false;
+        why = e.what();
+    }
+    set_cache_limit(kDefaultCacheLimit);
+    release_cached_memory();
+    report("block cache: blocks of a destroyed stream are evicted without error",
+           evicted_ok && cached_bytes() == 0, why);
 }
 
 // Runs the named checks (all of them when `only` is empty).
@@ -1338,6 +1450,8 @@ int selftest(const std::vector<std::string>& only) {
         {"matmul_f32", test_matmul_f32},
         {"empty_batch", test_empty_batch},
         {"bf16_layer", test_bf16_layer},
+        {"bf16_mixed_gradient_dtypes", test_bf16_mixed_gradient_dtypes},
+        {"scalar_literal", test_scalar_literal},
         {"seed_not_modified", test_seed_not_modified},
         {"user_stream", test_user_stream},
         {"row_ops_gradients", test_row_ops_gradients},
@@ -1414,6 +1528,16 @@ int dump(const std::string& dir) {
         write_tensor(dir + "/y_unfused.bin", y.val());
         write_tensor(dir + "/dx_unfused.bin", x.grad());
         write_tensor(dir + "/dg_unfused.bin", g.grad());
+    }
+    // scalar literals on both sides: rms(x) * 0.75f and -1.5f * rms(x)
+    const std::pair<const char*, float> scaled_runs[] = {{"scaled_r", 0.75f},
+                                                         {"scaled_l", -1.5f}};
+    for (auto& [tag, sc] : scaled_runs) {
+        Value x = make_tensor(make(xb, {rows, cols}, true), "x");
+        Value y = std::string(tag) == "scaled_r" ? rms(x) * sc : sc * rms(x);
+        backward(y, &dy);
+        write_tensor(dir + "/y_" + tag + ".bin", y.val());
+        write_tensor(dir + "/dx_" + tag + ".bin", x.grad());
     }
     std::printf("dumped %lld x %lld %s\n", static_cast<long long>(rows),
                 static_cast<long long>(cols), dtype_name(dtype));

@@ -109,6 +109,20 @@ def test_graph_layer_against_oracle(cuda, name, shape):
             print(f"  [{tag}] " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
             for k, v in errs.items():
                 assert v <= (TOL_F32 if k == "inv_rms" else t), (tag, k, v)
+        # scalar literals: rms(x) * 0.75f and -1.5f * rms(x) (eps 1e-5, as ag::rms)
+        # against the oracle's rms scaled by s, and its VJP of s * dy
+        ones = np.ones(cols, dtype=np.float32)
+        for tag, sc in (("scaled_r", 0.75), ("scaled_l", -1.5)):
+            xs32 = as_f32(xs)
+            ry, rinv = oracle.fwd(xs32, None, 1e-5)
+            rdx, _ = oracle.bwd(xs32, None, rinv, as_f32(dys) * np.float32(sc))
+            y, dx = load("y_" + tag), load("dx_" + tag)
+            errs = {"y": row_rel_err(as_f32(y), as_f32(ry) * np.float32(sc)),
+                    "dx": dx_rel_err(as_f32(dx), as_f32(rdx), xs32, ones,
+                                     as_f32(dys) * np.float32(sc), 1e-5)}
+            print(f"  [{tag}] " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+            for k, v in errs.items():
+                assert v <= tol, (tag, k, v)
         # parallel backward of a single node gives the same bits as sequential
         assert np.array_equal(load("dx_fused"), load("dx_fused_par"))
         assert np.array_equal(load("dg_fused", np.float32, (cols,)),

@@ -363,6 +363,40 @@ def test_masked_entries(cuda, dtype, cols):
     assert float((y.double().sum(-1) - 1).abs().max()) <= 2 * _tol(dtype == "bf16")
 
 
+# a resident width, a bf16 width of the 16-slot resident shape (32769-65536),
+# GPT-2's unaligned vocabulary (head/body/tail looped kernel, online max and
+# sum) and an aligned looped width
+@pytest.mark.parametrize("dtype,cols", [("f32", 96), ("bf16", 40000), ("bf16", 50257),
+                                        ("f32", 50257), ("bf16", 262144)])
+def test_fully_masked_rows_are_nan(cuda, dtype, cols):
+    """A row that is -inf throughout: the reference's two-pass rule
+    (reduction.cpp:42-66) computes exp(-inf - -inf) = NaN, and so does the
+    oracle; every kernel path gives NaN for softmax and log-sum-exp there, and
+    the other rows stay finite and match the oracle."""
+    import warnings
+    import torch
+    z = torch.randn(4, cols, device=cuda) * 3
+    z[1] = float("-inf")
+    z = z.to(torch.bfloat16 if dtype == "bf16" else torch.float32).contiguous()
+    y = agk.softmax_fwd(z)
+    lse = agk.logsumexp_fwd(z)
+    torch.cuda.synchronize()
+    zh = as_f32(to_host(z))
+    with warnings.catch_warnings(), np.errstate(invalid="ignore"):
+        warnings.simplefilter("ignore", RuntimeWarning)
+        ry = ro.softmax_fwd(zh)
+        rl = ro.logsumexp_fwd(zh)
+    assert np.all(np.isnan(ry[1])) and np.isnan(rl[1]).all()  # the oracle's own rule
+    yh, lh = as_f32(to_host(y)), as_f32(to_host(lse)).reshape(4, 1)
+    assert np.all(np.isnan(yh[1])), "softmax of a fully masked row"
+    assert np.isnan(lh[1]).all(), "log-sum-exp of a fully masked row"
+    keep = [0, 2, 3]
+    assert np.all(np.isfinite(yh[keep])) and np.all(np.isfinite(lh[keep]))
+    tol = _tol(dtype == "bf16")
+    assert _row_rel(yh[keep], ry[keep]) <= tol
+    assert np.abs(lh[keep] - rl[keep]).max() <= tol * np.abs(rl[keep]).max()
+
+
 @pytest.mark.parametrize("shape", [(4099, 1000), (7, 131072)], ids=str)
 def test_results_are_deterministic(cuda, shape):
     import torch

@@ -71,6 +71,36 @@ def test_noalloc_matches_workspace_backward_across_calls(cuda):
         assert np.array_equal(rdg.view(np.uint8), ndg.view(np.uint8)), f"dgamma differs, call {i}"
 
 
+# dx only (dgamma NULL) on wide rows: the split path with only the row
+# statistics in the scratch array, as agk_rmsnorm_bwd takes it with a workspace;
+# then a resident width, which needs no scratch at all.
+DX_ONLY_CALLS = [
+    (300, 65536, "f32", 0),
+    (1, 131072, "bf16", agk.AGK_ACCUM_DX),
+    (512, 4096, "f32", 0),
+]
+
+
+def test_noalloc_dx_only_matches_workspace_backward(cuda):
+    import torch
+    for i, (rows, cols, dtype, acc) in enumerate(DX_ONLY_CALLS):
+        print(f"noalloc dx-only call {i}: {rows}x{cols} {dtype} accumulate={acc}", flush=True)
+        x, g, dy = device_inputs((rows, cols), dtype, 300 + i, cuda)
+        _, inv = agk.rmsnorm_fwd(x, g, 1e-6)
+        stream = torch.cuda.current_stream()
+        gen = torch.Generator(device=cuda)
+        gen.manual_seed(400 + i)
+        dx0 = torch.randn((rows, cols), generator=gen, device=cuda).to(x.dtype)
+        ref = dx0.clone()
+        agk.rmsnorm_bwd(x, g, inv, dy, dx=ref, want_dgamma=False, accumulate=acc, stream=stream)
+        got = dx0.clone()
+        rc = _noalloc(x, g, inv, dy, got, None, acc, stream)
+        assert rc == 0, agk.STATUS.get(rc, rc)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(ref).view(np.uint8), to_host(got).view(np.uint8)), \
+            f"dx differs, dx-only call {i}"
+
+
 def test_noalloc_rejects_partials_beyond_the_scratch_array(cuda):
     import torch
     rows, cols = 300, 40001  # looped kernel: 300 row blocks x 40001 fp32 partials = 48 MB
