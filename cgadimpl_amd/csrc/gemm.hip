@@ -45,6 +45,8 @@
 
 #include <stdint.h>
 
+#include <atomic>
+
 #include "agk_rmsnorm.h"
 
 namespace agk_gemm {
@@ -391,15 +393,17 @@ __device__ __forceinline__ void store_c_impl(const f32x16 (&acc)[TM][TN], void* 
     }
 }
 
+// bn: the columns the calling tile covers from n0 (BN, or BN / 2 for a half tile).
 template <bool OUT_F32>
 __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __restrict__ C,
                                         int64_t ldc, int M, int N, int m0, int n0, int wm, int wn,
                                         int lane, const float* __restrict__ rowscale,
-                                        const uint16_t* __restrict__ colbias, int accumulate) {
+                                        const uint16_t* __restrict__ colbias, int accumulate,
+                                        int bn = BN) {
     if (rowscale != nullptr || colbias != nullptr || accumulate) {
         store_c_impl<OUT_F32, true, true>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, rowscale,
                                           colbias, accumulate);
-    } else if (m0 + BM <= M && n0 + BN <= N) {
+    } else if (m0 + BM <= M && n0 + bn <= N) {
         store_c_impl<OUT_F32, false, false>(acc, C, ldc, M, N, m0, n0, wm, wn, lane, nullptr,
                                             nullptr, 0);
     } else {
@@ -501,9 +505,11 @@ __device__ __forceinline__ void direct_offsets(uint32_t (&o)[8], int wave, int l
 }
 
 // The fragments of one 16-deep substep s (0..3) of a wave: 4 of A (128 rows),
-// 4 of B (128 columns).
+// NB of B (32 NB columns: 4 for the 256 x 256 tile, 2 for the 256 x 128 half
+// tiles of a last round).
+template <int NB>
 struct Frags {
-    bf16x8 a[TM], b[TN4];
+    bf16x8 a[TM], b[NB];
 };
 
 // MFMA operand lane l (row or column l % 32, k 8 (l / 32) .. + 7) of block
@@ -519,26 +525,28 @@ __device__ __forceinline__ bf16x8 tr_frag(const uint16_t* lds, int c0, int s, in
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-template <bool A_TR, bool B_TR>
-__device__ __forceinline__ void read_frags(Frags& f, const uint16_t* stage, int s, int wm, int wn,
-                                           int frow, int fk, int lane) {
+// bc: the wave's first B column within the stage.
+template <bool A_TR, bool B_TR, int NB>
+__device__ __forceinline__ void read_frags(Frags<NB>& f, const uint16_t* stage, int s, int wm,
+                                           int bc, int frow, int fk, int lane) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         if constexpr (A_TR) f.a[i] = tr_frag(stage, wm * WM + i * 32, s, lane);
         else f.a[i] = lds_frag(stage, wm * WM + i * 32 + frow, s * 16 + fk);
     }
 #pragma unroll
-    for (int j = 0; j < TN4; ++j) {
-        if constexpr (B_TR) f.b[j] = tr_frag(stage + BM * BK, wn * WN4 + j * 32, s, lane);
-        else f.b[j] = lds_frag(stage + BM * kStride, wn * WN4 + j * 32 + frow, s * 16 + fk);
+    for (int j = 0; j < NB; ++j) {
+        if constexpr (B_TR) f.b[j] = tr_frag(stage + BM * BK, bc + j * 32, s, lane);
+        else f.b[j] = lds_frag(stage + BM * kStride, bc + j * 32 + frow, s * 16 + fk);
     }
 }
 
-__device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN4]) {
+template <int NB>
+__device__ __forceinline__ void mfma_sub(const Frags<NB>& f, f32x16 (&acc)[TM][NB]) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN4; ++j)
+        for (int j = 0; j < NB; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
@@ -555,32 +563,44 @@ __device__ __forceinline__ void mfma_sub(const Frags& f, f32x16 (&acc)[TM][TN4])
 
 // Tile t of nk.  FIRST (tile 0) has no straddling substep; every step loads
 // tile t + 1 (the last tile again at the end, into the stage nothing reads
-// again).  Entering, f1 holds substep 3 of tile t - 1.
-template <bool FIRST, bool A_TR, bool B_TR>
+// again).  Entering, f1 holds substep 3 of tile t - 1.  NB = 4: the 256 x 256
+// tile, whose substeps interleave one load, one fragment read and two MFMAs;
+// NB = 2 (half tiles): the same loads and reads around half the MFMAs, left to
+// the compiler's schedule.
+#define AGK_SUBSTEP_LRM    \
+    if constexpr (NB == 4) { \
+        AGK_X8(AGK_LRM)    \
+    }
+#define AGK_SUBSTEP_RM     \
+    if constexpr (NB == 4) { \
+        AGK_X8(AGK_RM)     \
+    }
+template <bool FIRST, bool A_TR, bool B_TR, int NB>
 __device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t* cur,
                                             uint16_t* other, int t, int nk,
-                                            f32x16 (&acc)[TM][TN4], Frags& f0, Frags& f1, int wm,
-                                            int wn, int frow, int fk, int lane, int wave) {
+                                            f32x16 (&acc)[TM][NB], Frags<NB>& f0, Frags<NB>& f1,
+                                            int wm, int bc, int frow, int fk, int lane,
+                                            int wave) {
     const int tn = t + 1 < nk ? t + 1 : nk - 1;
     direct_issue_a(d, other, tn, wave);
-    read_frags<A_TR, B_TR>(f0, cur, 0, wm, wn, frow, fk, lane);
+    read_frags<A_TR, B_TR>(f0, cur, 0, wm, bc, frow, fk, lane);
     if constexpr (!FIRST) {
         mfma_sub(f1, acc);
-        AGK_X8(AGK_LRM)
+        AGK_SUBSTEP_LRM
     }
     __builtin_amdgcn_sched_barrier(0);
     direct_issue_b(d, other, tn, wave);
-    read_frags<A_TR, B_TR>(f1, cur, 1, wm, wn, frow, fk, lane);
+    read_frags<A_TR, B_TR>(f1, cur, 1, wm, bc, frow, fk, lane);
     mfma_sub(f0, acc);
-    AGK_X8(AGK_LRM)
+    AGK_SUBSTEP_LRM
     __builtin_amdgcn_sched_barrier(0);
-    read_frags<A_TR, B_TR>(f0, cur, 2, wm, wn, frow, fk, lane);
+    read_frags<A_TR, B_TR>(f0, cur, 2, wm, bc, frow, fk, lane);
     mfma_sub(f1, acc);
-    AGK_X8(AGK_RM)
+    AGK_SUBSTEP_RM
     __builtin_amdgcn_sched_barrier(0);
-    read_frags<A_TR, B_TR>(f1, cur, 3, wm, wn, frow, fk, lane);
+    read_frags<A_TR, B_TR>(f1, cur, 3, wm, bc, frow, fk, lane);
     mfma_sub(f0, acc);
-    AGK_X8(AGK_RM)
+    AGK_SUBSTEP_RM
     __builtin_amdgcn_sched_barrier(0);
     // This wave's loads of tile t + 1 have landed and its reads of tile t are
     // done; after the barrier every wave's are.  A bare barrier:
@@ -591,13 +611,80 @@ __device__ __forceinline__ void direct_step(const DirectStage& d, const uint16_t
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// One tile's k loop and store.  NB = 4: the 256 x 256 tile at (m0, n0), wave
+// (wm, wn) owning its 128 x 128 block; NB = 2: the 256 x 128 half of that tile
+// starting at column n0 + half_off, wave (wm, wn) owning a 128 x 64 block.
+// Both stage the tile's full 256 B columns (the same loads).
+template <bool OUT_F32, bool A_TR, bool B_TR, int NB>
+__device__ __forceinline__ void direct_tile(const DirectStage& d, uint16_t* st0, uint16_t* st1,
+                                            void* __restrict__ C, int64_t ldc, int M, int N,
+                                            int K, int m0, int n0, int half_off, int wm, int wn,
+                                            int lane, int wave,
+                                            const float* __restrict__ rowscale,
+                                            const uint16_t* __restrict__ colbias,
+                                            int accumulate) {
+    f32x16 acc[TM][NB];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int nk = K / BK;  // >= 1: K is a positive multiple of 64
+    const int frow = lane & 31;
+    const int fk = (lane >> 5) * 8;  // MFMA operand lanes 32..63 hold k 8..15
+    const int bc = half_off + wn * (NB * 32);  // the wave's first B column in the stage
+    direct_issue_a(d, st0, 0, wave);
+    direct_issue_b(d, st0, 0, wave);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    Frags<NB> f0, f1;
+    direct_step<true, A_TR, B_TR>(d, st0, st1, 0, nk, acc, f0, f1, wm, bc, frow, fk, lane, wave);
+    int t = 1;
+    for (; t + 1 < nk; t += 2) {
+        direct_step<false, A_TR, B_TR>(d, st1, st0, t, nk, acc, f0, f1, wm, bc, frow, fk, lane,
+                                       wave);
+        direct_step<false, A_TR, B_TR>(d, st0, st1, t + 1, nk, acc, f0, f1, wm, bc, frow, fk,
+                                       lane, wave);
+    }
+    if (t < nk)
+        direct_step<false, A_TR, B_TR>(d, st1, st0, t, nk, acc, f0, f1, wm, bc, frow, fk, lane,
+                                       wave);
+    mfma_sub(f1, acc);  // substep 3 of the last tile
+
+    if constexpr (NB == 4) {
+        // the wave's 128 x 128 block leaves as two 128 x 64 halves (store_c's layout)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x16 part[TM][TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) part[i][j] = acc[i][h * TN + j];
+            store_c<OUT_F32>(part, C, ldc, M, N, m0, n0, wm, 2 * wn + h, lane, rowscale, colbias,
+                             accumulate);
+        }
+    } else {
+        store_c<OUT_F32>(acc, C, ldc, M, N, m0, n0 + half_off, wm, wn, lane, rowscale, colbias,
+                         accumulate, BN / 2);
+    }
+}
+
 // A_TR: A stored [K][lda] (its m contiguous); B_TR: B stored [K][ldb] (its n
 // contiguous).  Otherwise the operand is [rows][ld] with k contiguous.
+// Workgroups below full_tiles compute whole 256 x 256 tiles (tile_of's order);
+// the ones after them split each remaining tile into two 256 x 128 halves
+// (workgroup full_tiles + 2 h + q: half q of tile full_tiles + h), so that a
+// last round of few tiles runs on twice as many CUs for half as long.  Every
+// output element is summed in the same k order either way (bit-identical).
 template <bool OUT_F32, bool A_TR, bool B_TR>
 __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B, int64_t ldb,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, const float* __restrict__ rowscale,
-    const uint16_t* __restrict__ colbias, int accumulate, int tiles_m, int tiles_n, int group_m) {
+    const uint16_t* __restrict__ colbias, int accumulate, int tiles_m, int tiles_n, int group_m,
+    int full_tiles) {
     __shared__ __attribute__((aligned(16))) uint16_t st0[kStageElems];
     __shared__ __attribute__((aligned(16))) uint16_t st1[kStageElems];
 
@@ -607,8 +694,11 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1;
     const int wn = wave & 1;
+    const int L = static_cast<int>(blockIdx.x);
+    const bool halves = L >= full_tiles;
+    const int tile = halves ? full_tiles + ((L - full_tiles) >> 1) : L;
     int tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
+    tile_of(tile, tiles_m, tiles_n, group_m, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
 
@@ -632,47 +722,13 @@ __global__ __launch_bounds__(kDirectThreads) void gemm_nt_direct_kernel(
     direct_offsets<A_TR>(d.oa, wave, lane, rows_a, lda);
     direct_offsets<B_TR>(d.ob, wave, lane, rows_b, ldb);
 
-    f32x16 acc[TM][TN4];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN4; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-    const int nk = K / BK;  // >= 1: K is a positive multiple of 64
-    const int frow = lane & 31;
-    const int fk = (lane >> 5) * 8;  // MFMA operand lanes 32..63 hold k 8..15
-    direct_issue_a(d, st0, 0, wave);
-    direct_issue_b(d, st0, 0, wave);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    Frags f0, f1;
-    direct_step<true, A_TR, B_TR>(d, st0, st1, 0, nk, acc, f0, f1, wm, wn, frow, fk, lane, wave);
-    int t = 1;
-    for (; t + 1 < nk; t += 2) {
-        direct_step<false, A_TR, B_TR>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, lane,
-                                       wave);
-        direct_step<false, A_TR, B_TR>(d, st0, st1, t + 1, nk, acc, f0, f1, wm, wn, frow, fk,
-                                       lane, wave);
-    }
-    if (t < nk)
-        direct_step<false, A_TR, B_TR>(d, st1, st0, t, nk, acc, f0, f1, wm, wn, frow, fk, lane,
-                                       wave);
-    mfma_sub(f1, acc);  // substep 3 of the last tile
-
-    // the wave's 128 x 128 block leaves as two 128 x 64 halves (store_c's layout)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        f32x16 half[TM][TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) half[i][j] = acc[i][h * TN + j];
-        store_c<OUT_F32>(half, C, ldc, M, N, m0, n0, wm, 2 * wn + h, lane, rowscale, colbias,
-                         accumulate);
-    }
+    if (!halves)
+        direct_tile<OUT_F32, A_TR, B_TR, 4>(d, st0, st1, C, ldc, M, N, K, m0, n0, 0, wm, wn, lane,
+                                            wave, rowscale, colbias, accumulate);
+    else
+        direct_tile<OUT_F32, A_TR, B_TR, 2>(d, st0, st1, C, ldc, M, N, K, m0, n0,
+                                            ((L - full_tiles) & 1) * (BN / 2), wm, wn, lane,
+                                            wave, rowscale, colbias, accumulate);
 }
 
 // C for an empty reduction (K == 0): zeros, or the bf16 column bias in every
@@ -751,6 +807,30 @@ inline int launch_transpose(const void* src, int64_t ld_src, void* dst, int64_t 
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Compute units of the current device (looked up once per device; 256 on
+// MI355X), for the direct kernel's last-round split.
+inline int device_cus() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cached[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+        v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
+
+// How many tiles the direct kernel computes whole: all of them, unless the
+// last round (tiles beyond a multiple of the CU count) would fill at most half
+// of the CUs; those tiles then run as two 256 x 128 halves each.
+inline int direct_full_tiles(int tiles, int cus) {
+    const int rem = tiles % cus;
+    return (rem != 0 && 2 * rem <= cus) ? tiles - rem : tiles;
+}
 
 template <bool AK, bool BK_, bool KS, bool F32>
 int launch(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int M,
@@ -900,12 +980,14 @@ int gemm_impl(const void* A, int64_t lda, int a_trans, const void* B, int64_t ld
     if (direct_eligible(K, kscale) && fits(lda, a_tr) && fits(ldb, b_tr)) {
         const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
         const int gm = tuned_group_m(tiles_m, tiles_n, k / BK, a_tr, b_tr);
-        const dim3 grid(tiles_m * tiles_n), block(kDirectThreads);
+        const int tiles = tiles_m * tiles_n;
+        const int full = direct_full_tiles(tiles, device_cus());
+        const dim3 grid(full + 2 * (tiles - full)), block(kDirectThreads);
         const uint16_t* a16 = static_cast<const uint16_t*>(A);
         const uint16_t* b16 = static_cast<const uint16_t*>(B);
 #define AGK_DIRECT(F32, ATR, BTR)                                                              \
     hipLaunchKernelGGL((gemm_nt_direct_kernel<F32, ATR, BTR>), grid, block, 0, st, a16, lda, b16, \
-                       ldb, C, ldc, m, n, k, rowscale, colbias, acc, tiles_m, tiles_n, gm)
+                       ldb, C, ldc, m, n, k, rowscale, colbias, acc, tiles_m, tiles_n, gm, full)
         const bool f32 = c_dtype == AGK_F32;
         if (f32) {
             if (a_tr && b_tr) AGK_DIRECT(true, true, true);

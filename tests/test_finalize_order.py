@@ -1,7 +1,8 @@
 """dgamma's fixed summation order, checked bit for bit from the partial rows.
 
 After a backward call the caller's workspace still holds the fp32 partial
-rows the finalize summed, so the host can redo the finalize in float64 in the
+rows the finalize summed (at its start, or after the split path's row
+statistics), so the host can redo the finalize in float64 in the
 documented order and compare every bit of dgamma:
   more than 64 partial rows: split s (of 64) adds rows s, s+64, s+128, ... in
   increasing order from +0.0, then the split sums are added in split order;
@@ -20,6 +21,10 @@ from gpu_util import device_inputs
 pytestmark = pytest.mark.gpu
 
 SPLITS = 64
+
+
+def _r256(b):
+    return (b + 255) // 256 * 256
 
 
 def _finalize_f64(parts):
@@ -68,7 +73,12 @@ def test_dgamma_is_the_documented_sum_of_the_partial_rows(cuda, dtype, rows, col
     # torch's allocations are; unaligned columns are what make them looped
     agk.rmsnorm_bwd(x, g, inv, dy, dgamma=dg, workspace=ws, accumulate=accumulate)
     torch.cuda.synchronize()
-    parts = ws[: nblk * cols * 4].view(torch.float32).view(nblk, cols).cpu().numpy()
+    # the split path keeps its row statistics (segment sums, then the
+    # coefficients, each 256-byte aligned) ahead of the partial rows
+    off = 0
+    if plan["tpr"] == 0 and plan["nv"] > 0:
+        off = _r256(rows * plan["nv"] * 4) + _r256(rows * 4)
+    parts = ws[off: off + nblk * cols * 4].view(torch.float32).view(nblk, cols).cpu().numpy()
     tot = _finalize_f64(parts).astype(np.float32)
     want = (pre.cpu().numpy() + tot).astype(np.float32) if accumulate else tot
     got = dg.cpu().numpy()
