@@ -53,7 +53,14 @@ namespace agk {
 //
 // MUL: the broadcast multiply y = x * gamma on the same launch shape (the
 // unfused layer's Mul): no row sum, no inv_rms.
-template <class S, int TPR, int NV, int G, bool MUL = false>
+// EARLY_G: gamma's slots are loaded with x's, before the row sum, so that
+// their latency overlaps it: for grids of at most one workgroup per CU with
+// short rows (at most 1024 16-byte slots), where the call is latency-bound.
+// Measured (graph replays, one box): [512, 512] fp32 2.57-2.61 -> 2.36-2.38 us;
+// but [51, 13824] fp32 4.19-4.21 -> 4.38-4.39 us (a long row's gamma loads
+// compete with its x loads before the sum) and many rows lose ~3 % (live
+// registers).  Same arithmetic either way.
+template <class S, int TPR, int NV, int G, bool MUL = false, bool EARLY_G = false>
 __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
     typename S::T* __restrict__ y, float* __restrict__ inv_rms, int64_t rows, int cols,
@@ -75,6 +82,17 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
     for (int k = 0; k < NV; ++k) {
         const int col = (t + k * TPR) * W;
         xv[k] = (active && col < cols) ? load16_stream<S>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+    [[maybe_unused]] u32x4 gv[EARLY_G ? NV : 1];
+    if constexpr (EARLY_G) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = (t + k * TPR) * W;
+            gv[k] = (active && col < cols) ? load16<S>(gamma + col) : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
         float f[W];
         S::unpack(xv[k], f);
 #pragma unroll
@@ -107,6 +125,11 @@ __global__ __launch_bounds__(TPR * G) void rms_fwd_resident(
                 S::unpack(load16<S>(gamma + col), gm);
 #pragma unroll
                 for (int e = 0; e < W; ++e) f[e] = f[e] * gm[e];
+            } else if (EARLY_G) {
+                float gm[W];
+                S::unpack(gv[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) f[e] = (f[e] * r) * gm[e];
             } else if (gamma) {
                 float gm[W];
                 S::unpack(load16<S>(gamma + col), gm);
@@ -1099,6 +1122,11 @@ inline int64_t bwd_num_blocks(int64_t rows) {
 
 #include "rmsnorm_wide.hpp"
 
+// Forward grids of at most this many workgroups (one per CU), over rows of at
+// most kFwdEarlyGammaSlots 16-byte slots per row shape, load gamma with x.
+constexpr int64_t kFwdEarlyGammaGrid = 256;
+constexpr int64_t kFwdEarlyGammaSlots = 1024;
+
 template <class S>
 int launch_fwd_plan(const Plan& p, const void* x, const void* gamma, void* y, float* inv_rms,
                     int64_t rows, int cols, float eps, hipStream_t st) {
@@ -1114,10 +1142,18 @@ int launch_fwd_plan(const Plan& p, const void* x, const void* gamma, void* y, fl
     }
     const int64_t grid = (rows + p.g - 1) / p.g;
     if (grid > 0x7fffffffLL) return AGK_EINVAL;
+    // one generation of workgroups over short rows, with gamma: gamma loaded beside x
+    const bool early_g = gp != nullptr && grid <= kFwdEarlyGammaGrid &&
+                         static_cast<int64_t>(p.tpr) * p.nv <= kFwdEarlyGammaSlots;
 #define AGK_X(a, b, c)                                                                       \
     if (p.tpr == a && p.nv == b && p.g == c) {                                               \
-        hipLaunchKernelGGL((rms_fwd_resident<S, a, b, c>), dim3(static_cast<unsigned>(grid)), \
-                           dim3(a * c), 0, st, xp, gp, yp, inv_rms, rows, cols, eps);        \
+        if (early_g)                                                                          \
+            hipLaunchKernelGGL((rms_fwd_resident<S, a, b, c, false, true>),                  \
+                               dim3(static_cast<unsigned>(grid)), dim3(a * c), 0, st, xp, gp, \
+                               yp, inv_rms, rows, cols, eps);                                \
+        else                                                                                  \
+            hipLaunchKernelGGL((rms_fwd_resident<S, a, b, c>), dim3(static_cast<unsigned>(grid)), \
+                               dim3(a * c), 0, st, xp, gp, yp, inv_rms, rows, cols, eps);    \
         return check_launch();                                                               \
     }
     AGK_FWD_SHAPES(AGK_X)
