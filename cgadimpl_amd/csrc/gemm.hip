@@ -378,8 +378,18 @@ __device__ __forceinline__ void store_c_impl(const f32x16 (&acc)[TM][TN], void* 
                 }
                 if constexpr (OUT_F32) {
                     float* p = static_cast<float*>(C) + static_cast<int64_t>(row) * ldc + col;
-                    if constexpr (GENERAL) v = accumulate ? *p + v : v;
-                    *p = v;
+                    if constexpr (GENERAL) {
+                        *p = accumulate ? *p + v : v;
+                    } else {
+                        // Plain fp32 stores are whole 128-byte lines per 32 lanes:
+                        // non-temporal, so a round's C tiles (64 MB) do not evict
+                        // the operand panels from L2 and stream out as they come.
+                        // Measured on dW at c5 (4096 x 11008 x 8192, one box, three
+                        // alternations): 557-561 -> 528-529 us.  bf16 outputs keep
+                        // ordinary stores: no gain there, and the RMSNorm backward
+                        // reads dh from the caches right after its product.
+                        __builtin_nontemporal_store(v, p);
+                    }
                 } else {
                     uint16_t* p = static_cast<uint16_t*>(C) + static_cast<int64_t>(row) * ldc + col;
                     if constexpr (GENERAL) {
