@@ -1162,6 +1162,10 @@ def run_wide_rowops(steps):
                 "logsumexp_bwd": (graph_replay_ms(
                     lambda i, st: agk.logsumexp_bwd(z, dl, dz=dz, stream=st), n), 2),
             }
+            # the backward from the forward's fp32 value (one streaming pass)
+            l32 = agk.logsumexp_fwd_keep(z)[1]
+            t["logsumexp_bwd_from_value"] = (graph_replay_ms(
+                lambda i, st: agk.logsumexp_bwd_from_value(z, l32, dl, dz=dz, stream=st), n), 2)
             if tag != "scalar":  # no row output: no element-wise layout
                 t["logsumexp_fwd"] = (graph_replay_ms(
                     lambda i, st: agk.logsumexp_fwd(z, y=lse, stream=st), n), 1)

@@ -17,7 +17,7 @@ __all__ = [
     "mul_rowbcast_fwd", "mul_rowbcast_bwd", "launch_plan", "gemm_bf16", "gemm_bf16_workspace_bytes",
     "transpose_bf16", "rmsnorm_linear_fwd", "rmsnorm_linear_bwd", "rmsnorm_jvp", "layernorm_fwd",
     "layernorm_bwd", "softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
-    "logsumexp_jvp", "rms_mul_bwd", "sum_rows", "linear_bf16",
+    "logsumexp_jvp", "logsumexp_fwd_keep", "logsumexp_bwd_from_value", "rms_mul_bwd", "sum_rows", "linear_bf16",
     "mul_bcast_shape", "mul_bcast_fwd", "mul_bcast_bwd",
     "mul_bcast_grad_dtype", "gemm_f32", "AGK_F32", "AGK_BF16", "STATUS",
 ]
@@ -80,6 +80,9 @@ SIGNATURES = {
     "agk_logsumexp_fwd": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_logsumexp_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_logsumexp_jvp": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_logsumexp_fwd_keep": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
+    "agk_logsumexp_bwd_from_value": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_int,
+                                                    ctypes.c_int, _P]),
     "agk_fill": (ctypes.c_int, [_P, _I64, ctypes.c_float, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
@@ -593,6 +596,31 @@ def logsumexp_bwd(z, dy, dz=None, accumulate: bool = False, stream=None):
     rc = lib().agk_logsumexp_bwd(_ptr(z), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(z),
                                  _acc_dx(accumulate), _stream(stream))
     _check(rc, "agk_logsumexp_bwd")
+    return dz
+
+
+def logsumexp_fwd_keep(z, y=None, lse=None, stream=None):
+    """logsumexp_fwd that also returns lse, the same values in float32, for
+    logsumexp_bwd_from_value; returns (y, lse)."""
+    torch = _torch()
+    rows, cols = _rows_cols(z)
+    y = _row_stat_like(z, z.dtype) if y is None else y
+    lse = _row_stat_like(z, torch.float32) if lse is None else lse
+    rc = lib().agk_logsumexp_fwd_keep(_ptr(z), _ptr(y), _ptr(lse), rows, cols, _dtype_code(z),
+                                      _stream(stream))
+    _check(rc, "agk_logsumexp_fwd_keep")
+    return y, lse
+
+
+def logsumexp_bwd_from_value(z, lse, dy, dz=None, accumulate: bool = False, stream=None):
+    """dz (+)= dy * exp(z - lse), lse the forward's float32 value (one pass over z)."""
+    torch = _torch()
+    rows, cols = _rows_cols(z)
+    dz = (torch.zeros_like(z) if accumulate else torch.empty_like(z)) if dz is None else dz
+    rc = lib().agk_logsumexp_bwd_from_value(_ptr(z), _ptr(lse), _ptr(dy), _ptr(dz), rows, cols,
+                                            _dtype_code(z), _acc_dx(accumulate),
+                                            _stream(stream))
+    _check(rc, "agk_logsumexp_bwd_from_value")
     return dz
 
 

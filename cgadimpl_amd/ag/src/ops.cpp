@@ -375,10 +375,14 @@ std::shared_ptr<Node> logsumexp_row_nodeops(const std::shared_ptr<Node>& z) {
     const Tensor& zv = z->value;
     if (zv.dim() < 1 || zv.cols() == 0) fail("logsumexp_row: needs a non-empty last axis");
     Tensor y = Tensor::empty(row_stat_shape(zv), zv.dtype());
-    agk_check(agk_logsumexp_fwd(zv.data(), y.data(), zv.rows(), zv.cols(),
-                                agk_dtype_of(zv.dtype()), stream_arg()),
+    // Tape: the same values in fp32 (a bf16 y is too coarse for exp(z - y)).
+    auto lse = std::make_shared<Tensor>(Tensor::empty(row_stat_shape(zv), Dtype::Float32));
+    agk_check(agk_logsumexp_fwd_keep(zv.data(), y.data(), static_cast<float*>(lse->data()),
+                                     zv.rows(), zv.cols(), agk_dtype_of(zv.dtype()),
+                                     stream_arg()),
               "logsumexp_row");
     auto n = std::make_shared<Node>(y, Op::LogSumExpRow, z->requires_grad(), "logsumexp_row");
+    n->tape.push_back(lse);
     link_inputs(n, {z});
     return n;
 }
@@ -703,9 +707,13 @@ void vjp_LogSumExpRow(Node* n, const Tensor& gy) {
     GradLocks lock(Z, nullptr);
     bool acc = false;
     Tensor& dz = Z->grad_for_write(z.dtype(), &acc);
-    agk_check(agk_logsumexp_bwd(z.data(), gy.data(), dz.data(), z.rows(), z.cols(),
-                                agk_dtype_of(z.dtype()), acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE,
-                                stream_arg()),
+    // softmax(z) = exp(z - lse): one pass over z with the forward's fp32 value
+    // (the reference recomputes the row maximum and sum, the same quantity)
+    const Tensor& lse = *n->tape.at(0);
+    agk_check(agk_logsumexp_bwd_from_value(z.data(), static_cast<const float*>(lse.data()),
+                                           gy.data(), dz.data(), z.rows(), z.cols(),
+                                           agk_dtype_of(z.dtype()),
+                                           acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE, stream_arg()),
               "vjp_LogSumExpRow");
 }
 

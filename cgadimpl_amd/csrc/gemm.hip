@@ -458,7 +458,6 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], void* __res
 // tile t - 1) multiplies while tile t's first fragments are read.  At the end
 // of the tile each wave waits for its own loads and reads, then the barrier.
 constexpr int kDirectThreads = 256;
-constexpr int WN4 = 128, TN4 = WN4 / 32;  // per-wave columns, MFMA tiles along them
 constexpr int kTrRow = 256;               // bf16 per LDS row of a k-strided operand
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));

@@ -880,7 +880,9 @@ struct LseFwd {
     __device__ static void run(C& c, const RowArgs& p) {
         float m, s;
         c.template max_sumexp<false>(m, s);
-        c.put_val(p.out_row, logf(s) + m);
+        const float y = logf(s) + m;
+        c.put_val(p.out_row, y);
+        if (p.ws0 != nullptr) c.put_f32(p.ws0, y);  // the fp32 value, for the backward
     }
 };
 
@@ -1045,6 +1047,109 @@ int run(const RowArgs& p, int64_t rows, int64_t cols, int dtype, agk_stream_t st
     return dtype == AGK_F32 ? launch<Op, F32>(p, rows, c, st) : launch<Op, BF16>(p, rows, c, st);
 }
 
+// ---- log-sum-exp backward from the forward's fp32 value ---------------------------
+// dz (+)= dy[row] * exp(z - lse[row]): softmax(z) = exp(z - lse(z)), so with the
+// forward's fp32 lse the backward is one streaming pass (read z, write dz)
+// instead of two passes over a row held on chip.  Workgroups of 256 lanes
+// take kLseChunkSlots 16-byte slots of one row (4 per lane).  A row is a head
+// of elements up to its first 16-byte boundary, a body of slots and a tail
+// (z and dz at the same offset from a boundary: SAME_OFF); the body goes
+// through buffer resources sized to it, so slots past the row's end are
+// dropped by the hardware.  Tensors at different offsets take the element-
+// wise form.
+constexpr int kLseLanes = 256;
+constexpr int kLseChunkSlots = kLseLanes * 4;
+
+template <class S, bool SAME_OFF, bool ACC>
+__global__ __launch_bounds__(kLseLanes) void lse_bwd_from_value(
+    const typename S::T* __restrict__ z, const float* __restrict__ lse,
+    const typename S::T* __restrict__ dy, typename S::T* __restrict__ dz, int cols,
+    int64_t nchunk) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) / nchunk;
+    const int chunk = static_cast<int>(static_cast<int64_t>(blockIdx.x) - row * nchunk);
+    const float L = lse[row];
+    const float g = S::get(dy + row);
+    const int64_t off = row * static_cast<int64_t>(cols);
+    const T* zr = z + off;
+    T* dr = dz + off;
+    const int t = threadIdx.x;
+    auto one = [&](int c) {
+        float v = g * fast_exp(S::get(zr + c) - L);
+        if constexpr (ACC) v = acc_add(S::get(dr + c), v);
+        S::put(dr + c, v);
+    };
+    if constexpr (!SAME_OFF) {
+        const int c0 = chunk * kLseChunkSlots * W;
+        const int c1 = c0 + kLseChunkSlots * W < cols ? c0 + kLseChunkSlots * W : cols;
+        for (int c = c0 + t; c < c1; c += kLseLanes) one(c);
+        return;
+    } else {
+        const uint32_t mis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(zr) & 15u);
+        int head = mis ? static_cast<int>((16u - mis) / sizeof(T)) : 0;
+        if (head > cols) head = cols;
+        const int nslot = (cols - head) / W;
+        const int tail0 = head + nslot * W;
+        if (chunk == 0 && t < head) one(t);
+        if (chunk == nchunk - 1 && t < cols - tail0) one(tail0 + t);
+        const uint32_t body = static_cast<uint32_t>(nslot) * 16u;
+        const rsrc_t rz = make_rsrc(zr + head, body);
+        const rsrc_t ro = make_rsrc(dr + head, body);
+        u32x4 v[4], o[4];
+        uint32_t at[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            at[k] = static_cast<uint32_t>(chunk * kLseChunkSlots + k * kLseLanes + t) * 16u;
+            v[k] = bload16_stream(rz, at[k]);
+            if constexpr (ACC) o[k] = bload16_stream(ro, at[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float f[W];
+            S::unpack(v[k], f);
+#pragma unroll
+            for (int e = 0; e < W; ++e) f[e] = g * fast_exp(f[e] - L);
+            if constexpr (ACC) {
+                float old[W];
+                S::unpack(o[k], old);
+#pragma unroll
+                for (int e = 0; e < W; ++e) f[e] = acc_add(old[e], f[e]);
+            }
+            bstore16_stream(ro, at[k], S::pack(f));
+        }
+    }
+}
+
+template <class S>
+int launch_lse_bwd_from_value(const void* z, const float* lse, const void* dy, void* dz,
+                              int64_t rows, int cols, int acc, hipStream_t st) {
+    using T = typename S::T;
+    const int64_t per = static_cast<int64_t>(kLseChunkSlots) * S::kVec;
+    // a head takes at most one slot's worth of columns from the body
+    const int64_t nchunk = (cols + per - 1) / per;
+    if (rows > 0x7fffffffLL / nchunk) return AGK_EINVAL;
+    const dim3 grid(static_cast<unsigned>(rows * nchunk)), block(kLseLanes);
+    const bool same = ((reinterpret_cast<uintptr_t>(z) - reinterpret_cast<uintptr_t>(dz)) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(z) % sizeof(T)) == 0 &&
+                      (reinterpret_cast<uintptr_t>(dz) % sizeof(T)) == 0;
+    const T* zp = static_cast<const T*>(z);
+    const T* gp = static_cast<const T*>(dy);
+    T* op = static_cast<T*>(dz);
+#define AGK_LSE(SAME, ACC_)                                                                    \
+    hipLaunchKernelGGL((lse_bwd_from_value<S, SAME, ACC_>), grid, block, 0, st, zp, lse, gp, op, \
+                       cols, nchunk)
+    if (same) {
+        if (acc) AGK_LSE(true, true);
+        else AGK_LSE(true, false);
+    } else {
+        if (acc) AGK_LSE(false, true);
+        else AGK_LSE(false, false);
+    }
+#undef AGK_LSE
+    return check_launch();
+}
+
 // Checks shared by every entry point; sets *done when there is nothing to do.
 inline int precheck(int64_t rows, int64_t cols, int dtype, bool* done) {
     *done = false;
@@ -1174,6 +1279,39 @@ int agk_logsumexp_bwd(const void* z, const void* dy, void* dz, int64_t rows, int
     p.out = dz;
     p.acc = accumulate & AGK_ACCUM_DX;
     return run<LseBwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_logsumexp_fwd_keep(const void* z, void* y, float* lse, int64_t rows, int64_t cols,
+                           int dtype, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (rows > 0 && cols == 0) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!z || !y || !lse) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.out_row = y;
+    p.ws0 = lse;
+    return run<LseFwd>(p, rows, cols, dtype, stream);
+}
+
+int agk_logsumexp_bwd_from_value(const void* z, const float* lse, const void* dy, void* dz,
+                                 int64_t rows, int64_t cols, int dtype, int accumulate,
+                                 agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (!valid_accumulate(accumulate)) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!z || !lse || !dy || !dz) return AGK_EINVAL;
+    agk::clear_pending_error();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int c = static_cast<int>(cols);
+    const int acc = accumulate & AGK_ACCUM_DX;
+    return dtype == AGK_F32
+               ? launch_lse_bwd_from_value<agk::F32>(z, lse, dy, dz, rows, c, acc, st)
+               : launch_lse_bwd_from_value<agk::BF16>(z, lse, dy, dz, rows, c, acc, st);
 }
 
 int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows, int64_t cols,

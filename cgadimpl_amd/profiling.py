@@ -460,13 +460,21 @@ def write_wide_summary(jsonl, out_md, command):
                   "'-'). % of 8 TB/s for the first layout (algorithmic bytes: softmax forward "
                   "2 tensors, backward 3, log-sum-exp forward 1, backward 2). The 16-byte "
                   "kernel computes the row maximum and the sum of exponentials in one online "
-                  "pass.", "",
-                  "| shape | softmax fwd | softmax bwd | log-sum-exp fwd | log-sum-exp bwd |",
-                  "|---|---|---|---|---|"]
+                  "pass. 'log-sum-exp bwd from value' is agk_logsumexp_bwd_from_value: "
+                  "dz = dy * exp(z - lse) with the forward's fp32 lse (one read of z, one "
+                  "write of dz; what the graph layer's vjp_LogSumExpRow runs); 'log-sum-exp "
+                  "bwd' recomputes the row maximum and sum as the reference's rule does.", "",
+                  "| shape | softmax fwd | softmax bwd | log-sum-exp fwd | log-sum-exp bwd | "
+                  "log-sum-exp bwd from value |",
+                  "|---|---|---|---|---|---|"]
         for r in ro:
             u, g = r["us"], r["gbs"]
             cells = []
-            for k in ("softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd"):
+            for k in ("softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
+                      "logsumexp_bwd_from_value"):
+                if k + "_vec" not in u:
+                    cells.append("-")
+                    continue
                 sc = u.get(k + "_scalar", "-")
                 cells.append(f"{u[k + '_vec']} / {u[k + '_offset']} / {sc} "
                              f"({g[k + '_vec'] / 80:.1f} %)")

@@ -94,6 +94,24 @@ int agk_logsumexp_bwd(const void* z, const void* dy, void* dz, int64_t rows,
                       int64_t cols, int dtype, int accumulate,
                       agk_stream_t stream);
 
+/* agk_logsumexp_fwd that also writes lse[row], the same value in fp32 (the
+ * storage-type y of bf16 rows is too coarse for the backward below), for the
+ * graph layer's tape.                                                        */
+int agk_logsumexp_fwd_keep(const void* z, void* y, float* lse, int64_t rows,
+                           int64_t cols, int dtype, agk_stream_t stream);
+
+/* VJP of the row log-sum-exp from the forward's fp32 value:
+ *     dz (+)= dy[row] * exp(z - lse[row])
+ * softmax(z) = exp(z - logsumexp(z)), so this is the reference's
+ * vjp_LogSumExpRow (autodiff_vjp_ops.cpp:430-440) without recomputing the
+ * row maximum and sum: one read of z and one write of dz, any row width at
+ * the streaming rate.  The result equals agk_logsumexp_bwd's to fp32
+ * rounding (the exponent carries lse's rounding, |lse| * 2^-24 relative).
+ * dy has `rows` elements of the storage type, lse `rows` fp32 values.      */
+int agk_logsumexp_bwd_from_value(const void* z, const float* lse, const void* dy,
+                                 void* dz, int64_t rows, int64_t cols, int dtype,
+                                 int accumulate, agk_stream_t stream);
+
 /* JVP of the row log-sum-exp: ty[row] = sum(softmax(z) * tz) over the row,
  * jvp_LogSumExpRow, autodiff_jvp_ops.cpp:421-434.  ty has `rows` elements of
  * the storage type.                                                          */

@@ -177,7 +177,11 @@ def check_logsumexp(z, t, label):
     y = agk.logsumexp_fwd(z)
     dz = agk.logsumexp_bwd(z, dy)
     ty = agk.logsumexp_jvp(z, t)
+    # the forward that keeps its fp32 value, and the one-pass backward from it
+    yk, lse = agk.logsumexp_fwd_keep(z)
+    dzv = agk.logsumexp_bwd_from_value(z, lse, dy)
     torch.cuda.synchronize()
+    assert torch.equal(yk, y), f"{label}: logsumexp_fwd_keep's y differs from logsumexp_fwd's"
     rows = _sample_rows(R, z.shape[1] + 3)
     zs, ts, dys = _host_rows(z, rows), _host_rows(t, rows), _host_rows(dy, rows)
     if bf16:
@@ -185,14 +189,19 @@ def check_logsumexp(z, t, label):
                         ro.logsumexp_jvp_bf16(zs, ts))
     else:
         ry, rdz, rty = ro.logsumexp_fwd(zs), ro.logsumexp_bwd(zs, dys), ro.logsumexp_jvp(zs, ts)
+    rl32 = ro.logsumexp_fwd(as_f32(zs))  # the fp32 value the storage-type y rounds
     zf = _f64(zs)
     sm = np.exp(zf - zf.max(-1, keepdims=True))
     sm /= sm.sum(-1, keepdims=True)
     jscale = np.sum(np.abs(sm * _f64(ts)), -1)
+    lscale = np.maximum(np.abs(_f64(rl32))[:, 0], 1.0)
     return {
         "y": _scaled_err(_host_rows(y, rows), ry, np.maximum(np.abs(_f64(ry))[:, 0], 1.0)),
         "dz": _row_rel(_host_rows(dz, rows), rdz),
         "ty": _scaled_err(_host_rows(ty, rows), rty, jscale),
+        # fp32 whatever the storage: held to the fp32 bar
+        "lse": _scaled_err(_host_rows(lse, rows), rl32, lscale) * (_tol(bf16) / TOL_F32),
+        "dz from lse": _row_rel(_host_rows(dzv, rows), rdz),
     }
 
 
@@ -301,6 +310,9 @@ def test_same_offset_tensors_take_the_16_byte_kernel(cuda, dtype, cols):
     dl = dy[:, :1].contiguous()
     lse = agk.logsumexp_fwd(z)
     agk.logsumexp_bwd(z, dl, dz=dlz)
+    _, l32 = agk.logsumexp_fwd_keep(z)
+    dlv = shifted(torch.zeros_like(x))
+    agk.logsumexp_bwd_from_value(z, l32, dl, dz=dlv)  # head/body/tail form
     torch.cuda.synchronize()
     zs, ds, ys, dls = to_host(z), to_host(d), to_host(y), to_host(dl)
     bf16 = dtype == "bf16"
@@ -314,7 +326,8 @@ def test_same_offset_tensors_take_the_16_byte_kernel(cuda, dtype, cols):
     scale = _rowmax(yf) * (_rowmax(gf) + np.abs(np.sum(yf * gf, -1)))
     e = {"softmax y": _row_rel(ys, ry), "softmax dz": _scaled_err(to_host(dz), rdz, scale),
          "lse y": _scaled_err(to_host(lse), rl, np.maximum(np.abs(_f64(rl))[:, 0], 1.0)),
-         "lse dz": _row_rel(to_host(dlz), rdl)}
+         "lse dz": _row_rel(to_host(dlz), rdl),
+         "lse dz from value": _row_rel(to_host(dlv), rdl)}
     assert_ok(e, _tol(bf16), f"same-offset {dtype} {rows}x{cols}")
 
 
@@ -335,6 +348,10 @@ def test_backward_accumulates(cuda, dtype, shape):
     dr = dy[:, :1].contiguous()
     outs["logsumexp"] = (agk.logsumexp_bwd(x, dr),
                          agk.logsumexp_bwd(x, dr, dz=pre.clone(), accumulate=True))
+    _, l32 = agk.logsumexp_fwd_keep(x)
+    outs["logsumexp from value"] = (
+        agk.logsumexp_bwd_from_value(x, l32, dr),
+        agk.logsumexp_bwd_from_value(x, l32, dr, dz=pre.clone(), accumulate=True))
     torch.cuda.synchronize()
     tol = 2 * _tol(dtype == "bf16")
     for name, (fresh, acc) in outs.items():
@@ -404,8 +421,10 @@ def test_results_are_deterministic(cuda, shape):
     first = None
     for _ in range(3):
         y, mean, rstd = agk.layernorm_fwd(x)
+        l32 = agk.logsumexp_fwd_keep(x)[1]
         outs = [y, mean, rstd, agk.layernorm_bwd(x, mean, rstd, dy), agk.softmax_fwd(x),
-                agk.logsumexp_fwd(x), agk.logsumexp_jvp(x, dy)]
+                agk.logsumexp_fwd(x), agk.logsumexp_jvp(x, dy), l32,
+                agk.logsumexp_bwd_from_value(x, l32, dy[:, :1].contiguous())]
         torch.cuda.synchronize()
         if first is None:
             first = [o.clone() for o in outs]
