@@ -475,6 +475,13 @@ def run(cfg_name, steps, warmup, cpu_seconds):
     # configurations.
     graph_step_one_set_ms = graph_replay_ms(lambda i, st: (fwd(0, st), bwd(0, st)), steps)
 
+    # What gamma costs the forward: the same calls with gamma == NULL (ag::rms's
+    # forward; the same traffic less gamma's per-row loads), replayed likewise.
+    def fwd_no_gamma(i, st):
+        x, g, dy, y, inv, dx, dg = sets[i % nsets]
+        agk.rmsnorm_fwd(x, None, cfg.eps, y=y, inv_rms=inv, stream=st)
+    graph_fwd_no_gamma_ms = graph_replay_ms(fwd_no_gamma, steps)
+
     ms_per_step = wall * 1e3 / steps
     alg = cfg.algorithmic_bytes()
     value = alg / (ms_per_step * 1e-3) / 1e9
@@ -536,6 +543,8 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "fwd_ms": round(graph_fwd_ms, 5),
             "bwd_ms": round(graph_bwd_ms, 5),
             "ms_per_step_one_set": round(graph_step_one_set_ms, 5),
+            "fwd_no_gamma_ms": round(graph_fwd_no_gamma_ms, 5),
+            "fwd_gamma_cost_pct": round(100.0 * (graph_fwd_ms / graph_fwd_no_gamma_ms - 1.0), 2),
         },
         "cpu_baseline": None,
     }
@@ -682,6 +691,13 @@ def run_c5(steps, warmup, cpu=True):
                                                 stream=stream)),
         "gemm_dW": lib_ms(lambda: agk.gemm_bf16(h, dy, dW, trans_a=True, workspace=ws_w,
                                                 stream=stream))}
+    # The forward product with the RMSNorm carried into it (normalize-on-load,
+    # y = diag(r) (x diag(gamma)) W: kscale = gamma, rowscale = inv_rms) instead
+    # of reading the materialised h.  A k-scale runs on the register-staged
+    # kernel (the direct-to-LDS kernel has no register stage to apply it in),
+    # so this is the price of not writing h.
+    g32 = g.float().contiguous()
+    kscale_ms = lib_ms(lambda: agk.gemm_bf16(x, W, y, kscale=g32, rowscale=inv, stream=stream))
     torch_ms = {"gemm_y": lib_ms(lambda: h @ W), "gemm_dh": lib_ms(lambda: dy @ W.t()),
                 "gemm_dW": lib_ms(lambda: h.t() @ dy)}
     flops = 2.0 * M * N * K
@@ -713,6 +729,7 @@ def run_c5(steps, warmup, cpu=True):
         "gpu_state": {"before_timed": state_before, "after_timed": state_after},
         "rmsnorm_gbs": round(norm_bytes / (norm_ms * 1e-3) / 1e9, 1),
         "alone_ms": {k: round(v, 4) for k, v in alone_ms.items()},
+        "gemm_y_normalize_on_load_ms": round(kscale_ms, 4),
         "torch_hipblaslt_ms": {k: round(v, 4) for k, v in torch_ms.items()},
         "torch_hipblaslt_tflops": round(3 * flops / (sum(torch_ms.values()) * 1e-3) / 1e12, 1),
         "cpu_baseline": cpu_baseline_c5() if cpu else None,
@@ -1032,6 +1049,53 @@ def mfma_probe(reps):
     return recs
 
 
+def gemm_f32_bench(reps):
+    """The graph layer's fp32 matmul (agk_gemm_f32, the fp32 MFMA kernel) at
+    square and layer-like sizes in its four layouts, against torch's fp32
+    matmul (the vendor library) on the same operands; HIP events on the
+    launch stream, after warm-up calls.  One JSON line per shape."""
+    import torch
+
+    import cgadimpl_amd as agk
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    def ms_of(f):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = TimingEvent(), TimingEvent()
+        e0.record(stream)
+        for _ in range(reps):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+    recs = []
+    for M, N, K in ((4096, 4096, 4096), (8192, 4096, 4096), (1024, 1024, 1024)):
+        rec = {"gemm_f32": f"{M}x{N}x{K}", "tflops": {}, "torch_tflops": {}}
+        for ta in (False, True):
+            for tb in (False, True):
+                a = torch.randn((K, M) if ta else (M, K), generator=gen, device=dev)
+                b = torch.randn((N, K) if tb else (K, N), generator=gen, device=dev)
+                c = torch.empty(M, N, device=dev)
+                tag = ("At" if ta else "A") + ("Bt" if tb else "B")
+                ms = ms_of(lambda: agk.gemm_f32(a, b, c=c, trans_a=ta, trans_b=tb,
+                                                stream=stream))
+                at, bt = (a.t() if ta else a), (b.t() if tb else b)
+                tms = ms_of(lambda: torch.matmul(at, bt, out=c))
+                rec["tflops"][tag] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
+                rec["torch_tflops"][tag] = round(2.0 * M * N * K / (tms * 1e-3) / 1e12, 1)
+                del a, b, c
+        rec["pct_of_fp32_matrix_peak"] = round(100.0 * max(rec["tflops"].values()) / 157.3, 1)
+        recs.append(rec)
+        print(json.dumps(rec), flush=True)
+    return recs
+
+
 WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
                ("f32", 256, 65536), ("f32", 4096, 32768), ("bf16", 8, 262144),
                ("bf16", 51, 32768), ("bf16", 1024, 65536), ("bf16", 16384, 20480),
@@ -1205,6 +1269,9 @@ def main():
                     help="only run the MFMA probe (the bf16 GEMM's inner loop without loads or "
                          "barriers, by operand content, with the shader clock it ran at), then "
                          "exit")
+    ap.add_argument("--gemm-f32", action="store_true",
+                    help="only time the fp32 GEMM (agk_gemm_f32) against torch's fp32 matmul, "
+                         "then exit")
     ap.add_argument("--wide", action="store_true",
                     help="only time rows wider than the register-resident kernels: the split "
                          "paths against the one-workgroup-per-row kernels, and softmax / "
@@ -1219,6 +1286,9 @@ def main():
         return
     if args.mfma_probe:
         mfma_probe(min(args.steps, 5))
+        return
+    if args.gemm_f32:
+        gemm_f32_bench(min(args.steps, 10))
         return
     if args.wide:
         run_wide(min(args.steps, 20))

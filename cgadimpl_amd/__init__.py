@@ -287,7 +287,7 @@ def gemm_bf16(a, b, c=None, trans_a: bool = False, trans_b: bool = False, out_dt
 
 def gemm_f32(a, b, c=None, trans_a: bool = False, trans_b: bool = False, accumulate=False,
              stream=None):
-    """C (+)= op(A) op(B) in fp32 (agk_gemm_f32, rocBLAS sgemm, deterministic).
+    """C (+)= op(A) op(B) in fp32 (agk_gemm_f32: the fp32 MFMA kernel, deterministic).
 
     a: [M, K] (or [K, M] with trans_a), b: [K, N] (or [N, K] with trans_b),
     row-major contiguous float32; c [M, N] float32."""

@@ -88,10 +88,10 @@ def host_library(name: str, sources: list[str], compiler: str = "g++") -> str:
     return out
 
 
-# The kernel library's sources, and what it links beyond the HIP runtime
-# (rocBLAS for the graph layer's fp32 matmul, gemm_f32.hip).
+# The kernel library's sources (every kernel hand-written: it links nothing
+# beyond the HIP runtime).
 KERNEL_SOURCES = ["rmsnorm.hip", "gemm.hip", "gemm_f32.hip", "rowops.hip", "bcast.hip"]
-KERNEL_LIBS = [f"-L{ROCM}/lib", "-lrocblas", f"-Wl,-rpath,{ROCM}/lib"]
+KERNEL_LIBS: list[str] = []
 # The benchmark's own measurement probes (csrc/agk_bench.h): loaded by bench.py
 # only, not part of the product ABI.
 BENCH_SOURCES = ["probe.hip", "mfma_probe.hip"]

@@ -151,7 +151,7 @@ void gemm(const void* A, int64_t lda, bool at, const void* B, int64_t ldb, bool 
               what);
 }
 
-// The same product on fp32 operands (rocBLAS sgemm through agk_gemm_f32).
+// The same product on fp32 operands (the fp32 MFMA kernel behind agk_gemm_f32).
 void gemm_f32(const void* A, int64_t lda, bool at, const void* B, int64_t ldb, bool bt, void* C,
               int64_t ldc, int64_t M, int64_t N, int64_t K, bool acc, const char* what) {
     agk_check(agk_gemm_f32(static_cast<const float*>(A), lda, at, static_cast<const float*>(B),

@@ -1,96 +1,212 @@
 // gemm_f32.hip -- fp32 GEMM for the graph layer's matmul on float32 tensors
-// (cgadimpl/src/ops/linalg.cpp:12-20 and its VJP,
-// cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:258-263).  A plain library GEMM:
-// it runs rocBLAS's sgemm (no fused work, not on the RMSNorm layer's path; the
-// layer's products are bf16 on the hand-written MFMA kernel in gemm.hip).
-// Host code only.
+// (cgadimpl/src/ops/linalg.cpp:12-20 and its VJP's products,
+// cgadimpl/src/autodiff/autodiff_vjp_ops.cpp:258-263), on CDNA4's fp32
+// matrix instruction v_mfma_f32_32x32x2_f32.  Not on the RMSNorm layer's
+// measured path (its products are bf16, gemm.hip): a general kernel for any
+// sizes, leading dimensions, layouts and alignment.
 //
-// Determinism: every handle has atomics disallowed, so rocBLAS picks kernels
-// without atomic split-K reductions and a call gives the same bits every run.
-// Handles: one per device, created on first use with that device current and
-// kept for the life of the process (never destroyed, so no teardown ordering
-// against the HIP runtime); a mutex serialises the enqueue of calls, which
-// return as soon as the work is queued on the caller's stream.
+//   C[M][ldc] (+)= op(A) op(B)
+//
+// Shape.  A workgroup of 256 lanes (4 waves, 2 x 2) computes a 128 x 128 tile
+// of C; each wave owns 64 x 64 of it as 2 x 2 MFMA accumulators (64 AGPRs).
+// K is walked in steps of 16 through two LDS stages (40 KiB per workgroup, so
+// four workgroups share a CU and hide each other's load latency): the next
+// step's 8 + 8 values per lane are loaded into registers while the current
+// step is multiplied, then written to the other stage (one barrier per step).
+//
+// Operands.  Each operand is staged as a logical [rows][K] matrix (A: M rows,
+// B: N rows) into LDS laid out [k][row], whatever its memory layout:
+//  - k contiguous in memory (A as [M][K], B given as B^T [N][K]): lane t loads
+//    k = t % 16 of rows t / 16 + 16 i, so 16 neighbouring lanes read 64
+//    contiguous bytes;
+//  - rows contiguous (A given as A^T [K][M], B as [K][N]): lane t loads row
+//    t % 128 of k = t / 128 + 2 i, 128 neighbouring lanes 512 bytes.
+// Elements outside the matrix are staged as zeros, so edge tiles need no
+// other special case.  LDS k-rows are kStride = 160 floats apart: k and k + 1
+// start 32 banks apart, so an MFMA operand read (lanes 0-31 at k, 32-63 at
+// k + 1, 32 consecutive rows each) touches every bank once.
+//
+// MFMA lane layout (the 32 x 32 block instructions' layout, as in gemm.hip):
+// A operand lane l holds row l % 32, k = l / 32; B operand lane l holds
+// column l % 32, the same k; accumulator element e of lane l is
+// C[8 * (e / 4) + 4 * (l / 32) + e % 4][l % 32].
+//
+// Determinism: every output element is summed in the same k order in every
+// call (no split-K, no atomics), so results are bit-identical run to run.
+// Rounding: fp32 products and sums in the matrix core; the bound is that of
+// fp32 summation, |C - exact| <= (K + 1) 2^-24 (|A| |B|).
 
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <stdint.h>
-
-#include <mutex>
 
 #include "agk_rmsnorm.h"
 #include "rowcommon.hpp"
 
-namespace {
+namespace agk_sgemm {
 
-constexpr int kMaxDevices = 64;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-struct Handles {
-    std::mutex mu;
-    rocblas_handle h[kMaxDevices] = {};
-};
+constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int kThreads = 256;
+constexpr int kStride = 160;              // floats per LDS k-row (128 used)
+constexpr int kStage = BK * kStride;      // floats per operand per stage
+constexpr int kPerLane = BM * BK / kThreads;  // staged values per lane per operand (8)
 
-Handles& handles() {
-    static Handles* p = new Handles;  // intentionally leaked: outlives every caller
-    return *p;
-}
-
-int status_of(rocblas_status s) {
-    switch (s) {
-        case rocblas_status_success: return AGK_OK;
-        case rocblas_status_invalid_size:
-        case rocblas_status_invalid_pointer:
-        case rocblas_status_invalid_value: return AGK_EINVAL;
-        default: return AGK_EHIP;
+// One operand's values for one k-step: element (row r0 + row, k0 + k) of the
+// logical [rows][K] matrix, at p[row * ld + k] (KC) or p[k * ld + row] (!KC).
+template <bool KC>
+__device__ __forceinline__ void load_step(float (&v)[kPerLane], const float* __restrict__ p,
+                                          int64_t ld, int r0, int rows, int k0, int K) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+        const int row = KC ? t / BK + (kThreads / BK) * i : t % BM;
+        const int k = KC ? t % BK : t / BM + (kThreads / BM) * i;
+        const int gr = r0 + row, gk = k0 + k;
+        v[i] = (gr < rows && gk < K)
+                   ? (KC ? p[static_cast<int64_t>(gr) * ld + gk] : p[static_cast<int64_t>(gk) * ld + gr])
+                   : 0.0f;
     }
 }
 
-}  // namespace
+template <bool KC>
+__device__ __forceinline__ void store_step(const float (&v)[kPerLane], float* lds) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+        const int row = KC ? t / BK + (kThreads / BK) * i : t % BM;
+        const int k = KC ? t % BK : t / BM + (kThreads / BM) * i;
+        lds[k * kStride + row] = v[i];
+    }
+}
+
+// A_KC: A is [M][lda] (k contiguous), else A^T [K][lda]; B_KC: B is given as
+// B^T [N][ldb] (k contiguous), else B [K][ldb].
+template <bool A_KC, bool B_KC>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
+    float* __restrict__ C, int64_t ldc, int M, int N, int K, int accumulate, int tiles_n) {
+    __shared__ float lds[2][2 * kStage];  // [stage][A k-rows, then B k-rows]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = (static_cast<int>(blockIdx.x) / tiles_n) * BM;
+    const int n0 = (static_cast<int>(blockIdx.x) % tiles_n) * BN;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    float va[kPerLane], vb[kPerLane];
+    const int nk = (K + BK - 1) / BK;
+    load_step<A_KC>(va, A, lda, m0, M, 0, K);
+    load_step<B_KC>(vb, B, ldb, n0, N, 0, K);
+    store_step<A_KC>(va, lds[0]);
+    store_step<B_KC>(vb, lds[0] + kStage);
+    __syncthreads();
+
+    const int fr = lane & 31;  // operand row / column within a 32-block
+    const int fk = lane >> 5;  // operand k within a 2-deep MFMA step
+    for (int kt = 0; kt < nk; ++kt) {
+        const float* as = lds[kt & 1];
+        const float* bs = as + kStage;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            load_step<A_KC>(va, A, lda, m0, M, (kt + 1) * BK, K);
+            load_step<B_KC>(vb, B, ldb, n0, N, (kt + 1) * BK, K);
+        }
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) a[i] = as[(kk + fk) * kStride + wm * 64 + i * 32 + fr];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = bs[(kk + fk) * kStride + wn * 64 + j * 32 + fr];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            float* nxt = lds[(kt + 1) & 1];
+            store_step<A_KC>(va, nxt);
+            store_step<B_KC>(vb, nxt + kStage);
+        }
+        __syncthreads();
+    }
+
+    const int col_l = lane & 31;
+    const int row_l = 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + row_l + (e & 3);
+            if (row >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = n0 + wn * 64 + j * 32 + col_l;
+                if (col >= N) continue;
+                float* p = C + static_cast<int64_t>(row) * ldc + col;
+                const float v = acc[i][j][e];
+                *p = accumulate ? agk::acc_add(*p, v) : v;
+            }
+        }
+    }
+}
+
+// C = 0 over M rows of N columns (ldc apart): the empty sum (K == 0).  A
+// kernel, not a memset, so that the call can be captured.
+__global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ C, int64_t ldc,
+                                                        int N) {
+    float* r = C + static_cast<int64_t>(blockIdx.x) * ldc;
+    for (int c = threadIdx.x; c < N; c += 256) r[c] = 0.0f;
+}
+
+}  // namespace agk_sgemm
 
 extern "C" int agk_gemm_f32(const float* A, int64_t lda, int a_trans, const float* B, int64_t ldb,
                             int b_trans, float* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                             int accumulate, agk_stream_t stream) {
-    constexpr int64_t kMax = 0x7fffffffLL;  // rocblas_int
+    using namespace agk_sgemm;
+    constexpr int64_t kMax = 0x7fffffffLL;
     if (M < 0 || N < 0 || K < 0 || M > kMax || N > kMax || K > kMax) return AGK_EINVAL;
     if (M == 0 || N == 0) return AGK_OK;
-    if (!C || ldc < N || ldc > kMax) return AGK_EINVAL;
+    if (!C || ldc < N) return AGK_EINVAL;
     if (K > 0) {
         if (!A || !B) return AGK_EINVAL;
-        if (lda < (a_trans ? M : K) || ldb < (b_trans ? K : N) || lda > kMax || ldb > kMax)
-            return AGK_EINVAL;
+        if (lda < (a_trans ? M : K) || ldb < (b_trans ? K : N)) return AGK_EINVAL;
     }
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return AGK_EHIP;
-    Handles& hs = handles();
-    std::lock_guard<std::mutex> lock(hs.mu);
-    rocblas_handle& h = hs.h[dev];
-    if (!h) {
-        if (rocblas_create_handle(&h) != rocblas_status_success) {
-            h = nullptr;
-            return AGK_EHIP;
-        }
-        if (rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed) != rocblas_status_success)
-            return AGK_EHIP;
+    agk::clear_pending_error();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    if (K == 0) {  // the empty sum: zeros, or C as it was
+        if (accumulate) return AGK_OK;
+        hipLaunchKernelGGL(zero_rows_kernel, dim3(static_cast<unsigned>(m)), dim3(256), 0, st, C,
+                           ldc, n);
+        return agk::check_launch();
     }
-    if (rocblas_set_stream(h, reinterpret_cast<hipStream_t>(stream)) != rocblas_status_success)
-        return AGK_EHIP;
-    // Row-major C = op(A) op(B) is column-major C^T = op(B)^T op(A)^T: the
-    // row-major arrays, read as column-major, are the transposes already.
-    const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
-    // K == 0: an empty sum; sgemm scales C by beta (zeros, or C unchanged)
-    // without reading the operands, which may be null: C stands in for them,
-    // with the smallest leading dimensions sgemm accepts for their layouts
-    auto at_least_1 = [](int64_t v) { return v > 1 ? v : int64_t{1}; };
-    const float* a = K > 0 ? A : C;
-    const float* b = K > 0 ? B : C;
-    const rocblas_int ld_a =
-        static_cast<rocblas_int>(K > 0 ? lda : at_least_1(a_trans ? M : K));
-    const rocblas_int ld_b =
-        static_cast<rocblas_int>(K > 0 ? ldb : at_least_1(b_trans ? K : N));
-    return status_of(rocblas_sgemm(h, b_trans ? rocblas_operation_transpose : rocblas_operation_none,
-                                   a_trans ? rocblas_operation_transpose : rocblas_operation_none,
-                                   static_cast<rocblas_int>(N), static_cast<rocblas_int>(M),
-                                   static_cast<rocblas_int>(K), &alpha, b, ld_b, a, ld_a, &beta,
-                                   C, static_cast<rocblas_int>(ldc)));
+    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    if (tiles_m * tiles_n > kMax) return AGK_EINVAL;
+    const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n)), block(kThreads);
+    const int acc = accumulate != 0;
+    const int tn = static_cast<int>(tiles_n);
+    // A k-contiguous unless given transposed; B k-contiguous only when given as B^T
+    const bool a_kc = a_trans == 0, b_kc = b_trans != 0;
+#define AGK_F32(AK, BKC)                                                                      \
+    hipLaunchKernelGGL((gemm_f32_kernel<AK, BKC>), grid, block, 0, st, A, lda, B, ldb, C, ldc, m, \
+                       n, k, acc, tn)
+    if (a_kc && b_kc) AGK_F32(true, true);
+    else if (a_kc) AGK_F32(true, false);
+    else if (b_kc) AGK_F32(false, true);
+    else AGK_F32(false, false);
+#undef AGK_F32
+    return agk::check_launch();
 }

@@ -209,10 +209,12 @@ int agk_fill(void* dst, int64_t n, float value, int dtype, agk_stream_t stream);
  * (cgadimpl/src/ops/linalg.cpp:12-20; VJP autodiff_vjp_ops.cpp:258-263):
  *   C[M][ldc] (+)= op(A) op(B), all fp32, row-major,
  *   A: a_trans == 0 -> [M][lda], else [K][lda];  B: b_trans == 0 -> [K][ldb],
- *   else [N][ldb].  A plain library GEMM (rocBLAS sgemm, atomics disallowed:
- *   deterministic), not on the RMSNorm layer's bf16 path.  M == 0 or N == 0
- *   is a no-op; K == 0 writes zeros (or leaves C when accumulating).  No
- *   alignment or multiple-of-8 requirements.                                */
+ *   else [N][ldb].  Hand-written on the fp32 matrix instruction
+ *   (v_mfma_f32_32x32x2_f32), 128 x 128 tiles, no split-K and no atomics:
+ *   bit-identical run to run.  Not on the RMSNorm layer's bf16 path.  M == 0
+ *   or N == 0 is a no-op; K == 0 writes zeros (or leaves C when
+ *   accumulating).  No alignment or multiple-of-8 requirements; a kernel
+ *   launch only, so it may be captured into a HIP graph.                     */
 int agk_gemm_f32(const float* A, int64_t lda, int a_trans, const float* B, int64_t ldb,
                  int b_trans, float* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                  int accumulate, agk_stream_t stream);

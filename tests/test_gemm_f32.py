@@ -4,10 +4,10 @@ autodiff_vjp_ops.cpp:258-263).
 
 Checked against a float64 product on the host.  Bar: the worst-case bound of
 fp32 summation in any order, |C - C64| <= K * 2^-24 * (|A| |B|) element-wise
-(plus one rounding of the stored result), which holds whatever blocking the
-library picks; every layout (A, B transposed or not), odd sizes, K == 0
-(zeros, or C unchanged when accumulating), accumulation, and bit-identical
-results across calls (atomics disallowed).
+(plus one rounding of the stored result); every layout (A, B transposed or
+not), odd sizes and edge tiles, leading dimensions wider than the rows, K == 0
+(zeros, or C unchanged when accumulating), accumulation, bit-identical results
+across calls, and replays of a captured HIP graph equal to eager calls.
 """
 from __future__ import annotations
 
@@ -20,7 +20,8 @@ from gpu_util import to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 OK, EINVAL = 0, 1  # agk_status
-SHAPES = [(1, 1, 1), (7, 5, 3), (64, 48, 33), (129, 257, 95), (300, 17, 1000), (1000, 520, 64)]
+SHAPES = [(1, 1, 1), (7, 5, 3), (64, 48, 33), (129, 257, 95), (300, 17, 1000), (1000, 520, 64),
+          (256, 384, 513), (2048, 1024, 160)]
 
 
 def _bound(a, b, K):
@@ -74,3 +75,53 @@ def test_rejects_bad_arguments(cuda):
     assert lib.agk_gemm_f32(p, 4, 0, p, 4, 0, p, 3, 4, 4, 4, 0, None) == EINVAL
     assert lib.agk_gemm_f32(p, 3, 0, p, 4, 0, p, 4, 4, 4, 4, 0, None) == EINVAL
     assert lib.agk_gemm_f32(None, 4, 0, None, 4, 0, None, 4, 0, 4, 4, 0, None) == OK
+
+
+def test_leading_dimensions_wider_than_rows(cuda):
+    """Operands and C inside wider buffers (ld > the used width), as views of
+    larger matrices: the product of the views, C's other columns untouched."""
+    import torch
+    g = torch.Generator(device=cuda)
+    g.manual_seed(11)
+    M, N, K = 70, 90, 50
+    abuf = torch.randn(M, K + 13, generator=g, device=cuda)
+    bbuf = torch.randn(K, N + 7, generator=g, device=cuda)
+    cbuf = torch.full((M, N + 5), 3.0, device=cuda)
+    rc = agk.lib().agk_gemm_f32(abuf.data_ptr(), K + 13, 0, bbuf.data_ptr(), N + 7, 0,
+                                cbuf.data_ptr(), N + 5, M, N, K, 0, None)
+    torch.cuda.synchronize()
+    assert rc == OK
+    a, b = to_host(abuf)[:, :K], to_host(bbuf)[:, :N]
+    c = to_host(cbuf)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.all(np.abs(c[:, :N] - ref) <= _bound(a, b, K))
+    assert np.all(c[:, N:] == 3.0)
+
+
+def test_graph_capture_replays_match_eager(cuda):
+    """agk_gemm_f32 is a plain kernel launch: captured once into a HIP graph,
+    three replays on new operands (eager work and synchronisations between
+    them) each equal the eager call bit for bit."""
+    import torch
+    M, N, K = 300, 260, 200
+    a = torch.empty(M, K, device=cuda)
+    b = torch.empty(N, K, device=cuda)  # given as B^T
+    c = torch.empty(M, N, device=cuda)
+    a.normal_()
+    b.normal_()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        agk.gemm_f32(a, b, c=c, trans_b=True, stream=torch.cuda.current_stream())
+    gen = torch.Generator(device=cuda)
+    for k in range(3):
+        gen.manual_seed(40 + k)
+        a.copy_(torch.randn(M, K, generator=gen, device=cuda))
+        b.copy_(torch.randn(N, K, generator=gen, device=cuda))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = c.clone()
+        want = agk.gemm_f32(a, b, trans_b=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), k
+    del graph
