@@ -7,8 +7,10 @@
 //
 //   C[M][ldc] (+)= op(A) op(B)
 //
-// Shape.  A workgroup of 256 lanes (4 waves, 2 x 2) computes a 128 x 128 tile
-// of C; each wave owns 64 x 64 of it as 2 x 2 MFMA accumulators (64 AGPRs).
+// Shape.  A workgroup of 256 lanes (4 waves, 2 x 2) computes a TILE x TILE
+// tile of C; each wave owns (TILE / 2)^2 of it as 32 x 32 MFMA accumulators
+// (TILE 128: 2 x 2 of them, 64 AGPRs).  Products with fewer 128-tiles than
+// the GPU has CUs take TILE 64 (four times the workgroups).
 // K is walked in steps of 16 through two LDS stages (40 KiB per workgroup, so
 // four workgroups share a CU and hide each other's load latency): the next
 // step's 8 + 8 values per lane are loaded into registers while the current
@@ -47,22 +49,23 @@ namespace agk_sgemm {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int BK = 16;
 constexpr int kThreads = 256;
-constexpr int kStride = 160;              // floats per LDS k-row (128 used)
+constexpr int kStride = 160;              // floats per LDS k-row (at most 128 used)
 constexpr int kStage = BK * kStride;      // floats per operand per stage
-constexpr int kPerLane = BM * BK / kThreads;  // staged values per lane per operand (8)
 
 // One operand's values for one k-step: element (row r0 + row, k0 + k) of the
-// logical [rows][K] matrix, at p[row * ld + k] (KC) or p[k * ld + row] (!KC).
-template <bool KC>
-__device__ __forceinline__ void load_step(float (&v)[kPerLane], const float* __restrict__ p,
-                                          int64_t ld, int r0, int rows, int k0, int K) {
+// logical [rows][K] matrix, at p[row * ld + k] (KC) or p[k * ld + row] (!KC);
+// TILE * BK / 256 values per lane.
+template <int TILE, bool KC>
+__device__ __forceinline__ void load_step(float (&v)[TILE * BK / kThreads],
+                                          const float* __restrict__ p, int64_t ld, int r0,
+                                          int rows, int k0, int K) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int row = KC ? t / BK + (kThreads / BK) * i : t % BM;
-        const int k = KC ? t % BK : t / BM + (kThreads / BM) * i;
+    for (int i = 0; i < TILE * BK / kThreads; ++i) {
+        const int row = KC ? t / BK + (kThreads / BK) * i : t % TILE;
+        const int k = KC ? t % BK : t / TILE + (kThreads / TILE) * i;
         const int gr = r0 + row, gk = k0 + k;
         v[i] = (gr < rows && gk < K)
                    ? (KC ? p[static_cast<int64_t>(gr) * ld + gk] : p[static_cast<int64_t>(gk) * ld + gr])
@@ -70,45 +73,47 @@ __device__ __forceinline__ void load_step(float (&v)[kPerLane], const float* __r
     }
 }
 
-template <bool KC>
-__device__ __forceinline__ void store_step(const float (&v)[kPerLane], float* lds) {
+template <int TILE, bool KC>
+__device__ __forceinline__ void store_step(const float (&v)[TILE * BK / kThreads], float* lds) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int row = KC ? t / BK + (kThreads / BK) * i : t % BM;
-        const int k = KC ? t % BK : t / BM + (kThreads / BM) * i;
+    for (int i = 0; i < TILE * BK / kThreads; ++i) {
+        const int row = KC ? t / BK + (kThreads / BK) * i : t % TILE;
+        const int k = KC ? t % BK : t / TILE + (kThreads / TILE) * i;
         lds[k * kStride + row] = v[i];
     }
 }
 
 // A_KC: A is [M][lda] (k contiguous), else A^T [K][lda]; B_KC: B is given as
 // B^T [N][ldb] (k contiguous), else B [K][ldb].
-template <bool A_KC, bool B_KC>
+template <int TILE, bool A_KC, bool B_KC>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, int M, int N, int K, int accumulate, int tiles_n) {
     __shared__ float lds[2][2 * kStage];  // [stage][A k-rows, then B k-rows]
 
+    constexpr int NT = TILE / 64;  // 32 x 32 MFMA blocks per wave along each dimension
+    constexpr int WT = TILE / 2;   // the wave's block of C is WT x WT
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = (static_cast<int>(blockIdx.x) / tiles_n) * BM;
-    const int n0 = (static_cast<int>(blockIdx.x) % tiles_n) * BN;
+    const int m0 = (static_cast<int>(blockIdx.x) / tiles_n) * TILE;
+    const int n0 = (static_cast<int>(blockIdx.x) % tiles_n) * TILE;
 
-    f32x16 acc[2][2];
+    f32x16 acc[NT][NT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    float va[kPerLane], vb[kPerLane];
+    float va[TILE * BK / kThreads], vb[TILE * BK / kThreads];
     const int nk = (K + BK - 1) / BK;
-    load_step<A_KC>(va, A, lda, m0, M, 0, K);
-    load_step<B_KC>(vb, B, ldb, n0, N, 0, K);
-    store_step<A_KC>(va, lds[0]);
-    store_step<B_KC>(vb, lds[0] + kStage);
+    load_step<TILE, A_KC>(va, A, lda, m0, M, 0, K);
+    load_step<TILE, B_KC>(vb, B, ldb, n0, N, 0, K);
+    store_step<TILE, A_KC>(va, lds[0]);
+    store_step<TILE, B_KC>(vb, lds[0] + kStage);
     __syncthreads();
 
     const int fr = lane & 31;  // operand row / column within a 32-block
@@ -118,26 +123,26 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
         const float* bs = as + kStage;
         const bool more = kt + 1 < nk;
         if (more) {
-            load_step<A_KC>(va, A, lda, m0, M, (kt + 1) * BK, K);
-            load_step<B_KC>(vb, B, ldb, n0, N, (kt + 1) * BK, K);
+            load_step<TILE, A_KC>(va, A, lda, m0, M, (kt + 1) * BK, K);
+            load_step<TILE, B_KC>(vb, B, ldb, n0, N, (kt + 1) * BK, K);
         }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
-            float a[2], b[2];
+            float a[NT], b[NT];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = as[(kk + fk) * kStride + wm * 64 + i * 32 + fr];
+            for (int i = 0; i < NT; ++i) a[i] = as[(kk + fk) * kStride + wm * WT + i * 32 + fr];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = bs[(kk + fk) * kStride + wn * 64 + j * 32 + fr];
+            for (int j = 0; j < NT; ++j) b[j] = bs[(kk + fk) * kStride + wn * WT + j * 32 + fr];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NT; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < NT; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (more) {
             float* nxt = lds[(kt + 1) & 1];
-            store_step<A_KC>(va, nxt);
-            store_step<B_KC>(vb, nxt + kStage);
+            store_step<TILE, A_KC>(va, nxt);
+            store_step<TILE, B_KC>(vb, nxt + kStage);
         }
         __syncthreads();
     }
@@ -145,14 +150,14 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     const int col_l = lane & 31;
     const int row_l = 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NT; ++i) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const int row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + row_l + (e & 3);
+            const int row = m0 + wm * WT + i * 32 + 8 * (e >> 2) + row_l + (e & 3);
             if (row >= M) continue;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = n0 + wn * 64 + j * 32 + col_l;
+            for (int j = 0; j < NT; ++j) {
+                const int col = n0 + wn * WT + j * 32 + col_l;
                 if (col >= N) continue;
                 float* p = C + static_cast<int64_t>(row) * ldc + col;
                 const float v = acc[i][j][e];
@@ -193,20 +198,34 @@ extern "C" int agk_gemm_f32(const float* A, int64_t lda, int a_trans, const floa
                            ldc, n);
         return agk::check_launch();
     }
-    const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    // 128 x 128 tiles, or 64 x 64 when the 128-tiles would not fill the CUs
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const bool small = ((M + 127) / 128) * ((N + 127) / 128) < cus;
+    const int tile = small ? 64 : 128;
+    const int64_t tiles_m = (M + tile - 1) / tile, tiles_n = (N + tile - 1) / tile;
     if (tiles_m * tiles_n > kMax) return AGK_EINVAL;
     const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n)), block(kThreads);
     const int acc = accumulate != 0;
     const int tn = static_cast<int>(tiles_n);
     // A k-contiguous unless given transposed; B k-contiguous only when given as B^T
     const bool a_kc = a_trans == 0, b_kc = b_trans != 0;
-#define AGK_F32(AK, BKC)                                                                      \
-    hipLaunchKernelGGL((gemm_f32_kernel<AK, BKC>), grid, block, 0, st, A, lda, B, ldb, C, ldc, m, \
-                       n, k, acc, tn)
-    if (a_kc && b_kc) AGK_F32(true, true);
-    else if (a_kc) AGK_F32(true, false);
-    else if (b_kc) AGK_F32(false, true);
-    else AGK_F32(false, false);
+#define AGK_F32(T, AK, BKC)                                                                     \
+    hipLaunchKernelGGL((gemm_f32_kernel<T, AK, BKC>), grid, block, 0, st, A, lda, B, ldb, C, ldc, \
+                       m, n, k, acc, tn)
+#define AGK_F32_LAYOUTS(T)                  \
+    if (a_kc && b_kc) AGK_F32(T, true, true);   \
+    else if (a_kc) AGK_F32(T, true, false);     \
+    else if (b_kc) AGK_F32(T, false, true);     \
+    else AGK_F32(T, false, false);
+    if (small) {
+        AGK_F32_LAYOUTS(64)
+    } else {
+        AGK_F32_LAYOUTS(128)
+    }
+#undef AGK_F32_LAYOUTS
 #undef AGK_F32
     return agk::check_launch();
 }

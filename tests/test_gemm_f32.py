@@ -20,8 +20,10 @@ from gpu_util import to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 OK, EINVAL = 0, 1  # agk_status
+# below the CU count in 128-tiles: the 64 x 64 tile; from (2048, 2048, 40) on
+# (256 and 289 128-tiles): the 128 x 128 tile, the second with edge tiles
 SHAPES = [(1, 1, 1), (7, 5, 3), (64, 48, 33), (129, 257, 95), (300, 17, 1000), (1000, 520, 64),
-          (256, 384, 513), (2048, 1024, 160)]
+          (256, 384, 513), (2048, 1024, 160), (2048, 2048, 40), (2100, 2060, 33)]
 
 
 def _bound(a, b, K):
