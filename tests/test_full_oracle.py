@@ -6,7 +6,8 @@ OpenMP build, 16 threads) runs the reference's op sequence over all rows; its
 y, inv_rms, dx and dgamma come back to the device, where the errors are taken
 in fp64 over every row, a block of rows at a time, with the criteria of
 `tolerances` (per-row relative for y, dx against the magnitude of its two
-terms, max-relative for inv_rms and dgamma).
+terms, max-relative for inv_rms and dgamma, and each dgamma column against
+the sum of its terms' magnitudes).
 """
 import os
 
@@ -79,12 +80,17 @@ def test_every_row_against_the_oracle(cuda, name):
 
     tol = TOL_BF16 if cfg.dtype == "bf16" else TOL_F32
     e = {"y": 0.0, "dx": 0.0}
+    absum = torch.zeros(D, dtype=torch.float64, device=cuda)  # sum_i |dy x r| per column
     for r0 in range(0, R, BLOCK):
         s = slice(r0, min(R, r0 + BLOCK))
         e["y"] = max(e["y"], _row_err(y[s], ry[s]))
         e["dx"] = max(e["dx"], _dx_err(dx[s], rdx[s], x[s], g, dy[s], cfg.eps))
+        absum += (dy[s].double() * x[s].double() * rinv[s].double().view(-1, 1)).abs().sum(0)
     e["inv_rms"] = _vec_err(inv, rinv)
     e["dgamma"] = _vec_err(dg, rdg)
+    # element-wise: each column against the magnitude of the terms it sums
+    num = (dg.double() - rdg.double()).abs()
+    e["dgamma_elem"] = float(torch.where(absum > 0, num / absum.clamp_min(1e-300), num).max())
     print(f"[{name}] all {R} rows: " + " ".join(f"{k}={v:.2e}" for k, v in e.items()),
           flush=True)
     for k, v in e.items():
