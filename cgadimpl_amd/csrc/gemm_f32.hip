@@ -19,8 +19,9 @@
 // Operands.  Each operand is staged as a logical [rows][K] matrix (A: M rows,
 // B: N rows) into LDS laid out [k][row], whatever its memory layout:
 //  - k contiguous in memory (A as [M][K], B given as B^T [N][K]): lane t loads
-//    k = t % 16 of rows t / 16 + 16 i, so 16 neighbouring lanes read 64
-//    contiguous bytes;
+//    k (t % 4) * 4 .. + 3 of rows t / 4 + 64 i as one 16-byte access when the
+//    rows are 16-byte aligned, else k = t % 16 of rows t / 16 + 16 i (16
+//    neighbouring lanes read 64 contiguous bytes either way);
 //  - rows contiguous (A given as A^T [K][M], B as [K][N]): lane t loads row
 //    t % 128 of k = t / 128 + 2 i, 128 neighbouring lanes 512 bytes.
 // Elements outside the matrix are staged as zeros, so edge tiles need no
@@ -57,11 +58,35 @@ constexpr int kStage = BK * kStride;      // floats per operand per stage
 // One operand's values for one k-step: element (row r0 + row, k0 + k) of the
 // logical [rows][K] matrix, at p[row * ld + k] (KC) or p[k * ld + row] (!KC);
 // TILE * BK / 256 values per lane.
-template <int TILE, bool KC>
+// KC with VEC (16-byte aligned rows, ld a multiple of 4): lane t loads the
+// four k (t % 4) * 4 .. + 3 of rows t / 4 + 64 i as one 16-byte access (a
+// group of four k past K element by element).
+template <int TILE, bool KC, bool VEC>
 __device__ __forceinline__ void load_step(float (&v)[TILE * BK / kThreads],
                                           const float* __restrict__ p, int64_t ld, int r0,
                                           int rows, int k0, int K) {
     const int t = threadIdx.x;
+    if constexpr (KC && VEC) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int i = 0; i < TILE * BK / kThreads / 4; ++i) {
+            const int row = t / 4 + (kThreads / 4) * i;
+            const int gr = r0 + row, gk = k0 + (t % 4) * 4;
+            f32x4 q = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (gr < rows) {
+                const float* a = p + static_cast<int64_t>(gr) * ld + gk;
+                if (gk + 3 < K) {
+                    q = *reinterpret_cast<const f32x4*>(a);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) q[e] = gk + e < K ? a[e] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * i + e] = q[e];
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TILE * BK / kThreads; ++i) {
         const int row = KC ? t / BK + (kThreads / BK) * i : t % TILE;
@@ -73,9 +98,17 @@ __device__ __forceinline__ void load_step(float (&v)[TILE * BK / kThreads],
     }
 }
 
-template <int TILE, bool KC>
+template <int TILE, bool KC, bool VEC>
 __device__ __forceinline__ void store_step(const float (&v)[TILE * BK / kThreads], float* lds) {
     const int t = threadIdx.x;
+    if constexpr (KC && VEC) {
+#pragma unroll
+        for (int i = 0; i < TILE * BK / kThreads / 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                lds[((t % 4) * 4 + e) * kStride + t / 4 + (kThreads / 4) * i] = v[4 * i + e];
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TILE * BK / kThreads; ++i) {
         const int row = KC ? t / BK + (kThreads / BK) * i : t % TILE;
@@ -86,7 +119,7 @@ __device__ __forceinline__ void store_step(const float (&v)[TILE * BK / kThreads
 
 // A_KC: A is [M][lda] (k contiguous), else A^T [K][lda]; B_KC: B is given as
 // B^T [N][ldb] (k contiguous), else B [K][ldb].
-template <int TILE, bool A_KC, bool B_KC>
+template <int TILE, bool A_KC, bool B_KC, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, int M, int N, int K, int accumulate, int tiles_n) {
@@ -110,10 +143,10 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 
     float va[TILE * BK / kThreads], vb[TILE * BK / kThreads];
     const int nk = (K + BK - 1) / BK;
-    load_step<TILE, A_KC>(va, A, lda, m0, M, 0, K);
-    load_step<TILE, B_KC>(vb, B, ldb, n0, N, 0, K);
-    store_step<TILE, A_KC>(va, lds[0]);
-    store_step<TILE, B_KC>(vb, lds[0] + kStage);
+    load_step<TILE, A_KC, VEC>(va, A, lda, m0, M, 0, K);
+    load_step<TILE, B_KC, VEC>(vb, B, ldb, n0, N, 0, K);
+    store_step<TILE, A_KC, VEC>(va, lds[0]);
+    store_step<TILE, B_KC, VEC>(vb, lds[0] + kStage);
     __syncthreads();
 
     const int fr = lane & 31;  // operand row / column within a 32-block
@@ -123,8 +156,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
         const float* bs = as + kStage;
         const bool more = kt + 1 < nk;
         if (more) {
-            load_step<TILE, A_KC>(va, A, lda, m0, M, (kt + 1) * BK, K);
-            load_step<TILE, B_KC>(vb, B, ldb, n0, N, (kt + 1) * BK, K);
+            load_step<TILE, A_KC, VEC>(va, A, lda, m0, M, (kt + 1) * BK, K);
+            load_step<TILE, B_KC, VEC>(vb, B, ldb, n0, N, (kt + 1) * BK, K);
         }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
@@ -141,8 +174,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
         }
         if (more) {
             float* nxt = lds[(kt + 1) & 1];
-            store_step<TILE, A_KC>(va, nxt);
-            store_step<TILE, B_KC>(vb, nxt + kStage);
+            store_step<TILE, A_KC, VEC>(va, nxt);
+            store_step<TILE, B_KC, VEC>(vb, nxt + kStage);
         }
         __syncthreads();
     }
@@ -212,9 +245,20 @@ extern "C" int agk_gemm_f32(const float* A, int64_t lda, int a_trans, const floa
     const int tn = static_cast<int>(tiles_n);
     // A k-contiguous unless given transposed; B k-contiguous only when given as B^T
     const bool a_kc = a_trans == 0, b_kc = b_trans != 0;
-#define AGK_F32(T, AK, BKC)                                                                     \
-    hipLaunchKernelGGL((gemm_f32_kernel<T, AK, BKC>), grid, block, 0, st, A, lda, B, ldb, C, ldc, \
-                       m, n, k, acc, tn)
+    // 16-byte loads of the k-contiguous operands when their rows allow it
+    auto vec_ok = [](const float* p, int64_t ld) {
+        return (reinterpret_cast<uintptr_t>(p) & 15u) == 0 && ld % 4 == 0;
+    };
+    const bool vec = (!a_kc || vec_ok(A, lda)) && (!b_kc || vec_ok(B, ldb));
+#define AGK_F32(T, AK, BKC)                                                                   \
+    do {                                                                                      \
+        if (vec)                                                                              \
+            hipLaunchKernelGGL((gemm_f32_kernel<T, AK, BKC, true>), grid, block, 0, st, A, lda, \
+                               B, ldb, C, ldc, m, n, k, acc, tn);                             \
+        else                                                                                  \
+            hipLaunchKernelGGL((gemm_f32_kernel<T, AK, BKC, false>), grid, block, 0, st, A,     \
+                               lda, B, ldb, C, ldc, m, n, k, acc, tn);                        \
+    } while (0)
 #define AGK_F32_LAYOUTS(T)                  \
     if (a_kc && b_kc) AGK_F32(T, true, true);   \
     else if (a_kc) AGK_F32(T, true, false);     \

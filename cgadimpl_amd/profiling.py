@@ -24,6 +24,8 @@ Usage:
   python -m cgadimpl_amd.profiling mfma <run_counter_collection.csv> <out.md> "<command>"
   python -m cgadimpl_amd.profiling bench <bench output (JSON lines)> <out.md> "<command>"
   python -m cgadimpl_amd.profiling probe <bench --stream-probe output> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling mfma-probe <bench --mfma-probe output> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling gemm-f32 <bench --gemm-f32 output> <out.md> "<command>"
   python -m cgadimpl_amd.profiling wide <bench --wide output> <out.md> "<command>"
   python -m cgadimpl_amd.profiling traffic <fetch_dir> <write_dir> <copy_fetch_dir>
         <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
@@ -428,6 +430,50 @@ def write_probe_summary(jsonl, out_md, command):
         fh.write("\n".join(lines) + "\n")
 
 
+def write_mfma_probe_summary(jsonl, out_md, command):
+    """Table of bench.py --mfma-probe lines: what the matrix cores sustain with
+    the bf16 GEMM's inner loop (no global loads, no barriers), by operand
+    content, with the shader clock the loop ran at."""
+    recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"mfma_probe"')]
+    lines = ["# MFMA probe: the bf16 GEMM's inner loop without loads (bench.py --mfma-probe)", "",
+             "Command:", "", "```", command, "```", "",
+             "256 workgroups of 4 waves (one wave per SIMD, as `gemm_nt_direct_kernel`), each "
+             "wave 16 `v_mfma_f32_32x32x16_bf16` accumulators (a 128 x 128 block), "
+             f"{recs[0]['k_steps_per_wave'] if recs else '?'} 64-deep k-steps per wave. "
+             "'lds': every substep's 8 fragments read from a 64 KiB LDS tile one substep "
+             "ahead (the GEMM's LDS traffic and schedule); 'registers': MFMAs only. "
+             "TFLOP/s from HIP events; the shader clock and cycles per k-step from "
+             "s_memtime / s_memrealtime (100 MHz) read by wave 0 of each workgroup around "
+             "its loop (medians over workgroups). A k-step is 64 MFMAs: 2048 cycles at the "
+             "full issue rate. Dense bf16 peak: 2500 TFLOP/s at 2.4 GHz.", "",
+             "| mode | operand data | TFLOP/s | % of dense peak | shader GHz | cycles per k-step |",
+             "|---|---|---|---|---|---|"]
+    for r in recs:
+        lines.append(f"| {r['mfma_probe']} | {r['data']} | {r['tflops']} | "
+                     f"{r['pct_of_dense_peak']} | {r['shader_ghz']} | {r['cycles_per_k_step']} |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
+def write_gemm_f32_summary(jsonl, out_md, command):
+    """Table of bench.py --gemm-f32 lines: agk_gemm_f32 against torch's fp32
+    matmul in the four operand layouts."""
+    recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"gemm_f32"')]
+    lays = ("AB", "ABt", "AtB", "AtBt")
+    lines = ["# fp32 GEMM (agk_gemm_f32, bench.py --gemm-f32)", "", "Command:", "", "```",
+             command, "```", "",
+             "TFLOP/s from HIP events on the launch stream (warm-up calls first), "
+             "agk_gemm_f32 / torch.matmul in fp32 on the same operands. Layouts: A [M, K] or "
+             "At = A given as [K, M]; B [K, N] or Bt = B given as [N, K]. fp32 matrix peak "
+             "157.3 TFLOP/s.", "",
+             "| M x N x K | " + " | ".join(lays) + " |", "|---|" + "---|" * len(lays)]
+    for r in recs:
+        lines.append(f"| {r['gemm_f32']} | " + " | ".join(
+            f"{r['tflops'][k]} / {r['torch_tflops'][k]}" for k in lays) + " |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
 def write_wide_summary(jsonl, out_md, command):
     """Table of bench.py --wide lines: the split paths against the
     one-workgroup-per-row kernels per shape (graph-replayed us and GB/s)."""
@@ -490,6 +536,10 @@ def main(argv):
         write_trace_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "probe":
         write_probe_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 4 and argv[0] == "mfma-probe":
+        write_mfma_probe_summary(argv[1], argv[2], argv[3])
+    elif len(argv) >= 4 and argv[0] == "gemm-f32":
+        write_gemm_f32_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "bench":
         write_bench_summary(argv[1], argv[2], argv[3])
     elif len(argv) >= 4 and argv[0] == "mfma":
