@@ -437,13 +437,15 @@ def run(cfg_name, steps, warmup, cpu_seconds):
 
     for i in range(warmup):
         step(i)
+    # the GPU's clocks and power, read while the warm-up steps still run (so the
+    # GPU does not idle between the warm-up and the timed region)
+    state_before = gpu_state()
     torch.cuda.synchronize()
 
     # The timed region: K steps, two events per step around the backward (the
     # roofline kernel), recorded on the stream the kernels run on.
     events = [[TimingEvent() for _ in range(2)] for _ in range(steps)]
     torch.cuda.synchronize()
-    state_before = gpu_state()
     t0 = time.perf_counter()
     for i in range(steps):
         step(i, ev_bwd=events[i])
@@ -531,7 +533,9 @@ def run(cfg_name, steps, warmup, cpu_seconds):
             "bwd": {"avg_ms": round(bwd_ms, 5), "median_ms": round(bwd_each[steps // 2], 5),
                     "alg_bytes": cfg.bwd_bytes(),
                     "gbs": round(bwd_gbs, 2), "frac": round(bwd_gbs / HBM_PEAK_GBS, 4)},
-            "gpu_state": {"before_timed": state_before, "after_timed": state_after},
+            "gpu_state": {"before_timed": state_before, "after_timed": state_after,
+                          "how": "sysfs (hwmon, pp_dpm) of this GPU, read during the last "
+                                 "warm-up steps and right after the timed region"},
         },
         "graph": {
             "how": (f"the {steps} steps (then {steps} forwards, then {steps} backwards) "
@@ -658,9 +662,9 @@ def run_c5(steps, warmup, cpu=True):
 
     for _ in range(warmup):
         step()
+    state_before = gpu_state()  # read while the warm-up steps still run
     torch.cuda.synchronize()
     events = [[TimingEvent() for _ in range(len(stages) + 1)] for _ in range(steps)]
-    state_before = gpu_state()
     t0 = time.perf_counter()
     for i in range(steps):
         step(events[i])
