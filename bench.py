@@ -1107,15 +1107,17 @@ WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
 
 
 def run_wide(steps):
-    """Rows wider than the register-resident kernels: the split paths against
+    """Rows wider than the register-resident kernels: the wide paths against
     the one-workgroup-per-row kernels on the same build, each call captured
     `steps` times into a HIP graph and replayed (GPU time per call).
 
     forward: out of place (split when the row is too wide for registers)
-    against in place (y = x, which keeps one workgroup per row); dx alone: with a workspace
-    (split) against without one (looped); and the full backward (dx and
-    dgamma, split).  One JSON line per shape; GB/s are algorithmic bytes
-    (forward 2 tensors, backward 3) over the time.
+    against in place (y = x, which keeps one workgroup per row); backward (dx
+    and dgamma) and dx alone as the library takes them with a workspace (the
+    one-pass or team kernel where they apply), the same with the team kernel
+    switched off (the split path), and dx alone without a workspace
+    (looped).  One JSON line per shape; GB/s are algorithmic bytes (forward 2
+    tensors, backward 3) over the time.
     """
     import torch
 
@@ -1150,17 +1152,25 @@ def run_wide(steps):
                     raise agk.AgkError(rc, "agk_rmsnorm_bwd")
             return body
         n = max(1, steps)
+
+        def bwd_full(i, st):
+            agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=st)
         t = {
             "fwd_split": graph_replay_ms(
                 lambda i, st: agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, stream=st), n),
             "fwd_in_place": graph_replay_ms(
                 lambda i, st: agk.rmsnorm_fwd(xin, g, 1e-6, y=xin, inv_rms=inv, stream=st), n),
-            "bwd_split": graph_replay_ms(
-                lambda i, st: agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws,
-                                              stream=st), n),
-            "bwd_dx_split": graph_replay_ms(dx_only(ws), n),
-            "bwd_dx_looped": graph_replay_ms(dx_only(None), n),
+            "bwd": graph_replay_ms(bwd_full, n),
+            "bwd_dx": graph_replay_ms(dx_only(ws), n),
         }
+        # the same calls with the team kernel switched off (the split path)
+        prev = agk.set_team_backward(0)
+        try:
+            t["bwd_split"] = graph_replay_ms(bwd_full, n)
+            t["bwd_dx_split"] = graph_replay_ms(dx_only(ws), n)
+        finally:
+            agk.set_team_backward(prev)
+        t["bwd_dx_looped"] = graph_replay_ms(dx_only(None), n)
         es = x.element_size()
         fb, bb = 2.0 * rows * cols * es, 3.0 * rows * cols * es
         fp, bp = agk.launch_plan(rows, cols, dt, False), agk.launch_plan(rows, cols, dt, True)

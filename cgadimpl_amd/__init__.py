@@ -19,7 +19,8 @@ __all__ = [
     "layernorm_bwd", "softmax_fwd", "softmax_bwd", "logsumexp_fwd", "logsumexp_bwd",
     "logsumexp_jvp", "logsumexp_fwd_keep", "logsumexp_bwd_from_value", "rms_mul_bwd", "sum_rows", "linear_bf16",
     "mul_bcast_shape", "mul_bcast_fwd", "mul_bcast_bwd",
-    "mul_bcast_grad_dtype", "gemm_f32", "AGK_F32", "AGK_BF16", "STATUS",
+    "mul_bcast_grad_dtype", "gemm_f32", "set_exchange_wait_limit", "set_team_backward",
+    "AGK_F32", "AGK_BF16", "STATUS",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -70,6 +71,8 @@ SIGNATURES = {
                                                         ctypes.c_int]),
     "agk_transpose_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),
     "agk_rmsnorm_launch_plan": (ctypes.c_int, [_I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
+    "agk_set_exchange_wait_limit": (ctypes.c_int, [ctypes.c_int]),
+    "agk_set_team_backward": (ctypes.c_int, [ctypes.c_int]),
     "agk_rmsnorm_jvp": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_layernorm_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_float, ctypes.c_int,
                                          _P]),
@@ -308,11 +311,27 @@ def launch_plan(rows: int, cols: int, dtype: int, backward: bool) -> dict:
 
     tpr == 0 with nv > 0 is the split path: nv segments and g chunks per
     row, rpb rows per backward tile, nblk dgamma partial rows (0: the tiles
-    write dgamma directly)."""
+    write dgamma directly).  g == 0 with tpr > 0 (backward) is the team
+    kernel: a row over tpr / 256 workgroups of nv slots per lane, nblk teams
+    (= dgamma partial rows) taking the rows in turn."""
     out = (ctypes.c_int32 * 5)()
     _check(lib().agk_rmsnorm_launch_plan(rows, cols, dtype, int(bool(backward)), out),
            "agk_rmsnorm_launch_plan")
     return {"tpr": out[0], "nv": out[1], "g": out[2], "rpb": out[3], "nblk": out[4]}
+
+
+def set_exchange_wait_limit(polls: int) -> int:
+    """Polls of the team kernel's wait before it recomputes a missing partial
+    sum itself (testing knob; the results do not change).  Negative: read
+    only.  Returns the previous value."""
+    return int(lib().agk_set_exchange_wait_limit(int(polls)))
+
+
+def set_team_backward(enabled: int) -> int:
+    """1 (default): the wide RMSNorm backward may take the team kernel; 0: the
+    split path instead (measurement and testing knob).  Negative: read only.
+    Returns the previous value."""
+    return int(lib().agk_set_team_backward(int(enabled)))
 
 
 def mul_rowbcast_fwd(a, b, y=None, stream=None):

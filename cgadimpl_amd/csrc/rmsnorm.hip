@@ -36,6 +36,7 @@
 
 #include <stdint.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -1446,6 +1447,14 @@ inline int zero_fill(float* p, int64_t n, hipStream_t st) {
     return check_launch();
 }
 
+// Polls of a team's wait before a missing segment sum is recomputed
+// (agk_set_exchange_wait_limit).
+std::atomic<int> g_team_wait_polls{kTeamWaitPolls};
+int team_wait_polls() { return g_team_wait_polls.load(std::memory_order_relaxed); }
+// Whether the team kernel may be taken (agk_set_team_backward).
+std::atomic<int> g_team_enabled{1};
+inline bool team_enabled() { return g_team_enabled.load(std::memory_order_relaxed) != 0; }
+
 // Bytes of dgamma partial rows the backward writes for these pointers and
 // sizes (the path launch_bwd takes): none for the few-rows kernel, 256 rows
 // for the resident kernel, the looped kernel's row blocks otherwise.
@@ -1488,22 +1497,46 @@ inline size_t bwd_res_wide_bytes(int64_t rows, int cols, bool comp) {
     return static_cast<size_t>(nblk) * static_cast<size_t>(cols) * 4u;
 }
 
+// Whether the team kernel (one pass, a row over several workgroups) takes
+// these arguments.
+template <class S>
+inline bool bwd_team_possible(const void* x, const void* gamma, const void* dy, const void* dx,
+                              int64_t rows, int cols) {
+    int64_t nblk = 0, rpb = 0;
+    const Plan p = bwd_plan_for<S>(x, gamma, dy, dx, rows, cols, nblk, rpb);
+    return team_enabled() && team_eligible<S>(x, gamma, dy, dx, rows, cols, p.tpr != 0);
+}
+
+// The workspace the wide paths need: the dgamma partial rows only when dgamma
+// is wanted (the team path takes the split path's regions).
+inline bool wide_ws_ok(int64_t rows, int cols, const void* ws, size_t ws_bytes,
+                       bool want_dgamma) {
+    const size_t need =
+        want_dgamma ? wide_ws_bytes(rows, cols, false) : wide_ws_stats_bytes(rows, cols);
+    return ws && aligned16(ws) && ws_bytes >= need;
+}
+inline bool bwd_takes_team(const void* x, const void* gamma, const void* dy, const void* dx,
+                           int64_t rows, int cols, int dtype, const void* ws, size_t ws_bytes,
+                           bool want_dgamma) {
+    if (!wide_ws_ok(rows, cols, ws, ws_bytes, want_dgamma)) return false;
+    return dtype == AGK_F32 ? bwd_team_possible<F32>(x, gamma, dy, dx, rows, cols)
+                            : bwd_team_possible<BF16>(x, gamma, dy, dx, rows, cols);
+}
+
 // The workspace must hold the dgamma partial rows only when dgamma is wanted.
 inline bool bwd_takes_wide(const void* x, const void* gamma, const void* dy, const void* dx,
                            int64_t rows, int cols, int dtype, const void* ws, size_t ws_bytes,
                            bool want_dgamma) {
-    const size_t need =
-        want_dgamma ? wide_ws_bytes(rows, cols, false) : wide_ws_stats_bytes(rows, cols);
-    if (!ws || !aligned16(ws) || ws_bytes < need) return false;
+    if (!wide_ws_ok(rows, cols, ws, ws_bytes, want_dgamma)) return false;
     return dtype == AGK_F32 ? bwd_wide_possible<F32>(x, gamma, dy, dx, rows, cols)
                             : bwd_wide_possible<BF16>(x, gamma, dy, dx, rows, cols);
 }
 
 // The RMSNorm backward with validated arguments.  Rows too wide for the
-// resident shapes take the wide path when `ws` (16-byte aligned, ws_bytes
-// long) holds wide_ws_bytes(rows, cols, false) (wide_ws_stats_bytes when
-// dgamma is NULL); otherwise dgamma partials go
-// to `partials` (which must hold bwd_partials_bytes when dgamma != NULL).
+// resident shapes take the team kernel (up to 1M columns) or the split path
+// when `ws` (16-byte aligned, ws_bytes long) holds wide_ws_bytes(rows, cols,
+// false) (wide_ws_stats_bytes when dgamma is NULL); otherwise dgamma partials
+// go to `partials` (which must hold bwd_partials_bytes when dgamma != NULL).
 inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rms,
                            const void* dy, void* dx, float* dgamma, float* partials, void* ws,
                            size_t ws_bytes, int64_t rows, int cols, int dtype, int acc_dx,
@@ -1514,6 +1547,12 @@ inline int rmsnorm_bwd_run(const void* x, const void* gamma, const float* inv_rm
                                               rows, cols, acc_dx, acc_dg, st)
                    : launch_wide_res_bwd<BF16>(x, gamma, inv_rms, dy, dx, nullptr, partials,
                                                dgamma, rows, cols, acc_dx, acc_dg, st);
+    if (bwd_takes_team(x, gamma, dy, dx, rows, cols, dtype, ws, ws_bytes, dgamma != nullptr))
+        return dtype == AGK_F32
+                   ? launch_wide_team_bwd<F32>(x, gamma, inv_rms, dy, dx, dgamma, ws, rows, cols,
+                                               acc_dx, acc_dg, st)
+                   : launch_wide_team_bwd<BF16>(x, gamma, inv_rms, dy, dx, dgamma, ws, rows,
+                                                cols, acc_dx, acc_dg, st);
     if (bwd_takes_wide(x, gamma, dy, dx, rows, cols, dtype, ws, ws_bytes, dgamma != nullptr))
         return dtype == AGK_F32
                    ? launch_wide_bwd<F32>(x, gamma, inv_rms, dy, dx, nullptr, dgamma, ws, rows,
@@ -1887,6 +1926,18 @@ int agk_sum_rows(const void* x, float* out, void* workspace, size_t workspace_by
     return launch_finalize(partials, out, nblk, c, accumulate, st);
 }
 
+int agk_set_exchange_wait_limit(int polls) {
+    const int prev = agk::g_team_wait_polls.load(std::memory_order_relaxed);
+    if (polls >= 0) agk::g_team_wait_polls.store(polls, std::memory_order_relaxed);
+    return prev;
+}
+
+int agk_set_team_backward(int enabled) {
+    const int prev = agk::g_team_enabled.load(std::memory_order_relaxed);
+    if (enabled >= 0) agk::g_team_enabled.store(enabled != 0 ? 1 : 0, std::memory_order_relaxed);
+    return prev;
+}
+
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan) {
     using namespace agk;
@@ -1926,6 +1977,24 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
             plan[2] = 1;
             plan[3] = static_cast<int32_t>((rows + wb - 1) / wb);
             plan[4] = static_cast<int32_t>(wb);
+            return AGK_OK;
+        }
+    }
+    if (p.tpr == 0 && backward && cols > 0 && cols <= 0x7fffffffLL) {
+        // the team kernel: a row over `parts` workgroups of 256 lanes
+        const void* a = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+        const int c = static_cast<int>(cols);
+        const bool team = team_enabled() &&
+                          (dtype == AGK_F32 ? team_eligible<F32>(a, a, a, a, rows, c, false)
+                                            : team_eligible<BF16>(a, a, a, a, rows, c, false));
+        if (team) {
+            const int segs = team_segs_for(dtype);
+            const TeamPlan tp = team_plan(rows, c, segs);
+            plan[0] = static_cast<int32_t>(tp.parts * kWideLanes);
+            plan[1] = segs * kWideSegCols / (w * kWideLanes);
+            plan[2] = 0;
+            plan[3] = static_cast<int32_t>((rows + tp.teams - 1) / tp.teams);
+            plan[4] = static_cast<int32_t>(tp.teams);
             return AGK_OK;
         }
     }

@@ -87,10 +87,13 @@ inline void wide_blocking(int64_t rows, int cols, bool comp, int64_t& rb, int64_
     }
 }
 
-// Workspace layout of the wide backward: [segment partials: rows x nseg fp32]
-// [coefficients: rows fp32] [dgamma partial rows: prows x cols fp32], each
-// region 256-byte aligned.  The row statistics come first, so a dx-only call
-// needs only the bytes before the partial rows (wide_ws_stats_bytes).
+// Workspace layout of the wide backward: [segment sums: rows x nseg 8-byte
+// slots] [coefficients: rows fp32] [dgamma partial rows: prows x cols fp32],
+// each region 256-byte aligned.  The split path keeps each segment's fp32 sum
+// in the low 4 bytes of its slot's place (float index row*nseg + seg of the
+// region); the team path (wide_bwd_team) uses the whole 64-bit slot.  The row
+// statistics come first, so a dx-only call needs only the bytes before the
+// partial rows (wide_ws_stats_bytes).
 struct WideWs {
     size_t partials = 0, segs = 0, coefs = 0, total = 0;
 };
@@ -98,7 +101,7 @@ inline WideWs wide_ws_layout(int64_t rows, int cols, int64_t prows) {
     const WidePlan p = wide_plan(rows, cols);
     WideWs w;
     w.segs = 0;
-    w.coefs = round256(static_cast<size_t>(rows) * static_cast<size_t>(p.nseg) * 4u);
+    w.coefs = round256(static_cast<size_t>(rows) * static_cast<size_t>(p.nseg) * 8u);
     w.partials = w.coefs + round256(static_cast<size_t>(rows) * 4u);
     w.total = w.partials + round256(static_cast<size_t>(prows) * static_cast<size_t>(cols) * 4u);
     return w;
@@ -782,5 +785,396 @@ int launch_wide_res_bwd(const void* x, const void* gamma, const float* inv_rms, 
 #undef AGK_RES
     if (int rc = check_launch()) return rc;
     if (dgamma) return launch_finalize(partials, dgamma, nblk, cols, acc_dg, st);
+    return AGK_OK;
+}
+
+// ---- one pass over rows wider than a workgroup holds: teams -----------------------
+// Aligned rows of up to kTeamMaxSegs segments, at least kTeamMinRows of them,
+// that the one-pass kernel above does not take (wider than 32768 columns, or
+// fewer than 256 rows).  A team of P workgroups holds one row at a time in
+// registers: workgroup p of the team owns segments [p*SEGS, (p+1)*SEGS) of
+// kWideSegCols columns (SEGS = team_segs: 1 for fp32, 2 for bf16), with the
+// same slots per lane as wide_row_stats.  Team t takes rows t, t+T, t+2T, ...
+// (T = kTeamWorkgroups / P, at most the split path's row blocks, so the
+// dgamma partial rows fit the same workspace region).  Per row each workgroup
+//   1. sums g*x, g = dy*gamma, over each of its segments exactly as
+//      wide_row_stats does (per lane over its slots in order, then the
+//      wave's DPP tree and the four waves in order);
+//   2. publishes each segment sum in the slot for (row, segment): one 64-bit
+//      word holding a set flag in the high half and the float's bits in the
+//      low half, stored at agent scope, so a reader sees either the cleared
+//      word or the whole value;
+//   3. reads the row's other slots: one wave polls them with agent-scope
+//      loads, at most `wait_polls` times, and a sum still missing after that
+//      is recomputed by the workgroup from x, dy and gamma with the same
+//      arithmetic (the same bits), so the result never depends on which
+//      workgroups are resident at once and every wait ends;
+//   4. adds the segment sums as wide_row_finish does (lane l: segments l,
+//      l+64, l+128, l+192 in turn from +0, then the DPP tree), so
+//      s = (r*r*dot)/cols and every dx element r*(g - x*s) are the split
+//      path's bits;
+//   5. writes dx, while the loads of the team's next row, issued before
+//      step 1, are in flight.
+// Each lane adds its columns' dgamma terms dy*(x*r) in row order; at the end
+// each workgroup writes its columns of partial row t, and dgamma_finalize
+// adds the T partial rows in a fixed order.  The slots are cleared by a fill
+// kernel ahead of the launch, in stream order, so a set flag means "written
+// by this call".  x and dy are read once: the split path's second read
+// disappears.  Without dx nothing is exchanged.
+constexpr int64_t kTeamMaxSegs = 256;  // 1M columns; wider rows take the split path
+constexpr int kTeamWaitPolls = 4096;   // polls before a missing sum is recomputed
+
+constexpr int64_t kTeamMinRows = 4;   // fewer rows take the split path
+// Workgroups a launch aims for: two 256-lane workgroups per CU of a 256-CU
+// MI355X, all resident at once at the kernel's register use.  A constant, so
+// the team count (and with it dgamma's summation order) depends only on the
+// shape, never on the device.
+constexpr int64_t kTeamWorkgroups = 512;
+
+// Segments per workgroup: one for fp32, two for bf16 -- 32 KiB of x and dy
+// per row either way, which the row's exchange is amortised over.  Measured
+// on MI355X (graph-replayed backward, dx and dgamma): bf16 [8192, 131072] in
+// 1189 us with two segments against 1985 us with one (the exchange, not the
+// bytes, bounds a workgroup that moves half as much per row); fp32 keeps one
+// because two would need more than 256 registers per lane.
+template <class S>
+constexpr int team_segs() {
+    return S::kVec == 4 ? 1 : 2;
+}
+inline int team_segs_for(int dtype) { return dtype == AGK_F32 ? 1 : 2; }
+
+struct TeamPlan {
+    int64_t parts = 0;  // workgroups per row (team size)
+    int64_t teams = 0;  // rows in flight = dgamma partial rows
+};
+inline TeamPlan team_plan(int64_t rows, int cols, int segs) {
+    TeamPlan tp;
+    const int64_t part_cols = static_cast<int64_t>(segs) * kWideSegCols;
+    tp.parts = (cols + part_cols - 1) / part_cols;
+    // at most the split path's row blocks (the workspace's partial rows)
+    const int64_t nrb = wide_plan(rows, cols).nrb;
+    const int64_t want = kTeamWorkgroups / tp.parts > 0 ? kTeamWorkgroups / tp.parts : 1;
+    tp.teams = want < nrb ? want : nrb;
+    return tp;
+}
+
+template <class S>
+inline bool team_eligible(const void* x, const void* gamma, const void* dy, const void* dx,
+                          int64_t rows, int cols, bool resident_plan) {
+    const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
+    return wide_bwd_eligible<S>(x, gamma, dy, dx, cols, resident_plan) && nseg <= kTeamMaxSegs &&
+           rows >= kTeamMinRows && !(rows >= kWideResMinRows && cols <= kWideResMaxCols);
+}
+
+__device__ __forceinline__ void slot_publish(uint64_t* p, float v) {
+    const uint64_t w = (static_cast<uint64_t>(1) << 32) | __float_as_uint(v);
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t slot_read(uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class S, bool ACC, int kTeamSegs>
+__global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    const float* __restrict__ inv_rms, const typename S::T* __restrict__ dy,
+    typename S::T* __restrict__ dx, uint64_t* __restrict__ slots, float* __restrict__ partials,
+    int64_t rows, int cols, int nseg, int nparts, int64_t nteams, int wait_polls) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    constexpr int NV = kWideSegCols / (W * kWideLanes);  // slots per lane per segment
+    constexpr int NS = kTeamSegs * NV;
+    constexpr int kWaves = kWideLanes / 64;
+    constexpr int kPerLane = static_cast<int>(kTeamMaxSegs / 64);
+    // one buffer: a wave writes it for the next row only after the barrier
+    // that follows the poll, which every wave reaches after reading it
+    __shared__ float red[kTeamSegs][kWaves];
+    __shared__ float fb[kWaves];
+    __shared__ float vals[kTeamMaxSegs];
+    __shared__ unsigned char missing[kTeamMaxSegs];
+    __shared__ int nmissing;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int64_t team = static_cast<int64_t>(blockIdx.x) / nparts;
+    const int seg0 = (static_cast<int>(static_cast<int64_t>(blockIdx.x) - team * nparts)) * kTeamSegs;
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    const bool want_dx = dx != nullptr, want_dg = partials != nullptr;
+    const float inv_cols = 1.0f / static_cast<float>(cols);
+    // slot q = s*NV + k of lane t: columns (seg0+s)*kWideSegCols + (t + k*256)*W ..
+    uint32_t off[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const int col = (seg0 + q / NV) * kWideSegCols + (t + (q % NV) * kWideLanes) * W;
+        off[q] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+    }
+    const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
+    u32x4 gv[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) gv[q] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+    float dg[NS][W];
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+#pragma unroll
+        for (int e = 0; e < W; ++e) dg[q][e] = 0.0f;
+
+    struct Set {
+        u32x4 xv[NS], dv[NS];
+        float r;
+    };
+    auto issue = [&](Set& b, int64_t row) {
+        const bool live = row < rows;
+        const int64_t e0 = (live ? row : 0) * static_cast<int64_t>(cols);
+        const rsrc_t rx = make_rsrc(x + e0, live ? row_bytes : 0u);
+        const rsrc_t rd = make_rsrc(dy + e0, live ? row_bytes : 0u);
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+            b.xv[q] = bload16_stream(rx, off[q]);
+            b.dv[q] = bload16_stream(rd, off[q]);
+        }
+        b.r = live ? inv_rms[row] : 0.0f;
+    };
+    // segment sg's sum of g*x for `row`, recomputed by the whole workgroup
+    // with wide_row_stats' arithmetic (workgroup-uniform call)
+    auto recompute = [&](int64_t row, int sg) -> float {
+        const int64_t e0 = row * static_cast<int64_t>(cols);
+        const rsrc_t rx = make_rsrc(x + e0, row_bytes);
+        const rsrc_t rd = make_rsrc(dy + e0, row_bytes);
+        u32x4 xv[NV], dv[NV], gk[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = sg * kWideSegCols + (t + k * kWideLanes) * W;
+            const uint32_t o = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+            dv[k] = __builtin_amdgcn_raw_buffer_load_b128(rd, o, 0, 0);
+            gk[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, o, 0, 0);
+        }
+        float part[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) part[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fx[W], fd[W];
+            S::unpack(xv[k], fx);
+            S::unpack(dv[k], fd);
+            if (gamma) {
+                float gm[W];
+                S::unpack(gk[k], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
+        }
+        float v = 0.0f;
+#pragma unroll
+        for (int e = 0; e < W; ++e) v += part[e];
+        v = group_sum<64>(v);
+        if (lane == 0) fb[wave] = v;
+        __syncthreads();
+        float a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) a += fb[w];
+        __syncthreads();
+        return a;
+    };
+
+    // One row: `cur` holds it; the loads of row `ahead` go into `fill` first.
+    auto step = [&](Set& cur, Set& fill, int64_t row, int64_t ahead) {
+        issue(fill, ahead);
+        const float r = cur.r;
+        // 1. per segment: g*x summed as wide_row_stats sums it; the dgamma
+        //    terms (they need r only)
+        float v[kTeamSegs];
+#pragma unroll
+        for (int s = 0; s < kTeamSegs; ++s) {
+            float part[W];
+#pragma unroll
+            for (int e = 0; e < W; ++e) part[e] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const int q = s * NV + k;
+                float fx[W], fd[W];
+                S::unpack(cur.xv[q], fx);
+                S::unpack(cur.dv[q], fd);
+                if (want_dg) {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) dg[q][e] += fd[e] * (fx[e] * r);
+                }
+                if (gamma) {
+                    float gm[W];
+                    S::unpack(gv[q], gm);
+#pragma unroll
+                    for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
+                }
+#pragma unroll
+                for (int e = 0; e < W; ++e) part[e] += fd[e] * fx[e];
+            }
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < W; ++e) a += part[e];
+            v[s] = group_sum<64>(a);
+        }
+        if (!want_dx) return;  // workgroup-uniform
+        if (lane == 0) {
+#pragma unroll
+            for (int s = 0; s < kTeamSegs; ++s) red[s][wave] = v[s];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kTeamSegs; ++s) {
+            float a = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) a += red[s][w];
+            v[s] = a;
+        }
+        // 2.-3. publish this workgroup's sums, gather the row's others
+        uint64_t* rs = slots + row * static_cast<int64_t>(nseg);
+        if (t == 0) {
+#pragma unroll
+            for (int s = 0; s < kTeamSegs; ++s)
+                if (seg0 + s < nseg) slot_publish(rs + seg0 + s, v[s]);
+        }
+        if (wave == 0) {
+            float val[kPerLane];
+            bool have[kPerLane];
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const int sg = lane + 64 * j;
+                const bool own = sg >= seg0 && sg < seg0 + kTeamSegs;
+                have[j] = sg >= nseg || own;
+                val[j] = own ? (sg == seg0 ? v[0] : v[kTeamSegs - 1]) : 0.0f;
+            }
+            for (int it = 0;; ++it) {
+                bool all = true;
+#pragma unroll
+                for (int j = 0; j < kPerLane; ++j) {
+                    if (!have[j]) {
+                        const uint64_t w = slot_read(rs + lane + 64 * j);
+                        if ((w >> 32) != 0) {
+                            have[j] = true;
+                            val[j] = __uint_as_float(static_cast<uint32_t>(w));
+                        } else {
+                            all = false;
+                        }
+                    }
+                }
+                if (__all(all) || it >= wait_polls) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            bool miss = false;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const int sg = lane + 64 * j;
+                if (sg < nseg) {
+                    vals[sg] = val[j];
+                    missing[sg] = have[j] ? 0 : 1;
+                    miss = miss || !have[j];
+                }
+            }
+            const int any_miss = __any(miss);
+            if (lane == 0) nmissing = any_miss;
+        }
+        __syncthreads();
+        if (nmissing != 0) {  // workgroup-uniform: a wait ran out
+            for (int sg = 0; sg < nseg; ++sg) {
+                if (!missing[sg]) continue;  // uniform (LDS)
+                const float a = recompute(row, sg);
+                if (t == 0) vals[sg] = a;
+            }
+            __syncthreads();
+        }
+        // 4. the row's dot as wide_row_finish adds it, then s
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int sg = lane + 64 * j;
+            dot += sg < nseg ? vals[sg] : 0.0f;
+        }
+        dot = group_sum<64>(dot);
+        const float sc = (r * r * dot) * inv_cols;
+        // 5. dx = r*(g - x*s)
+        const rsrc_t rdx = make_rsrc(dx + row * static_cast<int64_t>(cols), row_bytes);
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+            float fx[W], gk[W], o[W];
+            S::unpack(cur.xv[q], fx);
+            S::unpack(cur.dv[q], gk);
+            if (gamma) {
+                float gm[W];
+                S::unpack(gv[q], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) gk[e] = gk[e] * gm[e];
+            }
+#pragma unroll
+            for (int e = 0; e < W; ++e) o[e] = r * (gk[e] - fx[e] * sc);
+            if constexpr (ACC) {
+                float old[W];
+                S::unpack(bload16_stream(rdx, off[q]), old);
+#pragma unroll
+                for (int e = 0; e < W; ++e) o[e] = acc_add(old[e], o[e]);
+            }
+            bstore16_stream(rdx, off[q], S::pack(o));
+        }
+    };
+    // Two register sets in turn, so the loads of the team's next row are in
+    // flight while a row is summed, exchanged and written (unrolled by two,
+    // so no set is copied).  A third set (two rows ahead) measured level.
+    int64_t row = team;
+    Set a, b;
+    issue(a, row);
+    for (;;) {
+        step(a, b, row, row + nteams);
+        if ((row += nteams) >= rows) break;
+        step(b, a, row, row + nteams);
+        if ((row += nteams) >= rows) break;
+    }
+    if (!want_dg) return;
+    float* prow = partials + team * static_cast<int64_t>(cols);
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        if (off[q] == kOffOut) continue;
+        float* p = prow + off[q] / sizeof(T);
+#pragma unroll
+        for (int e = 0; e < W; e += 4)
+            *reinterpret_cast<float4*>(p + e) =
+                make_float4(dg[q][e], dg[q][e + 1], dg[q][e + 2], dg[q][e + 3]);
+    }
+}
+
+inline int zero_fill(float* p, int64_t n, hipStream_t st);
+int team_wait_polls();
+
+// ws: at least wide_ws_bytes(rows, cols, false) bytes (wide_ws_stats_bytes
+// without dgamma), 16-byte aligned (checked by the caller).
+template <class S>
+int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
+                         void* dx, float* dgamma, void* ws, int64_t rows, int cols, int acc_dx,
+                         int acc_dg, hipStream_t st) {
+    using T = typename S::T;
+    constexpr int kSegs = team_segs<S>();
+    const TeamPlan tp = team_plan(rows, cols, kSegs);
+    const WideWs w = wide_ws_layout(rows, cols, tp.teams);
+    const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
+    const int64_t grid = tp.teams * tp.parts;
+    if (grid > 0x7fffffffLL || nseg > kTeamMaxSegs) return AGK_EINVAL;
+    char* base = static_cast<char*>(ws);
+    uint64_t* slots = reinterpret_cast<uint64_t*>(base + w.segs);
+    float* partials = dgamma ? reinterpret_cast<float*>(base + w.partials) : nullptr;
+    if (dx) {
+        if (int rc = zero_fill(reinterpret_cast<float*>(slots), rows * nseg * 2, st)) return rc;
+    }
+    const T* xp = static_cast<const T*>(x);
+    const T* gp = static_cast<const T*>(gamma);
+    const T* dyp = static_cast<const T*>(dy);
+    T* dxp = static_cast<T*>(dx);
+    const int polls = team_wait_polls();
+#define AGK_TEAM(ACC_)                                                                         \
+    hipLaunchKernelGGL((wide_bwd_team<S, ACC_, kSegs>), dim3(static_cast<unsigned>(grid)),     \
+                       dim3(kWideLanes), 0, st, xp, gp, inv_rms, dyp, dxp, slots, partials, rows, \
+                       cols, static_cast<int>(nseg), static_cast<int>(tp.parts), tp.teams, polls)
+    if (acc_dx && dx) AGK_TEAM(true);
+    else AGK_TEAM(false);
+#undef AGK_TEAM
+    if (int rc = check_launch()) return rc;
+    if (dgamma) return launch_finalize(partials, dgamma, tp.teams, cols, acc_dg, st);
     return AGK_OK;
 }

@@ -230,10 +230,12 @@ def _counter_by_launch(run_dir, counter, name_part):
     return vals
 
 
-# The c5 products by grid size (256 lanes per 256 x 256 tile): their
-# algorithmic bytes, A + B read once and C written once.
+# The c5 products by grid size (256 lanes per 256 x 256 tile, or per half tile
+# in the last round; on 256 CUs y's 1376 tiles run as 1280 whole tiles and
+# 2 x 96 halves): their algorithmic bytes, A + B read once and C written once.
 C5_PRODUCTS = {
     32 * 43 * 256: ("y = h W", 8192 * 4096 * 2 + 4096 * 11008 * 2, 8192 * 11008 * 2),
+    (1280 + 2 * 96) * 256: ("y = h W", 8192 * 4096 * 2 + 4096 * 11008 * 2, 8192 * 11008 * 2),
     32 * 16 * 256: ("dh = dy W^T", 8192 * 11008 * 2 + 4096 * 11008 * 2, 8192 * 4096 * 2),
     16 * 43 * 256: ("dW = h^T dy", 8192 * 4096 * 2 + 8192 * 11008 * 2, 4096 * 11008 * 4),
 }
@@ -474,26 +476,46 @@ def write_gemm_f32_summary(jsonl, out_md, command):
         fh.write("\n".join(lines) + "\n")
 
 
+def _wide_bwd_path(plan):
+    """The backward path a launch plan names (agk_rmsnorm_launch_plan)."""
+    if plan["tpr"] > 0 and plan["g"] == 0:
+        return f"team of {plan['tpr'] // 256}"
+    if plan["tpr"] == 1024 and plan["nblk"] == 256:
+        return "one pass"
+    if plan["tpr"] == 0 and plan["nv"] > 0:
+        return "split"
+    return "resident" if plan["tpr"] > 0 else "looped"
+
+
 def write_wide_summary(jsonl, out_md, command):
-    """Table of bench.py --wide lines: the split paths against the
+    """Table of bench.py --wide lines: the wide paths against the
     one-workgroup-per-row kernels per shape (graph-replayed us and GB/s)."""
     recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"wide_rows"')]
     lines = ["# Rows wider than the register-resident kernels (MI355X, one GPU)", "",
              "Command:", "", "```", command, "```", "",
              "Each call captured into a HIP graph and replayed (GPU time per call, best of 5 "
              "replays). Forward: out of place (the split path for rows too wide for "
-             "registers) against in place (y = x keeps one workgroup per row). dx alone: with a workspace (split) "
-             "against without (looped). Backward: dx and dgamma (split). GB/s: algorithmic "
-             "bytes (forward 2 tensors, backward 3) over the time; % of 8 TB/s in brackets.",
+             "registers) against in place (y = x keeps one workgroup per row). Backward "
+             "(dx and dgamma) and dx alone: as the library takes them with a workspace "
+             "('path': the one-pass kernel for rows of up to 32768 columns from 256 rows, "
+             "the team kernel -- a row over that many workgroups exchanging partial sums -- "
+             "for other aligned rows of up to 1M columns), then the same calls with the team "
+             "kernel switched off (the split path: x and dy read twice), and dx alone "
+             "without a workspace (looped). GB/s: algorithmic bytes (forward 2 tensors, "
+             "backward 3) over the time; % of 8 TB/s in brackets.",
              "",
-             "| shape | fwd split us | fwd in place us | bwd dx split us | bwd dx looped us | "
-             "bwd (dx, dgamma) split us | fwd split GB/s | bwd split GB/s |",
-             "|---|---|---|---|---|---|---|---|"]
+             "| shape | bwd path | fwd split us | fwd in place us | bwd us | bwd split us | "
+             "bwd dx us | bwd dx split us | bwd dx looped us | fwd split GB/s | bwd GB/s | "
+             "bwd split GB/s |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|"]
     for r in recs:
         u, g = r["us"], r["gbs"]
-        lines.append(f"| {r['wide_rows']} | {u['fwd_split']} | {u['fwd_in_place']} | "
-                     f"{u['bwd_dx_split']} | {u['bwd_dx_looped']} | {u['bwd_split']} | "
+        lines.append(f"| {r['wide_rows']} | {_wide_bwd_path(r['bwd_plan'])} | "
+                     f"{u['fwd_split']} | {u['fwd_in_place']} | {u['bwd']} | "
+                     f"{u['bwd_split']} | {u['bwd_dx']} | {u['bwd_dx_split']} | "
+                     f"{u['bwd_dx_looped']} | "
                      f"{g['fwd_split']:.0f} ({g['fwd_split'] / 80:.1f} %) | "
+                     f"{g['bwd']:.0f} ({g['bwd'] / 80:.1f} %) | "
                      f"{g['bwd_split']:.0f} ({g['bwd_split'] / 80:.1f} %) |")
     ro = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"wide_rowops"')]
     if ro:

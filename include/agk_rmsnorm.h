@@ -310,6 +310,10 @@ int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_ds
  *   {lanes per row, 16-byte slots per lane, rows per workgroup,
  *    rows per dgamma partial row (backward; ceil(rows / partial rows)),
  *    dgamma partial rows (backward)};
+ * rows per workgroup == 0 (backward) is the team kernel: a row held by
+ * lanes per row / 256 workgroups of 256 lanes that exchange their partial
+ * sums (4096 fp32 or 8192 bf16 columns each), the teams taking the rows in
+ * turn;
  * lanes per row == 0 means a path that does not keep rows in registers:
  * the split path when slots per lane > 0 (then plan[1] = 4096-column
  * segments per row, plan[2] = 2048-column chunks per row, and for the
@@ -319,6 +323,22 @@ int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_ds
  * split).  A resident backward of at most 255 rows reports 0 partial rows:
  * it runs row and column workgroups in one launch and writes dgamma
  * directly.  Used by the tests to run every reachable shape.                 */
+/* Testing knob, with no counterpart in the reference: how many times a
+ * workgroup of the team kernel (the wide backward) polls for the other
+ * workgroups' partial sums of a row before it recomputes a missing one from
+ * x, dy and gamma itself (the same bits; default 4096).  polls >= 0 sets it
+ * for the process; a negative value only reads it.  Returns the previous
+ * value.  0 makes every wait end at its first look, so the tests can run the
+ * recompute path; the results do not change.                                */
+int agk_set_exchange_wait_limit(int polls);
+
+/* Testing and measurement knob, with no counterpart in the reference:
+ * enabled = 0 keeps the wide RMSNorm backward off the team kernel (rows then
+ * take the split path: row statistics, then dx and dgamma tiles, reading x
+ * and dy twice), 1 restores the default; a negative value only reads it.
+ * Process-wide; returns the previous value (1 or 0).                         */
+int agk_set_team_backward(int enabled);
+
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan);
 

@@ -26,7 +26,7 @@ def reachable_plans():
             for direction in ("fwd", "bwd"):
                 for nslot in range(1, MAX_SLOTS + 1):
                     p = agk.launch_plan(rows, nslot * w, dt, direction == "bwd")
-                    if p["tpr"] == 0:
+                    if p["tpr"] == 0 or p["g"] == 0:  # not resident: looped, split or team
                         continue
                     key = (dt, direction, p["tpr"], p["nv"], p["g"])
                     lo, hi = span.get((key, rows), (nslot * w, nslot * w))

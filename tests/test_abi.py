@@ -116,8 +116,8 @@ def _split_blocks(rows, cols):
 
 
 def _split_ws(rows, cols, prows):
-    """Partial rows, segment sums (4096 columns each), coefficients."""
-    return _r256(prows * cols * 4) + _r256(rows * -(-cols // 4096) * 4) + _r256(rows * 4)
+    """Partial rows, segment slots (8 bytes per 4096 columns), coefficients."""
+    return _r256(prows * cols * 4) + _r256(rows * -(-cols // 4096) * 8) + _r256(rows * 4)
 
 
 def test_wide_row_plans_and_workspace():
@@ -125,8 +125,10 @@ def test_wide_row_plans_and_workspace():
     the split path's regions (its own row blocks, and the looped blocking the
     composition uses) as well as the looped kernel's partial rows, the same for
     both dtypes; the plan diagnostic reports the one-pass backward from 256
-    rows of at most 32768 columns, the split paths otherwise (aligned rows),
-    the looped kernels for rows that are not whole 16-byte slots."""
+    rows of at most 32768 columns, the team kernel for other aligned rows of
+    up to 256 segments from 4 rows, the split paths otherwise (and for every
+    wide forward), the looped kernels for rows that are not whole 16-byte
+    slots."""
     lib = agk.lib()
     ws = lib.agk_rmsnorm_bwd_workspace_bytes
     assert agk.AGK_WIDE_MIN_COLS == 16385
@@ -149,6 +151,17 @@ def test_wide_row_plans_and_workspace():
             if rows >= 256 and cols <= 32768:
                 assert (bp["tpr"], bp["nv"], bp["g"]) == (1024, 32768 // (w * 1024), 1), label
                 assert bp["nblk"] == 256 and bp["rpb"] == -(-rows // 256), label
+            elif rows >= 4:
+                # the team kernel: 4096 fp32 / 8192 bf16 columns per workgroup,
+                # one partial row per team, 512 // parts teams (at most the
+                # split path's row blocks)
+                part = 4096 if w == 4 else 8192
+                parts = -(-cols // part)
+                teams = min(max(512 // parts, 1), nrb)
+                assert bp["g"] == 0, label
+                assert bp["tpr"] == 256 * parts, label
+                assert bp["nv"] == part // (w * 256), label
+                assert bp["nblk"] == teams and bp["rpb"] == -(-rows // teams), label
             else:
                 assert bp["tpr"] == 0, label
                 assert (bp["nv"], bp["g"]) == (-(-cols // 4096), -(-cols // 2048)), label

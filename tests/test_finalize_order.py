@@ -1,7 +1,7 @@
 """dgamma's fixed summation order, checked bit for bit from the partial rows.
 
 After a backward call the caller's workspace still holds the fp32 partial
-rows the finalize summed (at its start, or after the split path's row
+rows the finalize summed (at its start, or after the wide paths' row
 statistics), so the host can redo the finalize in float64 in the
 documented order and compare every bit of dgamma:
   more than 64 partial rows: split s (of 64) adds rows s, s+64, s+128, ... in
@@ -10,7 +10,9 @@ documented order and compare every bit of dgamma:
   split then holds at most one row);
 and with accumulation, the fp32 sum old + float(total).  Covers the resident
 kernel (256 partial rows), the looped kernel (unaligned rows: one partial row
-per row block, few and many) and the split path for wide rows (its row blocks).
+per row block, few and many), the one-pass kernel for rows of up to 32768
+columns (256 partial rows) and the team kernel for wider rows (one partial
+row per team).
 """
 import numpy as np
 import pytest
@@ -50,9 +52,10 @@ def _finalize_f64(parts):
     ("f32", 33, 1030),       # looped, 33 partial rows (at most 64), unaligned columns
     ("f32", 300, 1030),      # looped, 300 partial rows
     ("bf16", 70, 1001),      # looped, 70 partial rows
-    ("f32", 8, 262144),      # split path, 8 row blocks
-    ("f32", 300, 65536),     # split path, 64 row blocks (the boundary)
-    ("f32", 1100, 20480),    # split path, 184 row blocks
+    ("f32", 8, 262144),      # team kernel, 8 teams
+    ("f32", 300, 65536),     # team kernel, 64 teams (the boundary)
+    ("bf16", 1030, 65544),   # team kernel, 65 teams
+    ("f32", 1100, 20480),    # one pass, 256 partial rows
     ("f32", 4096, 4096),     # resident, 256 partial rows
 ], ids=str)
 @pytest.mark.parametrize("accumulate", [False, True])
@@ -73,11 +76,12 @@ def test_dgamma_is_the_documented_sum_of_the_partial_rows(cuda, dtype, rows, col
     # torch's allocations are; unaligned columns are what make them looped
     agk.rmsnorm_bwd(x, g, inv, dy, dgamma=dg, workspace=ws, accumulate=accumulate)
     torch.cuda.synchronize()
-    # the split path keeps its row statistics (segment sums, then the
-    # coefficients, each 256-byte aligned) ahead of the partial rows
+    # the split path and the team kernel keep their row statistics (8-byte
+    # segment slots, then the coefficients, each region 256-byte aligned)
+    # ahead of the partial rows
     off = 0
-    if plan["tpr"] == 0 and plan["nv"] > 0:
-        off = _r256(rows * plan["nv"] * 4) + _r256(rows * 4)
+    if (plan["tpr"] == 0 and plan["nv"] > 0) or (plan["tpr"] > 0 and plan["g"] == 0):
+        off = _r256(rows * -(-cols // 4096) * 8) + _r256(rows * 4)
     parts = ws[off: off + nblk * cols * 4].view(torch.float32).view(nblk, cols).cpu().numpy()
     tot = _finalize_f64(parts).astype(np.float32)
     want = (pre.cpu().numpy() + tot).astype(np.float32) if accumulate else tot

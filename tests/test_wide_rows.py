@@ -1,7 +1,10 @@
-"""Rows wider than the register-resident shapes: the split paths (several
-workgroups per row for the row statistics, row-block x column-chunk tiles for
-dx and dgamma) and, from 256 rows of at most 32768 columns, the one-pass
-backward (x and dy in registers, dgamma in LDS).
+"""Rows wider than the register-resident shapes: the split forward (several
+workgroups per row for the row statistics, then row-chunk scaling), and
+three backward paths: from 256 rows of at most 32768 columns the one-pass
+kernel (x and dy in registers, dgamma in LDS); other aligned rows of up to
+1M columns the team kernel (a row over several workgroups that exchange
+their segment sums through the workspace); wider rows the split path (row
+statistics, then row-block x column-chunk tiles for dx and dgamma).
 
 Against the CPU oracle (fp64 accumulation) at sizes it finishes in seconds,
 through the size-independent properties at full sizes, bit-identical across
@@ -78,6 +81,10 @@ def _one_pass(rows, cols):
     return rows >= 256 and cols <= 32768
 
 
+def _team(rows, cols):
+    return not _one_pass(rows, cols) and rows >= 4 and -(-cols // 4096) <= 256
+
+
 @pytest.mark.parametrize("dtype,rows,cols", WIDE_CASES, ids=str)
 def test_wide_parity(cuda, dtype, rows, cols):
     fp = agk.launch_plan(rows, cols, _dt(dtype), False)
@@ -87,6 +94,8 @@ def test_wide_parity(cuda, dtype, rows, cols):
     if _one_pass(rows, cols):
         assert bp["tpr"] == 1024 and bp["nv"] == (8 if dtype == "f32" else 4), \
             "backward should take the one-pass kernel"
+    elif _team(rows, cols):
+        assert bp["tpr"] > 0 and bp["g"] == 0, "backward should take the team kernel"
     else:
         assert bp["tpr"] == 0 and bp["nv"] > 0, "backward should take the split path"
     if fp["tpr"] == 0:
@@ -105,6 +114,71 @@ def test_wide_full_size_properties(cuda, dtype, rows, cols):
     print(label, flush=True)
     x, g, dy = device_inputs((rows, cols), dtype, rows + cols, cuda)
     check_on_device(x, g, dy, 1e-6, label, _compare, sample=16)
+
+
+# Team kernel shapes: many rows (more rows than teams), one row per team,
+# ragged last segment, the widest rows it takes (256 segments), bf16 parts of
+# two segments with an odd segment count.
+TEAM_CASES = [("f32", 300, 65536), ("bf16", 100, 131072), ("f32", 4, 40000),
+              ("bf16", 5, 131080), ("f32", 4, 1 << 20), ("bf16", 70, 36864),
+              ("f32", 9, 16388)]
+
+
+@pytest.mark.parametrize("dtype,rows,cols", TEAM_CASES, ids=str)
+@pytest.mark.parametrize("with_gamma", [True, False], ids=["gamma", "no_gamma"])
+def test_team_against_split_and_recompute(cuda, dtype, rows, cols, with_gamma):
+    """The team kernel against the split path on the same inputs (the team
+    switched off): dx bit-identical, since both add the same 4096-column
+    segment sums in the same order and apply the same per-element formula;
+    dgamma within the oracle's bar of each other (different partial rows: one
+    per team against one per row block).  With every wait cut to its first
+    look (wait limit 0, so the workgroups recompute the sums they do not find
+    yet), dx and dgamma bit-identical to the default: a recomputed sum is the
+    published one.  Both against the oracle."""
+    import torch
+    x, g, dy = configs.make_inputs((rows, cols), dtype=dtype, with_gamma=with_gamma,
+                                   seed=rows * 5 + cols)
+    xd, dyd = to_dev(x, cuda), to_dev(dy, cuda)
+    gd = to_dev(g, cuda) if with_gamma else None
+    _, inv = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    plan = agk.launch_plan(rows, cols, _dt(dtype), True)
+    print(f"team {dtype} {rows}x{cols} gamma={with_gamma} plan {plan}", flush=True)
+    assert plan["tpr"] > 0 and plan["g"] == 0
+    team_dx, team_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    prev = agk.set_team_backward(0)
+    try:
+        split_dx, split_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    finally:
+        agk.set_team_backward(prev)
+    prev = agk.set_exchange_wait_limit(0)
+    try:
+        rec_dx, rec_dg = agk.rmsnorm_bwd(xd, gd, inv, dyd)
+    finally:
+        agk.set_exchange_wait_limit(prev)
+    torch.cuda.synchronize()
+    assert torch.equal(team_dx, split_dx)
+    assert torch.equal(rec_dx, team_dx)
+    assert torch.equal(rec_dg, team_dg)
+    _, rinv = oracle.fwd(x, g if with_gamma else None, 1e-6)
+    rdx, rdg = oracle.bwd(x, g if with_gamma else None, rinv, dy)
+    e_team = vec_rel_err(to_host(team_dg), rdg)
+    e_split = vec_rel_err(to_host(split_dg), rdg)
+    e_dx = dx_rel_err(as_f32(to_host(team_dx)), as_f32(rdx), as_f32(x),
+                      as_f32(g) if with_gamma else None, as_f32(dy), 1e-6)
+    print(f"  dx {e_dx:.2e} dgamma team {e_team:.2e} split {e_split:.2e}", flush=True)
+    assert e_dx <= _tol(x) and e_team <= TOL_F32 and e_split <= TOL_F32
+
+
+def test_team_is_deterministic(cuda):
+    """Three calls of the team kernel on the same inputs: every bit equal."""
+    import torch
+    x, g, dy = device_inputs((700, 65536), "bf16", 77, cuda)
+    _, inv = agk.rmsnorm_fwd(x, g, 1e-6)
+    first = agk.rmsnorm_bwd(x, g, inv, dy)
+    for _ in range(2):
+        again = agk.rmsnorm_bwd(x, g, inv, dy)
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(first, again))
 
 
 def test_wide_no_gamma(cuda):
