@@ -1226,20 +1226,35 @@ def run_wide_rowops(steps):
 
         n = max(1, steps)
         rec = {"wide_rowops": f"{dtype} {rows}x{cols}", "dtype": dtype, "rows": rows,
-               "cols": cols, "calls_per_graph": n, "us": {}, "gbs": {}}
+               "cols": cols, "calls_per_graph": n, "us": {}, "gbs": {},
+               "team": {name: {op: agk.rowops_team_plan(op, rows, cols,
+                                                        0 if dtype == "f32" else 1, lay)
+                               for op in agk.ROWOPS_TEAM_OPS}
+                        for name, lay in (("aligned", True), ("offset", False))}}
         es = 4 if dtype == "f32" else 2
         tb = rows * cols * es
+        wsb = agk.rowops_workspace_bytes(rows, cols)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev) if wsb else False
         for tag, shift_in, shift_out in (("vec", 0, 0), ("offset", 1, 1), ("scalar", 1, 0)):
             z, dy, y, dz, lse, dl = tensors(shift_in, shift_out)
             t = {
                 "softmax_fwd": (graph_replay_ms(
-                    lambda i, st: agk.softmax_fwd(z, y=y, stream=st), n), 2),
+                    lambda i, st: agk.softmax_fwd(z, y=y, workspace=ws, stream=st), n), 2),
                 "softmax_bwd": (graph_replay_ms(
                     # y takes the outputs' layout: the inputs' here
-                    lambda i, st: agk.softmax_bwd(z, dy, dz=y, stream=st), n), 3),
+                    lambda i, st: agk.softmax_bwd(z, dy, dz=y, workspace=ws, stream=st), n), 3),
                 "logsumexp_bwd": (graph_replay_ms(
-                    lambda i, st: agk.logsumexp_bwd(z, dl, dz=dz, stream=st), n), 2),
+                    lambda i, st: agk.logsumexp_bwd(z, dl, dz=dz, workspace=ws, stream=st), n),
+                    2),
             }
+            if tag != "scalar":  # the same calls without a workspace (no team kernel)
+                t["softmax_fwd_nows"] = (graph_replay_ms(
+                    lambda i, st: agk.softmax_fwd(z, y=y, workspace=False, stream=st), n), 2)
+                t["softmax_bwd_nows"] = (graph_replay_ms(
+                    lambda i, st: agk.softmax_bwd(z, dy, dz=y, workspace=False, stream=st), n), 3)
+                t["logsumexp_bwd_nows"] = (graph_replay_ms(
+                    lambda i, st: agk.logsumexp_bwd(z, dl, dz=dz, workspace=False, stream=st),
+                    n), 2)
             # the backward from the forward's fp32 value (one streaming pass)
             l32 = agk.logsumexp_fwd_keep(z)[1]
             t["logsumexp_bwd_from_value"] = (graph_replay_ms(

@@ -86,6 +86,16 @@ SIGNATURES = {
     "agk_logsumexp_fwd_keep": (ctypes.c_int, [_P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_logsumexp_bwd_from_value": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_int,
                                                     ctypes.c_int, _P]),
+    "agk_rowops_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "agk_softmax_fwd_ws": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _I64, _I64, ctypes.c_int,
+                                          _P]),
+    "agk_softmax_bwd_ws": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
+                                          ctypes.c_int, ctypes.c_int, _P]),
+    "agk_logsumexp_bwd_ws": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
+                                            ctypes.c_int, ctypes.c_int, _P]),
+    "agk_set_rowops_team": (ctypes.c_int, [ctypes.c_int]),
+    "agk_rowops_team_plan": (ctypes.c_int, [ctypes.c_int, _I64, _I64, ctypes.c_int, ctypes.c_int,
+                                            _P]),
     "agk_fill": (ctypes.c_int, [_P, _I64, ctypes.c_float, ctypes.c_int, _P]),
     "agk_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "agk_last_error": (ctypes.c_char_p, []),
@@ -578,24 +588,77 @@ def layernorm_bwd(x, mean, rstd, dy, dx=None, accumulate: bool = False, stream=N
     return dx
 
 
-def softmax_fwd(z, y=None, stream=None):
+def rowops_workspace_bytes(rows: int, cols: int) -> int:
+    return int(lib().agk_rowops_workspace_bytes(rows, cols))
+
+
+def _rowops_ws(workspace, rows, cols, device):
+    """(pointer, bytes) for the *_ws row ops: None allocates what the shape
+    uses (nothing when it uses none), False passes no workspace (the
+    workspace-free kernels), a tensor is used as given."""
+    if workspace is False:
+        return None, 0
+    if workspace is None:
+        need = rowops_workspace_bytes(rows, cols)
+        if not need:
+            return None, 0
+        workspace = _torch().empty(need, dtype=_torch().uint8, device=device)
+    return workspace, workspace.numel() * workspace.element_size()
+
+
+def softmax_fwd(z, y=None, workspace=None, stream=None):
+    """y = softmax(z) over the last axis.  workspace: None (allocated as the
+    shape needs: rows too wide for one workgroup then take the team kernel),
+    False (the workspace-free entry point) or a device tensor."""
     torch = _torch()
     rows, cols = _rows_cols(z)
     y = torch.empty_like(z) if y is None else y
-    rc = lib().agk_softmax_fwd(_ptr(z), _ptr(y), rows, cols, _dtype_code(z), _stream(stream))
+    ws, ws_bytes = _rowops_ws(workspace, rows, cols, z.device)
+    if ws is None and workspace is False:
+        rc = lib().agk_softmax_fwd(_ptr(z), _ptr(y), rows, cols, _dtype_code(z),
+                                   _stream(stream))
+    else:
+        rc = lib().agk_softmax_fwd_ws(_ptr(z), _ptr(y), _ptr(ws), ws_bytes, rows, cols,
+                                      _dtype_code(z), _stream(stream))
     _check(rc, "agk_softmax_fwd")
     return y
 
 
-def softmax_bwd(y, dy, dz=None, accumulate: bool = False, stream=None):
-    """dz (+)= y * (dy - sum(y * dy)) (also the JVP for dy = a tangent)."""
+def softmax_bwd(y, dy, dz=None, accumulate: bool = False, workspace=None, stream=None):
+    """dz (+)= y * (dy - sum(y * dy)) (also the JVP for dy = a tangent).
+    workspace as for softmax_fwd."""
     torch = _torch()
     rows, cols = _rows_cols(y)
     dz = (torch.zeros_like(y) if accumulate else torch.empty_like(y)) if dz is None else dz
-    rc = lib().agk_softmax_bwd(_ptr(y), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(y),
-                               _acc_dx(accumulate), _stream(stream))
+    ws, ws_bytes = _rowops_ws(workspace, rows, cols, y.device)
+    if ws is None and workspace is False:
+        rc = lib().agk_softmax_bwd(_ptr(y), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(y),
+                                   _acc_dx(accumulate), _stream(stream))
+    else:
+        rc = lib().agk_softmax_bwd_ws(_ptr(y), _ptr(dy), _ptr(dz), _ptr(ws), ws_bytes, rows,
+                                      cols, _dtype_code(y), _acc_dx(accumulate),
+                                      _stream(stream))
     _check(rc, "agk_softmax_bwd")
     return dz
+
+
+ROWOPS_TEAM_OPS = {"softmax_fwd": 0, "softmax_bwd": 1, "logsumexp_bwd": 2}
+
+
+def rowops_team_plan(op: str, rows: int, cols: int, dtype: int, aligned: bool = True) -> dict:
+    """The team launch a *_ws row op ('softmax_fwd', 'softmax_bwd',
+    'logsumexp_bwd') takes for these sizes (parts 0: none)."""
+    out = (ctypes.c_int32 * 3)()
+    _check(lib().agk_rowops_team_plan(ROWOPS_TEAM_OPS[op], rows, cols, dtype,
+                                      int(bool(aligned)), out), "agk_rowops_team_plan")
+    return {"parts": out[0], "slots_per_part": out[1], "teams": out[2]}
+
+
+def set_rowops_team(mode: int) -> int:
+    """When the *_ws row ops take the team kernel: 0 never, 1 (default) for
+    rows too wide for one workgroup, 2 whenever the row fits it (testing and
+    measurement knob).  Other values: read only.  Returns the previous mode."""
+    return int(lib().agk_set_rowops_team(int(mode)))
 
 
 def logsumexp_fwd(z, y=None, stream=None):
@@ -607,13 +670,20 @@ def logsumexp_fwd(z, y=None, stream=None):
     return y
 
 
-def logsumexp_bwd(z, dy, dz=None, accumulate: bool = False, stream=None):
-    """dz (+)= dy * softmax(z); dy has shape z.shape[:-1] + (1,) and z's dtype."""
+def logsumexp_bwd(z, dy, dz=None, accumulate: bool = False, workspace=None, stream=None):
+    """dz (+)= dy * softmax(z); dy has shape z.shape[:-1] + (1,) and z's dtype.
+    workspace as for softmax_fwd."""
     torch = _torch()
     rows, cols = _rows_cols(z)
     dz = (torch.zeros_like(z) if accumulate else torch.empty_like(z)) if dz is None else dz
-    rc = lib().agk_logsumexp_bwd(_ptr(z), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(z),
-                                 _acc_dx(accumulate), _stream(stream))
+    ws, ws_bytes = _rowops_ws(workspace, rows, cols, z.device)
+    if ws is None and workspace is False:
+        rc = lib().agk_logsumexp_bwd(_ptr(z), _ptr(dy), _ptr(dz), rows, cols, _dtype_code(z),
+                                     _acc_dx(accumulate), _stream(stream))
+    else:
+        rc = lib().agk_logsumexp_bwd_ws(_ptr(z), _ptr(dy), _ptr(dz), _ptr(ws), ws_bytes, rows,
+                                        cols, _dtype_code(z), _acc_dx(accumulate),
+                                        _stream(stream))
     _check(rc, "agk_logsumexp_bwd")
     return dz
 

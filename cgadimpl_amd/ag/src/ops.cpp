@@ -357,13 +357,23 @@ std::shared_ptr<Node> laynor_nodeops(const std::shared_ptr<Node>& x) {
     return n;
 }
 
+// The exchange workspace of the row ops' team kernel (rows too wide for one
+// workgroup), from the pool on the current stream; null when the shape needs
+// none.
+static std::unique_ptr<Storage> rowops_workspace(const Tensor& t, size_t* bytes) {
+    *bytes = agk_rowops_workspace_bytes(t.rows(), t.cols());
+    return *bytes ? std::make_unique<Storage>(*bytes, current_stream()) : nullptr;
+}
+
 std::shared_ptr<Node> softmax_row_nodeops(const std::shared_ptr<Node>& z) {
     require_value(z, "softmax_row");
     const Tensor& zv = z->value;
     if (zv.dim() < 1) fail("softmax_row: input needs at least one axis");
     Tensor y = Tensor::empty(zv.shape(), zv.dtype());
-    agk_check(agk_softmax_fwd(zv.data(), y.data(), zv.rows(), zv.cols(), agk_dtype_of(zv.dtype()),
-                              stream_arg()),
+    size_t ws_bytes = 0;
+    const std::unique_ptr<Storage> ws = rowops_workspace(zv, &ws_bytes);
+    agk_check(agk_softmax_fwd_ws(zv.data(), y.data(), ws ? ws->data() : nullptr, ws_bytes,
+                                 zv.rows(), zv.cols(), agk_dtype_of(zv.dtype()), stream_arg()),
               "softmax_row");
     auto n = std::make_shared<Node>(y, Op::SoftmaxRow, z->requires_grad(), "softmax_row");
     link_inputs(n, {z});
@@ -692,9 +702,11 @@ void vjp_SoftmaxRow(Node* n, const Tensor& gy) {
     GradLocks lock(Z, nullptr);
     bool acc = false;
     Tensor& dz = Z->grad_for_write(y.dtype(), &acc);
-    agk_check(agk_softmax_bwd(y.data(), gy.data(), dz.data(), y.rows(), y.cols(),
-                              agk_dtype_of(y.dtype()), acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE,
-                              stream_arg()),
+    size_t ws_bytes = 0;
+    const std::unique_ptr<Storage> ws = rowops_workspace(y, &ws_bytes);
+    agk_check(agk_softmax_bwd_ws(y.data(), gy.data(), dz.data(), ws ? ws->data() : nullptr,
+                                 ws_bytes, y.rows(), y.cols(), agk_dtype_of(y.dtype()),
+                                 acc ? AGK_ACCUM_DX : AGK_ACCUM_NONE, stream_arg()),
               "vjp_SoftmaxRow");
 }
 
@@ -910,8 +922,11 @@ Tensor jvp_SoftmaxRow(Node* n, const TangentOf& tan) {
     check_tangent(tz, Z->value, "jvp_SoftmaxRow");
     const Tensor& y = n->value;
     Tensor out = Tensor::empty(y.shape(), y.dtype());
-    agk_check(agk_softmax_bwd(y.data(), tz.data(), out.data(), y.rows(), y.cols(),
-                              agk_dtype_of(y.dtype()), AGK_ACCUM_NONE, stream_arg()),
+    size_t ws_bytes = 0;
+    const std::unique_ptr<Storage> ws = rowops_workspace(y, &ws_bytes);
+    agk_check(agk_softmax_bwd_ws(y.data(), tz.data(), out.data(), ws ? ws->data() : nullptr,
+                                 ws_bytes, y.rows(), y.cols(), agk_dtype_of(y.dtype()),
+                                 AGK_ACCUM_NONE, stream_arg()),
               "jvp_SoftmaxRow");
     return out;
 }

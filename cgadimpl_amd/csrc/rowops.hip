@@ -25,19 +25,27 @@
 // interface: Resident (the row held in registers by TPR lanes, NV 16-byte
 // slots per lane, G rows per workgroup -- the launch shapes and plan of the
 // RMSNorm forward) and Looped (one 256-lane workgroup per row, element-wise
-// accesses that re-read the row from cache; any alignment, any width).
+// accesses that re-read the row from cache; any alignment, any width).  The
+// softmax forward and backward and the log-sum-exp backward also have a team
+// kernel (rowops_team.hpp) for rows too wide for one workgroup's registers:
+// a row over several workgroups that exchange partial sums through a caller
+// workspace (the *_ws entry points), so each input row is read once.
 
 #include <hip/hip_runtime.h>
 
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "agk_rowops.h"
 #include "rowcommon.hpp"
 
 namespace agk {
+// The team kernels' wait limit (agk_set_exchange_wait_limit, rmsnorm.hip).
+int team_wait_polls();
+
 namespace rowops {
 
 // Pointers and scalars of one call.  Each op names the fields it reads.
@@ -992,6 +1000,50 @@ inline bool same_offset(const RowArgs& p) {
     return (a % sizeof(T)) == 0 && ok(p.in1) && ok(p.out);
 }
 
+// ---- rows over several workgroups (teams) -------------------------------------------
+
+#include "rowops_team.hpp"
+
+// When the *_ws entry points take the team kernel (agk_set_rowops_team):
+// 0 never, 1 for the shapes it serves better than the one-workgroup-per-row
+// kernels (the default), 2 whenever the row fits it (tests and measurement).
+std::atomic<int> g_team_mode{1};
+
+// Least parts per row for which mode 1 takes the team kernel: rows of more
+// than 8192 16-byte slots (past the register-resident shapes), and for the
+// softmax backward also rows that do not start on a 16-byte boundary from
+// 2049 slots on.  Measured on MI355X (graph-replayed, 8192 rows): at 50257
+// columns (every row off a boundary) the backward's team kernel against the
+// 16-byte looped kernel, which reads y and dy twice: bf16 438 against 540 us,
+// fp32 855 against 1140 us; the forward and the log-sum-exp backward read
+// one tensor, which the looped kernel's second pass finds in the caches:
+// bf16 (4 parts) 397-411 against 318 us, fp32 (7 parts) 619-631 against
+// 690-696 us.
+template <class Op>
+constexpr int team_min_parts(bool aligned) {
+    return std::is_same<Op, SmBwd>::value && !aligned ? 2 : 5;
+}
+
+// Runs Op over the rows on the team kernel when the mode, the workspace and
+// the rows' layout allow it; *taken tells the caller.
+template <class Op, class S>
+int maybe_team(const RowArgs& p, void* ws, size_t ws_bytes, int64_t rows, int cols,
+               hipStream_t st, bool* taken) {
+    *taken = false;
+    const int mode = g_team_mode.load(std::memory_order_relaxed);
+    if (ws == nullptr || mode == 0) return AGK_OK;
+    bool aligned = false;
+    if (!team_fits<S, Op>(p, rows, cols, 1, &aligned)) return AGK_OK;
+    const TeamShape sh =
+        team_shape(rows, cols, S::kVec, team_nvl<Op>(std::is_same<S, BF16>::value, aligned));
+    if (mode == 1 && sh.parts < team_min_parts<Op>(aligned)) return AGK_OK;
+    if (ws_bytes < team_words_bytes(rows, sh, TeamVals<Op>::value)) return AGK_OK;
+    *taken = true;
+    return launch_team<Op, S>(p, ws, rows, cols, aligned, st);
+}
+
+int team_wait_limit() { return agk::team_wait_polls(); }
+
 template <class Op, class S>
 int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
     const bool vec = (cols % S::kVec) == 0 && aligned16(p.in0) && aligned_or_null(p.in1) &&
@@ -1312,6 +1364,117 @@ int agk_logsumexp_bwd_from_value(const void* z, const float* lse, const void* dy
     return dtype == AGK_F32
                ? launch_lse_bwd_from_value<agk::F32>(z, lse, dy, dz, rows, c, acc, st)
                : launch_lse_bwd_from_value<agk::BF16>(z, lse, dy, dz, rows, c, acc, st);
+}
+
+size_t agk_rowops_workspace_bytes(int64_t rows, int64_t cols) {
+    if (agk::check_sizes(rows, cols) != AGK_OK || rows == 0 || cols == 0) return 0;
+    return agk::rowops::team_ws_bytes(rows, cols);
+}
+
+int agk_rowops_team_plan(int op, int64_t rows, int64_t cols, int dtype, int aligned,
+                         int32_t* plan) {
+    using namespace agk::rowops;
+    if (!plan) return AGK_EINVAL;
+    plan[0] = plan[1] = plan[2] = 0;
+    if (op < 0 || op > 2) return AGK_EINVAL;
+    if (int rc = agk::check_sizes(rows, cols)) return rc;
+    if (!agk::valid_dtype(dtype)) return AGK_EDTYPE;
+    if (rows == 0 || cols == 0) return AGK_OK;
+    const int W = dtype == AGK_F32 ? 4 : 8;
+    const size_t esz = dtype == AGK_F32 ? 4u : 2u;
+    if (rows > 0x7fffffffLL || static_cast<uint64_t>(cols) * esz >= 0x80000000ull) return AGK_OK;
+    const bool al = aligned != 0 && cols % W == 0;
+    const TeamShape sh = team_shape(rows, cols, W, team_nvl_of(op, dtype == AGK_BF16, al));
+    const int mode = g_team_mode.load(std::memory_order_relaxed);
+    if (sh.parts == 0 || mode == 0 || sh.teams * sh.parts > 0x7fffffffLL) return AGK_OK;
+    const int least = op == 1 ? team_min_parts<SmBwd>(al) : team_min_parts<SmFwd>(al);
+    if (mode == 1 && sh.parts < least) return AGK_OK;
+    plan[0] = sh.parts;
+    plan[1] = sh.ps;
+    plan[2] = static_cast<int32_t>(sh.teams);
+    return AGK_OK;
+}
+
+int agk_set_rowops_team(int mode) {
+    const int prev = agk::rowops::g_team_mode.load(std::memory_order_relaxed);
+    if (mode >= 0 && mode <= 2) agk::rowops::g_team_mode.store(mode, std::memory_order_relaxed);
+    return prev;
+}
+
+}  // extern "C"
+
+namespace agk {
+namespace rowops {
+
+// The *_ws entry points: the team kernel where maybe_team takes it, else the
+// kernels of the workspace-free entry point.
+template <class Op>
+int run_ws(const RowArgs& p, void* ws, size_t ws_bytes, int64_t rows, int64_t cols, int dtype,
+           agk_stream_t stream) {
+    if (ws != nullptr) {
+        if ((reinterpret_cast<uintptr_t>(ws) & 7u) != 0) return AGK_EINVAL;
+        if (ws_bytes < team_ws_bytes(rows, cols)) return AGK_EWORKSPACE;
+    }
+    clear_pending_error();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int c = static_cast<int>(cols);
+    bool taken = false;
+    const int rc = dtype == AGK_F32 ? maybe_team<Op, F32>(p, ws, ws_bytes, rows, c, st, &taken)
+                                    : maybe_team<Op, BF16>(p, ws, ws_bytes, rows, c, st, &taken);
+    if (rc != AGK_OK || taken) return rc;
+    return dtype == AGK_F32 ? launch<Op, F32>(p, rows, c, st) : launch<Op, BF16>(p, rows, c, st);
+}
+
+}  // namespace rowops
+}  // namespace agk
+
+extern "C" {
+
+int agk_softmax_fwd_ws(const void* z, void* y, void* workspace, size_t workspace_bytes,
+                       int64_t rows, int64_t cols, int dtype, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (done) return AGK_OK;
+    if (!z || !y) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.out = y;
+    return run_ws<SmFwd>(p, workspace, workspace_bytes, rows, cols, dtype, stream);
+}
+
+int agk_softmax_bwd_ws(const void* y, const void* dy, void* dz, void* workspace,
+                       size_t workspace_bytes, int64_t rows, int64_t cols, int dtype,
+                       int accumulate, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (!valid_accumulate(accumulate)) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!y || !dy || !dz) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = y;
+    p.in1 = dy;
+    p.out = dz;
+    p.acc = accumulate & AGK_ACCUM_DX;
+    return run_ws<SmBwd>(p, workspace, workspace_bytes, rows, cols, dtype, stream);
+}
+
+int agk_logsumexp_bwd_ws(const void* z, const void* dy, void* dz, void* workspace,
+                         size_t workspace_bytes, int64_t rows, int64_t cols, int dtype,
+                         int accumulate, agk_stream_t stream) {
+    using namespace agk::rowops;
+    bool done;
+    if (int rc = precheck(rows, cols, dtype, &done)) return rc;
+    if (!valid_accumulate(accumulate)) return AGK_EINVAL;
+    if (done) return AGK_OK;
+    if (!z || !dy || !dz) return AGK_EINVAL;
+    RowArgs p;
+    p.in0 = z;
+    p.rsv = dy;
+    p.out = dz;
+    p.acc = accumulate & AGK_ACCUM_DX;
+    return run_ws<LseBwd>(p, workspace, workspace_bytes, rows, cols, dtype, stream);
 }
 
 int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows, int64_t cols,

@@ -532,9 +532,19 @@ def write_wide_summary(jsonl, out_md, command):
                   "dz = dy * exp(z - lse) with the forward's fp32 lse (one read of z, one "
                   "write of dz; what the graph layer's vjp_LogSumExpRow runs); 'log-sum-exp "
                   "bwd' recomputes the row maximum and sum as the reference's rule does.", "",
-                  "| shape | softmax fwd | softmax bwd | log-sum-exp fwd | log-sum-exp bwd | "
-                  "log-sum-exp bwd from value |",
-                  "|---|---|---|---|---|---|"]
+                  "Softmax forward and backward and the log-sum-exp backward are called "
+                  "with a workspace (agk_*_ws): rows of more than 8192 16-byte slots, and for "
+                  "the softmax backward rows off a 16-byte boundary of more than 2048, take "
+                  "the team kernel "
+                  "('team': workgroups per row for softmax fwd / softmax bwd / log-sum-exp bwd "
+                  "in the aligned and offset layouts, 0 for none; a row over that many "
+                  "workgroups that exchange partial sums, so each input row is read once). "
+                  "The 'no workspace' columns time the same calls without one (the "
+                  "one-workgroup-per-row kernels) in the first two layouts.", "",
+                  "| shape | team | softmax fwd | softmax bwd | log-sum-exp fwd | "
+                  "log-sum-exp bwd | log-sum-exp bwd from value | softmax fwd, no workspace | "
+                  "softmax bwd, no workspace | log-sum-exp bwd, no workspace |",
+                  "|---|---|---|---|---|---|---|---|---|---|"]
         for r in ro:
             u, g = r["us"], r["gbs"]
             cells = []
@@ -546,7 +556,18 @@ def write_wide_summary(jsonl, out_md, command):
                 sc = u.get(k + "_scalar", "-")
                 cells.append(f"{u[k + '_vec']} / {u[k + '_offset']} / {sc} "
                              f"({g[k + '_vec'] / 80:.1f} %)")
-            lines.append(f"| {r['wide_rowops']} | " + " | ".join(cells) + " |")
+            for k in ("softmax_fwd_nows", "softmax_bwd_nows", "logsumexp_bwd_nows"):
+                if k + "_vec" not in u:
+                    cells.append("-")
+                    continue
+                cells.append(f"{u[k + '_vec']} / {u[k + '_offset']} "
+                             f"({g[k + '_vec'] / 80:.1f} %)")
+            team = r.get("team")
+            tcell = ("; ".join(f"{lay}: " + "/".join(str(team[lay][op]["parts"]) for op in
+                                                    ("softmax_fwd", "softmax_bwd",
+                                                     "logsumexp_bwd")) for lay in
+                               ("aligned", "offset")) if team else "-")
+            lines.append(f"| {r['wide_rowops']} | {tcell} | " + " | ".join(cells) + " |")
     with open(out_md, "w") as fh:
         fh.write("\n".join(lines) + "\n")
 

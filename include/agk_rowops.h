@@ -118,6 +118,58 @@ int agk_logsumexp_bwd_from_value(const void* z, const float* lse, const void* dy
 int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows,
                       int64_t cols, int dtype, agk_stream_t stream);
 
+/* ---- the same ops with a workspace: rows over several workgroups ----------
+ * agk_softmax_fwd_ws, agk_softmax_bwd_ws and agk_logsumexp_bwd_ws compute
+ * what agk_softmax_fwd, agk_softmax_bwd and agk_logsumexp_bwd compute (the
+ * same references: softmax_row_nodeops, reduction.cpp:42-53; vjp_SoftmaxRow,
+ * autodiff_vjp_ops.cpp:421-428; vjp_LogSumExpRow, :430-440).  Given a
+ * workspace, rows too wide for one workgroup's registers (more than 8192
+ * 16-byte slots; for the softmax backward also rows that do not start on a
+ * 16-byte boundary from 2049 slots on, every row tensor at the same offset
+ * from one) are spread over a team of workgroups that exchange their partial
+ * row sums through the workspace, so each input row is read from HBM once
+ * (the workspace-free calls re-read such rows).  Results are within fp32 rounding of the
+ * workspace-free calls' (the row sums are added in another order) and bit-
+ * identical run to run.  workspace == NULL takes the workspace-free kernels;
+ * otherwise it must be 8-byte aligned and hold at least
+ * agk_rowops_workspace_bytes(rows, cols) bytes (AGK_EINVAL / AGK_EWORKSPACE
+ * if not): rows * parts * 16 bytes, parts = ceil(ceil(cols / W) / 2048) for
+ * W = 4 (fp32), or for W = 8 (bf16) where fp32 rows would need more than 64
+ * parts; 0 where that is below 2 or above 64 (rows that one workgroup holds,
+ * or too wide for the team kernel).  The workspace is scratch: its contents
+ * on entry do not matter, and calls that share one must not overlap in time. */
+size_t agk_rowops_workspace_bytes(int64_t rows, int64_t cols);
+
+int agk_softmax_fwd_ws(const void* z, void* y, void* workspace,
+                       size_t workspace_bytes, int64_t rows, int64_t cols,
+                       int dtype, agk_stream_t stream);
+
+int agk_softmax_bwd_ws(const void* y, const void* dy, void* dz, void* workspace,
+                       size_t workspace_bytes, int64_t rows, int64_t cols,
+                       int dtype, int accumulate, agk_stream_t stream);
+
+int agk_logsumexp_bwd_ws(const void* z, const void* dy, void* dz, void* workspace,
+                         size_t workspace_bytes, int64_t rows, int64_t cols,
+                         int dtype, int accumulate, agk_stream_t stream);
+
+/* Testing and measurement knob, with no counterpart in the reference: when
+ * the *_ws calls above take the team kernel.  0: never; 1 (default): for the
+ * rows described above; 2: for every row it can hold (up to 64 workgroups of
+ * 2048 16-byte slots).  A value outside 0..2 only reads the setting.
+ * Process-wide; returns the previous value.  Their wait on other workgroups
+ * is agk_set_exchange_wait_limit's (agk_rmsnorm.h).                          */
+int agk_set_rowops_team(int mode);
+
+/* Testing knob, with no counterpart in the reference: the team launch that
+ * op (0 agk_softmax_fwd_ws, 1 agk_softmax_bwd_ws, 2 agk_logsumexp_bwd_ws)
+ * takes for these sizes under the current mode, given a workspace, with
+ * every row tensor 16-byte aligned (aligned != 0; cols a multiple of the
+ * vector width) or all at one other offset from a boundary (aligned == 0).
+ * plan[0] = workgroups per row (0: the workspace-free kernels run instead),
+ * plan[1] = 16-byte slots per workgroup, plan[2] = rows in flight (teams).  */
+int agk_rowops_team_plan(int op, int64_t rows, int64_t cols, int dtype,
+                         int aligned, int32_t* plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -807,6 +807,37 @@ Vec central(const std::function<Vec(double)>& f, double h = 1e-4) {
     return o;
 }
 
+// softmax_row on rows too wide for one workgroup (the row ops' team kernel,
+// whose exchange workspace the graph layer takes from its pool): forward and
+// VJP against a host double-precision softmax, aligned rows and rows that
+// start off a 16-byte boundary (50257 columns).
+void test_wide_softmax() {
+    for (int64_t D : {int64_t{40000}, int64_t{50257}}) {
+        const int64_t R = 3;
+        Vec zd = to_d(normal(R * D, 70 + D));
+        for (double& v : zd) v *= 4.0;
+        std::vector<float> zf(zd.begin(), zd.end());
+        zd.assign(zf.begin(), zf.end());  // the values the device holds
+        Value z = leaf(zf, {R, D}, "z");
+        std::vector<float> gf = normal(R * D, 71 + D);
+        Tensor gy = Tensor::from_host_f32(gf, {R, D});
+        Value y = softmax_row(z);
+        backward(y, &gy);
+        const Vec ys = host_softmax(zd, R, D);
+        Vec dz(ys.size());
+        for (int64_t i = 0; i < R; ++i) {
+            double dot = 0.0;
+            for (int64_t j = 0; j < D; ++j) dot += ys[i * D + j] * gf[i * D + j];
+            for (int64_t j = 0; j < D; ++j) dz[i * D + j] = ys[i * D + j] * (gf[i * D + j] - dot);
+        }
+        const double ey = rel_err(y.val().to_host_f32(), ys);
+        const double ed = rel_err(z.grad().to_host_f32(), dz);
+        const std::string tag = "softmax_row [3," + std::to_string(D) + "] (team kernel)";
+        report((tag + " forward == host").c_str(), ey <= 1e-5, std::to_string(ey));
+        report((tag + " VJP == host").c_str(), ed <= 1e-5, std::to_string(ed));
+    }
+}
+
 void test_row_ops_gradients() {
     // the reference pattern: [4,10] input, numerical gradient of sum(f(a))
     Value a = leaf(normal(40, 60), {4, 10}, "a");
@@ -1455,6 +1486,7 @@ int selftest(const std::vector<std::string>& only) {
         {"seed_not_modified", test_seed_not_modified},
         {"user_stream", test_user_stream},
         {"row_ops_gradients", test_row_ops_gradients},
+        {"wide_softmax", test_wide_softmax},
         {"jvp", test_jvp},
         {"matmul_layer", test_matmul_layer},
         {"linear_layer", test_linear_layer},

@@ -392,6 +392,67 @@ def test_rowops_argument_validation():
     assert lib.agk_logsumexp_jvp(FAKE, FAKE, FAKE, 4, 8, 1 << 20, None) == 2
 
 
+def _rowops_ws_rule(rows, cols):
+    """The documented workspace of the *_ws row ops: two 8-byte values per
+    part and row, parts = ceil(ceil(cols / W) / 2048), the most over W = 4
+    (fp32) and 8 (bf16) with 2-64 parts."""
+    most = 0
+    for w in (4, 8):
+        parts = -(-(-(-cols // w)) // 2048)
+        if 2 <= parts <= 64:
+            most = max(most, rows * parts * 16)
+    return most
+
+
+def test_rowops_workspace_rule_and_team_plans():
+    """The *_ws row ops' workspace (the most any op uses at the shape, 0 for
+    rows one workgroup holds), the team plans in the default mode (rows of
+    more than 8192 aligned 16-byte slots, or off a boundary from 2049 slots),
+    and validation that rejects a workspace before any HIP call."""
+    lib = agk.lib()
+    wb = lib.agk_rowops_workspace_bytes
+    for rows, cols in [(8192, 128256), (3, 50257), (1, 8193), (5, 262144), (2, 1 << 19),
+                       (7, 1 << 20), (9, 6200)]:
+        assert wb(rows, cols) == _rowops_ws_rule(rows, cols), (rows, cols)
+    assert wb(8192, 128256) == 8192 * 16 * 2 * 8        # fp32 forward: 16 parts, 2 values
+    assert wb(100, 4096) == 0 and wb(4, 512) == 0 and wb(0, 131072) == 0
+    assert wb(4, 1 << 22) == 0  # more than 64 parts: the team kernel holds no such row
+    plan = agk.rowops_team_plan
+    # bf16 Llama 3 vocabulary: 16032 slots -> 8 parts of 2004, 512 / 8 teams
+    for op in agk.ROWOPS_TEAM_OPS:
+        assert plan(op, 8192, 128256, 1, True) == {"parts": 8, "slots_per_part": 2004,
+                                                   "teams": 64}
+    assert plan("softmax_fwd", 8192, 128256, 0, True)["parts"] == 16
+    assert plan("softmax_fwd", 4, 65536, 1, True)["parts"] == 0   # 8192 slots: resident kernels
+    assert plan("softmax_fwd", 4, 65536, 0, True)["parts"] == 8
+    assert plan("softmax_bwd", 4, 65536, 1, True)["parts"] == 0
+    # rows off a 16-byte boundary: the backward from 2 parts, the others from 5
+    assert plan("softmax_bwd", 9, 50257, 1, False) == {"parts": 4, "slots_per_part": 1571,
+                                                       "teams": 9}
+    assert plan("softmax_fwd", 9, 50257, 1, False)["parts"] == 0
+    assert plan("logsumexp_bwd", 9, 50257, 0, False)["parts"] == 7
+    assert plan("softmax_fwd", 3, 16384, 1, False)["parts"] == 0  # 2048 slots: one workgroup
+    prev = agk.set_rowops_team(0)
+    try:
+        assert plan("softmax_fwd", 8192, 128256, 1, True)["parts"] == 0
+        assert agk.set_rowops_team(2) == 0
+        assert plan("softmax_fwd", 3, 16384, 1, False)["parts"] == 1
+    finally:
+        agk.set_rowops_team(prev)
+    assert agk.set_rowops_team(-1) == prev
+    assert lib.agk_rowops_team_plan(3, 4, 8, 0, 1, (ctypes.c_int32 * 3)()) == 1
+    need = wb(4, 131072)
+    assert lib.agk_softmax_fwd_ws(FAKE, FAKE, FAKE, need - 1, 4, 131072, 1, None) == 3
+    assert lib.agk_softmax_fwd_ws(FAKE, FAKE, FAKE + 4, need, 4, 131072, 1, None) == 1
+    assert lib.agk_softmax_bwd_ws(FAKE, FAKE, FAKE, FAKE, need - 8, 4, 131072, 1, 0, None) == 3
+    assert lib.agk_softmax_bwd_ws(FAKE, None, FAKE, None, 0, 4, 131072, 1, 0, None) == 1
+    assert lib.agk_softmax_bwd_ws(FAKE, FAKE, FAKE, None, 0, 4, 131072, 1, 2, None) == 1
+    assert lib.agk_logsumexp_bwd_ws(FAKE, FAKE, FAKE, FAKE, 0, 4, 131072, 0, 0, None) == 3
+    assert lib.agk_logsumexp_bwd_ws(None, FAKE, FAKE, None, 0, 4, 8, 0, 0, None) == 1
+    assert lib.agk_softmax_fwd_ws(None, None, None, 0, 0, 8, 0, None) == 0
+    assert lib.agk_softmax_fwd_ws(FAKE, FAKE, None, 0, 4, 8, 5, None) == 2
+
+
 def test_python_binding_raises_without_gpu_tensors():
     torch = pytest.importorskip("torch")
     x = torch.zeros(4, 8)

@@ -471,3 +471,147 @@ def test_full_size(cuda, name):
     rel = abs(lhs - rhs) / max(abs(rhs), float((w.double() * ty.double()).abs().sum()) * 1e-3)
     print(f"[{name}] adjoint identity <w, J t> vs <J^T w, t>: {rel:.2e}", flush=True)
     assert rel <= (5e-2 if bf16 else 1e-4)
+
+
+# ---- rows over several workgroups: the *_ws entry points' team kernel -------------------
+
+# Vocabulary widths and one row per team: aligned rows of many parts (Llama 3's
+# 128256, Qwen's 151936, 2^19), rows that start at another offset in every row
+# (GPT-2's 50257), more rows than teams (each team then runs several rows, odd
+# and even counts), one row.
+TEAM_SHAPES = [("bf16", 700, 128256), ("f32", 65, 128256), ("bf16", 1, 151936),
+               ("bf16", 33, 50257), ("f32", 9, 50257), ("bf16", 3, 1 << 19),
+               ("f32", 130, 40000), ("f32", 2, 8193)]
+
+
+def _team_parts(dtype, rows, cols, aligned):
+    """Workgroups per row of the team launch (the most of the three ops: the
+    softmax backward takes rows off a 16-byte boundary from fewer parts)."""
+    return max(agk.rowops_team_plan(op, rows, cols, 0 if dtype == "f32" else 1, aligned)["parts"]
+               for op in agk.ROWOPS_TEAM_OPS)
+
+
+def _softmax_lse_outputs(z, dy, dl, ws):
+    y = agk.softmax_fwd(z, workspace=ws)
+    dz = agk.softmax_bwd(y, dy, workspace=ws)
+    dlz = agk.logsumexp_bwd(z, dl, workspace=ws)
+    return y, dz, dlz
+
+
+@pytest.mark.parametrize("dtype,rows,cols", TEAM_SHAPES, ids=str)
+def test_team_rows_match_oracle_and_recompute(cuda, dtype, rows, cols):
+    """Softmax forward and backward and the log-sum-exp backward on the team
+    kernel (a row over several workgroups that exchange their partial sums):
+    against the oracle with check_softmax's and check_logsumexp's bars, against
+    the workspace-free kernels within the same bars (the row sums are added in
+    another order), and with every wait cut to its first look (wait limit 0:
+    the workgroups recompute the partial sums they do not find yet)
+    bit-identical to the default -- a recomputed partial sum is the published
+    one."""
+    import torch
+    aligned = cols % (4 if dtype == "f32" else 8) == 0
+    parts = _team_parts(dtype, rows, cols, aligned)
+    print(f"team rowops {dtype} {rows}x{cols} parts {parts}", flush=True)
+    assert parts >= 2, "the shape should take the team kernel"
+    x, _, dy = device_inputs((rows, cols), dtype, rows + cols, cuda)
+    z = x * 4.0
+    dl = dy[:, :1].contiguous()
+    team = _softmax_lse_outputs(z, dy, dl, None)
+    plain = _softmax_lse_outputs(z, dy, dl, False)
+    prev = agk.set_exchange_wait_limit(0)
+    try:
+        rec = _softmax_lse_outputs(z, dy, dl, None)
+    finally:
+        agk.set_exchange_wait_limit(prev)
+    torch.cuda.synchronize()
+    for a, b in zip(team, rec):
+        assert torch.equal(a, b)
+    y, dz, dlz = team
+    bf16 = dtype == "bf16"
+    srows = _sample_rows(rows, cols)
+    zs, dys, ys, dls = (_host_rows(z, srows), _host_rows(dy, srows), _host_rows(y, srows),
+                        _host_rows(dl, srows))
+    if bf16:
+        ry, rdz, rdl = (ro.softmax_fwd_bf16(zs), ro.softmax_bwd_bf16(ys, dys),
+                        ro.logsumexp_bwd_bf16(zs, dls))
+    else:
+        ry, rdz, rdl = ro.softmax_fwd(zs), ro.softmax_bwd(ys, dys), ro.logsumexp_bwd(zs, dls)
+    yf, gf = _f64(ys), _f64(dys)
+    scale = _rowmax(yf) * (_rowmax(gf) + np.abs(np.sum(yf * gf, -1)))
+    py, pdz, pdl = (_host_rows(t, srows) for t in plain)
+    e = {"y": _row_rel(ys, ry), "dz": _scaled_err(_host_rows(dz, srows), rdz, scale),
+         "lse dz": _row_rel(_host_rows(dlz, srows), rdl),
+         "y vs workspace-free": _row_rel(ys, py),
+         "dz vs workspace-free": _scaled_err(_host_rows(dz, srows), pdz, scale),
+         "lse dz vs workspace-free": _row_rel(_host_rows(dlz, srows), pdl)}
+    assert_ok(e, _tol(bf16), f"team {dtype} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [("bf16", 50, 4096), ("f32", 300, 2048),
+                                             ("bf16", 20, 20000), ("f32", 17, 10001),
+                                             ("bf16", 5, 65536)], ids=str)
+def test_team_kernel_on_narrow_rows(cuda, dtype, rows, cols):
+    """Mode 2 puts rows the default keeps on one workgroup (one part, two or
+    three parts, a last part holding the tail) on the team kernel: the same
+    bars against the oracle, and the recompute path bit-identical."""
+    import torch
+    bf16 = dtype == "bf16"
+    prev = agk.set_rowops_team(2)
+    try:
+        aligned = cols % (8 if bf16 else 4) == 0
+        assert _team_parts(dtype, rows, cols, aligned) >= 1
+        x, _, dy = device_inputs((rows, cols), dtype, 3 * rows + cols, cuda)
+        z = x * 4.0
+        dl = dy[:, :1].contiguous()
+        ws = torch.empty(rows * 64 * 16, dtype=torch.uint8, device=cuda)
+        y, dz, dlz = _softmax_lse_outputs(z, dy, dl, ws)
+        pw = agk.set_exchange_wait_limit(0)
+        try:
+            rec = _softmax_lse_outputs(z, dy, dl, ws)
+        finally:
+            agk.set_exchange_wait_limit(pw)
+    finally:
+        agk.set_rowops_team(prev)
+    torch.cuda.synchronize()
+    for a, b in zip((y, dz, dlz), rec):
+        assert torch.equal(a, b)
+    zs, dys, ys, dls = to_host(z), to_host(dy), to_host(y), to_host(dl)
+    if bf16:
+        ry, rdz, rdl = (ro.softmax_fwd_bf16(zs), ro.softmax_bwd_bf16(ys, dys),
+                        ro.logsumexp_bwd_bf16(zs, dls))
+    else:
+        ry, rdz, rdl = ro.softmax_fwd(zs), ro.softmax_bwd(ys, dys), ro.logsumexp_bwd(zs, dls)
+    yf, gf = _f64(ys), _f64(dys)
+    scale = _rowmax(yf) * (_rowmax(gf) + np.abs(np.sum(yf * gf, -1)))
+    e = {"y": _row_rel(ys, ry), "dz": _scaled_err(to_host(dz), rdz, scale),
+         "lse dz": _row_rel(to_host(dlz), rdl)}
+    assert_ok(e, _tol(bf16), f"team mode 2 {dtype} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("dtype,cols", [("bf16", 131072), ("f32", 50257)], ids=str)
+def test_team_accumulates_and_is_deterministic(cuda, dtype, cols):
+    """The team kernel's backward outputs add into dz as the other kernels do
+    (fp32: pre + fresh within one rounding; bf16 within two), and three calls
+    give the same bits."""
+    import torch
+    rows = 37
+    x, _, dy = device_inputs((rows, cols), dtype, 11, cuda)
+    assert _team_parts(dtype, rows, cols, cols % 8 == 0) >= 2
+    pre = torch.randn(x.shape, device=cuda).to(x.dtype)
+    s = agk.softmax_fwd(x)
+    dl = dy[:, :1].contiguous()
+    outs = {"softmax": (agk.softmax_bwd(s, dy), agk.softmax_bwd(s, dy, dz=pre.clone(),
+                                                                accumulate=True)),
+            "logsumexp": (agk.logsumexp_bwd(x, dl),
+                          agk.logsumexp_bwd(x, dl, dz=pre.clone(), accumulate=True))}
+    first = [agk.softmax_fwd(x), agk.softmax_bwd(s, dy), agk.logsumexp_bwd(x, dl)]
+    for _ in range(2):
+        again = [agk.softmax_fwd(x), agk.softmax_bwd(s, dy), agk.logsumexp_bwd(x, dl)]
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(first, again))
+    tol = 2 * _tol(dtype == "bf16")
+    for name, (fresh, acc) in outs.items():
+        want = pre.double() + fresh.double()
+        err = float(((acc.double() - want).abs().max() / want.abs().max()).item())
+        print(f"[team accumulate {name} {dtype}] {err:.2e}", flush=True)
+        assert err <= tol, (name, err)
