@@ -982,7 +982,9 @@ def mfma_probe(reps):
     256 workgroups of 4 waves (one wave per SIMD, as the GEMM), each wave 16
     v_mfma_f32_32x32x16_bf16 accumulators.  Mode "lds": the GEMM's fragment
     reads from LDS one substep ahead of the MFMAs; mode "registers": MFMAs
-    only.  Operand contents: the c5 products' distributions (A ~ N(0,1),
+    only; modes "lds, 16x16x32" and "registers, 16x16x32": the same on
+    v_mfma_f32_16x16x32_bf16 (8 x 8 accumulators of 16 x 16 per wave, 128
+    MFMAs per k-step).  Operand contents: the c5 products' distributions (A ~ N(0,1),
     B ~ N(0,0.02^2) in bf16), uniform +-[0.5, 2), and zeros.  HIP events give
     TFLOP/s; wave 0 of every workgroup reads s_memtime and s_memrealtime
     (100 MHz) around its loop, which give the shader clock it ran at and its
@@ -1015,7 +1017,8 @@ def mfma_probe(reps):
     clocks = torch.zeros(wg * 4, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream()
     recs = []
-    for mode, mode_name in ((0, "lds"), (1, "registers")):
+    for mode, mode_name in ((0, "lds"), (1, "registers"), (2, "lds, 16x16x32"),
+                            (3, "registers, 16x16x32")):
         for name, src in datas:
             src = src.contiguous()
 

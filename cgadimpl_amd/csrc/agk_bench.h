@@ -32,7 +32,9 @@ int agk_probe_stream(const void* a, const void* b, void* c, void* d, int64_t byt
  * runs `steps` 64-deep k-steps of 64 MFMAs.  mode 0: each substep's 8 operand
  * fragments are read from a 64 KiB LDS tile filled once from `src` (the
  * GEMM's LDS traffic, no global loads); mode 1: the fragments stay in
- * registers (two sets, loaded once from `src`), only the MFMAs run.  src:
+ * registers (two sets, loaded once from `src`), only the MFMAs run; modes 2
+ * and 3: modes 0 and 1 on v_mfma_f32_16x16x32_bf16 (the same 128 x 128 block
+ * per wave as 8 x 8 accumulators, 128 MFMAs per k-step, the same FLOP).  src:
  * 64 KiB of bf16 operand data (random, zeros, ...).  out: 4 floats per
  * workgroup (a checksum of the accumulators, so the work is not removed).
  * clocks (may be NULL): per workgroup, the shader clock counter

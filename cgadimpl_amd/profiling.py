@@ -443,11 +443,13 @@ def write_mfma_probe_summary(jsonl, out_md, command):
              "wave 16 `v_mfma_f32_32x32x16_bf16` accumulators (a 128 x 128 block), "
              f"{recs[0]['k_steps_per_wave'] if recs else '?'} 64-deep k-steps per wave. "
              "'lds': every substep's 8 fragments read from a 64 KiB LDS tile one substep "
-             "ahead (the GEMM's LDS traffic and schedule); 'registers': MFMAs only. "
+             "ahead (the GEMM's LDS traffic and schedule); 'registers': MFMAs only; the "
+             "'16x16x32' modes: the same block as 8 x 8 `v_mfma_f32_16x16x32_bf16` "
+             "accumulators, 128 MFMAs per k-step, the same fragment bytes per k. "
              "TFLOP/s from HIP events; the shader clock and cycles per k-step from "
              "s_memtime / s_memrealtime (100 MHz) read by wave 0 of each workgroup around "
-             "its loop (medians over workgroups). A k-step is 64 MFMAs: 2048 cycles at the "
-             "full issue rate. Dense bf16 peak: 2500 TFLOP/s at 2.4 GHz.", "",
+             "its loop (medians over workgroups). A k-step is 2048 cycles at the full issue "
+             "rate of either instruction. Dense bf16 peak: 2500 TFLOP/s at 2.4 GHz.", "",
              "| mode | operand data | TFLOP/s | % of dense peak | shader GHz | cycles per k-step |",
              "|---|---|---|---|---|---|"]
     for r in recs:
