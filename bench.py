@@ -1114,8 +1114,10 @@ def run_wide(steps):
     the one-workgroup-per-row kernels on the same build, each call captured
     `steps` times into a HIP graph and replayed (GPU time per call).
 
-    forward: out of place (split when the row is too wide for registers)
-    against in place (y = x, which keeps one workgroup per row); backward (dx
+    forward: out of place (split when the row is too wide for registers),
+    the same with a workspace (agk_rmsnorm_fwd_ws: the team kernel where it
+    applies, x read once) and in place (y = x, which keeps one workgroup per
+    row); backward (dx
     and dgamma) and dx alone as the library takes them with a workspace (the
     one-pass or team kernel where they apply), the same with the team kernel
     switched off (the split path), and dx alone without a workspace
@@ -1142,6 +1144,8 @@ def run_wide(steps):
         dg = torch.empty(cols, dtype=torch.float32, device=dev)
         ws = torch.empty(agk.rmsnorm_bwd_workspace_bytes(rows, cols), dtype=torch.uint8,
                          device=dev)
+        fws = torch.empty(max(agk.rmsnorm_fwd_workspace_bytes(rows, cols), 8), dtype=torch.uint8,
+                          device=dev)
         agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv)
         fn = agk.lib().agk_rmsnorm_bwd
 
@@ -1161,6 +1165,9 @@ def run_wide(steps):
         t = {
             "fwd_split": graph_replay_ms(
                 lambda i, st: agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, stream=st), n),
+            "fwd_ws": graph_replay_ms(
+                lambda i, st: agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, workspace=fws,
+                                              stream=st), n),
             "fwd_in_place": graph_replay_ms(
                 lambda i, st: agk.rmsnorm_fwd(xin, g, 1e-6, y=xin, inv_rms=inv, stream=st), n),
             "bwd": graph_replay_ms(bwd_full, n),
@@ -1177,15 +1184,16 @@ def run_wide(steps):
         es = x.element_size()
         fb, bb = 2.0 * rows * cols * es, 3.0 * rows * cols * es
         fp, bp = agk.launch_plan(rows, cols, dt, False), agk.launch_plan(rows, cols, dt, True)
+        fwp = agk.launch_plan(rows, cols, dt, False, fwd_workspace=True)
         rec = {"wide_rows": f"{dtype} {rows}x{cols}", "dtype": dtype, "rows": rows,
                "cols": cols, "calls_per_graph": n,
-               "fwd_plan": fp, "bwd_plan": bp,
+               "fwd_plan": fp, "fwd_ws_plan": fwp, "bwd_plan": bp,
                "us": {k: round(v * 1e3, 2) for k, v in t.items()},
                "gbs": {k: round((fb if k.startswith("fwd") else bb) / (v * 1e-3) / 1e9, 1)
                        for k, v in t.items()}}
         print(json.dumps(rec), flush=True)
         out.append(rec)
-        del x, g, dy, y, dx, xin, inv, dg, ws
+        del x, g, dy, y, dx, xin, inv, dg, ws, fws
         torch.cuda.empty_cache()
     return out
 

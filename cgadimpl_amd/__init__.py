@@ -42,6 +42,9 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 SIGNATURES = {
     "agk_rmsnorm_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_float, ctypes.c_int, _P]),
+    "agk_rmsnorm_fwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "agk_rmsnorm_fwd_ws": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
+                                          ctypes.c_float, ctypes.c_int, _P]),
     "agk_rmsnorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "agk_rmsnorm_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64,
                                        ctypes.c_int, ctypes.c_int, _P]),
@@ -73,6 +76,7 @@ SIGNATURES = {
     "agk_rmsnorm_launch_plan": (ctypes.c_int, [_I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
     "agk_set_exchange_wait_limit": (ctypes.c_int, [ctypes.c_int]),
     "agk_set_team_backward": (ctypes.c_int, [ctypes.c_int]),
+    "agk_set_team_forward": (ctypes.c_int, [ctypes.c_int]),
     "agk_rmsnorm_jvp": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_int, _P]),
     "agk_layernorm_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, ctypes.c_float, ctypes.c_int,
                                          _P]),
@@ -203,8 +207,17 @@ def rmsnorm_bwd_workspace_bytes(rows: int, cols: int) -> int:
     return int(lib().agk_rmsnorm_bwd_workspace_bytes(rows, cols))
 
 
-def rmsnorm_fwd(x, gamma, eps: float, y=None, inv_rms=None, stream=None):
-    """y = x * rsqrt(mean(x^2, -1) + eps) * gamma; returns (y, inv_rms[rows])."""
+def rmsnorm_fwd_workspace_bytes(rows: int, cols: int) -> int:
+    return int(lib().agk_rmsnorm_fwd_workspace_bytes(rows, cols))
+
+
+def rmsnorm_fwd(x, gamma, eps: float, y=None, inv_rms=None, workspace=False, stream=None):
+    """y = x * rsqrt(mean(x^2, -1) + eps) * gamma; returns (y, inv_rms[rows]).
+
+    workspace: False (default) calls agk_rmsnorm_fwd; None allocates what
+    agk_rmsnorm_fwd_ws uses for the shape (wide rows then take the team
+    kernel, one read of x); a device tensor is passed to agk_rmsnorm_fwd_ws
+    as given."""
     torch = _torch()
     cols = x.shape[-1] if x.dim() else 1
     rows = x.numel() // cols if cols else 0
@@ -212,9 +225,19 @@ def rmsnorm_fwd(x, gamma, eps: float, y=None, inv_rms=None, stream=None):
         y = torch.empty_like(x)
     if inv_rms is None:
         inv_rms = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
-    rc = lib().agk_rmsnorm_fwd(_ptr(x), _ptr(gamma), _ptr(y), _ptr(inv_rms), rows, cols,
-                               float(eps), _dtype_code(x), _stream(stream))
-    _check(rc, "agk_rmsnorm_fwd")
+    if workspace is False:
+        rc = lib().agk_rmsnorm_fwd(_ptr(x), _ptr(gamma), _ptr(y), _ptr(inv_rms), rows, cols,
+                                   float(eps), _dtype_code(x), _stream(stream))
+        _check(rc, "agk_rmsnorm_fwd")
+        return y, inv_rms
+    if workspace is None:
+        need = rmsnorm_fwd_workspace_bytes(rows, cols)
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device) if need else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    rc = lib().agk_rmsnorm_fwd_ws(_ptr(x), _ptr(gamma), _ptr(y), _ptr(inv_rms), _ptr(workspace),
+                                  ws_bytes, rows, cols, float(eps), _dtype_code(x),
+                                  _stream(stream))
+    _check(rc, "agk_rmsnorm_fwd_ws")
     return y, inv_rms
 
 
@@ -316,16 +339,19 @@ def gemm_f32(a, b, c=None, trans_a: bool = False, trans_b: bool = False, accumul
     return c
 
 
-def launch_plan(rows: int, cols: int, dtype: int, backward: bool) -> dict:
-    """The launch shape agk_rmsnorm_{fwd,bwd} picks for these sizes (diagnostic).
+def launch_plan(rows: int, cols: int, dtype: int, backward, fwd_workspace: bool = False) -> dict:
+    """The launch shape agk_rmsnorm_{fwd,bwd} picks for these sizes (diagnostic;
+    fwd_workspace: the forward of agk_rmsnorm_fwd_ws given a workspace).
 
     tpr == 0 with nv > 0 is the split path: nv segments and g chunks per
     row, rpb rows per backward tile, nblk dgamma partial rows (0: the tiles
-    write dgamma directly).  g == 0 with tpr > 0 (backward) is the team
-    kernel: a row over tpr / 256 workgroups of nv slots per lane, nblk teams
-    (= dgamma partial rows) taking the rows in turn."""
+    write dgamma directly).  g == 0 with tpr > 0 (backward, or the forward
+    with a workspace) is the team kernel: a row over tpr / 256 workgroups of
+    nv slots per lane, nblk teams (the backward's dgamma partial rows) taking
+    the rows in turn."""
     out = (ctypes.c_int32 * 5)()
-    _check(lib().agk_rmsnorm_launch_plan(rows, cols, dtype, int(bool(backward)), out),
+    mode = 1 if backward else (2 if fwd_workspace else 0)
+    _check(lib().agk_rmsnorm_launch_plan(rows, cols, dtype, mode, out),
            "agk_rmsnorm_launch_plan")
     return {"tpr": out[0], "nv": out[1], "g": out[2], "rpb": out[3], "nblk": out[4]}
 
@@ -342,6 +368,13 @@ def set_team_backward(enabled: int) -> int:
     split path instead (measurement and testing knob).  Negative: read only.
     Returns the previous value."""
     return int(lib().agk_set_team_backward(int(enabled)))
+
+
+def set_team_forward(enabled: int) -> int:
+    """1 (default): agk_rmsnorm_fwd_ws may take the team kernel for wide rows;
+    0: the split path instead (measurement and testing knob).  Negative: read
+    only.  Returns the previous value."""
+    return int(lib().agk_set_team_forward(int(enabled)))
 
 
 def mul_rowbcast_fwd(a, b, y=None, stream=None):

@@ -187,6 +187,14 @@ Tensor zero_tangent(const Tensor& like) { return Tensor::zeros(like.shape(), lik
 
 namespace detail {
 
+// The exchange workspace of the RMSNorm forward's team kernel (rows wider
+// than one workgroup holds: x read once), from the pool on the current
+// stream; null when the shape needs none.
+static std::unique_ptr<Storage> rms_fwd_workspace(const Tensor& t, size_t* bytes) {
+    *bytes = agk_rmsnorm_fwd_workspace_bytes(t.rows(), t.cols());
+    return *bytes ? std::make_unique<Storage>(*bytes, current_stream()) : nullptr;
+}
+
 std::shared_ptr<Node> rms_nodeops(const std::shared_ptr<Node>& x) {
     require_value(x, "rms");
     const Tensor& xv = x->value;
@@ -194,8 +202,11 @@ std::shared_ptr<Node> rms_nodeops(const std::shared_ptr<Node>& x) {
     constexpr float kEps = 1e-5f;  // fixed, as cgadimpl/src/ops/normalization.cpp:26
     Tensor y = Tensor::empty(xv.shape(), xv.dtype());
     auto inv = std::make_shared<Tensor>(Tensor::empty(row_stat_shape(xv), Dtype::Float32));
-    agk_check(agk_rmsnorm_fwd(xv.data(), nullptr, y.data(), static_cast<float*>(inv->data()),
-                              xv.rows(), xv.cols(), kEps, agk_dtype_of(xv.dtype()), stream_arg()),
+    size_t ws_bytes = 0;
+    const std::unique_ptr<Storage> ws = rms_fwd_workspace(xv, &ws_bytes);
+    agk_check(agk_rmsnorm_fwd_ws(xv.data(), nullptr, y.data(), static_cast<float*>(inv->data()),
+                                 ws ? ws->data() : nullptr, ws_bytes, xv.rows(), xv.cols(), kEps,
+                                 agk_dtype_of(xv.dtype()), stream_arg()),
               "rms");
     auto n = std::make_shared<Node>(y, Op::RMSNorm, x->requires_grad(), "rmsnorm");
     n->eps = kEps;
@@ -218,8 +229,11 @@ std::shared_ptr<Node> rms_norm_nodeops(const std::shared_ptr<Node>& x,
     if (gv.dtype() != xv.dtype()) fail("rms_norm: gamma and x must have the same dtype");
     Tensor y = Tensor::empty(xv.shape(), xv.dtype());
     auto inv = std::make_shared<Tensor>(Tensor::empty(row_stat_shape(xv), Dtype::Float32));
-    agk_check(agk_rmsnorm_fwd(xv.data(), gv.data(), y.data(), static_cast<float*>(inv->data()),
-                              xv.rows(), xv.cols(), eps, agk_dtype_of(xv.dtype()), stream_arg()),
+    size_t ws_bytes = 0;
+    const std::unique_ptr<Storage> ws = rms_fwd_workspace(xv, &ws_bytes);
+    agk_check(agk_rmsnorm_fwd_ws(xv.data(), gv.data(), y.data(), static_cast<float*>(inv->data()),
+                                 ws ? ws->data() : nullptr, ws_bytes, xv.rows(), xv.cols(), eps,
+                                 agk_dtype_of(xv.dtype()), stream_arg()),
               "rms_norm");
     auto n = std::make_shared<Node>(y, Op::RMSNormAffine,
                                     x->requires_grad() || gamma->requires_grad(), "rms_norm");

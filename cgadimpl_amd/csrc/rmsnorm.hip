@@ -1162,15 +1162,22 @@ int launch_fwd_plan(const Plan& p, const void* x, const void* gamma, void* y, fl
     return AGK_EINVAL;
 }
 
+bool team_fwd_enabled();
+
+// ws: the team forward's slots (nullptr: none), at least
+// fwd_team_ws_bytes(rows, cols) bytes and 8-byte aligned (checked by the caller).
 template <class S>
 int launch_fwd(const void* x, const void* gamma, void* y, float* inv_rms, int64_t rows,
-               int cols, float eps, hipStream_t st) {
+               int cols, float eps, void* ws, hipStream_t st) {
     const bool vec = (cols % S::kVec) == 0 && aligned16(x) && aligned16(y) &&
                      (gamma == nullptr || aligned16(gamma));
     Plan p;
     if (vec) p = fwd_plan(cols / S::kVec, rows);
-    if (wide_fwd_eligible<S>(x, gamma, y, rows, cols, p.tpr != 0))
+    if (wide_fwd_eligible<S>(x, gamma, y, rows, cols, p.tpr != 0)) {
+        if (ws && team_fwd_enabled() && fwd_team_shape_ok(rows, cols))
+            return launch_wide_team_fwd<S>(x, gamma, y, inv_rms, ws, rows, cols, eps, st);
         return launch_wide_fwd<S>(x, gamma, y, inv_rms, rows, cols, eps, st);
+    }
     return launch_fwd_plan<S>(p, x, gamma, y, inv_rms, rows, cols, eps, st);
 }
 
@@ -1454,6 +1461,9 @@ int team_wait_polls() { return g_team_wait_polls.load(std::memory_order_relaxed)
 // Whether the team kernel may be taken (agk_set_team_backward).
 std::atomic<int> g_team_enabled{1};
 inline bool team_enabled() { return g_team_enabled.load(std::memory_order_relaxed) != 0; }
+// Whether the team forward may be taken (agk_set_team_forward).
+std::atomic<int> g_team_fwd_enabled{1};
+bool team_fwd_enabled() { return g_team_fwd_enabled.load(std::memory_order_relaxed) != 0; }
 
 // Bytes of dgamma partial rows the backward writes for these pointers and
 // sizes (the path launch_bwd takes): none for the few-rows kernel, 256 rows
@@ -1633,8 +1643,36 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms, i
     clear_pending_error();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (dtype == AGK_F32)
-        return launch_fwd<F32>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps, st);
-    return launch_fwd<BF16>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps, st);
+        return launch_fwd<F32>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps, nullptr,
+                               st);
+    return launch_fwd<BF16>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps, nullptr,
+                            st);
+}
+
+size_t agk_rmsnorm_fwd_workspace_bytes(int64_t rows, int64_t cols) {
+    if (agk::check_sizes(rows, cols) != AGK_OK) return 0;
+    return agk::fwd_team_ws_bytes(rows, cols);
+}
+
+int agk_rmsnorm_fwd_ws(const void* x, const void* gamma, void* y, float* inv_rms,
+                       void* workspace, size_t workspace_bytes, int64_t rows, int64_t cols,
+                       float eps, int dtype, agk_stream_t stream) {
+    using namespace agk;
+    if (int rc = check_sizes(rows, cols)) return rc;
+    if (!valid_dtype(dtype)) return AGK_EDTYPE;
+    if (rows == 0 || cols == 0) return AGK_OK;
+    if (!x || !y || !inv_rms) return AGK_EINVAL;
+    if (workspace) {
+        if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return AGK_EINVAL;
+        if (workspace_bytes < fwd_team_ws_bytes(rows, cols)) return AGK_EWORKSPACE;
+    }
+    clear_pending_error();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (dtype == AGK_F32)
+        return launch_fwd<F32>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps,
+                               workspace, st);
+    return launch_fwd<BF16>(x, gamma, y, inv_rms, rows, static_cast<int>(cols), eps, workspace,
+                            st);
 }
 
 size_t agk_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
@@ -1938,12 +1976,22 @@ int agk_set_team_backward(int enabled) {
     return prev;
 }
 
+int agk_set_team_forward(int enabled) {
+    const int prev = agk::g_team_fwd_enabled.load(std::memory_order_relaxed);
+    if (enabled >= 0)
+        agk::g_team_fwd_enabled.store(enabled != 0 ? 1 : 0, std::memory_order_relaxed);
+    return prev;
+}
+
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan) {
     using namespace agk;
     if (int rc = check_sizes(rows, cols)) return rc;
     if (!valid_dtype(dtype)) return AGK_EDTYPE;
     if (!plan) return AGK_EINVAL;
+    if (backward < 0 || backward > 2) return AGK_EINVAL;
+    const bool fwd_ws = backward == 2;  // a forward given a workspace
+    if (fwd_ws) backward = 0;
     const int w = dtype == AGK_F32 ? F32::kVec : BF16::kVec;
     Plan p;
     int64_t nblk = 0, rpb = 0;
@@ -1997,6 +2045,20 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
             plan[4] = static_cast<int32_t>(tp.teams);
             return AGK_OK;
         }
+    }
+    if (p.tpr == 0 && fwd_ws && cols > 0 && cols <= 0x7fffffffLL && team_fwd_enabled() &&
+        fwd_team_shape_ok(rows, cols) &&
+        (dtype == AGK_F32 ? wide_fwd_shape_ok<F32>(rows, static_cast<int>(cols), false)
+                          : wide_fwd_shape_ok<BF16>(rows, static_cast<int>(cols), false))) {
+        // the team forward: a row over `parts` workgroups of 256 lanes
+        const int segs = fwd_team_segs_for(dtype);
+        const TeamPlan tp = fwd_team_plan(rows, static_cast<int>(cols), segs);
+        plan[0] = static_cast<int32_t>(tp.parts * kWideLanes);
+        plan[1] = segs * kWideSegCols / (w * kWideLanes);
+        plan[2] = 0;
+        plan[3] = static_cast<int32_t>((rows + tp.teams - 1) / tp.teams);
+        plan[4] = static_cast<int32_t>(tp.teams);
+        return AGK_OK;
     }
     if (p.tpr == 0 && cols > 0 && cols <= 0x7fffffffLL) {
         // aligned stand-in pointers, and for the forward a y apart from x

@@ -1178,3 +1178,294 @@ int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms,
     if (dgamma) return launch_finalize(partials, dgamma, tp.teams, cols, acc_dg, st);
     return AGK_OK;
 }
+
+// ---- the forward in one read of x: teams ------------------------------------------
+// Given a workspace (agk_rmsnorm_fwd_ws), the rows the split forward takes,
+// of at most kTeamMaxSegs segments and at least kTeamMinRows rows, go to
+// teams of P workgroups as in the team backward (all 512 workgroups resident
+// at once at the kernel's register use): workgroup p owns segments
+// [p*SEGS, (p+1)*SEGS) (SEGS = fwd_team_segs), team t takes rows t, t+T, ...
+// (T = min(kFwdTeamWorkgroups / P, rows)).  Per row each workgroup
+//   1. sums x^2 over each of its segments as wide_row_stats does;
+//   2. publishes the sums in the row's slots and gathers the others with the
+//      team backward's bounded wait, recomputing a sum still missing after
+//      `wait_polls` polls from x itself (same arithmetic, same bits);
+//   3. adds the row's segment sums as wide_row_finish does and takes
+//      r = 1/sqrt(sum/cols + eps) (workgroup 0 of the team writes inv_rms);
+//   4. writes y = (x*r)*gamma as wide_fwd_scale does,
+// while the loads of the team's next row are in flight.  inv_rms and y are
+// the split path's bits, and x is read once (the split path reads it twice).
+// The slots are cleared by a fill kernel ahead of the launch, in stream
+// order, so a set flag means "written by this call".
+constexpr int64_t kFwdTeamWorkgroups = 512;
+
+// Segments per workgroup: 32 KiB of x per row for either dtype, which the
+// row's exchange is amortised over.  Measured on MI355X (graph-replayed
+// agk_rmsnorm_fwd_ws, 512 workgroups): fp32 [2048, 65536] 200 -> 176 us with
+// two segments against one, bf16 [8192, 131072] 925 -> 722 us with four
+// against two; four fp32 segments (241 VGPRs) ran 186 us at [2048, 65536],
+// and eight bf16 segments need 256 VGPRs, one wave per SIMD: too few for the
+// 512 workgroups to be resident together.  1024 workgroups of the narrower
+// parts measured between the two (fp32 189 us, bf16 816 us).
+template <class S>
+constexpr int fwd_team_segs() {
+    return S::kVec == 4 ? 2 : 4;
+}
+inline int fwd_team_segs_for(int dtype) { return dtype == AGK_F32 ? 2 : 4; }
+
+inline TeamPlan fwd_team_plan(int64_t rows, int cols, int segs) {
+    TeamPlan tp;
+    const int64_t part_cols = static_cast<int64_t>(segs) * kWideSegCols;
+    tp.parts = (cols + part_cols - 1) / part_cols;
+    const int64_t want = kFwdTeamWorkgroups / tp.parts > 0 ? kFwdTeamWorkgroups / tp.parts : 1;
+    tp.teams = want < rows ? want : rows;
+    return tp;
+}
+
+// The sizes the team forward can take (given the split forward's pointers):
+// at most kTeamMaxSegs segments and at least kTeamMinRows rows.
+inline bool fwd_team_shape_ok(int64_t rows, int64_t cols) {
+    const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
+    return cols >= kWideMinCols && nseg <= kTeamMaxSegs && rows >= kTeamMinRows;
+}
+// Bytes of the team forward's slots: one 8-byte word per (row, segment).
+// Depends only on rows and cols; 0 for sizes the team forward never takes.
+inline size_t fwd_team_ws_bytes(int64_t rows, int64_t cols) {
+    if (!fwd_team_shape_ok(rows, cols)) return 0;
+    const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
+    return static_cast<size_t>(rows) * static_cast<size_t>(nseg) * 8u;
+}
+
+template <class S, int kSegs>
+__global__ __launch_bounds__(kWideLanes) void wide_fwd_team(
+    const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
+    typename S::T* __restrict__ y, float* __restrict__ inv_rms, uint64_t* __restrict__ slots,
+    int64_t rows, int cols, int nseg, int nparts, int64_t nteams, float eps, int wait_polls) {
+    using T = typename S::T;
+    constexpr int W = S::kVec;
+    constexpr int NV = kWideSegCols / (W * kWideLanes);  // slots per lane per segment
+    constexpr int NS = kSegs * NV;
+    constexpr int kWaves = kWideLanes / 64;
+    constexpr int kPerLane = static_cast<int>(kTeamMaxSegs / 64);
+    // red, vals, missing and nmissing are written for the next row only after
+    // a barrier that every wave reaches after reading them for this one
+    __shared__ float red[kSegs][kWaves];
+    __shared__ float fb[kWaves];
+    __shared__ float vals[kTeamMaxSegs];
+    __shared__ unsigned char missing[kTeamMaxSegs];
+    __shared__ int nmissing;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int64_t team = static_cast<int64_t>(blockIdx.x) / nparts;
+    const int part = static_cast<int>(static_cast<int64_t>(blockIdx.x) - team * nparts);
+    const int seg0 = part * kSegs;
+    const uint32_t row_bytes = static_cast<uint32_t>(cols) * sizeof(T);
+    // slot q = s*NV + k of lane t: columns (seg0+s)*kWideSegCols + (t + k*256)*W ..
+    uint32_t off[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const int col = (seg0 + q / NV) * kWideSegCols + (t + (q % NV) * kWideLanes) * W;
+        off[q] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+    }
+    const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
+    u32x4 gv[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) gv[q] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+
+    struct Set {
+        u32x4 xv[NS];
+    };
+    auto issue = [&](Set& b, int64_t row) {
+        const bool live = row < rows;
+        const rsrc_t rx =
+            make_rsrc(x + (live ? row : 0) * static_cast<int64_t>(cols), live ? row_bytes : 0u);
+#pragma unroll
+        for (int q = 0; q < NS; ++q) b.xv[q] = bload16_stream(rx, off[q]);
+    };
+    // segment sg's sum of x^2 for `row`, recomputed by the whole workgroup
+    // with wide_row_stats' arithmetic (workgroup-uniform call)
+    auto recompute = [&](int64_t row, int sg) -> float {
+        const rsrc_t rx = make_rsrc(x + row * static_cast<int64_t>(cols), row_bytes);
+        u32x4 xv[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int col = sg * kWideSegCols + (t + k * kWideLanes) * W;
+            const uint32_t o = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
+            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+        }
+        float part_sum[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) part_sum[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float fx[W];
+            S::unpack(xv[k], fx);
+#pragma unroll
+            for (int e = 0; e < W; ++e) part_sum[e] += fx[e] * fx[e];
+        }
+        float v = 0.0f;
+#pragma unroll
+        for (int e = 0; e < W; ++e) v += part_sum[e];
+        v = group_sum<64>(v);
+        if (lane == 0) fb[wave] = v;
+        __syncthreads();
+        float a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) a += fb[w];
+        __syncthreads();
+        return a;
+    };
+
+    // One row: `cur` holds it; the loads of row `ahead` go into `fill` first.
+    auto step = [&](Set& cur, Set& fill, int64_t row, int64_t ahead) {
+        issue(fill, ahead);
+        // 1. per segment: x^2 summed as wide_row_stats sums it
+        float v[kSegs];
+#pragma unroll
+        for (int s = 0; s < kSegs; ++s) {
+            float part_sum[W];
+#pragma unroll
+            for (int e = 0; e < W; ++e) part_sum[e] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                float fx[W];
+                S::unpack(cur.xv[s * NV + k], fx);
+#pragma unroll
+                for (int e = 0; e < W; ++e) part_sum[e] += fx[e] * fx[e];
+            }
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < W; ++e) a += part_sum[e];
+            v[s] = group_sum<64>(a);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int s = 0; s < kSegs; ++s) red[s][wave] = v[s];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kSegs; ++s) {
+            float a = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) a += red[s][w];
+            v[s] = a;
+        }
+        // 2. publish this workgroup's sums, gather the row's others
+        uint64_t* rs = slots + row * static_cast<int64_t>(nseg);
+        if (t == 0) {
+#pragma unroll
+            for (int s = 0; s < kSegs; ++s)
+                if (seg0 + s < nseg) slot_publish(rs + seg0 + s, v[s]);
+        }
+        if (wave == 0) {
+            float val[kPerLane];
+            bool have[kPerLane];
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const int sg = lane + 64 * j;
+                const bool own = sg >= seg0 && sg < seg0 + kSegs;
+                have[j] = sg >= nseg || own;
+                val[j] = 0.0f;
+#pragma unroll
+                for (int s = 0; s < kSegs; ++s)
+                    if (sg == seg0 + s) val[j] = v[s];
+            }
+            for (int it = 0;; ++it) {
+                bool all = true;
+#pragma unroll
+                for (int j = 0; j < kPerLane; ++j) {
+                    if (!have[j]) {
+                        const uint64_t w = slot_read(rs + lane + 64 * j);
+                        if ((w >> 32) != 0) {
+                            have[j] = true;
+                            val[j] = __uint_as_float(static_cast<uint32_t>(w));
+                        } else {
+                            all = false;
+                        }
+                    }
+                }
+                if (__all(all) || it >= wait_polls) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            bool miss = false;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                const int sg = lane + 64 * j;
+                if (sg < nseg) {
+                    vals[sg] = val[j];
+                    missing[sg] = have[j] ? 0 : 1;
+                    miss = miss || !have[j];
+                }
+            }
+            const int any_miss = __any(miss);
+            if (lane == 0) nmissing = any_miss;
+        }
+        __syncthreads();
+        if (nmissing != 0) {  // workgroup-uniform: a wait ran out
+            for (int sg = 0; sg < nseg; ++sg) {
+                if (!missing[sg]) continue;  // uniform (LDS)
+                const float a = recompute(row, sg);
+                if (t == 0) vals[sg] = a;
+            }
+            __syncthreads();
+        }
+        // 3. the row's sum as wide_row_finish adds it, then r
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int sg = lane + 64 * j;
+            ss += sg < nseg ? vals[sg] : 0.0f;
+        }
+        ss = group_sum<64>(ss);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+        if (part == 0 && t == 0) inv_rms[row] = r;
+        // 4. y = (x*r)*gamma
+        const rsrc_t ry = make_rsrc(y + row * static_cast<int64_t>(cols), row_bytes);
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+            float f[W];
+            S::unpack(cur.xv[q], f);
+            if (gamma) {
+                float gm[W];
+                S::unpack(gv[q], gm);
+#pragma unroll
+                for (int e = 0; e < W; ++e) f[e] = (f[e] * r) * gm[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < W; ++e) f[e] = f[e] * r;
+            }
+            bstore16_stream(ry, off[q], S::pack(f));
+        }
+    };
+    // Two register sets in turn, as the team backward (unrolled by two, so no
+    // set is copied).
+    int64_t row = team;
+    Set a, b;
+    issue(a, row);
+    for (;;) {
+        step(a, b, row, row + nteams);
+        if ((row += nteams) >= rows) break;
+        step(b, a, row, row + nteams);
+        if ((row += nteams) >= rows) break;
+    }
+}
+
+// ws: at least fwd_team_ws_bytes(rows, cols) bytes, 8-byte aligned (checked
+// by the caller).
+template <class S>
+int launch_wide_team_fwd(const void* x, const void* gamma, void* y, float* inv_rms, void* ws,
+                         int64_t rows, int cols, float eps, hipStream_t st) {
+    using T = typename S::T;
+    constexpr int kSegs = fwd_team_segs<S>();
+    const TeamPlan tp = fwd_team_plan(rows, cols, kSegs);
+    const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
+    const int64_t grid = tp.teams * tp.parts;
+    if (grid > 0x7fffffffLL || nseg > kTeamMaxSegs) return AGK_EINVAL;
+    uint64_t* slots = static_cast<uint64_t*>(ws);
+    if (int rc = zero_fill(static_cast<float*>(ws), rows * nseg * 2, st)) return rc;
+    hipLaunchKernelGGL((wide_fwd_team<S, kSegs>), dim3(static_cast<unsigned>(grid)),
+                       dim3(kWideLanes), 0, st, static_cast<const T*>(x),
+                       static_cast<const T*>(gamma), static_cast<T*>(y), inv_rms, slots, rows,
+                       cols, static_cast<int>(nseg), static_cast<int>(tp.parts), tp.teams, eps,
+                       team_wait_polls());
+    return check_launch();
+}

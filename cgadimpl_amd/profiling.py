@@ -497,7 +497,10 @@ def write_wide_summary(jsonl, out_md, command):
              "Command:", "", "```", command, "```", "",
              "Each call captured into a HIP graph and replayed (GPU time per call, best of 5 "
              "replays). Forward: out of place (the split path for rows too wide for "
-             "registers) against in place (y = x keeps one workgroup per row). Backward "
+             "registers: x read twice), the same with a workspace (agk_rmsnorm_fwd_ws, "
+             "'fwd ws': the team kernel where 'fwd ws path' names it -- a row over that many "
+             "workgroups exchanging partial sums, x read once -- else the same kernels), "
+             "and in place (y = x keeps one workgroup per row). Backward "
              "(dx and dgamma) and dx alone: as the library takes them with a workspace "
              "('path': the one-pass kernel for rows of up to 32768 columns from 256 rows, "
              "the team kernel -- a row over that many workgroups exchanging partial sums -- "
@@ -506,17 +509,21 @@ def write_wide_summary(jsonl, out_md, command):
              "without a workspace (looped). GB/s: algorithmic bytes (forward 2 tensors, "
              "backward 3) over the time; % of 8 TB/s in brackets.",
              "",
-             "| shape | bwd path | fwd split us | fwd in place us | bwd us | bwd split us | "
-             "bwd dx us | bwd dx split us | bwd dx looped us | fwd split GB/s | bwd GB/s | "
-             "bwd split GB/s |",
-             "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+             "| shape | fwd ws path | bwd path | fwd split us | fwd ws us | fwd in place us | "
+             "bwd us | bwd split us | bwd dx us | bwd dx split us | bwd dx looped us | "
+             "fwd split GB/s | fwd ws GB/s | bwd GB/s | bwd split GB/s |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
     for r in recs:
         u, g = r["us"], r["gbs"]
-        lines.append(f"| {r['wide_rows']} | {_wide_bwd_path(r['bwd_plan'])} | "
-                     f"{u['fwd_split']} | {u['fwd_in_place']} | {u['bwd']} | "
+        fwp = r.get("fwd_ws_plan", {})
+        fpath = (f"team of {fwp['tpr'] // 256}" if fwp.get("g") == 0 and fwp.get("tpr")
+                 else ("split" if r["fwd_plan"]["tpr"] == 0 else "resident"))
+        lines.append(f"| {r['wide_rows']} | {fpath} | {_wide_bwd_path(r['bwd_plan'])} | "
+                     f"{u['fwd_split']} | {u['fwd_ws']} | {u['fwd_in_place']} | {u['bwd']} | "
                      f"{u['bwd_split']} | {u['bwd_dx']} | {u['bwd_dx_split']} | "
                      f"{u['bwd_dx_looped']} | "
                      f"{g['fwd_split']:.0f} ({g['fwd_split'] / 80:.1f} %) | "
+                     f"{g['fwd_ws']:.0f} ({g['fwd_ws'] / 80:.1f} %) | "
                      f"{g['bwd']:.0f} ({g['bwd'] / 80:.1f} %) | "
                      f"{g['bwd_split']:.0f} ({g['bwd_split'] / 80:.1f} %) |")
     ro = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith('{"wide_rowops"')]

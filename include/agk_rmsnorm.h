@@ -89,6 +89,26 @@ int agk_rmsnorm_fwd(const void* x, const void* gamma, void* y, float* inv_rms,
                     int64_t rows, int64_t cols, float eps, int dtype,
                     agk_stream_t stream);
 
+/* agk_rmsnorm_fwd with a workspace: the same results (y and inv_rms bit-
+ * identical to agk_rmsnorm_fwd's on the same inputs), computed with one HBM
+ * read of x for rows of AGK_WIDE_MIN_COLS to 1048576 columns, at least 4 of
+ * them, that the split path would take (16-byte aligned, y apart from x):
+ * each row is held by several workgroups that exchange their partial sums of
+ * squares through the workspace (agk_rmsnorm_fwd reads such rows twice).
+ * Same reference as agk_rmsnorm_fwd (rms_nodeops, normalization.cpp:23-35;
+ * mul_nodeops, arithmetic.cpp:31-39).  workspace == NULL is agk_rmsnorm_fwd;
+ * otherwise it must be 8-byte aligned (AGK_EINVAL) and hold at least
+ * agk_rmsnorm_fwd_workspace_bytes(rows, cols) bytes (AGK_EWORKSPACE):
+ * rows * ceil(cols / 4096) * 8 bytes for those sizes, 0 for others.  The
+ * workspace is scratch (its contents on entry do not matter), and calls that
+ * share one must not overlap in time.  No reference counterpart for the
+ * workspace itself: the reference's forward allocates its intermediates.    */
+size_t agk_rmsnorm_fwd_workspace_bytes(int64_t rows, int64_t cols);
+
+int agk_rmsnorm_fwd_ws(const void* x, const void* gamma, void* y, float* inv_rms,
+                       void* workspace, size_t workspace_bytes, int64_t rows,
+                       int64_t cols, float eps, int dtype, agk_stream_t stream);
+
 /* Bytes of workspace agk_rmsnorm_bwd needs for these sizes: fp32 dgamma
  * partials, one row of cols floats per workgroup.  The size is nblk * cols * 4
  * bytes with nblk = ceil(rows / rpb), rpb = ceil(rows / 1024) rows (at least
@@ -304,29 +324,10 @@ size_t agk_gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K, int a_tran
 int agk_transpose_bf16(const void* src, int64_t ld_src, void* dst, int64_t ld_dst,
                        int64_t rows, int64_t cols, agk_stream_t stream);
 
-/* Diagnostic, with no counterpart in the reference: the launch shape the
- * library picks for a forward (backward = 0) or backward (backward != 0)
- * call of these sizes with 16-byte aligned pointers.  plan[5] receives
- *   {lanes per row, 16-byte slots per lane, rows per workgroup,
- *    rows per dgamma partial row (backward; ceil(rows / partial rows)),
- *    dgamma partial rows (backward)};
- * rows per workgroup == 0 (backward) is the team kernel: a row held by
- * lanes per row / 256 workgroups of 256 lanes that exchange their partial
- * sums (4096 fp32 or 8192 bf16 columns each), the teams taking the rows in
- * turn;
- * lanes per row == 0 means a path that does not keep rows in registers:
- * the split path when slots per lane > 0 (then plan[1] = 4096-column
- * segments per row, plan[2] = 2048-column chunks per row, and for the
- * backward plan[3] = rows per tile, plan[4] = dgamma partial rows, 0 when
- * the tiles write dgamma directly), else the looped kernel (rows that are
- * not a whole number of 16-byte slots, or too wide for registers and not
- * split).  A resident backward of at most 255 rows reports 0 partial rows:
- * it runs row and column workgroups in one launch and writes dgamma
- * directly.  Used by the tests to run every reachable shape.                 */
 /* Testing knob, with no counterpart in the reference: how many times a
- * workgroup of the team kernel (the wide backward) polls for the other
- * workgroups' partial sums of a row before it recomputes a missing one from
- * x, dy and gamma itself (the same bits; default 4096).  polls >= 0 sets it
+ * workgroup of a team kernel (the wide backward, agk_rmsnorm_fwd_ws) polls
+ * for the other workgroups' partial sums of a row before it recomputes a
+ * missing one from the inputs itself (the same bits; default 4096).  polls >= 0 sets it
  * for the process; a negative value only reads it.  Returns the previous
  * value.  0 makes every wait end at its first look, so the tests can run the
  * recompute path; the results do not change.                                */
@@ -339,6 +340,34 @@ int agk_set_exchange_wait_limit(int polls);
  * Process-wide; returns the previous value (1 or 0).                         */
 int agk_set_team_backward(int enabled);
 
+/* Testing and measurement knob, with no counterpart in the reference:
+ * enabled = 0 keeps agk_rmsnorm_fwd_ws off the team kernel (wide rows then
+ * take agk_rmsnorm_fwd's split path), 1 restores the default; a negative
+ * value only reads it.  Process-wide; returns the previous value (1 or 0).  */
+int agk_set_team_forward(int enabled);
+
+/* Diagnostic, with no counterpart in the reference: the launch shape the
+ * library picks for a forward (backward = 0), backward (backward = 1) or
+ * forward given a workspace (agk_rmsnorm_fwd_ws; backward = 2) call of
+ * these sizes with 16-byte aligned pointers (other values: AGK_EINVAL).
+ * plan[5] receives
+ *   {lanes per row, 16-byte slots per lane, rows per workgroup,
+ *    rows per dgamma partial row (backward; ceil(rows / partial rows)),
+ *    dgamma partial rows (backward)};
+ * rows per workgroup == 0 (backward, or forward given a workspace) is a team
+ * kernel: a row held by lanes per row / 256 workgroups of 256 lanes that
+ * exchange their partial sums (backward: 4096 fp32 or 8192 bf16 columns
+ * each; forward: 8192 fp32 or 16384 bf16), the teams taking the rows in turn
+ * (plan[3] = rows per team, plan[4] = teams);
+ * lanes per row == 0 means a path that does not keep rows in registers:
+ * the split path when slots per lane > 0 (then plan[1] = 4096-column
+ * segments per row, plan[2] = 2048-column chunks per row, and for the
+ * backward plan[3] = rows per tile, plan[4] = dgamma partial rows, 0 when
+ * the tiles write dgamma directly), else the looped kernel (rows that are
+ * not a whole number of 16-byte slots, or too wide for registers and not
+ * split).  A resident backward of at most 255 rows reports 0 partial rows:
+ * it runs row and column workgroups in one launch and writes dgamma
+ * directly.  Used by the tests to run every reachable shape.                 */
 int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                             int32_t* plan);
 

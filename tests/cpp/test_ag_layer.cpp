@@ -838,6 +838,45 @@ void test_wide_softmax() {
     }
 }
 
+// rms_norm and rms on rows too wide for one workgroup: the forward's team
+// kernel (x read once, its exchange workspace from the graph layer's pool)
+// and the backward's, against host double precision.
+void test_wide_rms() {
+    for (int64_t D : {int64_t{40000}, int64_t{70000}}) {
+        const int64_t R = 5;
+        const double eps = 1e-5;
+        std::vector<float> xf = normal(R * D, 80 + D), gf = uniform(D, 81 + D, 0.5, 1.5),
+                           dyf = normal(R * D, 82 + D);
+        const Vec xd = to_d(xf), gd = to_d(gf);
+        Value x = leaf(xf, {R, D}, "x"), g = leaf(gf, {D}, "g");
+        Tensor dy = Tensor::from_host_f32(dyf, {R, D});
+        Value y = rms_norm(x, g, 1e-5f);
+        backward(y, &dy);
+        Value x2 = leaf(xf, {R, D}, "x2");
+        Value h = rms(x2);
+        const Vec ys = host_rms_layer(xd, &gd, R, D, eps), hs = host_rms_layer(xd, nullptr, R, D, eps);
+        Vec dx(R * D), dg(D, 0.0);
+        for (int64_t i = 0; i < R; ++i) {
+            double ss = 0.0, dot = 0.0;
+            for (int64_t j = 0; j < D; ++j) ss += xd[i * D + j] * xd[i * D + j];
+            const double r = 1.0 / std::sqrt(ss / D + eps);
+            for (int64_t j = 0; j < D; ++j) dot += dyf[i * D + j] * gd[j] * xd[i * D + j];
+            for (int64_t j = 0; j < D; ++j) {
+                dx[i * D + j] = r * (dyf[i * D + j] * gd[j] - xd[i * D + j] * r * r * dot / D);
+                dg[j] += dyf[i * D + j] * xd[i * D + j] * r;
+            }
+        }
+        const std::string tag = "rms_norm [5," + std::to_string(D) + "] (team kernels)";
+        const double ey = rel_err(y.val().to_host_f32(), ys), eh = rel_err(h.val().to_host_f32(), hs);
+        const double ex = rel_err(x.grad().to_host_f32(), dx), eg = rel_err(g.grad().to_host_f32(), dg);
+        report((tag + " forward == host").c_str(), ey <= 1e-5, std::to_string(ey));
+        report(("rms [5," + std::to_string(D) + "] forward == host").c_str(), eh <= 1e-5,
+               std::to_string(eh));
+        report((tag + " dx == host").c_str(), ex <= 1e-5, std::to_string(ex));
+        report((tag + " dgamma == host").c_str(), eg <= 1e-5, std::to_string(eg));
+    }
+}
+
 void test_row_ops_gradients() {
     // the reference pattern: [4,10] input, numerical gradient of sum(f(a))
     Value a = leaf(normal(40, 60), {4, 10}, "a");
@@ -1487,6 +1526,7 @@ int selftest(const std::vector<std::string>& only) {
         {"user_stream", test_user_stream},
         {"row_ops_gradients", test_row_ops_gradients},
         {"wide_softmax", test_wide_softmax},
+        {"wide_rms", test_wide_rms},
         {"jvp", test_jvp},
         {"matmul_layer", test_matmul_layer},
         {"linear_layer", test_linear_layer},

@@ -31,7 +31,8 @@ def declared_functions():
 
 def test_header_declares_expected_entry_points():
     fns = declared_functions()
-    for want in ("agk_rmsnorm_fwd", "agk_rmsnorm_bwd", "agk_rmsnorm_bwd_workspace_bytes",
+    for want in ("agk_rmsnorm_fwd", "agk_rmsnorm_fwd_ws", "agk_rmsnorm_bwd",
+                 "agk_rmsnorm_bwd_workspace_bytes",
                  "agk_status_str", "agk_rmsnorm_jvp", "agk_layernorm_fwd", "agk_layernorm_bwd",
                  "agk_softmax_fwd", "agk_softmax_bwd", "agk_logsumexp_fwd", "agk_logsumexp_bwd",
                  "agk_logsumexp_jvp", "agk_gemm_bf16"):
@@ -171,6 +172,59 @@ def test_wide_row_plans_and_workspace():
             else:
                 assert fp["tpr"] == 0, label
                 assert (fp["nv"], fp["g"]) == (-(-cols // 4096), -(-cols // 2048)), label
+
+
+def _fwd_ws_rule(rows, cols):
+    """The documented workspace of agk_rmsnorm_fwd_ws: one 8-byte word per
+    row and 4096-column segment for 4+ rows of 16385 to 1M columns, else 0."""
+    nseg = -(-cols // 4096)
+    return rows * nseg * 8 if cols >= 16385 and nseg <= 256 and rows >= 4 else 0
+
+
+def test_forward_team_plans_and_workspace():
+    """agk_rmsnorm_fwd_ws: its workspace rule, the plan diagnostic's team
+    forward (mode 2) wherever agk_rmsnorm_fwd would take the split path
+    (32 KiB of the row per workgroup: 8192 fp32 or 16384 bf16 columns,
+    min(512 // parts, rows) teams), the same plan as agk_rmsnorm_fwd elsewhere
+    or with the team switched off, and validation before any HIP call."""
+    lib = agk.lib()
+    wb = lib.agk_rmsnorm_fwd_workspace_bytes
+    for rows, cols in [(8, 262144), (300, 65536), (4, 1 << 20), (7, 50000), (3, 65536),
+                       (5, 1 << 21), (600, 40000), (9, 16384), (9, 16385), (0, 65536)]:
+        assert wb(rows, cols) == _fwd_ws_rule(rows, cols), (rows, cols)
+    assert wb(300, 65536) == 300 * 16 * 8
+    for rows, cols in [(8, 262144), (300, 65536), (4, 1 << 20), (7, 50000), (3, 65536),
+                       (5, 1 << 21), (600, 40000), (6, 70008), (9, 16388), (5, 40002)]:
+        for dt, w in ((agk.AGK_F32, 4), (agk.AGK_BF16, 8)):
+            label = (rows, cols, dt)
+            plain = agk.launch_plan(rows, cols, dt, False)
+            team = agk.launch_plan(rows, cols, dt, False, fwd_workspace=True)
+            split = plain["tpr"] == 0 and plain["nv"] > 0
+            if split and _fwd_ws_rule(rows, cols):
+                part = 8192 if w == 4 else 16384
+                parts = -(-cols // part)
+                teams = min(max(512 // parts, 1), rows)
+                assert team == {"tpr": 256 * parts, "nv": 8, "g": 0,
+                                "rpb": -(-rows // teams), "nblk": teams}, label
+            else:
+                assert team == plain, label
+    assert agk.launch_plan(300, 65536, agk.AGK_F32, False, fwd_workspace=True)["g"] == 0
+    prev = agk.set_team_forward(0)
+    try:
+        assert agk.launch_plan(300, 65536, agk.AGK_F32, False, fwd_workspace=True) == \
+            agk.launch_plan(300, 65536, agk.AGK_F32, False)
+    finally:
+        agk.set_team_forward(prev)
+    assert agk.set_team_forward(-1) == prev
+    assert lib.agk_rmsnorm_launch_plan(8, 65536, 0, 3, (ctypes.c_int32 * 5)()) == 1
+    f = lib.agk_rmsnorm_fwd_ws
+    need = wb(4, 65536)
+    assert f(FAKE, None, FAKE, FAKE, FAKE, need - 1, 4, 65536, 1e-6, 0, None) == 3
+    assert f(FAKE, None, FAKE, FAKE, FAKE + 4, need, 4, 65536, 1e-6, 0, None) == 1
+    assert f(None, None, FAKE, FAKE, FAKE, need, 4, 65536, 1e-6, 0, None) == 1
+    assert f(FAKE, None, FAKE, None, None, 0, 4, 65536, 1e-6, 0, None) == 1
+    assert f(FAKE, None, FAKE, FAKE, None, 0, 4, 65536, 1e-6, 9, None) == 2
+    assert f(None, None, None, None, None, 0, 0, 65536, 1e-6, 0, None) == 0
 
 
 def test_launch_plans_are_well_formed():

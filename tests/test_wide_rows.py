@@ -1,5 +1,7 @@
-"""Rows wider than the register-resident shapes: the split forward (several
-workgroups per row for the row statistics, then row-chunk scaling), and
+"""Rows wider than the register-resident shapes: two forward paths -- the
+split forward (several workgroups per row for the row statistics, then
+row-chunk scaling) and, given a workspace, the team forward (a row over
+several workgroups that exchange their segment sums: x read once) -- and
 three backward paths: from 256 rows of at most 32768 columns the one-pass
 kernel (x and dy in registers, dgamma in LDS); other aligned rows of up to
 1M columns the team kernel (a row over several workgroups that exchange
@@ -169,6 +171,74 @@ def test_team_against_split_and_recompute(cuda, dtype, rows, cols, with_gamma):
     assert e_dx <= _tol(x) and e_team <= TOL_F32 and e_split <= TOL_F32
 
 
+# Team forward shapes (agk_rmsnorm_fwd_ws): more rows than teams, a ragged
+# last segment (fp32) and an odd segment count (bf16 parts of two), the
+# widest rows it takes (256 segments), the fewest rows it takes (4).
+FWD_TEAM_CASES = [("f32", 600, 40000), ("f32", 7, 50000), ("f32", 4, 1 << 20),
+                  ("f32", 300, 65536), ("bf16", 100, 131072), ("bf16", 5, 131080),
+                  ("bf16", 6, 70008), ("bf16", 4, 1 << 20)]
+
+
+@pytest.mark.parametrize("dtype,rows,cols", FWD_TEAM_CASES, ids=str)
+@pytest.mark.parametrize("with_gamma", [True, False], ids=["gamma", "no_gamma"])
+def test_team_forward_against_split_and_recompute(cuda, dtype, rows, cols, with_gamma):
+    """agk_rmsnorm_fwd_ws (the team kernel, x read once) against
+    agk_rmsnorm_fwd (the split path, x read twice) on the same inputs: y and
+    inv_rms bit-identical, since both add the same 4096-column segment sums in
+    the same order and apply the same per-element formula.  The workspace
+    starts with every flag set (its contents on entry must not matter).  With
+    every wait cut to its first look (wait limit 0: the workgroups recompute
+    the sums they do not find yet) bit-identical again.  Against the oracle."""
+    import torch
+    x, g, _ = configs.make_inputs((rows, cols), dtype=dtype, with_gamma=with_gamma,
+                                  with_dy=False, seed=rows * 11 + cols)
+    xd = to_dev(x, cuda)
+    gd = to_dev(g, cuda) if with_gamma else None
+    plan = agk.launch_plan(rows, cols, _dt(dtype), False, fwd_workspace=True)
+    print(f"team fwd {dtype} {rows}x{cols} gamma={with_gamma} plan {plan}", flush=True)
+    assert plan["tpr"] > 0 and plan["g"] == 0
+    ws = torch.full((agk.rmsnorm_fwd_workspace_bytes(rows, cols),), 255, dtype=torch.uint8,
+                    device=cuda)
+    team_y, team_inv = agk.rmsnorm_fwd(xd, gd, 1e-6, workspace=ws)
+    split_y, split_inv = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    prev = agk.set_exchange_wait_limit(0)
+    try:
+        rec_y, rec_inv = agk.rmsnorm_fwd(xd, gd, 1e-6, workspace=ws)
+    finally:
+        agk.set_exchange_wait_limit(prev)
+    torch.cuda.synchronize()
+    assert torch.equal(team_inv, split_inv) and torch.equal(team_y, split_y)
+    assert torch.equal(rec_inv, team_inv) and torch.equal(rec_y, team_y)
+    ry, rinv = oracle.fwd(x, g if with_gamma else None, 1e-6)
+    ey = row_rel_err(as_f32(to_host(team_y)), as_f32(ry))
+    ei = vec_rel_err(to_host(team_inv), rinv)
+    print(f"  y {ey:.2e} inv_rms {ei:.2e}", flush=True)
+    assert ey <= _tol(x) and ei <= TOL_F32
+
+
+@pytest.mark.parametrize("rows,cols,in_place", [(3, 65536, False), (4, 65536, True),
+                                                (4, 40002, False), (5, 16384, False)],
+                         ids=str)
+def test_team_forward_fallbacks(cuda, rows, cols, in_place):
+    """agk_rmsnorm_fwd_ws where its team kernel does not apply -- fewer than 4
+    rows, y == x, rows that are not whole 16-byte slots, rows one workgroup
+    holds -- runs agk_rmsnorm_fwd's kernels: bit-identical to it."""
+    import torch
+    x, g, _ = configs.make_inputs((rows, cols), with_dy=False, seed=cols + rows)
+    xd, gd = to_dev(x, cuda), to_dev(g, cuda)
+    ws = torch.empty(max(agk.rmsnorm_fwd_workspace_bytes(rows, cols), 8), dtype=torch.uint8,
+                     device=cuda)
+    if in_place:
+        a, b = xd.clone(), xd.clone()
+        ya, inva = agk.rmsnorm_fwd(a, gd, 1e-6, y=a, workspace=ws)
+        yb, invb = agk.rmsnorm_fwd(b, gd, 1e-6, y=b)
+    else:
+        ya, inva = agk.rmsnorm_fwd(xd, gd, 1e-6, workspace=ws)
+        yb, invb = agk.rmsnorm_fwd(xd, gd, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb) and torch.equal(inva, invb)
+
+
 def test_team_is_deterministic(cuda):
     """Three calls of the team kernel on the same inputs: every bit equal."""
     import torch
@@ -298,12 +368,14 @@ def test_wide_workspace_size(cuda):
 
 
 @pytest.mark.parametrize("rows,cols", [(6, 65536), (300, 24576)], ids=str)
-def test_wide_paths_under_graph_capture(cuda, rows, cols):
-    """A forward and backward call (the split forward; the split or the one-pass
-    backward, with their partial sums in y and the workspace) captured once into
-    a HIP graph: three replays on new inputs, with eager calls and
-    synchronisations between them, each bit-identical to the eager calls on the
-    same inputs."""
+@pytest.mark.parametrize("fwd_ws", [False, True], ids=["fwd", "fwd_ws"])
+def test_wide_paths_under_graph_capture(cuda, rows, cols, fwd_ws):
+    """A forward and backward call (the split forward, or with fwd_ws the
+    team forward and its slot-clearing fill kernel; the team or the one-pass
+    backward, with their partial sums in y and the workspaces) captured once
+    into a HIP graph: three replays on new inputs, with eager calls and
+    synchronisations between them, each bit-identical to the eager calls on
+    the same inputs."""
     import torch
     x = torch.empty(rows, cols, device=cuda)
     dy = torch.empty_like(x)
@@ -312,13 +384,17 @@ def test_wide_paths_under_graph_capture(cuda, rows, cols):
     inv = torch.empty(rows, device=cuda)
     dg = torch.empty(cols, device=cuda)
     ws = torch.empty(agk.rmsnorm_bwd_workspace_bytes(rows, cols), dtype=torch.uint8, device=cuda)
+    fws = False
+    if fwd_ws:
+        fws = torch.empty(max(agk.rmsnorm_fwd_workspace_bytes(rows, cols), 8), dtype=torch.uint8,
+                          device=cuda)
     x.normal_()
     dy.normal_()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         st = torch.cuda.current_stream()
-        agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, stream=st)
+        agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, workspace=fws, stream=st)
         agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws, stream=st)
     gen = torch.Generator(device=cuda)
     for k in range(3):
