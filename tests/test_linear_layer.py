@@ -4,7 +4,8 @@ the reference graph (bf16 storage, exact products, dW in fp32).
 
 Small shapes run the oracle on every element (including K not a multiple of
 64, which takes the staging kernel); the full configuration is checked on
-sampled rows and columns and through the RMSNorm VJP of the GPU's own dh.
+every element against torch's fp32 products of the same bf16 operands and
+the oracle's RMSNorm VJP of an independently computed dh.
 """
 import numpy as np
 import pytest
@@ -52,7 +53,16 @@ def test_layer_against_oracle(cuda, M, K, N):
 
 
 def test_layer_full_size(cuda):
-    """c5: x [8192, 4096], W [4096, 11008], dy [8192, 11008], bf16."""
+    """c5: x [8192, 4096], W [4096, 11008], dy [8192, 11008], bf16, every output
+    element checked.  The references are fp32 products computed by torch on
+    the GPU (its own GEMM, not this library's) from the same bf16 operands:
+    h against the RMSNorm in fp32 (every row), y against h @ W (every row,
+    from the layer's own h, which the first check pins), dW against h^T @ dy
+    (every element), dx against the CPU oracle's RMSNorm VJP of an
+    independent dh = bf16(dy @ W^T) on every row, dgamma against an fp64 sum
+    over that independent dh (each column against the sum of its terms'
+    magnitudes) and, tighter, over the library's own dh (the GEMM is
+    deterministic, so a second call gives the dh the backward used)."""
     import torch
     M, K, N = 8192, 4096, 11008
     gen = torch.Generator(device=cuda)
@@ -65,27 +75,43 @@ def test_layer_full_size(cuda):
     y, h, inv = agk.rmsnorm_linear_fwd(x, g, W, eps)
     dx, dgamma, dW = agk.rmsnorm_linear_bwd(x, g, inv, h, W, dy)
     torch.cuda.synchronize()
-    rows = torch.randint(0, M, (48,), generator=gen, device=cuda)
-    ry = h[rows].float() @ W.float()
-    assert ((y[rows].float() - ry).abs().max() / ry.abs().max()).item() <= 8e-3
-    cols = torch.randint(0, K, (16,), generator=gen, device=cuda)
-    rdW = h[:, cols].float().t() @ dy.float()
-    assert ((dW[cols] - rdW).abs().max() / rdW.abs().max()).item() <= 1e-5
-    # dx, dgamma: the RMSNorm VJP of dh = dy W^T, on sampled rows against the oracle
-    dh = (dy[rows].float() @ W.float().t()).bfloat16()
-    xs, dhs = to_host(x[rows].contiguous()), to_host(dh)
-    _, rinv = oracle.fwd(xs, to_host(g), eps)
-    rdx, _ = oracle.bwd(xs, to_host(g), rinv, dhs)
-    e = dx_rel_err(as_f32(to_host(dx[rows].contiguous())), as_f32(rdx), as_f32(xs),
-                   as_f32(to_host(g)), as_f32(dhs), eps)
-    assert e <= TOL_BF16, e
-    # dgamma over all 8192 rows against an fp64 reduction of the same dh (the
-    # GEMM is deterministic, so a second dh = dy W^T is the one the backward
-    # used): dgamma[j] = sum_i dh[i, j] * x[i, j] * inv_rms[i]
-    dh_all = agk.gemm_bf16(dy, W, trans_b=True)
-    rdg = (dh_all.double() * x.double() * inv.double().view(M, 1)).sum(dim=0)
-    e = ((dgamma.double() - rdg).abs().max() / rdg.abs().max()).item()
-    assert e <= 1e-5, e
+
+    def rows_err(got, ref):
+        """max over rows of max|got - ref| / max|ref| (the row_rel_err form)."""
+        num = (got.float() - ref).abs().amax(dim=1)
+        return (num / ref.abs().amax(dim=1).clamp_min(1e-30)).max().item()
+
+    xf, gf, Wf, dyf = x.float(), g.float(), W.float(), dy.float()
+    rinv = torch.rsqrt(xf.pow(2).mean(dim=1, keepdim=True) + eps)
+    e_h = rows_err(h, xf * rinv * gf)
+    e_inv = ((inv.view(M, 1) - rinv).abs() / rinv).max().item()
+    e_y = rows_err(y, h.float() @ Wf)
+    rdW = h.float().t() @ dyf
+    e_dW = ((dW - rdW).abs().max() / rdW.abs().max()).item()
+    del rdW
+    dh_ref = (dyf @ Wf.t()).bfloat16()
+    print(f"c5 full size: h {e_h:.2e} inv_rms {e_inv:.2e} y {e_y:.2e} dW {e_dW:.2e}", flush=True)
+    assert e_h <= TOL_BF16 and e_inv <= 1e-5 and e_y <= 8e-3 and e_dW <= 1e-5
+    # dx on every row: the oracle's VJP of the independent dh.  That dh and the
+    # library's can differ by one bf16 unit (2^-8) where their fp32 sums round
+    # apart, and both dx are rounded to bf16 (2^-9 each): at most ~7.8e-3 of a
+    # row's dx scale, under the bf16 bar
+    xs, dhs, gs = to_host(x), to_host(dh_ref), to_host(g)
+    _, oinv = oracle.fwd(xs, gs, eps)
+    rdx, _ = oracle.bwd(xs, gs, oinv, dhs)
+    e_dx = dx_rel_err(as_f32(to_host(dx)), as_f32(rdx), as_f32(xs), as_f32(gs), as_f32(dhs), eps)
+    # dgamma: each column against the sum of its terms' magnitudes, over the
+    # independent dh; then norm-wise over the library's own dh
+    terms = dh_ref.double() * x.double() * inv.double().view(M, 1)
+    rdg = terms.sum(dim=0)
+    e_dg_ind = ((dgamma.double() - rdg).abs() / terms.abs().sum(dim=0)).max().item()
+    del terms
+    dh_own = agk.gemm_bf16(dy, W, trans_b=True)
+    rdg_own = (dh_own.double() * x.double() * inv.double().view(M, 1)).sum(dim=0)
+    e_dg = ((dgamma.double() - rdg_own).abs().max() / rdg_own.abs().max()).item()
+    print(f"  dx {e_dx:.2e} dgamma (independent dh, per column) {e_dg_ind:.2e} "
+          f"(own dh) {e_dg:.2e}", flush=True)
+    assert e_dx <= TOL_BF16 and e_dg_ind <= TOL_BF16 and e_dg <= 1e-5
     # determinism of the whole backward
     dx2, dg2, dW2 = agk.rmsnorm_linear_bwd(x, g, inv, h, W, dy)
     torch.cuda.synchronize()
