@@ -31,13 +31,17 @@
 //      M_p > -inf (S = NaN for a row that is -inf throughout, as on the
 //      other paths);
 //   5. writes its range of the output row -- y * (dy - dot), exp(z - M) / S,
-//      or dy[row] * (exp(z - M) / S) -- while the loads of the team's next
-//      row, issued before step 1, are in flight.
+//      or dy[row] * (exp(z - M) / S), the last two as the exponentials of
+//      step 1 kept in registers times exp(M_p - M) / S (the head and tail
+//      elements: exp(z - M) / S) -- while the loads of the team's next row,
+//      issued before step 1, are in flight.
 // The words are cleared by a fill kernel ahead of the launch, in stream
 // order, so a set flag means "written by this call".  The launch shape
 // depends only on rows, cols and the storage type, so results are bit-
 // identical run to run; they differ from the one-workgroup-per-row paths'
-// only in the order of the row sums.
+// in the order of the row sums and, for the forward and the log-sum-exp
+// backward, by the rounding of exp(z - M_p) * exp(M_p - M) against
+// exp(z - M) (a few fp32 units).
 
 constexpr int kTeamLanes = 256;
 constexpr int kTeamWaves = kTeamLanes / 64;
@@ -367,6 +371,7 @@ __global__ __launch_bounds__(kTeamLanes) __attribute__((amdgpu_waves_per_eu(2)))
         // 1. this range's value(s), in every wave
         float mine[NVALS];
         float acc[W];
+        float ex[NVALS == 2 ? NVL : 1][W];  // exp(a - this range's max)
 #pragma unroll
         for (int e = 0; e < W; ++e) acc[e] = 0.0f;
         float ha = 0.0f, hb = 0.0f, ta = 0.0f, tb = 0.0f;
@@ -393,9 +398,25 @@ __global__ __launch_bounds__(kTeamLanes) __attribute__((amdgpu_waves_per_eu(2)))
             if (cur.own_h) m = MaxR::op(m, ha);
             if (cur.own_t) m = MaxR::op(m, ta);
             const float M = wg_max(m);
+            // Each element's exp(a - M) is kept for the output, which scales
+            // it by exp(M - row max) / row sum: one exponential per element
+            // instead of two.  The sum adds the same values in the same order
+            // as team_exp_slot (the recompute's).  A range whose maximum is
+            // -inf exponentiates against 0 instead: its elements are -inf or
+            // masked, every kept value is 0, and the combine below ignores
+            // its published sum.
+            const float Mx = M == kNegInf ? 0.0f : M;
 #pragma unroll
-            for (int k = 0; k < NVL; ++k)
-                team_exp_slot<S>(acc, cur.a[k], M, t + k * kTeamLanes < cur.len);
+            for (int k = 0; k < NVL; ++k) {
+                float fa[W];
+                S::unpack(cur.a[k], fa);
+                const bool valid = t + k * kTeamLanes < cur.len;
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    ex[k][e] = valid ? fast_exp(fa[e] - Mx) : 0.0f;
+                    acc[e] += ex[k][e];
+                }
+            }
             float x = team_fold<W>(acc);
             if constexpr (!ALIGNED) {
                 float es = 0.0f;
@@ -487,6 +508,11 @@ __global__ __launch_bounds__(kTeamLanes) __attribute__((amdgpu_waves_per_eu(2)))
             if (M == kNegInf) sum = __builtin_nanf("");
             inv = 1.0f / sum;
         }
+        // the kept exponentials' scale: exp(m - M) / sum for this range's
+        // maximum m (exp(-inf - M) = 0 for a range of -inf; NaN where the
+        // whole row is -inf, as exp(a - M) / sum gives there)
+        float sc = 0.0f;
+        if constexpr (NVALS == 2) sc = fast_exp(mine[0] - M) * inv;
         // 5. this range of the output row
         const int64_t base = range_base(row, cur.geo, part);
         const rsrc_t ro = make_rsrc(out + base, static_cast<uint32_t>(cur.len) * 16u);
@@ -500,10 +526,15 @@ __global__ __launch_bounds__(kTeamLanes) __attribute__((amdgpu_waves_per_eu(2)))
         for (int k = 0; k < NVL; ++k) {
             const uint32_t o = static_cast<uint32_t>(t + k * kTeamLanes) * 16u;
             float fa[W], fb[W], r[W];
-            S::unpack(cur.a[k], fa);
-            if constexpr (NIN == 2) S::unpack(cur.b[k], fb);
+            if constexpr (NVALS == 2) {
 #pragma unroll
-            for (int e = 0; e < W; ++e) r[e] = f(fa[e], NIN == 2 ? fb[e] : 0.0f);
+                for (int e = 0; e < W; ++e) r[e] = kLse ? g * (ex[k][e] * sc) : ex[k][e] * sc;
+            } else {
+                S::unpack(cur.a[k], fa);
+                if constexpr (NIN == 2) S::unpack(cur.b[k], fb);
+#pragma unroll
+                for (int e = 0; e < W; ++e) r[e] = f(fa[e], NIN == 2 ? fb[e] : 0.0f);
+            }
             if constexpr (ACC) {
                 float old[W];
                 S::unpack(bload16_stream(ro, o), old);

@@ -128,9 +128,11 @@ int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows,
  * 16-byte boundary from 2049 slots on, every row tensor at the same offset
  * from one) are spread over a team of workgroups that exchange their partial
  * row sums through the workspace, so each input row is read from HBM once
- * (the workspace-free calls re-read such rows).  Results are within fp32 rounding of the
- * workspace-free calls' (the row sums are added in another order) and bit-
- * identical run to run.  workspace == NULL takes the workspace-free kernels;
+ * (the workspace-free calls re-read such rows).  Results are within fp32
+ * rounding of the workspace-free calls' (the row sums are added in another
+ * order, and the forward and the log-sum-exp backward scale each range's
+ * exp(z - range max) by exp(range max - row max)) and bit-identical run to
+ * run.  workspace == NULL takes the workspace-free kernels;
  * otherwise it must be 8-byte aligned and hold at least
  * agk_rowops_workspace_bytes(rows, cols) bytes (AGK_EINVAL / AGK_EWORKSPACE
  * if not): rows * parts * 16 bytes, parts = ceil(ceil(cols / W) / 2048) for

@@ -547,6 +547,56 @@ def test_team_rows_match_oracle_and_recompute(cuda, dtype, rows, cols):
     assert_ok(e, _tol(bf16), f"team {dtype} {rows}x{cols}")
 
 
+@pytest.mark.parametrize("dtype,cols", [("bf16", 131072), ("f32", 131072), ("f32", 100000)],
+                         ids=str)
+def test_team_masked_ranges(cuda, dtype, cols):
+    """Team rows where whole parts are -inf (masked spans wider than a part's
+    range, 16384 bf16 or 8192 fp32 elements): a part whose maximum is -inf
+    contributes nothing, its outputs are 0, and the other parts' outputs match
+    the oracle; a row that is -inf throughout gives NaN, as on the other paths.
+    Softmax forward and the log-sum-exp backward (the kernels that keep each
+    part's exponentials), with the workspace-free kernels within the bars."""
+    import warnings
+    import torch
+    rows = 6
+    bf16 = dtype == "bf16"
+    aligned = cols % (8 if bf16 else 4) == 0
+    assert _team_parts(dtype, rows, cols, aligned) >= 2
+    z = torch.randn(rows, cols, device=cuda) * 3
+    z[0, :40000] = float("-inf")           # the first parts, and part of the next
+    z[1, cols - 50000:] = float("-inf")    # the last parts
+    z[2, 20000:90000] = float("-inf")      # parts in the middle
+    z[3] = float("-inf")                   # the whole row
+    z[4, :] = float("-inf")
+    z[4, 70000] = 1.5                      # one finite element
+    z = z.to(torch.bfloat16 if bf16 else torch.float32).contiguous()
+    dl = torch.randn(rows, 1, device=cuda).to(z.dtype)
+    y = agk.softmax_fwd(z)
+    dz = agk.logsumexp_bwd(z, dl)
+    y0 = agk.softmax_fwd(z, workspace=False)
+    dz0 = agk.logsumexp_bwd(z, dl, workspace=False)
+    torch.cuda.synchronize()
+    zh, dlh = to_host(z), to_host(dl)
+    with warnings.catch_warnings(), np.errstate(invalid="ignore"):
+        warnings.simplefilter("ignore", RuntimeWarning)
+        if bf16:
+            ry, rdz = ro.softmax_fwd_bf16(zh), ro.logsumexp_bwd_bf16(zh, dlh)
+        else:
+            ry, rdz = ro.softmax_fwd(zh), ro.logsumexp_bwd(zh, dlh)
+    yh, dzh = as_f32(to_host(y)), as_f32(to_host(dz))
+    masked = np.isneginf(as_f32(zh))
+    live = [0, 1, 2, 4, 5]
+    assert np.all(np.isnan(yh[3])) and np.all(np.isnan(dzh[3])), "a fully masked row is NaN"
+    for r in live:
+        assert np.all(yh[r][masked[r]] == 0) and np.all(dzh[r][masked[r]] == 0), r
+    assert yh[4, 70000] == 1.0
+    tol = _tol(bf16)
+    e = {"y": _row_rel(yh[live], ry[live]), "lse dz": _row_rel(dzh[live], rdz[live]),
+         "y vs workspace-free": _row_rel(yh[live], as_f32(to_host(y0))[live]),
+         "lse dz vs workspace-free": _row_rel(dzh[live], as_f32(to_host(dz0))[live])}
+    assert_ok(e, tol, f"team masked ranges {dtype} {rows}x{cols}")
+
+
 @pytest.mark.parametrize("dtype,rows,cols", [("bf16", 50, 4096), ("f32", 300, 2048),
                                              ("bf16", 20, 20000), ("f32", 17, 10001),
                                              ("bf16", 5, 65536)], ids=str)
