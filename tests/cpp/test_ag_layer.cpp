@@ -1051,7 +1051,9 @@ void test_matmul_layer() {
 // three gradients and forward mode against host fp64 with the graph's bf16
 // roundings; sequential against parallel backward bitwise; errors.
 void test_linear_layer() {
-    for (auto [M, K, N] : {std::tuple<int64_t, int64_t, int64_t>{16, 32, 8}, {96, 136, 200}}) {
+    for (const auto& shape :
+         {std::tuple<int64_t, int64_t, int64_t>{16, 32, 8}, {96, 136, 200}}) {
+        const int64_t M = std::get<0>(shape), K = std::get<1>(shape), N = std::get<2>(shape);
         const std::string tag = "[" + std::to_string(M) + "," + std::to_string(K) + "] x [" +
                                 std::to_string(N) + "," + std::to_string(K) + "]^T";
         std::vector<float> xv = rounded(normal(M * K, 90 + K)), wv = rounded(normal(N * K, 91 + K, 0.2)),
