@@ -309,6 +309,17 @@ def _cfg_label(r):
             f"{r['config']['cols']} {r['dtype']}")
 
 
+def _gpu_state_line(gs):
+    """The shader clock and board power bench.py read from sysfs around a timed
+    region, as one sentence (None when the record has none)."""
+    if not gs or not gs.get("after_timed"):
+        return None
+    b, a = gs.get("before_timed") or {}, gs["after_timed"]
+    return (f"GPU state (sysfs): shader clock {b.get('sclk_mhz', '-')} -> {a.get('sclk_mhz', '-')}"
+            f" MHz, board power {b.get('power_w', '-')} -> {a.get('power_w', '-')} W (during the "
+            "last warm-up steps -> right after the timed steps).")
+
+
 def write_bench_summary(jsonl, out_md, command):
     """Tables of bench.py's JSON lines (RMSNorm configurations, c5, row ops)."""
     recs = [json.loads(ln) for ln in open(jsonl) if ln.strip().startswith("{")]
@@ -405,6 +416,17 @@ def write_bench_summary(jsonl, out_md, command):
                              f"{1e3 * tb[name]:.1f} | {fl / (tb[name] * 1e-3) / 1e12:.0f} |")
             else:
                 lines.append(f"| {name} | {1e3 * ms:.1f} | - | - | - | - | - |")
+        lines.append("")
+        state = _gpu_state_line(r.get("gpu_state"))
+        if state:
+            lines += [state + " The products run into the board's power limit, so their "
+                      "speed follows the power this box allows.", ""]
+    gstates = [(_cfg_label(r), _gpu_state_line((r.get("kernels") or {}).get("gpu_state")))
+               for r in norm]
+    gstates = [(c, g) for c, g in gstates if g]
+    if gstates:
+        lines += ["GPU state per RMSNorm configuration:", ""]
+        lines += [f"- {c}: {g}" for c, g in gstates]
         lines.append("")
     with open(out_md, "w") as fh:
         fh.write("\n".join(lines) + "\n")
