@@ -1106,7 +1106,8 @@ def gemm_f32_bench(reps):
 WIDE_SHAPES = (("f32", 8, 262144), ("f32", 1, 1 << 20), ("f32", 51, 32768),
                ("f32", 256, 65536), ("f32", 4096, 32768), ("bf16", 8, 262144),
                ("bf16", 51, 32768), ("bf16", 1024, 65536), ("bf16", 16384, 20480),
-               ("f32", 2048, 65536), ("bf16", 8192, 131072))
+               ("f32", 2048, 65536), ("bf16", 8192, 131072), ("f32", 2048, 131072),
+               ("f32", 256, 262144))
 
 
 def run_wide(steps):

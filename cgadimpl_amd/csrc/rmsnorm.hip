@@ -2036,7 +2036,7 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
                           (dtype == AGK_F32 ? team_eligible<F32>(a, a, a, a, rows, c, false)
                                             : team_eligible<BF16>(a, a, a, a, rows, c, false));
         if (team) {
-            const int segs = team_segs_for(dtype);
+            const int segs = team_segs_for(dtype, rows, c);
             const TeamPlan tp = team_plan(rows, c, segs);
             plan[0] = static_cast<int32_t>(tp.parts * kWideLanes);
             plan[1] = segs * kWideSegCols / (w * kWideLanes);

@@ -793,7 +793,7 @@ int launch_wide_res_bwd(const void* x, const void* gamma, const float* inv_rms, 
 // that the one-pass kernel above does not take (wider than 32768 columns, or
 // fewer than 256 rows).  A team of P workgroups holds one row at a time in
 // registers: workgroup p of the team owns segments [p*SEGS, (p+1)*SEGS) of
-// kWideSegCols columns (SEGS = team_segs: 1 for fp32, 2 for bf16), with the
+// kWideSegCols columns (SEGS = team_segs_for: 1 or 2 for fp32, 2 for bf16), with the
 // same slots per lane as wide_row_stats.  Team t takes rows t, t+T, t+2T, ...
 // (T = kTeamWorkgroups / P, at most the split path's row blocks, so the
 // dgamma partial rows fit the same workspace region).  Per row each workgroup
@@ -831,17 +831,27 @@ constexpr int64_t kTeamMinRows = 4;   // fewer rows take the split path
 // shape, never on the device.
 constexpr int64_t kTeamWorkgroups = 512;
 
-// Segments per workgroup: one for fp32, two for bf16 -- 32 KiB of x and dy
-// per row either way, which the row's exchange is amortised over.  Measured
-// on MI355X (graph-replayed backward, dx and dgamma): bf16 [8192, 131072] in
-// 1189 us with two segments against 1985 us with one (the exchange, not the
-// bytes, bounds a workgroup that moves half as much per row); fp32 keeps one
-// because two would need more than 256 registers per lane.
-template <class S>
-constexpr int team_segs() {
-    return S::kVec == 4 ? 1 : 2;
+// Segments per workgroup, which the row's exchange is amortised over.  bf16:
+// two (32 KiB of x and dy per row).  fp32: one (32 KiB), or two (64 KiB; gamma
+// then staged in LDS instead of registers, so the row fits 237 VGPRs at two
+// waves per SIMD) where one-segment parts would number 32 or more per row or
+// a two-segment team gets at least 16 rows.  A function of rows and cols
+// only, so the team count and dgamma's summation order are fixed by the
+// shape.  Measured on MI355X (graph-replayed backward, dx and dgamma, us,
+// one segment -> two): fp32 [2048, 65536] 284 -> 272, [4096, 65536] 559 ->
+// 525, [2048, 131072] 704 -> 537, [256, 262144] 226 -> 161, [128, 524288]
+// 246 -> 170, [4096, 40000] 358 -> 341; but [256, 65536] 46 -> 50 and
+// [512, 65536] 81 -> 84 (four and eight rows per team: the pipeline of each
+// team's rows too short).  bf16 [8192, 131072]: 1189 us with two segments
+// against 1985 with one; gamma in LDS cost it 3 % (1179 -> 1212 us), and
+// three segments (251 VGPRs) 1392 us.
+inline int team_segs_for(int dtype, int64_t rows, int64_t cols) {
+    if (dtype != AGK_F32) return 2;
+    const int64_t parts1 = (cols + kWideSegCols - 1) / kWideSegCols;
+    const int64_t parts2 = (cols + 2 * kWideSegCols - 1) / (2 * kWideSegCols);
+    const int64_t teams2 = kTeamWorkgroups / parts2 > 0 ? kTeamWorkgroups / parts2 : 1;
+    return (parts1 >= 32 || rows >= 16 * teams2) ? 2 : 1;
 }
-inline int team_segs_for(int dtype) { return dtype == AGK_F32 ? 1 : 2; }
 
 struct TeamPlan {
     int64_t parts = 0;  // workgroups per row (team size)
@@ -907,9 +917,25 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
         off[q] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
     }
     const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
-    u32x4 gv[NS];
+    // gamma of this workgroup's columns, loaded once: in LDS for fp32 parts of
+    // two segments (registers for the rows), else in registers
+    constexpr bool GLDS = std::is_same<S, F32>::value && kTeamSegs == 2;
+    __shared__ u32x4 glds[GLDS ? NS : 1][GLDS ? kWideLanes : 1];
+    u32x4 gv[GLDS ? 1 : NS];
+    if constexpr (GLDS) {
 #pragma unroll
-    for (int q = 0; q < NS; ++q) gv[q] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+        for (int q = 0; q < NS; ++q)
+            glds[q][t] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int q = 0; q < NS; ++q)
+            gv[q] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+    }
+    auto gam = [&](int q) -> u32x4 {
+        if constexpr (GLDS) return glds[q][t];
+        else return gv[q];
+    };
     float dg[NS][W];
 #pragma unroll
     for (int q = 0; q < NS; ++q)
@@ -1001,7 +1027,7 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
                 }
                 if (gamma) {
                     float gm[W];
-                    S::unpack(gv[q], gm);
+                    S::unpack(gam(q), gm);
 #pragma unroll
                     for (int e = 0; e < W; ++e) fd[e] = fd[e] * gm[e];
                 }
@@ -1041,7 +1067,10 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
                 const int sg = lane + 64 * j;
                 const bool own = sg >= seg0 && sg < seg0 + kTeamSegs;
                 have[j] = sg >= nseg || own;
-                val[j] = own ? (sg == seg0 ? v[0] : v[kTeamSegs - 1]) : 0.0f;
+                val[j] = 0.0f;
+#pragma unroll
+                for (int s = 0; s < kTeamSegs; ++s)
+                    if (sg == seg0 + s) val[j] = v[s];
             }
             for (int it = 0;; ++it) {
                 bool all = true;
@@ -1100,7 +1129,7 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
             S::unpack(cur.dv[q], gk);
             if (gamma) {
                 float gm[W];
-                S::unpack(gv[q], gm);
+                S::unpack(gam(q), gm);
 #pragma unroll
                 for (int e = 0; e < W; ++e) gk[e] = gk[e] * gm[e];
             }
@@ -1143,14 +1172,11 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
 inline int zero_fill(float* p, int64_t n, hipStream_t st);
 int team_wait_polls();
 
-// ws: at least wide_ws_bytes(rows, cols, false) bytes (wide_ws_stats_bytes
-// without dgamma), 16-byte aligned (checked by the caller).
-template <class S>
-int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
-                         void* dx, float* dgamma, void* ws, int64_t rows, int cols, int acc_dx,
-                         int acc_dg, hipStream_t st) {
+template <class S, int kSegs>
+int launch_wide_team_bwd_segs(const void* x, const void* gamma, const float* inv_rms,
+                              const void* dy, void* dx, float* dgamma, void* ws, int64_t rows,
+                              int cols, int acc_dx, int acc_dg, hipStream_t st) {
     using T = typename S::T;
-    constexpr int kSegs = team_segs<S>();
     const TeamPlan tp = team_plan(rows, cols, kSegs);
     const WideWs w = wide_ws_layout(rows, cols, tp.teams);
     const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
@@ -1177,6 +1203,24 @@ int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms,
     if (int rc = check_launch()) return rc;
     if (dgamma) return launch_finalize(partials, dgamma, tp.teams, cols, acc_dg, st);
     return AGK_OK;
+}
+
+// ws: at least wide_ws_bytes(rows, cols, false) bytes (wide_ws_stats_bytes
+// without dgamma), 16-byte aligned (checked by the caller).
+template <class S>
+int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms, const void* dy,
+                         void* dx, float* dgamma, void* ws, int64_t rows, int cols, int acc_dx,
+                         int acc_dg, hipStream_t st) {
+    if constexpr (std::is_same<S, F32>::value) {
+        if (team_segs_for(AGK_F32, rows, cols) == 2)
+            return launch_wide_team_bwd_segs<S, 2>(x, gamma, inv_rms, dy, dx, dgamma, ws, rows,
+                                                   cols, acc_dx, acc_dg, st);
+        return launch_wide_team_bwd_segs<S, 1>(x, gamma, inv_rms, dy, dx, dgamma, ws, rows, cols,
+                                               acc_dx, acc_dg, st);
+    } else {
+        return launch_wide_team_bwd_segs<S, 2>(x, gamma, inv_rms, dy, dx, dgamma, ws, rows, cols,
+                                               acc_dx, acc_dg, st);
+    }
 }
 
 // ---- the forward in one read of x: teams ------------------------------------------

@@ -136,7 +136,8 @@ def test_wide_row_plans_and_workspace():
     for rows in (1, 7, 300, 5000):
         assert ws(rows, 16384) == _blocks(rows) * 16384 * 4  # narrower: unchanged
     for rows, cols in [(1, 1 << 20), (8, 262144), (51, 32768), (255, 32768), (256, 16388),
-                       (300, 65536), (4096, 32768), (1100, 20480), (7, 16385), (3, 40002)]:
+                       (300, 65536), (4096, 32768), (1100, 20480), (7, 16385), (3, 40002),
+                       (1024, 65536), (1023, 65536), (2000, 40004), (12, 131072)]:
         nrb, rb = _split_blocks(rows, cols)
         want = max(_blocks(rows) * cols * 4, _split_ws(rows, cols, nrb),
                    _split_ws(rows, cols, _blocks(rows)))
@@ -153,10 +154,16 @@ def test_wide_row_plans_and_workspace():
                 assert (bp["tpr"], bp["nv"], bp["g"]) == (1024, 32768 // (w * 1024), 1), label
                 assert bp["nblk"] == 256 and bp["rpb"] == -(-rows // 256), label
             elif rows >= 4:
-                # the team kernel: 4096 fp32 / 8192 bf16 columns per workgroup,
-                # one partial row per team, 512 // parts teams (at most the
-                # split path's row blocks)
-                part = 4096 if w == 4 else 8192
+                # the team kernel: 8192 bf16 columns per workgroup; fp32 4096,
+                # or 8192 where 4096-column parts would be 32 or more or a team
+                # of 8192-column parts gets 16 rows or more; one partial row
+                # per team, 512 // parts teams (at most the split path's row
+                # blocks)
+                part = 8192
+                if w == 4:
+                    teams2 = max(512 // -(-cols // 8192), 1)
+                    if -(-cols // 4096) < 32 and rows < 16 * teams2:
+                        part = 4096
                 parts = -(-cols // part)
                 teams = min(max(512 // parts, 1), nrb)
                 assert bp["g"] == 0, label

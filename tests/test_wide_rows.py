@@ -120,10 +120,12 @@ def test_wide_full_size_properties(cuda, dtype, rows, cols):
 
 # Team kernel shapes: many rows (more rows than teams), one row per team,
 # ragged last segment, the widest rows it takes (256 segments), bf16 parts of
-# two segments with an odd segment count.
+# two segments with an odd segment count, fp32 parts of two segments (gamma
+# in LDS) chosen by the width (64 one-segment parts) and by the rows per team
+# (with a ragged last segment).
 TEAM_CASES = [("f32", 300, 65536), ("bf16", 100, 131072), ("f32", 4, 40000),
               ("bf16", 5, 131080), ("f32", 4, 1 << 20), ("bf16", 70, 36864),
-              ("f32", 9, 16388)]
+              ("f32", 9, 16388), ("f32", 40, 262144), ("f32", 1700, 40004)]
 
 
 @pytest.mark.parametrize("dtype,rows,cols", TEAM_CASES, ids=str)
