@@ -2051,7 +2051,7 @@ int agk_rmsnorm_launch_plan(int64_t rows, int64_t cols, int dtype, int backward,
         (dtype == AGK_F32 ? wide_fwd_shape_ok<F32>(rows, static_cast<int>(cols), false)
                           : wide_fwd_shape_ok<BF16>(rows, static_cast<int>(cols), false))) {
         // the team forward: a row over `parts` workgroups of 256 lanes
-        const int segs = fwd_team_segs_for(dtype);
+        const int segs = fwd_team_segs_for(dtype, rows, cols);
         const TeamPlan tp = fwd_team_plan(rows, static_cast<int>(cols), segs);
         plan[0] = static_cast<int32_t>(tp.parts * kWideLanes);
         plan[1] = segs * kWideSegCols / (w * kWideLanes);

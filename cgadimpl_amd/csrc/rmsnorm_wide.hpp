@@ -835,7 +835,9 @@ constexpr int64_t kTeamWorkgroups = 512;
 // two (32 KiB of x and dy per row).  fp32: one (32 KiB), or two (64 KiB; gamma
 // then staged in LDS instead of registers, so the row fits 237 VGPRs at two
 // waves per SIMD) where one-segment parts would number 32 or more per row or
-// a two-segment team gets at least 16 rows.  A function of rows and cols
+// a two-segment team gets at least 16 rows, and there are rows enough for
+// two-segment teams to fill the grid (at [8, 262144] two segments took 16.9
+// us against 16.5).  A function of rows and cols
 // only, so the team count and dgamma's summation order are fixed by the
 // shape.  Measured on MI355X (graph-replayed backward, dx and dgamma, us,
 // one segment -> two): fp32 [2048, 65536] 284 -> 272, [4096, 65536] 559 ->
@@ -850,7 +852,8 @@ inline int team_segs_for(int dtype, int64_t rows, int64_t cols) {
     const int64_t parts1 = (cols + kWideSegCols - 1) / kWideSegCols;
     const int64_t parts2 = (cols + 2 * kWideSegCols - 1) / (2 * kWideSegCols);
     const int64_t teams2 = kTeamWorkgroups / parts2 > 0 ? kTeamWorkgroups / parts2 : 1;
-    return (parts1 >= 32 || rows >= 16 * teams2) ? 2 : 1;
+    // two only where its teams still fill the grid (few rows want more parts)
+    return rows >= teams2 && (parts1 >= 32 || rows >= 16 * teams2) ? 2 : 1;
 }
 
 struct TeamPlan {
@@ -1228,7 +1231,7 @@ int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms,
 // of at most kTeamMaxSegs segments and at least kTeamMinRows rows, go to
 // teams of P workgroups as in the team backward (all 512 workgroups resident
 // at once at the kernel's register use): workgroup p owns segments
-// [p*SEGS, (p+1)*SEGS) (SEGS = fwd_team_segs), team t takes rows t, t+T, ...
+// [p*SEGS, (p+1)*SEGS) (SEGS = fwd_team_segs_for), team t takes rows t, t+T, ...
 // (T = min(kFwdTeamWorkgroups / P, rows)).  Per row each workgroup
 //   1. sums x^2 over each of its segments as wide_row_stats does;
 //   2. publishes the sums in the row's slots and gathers the others with the
@@ -1243,19 +1246,32 @@ int launch_wide_team_bwd(const void* x, const void* gamma, const float* inv_rms,
 // order, so a set flag means "written by this call".
 constexpr int64_t kFwdTeamWorkgroups = 512;
 
-// Segments per workgroup: 32 KiB of x per row for either dtype, which the
-// row's exchange is amortised over.  Measured on MI355X (graph-replayed
+// Segments per workgroup, which the row's exchange is amortised over: 32 KiB
+// of x per row (two fp32 or four bf16 segments), or for fp32 64 KiB (four
+// segments, gamma then staged in LDS) where two-segment parts would number 16
+// or more per row or a two-segment team would get at most 4 rows, and there
+// are rows enough for four-segment teams to fill the grid (at [8, 262144] four
+// segments ran 9.3 us against 7.7: 128 workgroups against 256).  A function
+// of rows and cols only.  Measured on MI355X (graph-replayed
 // agk_rmsnorm_fwd_ws, 512 workgroups): fp32 [2048, 65536] 200 -> 176 us with
 // two segments against one, bf16 [8192, 131072] 925 -> 722 us with four
-// against two; four fp32 segments (241 VGPRs) ran 186 us at [2048, 65536],
-// and eight bf16 segments need 256 VGPRs, one wave per SIMD: too few for the
-// 512 workgroups to be resident together.  1024 workgroups of the narrower
-// parts measured between the two (fp32 189 us, bf16 816 us).
-template <class S>
-constexpr int fwd_team_segs() {
-    return S::kVec == 4 ? 2 : 4;
+// against two.  fp32 two segments -> four: [512, 131072] 97 -> 94,
+// [2048, 131072] 373 -> 360, [64, 262144] 31 -> 24, [256, 262144] 111 -> 96,
+// [128, 524288] 121 -> 99, [256, 65536] 24 -> 23; but [1024, 65536] 91 -> 95,
+// [2048, 65536] 178 -> 189, [4096, 40000] 223 -> 230.  Gamma in registers
+// instead of LDS at four fp32 segments measured the same (241 VGPRs).  Eight
+// bf16 segments need 256 VGPRs (one wave per SIMD: the 512 workgroups would
+// not all be resident; measured 10-15 % slower), and 1024 workgroups of the
+// narrower parts measured between one and two segments.
+inline int fwd_team_segs_for(int dtype, int64_t rows, int64_t cols) {
+    if (dtype != AGK_F32) return 4;
+    const int64_t parts2 = (cols + 2 * kWideSegCols - 1) / (2 * kWideSegCols);
+    const int64_t parts4 = (cols + 4 * kWideSegCols - 1) / (4 * kWideSegCols);
+    const int64_t teams2 = kFwdTeamWorkgroups / parts2 > 0 ? kFwdTeamWorkgroups / parts2 : 1;
+    const int64_t teams4 = kFwdTeamWorkgroups / parts4 > 0 ? kFwdTeamWorkgroups / parts4 : 1;
+    // four only where its teams still fill the grid (few rows want more parts)
+    return rows >= teams4 && (parts2 >= 16 || rows <= 4 * teams2) ? 4 : 2;
 }
-inline int fwd_team_segs_for(int dtype) { return dtype == AGK_F32 ? 2 : 4; }
 
 inline TeamPlan fwd_team_plan(int64_t rows, int cols, int segs) {
     TeamPlan tp;
@@ -1311,9 +1327,25 @@ __global__ __launch_bounds__(kWideLanes) void wide_fwd_team(
         off[q] = col < cols ? static_cast<uint32_t>(col) * sizeof(T) : kOffOut;
     }
     const rsrc_t rg = make_rsrc(gamma, gamma ? row_bytes : 0u);
-    u32x4 gv[NS];
+    // gamma of this workgroup's columns, loaded once: in LDS for parts of more
+    // than 8 slots per lane (registers for the rows), else in registers
+    constexpr bool GLDS = NS > 8;
+    __shared__ u32x4 glds[GLDS ? NS : 1][GLDS ? kWideLanes : 1];
+    u32x4 gv[GLDS ? 1 : NS];
+    if constexpr (GLDS) {
 #pragma unroll
-    for (int q = 0; q < NS; ++q) gv[q] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+        for (int q = 0; q < NS; ++q)
+            glds[q][t] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int q = 0; q < NS; ++q)
+            gv[q] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[q], 0, 0);
+    }
+    auto gam = [&](int q) -> u32x4 {
+        if constexpr (GLDS) return glds[q][t];
+        else return gv[q];
+    };
 
     struct Set {
         u32x4 xv[NS];
@@ -1470,7 +1502,7 @@ __global__ __launch_bounds__(kWideLanes) void wide_fwd_team(
             S::unpack(cur.xv[q], f);
             if (gamma) {
                 float gm[W];
-                S::unpack(gv[q], gm);
+                S::unpack(gam(q), gm);
 #pragma unroll
                 for (int e = 0; e < W; ++e) f[e] = (f[e] * r) * gm[e];
             } else {
@@ -1495,11 +1527,10 @@ __global__ __launch_bounds__(kWideLanes) void wide_fwd_team(
 
 // ws: at least fwd_team_ws_bytes(rows, cols) bytes, 8-byte aligned (checked
 // by the caller).
-template <class S>
-int launch_wide_team_fwd(const void* x, const void* gamma, void* y, float* inv_rms, void* ws,
-                         int64_t rows, int cols, float eps, hipStream_t st) {
+template <class S, int kSegs>
+int launch_wide_team_fwd_segs(const void* x, const void* gamma, void* y, float* inv_rms,
+                              void* ws, int64_t rows, int cols, float eps, hipStream_t st) {
     using T = typename S::T;
-    constexpr int kSegs = fwd_team_segs<S>();
     const TeamPlan tp = fwd_team_plan(rows, cols, kSegs);
     const int64_t nseg = (cols + kWideSegCols - 1) / kWideSegCols;
     const int64_t grid = tp.teams * tp.parts;
@@ -1512,4 +1543,16 @@ int launch_wide_team_fwd(const void* x, const void* gamma, void* y, float* inv_r
                        cols, static_cast<int>(nseg), static_cast<int>(tp.parts), tp.teams, eps,
                        team_wait_polls());
     return check_launch();
+}
+
+template <class S>
+int launch_wide_team_fwd(const void* x, const void* gamma, void* y, float* inv_rms, void* ws,
+                         int64_t rows, int cols, float eps, hipStream_t st) {
+    if constexpr (std::is_same<S, F32>::value) {
+        if (fwd_team_segs_for(AGK_F32, rows, cols) == 4)
+            return launch_wide_team_fwd_segs<S, 4>(x, gamma, y, inv_rms, ws, rows, cols, eps, st);
+        return launch_wide_team_fwd_segs<S, 2>(x, gamma, y, inv_rms, ws, rows, cols, eps, st);
+    } else {
+        return launch_wide_team_fwd_segs<S, 4>(x, gamma, y, inv_rms, ws, rows, cols, eps, st);
+    }
 }

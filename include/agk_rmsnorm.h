@@ -358,8 +358,10 @@ int agk_set_team_forward(int enabled);
  * kernel: a row held by lanes per row / 256 workgroups of 256 lanes that
  * exchange their partial sums (backward: 8192 bf16 columns each, and 4096
  * or 8192 fp32 -- 8192 where 4096-column parts would number 32 or more, or
- * where a team of 8192-column parts gets 16 rows or more; forward: 8192
- * fp32 or 16384 bf16), the teams taking the rows in turn
+ * where a team of 8192-column parts gets 16 rows or more, given rows enough
+ * for 512 / parts teams; forward: 16384 bf16, and 8192 or 16384 fp32 --
+ * 16384 where 8192-column parts would number 16 or more, or where a team of
+ * them would get at most 4 rows, given rows enough for 512 / parts teams), the teams taking the rows in turn
  * (plan[3] = rows per team, plan[4] = teams);
  * lanes per row == 0 means a path that does not keep rows in registers:
  * the split path when slots per lane > 0 (then plan[1] = 4096-column

@@ -156,13 +156,14 @@ def test_wide_row_plans_and_workspace():
             elif rows >= 4:
                 # the team kernel: 8192 bf16 columns per workgroup; fp32 4096,
                 # or 8192 where 4096-column parts would be 32 or more or a team
-                # of 8192-column parts gets 16 rows or more; one partial row
+                # of 8192-column parts gets 16 rows or more (given rows for
+                # 512 // parts teams); one partial row
                 # per team, 512 // parts teams (at most the split path's row
                 # blocks)
                 part = 8192
                 if w == 4:
                     teams2 = max(512 // -(-cols // 8192), 1)
-                    if -(-cols // 4096) < 32 and rows < 16 * teams2:
+                    if rows < teams2 or (-(-cols // 4096) < 32 and rows < 16 * teams2):
                         part = 4096
                 parts = -(-cols // part)
                 teams = min(max(512 // parts, 1), nrb)
@@ -191,8 +192,9 @@ def _fwd_ws_rule(rows, cols):
 def test_forward_team_plans_and_workspace():
     """agk_rmsnorm_fwd_ws: its workspace rule, the plan diagnostic's team
     forward (mode 2) wherever agk_rmsnorm_fwd would take the split path
-    (32 KiB of the row per workgroup: 8192 fp32 or 16384 bf16 columns,
-    min(512 // parts, rows) teams), the same plan as agk_rmsnorm_fwd elsewhere
+    (16384 bf16 columns per workgroup; fp32 8192, or 16384 where 8192-column
+    parts would number 16 or more or a team of them would get at most 4 rows,
+    given rows for 512 // parts teams; min(512 // parts, rows) teams), the same plan as agk_rmsnorm_fwd elsewhere
     or with the team switched off, and validation before any HIP call."""
     lib = agk.lib()
     wb = lib.agk_rmsnorm_fwd_workspace_bytes
@@ -201,17 +203,23 @@ def test_forward_team_plans_and_workspace():
         assert wb(rows, cols) == _fwd_ws_rule(rows, cols), (rows, cols)
     assert wb(300, 65536) == 300 * 16 * 8
     for rows, cols in [(8, 262144), (300, 65536), (4, 1 << 20), (7, 50000), (3, 65536),
-                       (5, 1 << 21), (600, 40000), (6, 70008), (9, 16388), (5, 40002)]:
+                       (5, 1 << 21), (600, 40000), (6, 70008), (9, 16388), (5, 40002),
+                       (256, 65536), (257, 65536), (2048, 131072), (4096, 40000)]:
         for dt, w in ((agk.AGK_F32, 4), (agk.AGK_BF16, 8)):
             label = (rows, cols, dt)
             plain = agk.launch_plan(rows, cols, dt, False)
             team = agk.launch_plan(rows, cols, dt, False, fwd_workspace=True)
             split = plain["tpr"] == 0 and plain["nv"] > 0
             if split and _fwd_ws_rule(rows, cols):
-                part = 8192 if w == 4 else 16384
+                part = 16384
+                if w == 4:
+                    parts2 = -(-cols // 8192)
+                    teams4 = max(512 // -(-cols // 16384), 1)
+                    if rows < teams4 or (parts2 < 16 and rows > 4 * max(512 // parts2, 1)):
+                        part = 8192
                 parts = -(-cols // part)
                 teams = min(max(512 // parts, 1), rows)
-                assert team == {"tpr": 256 * parts, "nv": 8, "g": 0,
+                assert team == {"tpr": 256 * parts, "nv": part // (256 * w), "g": 0,
                                 "rpb": -(-rows // teams), "nblk": teams}, label
             else:
                 assert team == plain, label

@@ -174,11 +174,14 @@ def test_team_against_split_and_recompute(cuda, dtype, rows, cols, with_gamma):
 
 
 # Team forward shapes (agk_rmsnorm_fwd_ws): more rows than teams, a ragged
-# last segment (fp32) and an odd segment count (bf16 parts of two), the
-# widest rows it takes (256 segments), the fewest rows it takes (4).
+# last segment (fp32) and an odd segment count (bf16 parts of four), the
+# widest rows it takes (256 segments), the fewest rows it takes (4), fp32
+# parts of four segments (gamma in LDS) chosen by the rows per team and by
+# the width.
 FWD_TEAM_CASES = [("f32", 600, 40000), ("f32", 7, 50000), ("f32", 4, 1 << 20),
                   ("f32", 300, 65536), ("bf16", 100, 131072), ("bf16", 5, 131080),
-                  ("bf16", 6, 70008), ("bf16", 4, 1 << 20)]
+                  ("bf16", 6, 70008), ("bf16", 4, 1 << 20), ("f32", 256, 65536),
+                  ("f32", 40, 262144)]
 
 
 @pytest.mark.parametrize("dtype,rows,cols", FWD_TEAM_CASES, ids=str)
