@@ -547,6 +547,32 @@ def test_team_rows_match_oracle_and_recompute(cuda, dtype, rows, cols):
     assert_ok(e, _tol(bf16), f"team {dtype} {rows}x{cols}")
 
 
+def test_team_rowops_on_two_streams_at_once(cuda):
+    """The row ops' team kernels of two calls running at once on two streams
+    (default priority; together more workgroups than the GPU holds at once):
+    every output bit-identical to the same calls made one after the other."""
+    import torch
+    rows, cols = 2048, 128256
+    x, _, dy = device_inputs((rows, cols), "bf16", 17, cuda)
+    z = x * 4.0
+    dl = dy[:, :1].contiguous()
+    ref = (agk.softmax_fwd(z), agk.logsumexp_bwd(z, dl))
+    ref_b = agk.softmax_bwd(ref[0], dy)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    ws = [torch.empty(agk.rowops_workspace_bytes(rows, cols), dtype=torch.uint8, device=cuda)
+          for _ in range(3)]
+    for rep in range(3):
+        with torch.cuda.stream(s1):
+            y = agk.softmax_fwd(z, workspace=ws[0], stream=s1)
+            dzb = agk.softmax_bwd(ref[0], dy, workspace=ws[2], stream=s1)
+        with torch.cuda.stream(s2):
+            dz = agk.logsumexp_bwd(z, dl, workspace=ws[1], stream=s2)
+        torch.cuda.synchronize()
+        print(f"row ops on two streams, round {rep}", flush=True)
+        assert torch.equal(y, ref[0]) and torch.equal(dz, ref[1]) and torch.equal(dzb, ref_b), rep
+
+
 @pytest.mark.parametrize("dtype,cols", [("bf16", 131072), ("f32", 131072), ("f32", 100000)],
                          ids=str)
 def test_team_masked_ranges(cuda, dtype, cols):
