@@ -887,6 +887,101 @@ __device__ __forceinline__ uint64_t slot_read(uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Shared LDS of a team kernel's exchange: the row's segment sums, which of
+// them a wait missed, and whether any did.  Each field is written for the
+// next row only after a barrier that every wave reaches after reading it for
+// the current one.
+struct TeamXchg {
+    float vals[kTeamMaxSegs];
+    unsigned char missing[kTeamMaxSegs];
+    int nmissing;
+};
+
+// Steps 2-3 of both team kernels (workgroup-uniform call, 256 lanes): this
+// workgroup's kSegs segment sums v (segments seg0 ..) are published in the
+// row's slots rs, wave 0 gathers the row's other segments' sums with at most
+// `wait_polls` polls, and a sum still missing after that is recomputed by
+// the whole workgroup with recompute(sg) (the publisher's arithmetic, so the
+// same bits).  On return x.vals[0, nseg) holds every segment sum.
+template <int kSegs, class Recompute>
+__device__ __forceinline__ void team_gather(uint64_t* rs, const float (&v)[kSegs], int seg0,
+                                            int nseg, int wait_polls, TeamXchg& x,
+                                            Recompute recompute) {
+    constexpr int kPerLane = static_cast<int>(kTeamMaxSegs / 64);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (t == 0) {
+#pragma unroll
+        for (int s = 0; s < kSegs; ++s)
+            if (seg0 + s < nseg) slot_publish(rs + seg0 + s, v[s]);
+    }
+    if (wave == 0) {
+        float val[kPerLane];
+        bool have[kPerLane];
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int sg = lane + 64 * j;
+            const bool own = sg >= seg0 && sg < seg0 + kSegs;
+            have[j] = sg >= nseg || own;
+            val[j] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < kSegs; ++s)
+                if (sg == seg0 + s) val[j] = v[s];
+        }
+        for (int it = 0;; ++it) {
+            bool all = true;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                if (!have[j]) {
+                    const uint64_t w = slot_read(rs + lane + 64 * j);
+                    if ((w >> 32) != 0) {
+                        have[j] = true;
+                        val[j] = __uint_as_float(static_cast<uint32_t>(w));
+                    } else {
+                        all = false;
+                    }
+                }
+            }
+            if (__all(all) || it >= wait_polls) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        bool miss = false;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int sg = lane + 64 * j;
+            if (sg < nseg) {
+                x.vals[sg] = val[j];
+                x.missing[sg] = have[j] ? 0 : 1;
+                miss = miss || !have[j];
+            }
+        }
+        const int any_miss = __any(miss);
+        if (lane == 0) x.nmissing = any_miss;
+    }
+    __syncthreads();
+    if (x.nmissing != 0) {  // workgroup-uniform: a wait ran out
+        for (int sg = 0; sg < nseg; ++sg) {
+            if (!x.missing[sg]) continue;  // uniform (LDS)
+            const float a = recompute(sg);
+            if (t == 0) x.vals[sg] = a;
+        }
+        __syncthreads();
+    }
+}
+
+// The row total of the segment sums in wide_row_finish's order: lane l adds
+// segments l, l+64, l+128, l+192 in turn from +0, then the wave's lane tree.
+__device__ __forceinline__ float team_row_total(const TeamXchg& x, int nseg) {
+    constexpr int kPerLane = static_cast<int>(kTeamMaxSegs / 64);
+    const int lane = threadIdx.x & 63;
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int sg = lane + 64 * j;
+        a += sg < nseg ? x.vals[sg] : 0.0f;
+    }
+    return group_sum<64>(a);
+}
+
 template <class S, bool ACC, int kTeamSegs>
 __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
     const typename S::T* __restrict__ x, const typename S::T* __restrict__ gamma,
@@ -898,14 +993,12 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
     constexpr int NV = kWideSegCols / (W * kWideLanes);  // slots per lane per segment
     constexpr int NS = kTeamSegs * NV;
     constexpr int kWaves = kWideLanes / 64;
-    constexpr int kPerLane = static_cast<int>(kTeamMaxSegs / 64);
-    // one buffer: a wave writes it for the next row only after the barrier
-    // that follows the poll, which every wave reaches after reading it
+    // one buffer each: a wave writes red (and the exchange fields) for the
+    // next row only after the barrier that follows the poll, which every wave
+    // reaches after reading them
     __shared__ float red[kTeamSegs][kWaves];
     __shared__ float fb[kWaves];
-    __shared__ float vals[kTeamMaxSegs];
-    __shared__ unsigned char missing[kTeamMaxSegs];
-    __shared__ int nmissing;
+    __shared__ TeamXchg xchg;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int64_t team = static_cast<int64_t>(blockIdx.x) / nparts;
     const int seg0 = (static_cast<int>(static_cast<int64_t>(blockIdx.x) - team * nparts)) * kTeamSegs;
@@ -1056,72 +1149,10 @@ __global__ __launch_bounds__(kWideLanes) void wide_bwd_team(
             v[s] = a;
         }
         // 2.-3. publish this workgroup's sums, gather the row's others
-        uint64_t* rs = slots + row * static_cast<int64_t>(nseg);
-        if (t == 0) {
-#pragma unroll
-            for (int s = 0; s < kTeamSegs; ++s)
-                if (seg0 + s < nseg) slot_publish(rs + seg0 + s, v[s]);
-        }
-        if (wave == 0) {
-            float val[kPerLane];
-            bool have[kPerLane];
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                const int sg = lane + 64 * j;
-                const bool own = sg >= seg0 && sg < seg0 + kTeamSegs;
-                have[j] = sg >= nseg || own;
-                val[j] = 0.0f;
-#pragma unroll
-                for (int s = 0; s < kTeamSegs; ++s)
-                    if (sg == seg0 + s) val[j] = v[s];
-            }
-            for (int it = 0;; ++it) {
-                bool all = true;
-#pragma unroll
-                for (int j = 0; j < kPerLane; ++j) {
-                    if (!have[j]) {
-                        const uint64_t w = slot_read(rs + lane + 64 * j);
-                        if ((w >> 32) != 0) {
-                            have[j] = true;
-                            val[j] = __uint_as_float(static_cast<uint32_t>(w));
-                        } else {
-                            all = false;
-                        }
-                    }
-                }
-                if (__all(all) || it >= wait_polls) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-            bool miss = false;
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                const int sg = lane + 64 * j;
-                if (sg < nseg) {
-                    vals[sg] = val[j];
-                    missing[sg] = have[j] ? 0 : 1;
-                    miss = miss || !have[j];
-                }
-            }
-            const int any_miss = __any(miss);
-            if (lane == 0) nmissing = any_miss;
-        }
-        __syncthreads();
-        if (nmissing != 0) {  // workgroup-uniform: a wait ran out
-            for (int sg = 0; sg < nseg; ++sg) {
-                if (!missing[sg]) continue;  // uniform (LDS)
-                const float a = recompute(row, sg);
-                if (t == 0) vals[sg] = a;
-            }
-            __syncthreads();
-        }
+        team_gather<kTeamSegs>(slots + row * static_cast<int64_t>(nseg), v, seg0, nseg,
+                               wait_polls, xchg, [&](int sg) { return recompute(row, sg); });
         // 4. the row's dot as wide_row_finish adds it, then s
-        float dot = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
-            const int sg = lane + 64 * j;
-            dot += sg < nseg ? vals[sg] : 0.0f;
-        }
-        dot = group_sum<64>(dot);
+        const float dot = team_row_total(xchg, nseg);
         const float sc = (r * r * dot) * inv_cols;
         // 5. dx = r*(g - x*s)
         const rsrc_t rdx = make_rsrc(dx + row * static_cast<int64_t>(cols), row_bytes);
@@ -1306,14 +1337,11 @@ __global__ __launch_bounds__(kWideLanes) void wide_fwd_team(
     constexpr int NV = kWideSegCols / (W * kWideLanes);  // slots per lane per segment
     constexpr int NS = kSegs * NV;
     constexpr int kWaves = kWideLanes / 64;
-    constexpr int kPerLane = static_cast<int>(kTeamMaxSegs / 64);
-    // red, vals, missing and nmissing are written for the next row only after
-    // a barrier that every wave reaches after reading them for this one
+    // red and the exchange fields are written for the next row only after a
+    // barrier that every wave reaches after reading them for this one
     __shared__ float red[kSegs][kWaves];
     __shared__ float fb[kWaves];
-    __shared__ float vals[kTeamMaxSegs];
-    __shared__ unsigned char missing[kTeamMaxSegs];
-    __shared__ int nmissing;
+    __shared__ TeamXchg xchg;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int64_t team = static_cast<int64_t>(blockIdx.x) / nparts;
     const int part = static_cast<int>(static_cast<int64_t>(blockIdx.x) - team * nparts);
@@ -1426,72 +1454,10 @@ __global__ __launch_bounds__(kWideLanes) void wide_fwd_team(
             v[s] = a;
         }
         // 2. publish this workgroup's sums, gather the row's others
-        uint64_t* rs = slots + row * static_cast<int64_t>(nseg);
-        if (t == 0) {
-#pragma unroll
-            for (int s = 0; s < kSegs; ++s)
-                if (seg0 + s < nseg) slot_publish(rs + seg0 + s, v[s]);
-        }
-        if (wave == 0) {
-            float val[kPerLane];
-            bool have[kPerLane];
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                const int sg = lane + 64 * j;
-                const bool own = sg >= seg0 && sg < seg0 + kSegs;
-                have[j] = sg >= nseg || own;
-                val[j] = 0.0f;
-#pragma unroll
-                for (int s = 0; s < kSegs; ++s)
-                    if (sg == seg0 + s) val[j] = v[s];
-            }
-            for (int it = 0;; ++it) {
-                bool all = true;
-#pragma unroll
-                for (int j = 0; j < kPerLane; ++j) {
-                    if (!have[j]) {
-                        const uint64_t w = slot_read(rs + lane + 64 * j);
-                        if ((w >> 32) != 0) {
-                            have[j] = true;
-                            val[j] = __uint_as_float(static_cast<uint32_t>(w));
-                        } else {
-                            all = false;
-                        }
-                    }
-                }
-                if (__all(all) || it >= wait_polls) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-            bool miss = false;
-#pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                const int sg = lane + 64 * j;
-                if (sg < nseg) {
-                    vals[sg] = val[j];
-                    missing[sg] = have[j] ? 0 : 1;
-                    miss = miss || !have[j];
-                }
-            }
-            const int any_miss = __any(miss);
-            if (lane == 0) nmissing = any_miss;
-        }
-        __syncthreads();
-        if (nmissing != 0) {  // workgroup-uniform: a wait ran out
-            for (int sg = 0; sg < nseg; ++sg) {
-                if (!missing[sg]) continue;  // uniform (LDS)
-                const float a = recompute(row, sg);
-                if (t == 0) vals[sg] = a;
-            }
-            __syncthreads();
-        }
+        team_gather<kSegs>(slots + row * static_cast<int64_t>(nseg), v, seg0, nseg, wait_polls,
+                           xchg, [&](int sg) { return recompute(row, sg); });
         // 3. the row's sum as wide_row_finish adds it, then r
-        float ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
-            const int sg = lane + 64 * j;
-            ss += sg < nseg ? vals[sg] : 0.0f;
-        }
-        ss = group_sum<64>(ss);
+        const float ss = team_row_total(xchg, nseg);
         const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
         if (part == 0 && t == 0) inv_rms[row] = r;
         // 4. y = (x*r)*gamma
