@@ -1199,6 +1199,59 @@ def run_wide(steps):
     return out
 
 
+WIDE_CALLS = ("fwd_split", "fwd_team", "bwd_team", "bwd_split")
+
+
+def run_wide_call(spec, reps=3):
+    """One RMSNorm call on rows wider than the register-resident kernels,
+    repeated `reps` times eagerly, for HBM counters (rocprofv3 --pmc): spec is
+    DTYPE:ROWS:COLS:CALL with CALL one of WIDE_CALLS -- agk_rmsnorm_fwd (the
+    split path), agk_rmsnorm_fwd_ws (the team forward), agk_rmsnorm_bwd with
+    the team kernel or with it switched off (the split path).  The inputs and
+    the backward's inv_rms are made with torch, so the library's kernels in
+    the run are the call's alone.  Prints one JSON line with the call's
+    algorithmic bytes."""
+    import torch
+
+    import cgadimpl_amd as agk
+    dtype, rows, cols, call = spec.split(":")
+    rows, cols = int(rows), int(cols)
+    if call not in WIDE_CALLS:
+        raise SystemExit(f"--wide-call: CALL must be one of {WIDE_CALLS}")
+    dev = torch.device("cuda:0")
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=gen, device=dev).to(tdt)
+    g = (torch.rand(cols, generator=gen, device=dev) + 0.5).to(tdt)
+    dy = torch.randn(rows, cols, generator=gen, device=dev).to(tdt)
+    inv = torch.rsqrt(x.float().pow(2).mean(dim=1) + 1e-6).contiguous()
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    dg = torch.empty(cols, dtype=torch.float32, device=dev)
+    fws = torch.empty(max(agk.rmsnorm_fwd_workspace_bytes(rows, cols), 8), dtype=torch.uint8,
+                      device=dev)
+    ws = torch.empty(agk.rmsnorm_bwd_workspace_bytes(rows, cols), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    prev = agk.set_team_backward(0 if call == "bwd_split" else 1)
+    try:
+        for _ in range(reps):
+            if call == "fwd_split":
+                agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv)
+            elif call == "fwd_team":
+                agk.rmsnorm_fwd(x, g, 1e-6, y=y, inv_rms=inv, workspace=fws)
+            else:
+                agk.rmsnorm_bwd(x, g, inv, dy, dx=dx, dgamma=dg, workspace=ws)
+            torch.cuda.synchronize()
+    finally:
+        agk.set_team_backward(prev)
+    s = x.element_size()
+    n = rows * cols
+    alg = (2 * n * s + cols * s + rows * 4 if call.startswith("fwd")
+           else 3 * n * s + cols * s + rows * 4 + cols * 4)
+    print(json.dumps({"wide_call": call, "dtype": dtype, "rows": rows, "cols": cols,
+                      "reps": reps, "algorithmic_bytes": alg}), flush=True)
+
+
 WIDE_ROWOP_SHAPES = (("bf16", 8192, 128256), ("f32", 8192, 128256), ("bf16", 4096, 151936),
                      ("bf16", 16, 128256), ("bf16", 8192, 50257), ("f32", 8192, 50257))
 
@@ -1313,6 +1366,9 @@ def main():
     ap.add_argument("--gemm-f32", action="store_true",
                     help="only time the fp32 GEMM (agk_gemm_f32) against torch's fp32 matmul, "
                          "then exit")
+    ap.add_argument("--wide-call", metavar="DTYPE:ROWS:COLS:CALL",
+                    help="run one wide-row RMSNorm call three times eagerly (for rocprofv3 "
+                         "--pmc): CALL is fwd_split, fwd_team, bwd_team or bwd_split; then exit")
     ap.add_argument("--wide", action="store_true",
                     help="only time rows wider than the register-resident kernels: the split "
                          "paths against the one-workgroup-per-row kernels, and softmax / "
@@ -1330,6 +1386,9 @@ def main():
         return
     if args.gemm_f32:
         gemm_f32_bench(min(args.steps, 10))
+        return
+    if args.wide_call:
+        run_wide_call(args.wide_call)
         return
     if args.wide:
         run_wide(min(args.steps, 20))

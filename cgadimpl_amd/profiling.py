@@ -31,6 +31,8 @@ Usage:
         <copy_write_dir> <copy_mib> <config> <out_stem> "<command>"
   python -m cgadimpl_amd.profiling gemm-traffic <fetch_dir> <write_dir> <copy_fetch_dir>
         <copy_write_dir> <copy_mib> <out.md> "<command>"
+  python -m cgadimpl_amd.profiling wide-traffic <out.md> "<command>" <copy_mib>
+        <copy_fetch_dir> <copy_write_dir> <label>,<fetch_dir>,<write_dir>,<bench output> ...
 """
 from __future__ import annotations
 
@@ -217,6 +219,46 @@ def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, 
     with open(out_stem + ".json", "w") as fh:
         json.dump(rec, fh, indent=1)
         fh.write("\n")
+
+
+# Kernel-name prefixes of the RMSNorm library's kernels (the rest of a run's
+# dispatches are torch's input generation).
+LIB_KERNEL_PREFIXES = ("fill_zero_f32", "wide_", "dgamma_finalize", "rms_", "bwd_fewrows")
+
+
+def write_wide_traffic_summary(out_md, command, copy_mib, copy_fetch_dir, copy_write_dir,
+                               runs):
+    """HBM bytes per wide-row call (bench.py --wide-call runs): each run's
+    library kernels (medians per kernel over the run's dispatches, scaled by the
+    copy's counters) summed against the call's algorithmic bytes.  runs:
+    [(label, fetch_dir, write_dir, jsonl_with_the_call_line)]."""
+    cf = _counter_by_kernel(copy_fetch_dir, "FETCH_SIZE")
+    cw = _counter_by_kernel(copy_write_dir, "WRITE_SIZE")
+    copy_kib = copy_mib * 1024.0
+    fs = copy_kib / _median(next(v for k, v in cf.items() if "copy" in k.lower()))
+    wsc = copy_kib / _median(next(v for k, v in cw.items() if "copy" in k.lower()))
+    lines = ["# HBM traffic of the wide-row RMSNorm calls: team kernels against split paths",
+             "", "Commands (each counter in its own run):", "", "```", command, "```", "",
+             f"Counter scale from a {copy_mib} MiB device copy (`bench.py --copy-probe "
+             f"{copy_mib}`): FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {wsc:.4f}. Each run makes "
+             "its inputs with torch and repeats one call three times; the library's kernels "
+             "are medians over their dispatches, summed per call.", "",
+             "| call | kernels | read MB | write MB | HBM bytes | algorithmic bytes | ratio |",
+             "|---|---|---|---|---|---|---|"]
+    for label, fdir, wdir, jsonl in runs:
+        rec = next(json.loads(ln) for ln in open(jsonl) if ln.startswith('{"wide_call"'))
+        f = _counter_by_kernel(fdir, "FETCH_SIZE")
+        w = _counter_by_kernel(wdir, "WRITE_SIZE")
+        names = sorted(k for k in set(f) | set(w)
+                       if short_name(k).startswith(LIB_KERNEL_PREFIXES))
+        rd = sum(_median(f[k]) * fs * 1024.0 for k in names if k in f)
+        wr = sum(_median(w[k]) * wsc * 1024.0 for k in names if k in w)
+        short = ", ".join(sorted({short_name(k) for k in names}))
+        alg = rec["algorithmic_bytes"]
+        lines.append(f"| {label} | {short} | {rd / 1e6:.1f} | {wr / 1e6:.1f} | "
+                     f"{rd + wr:.4g} | {alg:.4g} | {(rd + wr) / alg:.3f} |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
 
 
 def _counter_by_launch(run_dir, counter, name_part):
@@ -621,6 +663,9 @@ def main(argv):
     elif len(argv) >= 8 and argv[0] == "gemm-traffic":
         write_gemm_traffic_summary(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6],
                                    argv[7])
+    elif len(argv) >= 7 and argv[0] == "wide-traffic":
+        runs = [tuple(a.split(",")) for a in argv[6:]]
+        write_wide_traffic_summary(argv[1], argv[2], int(argv[3]), argv[4], argv[5], runs)
     elif len(argv) >= 9 and argv[0] == "traffic":
         write_traffic_summary(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6],
                               argv[7], argv[8])
