@@ -1252,6 +1252,49 @@ def run_wide_call(spec, reps=3):
                       "reps": reps, "algorithmic_bytes": alg}), flush=True)
 
 
+WIDE_ROWOP_CALLS = ("softmax_fwd", "softmax_bwd", "logsumexp_bwd")
+
+
+def run_wide_rowop_call(spec, reps=3):
+    """One vocabulary-width row-op call repeated `reps` times eagerly, for HBM
+    counters: spec is DTYPE:ROWS:COLS:OP:WS with OP one of WIDE_ROWOP_CALLS and
+    WS "ws" (the *_ws entry point given a workspace: the team kernel) or "nows"
+    (the workspace-free kernel).  Inputs made with torch.  Prints one JSON line
+    with the call's algorithmic bytes."""
+    import torch
+
+    import cgadimpl_amd as agk
+    dtype, rows, cols, op, wsmode = spec.split(":")
+    rows, cols = int(rows), int(cols)
+    if op not in WIDE_ROWOP_CALLS or wsmode not in ("ws", "nows"):
+        raise SystemExit(f"--wide-rowop-call: OP in {WIDE_ROWOP_CALLS}, WS ws or nows")
+    dev = torch.device("cuda:0")
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(rows + cols)
+    z = (torch.randn(rows, cols, generator=gen, device=dev) * 4).to(tdt)
+    dy = torch.randn(rows, cols, generator=gen, device=dev).to(tdt)
+    dl = torch.randn(rows, 1, generator=gen, device=dev).to(tdt)
+    y = torch.softmax(z.float(), dim=-1).to(tdt)
+    out = torch.empty_like(z)
+    ws = (torch.empty(max(agk.rowops_workspace_bytes(rows, cols), 8), dtype=torch.uint8,
+                      device=dev) if wsmode == "ws" else False)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        if op == "softmax_fwd":
+            agk.softmax_fwd(z, y=out, workspace=ws)
+        elif op == "softmax_bwd":
+            agk.softmax_bwd(y, dy, dz=out, workspace=ws)
+        else:
+            agk.logsumexp_bwd(z, dl, dz=out, workspace=ws)
+        torch.cuda.synchronize()
+    n, s = rows * cols, z.element_size()
+    alg = {"softmax_fwd": 2 * n * s, "softmax_bwd": 3 * n * s,
+           "logsumexp_bwd": 2 * n * s + rows * s}[op]
+    print(json.dumps({"wide_call": f"{op} {wsmode}", "dtype": dtype, "rows": rows,
+                      "cols": cols, "reps": reps, "algorithmic_bytes": alg}), flush=True)
+
+
 WIDE_ROWOP_SHAPES = (("bf16", 8192, 128256), ("f32", 8192, 128256), ("bf16", 4096, 151936),
                      ("bf16", 16, 128256), ("bf16", 8192, 50257), ("f32", 8192, 50257))
 
@@ -1369,6 +1412,10 @@ def main():
     ap.add_argument("--wide-call", metavar="DTYPE:ROWS:COLS:CALL",
                     help="run one wide-row RMSNorm call three times eagerly (for rocprofv3 "
                          "--pmc): CALL is fwd_split, fwd_team, bwd_team or bwd_split; then exit")
+    ap.add_argument("--wide-rowop-call", metavar="DTYPE:ROWS:COLS:OP:WS",
+                    help="run one vocabulary-width row-op call three times eagerly (for "
+                         "rocprofv3 --pmc): OP is softmax_fwd, softmax_bwd or logsumexp_bwd, "
+                         "WS is ws (the team kernel) or nows; then exit")
     ap.add_argument("--wide", action="store_true",
                     help="only time rows wider than the register-resident kernels: the split "
                          "paths against the one-workgroup-per-row kernels, and softmax / "
@@ -1389,6 +1436,9 @@ def main():
         return
     if args.wide_call:
         run_wide_call(args.wide_call)
+        return
+    if args.wide_rowop_call:
+        run_wide_rowop_call(args.wide_rowop_call)
         return
     if args.wide:
         run_wide(min(args.steps, 20))

@@ -223,7 +223,8 @@ def write_traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, 
 
 # Kernel-name prefixes of the RMSNorm library's kernels (the rest of a run's
 # dispatches are torch's input generation).
-LIB_KERNEL_PREFIXES = ("fill_zero_f32", "wide_", "dgamma_finalize", "rms_", "bwd_fewrows")
+LIB_KERNEL_PREFIXES = ("fill_zero_f32", "wide_", "dgamma_finalize", "rms_", "bwd_fewrows",
+                       "row_", "team_clear", "lse_bwd_from_value")
 
 
 def write_wide_traffic_summary(out_md, command, copy_mib, copy_fetch_dir, copy_write_dir,
@@ -237,7 +238,7 @@ def write_wide_traffic_summary(out_md, command, copy_mib, copy_fetch_dir, copy_w
     copy_kib = copy_mib * 1024.0
     fs = copy_kib / _median(next(v for k, v in cf.items() if "copy" in k.lower()))
     wsc = copy_kib / _median(next(v for k, v in cw.items() if "copy" in k.lower()))
-    lines = ["# HBM traffic of the wide-row RMSNorm calls: team kernels against split paths",
+    lines = ["# HBM traffic of wide-row calls: team kernels against the paths without them",
              "", "Commands (each counter in its own run):", "", "```", command, "```", "",
              f"Counter scale from a {copy_mib} MiB device copy (`bench.py --copy-probe "
              f"{copy_mib}`): FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {wsc:.4f}. Each run makes "
