@@ -1292,7 +1292,7 @@ constexpr int64_t kFwdTeamWorkgroups = 512;
 // [2048, 65536] 178 -> 189, [4096, 40000] 223 -> 230.  Gamma in registers
 // instead of LDS at four fp32 segments measured the same (241 VGPRs).  Eight
 // bf16 segments need 256 VGPRs (one wave per SIMD: the 512 workgroups would
-// not all be resident; measured 10-15 % slower), and 1024 workgroups of the
+// not all be resident; measured 9-16 % slower), and 1024 workgroups of the
 // narrower parts measured between one and two segments.
 inline int fwd_team_segs_for(int dtype, int64_t rows, int64_t cols) {
     if (dtype != AGK_F32) return 4;
