@@ -156,7 +156,9 @@ __device__ __forceinline__ void row_reduce(float (&v)[N],
 //                                    values where the row is held in registers
 //   max_sumexp<KEEP>(m, s)           m = max over the row of a, s = sum of
 //                                    fast_exp(a - m) (KEEP: kept as sum_keep
-//                                    keeps them); one online pass in LoopedVec
+//                                    keeps them; without KEEP the resident
+//                                    context folds the shift into the
+//                                    exponent); one online pass in LoopedVec
 //   store_kept(out, acc, f, g)       out[col] (+)= g(f(a, b)), f's values as
 //                                    kept by the last sum_keep (recomputed by
 //                                    the looped context)
@@ -273,15 +275,27 @@ struct Resident {
         s1 = r[1];
     }
 
+    // Without KEEP (log-sum-exp forward: only the sum is used) the shift is
+    // folded into the exponent, exp2(fma(a, log2(e), -m * log2(e))): one
+    // instruction fewer per element than fast_exp(a - m).  The rounding of
+    // m * log2(e) scales every term by the same factor 2^d (|d| <= |m| 2^-24
+    // log2(e)), i.e. moves log(s) + m by at most |m| 2^-24, the size of one
+    // rounding of m.  Special values give what fast_exp(a - m) gives (-inf
+    // terms 0, NaN through).
     template <bool KEEP>
     __device__ __forceinline__ void max_sumexp(float& m, float& s) {
         m = max([](float z, float) { return z; });
         const float mm = m;
         auto e = [=](float z, float) { return fast_exp(z - mm); };
-        if constexpr (KEEP && !kBig)
+        if constexpr (KEEP && !kBig) {
             s = sum_keep(e);
-        else
+        } else if constexpr (KEEP) {
             s = sum(e);
+        } else {
+            constexpr float kLog2e = 1.4426950408889634f;
+            const float nml = -mm * kLog2e;
+            s = sum([=](float z, float) { return __builtin_amdgcn_exp2f(fmaf(z, kLog2e, nml)); });
+        }
     }
 
     template <class F>
@@ -884,6 +898,14 @@ struct LseFwd {
     // the 16-byte looped kernel's one online pass (GPT-2-sized vocabularies:
     // 52-61 % of HBM peak resident, 78 % streamed)
     static constexpr bool kStreamWideBf16 = true;
+    // bf16 rows that the plan gives 2 slots per lane on 128-1024 lanes
+    // (2048-16384 columns) take 4 slots per lane on half the lanes: the row's
+    // two reductions, its log and its set-up are then spread over 32 elements
+    // per lane instead of 16, and this read-only op is bound by instructions
+    // per byte, not by HBM, at 2 slots (MI355X, 1 GiB of bf16 logits, graph
+    // replays: 2048-16384 columns 70-79 % of HBM peak at 2 slots, 87-88.5 % at
+    // 4; fp32 rows at 4 slots measured slower and keep the plan)
+    static constexpr bool kFourSlotsBf16 = true;
     template <class C>
     __device__ static void run(C& c, const RowArgs& p) {
         float m, s;
@@ -971,6 +993,15 @@ struct StreamWideBf16<Op, std::void_t<decltype(Op::kStreamWideBf16)>>
 template <class Op>
 constexpr bool stream_wide_bf16() { return StreamWideBf16<Op>::value; }
 
+// Op::kFourSlotsBf16 when the op declares it, else false.
+template <class Op, class = void>
+struct FourSlotsBf16 : std::false_type {};
+template <class Op>
+struct FourSlotsBf16<Op, std::void_t<decltype(Op::kFourSlotsBf16)>>
+    : std::integral_constant<bool, Op::kFourSlotsBf16> {};
+template <class Op>
+constexpr bool four_slots_bf16() { return FourSlotsBf16<Op>::value; }
+
 // Op::kResident16 when the op declares it, else false: rows of 8193-16384
 // 16-byte slots (65537-131072 bf16 or 32769-65536 fp32 columns) take a
 // 1024-lane workgroup of 16 slots per lane, the row read once, instead of the
@@ -1052,6 +1083,10 @@ int launch(const RowArgs& p, int64_t rows, int cols, hipStream_t st) {
     Plan pl;
     if (vec) pl = fwd_plan(cols / S::kVec, rows);
     if (stream_wide_bf16<Op>() && std::is_same<S, BF16>::value && pl.nv == 8) pl = Plan{};
+    if (four_slots_bf16<Op>() && std::is_same<S, BF16>::value && pl.nv == 2 && pl.tpr >= 128) {
+        const Plan q{pl.tpr / 2, 4, pl.tpr >= 512 ? 1 : 512 / pl.tpr};
+        if (has_shape(kFwdShapes, q)) pl = q;
+    }
     if constexpr (Resident16<Op>::value) {
         const int64_t nslot = cols / S::kVec;
         if (vec && pl.tpr == 0 && nslot > 8192 && nslot <= 16384) {
