@@ -1296,7 +1296,8 @@ def run_wide_rowop_call(spec, reps=3):
 
 
 WIDE_ROWOP_SHAPES = (("bf16", 8192, 128256), ("f32", 8192, 128256), ("bf16", 4096, 151936),
-                     ("bf16", 16, 128256), ("bf16", 8192, 50257), ("f32", 8192, 50257))
+                     ("bf16", 16, 128256), ("bf16", 8192, 50257), ("f32", 8192, 50257),
+                     ("bf16", 8192, 65536), ("bf16", 8192, 48000))
 
 
 def run_wide_rowops(steps):

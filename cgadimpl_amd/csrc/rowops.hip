@@ -1040,19 +1040,27 @@ inline bool same_offset(const RowArgs& p) {
 // kernels (the default), 2 whenever the row fits it (tests and measurement).
 std::atomic<int> g_team_mode{1};
 
-// Least parts per row for which mode 1 takes the team kernel: rows of more
-// than 8192 16-byte slots (past the register-resident shapes), and for the
-// softmax backward also rows that do not start on a 16-byte boundary from
-// 2049 slots on.  Measured on MI355X (graph-replayed, 8192 rows): at 50257
-// columns (every row off a boundary) the backward's team kernel against the
-// 16-byte looped kernel, which reads y and dy twice: bf16 438 against 540 us,
-// fp32 855 against 1140 us; the forward and the log-sum-exp backward read
-// one tensor, which the looped kernel's second pass finds in the caches:
-// bf16 (4 parts) 397-411 against 318 us, fp32 (7 parts) 619-631 against
-// 690-696 us.
+// Least parts per row for which mode 1 takes the team kernel.  Measured on
+// MI355X (graph-replayed, 8192 rows, us, one-workgroup-per-row kernel against
+// the team kernel):
+//  - rows on a 16-byte boundary, held in registers by one workgroup up to 8192
+//    slots: the softmax forward and the log-sum-exp backward gain from 3
+//    parts (bf16 40000 columns 254-262 against 243-245, 48000 299-309
+//    against 274-276, 65536 397-407 against 358-364; fp32 24000 level,
+//    32768 362-367 against 352-353) and lose at 2 (bf16 32000 174-178
+//    against 184-187); the softmax backward gains from 4 (bf16 65536 566
+//    against 532, fp32 32768 538 against 521) and is level or slower at 3
+//    (bf16 40000 329 against 342, 48000 403 against 401);
+//  - rows off a 16-byte boundary: the backward from 2 parts (at 50257
+//    columns the 16-byte looped kernel reads y and dy twice: bf16 540
+//    against 438, fp32 1140 against 855); the forward and the log-sum-exp
+//    backward read one tensor, which the looped kernel's second pass finds
+//    in the caches, so they keep it below 5 parts (bf16 50257, 4 parts:
+//    313-316 against 313-319).
 template <class Op>
 constexpr int team_min_parts(bool aligned) {
-    return std::is_same<Op, SmBwd>::value && !aligned ? 2 : 5;
+    if (std::is_same<Op, SmBwd>::value) return aligned ? 4 : 2;
+    return aligned ? 3 : 5;
 }
 
 // Runs Op over the rows on the team kernel when the mode, the workspace and

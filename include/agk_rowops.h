@@ -123,12 +123,14 @@ int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows,
  * what agk_softmax_fwd, agk_softmax_bwd and agk_logsumexp_bwd compute (the
  * same references: softmax_row_nodeops, reduction.cpp:42-53; vjp_SoftmaxRow,
  * autodiff_vjp_ops.cpp:421-428; vjp_LogSumExpRow, :430-440).  Given a
- * workspace, rows too wide for one workgroup's registers (more than 8192
- * 16-byte slots; for the softmax backward also rows that do not start on a
- * 16-byte boundary from 2049 slots on, every row tensor at the same offset
- * from one) are spread over a team of workgroups that exchange their partial
+ * workspace, wide rows are spread over a team of parts = ceil(slots / 2048)
+ * workgroups (slots = the row's 16-byte slots) that exchange their partial
  * row sums through the workspace, so each input row is read from HBM once
- * (the workspace-free calls re-read such rows).  Results are within fp32
+ * (the workspace-free calls re-read rows too wide for one workgroup's
+ * registers): rows on a 16-byte boundary from 3 parts (the softmax
+ * backward from 4), rows that do not start on one (every row tensor at the
+ * same offset from one) from 5 parts (the softmax backward from 2).
+ * Results are within fp32
  * rounding of the workspace-free calls' (the row sums are added in another
  * order, and the forward and the log-sum-exp backward scale each range's
  * exp(z - range max) by exp(range max - row max)) and bit-identical run to

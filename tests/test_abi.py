@@ -492,9 +492,14 @@ def test_rowops_workspace_rule_and_team_plans():
         assert plan(op, 8192, 128256, 1, True) == {"parts": 8, "slots_per_part": 2004,
                                                    "teams": 64}
     assert plan("softmax_fwd", 8192, 128256, 0, True)["parts"] == 16
-    assert plan("softmax_fwd", 4, 65536, 1, True)["parts"] == 0   # 8192 slots: resident kernels
+    # aligned rows: the forward and the log-sum-exp backward from 3 parts, the
+    # softmax backward from 4 (below, the resident kernels)
+    assert plan("softmax_fwd", 4, 65536, 1, True)["parts"] == 4   # bf16 8192 slots
+    assert plan("logsumexp_bwd", 4, 40000, 1, True)["parts"] == 3
+    assert plan("softmax_fwd", 4, 32000, 1, True)["parts"] == 0   # 2 parts
     assert plan("softmax_fwd", 4, 65536, 0, True)["parts"] == 8
-    assert plan("softmax_bwd", 4, 65536, 1, True)["parts"] == 0
+    assert plan("softmax_bwd", 4, 65536, 1, True)["parts"] == 4
+    assert plan("softmax_bwd", 4, 40000, 1, True)["parts"] == 0   # 3 parts
     # rows off a 16-byte boundary: the backward from 2 parts, the others from 5
     assert plan("softmax_bwd", 9, 50257, 1, False) == {"parts": 4, "slots_per_part": 1571,
                                                        "teams": 9}
