@@ -1055,12 +1055,12 @@ std::atomic<int> g_team_mode{1};
 //    columns the 16-byte looped kernel reads y and dy twice: bf16 540
 //    against 438, fp32 1140 against 855); the forward and the log-sum-exp
 //    backward read one tensor, which the looped kernel's second pass finds
-//    in the caches, so they keep it below 5 parts (bf16 50257, 4 parts:
-//    313-316 against 313-319).
+//    in the caches, from 4 parts (bf16 50257: 313-316 against 305-306 with
+//    three workgroups per CU).
 template <class Op>
 constexpr int team_min_parts(bool aligned) {
     if (std::is_same<Op, SmBwd>::value) return aligned ? 4 : 2;
-    return aligned ? 3 : 5;
+    return aligned ? 3 : 4;
 }
 
 // Runs Op over the rows on the team kernel when the mode, the workspace and
@@ -1074,7 +1074,8 @@ int maybe_team(const RowArgs& p, void* ws, size_t ws_bytes, int64_t rows, int co
     bool aligned = false;
     if (!team_fits<S, Op>(p, rows, cols, 1, &aligned)) return AGK_OK;
     const TeamShape sh =
-        team_shape(rows, cols, S::kVec, team_nvl<Op>(std::is_same<S, BF16>::value, aligned));
+        team_shape(rows, cols, S::kVec, team_nvl<Op>(std::is_same<S, BF16>::value, aligned),
+                   team_grid<Op>());
     if (mode == 1 && sh.parts < team_min_parts<Op>(aligned)) return AGK_OK;
     if (ws_bytes < team_words_bytes(rows, sh, TeamVals<Op>::value)) return AGK_OK;
     *taken = true;
@@ -1427,7 +1428,8 @@ int agk_rowops_team_plan(int op, int64_t rows, int64_t cols, int dtype, int alig
     const size_t esz = dtype == AGK_F32 ? 4u : 2u;
     if (rows > 0x7fffffffLL || static_cast<uint64_t>(cols) * esz >= 0x80000000ull) return AGK_OK;
     const bool al = aligned != 0 && cols % W == 0;
-    const TeamShape sh = team_shape(rows, cols, W, team_nvl_of(op, dtype == AGK_BF16, al));
+    const TeamShape sh = team_shape(rows, cols, W, team_nvl_of(op, dtype == AGK_BF16, al),
+                                    op == 1 ? team_grid<SmBwd>() : team_grid<SmFwd>());
     const int mode = g_team_mode.load(std::memory_order_relaxed);
     if (sh.parts == 0 || mode == 0 || sh.teams * sh.parts > 0x7fffffffLL) return AGK_OK;
     const int least = op == 1 ? team_min_parts<SmBwd>(al) : team_min_parts<SmFwd>(al);

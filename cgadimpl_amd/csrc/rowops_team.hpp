@@ -46,10 +46,6 @@
 constexpr int kTeamLanes = 256;
 constexpr int kTeamWaves = kTeamLanes / 64;
 constexpr int kTeamMaxParts = 64;  // one polling lane per part
-// Workgroups a launch aims for: two per CU of a 256-CU MI355X, all resident
-// at once at the kernels' register use.  A constant, so the team count
-// depends only on the shape, never on the device.
-constexpr int64_t kTeamGrid = 512;
 // Slots per lane per row tensor: a part covers NVL * 256 slots (32 KiB of
 // each row tensor).  Measured on MI355X (graph-replayed, bf16 and fp32
 // [8192, 128256], [8192, 50257], bf16 [4096, 151936]): 8 slots per lane
@@ -73,14 +69,35 @@ struct TeamVals : std::integral_constant<int, 2> {};
 template <>
 struct TeamVals<SmBwd> : std::integral_constant<int, 1> {};
 
+// Workgroups per CU a launch aims for, all resident at once at the kernel's
+// register use (the kernel is built for that many waves per SIMD): three for
+// the forward and the log-sum-exp backward (at most 168 registers per lane;
+// they use 102-154), two for the softmax backward (up to 190).  Measured on
+// MI355X (graph-replayed, three against two per CU, us): bf16 [8192, 50257]
+// 313-319 -> 305-306, [4096, 151936] 464-466 -> 450, fp32 [8192, 128256]
+// 1519-1525 -> 1502-1503; bf16 [8192, 128256] and [8192, 65536] and fp32
+// [8192, 50257] within 1 %.
+template <class Op>
+constexpr int team_per_cu() {
+    return TeamVals<Op>::value == 2 ? 3 : 2;
+}
+// Workgroups a launch aims for on a 256-CU MI355X.  A constant per op, so the
+// team count depends only on the shape, never on the device.
+template <class Op>
+constexpr int64_t team_grid() {
+    return 256 * team_per_cu<Op>();
+}
+
 struct TeamShape {
     int parts = 0;       // workgroups per row
     int ps = 0;          // slots per part
     int64_t teams = 0;   // rows in flight
 };
 
-// Depends only on rows, cols, the slot width W and the op's slots per lane.
-inline TeamShape team_shape(int64_t rows, int64_t cols, int W, int nvl) {
+// Depends only on rows, cols, the slot width W, the op's slots per lane and
+// its grid (teams = grid / parts rows in flight; the grid never changes the
+// arithmetic, only which workgroups run a row).
+inline TeamShape team_shape(int64_t rows, int64_t cols, int W, int nvl, int64_t grid) {
     TeamShape s;
     const int64_t nslot = (cols + W - 1) / W;  // at least any row's body slots
     const int64_t per = static_cast<int64_t>(nvl) * kTeamLanes;  // slots per part
@@ -88,7 +105,7 @@ inline TeamShape team_shape(int64_t rows, int64_t cols, int W, int nvl) {
     if (parts < 1 || parts > kTeamMaxParts) return s;
     s.parts = static_cast<int>(parts);
     s.ps = static_cast<int>((nslot + parts - 1) / parts);
-    const int64_t want = kTeamGrid / parts > 0 ? kTeamGrid / parts : 1;
+    const int64_t want = grid / parts > 0 ? grid / parts : 1;
     s.teams = want < rows ? want : rows;
     return s;
 }
@@ -110,7 +127,7 @@ inline size_t team_ws_bytes(int64_t rows, int64_t cols) {
         for (int bf16 = 0; bf16 < 2; ++bf16)
             for (int al = 0; al < 2; ++al) {
                 const TeamShape s = team_shape(rows, cols, bf16 ? 8 : 4,
-                                               team_nvl_of(op, bf16 != 0, al != 0));
+                                               team_nvl_of(op, bf16 != 0, al != 0), 1);
                 const size_t n = s.parts >= 2 ? team_words_bytes(rows, s, op == 1 ? 1 : 2) : 0;
                 most = n > most ? n : most;
             }
@@ -169,10 +186,10 @@ __device__ __forceinline__ float team_fold(const float (&acc)[W]) {
     return v;
 }
 
-// Two workgroups resident on every CU, the grid kTeamGrid assumes: two
-// waves per SIMD, at most 256 registers per lane.
+// team_per_cu<Op>() workgroups resident on every CU, as the grid assumes:
+// that many waves per SIMD (2: at most 256 registers per lane, 3: 168).
 template <class S, class Op, bool ALIGNED, bool ACC>
-__global__ __launch_bounds__(kTeamLanes) __attribute__((amdgpu_waves_per_eu(2))) void row_team(const RowArgs p, uint64_t* __restrict__ words,
+__global__ __launch_bounds__(kTeamLanes) __attribute__((amdgpu_waves_per_eu(team_per_cu<Op>()))) void row_team(const RowArgs p, uint64_t* __restrict__ words,
                                                        int64_t rows, int cols, int parts, int ps,
                                                        int64_t teams, int polls) {
     using T = typename S::T;
@@ -585,7 +602,8 @@ inline bool team_fits(const RowArgs& p, int64_t rows, int cols, int min_parts, b
                aligned16(p.out);
     if (!*aligned && !same_offset<T>(p)) return false;
     const TeamShape s = team_shape(rows, cols, S::kVec,
-                                   team_nvl<Op>(std::is_same<S, BF16>::value, *aligned));
+                                   team_nvl<Op>(std::is_same<S, BF16>::value, *aligned),
+                                   team_grid<Op>());
     return s.parts >= min_parts && s.parts != 0 && s.teams * s.parts <= 0x7fffffffLL;
 }
 
@@ -594,7 +612,8 @@ int team_wait_limit();
 template <class Op, class S>
 int launch_team(const RowArgs& p, void* ws, int64_t rows, int cols, bool aligned, hipStream_t st) {
     const TeamShape s = team_shape(rows, cols, S::kVec,
-                                   team_nvl<Op>(std::is_same<S, BF16>::value, aligned));
+                                   team_nvl<Op>(std::is_same<S, BF16>::value, aligned),
+                                   team_grid<Op>());
     uint64_t* words = static_cast<uint64_t*>(ws);
     const int64_t nwords = rows * s.parts * TeamVals<Op>::value;
     {

@@ -129,7 +129,7 @@ int agk_logsumexp_jvp(const void* z, const void* tz, void* ty, int64_t rows,
  * (the workspace-free calls re-read rows too wide for one workgroup's
  * registers): rows on a 16-byte boundary from 3 parts (the softmax
  * backward from 4), rows that do not start on one (every row tensor at the
- * same offset from one) from 5 parts (the softmax backward from 2).
+ * same offset from one) from 4 parts (the softmax backward from 2).
  * Results are within fp32
  * rounding of the workspace-free calls' (the row sums are added in another
  * order, and the forward and the log-sum-exp backward scale each range's

@@ -475,9 +475,10 @@ def _rowops_ws_rule(rows, cols):
 
 def test_rowops_workspace_rule_and_team_plans():
     """The *_ws row ops' workspace (the most any op uses at the shape, 0 for
-    rows one workgroup holds), the team plans in the default mode (rows of
-    more than 8192 aligned 16-byte slots, or off a boundary from 2049 slots),
-    and validation that rejects a workspace before any HIP call."""
+    rows one workgroup holds), the team plans in the default mode (aligned
+    rows from 3 parts of 2048 16-byte slots, 4 for the softmax backward; rows
+    off a boundary from 4 parts, 2 for the softmax backward), and validation
+    that rejects a workspace before any HIP call."""
     lib = agk.lib()
     wb = lib.agk_rowops_workspace_bytes
     for rows, cols in [(8192, 128256), (3, 50257), (1, 8193), (5, 262144), (2, 1 << 19),
@@ -487,10 +488,11 @@ def test_rowops_workspace_rule_and_team_plans():
     assert wb(100, 4096) == 0 and wb(4, 512) == 0 and wb(0, 131072) == 0
     assert wb(4, 1 << 22) == 0  # more than 64 parts: the team kernel holds no such row
     plan = agk.rowops_team_plan
-    # bf16 Llama 3 vocabulary: 16032 slots -> 8 parts of 2004, 512 / 8 teams
+    # bf16 Llama 3 vocabulary: 16032 slots -> 8 parts of 2004; grid / 8 teams, the
+    # grid 3 workgroups per CU of 256 for the two-value ops, 2 for the softmax backward
     for op in agk.ROWOPS_TEAM_OPS:
-        assert plan(op, 8192, 128256, 1, True) == {"parts": 8, "slots_per_part": 2004,
-                                                   "teams": 64}
+        assert plan(op, 8192, 128256, 1, True) == {
+            "parts": 8, "slots_per_part": 2004, "teams": 64 if op == "softmax_bwd" else 96}
     assert plan("softmax_fwd", 8192, 128256, 0, True)["parts"] == 16
     # aligned rows: the forward and the log-sum-exp backward from 3 parts, the
     # softmax backward from 4 (below, the resident kernels)
@@ -500,10 +502,12 @@ def test_rowops_workspace_rule_and_team_plans():
     assert plan("softmax_fwd", 4, 65536, 0, True)["parts"] == 8
     assert plan("softmax_bwd", 4, 65536, 1, True)["parts"] == 4
     assert plan("softmax_bwd", 4, 40000, 1, True)["parts"] == 0   # 3 parts
-    # rows off a 16-byte boundary: the backward from 2 parts, the others from 5
+    # rows off a 16-byte boundary: the backward from 2 parts, the others from 4
     assert plan("softmax_bwd", 9, 50257, 1, False) == {"parts": 4, "slots_per_part": 1571,
                                                        "teams": 9}
-    assert plan("softmax_fwd", 9, 50257, 1, False)["parts"] == 0
+    assert plan("softmax_fwd", 9000, 50257, 1, False) == {"parts": 4, "slots_per_part": 1571,
+                                                          "teams": 192}
+    assert plan("logsumexp_bwd", 9, 40004, 1, False)["parts"] == 0  # 3 parts
     assert plan("logsumexp_bwd", 9, 50257, 0, False)["parts"] == 7
     assert plan("softmax_fwd", 3, 16384, 1, False)["parts"] == 0  # 2048 slots: one workgroup
     prev = agk.set_rowops_team(0)
